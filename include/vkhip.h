@@ -1,0 +1,199 @@
+/*
+ * vkhip — the C-ABI seam between the vknn host code (C++) and the MI355X (gfx950) HIP kernels of
+ * the fused fp16 convolution path. Plain pointers, sizes and POD descriptors; every entry point
+ * returns an int status (0 = ok) and never throws. vkhip_last_error() holds the last message.
+ *
+ * It replaces, for the HIP backend, the reference's Vulkan device runtime and per-op dispatch:
+ *   - device/buffers/streams/events/graphs  <- src/backend/vulkan/vk_context.cpp, vk_buffer.cpp,
+ *                                              vk_command.cpp (submitAndWait, timestamp queries)
+ *   - conv launchers                         <- src/backend/vulkan/ops/conv.cpp:491-553 (record):
+ *                                              conv1x1 / split-K / conv1x1_s2 / direct / Winograd
+ *   - weight prepack                         <- src/backend/vulkan/ops/conv.cpp:364-437 (prepare)
+ *   - depthwise, fused dw+pw, fused SE       <- ops/conv.cpp:535-552, ops/fused_dwpw.cpp:42-111,
+ *                                              ops/fused_se.cpp:134-163
+ *   - pack / unpack                          <- src/backend/vulkan/vk_backend.cpp:558-696
+ *   - add, channel-broadcast mul             <- ops/add.cpp:21-41, ops/binary.cpp:32-43
+ *
+ * Activation tensors on the device are NC4HW4 fp16: element (n,c,h,w) sits at
+ * (((n*Cb + c/4)*H + h)*W + w)*4 + c%4 with Cb = ceil(C/4); lanes with c >= C hold +0.
+ * Arithmetic is fp32; every fp16 activation store rounds to nearest even.
+ */
+#ifndef VKHIP_H
+#define VKHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+#define VKHIP_OK 0
+#define VKHIP_ERR_INVALID 1     /* bad argument / shape the kernel does not take */
+#define VKHIP_ERR_UNSUPPORTED 2 /* valid request this build does not implement */
+#define VKHIP_ERR_RUNTIME 3     /* HIP runtime error */
+#define VKHIP_ERR_NODEVICE 4    /* no usable gfx950 device */
+
+typedef void *vkhip_stream_t; /* hipStream_t; NULL = the library's own default stream */
+typedef void *vkhip_event_t;  /* hipEvent_t */
+typedef void *vkhip_graph_t;  /* hipGraphExec_t */
+
+/* ---------------------------------------------------------------- runtime */
+int         vkhip_init(void);      /* select device 0, create the default stream */
+int         vkhip_available(void); /* 1 when a gfx950 device is present and usable */
+int         vkhip_device_info(char *name, int name_len, int *cu_count, int *clock_khz, size_t *hbm_bytes);
+const char *vkhip_last_error(void);
+const char *vkhip_build_info(void);
+
+int vkhip_malloc(void **p, size_t bytes);
+int vkhip_free(void *p);
+int vkhip_memcpy_h2d(void *dst, const void *src, size_t bytes, vkhip_stream_t s);
+int vkhip_memcpy_d2h(void *dst, const void *src, size_t bytes, vkhip_stream_t s);
+int vkhip_memcpy_d2d(void *dst, const void *src, size_t bytes, vkhip_stream_t s);
+/* Zero `bytes` with a fill kernel (safe inside a captured graph, unlike a memset node). */
+int vkhip_fill_zero(void *p, size_t bytes, vkhip_stream_t s);
+
+int vkhip_stream_create(vkhip_stream_t *s);
+int vkhip_stream_destroy(vkhip_stream_t s);
+int vkhip_stream_sync(vkhip_stream_t s);
+int vkhip_device_sync(void);
+
+int vkhip_event_create(vkhip_event_t *e);
+int vkhip_event_destroy(vkhip_event_t e);
+int vkhip_event_record(vkhip_event_t e, vkhip_stream_t s);
+int vkhip_event_sync(vkhip_event_t e);
+int vkhip_event_elapsed_ms(vkhip_event_t start, vkhip_event_t stop, float *ms);
+
+/* Stream capture into an executable graph (the analogue of a pre-recorded command buffer). */
+int vkhip_graph_begin(vkhip_stream_t s);
+int vkhip_graph_end(vkhip_stream_t s, vkhip_graph_t *g);
+int vkhip_graph_launch(vkhip_graph_t g, vkhip_stream_t s);
+int vkhip_graph_destroy(vkhip_graph_t g);
+
+/* ---------------------------------------------------------------- activations */
+#define VKHIP_ACT_NONE 0
+#define VKHIP_ACT_RELU 1
+#define VKHIP_ACT_RELU6 2
+#define VKHIP_ACT_CLIP 3
+#define VKHIP_ACT_HARDSWISH 4
+#define VKHIP_ACT_SILU 5
+
+/* ---------------------------------------------------------------- pack / unpack
+ * NCHW fp32 (host or device memory the kernel can read) <-> NC4HW4 fp16 on the device.
+ * The fp32->fp16 rounding is bit-identical to the reference host codec floatToHalf
+ * (include/vknn/dtype.h:121-157: half-away-from-zero on the dropped bits, NaN -> sign|0x7E00,
+ * overflow -> inf, underflow below 2^-25 -> 0), so a device pack equals the reference host pack
+ * (vk_backend.cpp:576-611) bit for bit. Unpack is exact. */
+int vkhip_pack_nchw_f32(const float *src, void *dst, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s);
+int vkhip_unpack_nchw_f32(const void *src, float *dst, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s);
+/* Flat (row-major) variants: a straight element-wise convert (vk_backend.cpp:559-575, 637-651). */
+int vkhip_pack_flat_f32(const float *src, void *dst, int64_t n, vkhip_stream_t s);
+int vkhip_unpack_flat_f32(const void *src, float *dst, int64_t n, vkhip_stream_t s);
+
+/* ---------------------------------------------------------------- convolution
+ * One descriptor covers dense (group 1) and depthwise (group == Cin == Cout) 2-D convolution
+ * with a fused epilogue y = act(conv(x) + bias (+ residual)). OH/OW are the caller's (ONNX rule
+ * OH = (H + pad_top + pad_bottom - (DH*(KH-1)+1))/SH + 1); only pad_top/pad_left matter. */
+typedef struct vkhip_conv_desc {
+    int32_t N, Cin, H, W;
+    int32_t Cout, OH, OW;
+    int32_t KH, KW, SH, SW, PT, PL, DH, DW;
+    int32_t group;
+    int32_t act;
+    float   act_lo, act_hi;
+    int32_t has_res; /* residual tensor of the output's shape is added before the activation */
+} vkhip_conv_desc;
+
+/* Algorithms. GEMM is the implicit-GEMM MFMA kernel (any KHxKW/stride/pad/dilation, group 1);
+ * SPLITK splits its reduction over `ksplit` workgroups and reduces fp32 partials in a second pass;
+ * WINOGRAD is F(2x2,3x3) (3x3 s1 p1 d1 only): input transform, 16 batched MFMA GEMMs, output
+ * transform; DEPTHWISE is the bandwidth kernel for group == C. */
+#define VKHIP_CONV_AUTO 0
+#define VKHIP_CONV_GEMM 1
+#define VKHIP_CONV_SPLITK 2
+#define VKHIP_CONV_WINOGRAD 3
+#define VKHIP_CONV_DEPTHWISE 4
+
+typedef struct vkhip_conv_plan {
+    int32_t algo;            /* one of VKHIP_CONV_* (never AUTO once planned) */
+    int32_t tile;            /* GEMM tile configuration index (see vkhip_conv_tile_count) */
+    int32_t ksplit;          /* split-K parts (SPLITK only) */
+    int32_t reserved;
+    size_t  weight_bytes;    /* size of the packed weight blob */
+    size_t  workspace_bytes; /* device scratch the forward call needs (0 = none) */
+} vkhip_conv_plan;
+
+/* Fill `plan` for `algo` (AUTO picks by shape heuristics). `tile` < 0 picks the default tile. */
+int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, int32_t ksplit, vkhip_conv_plan *plan);
+int vkhip_conv_tile_count(void);
+/* Host-side prepack: fp32 OIHW weights [Cout][Cin/group][KH][KW] and optional fp32 bias[Cout]
+ * into the blob the plan's kernel reads (bias stays fp32; weights become fp16, RNE). */
+int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const float *w, const float *bias, void *blob);
+/* y = act(conv(x) + bias (+ res)). x, y, res: NC4HW4 fp16 device tensors. */
+int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob,
+                       const void *res, void *y, void *workspace, vkhip_stream_t s);
+
+/* ---------------------------------------------------------------- fused depthwise + 1x1 project
+ * Reference FusedDwPw (src/backend/cpu/ops/fused_dwpw.cpp:10-87): t = dw_act(dwconv(x) + dw_b)
+ * with dw_act in {None, Relu, Relu6}; y = act(W_pw t + pw_b (+ res)). The E-channel intermediate
+ * stays on chip. The descriptor's Cin/Cout/act describe the dw stage (Cout == Cin == E). */
+typedef struct vkhip_dwpw_desc {
+    vkhip_conv_desc dw;
+    int32_t         Cout;
+    int32_t         act;
+    float           act_lo, act_hi;
+    int32_t         has_res;
+} vkhip_dwpw_desc;
+int    vkhip_dwpw_supported(const vkhip_dwpw_desc *d);
+size_t vkhip_dwpw_weight_bytes(const vkhip_dwpw_desc *d);
+int    vkhip_dwpw_pack_weights(const vkhip_dwpw_desc *d, const float *dw_w, const float *dw_b, const float *pw_w,
+                               const float *pw_b, void *blob);
+int    vkhip_dwpw_forward(const vkhip_dwpw_desc *d, const void *x, const void *blob, const void *res, void *y, vkhip_stream_t s);
+
+/* ---------------------------------------------------------------- squeeze-excite + pooling
+ * Global average pool: x [N,C,H,W] -> y [N,C,1,1] (both NC4HW4 fp16; fp32 accumulation). */
+int vkhip_global_avg_pool(const void *x, void *y, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s);
+/* Fused SE middle (reference FusedSE, src/backend/cpu/ops/fused_se.cpp:9-47):
+ * s = clamp(alpha*(W2 relu(W1 avg + b1) + b2) + beta, 0, 1). avg/y: NC4HW4 fp16 [N,C,1,1].
+ * Blob: fp32 W1[Cr][C], b1[Cr], W2[C][Cr], b2[C] (vkhip_se_weight_bytes). */
+size_t vkhip_se_weight_bytes(int64_t C, int64_t Cr);
+int    vkhip_se_pack_weights(int64_t C, int64_t Cr, const float *w1, const float *b1, const float *w2, const float *b2, void *blob);
+int    vkhip_fused_se(const void *avg, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr, float alpha, float beta,
+                      vkhip_stream_t s);
+/* y = x * scale[n,c] (channel broadcast; reference Binary Mul BCAST, ops/binary.cpp:32-43). */
+int vkhip_channel_scale(const void *x, const void *scale, void *y, int64_t N, int64_t C, int64_t HW, vkhip_stream_t s);
+
+/* ---------------------------------------------------------------- element-wise
+ * y = act(a + b) over `n` packed fp16 elements (reference Add same-shape path, add.cpp:67-86). */
+int vkhip_add(const void *a, const void *b, void *y, int64_t n, int32_t act, float lo, float hi, vkhip_stream_t s);
+/* y = op(x) on `n` packed fp16 elements; op is a vknn UnaryType code (Sigmoid 0, HardSwish 2,
+ * HardSigmoid 3 with alpha/beta in p0/p1, Relu 13, SiLU 14) or, with unary = -1, a clip to [p0,p1]. */
+int vkhip_unary(const void *x, void *y, int64_t n, int32_t unary, float p0, float p1, vkhip_stream_t s);
+/* Element-wise binary on equal shapes (BinaryType code: Mul 0, Sub 1, Div 2, Max 3, Min 4, Add 6). */
+int vkhip_binary(const void *a, const void *b, void *y, int64_t n, int32_t op, vkhip_stream_t s);
+
+/* ---------------------------------------------------------------- whole-network data movement */
+typedef struct vkhip_pool_desc {
+    int32_t N, C, H, W, OH, OW, KH, KW, SH, SW, PT, PL;
+} vkhip_pool_desc;
+int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s);
+/* Fully connected y[N,M] = act(x[N,K] W^T + b): x/y are [N,C,1,1] NC4HW4 fp16 tensors.
+ * Blob: fp16 W[M][K padded to 8] followed by fp32 b[M] (vkhip_fc_weight_bytes). */
+size_t vkhip_fc_weight_bytes(int64_t K, int64_t M);
+int    vkhip_fc_pack_weights(int64_t K, int64_t M, const float *w, int32_t transB, const float *b, float alpha, float beta, void *blob);
+int    vkhip_fc(const void *x, const void *blob, void *y, int64_t N, int64_t K, int64_t M, int32_t act, float lo, float hi,
+                vkhip_stream_t s);
+/* Channel concat of `count` NC4HW4 inputs (any channel counts) into y. */
+int vkhip_concat_channels(const void *const *xs, const int64_t *cs, int32_t count, void *y, int64_t N, int64_t HW,
+                          vkhip_stream_t s);
+/* Channel slice [c0, c0+C) of x (Cx channels) into y (C channels). */
+int vkhip_slice_channels(const void *x, void *y, int64_t N, int64_t Cx, int64_t c0, int64_t C, int64_t HW, vkhip_stream_t s);
+/* Nearest-neighbour resize (ONNX asymmetric/floor): y[oy,ox] = x[floor(oy*H/OH), floor(ox*W/OW)]. */
+int vkhip_resize_nearest(const void *x, void *y, int64_t N, int64_t C, int64_t H, int64_t W, int64_t OH, int64_t OW,
+                         vkhip_stream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VKHIP_H */

@@ -1,0 +1,3 @@
+// Forwarding header kept so code that includes the reference header name compiles unchanged.
+#pragma once
+#include "vknn/backend.h"

@@ -1,0 +1,79 @@
+// Runtime configuration. Mirrors the reference Config (config_struct.h:13-94), BackendKind
+// (backend_kind.h:7), Precision (precision.h:11), Hint/Mode (hint.h:8-26) and CacheMode
+// (cache_mode.h:10). BackendKind gains one enumerator, Hip, for the MI355X backend; the existing
+// values keep their numbers.
+#pragma once
+#include "vknn/types.h"
+#include <string>
+#include <vector>
+
+namespace vknn {
+
+    enum class BackendKind { Vulkan = 0, Cpu = 1, Hip = 2 };
+    const char *backendName(BackendKind k);
+    // "vulkan"/"gpu" -> Vulkan, "hip"/"rocm" -> Hip, anything else -> Cpu (reference config.cpp:19-25
+    // maps unknown strings to CPU; "hip" is the one new spelling).
+    BackendKind backendFromStr(const std::string &s);
+
+    enum class Precision { Low = 0, Normal = 1, High = 2 };
+    Precision precisionFromStr(const std::string &s);
+
+    enum class CacheMode { Off = 0, Tune = 1, Full = 2 };
+
+    enum class Hint { Winograd = 0, Tuning = 1, WinogradVariant = 2, WinogradUnit = 3, DirectConv3x3 = 4 };
+    enum class Mode {
+        Auto = 0, On = 1, Off = 2,
+        NoTune = 0, Fast = 1, Thorough = 2,
+        TiledGemm = 0, Fused = 1, FusedSplit = 2, FullyFused = 3, SubgroupGemm = 4,
+        F23 = 0, F43 = 4,
+        DirectAuto = 0, RegisterTiled = 1, LdsHalo = 2,
+    };
+    Mode winogradFromStr(const std::string &s);
+    Mode tuningFromStr(const std::string &s);
+
+    struct Config {
+        BackendKind              backend          = BackendKind::Hip;
+        std::vector<BackendKind> fallback         = {};
+        // The HIP build ships no CPU backend: a node the HIP backend cannot run is an Unsupported
+        // error, never a silent host fallback.
+        bool                     allowCpuFallback = false;
+
+        Precision precision = Precision::Low;
+
+        std::string cacheFile;
+        std::string cacheDir  = "";
+        CacheMode   cacheMode = CacheMode::Full;
+        bool        cachesPipeline() const { return cacheMode != CacheMode::Off; }
+        bool        cachesTuning() const { return cacheMode != CacheMode::Off; }
+        bool        cachesWeights() const { return cacheMode == CacheMode::Full; }
+
+        bool        freeWeightsAfterUpload = true;
+        int         maxSubmitNodes         = 500;
+        bool        noFlatOps              = false;
+        bool        timing                 = false;
+        bool        debugSegments          = false;
+        std::string disableVkOps;
+        std::string dumpTensors;
+        std::string fp32Tensors;
+        bool        profile      = false;
+        int         verbosity    = 1;
+        bool        layerDump    = false;
+        std::string layerDumpDir = "";
+
+        // HIP backend: capture each segment's launch sequence into a HIP graph after the first run
+        // and replay it (the analogue of the reference's pre-recorded command buffer).
+        bool hipGraphs = true;
+        // Fusion passes the reference exposes only as compiler flags (passes.h:33-40).
+        bool fuseDwPw          = false;
+        bool fuseSqueezeExcite = false;
+
+        std::vector<int> hints;
+        void setHint(Hint h, int value) {
+            if ((int) h >= (int) hints.size()) hints.resize((int) h + 1, 0);
+            hints[(int) h] = value;
+        }
+        void setHint(Hint h, Mode v) { setHint(h, (int) v); }
+        int  hint(Hint h, int dflt = 0) const { return (int) h < (int) hints.size() ? hints[(int) h] : dflt; }
+    };
+
+} // namespace vknn

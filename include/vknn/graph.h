@@ -1,0 +1,34 @@
+// The graph IR (backend-agnostic; every tensor is logically NCHW). Mirrors the reference's
+// Graph (include/vknn/graph.h:11-41): tensors indexed by TensorId, topologically ordered nodes,
+// name lookup, graph inputs/outputs and initializer host data keyed by tensor id.
+#pragma once
+#include "vknn/types.h"
+#include <map>
+#include <string>
+#include <vector>
+
+namespace vknn {
+
+    class Graph {
+      public:
+        std::vector<TensorDesc>         tensors;
+        std::vector<Node>               nodes;
+        std::map<std::string, TensorId> tensorByName;
+        std::vector<TensorId>           inputs;
+        std::vector<TensorId>           outputs;
+        std::map<TensorId, HostBuffer>  initializers;
+
+        TensorId findOrAdd(const std::string &name);
+        TensorId find(const std::string &name) const;
+        TensorId addTensor(TensorDesc d);
+        bool     isInitializer(TensorId id) const { return initializers.count(id) > 0; }
+
+        const TensorDesc &desc(TensorId id) const { return tensors[id]; }
+        TensorDesc       &desc(TensorId id) { return tensors[id]; }
+
+        // Stable topological sort of nodes by tensor dependencies. Throws on a cycle.
+        void        topoSort();
+        std::string dump() const;
+    };
+
+} // namespace vknn

@@ -1,0 +1,55 @@
+/*
+ * vknn_c — a C ABI over the vknn Session with the HIP backend, for callers that cannot use the
+ * C++ API (Python ctypes in the tests and the benchmark). The reference has no C API; its public
+ * surface is the C++ Session/Model (include/vknn/session_class.h:18-85, model_class.h:14-54).
+ * These entry points wrap exactly that: build a graph (here: a named model from the built-in
+ * zoo), Session::create with BackendKind::Hip, run.
+ *
+ * Options string: ';'-separated key=value pairs, all optional:
+ *   winograd=auto|on|off   tuning=off|fast|thorough   graphs=0|1   profile=0|1
+ *   fuse_dwpw=0|1          fuse_se=0|1
+ */
+#ifndef VKNN_C_H
+#define VKNN_C_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct vknn_session_s *vknn_session;
+
+const char *vknn_last_error(void);
+
+/* Input shape (4 dims) and the number of outputs / their element counts of a zoo model. */
+int vknn_model_io(const char *model, int64_t batch, int64_t *in_shape4, int64_t *out_elems, int32_t *n_out, int32_t max_out);
+/* Algorithmic conv + FC FLOPs per image of a zoo model. */
+double vknn_model_flops(const char *model);
+
+int vknn_session_create_model(const char *model, int64_t batch, uint64_t seed, const char *options, vknn_session *out);
+int vknn_session_destroy(vknn_session s);
+/* Host path: x (NCHW fp32) in, all outputs (NCHW fp32, concatenated in graph order) out. */
+int vknn_session_run_host(vknn_session s, const float *x, int64_t nx, float *y, int64_t ny);
+/* Device path: the input is read from device memory (NCHW fp32, e.g. from vkhip_malloc); the run
+ * is enqueued on the session stream and returns without waiting. */
+int vknn_session_bind_device_input(vknn_session s, const float *dev_x);
+int vknn_session_run_device(vknn_session s);
+int vknn_session_sync(vknn_session s);
+/* Device pointer of output k (NCHW fp32, valid after a run completes). */
+const float *vknn_session_device_output(vknn_session s, int32_t k);
+int vknn_session_read_outputs(vknn_session s, float *y, int64_t ny);
+void *vknn_session_stream(vknn_session s);
+/* Per-op profile of the last profiled run (JSON array) and the per-op kernel plan (text). */
+int vknn_session_profile_json(vknn_session s, char *buf, int64_t cap);
+int vknn_session_describe(vknn_session s, char *buf, int64_t cap);
+/* Number of nodes of one op type (e.g. "Conv", "FusedDwPw") in the session's planned graph. */
+int vknn_session_count_ops(vknn_session s, const char *op_type_name);
+/* Host only (no device needed): run the standard passes on a zoo model and write the resulting
+ * node list, one node per line: "<OpType> <name> act=<ActType> res=<0|1> out=<shape>". */
+int vknn_graph_after_passes(const char *model, int64_t batch, const char *options, char *buf, int64_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

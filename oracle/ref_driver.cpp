@@ -1,0 +1,168 @@
+// TEST INFRASTRUCTURE — a C entry layer over the REFERENCE's own CPU backend, compiled from the
+// reference sources under /root/reference by oracle/Makefile into oracle/_ref/libvknn_ref.so.
+// It is used to pin the oracle restatement (bit-exact comparisons on the same inputs) and to
+// write the golden fixtures under tests/golden/. Built against the reference headers only; the
+// model graphs come from the same zoo source the product uses (vknn_amd/csrc/host/model_zoo.cpp),
+// which compiles against either header set.
+#include "vknn/graph.h"
+#include "vknn/session.h"
+#include "model_zoo.h"
+#include <cstring>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#define REF_API extern "C" __attribute__((visibility("default")))
+
+using namespace vknn;
+
+namespace {
+    std::string g_err;
+
+    int runSession(Graph &&g, const std::vector<std::vector<float>> &ins, float *y, int64_t ny, int64_t *yshape) {
+        Config cfg;
+        cfg.backend          = BackendKind::Cpu;
+        cfg.fallback         = {};
+        cfg.cacheMode        = CacheMode::Off;
+        cfg.verbosity        = 0;
+        std::unique_ptr<Session> s;
+        try {
+            s = Session::create(std::move(g), cfg);
+        } catch (const std::exception &e) {
+            g_err = e.what();
+            return 1;
+        }
+        if (!s) {
+            g_err = "Session::create failed";
+            return 1;
+        }
+        std::vector<IOTensor> outs;
+        Status                st = s->run(ins, outs);
+        if (st != Status::Ok) {
+            g_err = std::string("run: ") + statusStr(st);
+            return 1;
+        }
+        int64_t off = 0;
+        for (auto &o: outs) {
+            int64_t n = numElements(o.shape);
+            if (off + n > ny) {
+                g_err = "output buffer too small";
+                return 1;
+            }
+            std::memcpy(y + off, o.f32(), (size_t) n * 4);
+            if (yshape && off == 0)
+                for (size_t k = 0; k < 4; ++k) yshape[k] = k < o.shape.size() ? o.shape[k] : 1;
+            off += n;
+        }
+        return 0;
+    }
+
+    // "i:group=1;l:strides=1,1;f:alpha=1.0;s:mode=nearest"
+    Attributes parseAttrs(const char *spec) {
+        Attributes        a;
+        std::stringstream ss(spec ? spec : "");
+        std::string       item;
+        while (std::getline(ss, item, ';')) {
+            if (item.size() < 3 || item[1] != ':') continue;
+            char        kind = item[0];
+            auto        eq   = item.find('=');
+            std::string k = item.substr(2, eq - 2), v = item.substr(eq + 1);
+            Attr        at;
+            if (kind == 'i') {
+                at.kind = Attr::Int;
+                at.i    = std::stoll(v);
+            } else if (kind == 'f') {
+                at.kind = Attr::Float;
+                at.f    = std::stof(v);
+            } else if (kind == 's') {
+                at.kind = Attr::String;
+                at.str  = v;
+            } else {
+                at.kind = Attr::Ints;
+                std::stringstream vs(v);
+                std::string       t;
+                while (std::getline(vs, t, ',')) at.ints.push_back(std::stoll(t));
+            }
+            a.map[k] = at;
+        }
+        return a;
+    }
+} // namespace
+
+REF_API const char *ref_last_error(void) { return g_err.c_str(); }
+
+REF_API void ref_float_to_half_n(const float *src, uint16_t *dst, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) dst[i] = floatToHalf(src[i]);
+}
+REF_API void ref_half_to_float_n(const uint16_t *src, float *dst, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) dst[i] = halfToFloat(src[i]);
+}
+
+REF_API int ref_model_run(const char *name, int64_t batch, uint64_t seed, const float *x, int64_t nx, float *y, int64_t ny) {
+    Graph g = vknn_zoo::build(name, batch, seed);
+    if (g.nodes.empty()) {
+        g_err = "unknown model";
+        return 1;
+    }
+    return runSession(std::move(g), {std::vector<float>(x, x + nx)}, y, ny, nullptr);
+}
+
+// One node of type `op` (vknn OpType code) through the reference Session on the CPU backend.
+// Input 0 is the graph input; inputs 1.. are initializers (is_init[k] = 1) — or, with is_init[k]
+// = 0, a second graph input is not supported (all extra inputs are constants). Shapes: 4 dims per
+// input (rank[k] dims used). fused_res >= 0 names the input index fused as the conv residual.
+REF_API int ref_single_node(int op, int sub_op, int fused_act, float act_lo, float act_hi, const char *attrs, int n_in,
+                            const float *const *data, const int64_t *shapes, const int32_t *ranks, int fused_res, int n_out,
+                            float *y, int64_t ny, int64_t *yshape) {
+    Graph g;
+    std::vector<TensorId> ids;
+    for (int k = 0; k < n_in; ++k) {
+        TensorDesc d;
+        d.name = "in" + std::to_string(k);
+        for (int r = 0; r < ranks[k]; ++r) d.shape.push_back(shapes[4 * k + r]);
+        if (!data[k]) {
+            ids.push_back(kNoTensor);
+            continue;
+        }
+        bool isInput  = (k == 0) || (k == fused_res);
+        d.isInput       = isInput;
+        d.isInitializer = !isInput;
+        TensorId id     = g.addTensor(d);
+        if (isInput) {
+            g.inputs.push_back(id);
+        } else {
+            HostBuffer hb;
+            int64_t    n = numElements(d.shape);
+            if (ranks[k] == 0) n = 1;
+            hb.resizeElems(n, DType::Float32);
+            std::memcpy(hb.f32(), data[k], (size_t) n * 4);
+            g.initializers[id] = hb;
+        }
+        ids.push_back(id);
+    }
+    Node nd;
+    nd.type     = (OpType) op;
+    nd.name     = "op";
+    nd.subOp    = sub_op;
+    nd.fusedAct = (ActType) fused_act;
+    nd.actLo    = act_lo;
+    nd.actHi    = act_hi;
+    nd.attr     = parseAttrs(attrs);
+    nd.inputs   = ids;
+    if (fused_res >= 0) nd.fusedResidual = ids[fused_res];
+    for (int o = 0; o < n_out; ++o) {
+        TensorDesc d;
+        d.name     = "y" + std::to_string(o);
+        d.isOutput = true;
+        TensorId y = g.addTensor(d);
+        nd.outputs.push_back(y);
+        g.outputs.push_back(y);
+    }
+    g.nodes.push_back(nd);
+    std::vector<std::vector<float>> ins;
+    for (TensorId t: g.inputs) {
+        for (int k = 0; k < n_in; ++k)
+            if (ids[k] == t) ins.emplace_back(data[k], data[k] + numElements(g.desc(t).shape));
+    }
+    return runSession(std::move(g), ins, y, ny, yshape);
+}

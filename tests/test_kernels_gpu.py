@@ -1,0 +1,422 @@
+"""Kernel-level parity of the HIP path against the CPU oracle, through the vkhip C ABI.
+
+Bar (north star): pack/unpack/layout bit-exact; fp16 conv outputs max|d|/max|ref| <= 2e-2 and
+cosine >= 0.9999 against the oracle on the same seeded inputs (the oracle sees the fp16-rounded
+input the kernel sees; weights stay fp32 in the oracle, fp16 on the device).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import vknn_amd as V
+from tests.gpu_helpers import (DeviceBuffer, check, conv_desc, from_device_nc4, gpu_conv, raw_nc4, round_half,
+                               to_device_nc4)
+from tests.oracle_lib import (oracle, oracle_conv, oracle_dwpw, oracle_pack, oracle_unpack, parity)
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL, COS_TOL = 2e-2, 0.9999
+
+
+def assert_parity(got, ref, what=""):
+    rel, cos = parity(got, ref)
+    print(f"{what}: max_rel={rel:.2e} cos={cos:.7f}", flush=True)
+    assert rel <= REL_TOL and cos >= COS_TOL, (what, rel, cos)
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------- pack / unpack (bit-exact)
+EDGE = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.996, 65520.0, -65520.0, 1e9, -1e9, np.inf, -np.inf, np.nan,
+                 6.1035156e-05, 6.0975552e-05, 5.9604645e-08, 2.9802322e-08, 2.9802326e-08, 1e-10, -3e-8,
+                 1.00048828125, 1.0009765625, 1.00146484375, 2049.0, 2051.0, 0.1, 1.0 / 3.0], np.float32)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1, 1), (1, 3, 5, 7), (2, 5, 3, 3), (2, 6, 4, 9), (1, 7, 11, 2),
+                                   (3, 64, 14, 14), (1, 3, 224, 224)])
+def test_pack_bitexact(gpu, shape):
+    x = rng(1).standard_normal(shape).astype(np.float32) * 300
+    flat = x.ravel()
+    flat[:min(flat.size, EDGE.size)] = EDGE[:min(flat.size, EDGE.size)]
+    buf = to_device_nc4(x)
+    got = raw_nc4(buf, shape)
+    want = oracle_pack(x)
+    nan = np.isnan(x).any()
+    assert np.array_equal(got, want), f"pack mismatch at {np.nonzero(got != want)[0][:10]} (nan={nan})"
+    back = from_device_nc4(buf, shape)
+    assert np.array_equal(back.view(np.uint32), oracle_unpack(want, shape).view(np.uint32))
+
+
+def test_pack_exhaustive_rounding_boundaries(gpu):
+    """Every fp32 bit pattern whose low 13 bits sit on a rounding boundary, for all sign/exponent/
+    high-mantissa values (2^19 * 6 inputs): device pack == oracle codec bit for bit."""
+    hi = np.arange(1 << 19, dtype=np.uint32) << 13
+    lows = np.array([0, 1, 0x0FFF, 0x1000, 0x1001, 0x1FFF], np.uint32)
+    bits = (hi[:, None] | lows[None, :]).ravel()
+    x = bits.view(np.float32).reshape(1, 1, 1, -1)
+    x4 = np.zeros((1, 4, 1, x.shape[-1]), np.float32)
+    x4[0, 0] = x[0, 0]
+    buf = to_device_nc4(x4)
+    got = raw_nc4(buf, x4.shape).reshape(-1, 4)[:, 0]
+    want = np.zeros(bits.size, np.uint16)
+    oracle().oracle_float_to_half_n(x.ctypes.data, want.ctypes.data, bits.size)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [(hex(bits[i]), hex(got[i]), hex(want[i])) for i in bad[:8]]
+
+
+def test_flat_pack_unpack(gpu):
+    x = rng(2).standard_normal(1003).astype(np.float32) * 1000
+    src = DeviceBuffer.from_array(x)
+    dst = DeviceBuffer(x.size * 2)
+    check(V.vkhip().vkhip_pack_flat_f32(src.ptr, dst.ptr, x.size, None))
+    check(V.vkhip().vkhip_stream_sync(None))
+    got = dst.download(np.uint16, x.size)
+    want = np.zeros(x.size, np.uint16)
+    oracle().oracle_float_to_half_n(x.ctypes.data, want.ctypes.data, x.size)
+    assert np.array_equal(got, want)
+    back = DeviceBuffer(x.size * 4)
+    check(V.vkhip().vkhip_unpack_flat_f32(dst.ptr, back.ptr, x.size, None))
+    check(V.vkhip().vkhip_stream_sync(None))
+    ref = np.zeros(x.size, np.float32)
+    oracle().oracle_half_to_float_n(want.ctypes.data, ref.ctypes.data, x.size)
+    assert np.array_equal(back.download(np.float32, x.size), ref)
+
+
+# ---------------------------------------------------------------- dense conv (implicit GEMM on MFMA)
+# (N, Cin, H, W, Cout, K, stride, pad, act, residual)
+CONV_CASES = [
+    (1, 64, 56, 56, 64, 3, 1, 1, 1, False),     # config 0 shape
+    (1, 24, 56, 56, 144, 1, 1, 0, 2, False),    # MNv2 expand
+    (2, 144, 14, 14, 24, 1, 1, 0, 0, True),     # MNv2 project + residual
+    (2, 64, 28, 28, 256, 1, 1, 0, 1, True),     # ResNet 1x1 + residual + relu
+    (2, 256, 14, 14, 512, 1, 2, 0, 0, False),   # ResNet downsample 1x1 s2
+    (2, 128, 28, 28, 128, 3, 2, 1, 1, False),   # ResNet v1.5 3x3 s2
+    (1, 3, 64, 64, 64, 7, 2, 3, 1, False),      # stem 7x7 s2 (Cin=3)
+    (1, 3, 32, 32, 16, 3, 2, 1, 4, False),      # MNv3 stem, HardSwish
+    (2, 16, 20, 20, 32, 3, 1, 1, 5, False),     # YOLO 3x3 SiLU
+    (1, 40, 9, 9, 20, 3, 1, 1, 3, False),       # clip act, ragged channels
+    (1, 5, 7, 7, 7, 3, 1, 1, 0, False),         # odd everything
+    (1, 512, 7, 7, 2048, 1, 1, 0, 1, True),     # deep 1x1 at 7x7
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=lambda c: "x".join(map(str, c[:6])) + f"s{c[6]}a{c[8]}r{int(c[9])}")
+def test_conv_auto(gpu, case):
+    N, C, H, W, Cout, K, s, p, act, has_res = case
+    r = rng(hash(case) & 0xFFFF)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, K, K)) * np.sqrt(2.0 / (C * K * K))).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    OH = (H + 2 * p - K) // s + 1
+    res = round_half(r.standard_normal((N, Cout, OH, OH))) if has_res else None
+    lo, hi = (-0.5, 0.7) if act == 3 else (0.0, 0.0)
+    got, plan, _ = gpu_conv(x, w, b, (s, s), (p, p, p, p), act=act, lo=lo, hi=hi, res=res)
+    ref = oracle_conv(x, w, b, (s, s), (p, p, p, p), res=res, act=act, lo=lo, hi=hi)
+    assert_parity(got, ref, f"conv {case} algo={plan.algo} tile={plan.tile}")
+
+
+@pytest.mark.parametrize("tile", range(8))
+def test_conv_every_tile(gpu, tile):
+    r = rng(10 + tile)
+    x = round_half(r.standard_normal((2, 48, 17, 19)))
+    w = (r.standard_normal((72, 48, 3, 3)) * 0.1).astype(np.float32)
+    b = (r.standard_normal(72) * 0.1).astype(np.float32)
+    got, _, _ = gpu_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1, algo=V.CONV_GEMM, tile=tile)
+    ref = oracle_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1)
+    assert_parity(got, ref, f"tile {tile}")
+
+
+@pytest.mark.parametrize("tile", [0, 3, 6])
+def test_conv_every_tile_1x1_aligned(gpu, tile):
+    r = rng(20 + tile)
+    x = round_half(r.standard_normal((3, 64, 9, 9)))
+    w = (r.standard_normal((96, 64, 1, 1)) * 0.1).astype(np.float32)
+    got, _, _ = gpu_conv(x, w, None, act=0, algo=V.CONV_GEMM, tile=tile)
+    assert_parity(got, oracle_conv(x, w), f"1x1 tile {tile}")
+
+
+@pytest.mark.parametrize("ksplit", [2, 3, 8, 16])
+def test_conv_splitk(gpu, ksplit):
+    r = rng(30 + ksplit)
+    x = round_half(r.standard_normal((1, 512, 7, 7)))
+    w = (r.standard_normal((128, 512, 1, 1)) * 0.05).astype(np.float32)
+    b = (r.standard_normal(128) * 0.1).astype(np.float32)
+    res = round_half(r.standard_normal((1, 128, 7, 7)))
+    got, plan, _ = gpu_conv(x, w, b, act=1, res=res, algo=V.CONV_SPLITK, tile=3, ksplit=ksplit)
+    assert plan.algo == V.CONV_SPLITK
+    assert_parity(got, oracle_conv(x, w, b, res=res, act=1), f"splitk {ksplit}")
+
+
+@pytest.mark.parametrize("shape", [(1, 64, 56, 56, 64), (2, 32, 13, 15, 40), (1, 256, 14, 14, 256), (2, 512, 7, 7, 512)])
+def test_conv_winograd(gpu, shape):
+    N, C, H, W, Cout = shape
+    r = rng(sum(shape))
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    got, plan, _ = gpu_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1, algo=V.CONV_WINOGRAD)
+    assert plan.algo == V.CONV_WINOGRAD
+    assert_parity(got, oracle_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1), f"winograd {shape}")
+
+
+def test_conv_dilation(gpu):
+    r = rng(40)
+    x = round_half(r.standard_normal((1, 16, 15, 15)))
+    w = (r.standard_normal((16, 16, 3, 3)) * 0.2).astype(np.float32)
+    got, _, _ = gpu_conv(x, w, None, (1, 1), (2, 2, 2, 2), dil=(2, 2))
+    assert_parity(got, oracle_conv(x, w, None, (1, 1), (2, 2, 2, 2), (2, 2)), "dilated")
+
+
+def test_conv_padding_lanes_zero(gpu):
+    """Channel lanes past Cout stay +0 even with an activation that maps 0 to a nonzero value."""
+    r = rng(41)
+    x = round_half(r.standard_normal((1, 8, 6, 6)))
+    w = (r.standard_normal((6, 8, 1, 1))).astype(np.float32)
+    _, _, dy = gpu_conv(x, w, None, act=3, lo=0.5, hi=2.0)
+    raw = raw_nc4(dy, (1, 6, 6, 6)).reshape(1, 2, 6, 6, 4)
+    assert np.all(raw[:, 1, :, :, 2:] == 0)
+
+
+# ---------------------------------------------------------------- depthwise
+@pytest.mark.parametrize("k,s,C,act", [(3, 1, 144, 2), (3, 2, 72, 1), (5, 1, 120, 4), (5, 2, 40, 0), (3, 1, 6, 2)])
+def test_depthwise(gpu, k, s, C, act):
+    r = rng(50 + k * 10 + s + C)
+    x = round_half(r.standard_normal((2, C, 23, 21)))
+    w = (r.standard_normal((C, 1, k, k)) * 0.3).astype(np.float32)
+    b = (r.standard_normal(C) * 0.1).astype(np.float32)
+    p = k // 2
+    got, plan, _ = gpu_conv(x, w, b, (s, s), (p, p, p, p), group=C, act=act)
+    assert plan.algo == V.CONV_DEPTHWISE
+    assert_parity(got, oracle_conv(x, w, b, (s, s), (p, p, p, p), group=C, act=act), f"dw k{k} s{s}")
+
+
+def test_depthwise_dilated_generic(gpu):
+    r = rng(55)
+    x = round_half(r.standard_normal((1, 12, 16, 16)))
+    w = (r.standard_normal((12, 1, 3, 3)) * 0.3).astype(np.float32)
+    got, _, _ = gpu_conv(x, w, None, (1, 1), (2, 2, 2, 2), dil=(2, 2), group=12)
+    assert_parity(got, oracle_conv(x, w, None, (1, 1), (2, 2, 2, 2), (2, 2), group=12), "dw dilated")
+
+
+# ---------------------------------------------------------------- fused dw + pw
+@pytest.mark.parametrize("N,E,H,k,s,Cout,dw_act,act,res", [(2, 144, 14, 3, 1, 24, 2, 0, True),
+                                                           (1, 960, 7, 5, 1, 160, 1, 0, False),
+                                                           (3, 72, 11, 3, 2, 40, 0, 1, False),
+                                                           (1, 22, 9, 3, 1, 10, 2, 3, True)])
+def test_fused_dwpw(gpu, N, E, H, k, s, Cout, dw_act, act, res):
+    lib = V.vkhip()
+    r = rng(E + Cout + H)
+    x = round_half(r.standard_normal((N, E, H, H)))
+    dw_w = (r.standard_normal((E, 1, k, k)) * 0.3).astype(np.float32)
+    dw_b = (r.standard_normal(E) * 0.1).astype(np.float32)
+    pw_w = (r.standard_normal((Cout, E)) * np.sqrt(1.0 / E)).astype(np.float32)
+    pw_b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    p = k // 2
+    OH = (H + 2 * p - k) // s + 1
+    resid = round_half(r.standard_normal((N, Cout, OH, OH))) if res else None
+    lo, hi = (-0.3, 0.4) if act == 3 else (0.0, 0.0)
+    dwd, _ = conv_desc(x.shape, (E, 1, k, k), (s, s), (p, p, p, p), group=E, act=dw_act, lo=0.0, hi=6.0)
+    d = V.DwPwDesc(dw=dwd, Cout=Cout, act=act, act_lo=lo, act_hi=hi, has_res=int(res))
+    assert lib.vkhip_dwpw_supported(ctypes.byref(d)) == 1
+    blob = np.zeros(lib.vkhip_dwpw_weight_bytes(ctypes.byref(d)), np.uint8)
+    check(lib.vkhip_dwpw_pack_weights(ctypes.byref(d), dw_w.ctypes.data, dw_b.ctypes.data, pw_w.ctypes.data,
+                                      pw_b.ctypes.data, blob.ctypes.data))
+    dblob = DeviceBuffer.from_array(blob)
+    dx = to_device_nc4(x)
+    dres = to_device_nc4(resid) if res else None
+    yshape = (N, Cout, OH, OH)
+    dy = DeviceBuffer(V.nc4_elems(*yshape) * 2)
+    check(lib.vkhip_dwpw_forward(ctypes.byref(d), dx.ptr, dblob.ptr, dres.ptr if dres else None, dy.ptr, None))
+    check(lib.vkhip_stream_sync(None))
+    got = from_device_nc4(dy, yshape)
+    ref = oracle_dwpw(x, dw_w, dw_b, pw_w, pw_b, (s, s), (p, p, p, p), dw_act=dw_act, res=resid, act=act, lo=lo, hi=hi)
+    assert_parity(got, ref, f"dwpw E{E} k{k} s{s}")
+
+
+# ---------------------------------------------------------------- SE + pooling + element-wise
+def test_gap_se_scale(gpu):
+    lib = V.vkhip()
+    o = oracle()
+    r = rng(60)
+    N, C, H, Cr = 3, 120, 14, 32
+    x = round_half(r.standard_normal((N, C, H, H)))
+    dx = to_device_nc4(x)
+    davg = DeviceBuffer(V.nc4_elems(N, C, 1, 1) * 2)
+    check(lib.vkhip_global_avg_pool(dx.ptr, davg.ptr, N, C, H, H, None))
+    avg_ref = np.zeros((N, C), np.float32)
+    o.oracle_global_avg_pool(x.ctypes.data, avg_ref.ctypes.data, N, C, H * H)
+    avg = from_device_nc4(davg, (N, C, 1, 1)).reshape(N, C)
+    assert_parity(avg, avg_ref, "gap")
+    w1 = (r.standard_normal((Cr, C)) * 0.2).astype(np.float32)
+    b1 = (r.standard_normal(Cr) * 0.1).astype(np.float32)
+    w2 = (r.standard_normal((C, Cr)) * 0.2).astype(np.float32)
+    b2 = (r.standard_normal(C) * 0.1).astype(np.float32)
+    blob = np.zeros(lib.vkhip_se_weight_bytes(C, Cr), np.uint8)
+    check(lib.vkhip_se_pack_weights(C, Cr, w1.ctypes.data, b1.ctypes.data, w2.ctypes.data, b2.ctypes.data, blob.ctypes.data))
+    dblob = DeviceBuffer.from_array(blob)
+    ds = DeviceBuffer(V.nc4_elems(N, C, 1, 1) * 2)
+    check(lib.vkhip_fused_se(davg.ptr, dblob.ptr, ds.ptr, N, C, Cr, 1.0 / 6.0, 0.5, None))
+    avg16 = round_half(avg)
+    s_ref = np.zeros((N, C), np.float32)
+    o.oracle_fused_se(avg16.ctypes.data, N, C, w1.ctypes.data, Cr, b1.ctypes.data, w2.ctypes.data, b2.ctypes.data,
+                      1.0 / 6.0, 0.5, s_ref.ctypes.data)
+    s = from_device_nc4(ds, (N, C, 1, 1)).reshape(N, C)
+    assert_parity(s, s_ref, "fused_se")
+    dy = DeviceBuffer(V.nc4_elems(N, C, H, H) * 2)
+    check(lib.vkhip_channel_scale(dx.ptr, ds.ptr, dy.ptr, N, C, H * H, None))
+    y = from_device_nc4(dy, (N, C, H, H))
+    y_ref = np.zeros_like(x)
+    s16 = round_half(s)
+    o.oracle_mul_channel(x.ctypes.data, s16.ctypes.data, y_ref.ctypes.data, N, C, H * H)
+    assert_parity(y, y_ref, "channel scale")
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3, 4, 5])
+def test_add_act(gpu, act):
+    lib = V.vkhip()
+    r = rng(70 + act)
+    shape = (2, 13, 9, 7)
+    a = round_half(r.standard_normal(shape) * 4)
+    b = round_half(r.standard_normal(shape) * 4)
+    da, db = to_device_nc4(a), to_device_nc4(b)
+    dy = DeviceBuffer(V.nc4_elems(*shape) * 2)
+    check(lib.vkhip_add(da.ptr, db.ptr, dy.ptr, V.nc4_elems(*shape), act, -1.0, 2.0, None))
+    ref = np.zeros(a.size, np.float32)
+    oracle().oracle_add(a.ctypes.data, b.ctypes.data, ref.ctypes.data, a.size, act, -1.0, 2.0)
+    assert_parity(from_device_nc4(dy, shape), ref, f"add act{act}")
+
+
+@pytest.mark.parametrize("op,p0,p1", [(0, 0, 0), (2, 0, 0), (3, 1.0 / 6, 0.5), (13, 0, 0), (14, 0, 0), (-1, -0.5, 1.5)])
+def test_unary(gpu, op, p0, p1):
+    lib = V.vkhip()
+    shape = (1, 10, 5, 5)
+    x = round_half(rng(80).standard_normal(shape) * 4)
+    dx = to_device_nc4(x)
+    dy = DeviceBuffer(V.nc4_elems(*shape) * 2)
+    check(lib.vkhip_unary(dx.ptr, dy.ptr, V.nc4_elems(*shape), op, p0, p1, None))
+    ref = np.zeros(x.size, np.float32)
+    oracle().oracle_unary(x.ctypes.data, ref.ctypes.data, x.size, op, p0, p1)
+    assert_parity(from_device_nc4(dy, shape), ref, f"unary {op}")
+
+
+def test_maxpool(gpu):
+    lib = V.vkhip()
+    shape = (2, 9, 17, 17)
+    x = round_half(rng(90).standard_normal(shape))
+    for k, s, p in [(3, 2, 1), (5, 1, 2)]:
+        OH = (17 + 2 * p - k) // s + 1
+        d = V.PoolDesc(N=2, C=9, H=17, W=17, OH=OH, OW=OH, KH=k, KW=k, SH=s, SW=s, PT=p, PL=p)
+        dx = to_device_nc4(x)
+        dy = DeviceBuffer(V.nc4_elems(2, 9, OH, OH) * 2)
+        check(lib.vkhip_maxpool(ctypes.byref(d), dx.ptr, dy.ptr, None))
+        ref = np.zeros((2, 9, OH, OH), np.float32)
+        oracle().oracle_maxpool(x.ctypes.data, ref.ctypes.data, 2, 9, 17, 17, k, k, s, s, p, p, OH, OH)
+        got = from_device_nc4(dy, (2, 9, OH, OH))
+        assert np.array_equal(got, ref), f"maxpool k{k}"  # max of fp16 values is exact
+
+
+def test_fc(gpu):
+    lib = V.vkhip()
+    r = rng(100)
+    N, K, M = 5, 2048, 1000
+    x = round_half(r.standard_normal((N, K)))
+    w = (r.standard_normal((M, K)) * 0.02).astype(np.float32)
+    b = (r.standard_normal(M) * 0.1).astype(np.float32)
+    blob = np.zeros(lib.vkhip_fc_weight_bytes(K, M), np.uint8)
+    check(lib.vkhip_fc_pack_weights(K, M, w.ctypes.data, 1, b.ctypes.data, 1.0, 1.0, blob.ctypes.data))
+    dblob = DeviceBuffer.from_array(blob)
+    dx = to_device_nc4(x.reshape(N, K, 1, 1))
+    dy = DeviceBuffer(V.nc4_elems(N, M, 1, 1) * 2)
+    check(lib.vkhip_fc(dx.ptr, dblob.ptr, dy.ptr, N, K, M, 0, 0.0, 0.0, None))
+    ref = np.zeros((N, M), np.float32)
+    oracle().oracle_gemm(x.ctypes.data, w.ctypes.data, b.ctypes.data, ref.ctypes.data, N, K, M, 1, 1.0, 1.0, 0, 0, 0)
+    assert_parity(from_device_nc4(dy, (N, M, 1, 1)).reshape(N, M), ref, "fc")
+
+
+def test_concat_slice_resize(gpu):
+    lib = V.vkhip()
+    o = oracle()
+    r = rng(110)
+    N, H = 2, 6
+    parts = [round_half(r.standard_normal((N, c, H, H))) for c in (8, 6, 5, 4)]
+    dparts = [to_device_nc4(p) for p in parts]
+    cs = np.array([p.shape[1] for p in parts], np.int64)
+    Ct = int(cs.sum())
+    dy = DeviceBuffer(V.nc4_elems(N, Ct, H, H) * 2)
+    ptrs = (ctypes.c_void_p * 4)(*[d.ptr for d in dparts])
+    check(lib.vkhip_concat_channels(ptrs, cs.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), 4, dy.ptr, N, H * H, None))
+    got = from_device_nc4(dy, (N, Ct, H, H))
+    ref = np.concatenate(parts, axis=1)
+    assert np.array_equal(got, ref)
+    raw = raw_nc4(dy, (N, Ct, H, H)).reshape(N, -1, H, H, 4)
+    assert np.all(raw[:, -1, :, :, Ct % 4:] == 0)  # padding lanes stay zero
+    for c0, c in [(0, 8), (8, 6), (14, 9), (3, 5)]:
+        ds = DeviceBuffer(V.nc4_elems(N, c, H, H) * 2)
+        check(lib.vkhip_slice_channels(dy.ptr, ds.ptr, N, Ct, c0, c, H * H, None))
+        assert np.array_equal(from_device_nc4(ds, (N, c, H, H)), ref[:, c0:c0 + c])
+    dr = DeviceBuffer(V.nc4_elems(N, Ct, 2 * H, 2 * H) * 2)
+    check(lib.vkhip_resize_nearest(dy.ptr, dr.ptr, N, Ct, H, H, 2 * H, 2 * H, None))
+    want = np.zeros((N, Ct, 2 * H, 2 * H), np.float32)
+    o.oracle_resize_nearest(ref.ctypes.data, want.ctypes.data, N * Ct, H, H, 2 * H, 2 * H, 2)
+    assert np.array_equal(from_device_nc4(dr, (N, Ct, 2 * H, 2 * H)), want)
+
+
+def test_binary_same_shape(gpu):
+    lib = V.vkhip()
+    r = rng(120)
+    shape = (1, 9, 4, 4)
+    a = round_half(r.standard_normal(shape))
+    b = round_half(r.standard_normal(shape) + 3)
+    for op in (0, 1, 2, 3, 4, 6):
+        da, db = to_device_nc4(a), to_device_nc4(b)
+        dy = DeviceBuffer(V.nc4_elems(*shape) * 2)
+        check(lib.vkhip_binary(da.ptr, db.ptr, dy.ptr, V.nc4_elems(*shape), op, None))
+        ref = np.zeros(a.size, np.float32)
+        oracle().oracle_binary(a.ctypes.data, b.ctypes.data, ref.ctypes.data, a.size, op)
+        assert_parity(from_device_nc4(dy, shape), ref, f"binary {op}")
+
+
+def test_graph_capture_replay(gpu):
+    """A conv captured into a HIP graph replays to the eager result, several times, with eager work
+    and synchronisation between replays."""
+    lib = V.vkhip()
+    r = rng(130)
+    x = round_half(r.standard_normal((2, 64, 14, 14)))
+    w = (r.standard_normal((64, 64, 3, 3)) * 0.05).astype(np.float32)
+    eager, plan, _ = gpu_conv(x, w, None, (1, 1), (1, 1, 1, 1), act=1)
+    d, yshape = conv_desc(x.shape, w.shape, (1, 1), (1, 1, 1, 1), act=1)
+    blob = np.zeros(plan.weight_bytes, np.uint8)
+    check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(plan), w.ctypes.data, None, blob.ctypes.data))
+    dblob = DeviceBuffer.from_array(blob)
+    dx = to_device_nc4(x)
+    dy = DeviceBuffer(V.nc4_elems(*yshape) * 2)
+    s = ctypes.c_void_p()
+    check(lib.vkhip_stream_create(ctypes.byref(s)))
+    g = ctypes.c_void_p()
+    check(lib.vkhip_graph_begin(s))
+    check(lib.vkhip_conv_forward(ctypes.byref(d), ctypes.byref(plan), dx.ptr, dblob.ptr, None, dy.ptr, None, s))
+    check(lib.vkhip_graph_end(s, ctypes.byref(g)))
+    for _ in range(3):
+        dy.zero()
+        check(lib.vkhip_stream_sync(None))
+        check(lib.vkhip_graph_launch(g, s))
+        check(lib.vkhip_stream_sync(s))
+        assert np.array_equal(from_device_nc4(dy, yshape), eager)
+    check(lib.vkhip_graph_destroy(g))
+    check(lib.vkhip_stream_destroy(s))
+
+
+def test_invalid_arguments_rejected(gpu):
+    lib = V.vkhip()
+    d, _ = conv_desc((1, 8, 5, 5), (8, 8, 3, 3), (1, 1), (1, 1, 1, 1))
+    plan = V.ConvPlan()
+    d.group = 2  # grouped but not depthwise
+    assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_AUTO, -1, 0, ctypes.byref(plan)) == 2
+    d.group = 1
+    d.KH = 0
+    assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_AUTO, -1, 0, ctypes.byref(plan)) == 1
+    d2, _ = conv_desc((1, 8, 5, 5), (8, 8, 3, 3), (2, 2), (1, 1, 1, 1))
+    assert lib.vkhip_conv_plan_make(ctypes.byref(d2), V.CONV_WINOGRAD, -1, 0, ctypes.byref(plan)) == 1

@@ -1,0 +1,94 @@
+"""Network-level parity: the vknn Session on the HIP backend (through include/vknn_c.h) against the
+CPU oracle on the same seeded graphs and inputs. Bar: max|d|/max|ref| <= 2e-2, cosine >= 0.9999
+per output tensor. The input is fp32 NCHW on both sides (the HIP path packs it to fp16 itself)."""
+import numpy as np
+import pytest
+
+import vknn_amd as V
+from tests.oracle_lib import oracle_model_run, parity
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL, COS_TOL = 2e-2, 0.9999
+
+
+def check_outputs(got, ref, outs, what):
+    off = 0
+    for k, n in enumerate(outs):
+        rel, cos = parity(got[off:off + n], ref[off:off + n])
+        print(f"{what} out{k}: max_rel={rel:.2e} cos={cos:.7f}", flush=True)
+        assert rel <= REL_TOL and cos >= COS_TOL, (what, k, rel, cos)
+        off += n
+
+
+def make_input(shape, seed, uniform=False):
+    r = np.random.default_rng(seed)
+    if uniform:
+        return r.uniform(-1, 1, size=shape).astype(np.float32)
+    return r.standard_normal(shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("model,batch,opts", [
+    ("conv_tiny", 2, ""),
+    ("mnv2_tiny", 2, ""),
+    ("mnv2_tiny", 2, "fuse_dwpw=1"),
+    ("resnet_tiny", 3, ""),
+    ("resnet_tiny", 2, "winograd=on"),
+    ("mnv3_tiny", 2, ""),
+    ("mnv3_tiny", 2, "fuse_se=1;fuse_dwpw=1"),
+    ("yolo_tiny", 2, ""),
+    ("resnet_tiny", 2, "tuning=off;graphs=0"),
+])
+def test_tiny_models(gpu, model, batch, opts):
+    sess = V.Session(model, batch, seed=11, options=opts)
+    x = make_input(sess.in_shape, 5)
+    got = sess.run(x)
+    ref = oracle_model_run(model, batch, 11, x)
+    check_outputs(got, ref, sess.out_elems, f"{model}[{opts}]")
+    # a second and third run replay the captured graph and must give the same bits
+    assert np.array_equal(sess.run(x), got)
+    assert np.array_equal(sess.run(x), got)
+
+
+def test_config0_conv3x3_bn_relu(gpu):
+    sess = V.Session("conv3x3_bn_relu", 1, seed=7)
+    x = make_input(sess.in_shape, 0, uniform=True)
+    check_outputs(sess.run(x), oracle_model_run("conv3x3_bn_relu", 1, 7, x), sess.out_elems, "config0")
+
+
+@pytest.mark.parametrize("opts", ["", "fuse_dwpw=1"])
+def test_config1_mnv2_block(gpu, opts):
+    sess = V.Session("mnv2_block", 1, seed=7, options=opts)
+    x = make_input(sess.in_shape, 1)
+    check_outputs(sess.run(x), oracle_model_run("mnv2_block", 1, 7, x), sess.out_elems, f"config1[{opts}]")
+
+
+def test_config2_resnet50_b1(gpu):
+    sess = V.Session("resnet50", 1, seed=7)
+    x = make_input(sess.in_shape, 2)
+    check_outputs(sess.run(x), oracle_model_run("resnet50", 1, 7, x), sess.out_elems, "resnet50 b1")
+
+
+def test_device_input_path_matches_host_path(gpu):
+    """Binding a device-resident fp32 input gives the same bits as the host upload path."""
+    sess = V.Session("resnet_tiny", 2, seed=3)
+    x = make_input(sess.in_shape, 9)
+    host = sess.run(x)
+    dx = V.DeviceBuffer.from_array(x)
+    sess.bind_device_input(dx.ptr)
+    for _ in range(3):
+        sess.run_device()
+        sess.sync()
+        assert np.array_equal(sess.read_outputs(), host)
+
+
+def test_batch_items_independent(gpu):
+    """Item k of a batched run equals a batch-1 run on image k (convs are per-image)."""
+    sb = V.Session("resnet_tiny", 4, seed=3)
+    s1 = V.Session("resnet_tiny", 1, seed=3)
+    x = make_input(sb.in_shape, 4)
+    yb = sb.run(x).reshape(4, -1)
+    for k in (0, 3):
+        y1 = s1.run(x[k:k + 1])
+        rel, cos = parity(yb[k], y1)
+        assert rel <= 5e-3 and cos >= 0.99999, (k, rel, cos)

@@ -1,0 +1,219 @@
+// C ABI over Session + the HIP backend (declared in include/vknn_c.h).
+#include "vknn_c.h"
+#include "hip_backend.h"
+#include "model_zoo.h"
+#include "vknn/session.h"
+#include <cstring>
+#include <sstream>
+#include <string>
+
+using namespace vknn;
+
+namespace {
+    thread_local std::string g_err;
+
+    int fail(const std::string &m) {
+        g_err = m;
+        return 1;
+    }
+
+    void copyOut(const std::string &s, char *buf, int64_t cap) {
+        if (!buf || cap <= 0) return;
+        size_t n = std::min<size_t>((size_t) cap - 1, s.size());
+        std::memcpy(buf, s.data(), n);
+        buf[n] = 0;
+    }
+
+    struct Opts {
+        Config cfg;
+        Opts(const char *s) {
+            cfg.backend = BackendKind::Hip;
+            std::string str = s ? s : "";
+            std::stringstream ss(str);
+            std::string item;
+            while (std::getline(ss, item, ';')) {
+                auto eq = item.find('=');
+                if (eq == std::string::npos) continue;
+                std::string k = item.substr(0, eq), v = item.substr(eq + 1);
+                if (k == "winograd") cfg.setHint(Hint::Winograd, winogradFromStr(v));
+                else if (k == "tuning") cfg.setHint(Hint::Tuning, tuningFromStr(v));
+                else if (k == "graphs") cfg.hipGraphs = v != "0";
+                else if (k == "profile") cfg.profile = v != "0";
+                else if (k == "fuse_dwpw") cfg.fuseDwPw = v != "0";
+                else if (k == "fuse_se") cfg.fuseSqueezeExcite = v != "0";
+            }
+            // setHint resizes the hint table with zeros; keep unset knobs at their defaults.
+            if (cfg.hints.size() > (size_t) Hint::Tuning && !std::strstr(str.c_str(), "tuning=")) cfg.setHint(Hint::Tuning, Mode::Fast);
+        }
+    };
+} // namespace
+
+struct vknn_session_s {
+    std::unique_ptr<Session> sess;
+    std::string              model;
+};
+
+static hipbe::HipSegment *onlySegment(vknn_session s) {
+    auto &segs = s->sess->segments();
+    if (segs.size() != 1) throw Error(Status::Unsupported, "device I/O needs the whole graph in one HIP segment");
+    auto *h = dynamic_cast<hipbe::HipSegment *>(segs[0].get());
+    if (!h) throw Error(Status::Unsupported, "segment is not a HIP segment");
+    return h;
+}
+
+extern "C" {
+
+const char *vknn_last_error(void) { return g_err.c_str(); }
+
+int vknn_model_io(const char *model, int64_t batch, int64_t *in_shape4, int64_t *out_elems, int32_t *n_out, int32_t max_out) {
+    std::vector<int64_t> in, out;
+    if (!vknn_zoo::io_shapes(model, batch, in, out)) return fail(std::string("unknown model ") + model);
+    for (int i = 0; i < 4; ++i) in_shape4[i] = in[i];
+    *n_out = (int32_t) out.size();
+    for (int i = 0; i < (int) out.size() && i < max_out; ++i) out_elems[i] = out[i];
+    return 0;
+}
+
+double vknn_model_flops(const char *model) { return vknn_zoo::conv_flops_per_image(model); }
+
+int vknn_session_create_model(const char *model, int64_t batch, uint64_t seed, const char *options, vknn_session *out) {
+    try {
+        Graph g = vknn_zoo::build(model, batch, seed);
+        if (g.nodes.empty()) return fail(std::string("unknown model ") + model);
+        Opts o(options);
+        auto s   = new vknn_session_s();
+        s->model = model;
+        s->sess  = Session::create(std::move(g), o.cfg);
+        *out     = s;
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+int vknn_session_destroy(vknn_session s) {
+    delete s;
+    return 0;
+}
+
+int vknn_session_run_host(vknn_session s, const float *x, int64_t nx, float *y, int64_t ny) {
+    try {
+        std::vector<float> in(x, x + nx);
+        std::vector<IOTensor> outs;
+        Status st = s->sess->run(std::vector<std::vector<float>> {in}, outs);
+        if (st != Status::Ok) return fail(std::string("run failed: ") + statusStr(st));
+        int64_t off = 0;
+        for (auto &o: outs) {
+            int64_t n = numElements(o.shape);
+            if (off + n > ny) return fail("output buffer too small");
+            std::memcpy(y + off, o.f32(), (size_t) n * 4);
+            off += n;
+        }
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+int vknn_session_bind_device_input(vknn_session s, const float *dev_x) {
+    try {
+        auto *seg = onlySegment(s);
+        seg->bindDeviceInput(s->sess->graph().inputs[0], dev_x);
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+int vknn_session_run_device(vknn_session s) {
+    Status st = s->sess->runSegments();
+    return st == Status::Ok ? 0 : fail(std::string("run failed: ") + statusStr(st));
+}
+
+int vknn_session_sync(vknn_session s) {
+    try {
+        hipbe::check(vkhip_stream_sync(onlySegment(s)->stream()), "sync");
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+const float *vknn_session_device_output(vknn_session s, int32_t k) {
+    try {
+        return onlySegment(s)->deviceOutput(s->sess->graph().outputs.at(k));
+    } catch (const std::exception &e) {
+        fail(e.what());
+        return nullptr;
+    }
+}
+
+int vknn_session_read_outputs(vknn_session s, float *y, int64_t ny) {
+    try {
+        auto   *seg = onlySegment(s);
+        int64_t off = 0;
+        for (TensorId t: s->sess->graph().outputs) {
+            int64_t n = numElements(s->sess->graph().desc(t).shape);
+            if (off + n > ny) return fail("output buffer too small");
+            seg->download(t, y + off);
+            off += n;
+        }
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+void *vknn_session_stream(vknn_session s) {
+    try {
+        return onlySegment(s)->stream();
+    } catch (const std::exception &e) {
+        fail(e.what());
+        return nullptr;
+    }
+}
+
+int vknn_session_profile_json(vknn_session s, char *buf, int64_t cap) {
+    copyOut(s->sess->profiler().toJson(), buf, cap);
+    s->sess->profiler().clear();
+    return 0;
+}
+
+int vknn_session_describe(vknn_session s, char *buf, int64_t cap) {
+    std::string d;
+    for (auto &seg: s->sess->segments())
+        if (auto *h = dynamic_cast<hipbe::HipSegment *>(seg.get())) d += h->describe();
+    copyOut(d, buf, cap);
+    return 0;
+}
+
+int vknn_session_count_ops(vknn_session s, const char *op) {
+    int n = 0;
+    for (const Node &nd: s->sess->graph().nodes)
+        if (std::string(opTypeName(nd.type)) == op) ++n;
+    return n;
+}
+
+int vknn_graph_after_passes(const char *model, int64_t batch, const char *options, char *buf, int64_t cap) {
+    try {
+        Graph g = vknn_zoo::build(model, batch, 1);
+        if (g.nodes.empty()) return fail(std::string("unknown model ") + model);
+        Opts        o(options);
+        PassOptions po;
+        po.batch             = batch;
+        po.fuseDwPw          = o.cfg.fuseDwPw;
+        po.fuseSqueezeExcite = o.cfg.fuseSqueezeExcite;
+        runStandardPasses(g, po);
+        g.topoSort();
+        std::string d;
+        for (const Node &nd: g.nodes)
+            d += std::string(opTypeName(nd.type)) + " " + nd.name + " act=" + std::to_string((int) nd.fusedAct) +
+                 " res=" + std::to_string(nd.fusedResidual != kNoTensor ? 1 : 0) + " out=" + shapeStr(g.desc(nd.outputs[0]).shape) + "\n";
+        copyOut(d, buf, cap);
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+} // extern "C"

@@ -1,0 +1,835 @@
+// The HIP backend: vknn::Backend + Segment implementations that run the fused fp16 conv path on
+// MI355X through the vkhip C ABI only (no HIP headers here). Behaviour mirrors the reference's
+// Vulkan backend for this path:
+//   capability gate        src/backend/vulkan/vk_backend.cpp:173-434 (supportsNode; FusedDwPw E<=1024,
+//                          FusedSE C<=1024 Cr<=256; High precision declined)
+//   segment                vk_backend.cpp:716-1458 (device buffers per activation, boundary pack
+//                          of host NCHW fp32 into NC4HW4 fp16, one in-order queue, boundary unpack,
+//                          optional per-op timing into the profiler)
+//   conv op                src/backend/vulkan/ops/conv.cpp:342-553 (kernel classification,
+//                          weight prepack, per-shape autotune with the 3% Winograd margin)
+//   other ops              ops/fused_dwpw.cpp, ops/fused_se.cpp, ops/add.cpp, ops/binary.cpp
+// MI355X-specific: the launch sequence of a segment is captured once into a HIP graph and replayed.
+#include "hip_backend.h"
+#include "vkhip.h"
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <set>
+
+namespace vknn {
+
+    struct DeviceStorage {
+        void  *ptr   = nullptr;
+        size_t bytes = 0;
+        bool   owned = true;
+        ~DeviceStorage() {
+            if (owned && ptr) vkhip_free(ptr);
+        }
+    };
+
+    namespace hipbe {
+
+        void check(int rc, const std::string &what) {
+            if (rc) throw Error(Status::RuntimeError, what + ": " + vkhip_last_error());
+        }
+
+        DevBuf::DevBuf(size_t n): bytes(n) { check(vkhip_malloc(&ptr, std::max<size_t>(n, 256)), "device allocation"); }
+        DevBuf::~DevBuf() {
+            if (ptr) vkhip_free(ptr);
+        }
+
+        std::shared_ptr<DevBuf> upload(const void *host, size_t bytes) {
+            auto b = std::make_shared<DevBuf>(bytes);
+            check(vkhip_memcpy_h2d(b->ptr, host, bytes, nullptr), "weight upload");
+            return b;
+        }
+
+        static std::vector<int64_t> attrInts(const Node &n, const char *k, std::vector<int64_t> d) {
+            const auto &v = n.attr.getints(k);
+            return v.empty() ? d : v;
+        }
+
+        static const float *initF32(const Graph &g, TensorId id) {
+            if (id == kNoTensor) return nullptr;
+            auto it = g.initializers.find(id);
+            if (it == g.initializers.end()) throw Error(Status::Unsupported, "HIP backend needs constant weights (tensor " + g.desc(id).name + ")");
+            return it->second.f32();
+        }
+
+        static TensorId biasOf(const Node &c) {
+            if (c.inputs.size() > 2 && c.inputs[2] != c.fusedResidual) return c.inputs[2];
+            return kNoTensor;
+        }
+
+        size_t nc4Bytes(const Shape &s) { return (size_t) formatElems(TensorFormat::NC4HW4, NCHW::from(s)) * 2; }
+
+        // ------------------------------------------------------------ conv autotune cache
+        // Keyed by the conv geometry; the chosen (algo, tile, ksplit) survives across sessions in
+        // the process, like the reference's in-memory tuned table (vk_backend.cpp WeightCache).
+        struct TuneKey {
+            std::vector<int32_t> k;
+            bool operator<(const TuneKey &o) const { return k < o.k; }
+        };
+        static std::map<TuneKey, std::array<int32_t, 3>> g_tuned;
+        static std::mutex                                g_tune_mu;
+
+        static TuneKey keyOf(const vkhip_conv_desc &d, int mode) {
+            return TuneKey {{d.N, d.Cin, d.H, d.W, d.Cout, d.OH, d.OW, d.KH, d.KW, d.SH, d.SW, d.PT, d.PL, d.DH, d.DW, d.group, d.has_res, mode}};
+        }
+
+        // ------------------------------------------------------------ conv
+        struct ConvOp: HipOp {
+            vkhip_conv_desc         d {};
+            vkhip_conv_plan         plan {};
+            std::shared_ptr<DevBuf> blob, ws;
+            TensorId                in = kNoTensor, out = kNoTensor, res = kNoTensor;
+
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g = *env.graph;
+                in             = node.inputs[0];
+                out            = node.outputs[0];
+                res            = node.fusedResidual;
+                NCHW         x  = NCHW::from(g.desc(in).shape);
+                NCHW         y  = NCHW::from(g.desc(out).shape);
+                const Shape &ws_ = g.desc(node.inputs[1]).shape;
+                auto st  = attrInts(node, "strides", {1, 1});
+                auto pad = attrInts(node, "pads", {0, 0, 0, 0});
+                auto dil = attrInts(node, "dilations", {1, 1});
+                d.N = (int) x.n; d.Cin = (int) x.c; d.H = (int) x.h; d.W = (int) x.w;
+                d.Cout = (int) ws_[0]; d.OH = (int) y.h; d.OW = (int) y.w;
+                d.KH = (int) ws_[2]; d.KW = (int) ws_[3]; d.SH = (int) st[0]; d.SW = (int) st[1];
+                d.PT = (int) pad[0]; d.PL = (int) pad[1]; d.DH = (int) dil[0]; d.DW = (int) dil[1];
+                d.group = (int) node.attr.geti("group", 1);
+                d.act = (int) node.fusedAct; d.act_lo = node.actLo; d.act_hi = node.actHi;
+                d.has_res = res != kNoTensor;
+                kind  = d.group > 1 ? "dwconv" : "conv";
+                flops = 2.0 * d.N * d.Cout * (double) (d.Cin / d.group) * d.KH * d.KW * d.OH * d.OW;
+                bytes = (int64_t) (nc4Bytes(g.desc(in).shape) + nc4Bytes(g.desc(out).shape) * (d.has_res ? 2 : 1)) +
+                        (int64_t) d.Cout * (d.Cin / d.group) * d.KH * d.KW * 2;
+                const float *w = initF32(g, node.inputs[1]);
+                const float *b = initF32(g, biasOf(node));
+                choosePlan(env, w, b);
+            }
+
+            void build(const float *w, const float *b) {
+                std::vector<uint8_t> host(plan.weight_bytes);
+                check(vkhip_conv_pack_weights(&d, &plan, w, b, host.data()), "conv weight pack");
+                blob = upload(host.data(), host.size());
+                ws   = plan.workspace_bytes ? std::make_shared<DevBuf>(plan.workspace_bytes) : nullptr;
+            }
+
+            void choosePlan(SegEnv &env, const float *w, const float *b) {
+                const Config &cfg    = *env.config;
+                const int     tuning = cfg.hint(Hint::Tuning, (int) Mode::Fast);
+                const int     wino   = cfg.hint(Hint::Winograd, (int) Mode::Auto);
+                if (d.group > 1) {
+                    check(vkhip_conv_plan_make(&d, VKHIP_CONV_DEPTHWISE, -1, 0, &plan), "conv plan");
+                    build(w, b);
+                    return;
+                }
+                vkhip_conv_plan tmp;
+                const bool wino_ok = vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, -1, 0, &tmp) == VKHIP_OK && d.Cin >= 32 && d.Cout >= 32;
+                if (wino == (int) Mode::On && wino_ok) {
+                    check(vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, -1, 0, &plan), "conv plan");
+                    build(w, b);
+                    return;
+                }
+                if (tuning == (int) Mode::NoTune || !env.tunable) {
+                    check(vkhip_conv_plan_make(&d, VKHIP_CONV_AUTO, -1, 0, &plan), "conv plan");
+                    build(w, b);
+                    return;
+                }
+                TuneKey key = keyOf(d, tuning * 4 + wino);
+                {
+                    std::lock_guard<std::mutex> lk(g_tune_mu);
+                    auto it = g_tuned.find(key);
+                    if (it != g_tuned.end()) {
+                        check(vkhip_conv_plan_make(&d, it->second[0], it->second[1], it->second[2], &plan), "conv plan");
+                        build(w, b);
+                        return;
+                    }
+                }
+                // Candidates: every GEMM tile, split-K for low-parallelism shapes, Winograd if eligible.
+                std::vector<std::array<int32_t, 3>> cands;
+                const int ntiles = vkhip_conv_tile_count();
+                for (int t = 0; t < ntiles; ++t) cands.push_back({VKHIP_CONV_GEMM, t, 0});
+                vkhip_conv_plan base;
+                check(vkhip_conv_plan_make(&d, VKHIP_CONV_AUTO, -1, 0, &base), "conv plan");
+                int64_t pixels = (int64_t) d.N * d.OH * d.OW;
+                if (pixels <= 4096 || base.algo == VKHIP_CONV_SPLITK) {
+                    for (int t: {3, 6, 1})
+                        for (int ks: {2, 4, 8, 16}) cands.push_back({VKHIP_CONV_SPLITK, t, ks});
+                }
+                if (tuning != (int) Mode::Thorough) {
+                    // Fast: the heuristic pick, its neighbours and the split-K set.
+                    std::vector<std::array<int32_t, 3>> keep;
+                    for (auto &c: cands)
+                        if (c[0] == VKHIP_CONV_SPLITK || c[1] == base.tile || c[1] == 0 || c[1] == 1 || c[1] == 3 || c[1] == 5 || c[1] == 7) keep.push_back(c);
+                    cands = keep;
+                }
+                double                 best = 1e30, bestDirect = 1e30;
+                std::array<int32_t, 3> pick = {base.algo, base.tile, base.ksplit};
+                auto x  = std::make_shared<DevBuf>(nc4Bytes({d.N, d.Cin, d.H, d.W}));
+                auto yb = std::make_shared<DevBuf>(nc4Bytes({d.N, d.Cout, d.OH, d.OW}));
+                check(vkhip_fill_zero(x->ptr, x->bytes, nullptr), "tune fill");
+                check(vkhip_fill_zero(yb->ptr, yb->bytes, nullptr), "tune fill");
+                for (auto &c: cands) {
+                    vkhip_conv_plan p;
+                    if (vkhip_conv_plan_make(&d, c[0], c[1], c[2], &p)) continue;
+                    double ms = timePlan(p, w, b, x->ptr, yb->ptr);
+                    if (ms < best) {
+                        best = ms;
+                        pick = {p.algo, p.tile, p.ksplit};
+                    }
+                }
+                bestDirect = best;
+                if (wino_ok && wino != (int) Mode::Off) {
+                    vkhip_conv_plan p;
+                    if (!vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, -1, 0, &p)) {
+                        double ms = timePlan(p, w, b, x->ptr, yb->ptr);
+                        // Winograd must win by 3% (reference ops/conv.cpp:16 kWinoMargin) so timing noise
+                        // cannot flip a near-tie between kernels that round differently.
+                        if (ms < bestDirect * 0.97) pick = {p.algo, p.tile, p.ksplit};
+                    }
+                }
+                {
+                    std::lock_guard<std::mutex> lk(g_tune_mu);
+                    g_tuned[key] = pick;
+                }
+                check(vkhip_conv_plan_make(&d, pick[0], pick[1], pick[2], &plan), "conv plan");
+                build(w, b);
+            }
+
+            // min over 3 timings of 4 back-to-back launches on scratch buffers
+            double timePlan(const vkhip_conv_plan &p, const float *w, const float *b, void *x, void *y) {
+                std::vector<uint8_t> host(p.weight_bytes);
+                if (vkhip_conv_pack_weights(&d, &p, w, b, host.data())) return 1e30;
+                auto   bl  = upload(host.data(), host.size());
+                auto   wsb = p.workspace_bytes ? std::make_shared<DevBuf>(p.workspace_bytes) : nullptr;
+                vkhip_conv_desc dd = d;
+                dd.has_res = 0;
+                vkhip_event_t e0, e1;
+                check(vkhip_event_create(&e0), "event");
+                check(vkhip_event_create(&e1), "event");
+                double best = 1e30;
+                if (vkhip_conv_forward(&dd, &p, x, bl->ptr, nullptr, y, wsb ? wsb->ptr : nullptr, nullptr) == VKHIP_OK) {
+                    for (int r = 0; r < 3; ++r) {
+                        vkhip_event_record(e0, nullptr);
+                        for (int k = 0; k < 4; ++k) vkhip_conv_forward(&dd, &p, x, bl->ptr, nullptr, y, wsb ? wsb->ptr : nullptr, nullptr);
+                        vkhip_event_record(e1, nullptr);
+                        vkhip_event_sync(e1);
+                        float ms = 0;
+                        vkhip_event_elapsed_ms(e0, e1, &ms);
+                        best = std::min(best, (double) ms);
+                    }
+                }
+                check(vkhip_stream_sync(nullptr), "tune sync");
+                vkhip_event_destroy(e0);
+                vkhip_event_destroy(e1);
+                return best;
+            }
+
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                check(vkhip_conv_forward(&d, &plan, env.dev(in), blob->ptr, res != kNoTensor ? env.dev(res) : nullptr, env.dev(out),
+                                         ws ? ws->ptr : nullptr, s),
+                      "conv " + name);
+            }
+
+            std::string describe() const override {
+                static const char *algos[] = {"auto", "gemm", "splitk", "winograd", "depthwise"};
+                return std::string(algos[plan.algo]) + " tile=" + std::to_string(plan.tile) + " ksplit=" + std::to_string(plan.ksplit);
+            }
+        };
+
+        // ------------------------------------------------------------ fused dw + pw
+        struct DwPwOp: HipOp {
+            vkhip_dwpw_desc         d {};
+            std::shared_ptr<DevBuf> blob;
+            TensorId                in, out, res = kNoTensor;
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g = *env.graph;
+                in  = node.inputs[0];
+                out = node.outputs[0];
+                res = node.fusedResidual;
+                NCHW x = NCHW::from(g.desc(in).shape), y = NCHW::from(g.desc(out).shape);
+                const Shape &dws = g.desc(node.inputs[1]).shape;
+                auto st = attrInts(node, "strides", {1, 1}), pad = attrInts(node, "pads", {0, 0, 0, 0}), dil = attrInts(node, "dilations", {1, 1});
+                vkhip_conv_desc &c = d.dw;
+                c.N = (int) x.n; c.Cin = (int) x.c; c.H = (int) x.h; c.W = (int) x.w; c.Cout = (int) x.c; c.OH = (int) y.h; c.OW = (int) y.w;
+                c.KH = (int) dws[2]; c.KW = (int) dws[3]; c.SH = (int) st[0]; c.SW = (int) st[1]; c.PT = (int) pad[0]; c.PL = (int) pad[1];
+                c.DH = (int) dil[0]; c.DW = (int) dil[1]; c.group = (int) x.c; c.act = node.subOp; c.act_lo = 0; c.act_hi = 6;
+                d.Cout = (int) y.c; d.act = (int) node.fusedAct; d.act_lo = node.actLo; d.act_hi = node.actHi; d.has_res = res != kNoTensor;
+                if (!vkhip_dwpw_supported(&d)) throw Error(Status::Unsupported, "FusedDwPw shape not supported: " + name);
+                std::vector<uint8_t> host(vkhip_dwpw_weight_bytes(&d));
+                check(vkhip_dwpw_pack_weights(&d, initF32(g, node.inputs[1]), initF32(g, node.inputs[2]), initF32(g, node.inputs[3]),
+                                              initF32(g, node.inputs[4]), host.data()),
+                      "dwpw pack");
+                blob  = upload(host.data(), host.size());
+                kind  = "dwpw";
+                flops = 2.0 * c.N * c.OH * c.OW * ((double) c.Cin * c.KH * c.KW + (double) c.Cin * d.Cout);
+                bytes = (int64_t) (nc4Bytes(g.desc(in).shape) + nc4Bytes(g.desc(out).shape) * (d.has_res ? 2 : 1));
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                check(vkhip_dwpw_forward(&d, env.dev(in), blob->ptr, res != kNoTensor ? env.dev(res) : nullptr, env.dev(out), s), "dwpw " + name);
+            }
+        };
+
+        // ------------------------------------------------------------ fused SE middle
+        struct SeOp: HipOp {
+            std::shared_ptr<DevBuf> blob;
+            TensorId                in, out;
+            int64_t                 N, C, Cr;
+            float                   alpha, beta;
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g = *env.graph;
+                in  = node.inputs[0];
+                out = node.outputs[0];
+                NCHW x = NCHW::from(g.desc(in).shape);
+                N = x.n; C = x.c; Cr = g.desc(node.inputs[1]).shape[0];
+                alpha = node.actLo; beta = node.actHi;
+                std::vector<uint8_t> host(vkhip_se_weight_bytes(C, Cr));
+                check(vkhip_se_pack_weights(C, Cr, initF32(g, node.inputs[1]), initF32(g, node.inputs[2]), initF32(g, node.inputs[3]),
+                                            initF32(g, node.inputs[4]), host.data()),
+                      "se pack");
+                blob  = upload(host.data(), host.size());
+                kind  = "se";
+                flops = 4.0 * N * C * Cr;
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                check(vkhip_fused_se(env.dev(in), blob->ptr, env.dev(out), N, C, Cr, alpha, beta, s), "fused_se " + name);
+            }
+        };
+
+        // ------------------------------------------------------------ Gemm (FC head) as a 1x1 conv
+        struct GemmOp: HipOp {
+            std::unique_ptr<ConvOp> conv;
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g  = *env.graph;
+                const Shape &as = g.desc(node.inputs[0]).shape;
+                const Shape &bs = g.desc(node.inputs[1]).shape;
+                if (as.size() != 2 || node.attr.geti("transA", 0)) throw Error(Status::Unsupported, "Gemm: only A [M,K] without transA");
+                const int64_t M = as[0], K = as[1];
+                const bool    tB = node.attr.geti("transB", 0) != 0;
+                const int64_t Nn = tB ? bs[0] : bs[1];
+                const float   alpha = node.attr.getf("alpha", 1.f), beta = node.attr.getf("beta", 1.f);
+                const float  *B     = initF32(g, node.inputs[1]);
+                const float  *Cv    = node.inputs.size() > 2 ? initF32(g, node.inputs[2]) : nullptr;
+                if (Cv && numElements(g.desc(node.inputs[2]).shape) != Nn) throw Error(Status::Unsupported, "Gemm: C must be [N]");
+                std::vector<float> w((size_t) (Nn * K)), b((size_t) Nn, 0.f);
+                for (int64_t n = 0; n < Nn; ++n) {
+                    for (int64_t k = 0; k < K; ++k) w[n * K + k] = alpha * (tB ? B[n * K + k] : B[k * Nn + n]);
+                    if (Cv) b[n] = beta * Cv[n];
+                }
+                conv        = std::make_unique<ConvOp>();
+                conv->name  = name;
+                conv->in    = node.inputs[0];
+                conv->out   = node.outputs[0];
+                vkhip_conv_desc &d = conv->d;
+                d.N = (int) M; d.Cin = (int) K; d.H = d.W = 1; d.Cout = (int) Nn; d.OH = d.OW = 1; d.KH = d.KW = 1;
+                d.SH = d.SW = d.DH = d.DW = 1; d.group = 1; d.act = (int) node.fusedAct; d.act_lo = node.actLo; d.act_hi = node.actHi;
+                conv->choosePlan(env, w.data(), b.data());
+                kind  = "gemm";
+                flops = 2.0 * M * K * Nn;
+                bytes = (M * K + M * Nn + K * Nn) * 2;
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override { conv->record(env, s); }
+            std::string describe() const override { return conv->describe(); }
+        };
+
+        // ------------------------------------------------------------ element-wise & data movement
+        struct AddOp: HipOp {
+            TensorId a, b, out;
+            int64_t  n;
+            int      act;
+            float    lo, hi;
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g = *env.graph;
+                a = node.inputs[0]; b = node.inputs[1]; out = node.outputs[0];
+                if (g.desc(a).shape != g.desc(b).shape) throw Error(Status::Unsupported, "Add: only same-shape operands");
+                n = (int64_t) nc4Bytes(g.desc(out).shape) / 2;
+                act = (int) node.fusedAct; lo = node.actLo; hi = node.actHi;
+                kind = "add";
+                bytes = n * 6;
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                check(vkhip_add(env.dev(a), env.dev(b), env.dev(out), n, act, lo, hi, s), "add " + name);
+            }
+        };
+
+        struct BinaryOp: HipOp {
+            TensorId a, b, out;
+            int64_t  n = 0, N = 0, C = 0, HW = 0;
+            int      op;
+            bool     bcast = false;
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g = *env.graph;
+                a = node.inputs[0]; b = node.inputs[1]; out = node.outputs[0];
+                op = node.subOp;
+                Shape sa = g.desc(a).shape, sb = g.desc(b).shape;
+                if (sa == sb) {
+                    n = (int64_t) nc4Bytes(sa) / 2;
+                } else if ((BinaryType) op == BinaryType::Mul && sa.size() == 4 && sb.size() == 4 && sa[0] == sb[0] && sa[1] == sb[1] &&
+                           (sb[2] * sb[3] == 1 || sa[2] * sa[3] == 1)) {
+                    if (sa[2] * sa[3] == 1) std::swap(a, b), std::swap(sa, sb);
+                    bcast = true;
+                    N = sa[0]; C = sa[1]; HW = sa[2] * sa[3];
+                } else {
+                    throw Error(Status::Unsupported, "Binary: only same-shape or Mul with [N,C,1,1] broadcast");
+                }
+                kind = bcast ? "scale" : "binary";
+                bytes = (int64_t) nc4Bytes(g.desc(out).shape) * (bcast ? 2 : 3);
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                if (bcast) check(vkhip_channel_scale(env.dev(a), env.dev(b), env.dev(out), N, C, HW, s), "scale " + name);
+                else check(vkhip_binary(env.dev(a), env.dev(b), env.dev(out), n, op, s), "binary " + name);
+            }
+        };
+
+        struct UnaryOp: HipOp {
+            TensorId in, out;
+            int64_t  n;
+            int      op;
+            float    p0, p1;
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g = *env.graph;
+                in = node.inputs[0]; out = node.outputs[0];
+                n  = (int64_t) nc4Bytes(g.desc(out).shape) / 2;
+                if (node.type == OpType::Relu) {
+                    op = (int) UnaryType::Relu; p0 = p1 = 0;
+                } else if (node.type == OpType::Clip) {
+                    op = -1; p0 = -INFINITY; p1 = INFINITY;
+                    if (node.inputs.size() > 1 && node.inputs[1] != kNoTensor) p0 = initF32(g, node.inputs[1])[0];
+                    if (node.inputs.size() > 2 && node.inputs[2] != kNoTensor) p1 = initF32(g, node.inputs[2])[0];
+                    if (node.attr.has("min")) p0 = node.attr.getf("min", p0);
+                    if (node.attr.has("max")) p1 = node.attr.getf("max", p1);
+                } else {
+                    op = node.subOp; p0 = node.actLo; p1 = node.actHi;
+                }
+                kind = "unary";
+                bytes = n * 4;
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                check(vkhip_unary(env.dev(in), env.dev(out), n, op, p0, p1, s), "unary " + name);
+            }
+        };
+
+        struct GapOp: HipOp {
+            TensorId in, out;
+            NCHW     x;
+            void prepare(const Node &node, SegEnv &env) override {
+                in = node.inputs[0]; out = node.outputs[0];
+                x = NCHW::from(env.graph->desc(in).shape);
+                kind = "gap";
+                bytes = (int64_t) nc4Bytes(env.graph->desc(in).shape);
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                check(vkhip_global_avg_pool(env.dev(in), env.dev(out), x.n, x.c, x.h, x.w, s), "gap " + name);
+            }
+        };
+
+        struct MaxPoolOp: HipOp {
+            TensorId        in, out;
+            vkhip_pool_desc d {};
+            void prepare(const Node &node, SegEnv &env) override {
+                in = node.inputs[0]; out = node.outputs[0];
+                NCHW x = NCHW::from(env.graph->desc(in).shape), y = NCHW::from(env.graph->desc(out).shape);
+                auto k = attrInts(node, "kernel_shape", {1, 1}), st = attrInts(node, "strides", {1, 1}), p = attrInts(node, "pads", {0, 0, 0, 0});
+                auto dl = attrInts(node, "dilations", {1, 1});
+                if (node.attr.geti("ceil_mode", 0) || dl[0] != 1 || dl[1] != 1)
+                    throw Error(Status::Unsupported, "MaxPool: ceil_mode/dilation");
+                d.N = (int) x.n; d.C = (int) x.c; d.H = (int) x.h; d.W = (int) x.w; d.OH = (int) y.h; d.OW = (int) y.w;
+                d.KH = (int) k[0]; d.KW = (int) k[1]; d.SH = (int) st[0]; d.SW = (int) st[1]; d.PT = (int) p[0]; d.PL = (int) p[1];
+                kind = "maxpool";
+                bytes = (int64_t) (nc4Bytes(env.graph->desc(in).shape) + nc4Bytes(env.graph->desc(out).shape));
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override { check(vkhip_maxpool(&d, env.dev(in), env.dev(out), s), "maxpool " + name); }
+        };
+
+        struct ConcatOp: HipOp {
+            std::vector<TensorId> ins;
+            std::vector<int64_t>  cs;
+            TensorId              out;
+            int64_t               N, HW;
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g = *env.graph;
+                ins = node.inputs; out = node.outputs[0];
+                const Shape &os = g.desc(out).shape;
+                int64_t axis = node.attr.geti("axis", 0);
+                if (axis < 0) axis += (int64_t) os.size();
+                if (os.size() != 4 || axis != 1) throw Error(Status::Unsupported, "Concat: only 4-D channel concat");
+                for (TensorId t: ins) cs.push_back(g.desc(t).shape[1]);
+                N = os[0]; HW = os[2] * os[3];
+                kind = "concat";
+                bytes = (int64_t) nc4Bytes(os) * 2;
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                std::vector<const void *> xs;
+                for (TensorId t: ins) xs.push_back(env.dev(t));
+                check(vkhip_concat_channels(xs.data(), cs.data(), (int) xs.size(), env.dev(out), N, HW, s), "concat " + name);
+            }
+        };
+
+        struct SplitOp: HipOp {
+            TensorId              in;
+            std::vector<TensorId> outs;
+            std::vector<int64_t>  c0s, cs;
+            int64_t               N, Cx, HW;
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g = *env.graph;
+                in = node.inputs[0]; outs = node.outputs;
+                const Shape &is = g.desc(in).shape;
+                int64_t axis = node.attr.geti("axis", 0);
+                if (axis < 0) axis += (int64_t) is.size();
+                if (is.size() != 4 || axis != 1) throw Error(Status::Unsupported, "Split: only 4-D channel split");
+                N = is[0]; Cx = is[1]; HW = is[2] * is[3];
+                int64_t c0 = 0;
+                for (TensorId t: outs) {
+                    int64_t c = t == kNoTensor ? 0 : g.desc(t).shape[1];
+                    c0s.push_back(c0); cs.push_back(c);
+                    c0 += c;
+                }
+                kind = "split";
+                bytes = (int64_t) nc4Bytes(is) * 2;
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                for (size_t i = 0; i < outs.size(); ++i)
+                    if (outs[i] != kNoTensor) check(vkhip_slice_channels(env.dev(in), env.dev(outs[i]), N, Cx, c0s[i], cs[i], HW, s), "split " + name);
+            }
+        };
+
+        struct ResizeOp: HipOp {
+            TensorId in, out;
+            NCHW     x, y;
+            void prepare(const Node &node, SegEnv &env) override {
+                in = node.inputs[0]; out = node.outputs[0];
+                x = NCHW::from(env.graph->desc(in).shape); y = NCHW::from(env.graph->desc(out).shape);
+                if (node.attr.gets("mode", "nearest") != "nearest") throw Error(Status::Unsupported, "Resize: only nearest");
+                if (y.n != x.n || y.c != x.c || y.h % x.h || y.w % x.w) throw Error(Status::Unsupported, "Resize: only integer spatial upscales");
+                kind = "resize";
+                bytes = (int64_t) (nc4Bytes(env.graph->desc(in).shape) + nc4Bytes(env.graph->desc(out).shape));
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                check(vkhip_resize_nearest(env.dev(in), env.dev(out), x.n, x.c, x.h, x.w, y.h, y.w, s), "resize " + name);
+            }
+        };
+
+        // Metadata-only ops: the output aliases the input buffer (no launch).
+        struct AliasOp: HipOp {
+            void prepare(const Node &, SegEnv &) override { kind = "alias"; }
+            void record(SegEnv &, vkhip_stream_t) override {}
+        };
+
+        static bool isAliasOp(const Graph &g, const Node &nd) {
+            if (nd.type == OpType::Identity) return true;
+            if (nd.type == OpType::Flatten || nd.type == OpType::Reshape || nd.type == OpType::Squeeze || nd.type == OpType::Unsqueeze) {
+                // [N,C,1,1] <-> [N,C]: the NC4HW4 bytes are identical.
+                NCHW a = NCHW::from(g.desc(nd.inputs[0]).shape), b = NCHW::from(g.desc(nd.outputs[0]).shape);
+                return a.n == b.n && a.c == b.c && a.h * a.w == 1 && b.h * b.w == 1;
+            }
+            return false;
+        }
+
+        std::unique_ptr<HipOp> makeOp(const Graph &g, const Node &nd) {
+            if (isAliasOp(g, nd)) return std::make_unique<AliasOp>();
+            switch (nd.type) {
+                case OpType::Conv: return std::make_unique<ConvOp>();
+                case OpType::FusedDwPw: return std::make_unique<DwPwOp>();
+                case OpType::FusedSE: return std::make_unique<SeOp>();
+                case OpType::Gemm: return std::make_unique<GemmOp>();
+                case OpType::Add: return std::make_unique<AddOp>();
+                case OpType::Binary: return std::make_unique<BinaryOp>();
+                case OpType::Unary: case OpType::Relu: case OpType::Clip: return std::make_unique<UnaryOp>();
+                case OpType::GlobalAvgPool: return std::make_unique<GapOp>();
+                case OpType::MaxPool: return std::make_unique<MaxPoolOp>();
+                case OpType::Concat: return std::make_unique<ConcatOp>();
+                case OpType::Split: return std::make_unique<SplitOp>();
+                case OpType::Resize: return std::make_unique<ResizeOp>();
+                default: return nullptr;
+            }
+        }
+
+        // ------------------------------------------------------------ segment
+        HipSegment::HipSegment(const std::vector<int> &idx, Graph &g, const Config &cfg): g_(g), cfg_(cfg) {
+            nodeIdx = idx;
+            check(vkhip_stream_create(&stream_), "stream");
+            env_.graph   = &g;
+            env_.config  = &cfg;
+            env_.tunable = true;
+            env_.seg     = this;
+            // Tensors this segment touches, in first-use order.
+            std::set<TensorId> produced;
+            for (int i: idx) {
+                const Node &nd = g.nodes[i];
+                for (TensorId t: nd.outputs)
+                    if (t != kNoTensor) produced.insert(t);
+            }
+            // Device buffers: one NC4HW4 fp16 buffer per activation (aliases share their source's).
+            for (int i: idx) {
+                const Node &nd = g.nodes[i];
+                if (isAliasOp(g, nd)) {
+                    alias_[nd.outputs[0]] = resolve(nd.inputs[0]);
+                    continue;
+                }
+                for (TensorId t: nd.inputs)
+                    if (t != kNoTensor && !g.isInitializer(t) && !produced.count(t) && !bufs_.count(t)) bufs_[t] = std::make_shared<DevBuf>(nc4Bytes(g.desc(t).shape));
+                for (TensorId t: nd.outputs)
+                    if (t != kNoTensor && !bufs_.count(t)) bufs_[t] = std::make_shared<DevBuf>(nc4Bytes(g.desc(t).shape));
+            }
+            for (int i: idx) {
+                const Node &nd = g.nodes[i];
+                auto        op = makeOp(g, nd);
+                if (!op) throw Error(Status::Unsupported, std::string("HIP backend has no kernel for ") + opTypeName(nd.type) + " (" + nd.name + ")");
+                op->name = nd.name;
+                op->type = nd.type;
+                op->prepare(nd, env_);
+                ops_.push_back(std::move(op));
+            }
+            check(vkhip_stream_sync(nullptr), "prepare sync");
+        }
+
+        HipSegment::~HipSegment() {
+            if (graph_) vkhip_graph_destroy(graph_);
+            for (auto &e: events_) vkhip_event_destroy(e);
+            if (stream_) {
+                vkhip_stream_sync(stream_);
+                vkhip_stream_destroy(stream_);
+            }
+        }
+
+        TensorId HipSegment::resolve(TensorId t) const {
+            auto it = alias_.find(t);
+            while (it != alias_.end()) {
+                t  = it->second;
+                it = alias_.find(t);
+            }
+            return t;
+        }
+
+        void *HipSegment::dev(TensorId t) {
+            auto it = bufs_.find(resolve(t));
+            if (it == bufs_.end()) throw Error(Status::RuntimeError, "no device buffer for tensor " + std::to_string(t));
+            return it->second->ptr;
+        }
+
+        void *SegEnv::dev(TensorId t) { return seg->dev(t); }
+
+        void HipSegment::bindDeviceInput(TensorId t, const float *devNchw) {
+            if (extIn_[t] != devNchw) {
+                extIn_[t] = devNchw;
+                dropGraph();
+            }
+        }
+
+        void HipSegment::dropGraph() {
+            if (graph_) vkhip_graph_destroy(graph_);
+            graph_  = nullptr;
+            replay_ = 0;
+        }
+
+        // Everything the segment does on the device for one run: boundary packs, ops, boundary unpacks.
+        void HipSegment::recordAll(bool timed) {
+            for (TensorId t: boundaryInputs) {
+                const Shape &s = g_.desc(t).shape;
+                NCHW         x = NCHW::from(s);
+                const float *src = extIn_.count(t) ? extIn_[t] : (const float *) staging_[t]->ptr;
+                check(vkhip_pack_nchw_f32(src, dev(t), x.n, x.c, x.h, x.w, stream_), "pack");
+            }
+            for (size_t k = 0; k < ops_.size(); ++k) {
+                if (timed) vkhip_event_record(events_[2 * k], stream_);
+                ops_[k]->record(env_, stream_);
+                if (timed) vkhip_event_record(events_[2 * k + 1], stream_);
+            }
+            for (TensorId t: boundaryOutputs) {
+                NCHW y = NCHW::from(g_.desc(t).shape);
+                check(vkhip_unpack_nchw_f32(dev(t), (float *) outStaging_[t]->ptr, y.n, y.c, y.h, y.w, stream_), "unpack");
+            }
+        }
+
+        void HipSegment::launch(bool profile) {
+            // staging buffers for boundary tensors
+            for (TensorId t: boundaryInputs)
+                if (!extIn_.count(t) && !staging_.count(t)) staging_[t] = std::make_shared<DevBuf>((size_t) numElements(g_.desc(t).shape) * 4);
+            for (TensorId t: boundaryOutputs)
+                if (!outStaging_.count(t)) outStaging_[t] = std::make_shared<DevBuf>((size_t) numElements(g_.desc(t).shape) * 4);
+            if (profile) {
+                while (events_.size() < 2 * ops_.size()) {
+                    vkhip_event_t e;
+                    check(vkhip_event_create(&e), "event");
+                    events_.push_back(e);
+                }
+                recordAll(true);
+                return;
+            }
+            if (!cfg_.hipGraphs) {
+                recordAll(false);
+                return;
+            }
+            // First run executes eagerly; the second captures the identical sequence into a graph.
+            if (!graph_ && replay_ == 0) {
+                recordAll(false);
+                replay_ = 1;
+                return;
+            }
+            if (!graph_) {
+                check(vkhip_graph_begin(stream_), "graph capture");
+                recordAll(false);
+                check(vkhip_graph_end(stream_, &graph_), "graph capture");
+            }
+            check(vkhip_graph_launch(graph_, stream_), "graph launch");
+        }
+
+        void HipSegment::run(ExecContext &ctx) {
+            const bool profile = ctx.profiler && ctx.profiler->enabled();
+            auto       t0      = std::chrono::high_resolution_clock::now();
+            for (TensorId t: boundaryInputs) {
+                RtTensor &rt = ctx.t(t);
+                if (extIn_.count(t)) continue;
+                if (!rt.hostValid) throw Error(Status::RuntimeError, "boundary input without host data: " + g_.desc(t).name);
+                if (!staging_.count(t)) staging_[t] = std::make_shared<DevBuf>((size_t) numElements(g_.desc(t).shape) * 4);
+                check(vkhip_memcpy_h2d(staging_[t]->ptr, rt.host.f32(), (size_t) rt.elems() * 4, stream_), "input upload");
+            }
+            launch(profile);
+            for (TensorId t: boundaryOutputs) {
+                RtTensor &rt = ctx.t(t);
+                rt.shape       = g_.desc(t).shape;
+                rt.deviceValid = true;
+                rt.hostValid   = false;
+                rt.deviceFormat = TensorFormat::NC4HW4;
+                rt.deviceDtype  = DType::Float16;
+            }
+            if (profile) {
+                check(vkhip_stream_sync(stream_), "profile sync");
+                auto t1 = std::chrono::high_resolution_clock::now();
+                for (size_t k = 0; k < ops_.size(); ++k) {
+                    OpRecord r;
+                    r.name    = ops_[k]->name;
+                    r.type    = ops_[k]->type;
+                    r.backend = "HIP";
+                    float ms  = 0;
+                    vkhip_event_elapsed_ms(events_[2 * k], events_[2 * k + 1], &ms);
+                    r.gpuMs   = ms;
+                    r.flops   = ops_[k]->flops;
+                    r.bytesIO = ops_[k]->bytes;
+                    r.cpuMs   = std::chrono::duration<double, std::milli>(t1 - t0).count() / (double) ops_.size();
+                    ctx.profiler->add(r);
+                }
+            }
+        }
+
+        void HipSegment::download(TensorId t, float *dst) {
+            check(vkhip_stream_sync(stream_), "sync");
+            auto it = outStaging_.find(t);
+            if (it == outStaging_.end()) throw Error(Status::RuntimeError, "not a boundary output of this segment");
+            check(vkhip_memcpy_d2h(dst, it->second->ptr, (size_t) numElements(g_.desc(t).shape) * 4, stream_), "output download");
+        }
+
+        std::string HipSegment::describe() const {
+            std::string s;
+            for (auto &op: ops_) s += op->name + " [" + op->kind + "] " + op->describe() + "\n";
+            return s;
+        }
+
+        // ------------------------------------------------------------ backend
+        bool HipBackend::available() const { return vkhip_available() == 1; }
+
+        void HipBackend::configure(const Config &cfg) {
+            disabled_ = cfg.disableVkOps;
+            high_     = cfg.precision == Precision::High;
+        }
+
+        bool HipBackend::supports(OpType t, DType) const {
+            if (high_) return false; // fp32 storage tier is not part of this backend
+            if (!disabled_.empty() && disabled_.find(opTypeName(t)) != std::string::npos) return false;
+            switch (t) {
+                case OpType::Conv: case OpType::FusedDwPw: case OpType::FusedSE: case OpType::Gemm: case OpType::Add: case OpType::Binary:
+                case OpType::Unary: case OpType::Relu: case OpType::Clip: case OpType::GlobalAvgPool: case OpType::MaxPool:
+                case OpType::Concat: case OpType::Split: case OpType::Resize: case OpType::Flatten: case OpType::Reshape:
+                case OpType::Identity: case OpType::Squeeze: case OpType::Unsqueeze:
+                    return true;
+                default: return false;
+            }
+        }
+
+        bool HipBackend::supportsNode(const Graph &g, const Node &nd, DType dt) const {
+            if (!supports(nd.type, dt)) return false;
+            for (TensorId t: nd.inputs)
+                if (t != kNoTensor && !g.isInitializer(t) && g.desc(t).shape.empty()) return false;
+            switch (nd.type) {
+                case OpType::Conv: {
+                    if (nd.inputs.size() < 2 || !g.isInitializer(nd.inputs[1])) return false;
+                    const Shape &w = g.desc(nd.inputs[1]).shape;
+                    NCHW         x = NCHW::from(g.desc(nd.inputs[0]).shape);
+                    int64_t      grp = nd.attr.geti("group", 1);
+                    return w.size() == 4 && (grp == 1 || (grp == x.c && w[0] == x.c && w[1] == 1));
+                }
+                case OpType::FusedDwPw: return g.desc(nd.inputs[0]).shape.size() == 4 && g.desc(nd.inputs[0]).shape[1] <= 1024;
+                case OpType::FusedSE: {
+                    const Shape &f = g.desc(nd.inputs[0]).shape, &w1 = g.desc(nd.inputs[1]).shape;
+                    return f.size() == 4 && f[1] <= 1024 && !w1.empty() && w1[0] <= 256;
+                }
+                case OpType::Gemm: return nd.inputs.size() >= 2 && g.isInitializer(nd.inputs[1]) && !nd.attr.geti("transA", 0);
+                case OpType::Add: return nd.inputs.size() == 2 && g.desc(nd.inputs[0]).shape == g.desc(nd.inputs[1]).shape;
+                case OpType::Binary: {
+                    if (nd.inputs.size() != 2) return false;
+                    const Shape &a = g.desc(nd.inputs[0]).shape, &b = g.desc(nd.inputs[1]).shape;
+                    if (a == b) return nd.subOp >= 0 && nd.subOp != (int) BinaryType::Pow;
+                    return nd.subOp == (int) BinaryType::Mul && a.size() == 4 && b.size() == 4 && a[0] == b[0] && a[1] == b[1] &&
+                           (a[2] * a[3] == 1 || b[2] * b[3] == 1);
+                }
+                case OpType::Unary: {
+                    UnaryType u = (UnaryType) nd.subOp;
+                    return u == UnaryType::Sigmoid || u == UnaryType::HardSwish || u == UnaryType::HardSigmoid || u == UnaryType::Relu || u == UnaryType::SiLU;
+                }
+                case OpType::Clip:
+                    for (size_t i = 1; i < nd.inputs.size() && i < 3; ++i)
+                        if (nd.inputs[i] != kNoTensor && !g.isInitializer(nd.inputs[i])) return false;
+                    return true;
+                case OpType::Flatten: case OpType::Reshape: case OpType::Squeeze: case OpType::Unsqueeze: return isAliasOp(g, nd);
+                case OpType::Concat: return g.desc(nd.outputs[0]).shape.size() == 4 && (nd.attr.geti("axis", 0) == 1 || nd.attr.geti("axis", 0) == -3);
+                case OpType::Split: return g.desc(nd.inputs[0]).shape.size() == 4 && (nd.attr.geti("axis", 0) == 1 || nd.attr.geti("axis", 0) == -3);
+                case OpType::Resize: {
+                    const Shape &i = g.desc(nd.inputs[0]).shape, &o = g.desc(nd.outputs[0]).shape;
+                    return nd.attr.gets("mode", "nearest") == "nearest" && i.size() == 4 && o.size() == 4 && i[0] == o[0] && i[1] == o[1] &&
+                           o[2] % i[2] == 0 && o[3] % i[3] == 0;
+                }
+                default: return true;
+            }
+        }
+
+        std::unique_ptr<Segment> HipBackend::compileSegment(const std::vector<int> &idx, Graph &g, const Config &cfg) {
+            auto s     = std::make_unique<HipSegment>(idx, g, cfg);
+            s->backend = this;
+            segs_.push_back(s.get());
+            return s;
+        }
+
+        void HipBackend::toHost(RtTensor &rt, ExecContext &) {
+            if (rt.hostValid) return;
+            for (HipSegment *s: segs_)
+                if (s->ownsOutput(rt.id)) {
+                    rt.host.resizeElems(rt.elems(), DType::Float32);
+                    rt.dtype = DType::Float32;
+                    s->download(rt.id, rt.host.f32());
+                    rt.hostValid = true;
+                    return;
+                }
+            throw Error(Status::RuntimeError, "tensor has no host data and no HIP segment owns it");
+        }
+
+        const float *HipSegment::deviceOutput(TensorId t) const {
+            auto it = outStaging_.find(t);
+            return it == outStaging_.end() ? nullptr : (const float *) it->second->ptr;
+        }
+
+        bool HipSegment::ownsOutput(TensorId t) const { return outStaging_.count(t) > 0; }
+
+    } // namespace hipbe
+
+    using hipbe::HipBackend;
+    VKNN_REGISTER_BACKEND(BackendKind::Hip, HipBackend);
+
+} // namespace vknn

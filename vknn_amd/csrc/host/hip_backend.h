@@ -1,0 +1,103 @@
+// HIP backend classes (internal header of the vknn host library).
+#pragma once
+#include "vkhip.h"
+#include "vknn/backend.h"
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace vknn {
+    namespace hipbe {
+
+        void check(int rc, const std::string &what);
+
+        // RAII device allocation through the vkhip ABI.
+        struct DevBuf {
+            void  *ptr   = nullptr;
+            size_t bytes = 0;
+            explicit DevBuf(size_t n);
+            ~DevBuf();
+            DevBuf(const DevBuf &)            = delete;
+            DevBuf &operator=(const DevBuf &) = delete;
+        };
+        std::shared_ptr<DevBuf> upload(const void *host, size_t bytes);
+        size_t                  nc4Bytes(const Shape &s);
+
+        class HipSegment;
+
+        struct SegEnv {
+            const Graph  *graph   = nullptr;
+            const Config *config  = nullptr;
+            bool          tunable = true;
+            HipSegment   *seg     = nullptr;
+            void         *dev(TensorId t);
+        };
+
+        // One HIP operator: prepare = classify + prepack/upload weights (+ autotune); record =
+        // append its launches to the segment's stream.
+        struct HipOp {
+            virtual ~HipOp()                                  = default;
+            virtual void        prepare(const Node &, SegEnv &) = 0;
+            virtual void        record(SegEnv &, vkhip_stream_t) = 0;
+            virtual std::string describe() const { return ""; }
+            std::string         name, kind;
+            OpType              type  = OpType::Unknown;
+            double              flops = 0;
+            int64_t             bytes = 0;
+        };
+
+        class HipSegment: public Segment {
+          public:
+            HipSegment(const std::vector<int> &idx, Graph &g, const Config &cfg);
+            ~HipSegment() override;
+            void        run(ExecContext &ctx) override;
+            void       *dev(TensorId t);
+            // Read a boundary input straight from device memory (NCHW fp32) instead of host data.
+            void        bindDeviceInput(TensorId t, const float *devNchw);
+            // Copy a boundary output (already unpacked to NCHW fp32 on the device) to the host.
+            void        download(TensorId t, float *dst);
+            const float *deviceOutput(TensorId t) const;
+            bool        ownsOutput(TensorId t) const;
+            vkhip_stream_t stream() const { return stream_; }
+            std::string describe() const;
+            const std::vector<std::unique_ptr<HipOp>> &ops() const { return ops_; }
+
+          private:
+            TensorId resolve(TensorId t) const;
+            void     recordAll(bool timed);
+            void     launch(bool profile);
+            void     dropGraph();
+
+            Graph                                         &g_;
+            const Config                                  &cfg_;
+            SegEnv                                         env_;
+            vkhip_stream_t                                 stream_ = nullptr;
+            vkhip_graph_t                                  graph_  = nullptr;
+            int                                            replay_ = 0;
+            std::vector<std::unique_ptr<HipOp>>            ops_;
+            std::map<TensorId, std::shared_ptr<DevBuf>>    bufs_, staging_, outStaging_;
+            std::map<TensorId, TensorId>                   alias_;
+            std::map<TensorId, const float *>              extIn_;
+            std::vector<vkhip_event_t>                     events_;
+        };
+
+        class HipBackend: public Backend {
+          public:
+            BackendKind kind() const override { return BackendKind::Hip; }
+            const char *name() const override { return "HIP"; }
+            bool        available() const override;
+            void        configure(const Config &cfg) override;
+            bool        supports(OpType t, DType dt) const override;
+            bool        supportsNode(const Graph &g, const Node &nd, DType dt) const override;
+            void        toHost(RtTensor &rt, ExecContext &ctx) override;
+            std::unique_ptr<Segment> compileSegment(const std::vector<int> &idx, Graph &g, const Config &cfg) override;
+
+          private:
+            std::string               disabled_;
+            bool                      high_ = false;
+            std::vector<HipSegment *> segs_;
+        };
+
+    } // namespace hipbe
+} // namespace vknn

@@ -1,0 +1,459 @@
+// Programmatic model graphs for the fused conv path's benchmark configurations. Written only against
+// the vknn graph API so it compiles against this repository's headers and the reference's headers.
+// Topologies: ResNet-50 v1.5 (stride on the 3x3), MobileNetV2 inverted residual, MobileNetV3-Large
+// (torchvision block table, SE with make_divisible(E/4, 8)), YOLOv8n backbone + neck (C2f, SPPF,
+// nearest 2x upsample, channel concat) at width 0.25 / depth 0.33.
+#include "model_zoo.h"
+#include <cmath>
+#include <map>
+
+namespace vknn_zoo {
+
+    using namespace vknn;
+
+    float Rng::normal() {
+        double u1 = ((double) (next() >> 11) + 1.0) * (1.0 / 9007199254740992.0); // (0, 1]
+        double u2 = (double) (next() >> 11) * (1.0 / 9007199254740992.0);
+        return (float) (std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2));
+    }
+
+    namespace {
+
+        Attr ints(std::vector<int64_t> v) {
+            Attr a;
+            a.kind = Attr::Ints;
+            a.ints = std::move(v);
+            return a;
+        }
+        Attr aint(int64_t v) {
+            Attr a;
+            a.kind = Attr::Int;
+            a.i    = v;
+            return a;
+        }
+        Attr afloat(float v) {
+            Attr a;
+            a.kind = Attr::Float;
+            a.f    = v;
+            return a;
+        }
+        Attr astr(const std::string &s) {
+            Attr a;
+            a.kind = Attr::String;
+            a.str  = s;
+            return a;
+        }
+
+        struct Builder {
+            Graph  g;
+            Rng    rng;
+            int    counter = 0;
+            double flops   = 0; // conv + FC FLOPs per image, accumulated as layers are added
+            std::map<TensorId, std::vector<int64_t>> shp; // builder-side shape tracking (C,H,W per image)
+
+            explicit Builder(uint64_t seed): rng(seed) {}
+
+            std::string nm(const char *p) { return std::string(p) + "_" + std::to_string(counter++); }
+
+            TensorId tensor(const std::string &name) {
+                TensorDesc d;
+                d.name = name;
+                return g.addTensor(d);
+            }
+            TensorId init(const std::string &name, const Shape &shape, const std::vector<float> &data) {
+                TensorDesc d;
+                d.name          = name;
+                d.shape         = shape;
+                d.isInitializer = true;
+                TensorId   id   = g.addTensor(d);
+                HostBuffer hb;
+                hb.resizeElems((int64_t) data.size(), DType::Float32);
+                for (size_t i = 0; i < data.size(); ++i) hb.f32()[i] = data[i];
+                g.initializers[id] = hb;
+                return id;
+            }
+            TensorId input(const Shape &shape) {
+                TensorDesc d;
+                d.name    = "input";
+                d.shape   = shape;
+                d.isInput = true;
+                TensorId x = g.addTensor(d);
+                g.inputs.push_back(x);
+                shp[x] = {shape[1], shape[2], shape[3]};
+                return x;
+            }
+            void output(TensorId t) {
+                g.tensors[t].isOutput = true;
+                g.outputs.push_back(t);
+            }
+            Node &node(OpType t, const std::string &name, std::vector<TensorId> in, std::vector<TensorId> out) {
+                Node n;
+                n.type    = t;
+                n.name    = name;
+                n.inputs  = std::move(in);
+                n.outputs = std::move(out);
+                g.nodes.push_back(n);
+                return g.nodes.back();
+            }
+
+            // Conv (Kaiming-normal weights, std = sqrt(2/fan_in)), optional bias ~ N(0, 0.1).
+            TensorId conv(TensorId x, int64_t cout, int64_t k, int64_t s, int64_t p, int64_t group = 1, bool bias = false) {
+                auto    is  = shp[x];
+                int64_t cin = is[0];
+                int64_t icg = cin / group;
+                std::vector<float> w((size_t) (cout * icg * k * k));
+                float std_ = std::sqrt(2.0f / (float) (icg * k * k));
+                for (auto &v: w) v = rng.normal() * std_;
+                std::string n  = nm("conv");
+                TensorId    wt = init(n + "_w", {cout, icg, k, k}, w);
+                std::vector<TensorId> ins = {x, wt};
+                if (bias) {
+                    std::vector<float> b((size_t) cout);
+                    for (auto &v: b) v = rng.normal() * 0.1f;
+                    ins.push_back(init(n + "_b", {cout}, b));
+                }
+                TensorId y  = tensor(n + "_out");
+                Node    &nd = node(OpType::Conv, n, ins, {y});
+                nd.attr.map["kernel_shape"] = ints({k, k});
+                nd.attr.map["strides"]      = ints({s, s});
+                nd.attr.map["pads"]         = ints({p, p, p, p});
+                nd.attr.map["dilations"]    = ints({1, 1});
+                nd.attr.map["group"]        = aint(group);
+                int64_t oh = (is[1] + 2 * p - k) / s + 1, ow = (is[2] + 2 * p - k) / s + 1;
+                shp[y]     = {cout, oh, ow};
+                flops += 2.0 * (double) cout * (double) icg * (double) (k * k) * (double) (oh * ow);
+                return y;
+            }
+            // BatchNorm with random stats: gamma U[0.5,1.5], beta N(0,0.1), mean N(0,0.1), var U[0.5,1.5].
+            TensorId bn(TensorId x) {
+                int64_t            c = shp[x][0];
+                std::vector<float> ga(c), be(c), me(c), va(c);
+                for (int64_t i = 0; i < c; ++i) {
+                    ga[i] = rng.uniform(0.5f, 1.5f);
+                    be[i] = rng.normal() * 0.1f;
+                    me[i] = rng.normal() * 0.1f;
+                    va[i] = rng.uniform(0.5f, 1.5f);
+                }
+                std::string n = nm("bn");
+                TensorId    y = tensor(n + "_out");
+                Node &nd = node(OpType::BatchNorm, n, {x, init(n + "_g", {c}, ga), init(n + "_b", {c}, be), init(n + "_m", {c}, me), init(n + "_v", {c}, va)}, {y});
+                nd.attr.map["epsilon"] = afloat(1e-5f);
+                shp[y]                 = shp[x];
+                return y;
+            }
+            TensorId relu(TensorId x) {
+                std::string n = nm("relu");
+                TensorId    y = tensor(n + "_out");
+                node(OpType::Relu, n, {x}, {y});
+                shp[y] = shp[x];
+                return y;
+            }
+            TensorId clip(TensorId x, float lo, float hi) {
+                std::string n = nm("clip");
+                TensorId    y = tensor(n + "_out");
+                TensorId    l = init(n + "_lo", {}, {lo});
+                TensorId    h = init(n + "_hi", {}, {hi});
+                node(OpType::Clip, n, {x, l, h}, {y});
+                shp[y] = shp[x];
+                return y;
+            }
+            TensorId unary(TensorId x, UnaryType t, float a = 0, float b = 0) {
+                std::string n  = nm("unary");
+                TensorId    y  = tensor(n + "_out");
+                Node       &nd = node(OpType::Unary, n, {x}, {y});
+                nd.subOp       = (int32_t) t;
+                nd.actLo       = a;
+                nd.actHi       = b;
+                shp[y]         = shp[x];
+                return y;
+            }
+            TensorId binary(TensorId a, TensorId b, BinaryType t) {
+                std::string n  = nm("bin");
+                TensorId    y  = tensor(n + "_out");
+                Node       &nd = node(OpType::Binary, n, {a, b}, {y});
+                nd.subOp       = (int32_t) t;
+                shp[y]         = shp[a];
+                return y;
+            }
+            TensorId add(TensorId a, TensorId b) {
+                std::string n = nm("add");
+                TensorId    y = tensor(n + "_out");
+                node(OpType::Add, n, {a, b}, {y});
+                shp[y] = shp[a];
+                return y;
+            }
+            // x * HardSigmoid(x) (alpha 1/6, beta 0.5) and x * Sigmoid(x): the exported forms of
+            // HardSwish and SiLU, which the swish pass folds into the producer's epilogue.
+            TensorId hswish(TensorId x) { return binary(x, unary(x, UnaryType::HardSigmoid, 1.f / 6.f, 0.5f), BinaryType::Mul); }
+            TensorId silu(TensorId x) { return binary(x, unary(x, UnaryType::Sigmoid), BinaryType::Mul); }
+            TensorId gap(TensorId x) {
+                std::string n = nm("gap");
+                TensorId    y = tensor(n + "_out");
+                node(OpType::GlobalAvgPool, n, {x}, {y});
+                shp[y] = {shp[x][0], 1, 1};
+                return y;
+            }
+            TensorId maxpool(TensorId x, int64_t k, int64_t s, int64_t p) {
+                std::string n  = nm("maxpool");
+                TensorId    y  = tensor(n + "_out");
+                Node       &nd = node(OpType::MaxPool, n, {x}, {y});
+                nd.attr.map["kernel_shape"] = ints({k, k});
+                nd.attr.map["strides"]      = ints({s, s});
+                nd.attr.map["pads"]         = ints({p, p, p, p});
+                auto is = shp[x];
+                shp[y]  = {is[0], (is[1] + 2 * p - k) / s + 1, (is[2] + 2 * p - k) / s + 1};
+                return y;
+            }
+            TensorId flatten(TensorId x) {
+                std::string n  = nm("flatten");
+                TensorId    y  = tensor(n + "_out");
+                Node       &nd = node(OpType::Flatten, n, {x}, {y});
+                nd.attr.map["axis"] = aint(1);
+                shp[y] = {shp[x][0] * shp[x][1] * shp[x][2], 1, 1};
+                return y;
+            }
+            // Gemm as exported from nn.Linear: B = W [M][K] with transB = 1, bias ~ N(0, 0.1).
+            TensorId gemm(TensorId x, int64_t M) {
+                int64_t            K = shp[x][0];
+                std::vector<float> w((size_t) (M * K)), b((size_t) M);
+                float              std_ = std::sqrt(1.0f / (float) K);
+                for (auto &v: w) v = rng.normal() * std_;
+                for (auto &v: b) v = rng.normal() * 0.1f;
+                std::string n  = nm("gemm");
+                TensorId    y  = tensor(n + "_out");
+                Node       &nd = node(OpType::Gemm, n, {x, init(n + "_w", {M, K}, w), init(n + "_b", {M}, b)}, {y});
+                nd.attr.map["transB"] = aint(1);
+                nd.attr.map["alpha"]  = afloat(1.f);
+                nd.attr.map["beta"]   = afloat(1.f);
+                shp[y] = {M, 1, 1};
+                flops += 2.0 * (double) M * (double) K;
+                return y;
+            }
+            TensorId concat(const std::vector<TensorId> &xs) {
+                std::string n  = nm("concat");
+                TensorId    y  = tensor(n + "_out");
+                Node       &nd = node(OpType::Concat, n, xs, {y});
+                nd.attr.map["axis"] = aint(1);
+                int64_t c = 0;
+                for (TensorId t: xs) c += shp[t][0];
+                shp[y] = {c, shp[xs[0]][1], shp[xs[0]][2]};
+                return y;
+            }
+            std::vector<TensorId> split2(TensorId x) {
+                std::string n  = nm("split");
+                TensorId    a  = tensor(n + "_a");
+                TensorId    b  = tensor(n + "_b");
+                Node       &nd = node(OpType::Split, n, {x}, {a, b});
+                nd.attr.map["axis"] = aint(1);
+                auto is = shp[x];
+                shp[a]  = {is[0] / 2, is[1], is[2]};
+                shp[b]  = shp[a];
+                return {a, b};
+            }
+            TensorId upsample2(TensorId x) {
+                std::string n  = nm("resize");
+                TensorId    y  = tensor(n + "_out");
+                TensorId    sc = init(n + "_scales", {4}, {1.f, 1.f, 2.f, 2.f});
+                Node       &nd = node(OpType::Resize, n, {x, kNoTensor, sc}, {y});
+                nd.attr.map["mode"]                           = astr("nearest");
+                nd.attr.map["coordinate_transformation_mode"] = astr("asymmetric");
+                nd.attr.map["nearest_mode"]                   = astr("floor");
+                auto is = shp[x];
+                shp[y]  = {is[0], is[1] * 2, is[2] * 2};
+                return y;
+            }
+
+            // conv + BN (+ activation) helpers
+            TensorId cbr(TensorId x, int64_t c, int64_t k, int64_t s, int64_t g = 1) { return relu(bn(conv(x, c, k, s, k / 2, g))); }
+            TensorId cb(TensorId x, int64_t c, int64_t k, int64_t s, int64_t g = 1) { return bn(conv(x, c, k, s, k / 2, g)); }
+        };
+
+        // ---------------------------------------------------------------- configs
+        void conv3x3_bn_relu(Builder &b, int64_t N, int64_t C, int64_t HW) {
+            TensorId x = b.input({N, C, HW, HW});
+            b.output(b.cbr(x, C, 3, 1));
+        }
+
+        TensorId mnv2_block(Builder &b, TensorId x, int64_t cin, int64_t E, int64_t cout, int64_t stride) {
+            TensorId h = b.bn(b.conv(x, E, 1, 1, 0));
+            h          = b.clip(h, 0.f, 6.f);
+            h          = b.clip(b.bn(b.conv(h, E, 3, stride, 1, E)), 0.f, 6.f);
+            h          = b.bn(b.conv(h, cout, 1, 1, 0));
+            if (stride == 1 && cin == cout) h = b.add(h, x);
+            return h;
+        }
+
+        TensorId bottleneck(Builder &b, TensorId x, int64_t width, int64_t stride, bool down) {
+            int64_t  out = width * 4;
+            TensorId h   = b.cbr(x, width, 1, 1);
+            h            = b.cbr(h, width, 3, stride); // v1.5: stride on the 3x3
+            h            = b.cb(h, out, 1, 1);
+            TensorId id  = down ? b.cb(x, out, 1, stride) : x;
+            return b.relu(b.add(h, id));
+        }
+
+        void resnet(Builder &b, int64_t N, int64_t HW, const std::vector<int> &blocks, int64_t base, int64_t classes) {
+            TensorId x = b.input({N, 3, HW, HW});
+            TensorId h = b.relu(b.bn(b.conv(x, base, 7, 2, 3)));
+            h          = b.maxpool(h, 3, 2, 1);
+            int64_t w  = base;
+            for (size_t L = 0; L < blocks.size(); ++L) {
+                for (int i = 0; i < blocks[L]; ++i) {
+                    int64_t s = (i == 0 && L > 0) ? 2 : 1;
+                    h         = bottleneck(b, h, w, s, i == 0);
+                }
+                w *= 2;
+            }
+            h = b.flatten(b.gap(h));
+            b.output(b.gemm(h, classes));
+        }
+
+        int64_t make_div(double v, int64_t d = 8) {
+            int64_t nv = std::max<int64_t>(d, (int64_t) (v + d / 2.0) / d * d);
+            if ((double) nv < 0.9 * v) nv += d;
+            return nv;
+        }
+
+        struct Bneck {
+            int64_t k, exp, out;
+            bool    se, hs;
+            int64_t s;
+        };
+
+        TensorId act(Builder &b, TensorId x, bool hs) { return hs ? b.hswish(x) : b.relu(x); }
+
+        TensorId squeeze_excite(Builder &b, TensorId x, int64_t E) {
+            int64_t  sq = make_div((double) E / 4.0);
+            TensorId s  = b.gap(x);
+            s           = b.relu(b.conv(s, sq, 1, 1, 0, 1, true));
+            s           = b.conv(s, E, 1, 1, 0, 1, true);
+            s           = b.unary(s, UnaryType::HardSigmoid, 1.f / 6.f, 0.5f);
+            return b.binary(x, s, BinaryType::Mul);
+        }
+
+        void mobilenetv3(Builder &b, int64_t N, int64_t HW, const std::vector<Bneck> &cfg, int64_t last, int64_t head, int64_t classes) {
+            TensorId x   = b.input({N, 3, HW, HW});
+            TensorId h   = b.hswish(b.bn(b.conv(x, 16, 3, 2, 1)));
+            int64_t  cin = 16;
+            for (const Bneck &c: cfg) {
+                TensorId in = h;
+                if (c.exp != cin) h = act(b, b.bn(b.conv(h, c.exp, 1, 1, 0)), c.hs);
+                h = act(b, b.bn(b.conv(h, c.exp, c.k, c.s, c.k / 2, c.exp)), c.hs);
+                if (c.se) h = squeeze_excite(b, h, c.exp);
+                h = b.bn(b.conv(h, c.out, 1, 1, 0));
+                if (c.s == 1 && cin == c.out) h = b.add(h, in);
+                cin = c.out;
+            }
+            h = b.hswish(b.bn(b.conv(h, last, 1, 1, 0)));
+            h = b.flatten(b.gap(h));
+            h = b.hswish(b.gemm(h, head));
+            b.output(b.gemm(h, classes));
+        }
+
+        const std::vector<Bneck> kMnv3Large = {
+            {3, 16, 16, false, false, 1},   {3, 64, 24, false, false, 2},   {3, 72, 24, false, false, 1},
+            {5, 72, 40, true, false, 2},    {5, 120, 40, true, false, 1},   {5, 120, 40, true, false, 1},
+            {3, 240, 80, false, true, 2},   {3, 200, 80, false, true, 1},   {3, 184, 80, false, true, 1},
+            {3, 184, 80, false, true, 1},   {3, 480, 112, true, true, 1},   {3, 672, 112, true, true, 1},
+            {5, 672, 160, true, true, 2},   {5, 960, 160, true, true, 1},   {5, 960, 160, true, true, 1},
+        };
+
+        // YOLOv8 building blocks (Conv = conv + BN + SiLU).
+        TensorId yconv(Builder &b, TensorId x, int64_t c, int64_t k, int64_t s) { return b.silu(b.bn(b.conv(x, c, k, s, k / 2))); }
+
+        TensorId c2f(Builder &b, TensorId x, int64_t c2, int n, bool shortcut) {
+            int64_t               c = c2 / 2;
+            TensorId              y = yconv(b, x, 2 * c, 1, 1);
+            std::vector<TensorId> parts = b.split2(y);
+            for (int i = 0; i < n; ++i) {
+                TensorId in = parts.back();
+                TensorId h  = yconv(b, yconv(b, in, c, 3, 1), c, 3, 1);
+                parts.push_back(shortcut ? b.add(in, h) : h);
+            }
+            return yconv(b, b.concat(parts), c2, 1, 1);
+        }
+
+        TensorId sppf(Builder &b, TensorId x, int64_t c2) {
+            int64_t  c  = b.shp[x][0] / 2;
+            TensorId y0 = yconv(b, x, c, 1, 1);
+            TensorId y1 = b.maxpool(y0, 5, 1, 2);
+            TensorId y2 = b.maxpool(y1, 5, 1, 2);
+            TensorId y3 = b.maxpool(y2, 5, 1, 2);
+            return yconv(b, b.concat({y0, y1, y2, y3}), c2, 1, 1);
+        }
+
+        void yolov8(Builder &b, int64_t N, int64_t HW, int64_t w0) {
+            // widths at scale n: 16, 32, 64, 128, 256 (w0 = 16)
+            TensorId x  = b.input({N, 3, HW, HW});
+            TensorId h  = yconv(b, x, w0, 3, 2);
+            h           = yconv(b, h, 2 * w0, 3, 2);
+            h           = c2f(b, h, 2 * w0, 1, true);
+            h           = yconv(b, h, 4 * w0, 3, 2);
+            TensorId p3 = c2f(b, h, 4 * w0, 2, true);
+            h           = yconv(b, p3, 8 * w0, 3, 2);
+            TensorId p4 = c2f(b, h, 8 * w0, 2, true);
+            h           = yconv(b, p4, 16 * w0, 3, 2);
+            h           = c2f(b, h, 16 * w0, 1, true);
+            TensorId p5 = sppf(b, h, 16 * w0);
+            TensorId u  = b.concat({b.upsample2(p5), p4});
+            TensorId n4 = c2f(b, u, 8 * w0, 1, false);
+            u           = b.concat({b.upsample2(n4), p3});
+            TensorId o3 = c2f(b, u, 4 * w0, 1, false);
+            u           = b.concat({yconv(b, o3, 4 * w0, 3, 2), n4});
+            TensorId o4 = c2f(b, u, 8 * w0, 1, false);
+            u           = b.concat({yconv(b, o4, 8 * w0, 3, 2), p5});
+            TensorId o5 = c2f(b, u, 16 * w0, 1, false);
+            b.output(o3);
+            b.output(o4);
+            b.output(o5);
+        }
+
+        bool build_into(Builder &b, const std::string &name, int64_t N) {
+            if (name == "conv3x3_bn_relu") conv3x3_bn_relu(b, N, 64, 56);
+            else if (name == "conv_tiny") conv3x3_bn_relu(b, N, 6, 9);
+            else if (name == "mnv2_block") {
+                TensorId x = b.input({N, 24, 56, 56});
+                b.output(mnv2_block(b, x, 24, 144, 24, 1));
+            } else if (name == "mnv2_tiny") {
+                TensorId x = b.input({N, 24, 10, 10});
+                b.output(mnv2_block(b, x, 24, 144, 24, 1));
+            } else if (name == "resnet50") resnet(b, N, 224, {3, 4, 6, 3}, 64, 1000);
+            else if (name == "resnet_tiny") resnet(b, N, 32, {1, 1, 1, 1}, 8, 10);
+            else if (name == "mobilenetv3_large") mobilenetv3(b, N, 224, kMnv3Large, 960, 1280, 1000);
+            else if (name == "mnv3_tiny") {
+                std::vector<Bneck> cfg = {{3, 16, 16, false, false, 1}, {3, 64, 24, false, false, 2}, {5, 72, 40, true, false, 2},
+                                          {3, 120, 40, true, true, 1},  {5, 240, 48, true, true, 2}};
+                mobilenetv3(b, N, 48, cfg, 96, 64, 10);
+            } else if (name == "yolov8n") yolov8(b, N, 640, 16);
+            else if (name == "yolo_tiny") yolov8(b, N, 64, 8);
+            else return false;
+            return true;
+        }
+
+    } // namespace
+
+    Graph build(const std::string &name, int64_t batch, uint64_t seed) {
+        Builder b(seed);
+        if (!build_into(b, name, batch)) return Graph();
+        return std::move(b.g);
+    }
+
+    bool io_shapes(const std::string &name, int64_t batch, std::vector<int64_t> &in, std::vector<int64_t> &out) {
+        Builder b(1);
+        if (!build_into(b, name, batch)) return false;
+        in = b.g.tensors[b.g.inputs[0]].shape;
+        out.clear();
+        for (TensorId o: b.g.outputs) {
+            auto s = b.shp[o];
+            out.push_back(batch * s[0] * s[1] * s[2]);
+        }
+        return true;
+    }
+
+    double conv_flops_per_image(const std::string &name) {
+        Builder b(1);
+        if (!build_into(b, name, 1)) return 0;
+        return b.flops;
+    }
+
+} // namespace vknn_zoo

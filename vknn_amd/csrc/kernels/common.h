@@ -1,0 +1,63 @@
+// Device-side helpers shared by the gfx950 kernels: fp16 vector types, the fused activation, the
+// launch-error plumbing used by every extern "C" launcher.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "vkhip.h"
+
+namespace vkhip {
+
+    typedef _Float16 half_t;
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+    typedef float    float4v __attribute__((ext_vector_type(4)));
+    typedef float    float16v __attribute__((ext_vector_type(16)));
+
+    // Fused activation (codes = vknn ActType). The formulas follow the reference's applyAct
+    // (src/backend/cpu/cpu_backend.cpp:33-72): HardSwish = v*clamp(v+3,0,6)/6, SiLU = v/(1+e^-v).
+    __device__ __forceinline__ float apply_act(float v, int act, float lo, float hi) {
+        switch (act) {
+            case VKHIP_ACT_RELU: return v > 0.f ? v : 0.f;
+            case VKHIP_ACT_RELU6: return v < 0.f ? 0.f : (v > 6.f ? 6.f : v);
+            case VKHIP_ACT_CLIP: return v < lo ? lo : (v > hi ? hi : v);
+            case VKHIP_ACT_HARDSWISH: {
+                float c = fminf(fmaxf(v + 3.f, 0.f), 6.f);
+                return v * c / 6.f;
+            }
+            case VKHIP_ACT_SILU: return v / (1.f + __expf(-v));
+            default: return v;
+        }
+    }
+
+    // 4 fp16 lanes <-> 4 fp32 values. The fp32 -> fp16 conversion is v_cvt_f16_f32 under the
+    // default round-to-nearest-even mode.
+    __device__ __forceinline__ float4v h4_to_f4(half4 h) {
+        float4v r;
+        r.x = (float) h.x; r.y = (float) h.y; r.z = (float) h.z; r.w = (float) h.w;
+        return r;
+    }
+    __device__ __forceinline__ half4 f4_to_h4(float4v f) {
+        half4 r;
+        r.x = (half_t) f.x; r.y = (half_t) f.y; r.z = (half_t) f.z; r.w = (half_t) f.w;
+        return r;
+    }
+    __device__ __forceinline__ half4 u2_as_h4(uint2 u) {
+        half4 h;
+        __builtin_memcpy(&h, &u, 8);
+        return h;
+    }
+    __device__ __forceinline__ uint2 h4_as_u2(half4 h) {
+        uint2 u;
+        __builtin_memcpy(&u, &h, 8);
+        return u;
+    }
+
+    // Host-side error recording (defined in runtime.hip).
+    int  set_error(int code, const char *fmt, ...);
+    int  check_launch(const char *what);
+    hipStream_t resolve_stream(vkhip_stream_t s);
+
+    inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+    inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+} // namespace vkhip

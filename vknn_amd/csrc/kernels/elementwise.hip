@@ -1,0 +1,418 @@
+// Bandwidth-bound kernels of the path: NC4HW4 pack/unpack (bit-exact with the reference host
+// codec), residual add, unary/binary element-wise ops, channel-broadcast scale (SE), global average
+// pool, the fused SE middle, max pool, channel concat/slice and nearest resize. All are coalesced
+// wave64 kernels over 8- or 16-byte vectors; none uses MFMA.
+#include "common.h"
+#include <cstring>
+
+namespace vkhip {
+
+    // fp32 -> fp16 with the reference host codec's integer rounding (include/vknn/dtype.h:121-157):
+    // half-away-from-zero on the dropped bits, carries may ripple into the exponent.
+    __device__ __forceinline__ uint16_t ref_float_to_half(float v) {
+        uint32_t bits = __float_as_uint(v);
+        uint32_t sign = (bits >> 16) & 0x8000u;
+        uint32_t fexp = (bits >> 23) & 0xFFu;
+        uint32_t man  = bits & 0x7FFFFFu;
+        if (fexp == 0xFFu) return (uint16_t) (sign | 0x7C00u | (man ? 0x200u : 0u));
+        int e = (int) fexp - 112;
+        if (e >= 31) return (uint16_t) (sign | 0x7C00u);
+        if (e > 0) return (uint16_t) ((sign | ((uint32_t) e << 10) | (man >> 13)) + ((man >> 12) & 1u));
+        if (e < -10) return (uint16_t) sign;
+        uint32_t full = man | 0x800000u;
+        uint32_t sh   = (uint32_t) (14 - e);
+        return (uint16_t) (sign | ((full >> sh) + ((full >> (sh - 1)) & 1u)));
+    }
+
+    // NCHW fp32 -> NC4HW4 fp16; thread = one (n, cb, pixel) 4-lane vector.
+    __global__ void pack_kernel(const float *src, uint2 *dst, int64_t C, int64_t HW, int64_t Cb, int64_t total) {
+        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return;
+        int64_t p  = i % HW;
+        int64_t t  = i / HW;
+        int64_t cb = t % Cb;
+        int64_t n  = t / Cb;
+        uint16_t h[4];
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            int64_t c = cb * 4 + l;
+            h[l]      = c < C ? ref_float_to_half(src[(n * C + c) * HW + p]) : (uint16_t) 0;
+        }
+        dst[i] = make_uint2((uint32_t) h[0] | ((uint32_t) h[1] << 16), (uint32_t) h[2] | ((uint32_t) h[3] << 16));
+    }
+
+    // NC4HW4 fp16 -> NCHW fp32 (exact); thread = one NCHW element, reads are 2-byte gathers.
+    __global__ void unpack_kernel(const half_t *src, float *dst, int64_t C, int64_t HW, int64_t Cb, int64_t total) {
+        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return;
+        int64_t p = i % HW;
+        int64_t t = i / HW;
+        int64_t c = t % C;
+        int64_t n = t / C;
+        dst[i]    = (float) src[((n * Cb + c / 4) * HW + p) * 4 + (c & 3)];
+    }
+
+    __global__ void pack_flat_kernel(const float *src, uint16_t *dst, int64_t n) {
+        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i < n) dst[i] = ref_float_to_half(src[i]);
+    }
+    __global__ void unpack_flat_kernel(const half_t *src, float *dst, int64_t n) {
+        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i < n) dst[i] = (float) src[i];
+    }
+
+    // y = act(a + b) over 8 fp16 per thread (16-byte vectors) plus a scalar tail.
+    __global__ void add_kernel(const half_t *a, const half_t *b, half_t *y, int64_t n, int act, float lo, float hi) {
+        int64_t i  = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) * 8;
+        if (i + 8 <= n) {
+            half8 va = *reinterpret_cast<const half8 *>(a + i);
+            half8 vb = *reinterpret_cast<const half8 *>(b + i);
+            half8 r;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) r[k] = (half_t) apply_act((float) va[k] + (float) vb[k], act, lo, hi);
+            *reinterpret_cast<half8 *>(y + i) = r;
+        } else {
+            for (int64_t k = i; k < n; ++k) y[k] = (half_t) apply_act((float) a[k] + (float) b[k], act, lo, hi);
+        }
+    }
+
+    __device__ __forceinline__ float unary_op(float v, int op, float p0, float p1) {
+        switch (op) {
+            case -1: return v < p0 ? p0 : (v > p1 ? p1 : v);      // clip
+            case 0: return 1.f / (1.f + __expf(-v));               // Sigmoid
+            case 2: return v * fminf(fmaxf(v + 3.f, 0.f), 6.f) / 6.f; // HardSwish
+            case 3: return fmaxf(0.f, fminf(1.f, p0 * v + p1));    // HardSigmoid(alpha, beta)
+            case 13: return v > 0.f ? v : 0.f;                     // Relu
+            case 14: return v / (1.f + __expf(-v));                // SiLU
+            default: return v;
+        }
+    }
+
+    __global__ void unary_kernel(const half_t *x, half_t *y, int64_t n, int op, float p0, float p1) {
+        int64_t i = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) * 8;
+        if (i + 8 <= n) {
+            half8 v = *reinterpret_cast<const half8 *>(x + i);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = (half_t) unary_op((float) v[k], op, p0, p1);
+            *reinterpret_cast<half8 *>(y + i) = v;
+        } else {
+            for (int64_t k = i; k < n; ++k) y[k] = (half_t) unary_op((float) x[k], op, p0, p1);
+        }
+    }
+
+    __device__ __forceinline__ float binary_op(float a, float b, int op) {
+        switch (op) {
+            case 0: return a * b;
+            case 1: return a - b;
+            case 2: return a / b;
+            case 3: return fmaxf(a, b);
+            case 4: return fminf(a, b);
+            default: return a + b;
+        }
+    }
+
+    __global__ void binary_kernel(const half_t *a, const half_t *b, half_t *y, int64_t n, int op) {
+        int64_t i = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) * 8;
+        if (i + 8 <= n) {
+            half8 va = *reinterpret_cast<const half8 *>(a + i);
+            half8 vb = *reinterpret_cast<const half8 *>(b + i);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) va[k] = (half_t) binary_op((float) va[k], (float) vb[k], op);
+            *reinterpret_cast<half8 *>(y + i) = va;
+        } else {
+            for (int64_t k = i; k < n; ++k) y[k] = (half_t) binary_op((float) a[k], (float) b[k], op);
+        }
+    }
+
+    // y[n,c,p] = x[n,c,p] * s[n,c]; thread = two adjacent pixels of one 4-channel block.
+    __global__ void channel_scale_kernel(const uint2 *x, const uint2 *s, uint2 *y, int64_t Cb, int64_t HW, int64_t total) {
+        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return;
+        int64_t nc = i / HW; // n*Cb + cb
+        float4v sc = h4_to_f4(u2_as_h4(s[nc]));
+        float4v v  = h4_to_f4(u2_as_h4(x[i]));
+        y[i]       = h4_as_u2(f4_to_h4(v * sc));
+    }
+
+    // One wave per (n, cb): mean over HW pixels of 4 channels (fp32 sums).
+    __global__ void gap_kernel(const uint2 *x, uint2 *y, int64_t NCb, int64_t HW) {
+        int64_t w    = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+        int     lane = threadIdx.x & 63;
+        if (w >= NCb) return;
+        const uint2 *src = x + w * HW;
+        float4v      s   = {0.f, 0.f, 0.f, 0.f};
+        for (int64_t p = lane; p < HW; p += 64) s += h4_to_f4(u2_as_h4(src[p]));
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            s.x += __shfl_xor(s.x, off);
+            s.y += __shfl_xor(s.y, off);
+            s.z += __shfl_xor(s.z, off);
+            s.w += __shfl_xor(s.w, off);
+        }
+        if (lane == 0) y[w] = h4_as_u2(f4_to_h4(s / (float) HW));
+    }
+
+    // Fused SE middle, one workgroup per image: s1 = relu(W1 avg + b1); s = clamp(alpha*(W2 s1 +
+    // b2) + beta, 0, 1). Dot products are split across the wave and reduced with shuffles.
+    __global__ __launch_bounds__(256) void fused_se_kernel(const half_t *avg, const float *blob, half_t *y, int C, int Cr,
+                                                           float alpha, float beta) {
+        extern __shared__ float sm[];
+        float *a  = sm;      // [C]
+        float *s1 = sm + C;  // [Cr]
+        const int    n  = blockIdx.x;
+        const int    Cp = ((C + 3) / 4) * 4;
+        const float *W1 = blob;
+        const float *b1 = W1 + (int64_t) Cr * C;
+        const float *W2 = b1 + Cr;
+        const float *b2 = W2 + (int64_t) C * Cr;
+        for (int c = threadIdx.x; c < C; c += blockDim.x) a[c] = (float) avg[(int64_t) n * Cp + c];
+        __syncthreads();
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+        for (int j = wave; j < Cr; j += nw) {
+            float acc = 0.f;
+            for (int c = lane; c < C; c += 64) acc += W1[(int64_t) j * C + c] * a[c];
+            for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+            if (lane == 0) {
+                float v = acc + b1[j];
+                s1[j]   = v > 0.f ? v : 0.f;
+            }
+        }
+        __syncthreads();
+        for (int k = wave; k < C; k += nw) {
+            float acc = 0.f;
+            for (int j = lane; j < Cr; j += 64) acc += W2[(int64_t) k * Cr + j] * s1[j];
+            for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+            if (lane == 0) {
+                float v = fminf(fmaxf(alpha * (acc + b2[k]) + beta, 0.f), 1.f);
+                y[(int64_t) n * Cp + k] = (half_t) v;
+            }
+        }
+        for (int k = C + threadIdx.x; k < Cp; k += blockDim.x) y[(int64_t) n * Cp + k] = (half_t) 0.f;
+    }
+
+    // Max pool over NC4HW4; out-of-image taps are skipped (reference maxpool.cpp semantics).
+    __global__ void maxpool_kernel(vkhip_pool_desc d, const uint2 *x, uint2 *y, int64_t total) {
+        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return;
+        int     ox = (int) (i % d.OW);
+        int64_t t  = i / d.OW;
+        int     oy = (int) (t % d.OH);
+        int64_t nc = t / d.OH;
+        const uint2 *src = x + nc * d.H * d.W;
+        float4v m = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        for (int ky = 0; ky < d.KH; ++ky) {
+            int iy = oy * d.SH - d.PT + ky;
+            if (iy < 0 || iy >= d.H) continue;
+            for (int kx = 0; kx < d.KW; ++kx) {
+                int ix = ox * d.SW - d.PL + kx;
+                if (ix < 0 || ix >= d.W) continue;
+                float4v v = h4_to_f4(u2_as_h4(src[iy * d.W + ix]));
+                m.x = fmaxf(m.x, v.x);
+                m.y = fmaxf(m.y, v.y);
+                m.z = fmaxf(m.z, v.z);
+                m.w = fmaxf(m.w, v.w);
+            }
+        }
+        y[i] = h4_as_u2(f4_to_h4(m));
+    }
+
+    // Channel concat / slice at 4-channel granularity when aligned, element granularity otherwise.
+    __global__ void copy_channels_kernel(const half_t *x, half_t *y, int64_t Cx, int64_t Cy, int64_t cx0, int64_t cy0,
+                                         int64_t C, int64_t HW, int64_t total) {
+        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return; // total = N * C * HW
+        int64_t p  = i % HW;
+        int64_t t  = i / HW;
+        int64_t c  = t % C;
+        int64_t n  = t / C;
+        int64_t Cbx = (Cx + 3) / 4, Cby = (Cy + 3) / 4;
+        int64_t ci = cx0 + c, co = cy0 + c;
+        y[((n * Cby + co / 4) * HW + p) * 4 + (co & 3)] = x[((n * Cbx + ci / 4) * HW + p) * 4 + (ci & 3)];
+    }
+
+    __global__ void copy_blocks_kernel(const uint2 *x, uint2 *y, int64_t Cbx, int64_t Cby, int64_t cbx0, int64_t cby0,
+                                       int64_t Cb, int64_t HW, int64_t total) {
+        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return; // total = N * Cb * HW
+        int64_t p  = i % HW;
+        int64_t t  = i / HW;
+        int64_t cb = t % Cb;
+        int64_t n  = t / Cb;
+        y[(n * Cby + cby0 + cb) * HW + p] = x[(n * Cbx + cbx0 + cb) * HW + p];
+    }
+
+    // Zero the padding lanes of the last channel block (c >= C) after an element-granular copy.
+    __global__ void zero_tail_lanes_kernel(half_t *y, int64_t C, int64_t HW, int64_t N) {
+        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+        int64_t Cb = (C + 3) / 4;
+        if (i >= N * HW) return;
+        int64_t n = i / HW, p = i % HW;
+        for (int64_t c = C; c < Cb * 4; ++c) y[((n * Cb + c / 4) * HW + p) * 4 + (c & 3)] = (half_t) 0.f;
+    }
+
+    __global__ void resize_nearest_kernel(const uint2 *x, uint2 *y, int64_t H, int64_t W, int64_t OH, int64_t OW, int64_t total) {
+        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return;
+        int64_t ox = i % OW;
+        int64_t t  = i / OW;
+        int64_t oy = t % OH;
+        int64_t nc = t / OH;
+        int64_t iy = (oy * H) / OH, ix = (ox * W) / OW;
+        y[i]       = x[(nc * H + iy) * W + ix];
+    }
+
+    static dim3 grid1(int64_t n, int bs = 256) { return dim3((unsigned) ceil_div(n, bs)); }
+
+} // namespace vkhip
+
+using namespace vkhip;
+
+extern "C" {
+
+int vkhip_pack_nchw_f32(const float *src, void *dst, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s) {
+    if (!src || !dst || N <= 0 || C <= 0 || H <= 0 || W <= 0) return set_error(VKHIP_ERR_INVALID, "pack: bad arguments");
+    int64_t Cb = ceil_div(C, 4), total = N * Cb * H * W;
+    pack_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>(src, (uint2 *) dst, C, H * W, Cb, total);
+    return check_launch("pack");
+}
+
+int vkhip_unpack_nchw_f32(const void *src, float *dst, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s) {
+    if (!src || !dst || N <= 0 || C <= 0 || H <= 0 || W <= 0) return set_error(VKHIP_ERR_INVALID, "unpack: bad arguments");
+    int64_t Cb = ceil_div(C, 4), total = N * C * H * W;
+    unpack_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>((const half_t *) src, dst, C, H * W, Cb, total);
+    return check_launch("unpack");
+}
+
+int vkhip_pack_flat_f32(const float *src, void *dst, int64_t n, vkhip_stream_t s) {
+    if (!src || !dst || n < 0) return set_error(VKHIP_ERR_INVALID, "pack_flat: bad arguments");
+    if (!n) return VKHIP_OK;
+    pack_flat_kernel<<<grid1(n), 256, 0, resolve_stream(s)>>>(src, (uint16_t *) dst, n);
+    return check_launch("pack_flat");
+}
+
+int vkhip_unpack_flat_f32(const void *src, float *dst, int64_t n, vkhip_stream_t s) {
+    if (!src || !dst || n < 0) return set_error(VKHIP_ERR_INVALID, "unpack_flat: bad arguments");
+    if (!n) return VKHIP_OK;
+    unpack_flat_kernel<<<grid1(n), 256, 0, resolve_stream(s)>>>((const half_t *) src, dst, n);
+    return check_launch("unpack_flat");
+}
+
+int vkhip_add(const void *a, const void *b, void *y, int64_t n, int32_t act, float lo, float hi, vkhip_stream_t s) {
+    if (!a || !b || !y || n < 0) return set_error(VKHIP_ERR_INVALID, "add: bad arguments");
+    if (!n) return VKHIP_OK;
+    add_kernel<<<grid1(ceil_div(n, 8)), 256, 0, resolve_stream(s)>>>((const half_t *) a, (const half_t *) b, (half_t *) y, n, act, lo, hi);
+    return check_launch("add");
+}
+
+int vkhip_unary(const void *x, void *y, int64_t n, int32_t op, float p0, float p1, vkhip_stream_t s) {
+    if (!x || !y || n < 0) return set_error(VKHIP_ERR_INVALID, "unary: bad arguments");
+    if (op != -1 && op != 0 && op != 2 && op != 3 && op != 13 && op != 14) return set_error(VKHIP_ERR_UNSUPPORTED, "unary op %d", op);
+    if (!n) return VKHIP_OK;
+    unary_kernel<<<grid1(ceil_div(n, 8)), 256, 0, resolve_stream(s)>>>((const half_t *) x, (half_t *) y, n, op, p0, p1);
+    return check_launch("unary");
+}
+
+int vkhip_binary(const void *a, const void *b, void *y, int64_t n, int32_t op, vkhip_stream_t s) {
+    if (!a || !b || !y || n < 0) return set_error(VKHIP_ERR_INVALID, "binary: bad arguments");
+    if (op < 0 || op == 5 || op > 6) return set_error(VKHIP_ERR_UNSUPPORTED, "binary op %d", op);
+    if (!n) return VKHIP_OK;
+    binary_kernel<<<grid1(ceil_div(n, 8)), 256, 0, resolve_stream(s)>>>((const half_t *) a, (const half_t *) b, (half_t *) y, n, op);
+    return check_launch("binary");
+}
+
+int vkhip_channel_scale(const void *x, const void *scale, void *y, int64_t N, int64_t C, int64_t HW, vkhip_stream_t s) {
+    if (!x || !scale || !y || N <= 0 || C <= 0 || HW <= 0) return set_error(VKHIP_ERR_INVALID, "channel_scale: bad arguments");
+    int64_t Cb = ceil_div(C, 4), total = N * Cb * HW;
+    channel_scale_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>((const uint2 *) x, (const uint2 *) scale, (uint2 *) y, Cb, HW, total);
+    return check_launch("channel_scale");
+}
+
+int vkhip_global_avg_pool(const void *x, void *y, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s) {
+    if (!x || !y || N <= 0 || C <= 0 || H <= 0 || W <= 0) return set_error(VKHIP_ERR_INVALID, "gap: bad arguments");
+    int64_t NCb = N * ceil_div(C, 4);
+    gap_kernel<<<grid1(NCb * 64), 256, 0, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, NCb, H * W);
+    return check_launch("global_avg_pool");
+}
+
+size_t vkhip_se_weight_bytes(int64_t C, int64_t Cr) { return (size_t) (2 * C * Cr + Cr + C) * 4; }
+
+int vkhip_se_pack_weights(int64_t C, int64_t Cr, const float *w1, const float *b1, const float *w2, const float *b2, void *blob) {
+    if (!w1 || !w2 || !blob || C <= 0 || Cr <= 0) return set_error(VKHIP_ERR_INVALID, "se_pack: bad arguments");
+    float *p = (float *) blob;
+    std::memcpy(p, w1, (size_t) C * Cr * 4);
+    p += C * Cr;
+    for (int64_t j = 0; j < Cr; ++j) p[j] = b1 ? b1[j] : 0.f;
+    p += Cr;
+    std::memcpy(p, w2, (size_t) C * Cr * 4);
+    p += C * Cr;
+    for (int64_t k = 0; k < C; ++k) p[k] = b2 ? b2[k] : 0.f;
+    return VKHIP_OK;
+}
+
+int vkhip_fused_se(const void *avg, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr, float alpha, float beta, vkhip_stream_t s) {
+    if (!avg || !blob || !y || N <= 0 || C <= 0 || Cr <= 0) return set_error(VKHIP_ERR_INVALID, "fused_se: bad arguments");
+    if (C + Cr > 16384) return set_error(VKHIP_ERR_UNSUPPORTED, "fused_se: C + Cr > 16384");
+    size_t sm = (size_t) (C + Cr) * 4;
+    fused_se_kernel<<<dim3((unsigned) N), 256, sm, resolve_stream(s)>>>((const half_t *) avg, (const float *) blob, (half_t *) y, (int) C, (int) Cr, alpha, beta);
+    return check_launch("fused_se");
+}
+
+int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s) {
+    if (!d || !x || !y || d->N <= 0 || d->C <= 0 || d->OH <= 0 || d->OW <= 0 || d->KH <= 0 || d->KW <= 0 || d->SH <= 0 || d->SW <= 0)
+        return set_error(VKHIP_ERR_INVALID, "maxpool: bad arguments");
+    int64_t total = (int64_t) d->N * ceil_div(d->C, 4) * d->OH * d->OW;
+    maxpool_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>(*d, (const uint2 *) x, (uint2 *) y, total);
+    return check_launch("maxpool");
+}
+
+int vkhip_concat_channels(const void *const *xs, const int64_t *cs, int32_t count, void *y, int64_t N, int64_t HW, vkhip_stream_t s) {
+    if (!xs || !cs || count <= 0 || !y || N <= 0 || HW <= 0) return set_error(VKHIP_ERR_INVALID, "concat: bad arguments");
+    int64_t Cy = 0;
+    for (int i = 0; i < count; ++i) Cy += cs[i];
+    hipStream_t st = resolve_stream(s);
+    int64_t     c0 = 0;
+    bool        any_unaligned = false;
+    for (int i = 0; i < count; ++i) {
+        if (c0 % 4 == 0 && cs[i] % 4 == 0) {
+            int64_t Cb = cs[i] / 4, total = N * Cb * HW;
+            copy_blocks_kernel<<<grid1(total), 256, 0, st>>>((const uint2 *) xs[i], (uint2 *) y, Cb, ceil_div(Cy, 4), 0, c0 / 4, Cb, HW, total);
+        } else {
+            any_unaligned = true;
+            int64_t total = N * cs[i] * HW;
+            copy_channels_kernel<<<grid1(total), 256, 0, st>>>((const half_t *) xs[i], (half_t *) y, cs[i], Cy, 0, c0, cs[i], HW, total);
+        }
+        int rc = check_launch("concat");
+        if (rc) return rc;
+        c0 += cs[i];
+    }
+    if (any_unaligned && Cy % 4) {
+        zero_tail_lanes_kernel<<<grid1(N * HW), 256, 0, st>>>((half_t *) y, Cy, HW, N);
+        return check_launch("concat_tail");
+    }
+    return VKHIP_OK;
+}
+
+int vkhip_slice_channels(const void *x, void *y, int64_t N, int64_t Cx, int64_t c0, int64_t C, int64_t HW, vkhip_stream_t s) {
+    if (!x || !y || N <= 0 || C <= 0 || HW <= 0 || c0 < 0 || c0 + C > Cx) return set_error(VKHIP_ERR_INVALID, "slice: bad arguments");
+    hipStream_t st = resolve_stream(s);
+    if (c0 % 4 == 0 && (C % 4 == 0 || c0 + C == Cx)) {
+        int64_t Cb = ceil_div(C, 4), total = N * Cb * HW;
+        copy_blocks_kernel<<<grid1(total), 256, 0, st>>>((const uint2 *) x, (uint2 *) y, ceil_div(Cx, 4), Cb, c0 / 4, 0, Cb, HW, total);
+        return check_launch("slice");
+    }
+    int64_t total = N * C * HW;
+    copy_channels_kernel<<<grid1(total), 256, 0, st>>>((const half_t *) x, (half_t *) y, Cx, C, c0, 0, C, HW, total);
+    int rc = check_launch("slice");
+    if (rc || C % 4 == 0) return rc;
+    zero_tail_lanes_kernel<<<grid1(N * HW), 256, 0, st>>>((half_t *) y, C, HW, N);
+    return check_launch("slice_tail");
+}
+
+int vkhip_resize_nearest(const void *x, void *y, int64_t N, int64_t C, int64_t H, int64_t W, int64_t OH, int64_t OW, vkhip_stream_t s) {
+    if (!x || !y || N <= 0 || C <= 0 || H <= 0 || W <= 0 || OH <= 0 || OW <= 0) return set_error(VKHIP_ERR_INVALID, "resize: bad arguments");
+    int64_t total = N * ceil_div(C, 4) * OH * OW;
+    resize_nearest_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, H, W, OH, OW, total);
+    return check_launch("resize_nearest");
+}
+
+} // extern "C"
