@@ -1,0 +1,198 @@
+"""Benchmark of the fused fp16 conv path on one MI355X: ResNet-50 v1.5 forward (config 2) through
+the vknn Session on the HIP backend.
+
+A step = one forward pass of one batch (default 64) with the fp32 NCHW input already resident in
+HBM: device pack to NC4HW4 fp16, 53 convs (+ fused BN/ReLU/residual epilogues), max pool, global
+average pool, FC, device unpack of the logits. Prints one JSON line (see the end of main()).
+
+Also reported: batch-1 latency/throughput, the conv layers' MFMA fraction and the bandwidth of the
+1x1 convs (per-op HIP events on the segment stream), and the reference CPU backend timed on this
+host on a bounded sample (cpu_baseline).
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA (published)
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E (published)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_steps(sess, steps, warmup):
+    """Warm up, then time exactly `steps` forward passes on the session stream: host wall clock
+    bracketed by a device sync on both sides, and HIP events on the stream."""
+    import vknn_amd as V
+    lib = V.vkhip()
+    for _ in range(warmup):
+        sess.run_device()
+    sess.sync()
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    V.check(lib.vkhip_event_create(ctypes.byref(e0)))
+    V.check(lib.vkhip_event_create(ctypes.byref(e1)))
+    stream = sess.stream
+    V.check(lib.vkhip_device_sync())
+    t0 = time.perf_counter()
+    V.check(lib.vkhip_event_record(e0, stream))
+    for _ in range(steps):
+        sess.run_device()
+    V.check(lib.vkhip_event_record(e1, stream))
+    sess.sync()
+    V.check(lib.vkhip_device_sync())
+    wall = time.perf_counter() - t0
+    ms = ctypes.c_float()
+    V.check(lib.vkhip_event_elapsed_ms(e0, e1, ctypes.byref(ms)))
+    lib.vkhip_event_destroy(e0)
+    lib.vkhip_event_destroy(e1)
+    return wall, ms.value / 1e3
+
+
+def profile_ops(model, batch, x_dev, options="", reps=3):
+    """Per-op device times (HIP events around each op's launches on the segment stream)."""
+    import vknn_amd as V
+    sess = V.Session(model, batch, seed=7, options=(options + ";profile=1").lstrip(";"))
+    sess.bind_device_input(x_dev.ptr)
+    sess.run_device()
+    sess.sync()
+    sess.profile()
+    acc = {}
+    for _ in range(reps):
+        sess.run_device()
+        sess.sync()
+        for r in sess.profile():
+            a = acc.setdefault(r["name"], dict(r, gpu_ms=0.0))
+            a["gpu_ms"] += r["gpu_ms"] / reps
+    plan = sess.describe()
+    sess.close()
+    return list(acc.values()), plan
+
+
+def cpu_baseline(model, seconds_budget=20.0):
+    """The reference CPU backend (oracle/_ref, compiled from the reference sources) or, where that
+    library is absent, the oracle restatement: single thread, batch 1, whole images until the
+    time budget is spent (at least one)."""
+    from tests import oracle_lib as O
+    kind = "reference" if O.ref_available() else "port"
+    run = O.ref_model_run if kind == "reference" else O.oracle_model_run
+    in_shape, _ = O.model_io(model, 1)
+    x = np.random.default_rng(0).standard_normal(in_shape).astype(np.float32)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        run(model, 1, 7, x)
+        n += 1
+        if time.perf_counter() - t0 >= seconds_budget or n >= 8:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "img/s", "cores": 1, "kind": kind,
+            "sample": f"{n} image(s) of {model} at batch 1, full forward, single-threaded ({dt:.1f} s)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--model", default="resnet50")
+    ap.add_argument("--options", default="")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--b1-steps", type=int, default=100)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (--gpus {args.gpus} refused). "
+              "The conv path shards by batch with no exchange; run one process per GPU.", file=sys.stderr)
+        sys.exit(2)
+
+    import vknn_amd as V
+    V.require_gpu()
+    flops_img = V.vknn().vknn_model_flops(args.model.encode())
+
+    # ---- batch-B throughput (the headline)
+    t = time.perf_counter()
+    sess = V.Session(args.model, args.batch, seed=7, options=args.options)
+    log(f"session create (plan + autotune) {time.perf_counter() - t:.1f}s")
+    x = np.random.default_rng(0).standard_normal(sess.in_shape).astype(np.float32)
+    x_dev = V.DeviceBuffer.from_array(x)
+    sess.bind_device_input(x_dev.ptr)
+    wall, ev = time_steps(sess, args.steps, args.warmup)
+    ms_step = wall / args.steps * 1e3
+    img_s = args.batch * args.steps / wall
+    log(f"b{args.batch}: {ms_step:.3f} ms/step wall, {ev / args.steps * 1e3:.3f} ms/step events, {img_s:.1f} img/s")
+
+    # ---- batch-1 latency
+    s1 = V.Session(args.model, 1, seed=7, options=args.options)
+    x1 = V.DeviceBuffer.from_array(x[:1])
+    s1.bind_device_input(x1.ptr)
+    wall1, _ = time_steps(s1, args.b1_steps, 10)
+    b1_ms = wall1 / args.b1_steps * 1e3
+    s1.close()
+    log(f"b1: {b1_ms:.3f} ms/img")
+
+    # ---- per-op roofline (separate profiled session, same graph and tuned plans)
+    extra = {}
+    roof = None
+    if not args.no_profile:
+        ops, plan = profile_ops(args.model, args.batch, x_dev, args.options)
+        conv = [o for o in ops if o["type"] in ("Conv", "Gemm", "FusedDwPw") and o["flops"] > 0]
+        conv_ms = sum(o["gpu_ms"] for o in conv)
+        conv_fl = sum(o["flops"] for o in conv)
+        all_ms = sum(o["gpu_ms"] for o in ops)
+        achieved = conv_fl / (conv_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                "kernel": "conv_gemm_kernel (all conv/FC launches of one step)",
+                "launch_ms": round(conv_ms, 4), "flops_per_step": conv_fl}
+        pw = [o for o in conv if "conv" in o["name"] and o["bytes"] > 0]
+        one = [o for o in pw if o["flops"] / max(o["bytes"], 1) < 315]  # layers below the ridge
+        if one:
+            b_ms = sum(o["gpu_ms"] for o in one)
+            b_bytes = sum(o["bytes"] for o in one)
+            extra["hbm_bound_convs"] = {"count": len(one), "achieved_GBs": round(b_bytes / (b_ms * 1e-3) / 1e9, 1),
+                                        "peak_GBs": PEAK_HBM_GBS, "frac": round(b_bytes / (b_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        extra["op_time_share"] = {"conv_ms": round(conv_ms, 4), "all_ops_ms": round(all_ms, 4)}
+        with open(os.path.join(ROOT, "gpurun_out", "bench_ops.json") if os.path.isdir(os.path.join(ROOT, "gpurun_out")) else os.devnull, "w") as f:
+            json.dump({"ops": ops, "plan": plan}, f, indent=1)
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.model)
+
+    out = {
+        "metric": "ResNet-50 fp16 img/s at b=1/64; conv % of MFMA peak; dw/1x1 HBM GB/s",
+        "value": round(img_s, 2),
+        "unit": "img/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 storage, fp32 accumulation (MFMA f32_32x32x16_f16)",
+        "data": "synthetic N(0,1) input, random He-init weights with folded random BN (seeded)",
+        "config": {"workload": f"{args.model} v1.5 forward, config 2" if args.model == "resnet50" else args.model,
+                   "batch": args.batch, "input": "x".join(map(str, sess.in_shape[1:])),
+                   "layout": "NC4HW4 fp16", "options": args.options or "default",
+                   "tflops_per_step": round(flops_img * args.batch / 1e12, 4)},
+        "b1_ms_per_img": round(b1_ms, 4),
+        "b1_img_per_s": round(1000.0 / b1_ms, 1),
+        "tflops": round(flops_img * img_s / 1e12, 2),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    out.update(extra)
+    sess.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -35,7 +35,7 @@ namespace {
 
     std::string g_err;
 
-    int run_graph(Graph &g, const float *x, int64_t nx, float *y, int64_t ny) {
+    int run_graph(Graph &g, const float *x, int64_t nx, float *y, int64_t ny, float *trace = nullptr) {
         std::map<TensorId, T> vals;
         for (auto &kv: g.initializers) {
             const HostBuffer &hb = kv.second;
@@ -250,6 +250,11 @@ namespace {
                     g_err = std::string("oracle: no op ") + std::to_string((int) nd.type);
                     return 1;
             }
+            if (trace) {
+                float m = 0.f;
+                for (float v: out.v) m = std::fmax(m, std::fabs(v));
+                trace[i] = m;
+            }
             vals[nd.outputs[0]] = std::move(out);
         }
         int64_t off = 0;
@@ -276,6 +281,14 @@ ORACLE_API int oracle_model_run(const char *name, int64_t batch, uint64_t seed, 
         return 1;
     }
     return run_graph(g, x, nx, y, ny);
+}
+
+// Per-node max |output| (index = node order of the unfused zoo graph); for range diagnostics.
+ORACLE_API int oracle_model_trace(const char *name, int64_t batch, uint64_t seed, const float *x, int64_t nx, float *y, int64_t ny,
+                                  float *trace, int64_t ntrace) {
+    Graph g = vknn_zoo::build(name, batch, seed);
+    if ((int64_t) g.nodes.size() > ntrace) return 1;
+    return run_graph(g, x, nx, y, ny, trace);
 }
 
 ORACLE_API int oracle_model_io(const char *name, int64_t batch, int64_t *in4, int64_t *out_elems, int32_t *n_out, int32_t max_out) {

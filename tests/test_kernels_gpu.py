@@ -386,7 +386,7 @@ def test_graph_capture_replay(gpu):
     r = rng(130)
     x = round_half(r.standard_normal((2, 64, 14, 14)))
     w = (r.standard_normal((64, 64, 3, 3)) * 0.05).astype(np.float32)
-    eager, plan, _ = gpu_conv(x, w, None, (1, 1), (1, 1, 1, 1), act=1)
+    eager, plan, _ = gpu_conv(x, w, None, (1, 1), (1, 1, 1, 1), act=1, algo=V.CONV_GEMM, tile=3)
     d, yshape = conv_desc(x.shape, w.shape, (1, 1), (1, 1, 1, 1), act=1)
     blob = np.zeros(plan.weight_bytes, np.uint8)
     check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(plan), w.ctypes.data, None, blob.ctypes.data))
