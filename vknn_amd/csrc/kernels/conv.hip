@@ -8,7 +8,7 @@
 //                                      so every epilogue store is one 8-byte fp16x4 write)
 //   columns p = (n, oy, ox)           (MFMA "N")
 //   reduction k = slot*4 + lane, slot = tap*Cinb + cb, tap = ky*KW + kx
-// A = packed weights [Coutp][Kp] fp16 (host prepack, zero padded); B = input pixels gathered on
+// A = packed weights fp16 in [m_tile][k_stage][BM][64] order (host prepack, zero padded); B = input pixels gathered on
 // the fly from NC4HW4 fp16 (8 bytes per (pixel, slot)), zero outside the image.
 //
 // Reference semantics followed: ConvCpu (src/backend/cpu/ops/conv.cpp:9-92) for the convolution,
@@ -18,7 +18,10 @@
 #include "common.h"
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 namespace vkhip {
@@ -26,7 +29,7 @@ namespace vkhip {
     // ------------------------------------------------------------------ kernel arguments
     struct GemmArgs {
         const uint2  *x;    // NC4HW4 fp16, 8-byte (4-channel) vectors
-        const half_t *w;    // [Coutp][Kp]
+        const half_t *w;    // tiled [m_tile][k_stage][BM][64]
         const float  *bias; // [Coutp]
         const uint2  *res;
         uint2        *y;
@@ -34,33 +37,78 @@ namespace vkhip {
         int           Cinb, H, W, HW;
         int           Coutb, Cout, OW, OHW;
         int           KW, SH, SW, PT, PL, DH, DW;
-        int           P, Kslots, Kp, nsteps, steps_per_split;
+        int           P, Kslots, nsteps, steps_per_split;
         int           act;
         float         lo, hi;
         int           has_res, omode, m_tiles;
         long long     x_bstride, w_bstride, y_bstride; // batch (blockIdx.z) strides: uint2 / half / uint2
+        unsigned      x_bytes;                         // bytes of one batch slice of x (< 2 GiB)
+        unsigned      y_bytes;                         // bytes of one batch slice of y (< 2 GiB)
     };
 
     enum { OMODE_EPILOGUE = 0, OMODE_RAW = 1, OMODE_PARTIAL = 2 };
-    enum { BMODE_1X1 = 0, BMODE_ALIGNED = 1, BMODE_GENERAL = 2 };
+    // B gather modes. *_P16 variants load two adjacent output pixels of one channel slot with a
+    // single 16-byte load (the vector memory pipe costs the same per instruction for 8 or 16
+    // bytes); they need every pixel pair to be adjacent in memory at every tap (unit stride, even
+    // row width / even image size).
+    enum { BMODE_1X1 = 0, BMODE_ALIGNED = 1, BMODE_GENERAL = 2, BMODE_1X1_P16 = 3, BMODE_ALIGNED_P16 = 4 };
 
     constexpr int kThreads = 256; // 4 wave64s per workgroup
-    constexpr int kAStride = 40;  // LDS row stride of the A tile in halves (32 + 8 pad, 80 bytes)
+    constexpr int kBK      = 64;  // reduction halves per LDS stage (16 channel slots)
+    constexpr int kAStride = 72;  // LDS row stride of the A tile in halves (64 + 8 pad = 144 bytes)
 
-    template <int BM, int BN, int WM, int WN, int BMODE>
+    // 16-byte global load from an 8-byte aligned address (two adjacent NC4HW4 pixels).
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    typedef unsigned int u32x4_a8 __attribute__((ext_vector_type(4), aligned(8)));
+    __device__ __forceinline__ u32x4 u32x4_make(unsigned a, unsigned b, unsigned c, unsigned d) { return u32x4 {a, b, c, d}; }
+
+    // Spread consecutive workgroup ids (dispatched round-robin over the 8 XCDs) so that runs of
+    // consecutive logical tiles land on one XCD and share its L2.
+    __device__ __forceinline__ int xcd_remap(int bid, int nwg) {
+        const int xcd = bid & 7, local = bid >> 3, q = nwg >> 3, r = nwg & 7;
+        return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+    }
+
+
+    // Instruction-interleaving hints for one 16-K step: after each MFMA, place a share of the LDS
+    // reads (next step's fragments), LDS writes (next stage's tile) and global loads (the stage
+    // after), so the wave keeps the matrix core busy while those are in flight.
+    enum { SG_MFMA = 0x008, SG_VALU = 0x002, SG_VMEM_READ = 0x020, SG_DS_READ = 0x100, SG_DS_WRITE = 0x200 };
+    template <int I, int NM, int NR, int NW, int NV>
+    struct Interleave {
+        static __device__ __forceinline__ void apply() {
+            if constexpr (I < NM) {
+                constexpr int r = NR * (I + 1) / NM - NR * I / NM;
+                constexpr int w = NW * (I + 1) / NM - NW * I / NM;
+                constexpr int v = NV * (I + 1) / NM - NV * I / NM;
+                __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+                if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, r, 0);
+                if constexpr (w > 0) __builtin_amdgcn_sched_group_barrier(SG_DS_WRITE, w, 0);
+                if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, v, 0);
+                Interleave<I + 1, NM, NR, NW, NV>::apply();
+            }
+        }
+    };
+
+    template <int BM, int BN, int WM, int WN, int BMODE_>
     __global__ __launch_bounds__(kThreads) void conv_gemm_kernel(GemmArgs a) {
+        constexpr bool P16   = BMODE_ >= BMODE_1X1_P16;
+        constexpr int  BMODE = BMODE_ == BMODE_1X1_P16 ? BMODE_1X1 : (BMODE_ == BMODE_ALIGNED_P16 ? BMODE_ALIGNED : BMODE_);
         constexpr int TM = BM / WM, TN = BN / WN; // wave tile
         constexpr int FM = TM / 32, FN = TN / 32; // 32x32 MFMA fragments per wave
         static_assert(WM * WN == 4, "4 waves");
         static_assert(FM >= 1 && FN >= 1, "wave tile >= 32x32");
-        constexpr int SPT     = 8 * BN / kThreads;       // B slots loaded per thread per K step
-        constexpr int SSTRIDE = kThreads / BN;           // slot stride between a thread's loads
-        constexpr int ACHUNK  = BM * 4;                  // 16-byte chunks in an A tile
-        constexpr int ALOADS  = (ACHUNK + kThreads - 1) / kThreads;
-        static_assert(SPT >= 1 && kThreads % BN == 0, "BN must divide 256");
+        constexpr int ACHUNK  = BM * kBK / 8;            // 16-byte chunks in one A stage
+        constexpr int ALOADS  = ACHUNK / kThreads;
+        constexpr int QN      = BN / 2;                  // pixel pairs in the tile
+        constexpr int BITEMS  = 8 * QN / kThreads;       // (slot pair, pixel pair) items per thread
+        constexpr int SPSTEP  = kThreads / QN;           // slot-pair stride between a thread's items
+        static_assert(ALOADS >= 1 && ACHUNK % kThreads == 0, "A tile");
+        static_assert(BITEMS >= 1 && kThreads % QN == 0, "B tile");
 
-        __shared__ __attribute__((aligned(16))) half_t As[2][BM * kAStride];
-        __shared__ __attribute__((aligned(16))) uint4  Bs[2][4 * BN];
+        __shared__ u32x4 As[2][BM * kAStride / 8];
+        __shared__ u32x4 Bs[2][8 * BN]; // [slot pair][pixel] x (8 channels, fp16)
 
         const int tid  = threadIdx.x;
         const int lane = tid & 63;
@@ -68,101 +116,175 @@ namespace vkhip {
         const int wm0  = (wave / WN) * TM;
         const int wn0  = (wave % WN) * TN;
 
-        const int bid    = blockIdx.x;
-        const int m_tile = bid % a.m_tiles;
-        const int n_tile = bid / a.m_tiles;
+        const int lin    = xcd_remap(blockIdx.x, gridDim.x);
+        const int m_tile = lin % a.m_tiles;
+        const int n_tile = lin / a.m_tiles;
         const int m0     = m_tile * BM;
         const int n0     = n_tile * BN;
         const int split  = blockIdx.y;
         const int bz     = blockIdx.z;
 
         const uint2  *X  = a.x + bz * a.x_bstride;
-        const half_t *Wt = a.w + bz * a.w_bstride;
+        const half_t *Wt = a.w + bz * a.w_bstride + (long long) m_tile * a.nsteps * (BM * kBK);
 
-        // ---- this thread's B pixel (fixed for the whole K loop)
-        const int  pl     = tid % BN;
-        const int  sbase  = tid / BN;
-        const int  p      = n0 + pl;
-        const bool pvalid = p < a.P;
-        int        n = 0, iy0 = 0, ix0 = 0;
-        {
-            int pp = pvalid ? p : 0;
-            n      = pp / a.OHW;
-            int r  = pp - n * a.OHW;
-            int oy = r / a.OW;
-            int ox = r - oy * a.OW;
-            iy0    = oy * a.SH - a.PT;
-            ix0    = ox * a.SW - a.PL;
+        // ---- this thread's pixel pair (fixed for the whole K loop)
+        const int q   = tid % QN;
+        // slot pair of this thread; wave-uniform when a wave covers one slot pair (QN >= 64)
+        const int sp0 = QN >= 64 ? __builtin_amdgcn_readfirstlane(tid / QN) : tid / QN;
+        int       pv[2], piy[2], pix[2], pbyte[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int p = n0 + 2 * q + i;
+            pv[i]       = p < a.P;
+            const int pp = pv[i] ? p : 0;
+            const int n  = pp / a.OHW;
+            const int r  = pp - n * a.OHW;
+            const int oy = r / a.OW;
+            const int ox = r - oy * a.OW;
+            piy[i]       = oy * a.SH - a.PT;
+            pix[i]       = ox * a.SW - a.PL;
+            // byte offset of (n, channel block 0, iy0, ix0); x slices are < 2 GiB
+            pbyte[i] = (n * a.Cinb * a.HW + piy[i] * a.W + pix[i]) * 8;
         }
-        const long long xbase   = (long long) n * a.Cinb * a.HW;
-        const int       pix_off = iy0 * a.W + ix0; // 1x1 mode: always inside the image
 
         const int ks_begin = split * a.steps_per_split;
         const int ks_end   = min(a.nsteps, ks_begin + a.steps_per_split);
 
-        uint4 areg[ALOADS];
-        uint2 breg[SPT];
+        // Two register prefetch sets: stage ks+3 is loaded while stage ks computes and is written
+        // to LDS at the start of stage ks+2 (1.75 stages of lead time for L2/HBM latency).
+        u32x4 areg[2][ALOADS];
+        u32x4 b0[2][BITEMS], b1[2][BITEMS]; // per item: slot e=0 / e=1, each {pixel 0 (8 B), pixel 1 (8 B)}
+        unsigned bfix[2];                      // P16: per (item, slot) 4 bits {pixel0 ok, pixel1 ok, shift right, shift left}
 
-        auto load_tiles = [&](int ks) {
+        // B gathers go through a raw buffer resource: an offset at or past num_records returns zero
+        // in hardware, so padding taps, K tails and pixels past P need no branch.
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *) X, (short) 0, (int) a.x_bytes, 0x00020000);
+        constexpr unsigned kInvalid = 0x80000000u;
+        const int          xmax16   = (int) a.x_bytes - 16;
+
+        // weights of this M tile only: prefetches past the last stage read zeros, not other tiles
+        const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *) Wt, (short) 0, ks_end * (BM * kBK * 2), 0x00020000);
+        const int kslots = min(a.Kslots, ks_end * 16); // slots past this split read zeros
+        const int hw8 = a.HW * 8;
+
+        auto load_tiles = [&](int ks, auto set_c) __attribute__((always_inline)) {
+            constexpr int S = decltype(set_c)::value;
+            const int wsoff = ks * (BM * kBK * 2);
+            unsigned  fixbits = 0;
 #pragma unroll
-            for (int i = 0; i < ALOADS; ++i) {
-                int c = tid + i * kThreads;
-                if (ACHUNK % kThreads == 0 || c < ACHUNK) {
-                    int row = c >> 2, col8 = c & 3;
-                    areg[i] = *reinterpret_cast<const uint4 *>(Wt + (long long) (m0 + row) * a.Kp + ks * 32 + col8 * 8);
-                }
-            }
-            if (BMODE == BMODE_ALIGNED) {
-                // Cinb % 8 == 0: all 8 slots of this step share one tap (uniform across the block).
-                int tap = (ks * 8) / a.Cinb;
-                int cb0 = ks * 8 - tap * a.Cinb;
-                int ky  = tap / a.KW;
-                int kx  = tap - ky * a.KW;
-                int iy  = iy0 + ky * a.DH;
-                int ix  = ix0 + kx * a.DW;
-                bool ok = pvalid && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
-                const uint2 *src = X + xbase + (long long) cb0 * a.HW + iy * a.W + ix;
+            for (int i = 0; i < ALOADS; ++i) areg[S][i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, (tid + i * kThreads) * 16, wsoff, 0);
 #pragma unroll
-                for (int j = 0; j < SPT; ++j) {
-                    int s   = sbase + j * SSTRIDE;
-                    breg[j] = ok ? src[(long long) s * a.HW] : make_uint2(0u, 0u);
-                }
-            } else {
+            for (int j = 0; j < BITEMS; ++j) {
+                const int sp   = sp0 + j * SPSTEP; // slot pair within the stage (0..7), wave-uniform
+                const int slot = ks * 16 + 2 * sp;  // first slot of the pair
+                unsigned  off[2][2];                // [slot e][pixel i], byte offsets or kInvalid
+                int       p16o[2];                  // P16: pixel 0 byte offset per slot
+                bool      p16ok[2][2];              // P16: [slot e][pixel i] validity
+                if (BMODE == BMODE_1X1) {
+                    const int s0 = slot * hw8;
+                    p16o[0] = pbyte[0] + s0;
+                    p16o[1] = pbyte[0] + s0 + hw8;
 #pragma unroll
-                for (int j = 0; j < SPT; ++j) {
-                    int  g  = ks * 8 + sbase + j * SSTRIDE;
-                    bool ok = pvalid && g < a.Kslots;
-                    long long off = 0;
-                    if (BMODE == BMODE_1X1) {
-                        off = xbase + (long long) g * a.HW + pix_off;
-                    } else {
-                        int tap = g / a.Cinb;
-                        int cb  = g - tap * a.Cinb;
-                        int ky  = tap / a.KW;
-                        int kx  = tap - ky * a.KW;
-                        int iy  = iy0 + ky * a.DH;
-                        int ix  = ix0 + kx * a.DW;
-                        ok      = ok && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
-                        off     = xbase + (long long) cb * a.HW + iy * a.W + ix;
+                    for (int i = 0; i < 2; ++i) {
+                        p16ok[0][i] = (pv[i] != 0) & (slot < kslots);
+                        p16ok[1][i] = (pv[i] != 0) & (slot + 1 < kslots);
+                        off[0][i] = ((pv[i] != 0) & (slot < kslots)) ? (unsigned) (pbyte[i] + s0) : kInvalid;
+                        off[1][i] = ((pv[i] != 0) & (slot + 1 < kslots)) ? (unsigned) (pbyte[i] + s0 + hw8) : kInvalid;
                     }
-                    breg[j] = ok ? X[off] : make_uint2(0u, 0u);
+                } else if (BMODE == BMODE_ALIGNED) {
+                    // Cinb % 8 == 0: the 8 slots of each half stage share one tap (all scalar).
+                    const int half = ks * 16 + (sp >> 2) * 8;
+                    const int tap  = half / a.Cinb;
+                    const int cb   = half - tap * a.Cinb + 2 * (sp & 3);
+                    const int ky   = tap / a.KW;
+                    const int kx   = tap - ky * a.KW;
+                    const int dy = ky * a.DH, dx = kx * a.DW;
+                    const int soff = cb * hw8 + (dy * a.W + dx) * 8;
+                    const bool kin = slot < kslots;
+                    p16o[0] = pbyte[0] + soff;
+                    p16o[1] = pbyte[0] + soff + hw8;
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const bool ok = kin & (pv[i] != 0) & ((unsigned) (piy[i] + dy) < (unsigned) a.H) & ((unsigned) (pix[i] + dx) < (unsigned) a.W);
+                        p16ok[0][i] = ok;
+                        p16ok[1][i] = ok;
+                        off[0][i] = ok ? (unsigned) (pbyte[i] + soff) : kInvalid;
+                        off[1][i] = ok ? (unsigned) (pbyte[i] + soff + hw8) : kInvalid;
+                    }
+                } else {
+                    p16o[0] = p16o[1] = 0;
+                    p16ok[0][0] = p16ok[0][1] = p16ok[1][0] = p16ok[1][1] = false;
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int g   = slot + e;
+                        const int tap = g / a.Cinb;
+                        const int cb  = g - tap * a.Cinb;
+                        const int ky  = tap / a.KW;
+                        const int kx  = tap - ky * a.KW;
+                        const int dy = ky * a.DH, dx = kx * a.DW;
+                        const int soff = cb * hw8 + (dy * a.W + dx) * 8;
+#pragma unroll
+                        for (int i = 0; i < 2; ++i) {
+                            const bool ok = (g < kslots) & (pv[i] != 0) & ((unsigned) (piy[i] + dy) < (unsigned) a.H) & ((unsigned) (pix[i] + dx) < (unsigned) a.W);
+                            off[e][i]     = ok ? (unsigned) (pbyte[i] + soff) : kInvalid;
+                        }
+                    }
+                }
+                if constexpr (P16) {
+                    // off[e][0] holds pixel 0's byte offset even when pixel 0 is padding (the pair is
+                    // adjacent in memory); load 16 bytes from there, clamped into the tensor.
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int  o0 = p16o[e];
+                        const bool ok0 = p16ok[e][0], ok1 = p16ok[e][1];
+                        const int  ol = o0 < 0 ? 0 : (o0 > xmax16 ? xmax16 : o0);
+                        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, (ok0 | ok1) ? (unsigned) ol : kInvalid, 0, 0);
+                        if (e == 0) b0[S][j] = v;
+                        else b1[S][j] = v;
+                        const unsigned bits = (ok0 ? 1u : 0u) | (ok1 ? 2u : 0u) | (o0 < 0 ? 4u : 0u) | (o0 > xmax16 ? 8u : 0u);
+                        fixbits |= bits << (4 * (2 * j + e));
+                    }
+                } else {
+                    const u32x2 v00 = __builtin_amdgcn_raw_buffer_load_b64(xrs, off[0][0], 0, 0);
+                    const u32x2 v01 = __builtin_amdgcn_raw_buffer_load_b64(xrs, off[0][1], 0, 0);
+                    const u32x2 v10 = __builtin_amdgcn_raw_buffer_load_b64(xrs, off[1][0], 0, 0);
+                    const u32x2 v11 = __builtin_amdgcn_raw_buffer_load_b64(xrs, off[1][1], 0, 0);
+                    b0[S][j] = u32x4_make(v00.x, v00.y, v01.x, v01.y);
+                    b1[S][j] = u32x4_make(v10.x, v10.y, v11.x, v11.y);
                 }
             }
+            bfix[S] = fixbits;
         };
 
-        auto store_tiles = [&](int buf) {
+        auto store_tiles = [&](int buf, auto set_c) __attribute__((always_inline)) {
+            constexpr int S = decltype(set_c)::value;
 #pragma unroll
             for (int i = 0; i < ALOADS; ++i) {
-                int c = tid + i * kThreads;
-                if (ACHUNK % kThreads == 0 || c < ACHUNK) {
-                    int row = c >> 2, col8 = c & 3;
-                    *reinterpret_cast<uint4 *>(&As[buf][row * kAStride + col8 * 8]) = areg[i];
-                }
+                const int c = tid + i * kThreads, row = c >> 3, col = c & 7;
+                As[buf][row * (kAStride / 8) + col] = areg[S][i];
+            }
+            if constexpr (P16) {
+                const unsigned fb = bfix[S];
+#pragma unroll
+                for (int j = 0; j < BITEMS; ++j)
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const unsigned bits = fb >> (4 * (2 * j + e));
+                        u32x4          v    = e == 0 ? b0[S][j] : b1[S][j];
+                        if (bits & 4u) v = u32x4_make(0u, 0u, v.x, v.y);  // pair began 8 bytes before the tensor
+                        if (bits & 8u) v = u32x4_make(v.z, v.w, 0u, 0u);  // pair ended 8 bytes past the tensor
+                        if (!(bits & 1u)) v.x = v.y = 0u;                  // pixel 0 is padding
+                        if (!(bits & 2u)) v.z = v.w = 0u;                  // pixel 1 is padding
+                        if (e == 0) b0[S][j] = v;
+                        else b1[S][j] = v;
+                    }
             }
 #pragma unroll
-            for (int j = 0; j < SPT; ++j) {
-                int s = sbase + j * SSTRIDE;
-                reinterpret_cast<uint2 *>(&Bs[buf][(s >> 1) * BN + pl])[s & 1] = breg[j];
+            for (int j = 0; j < BITEMS; ++j) {
+                const int sp = sp0 + j * SPSTEP;
+                // pixel 0 gets {slot e=0 lanes, slot e=1 lanes}, pixel 1 likewise
+                Bs[buf][sp * BN + 2 * q]     = u32x4_make(b0[S][j].x, b0[S][j].y, b1[S][j].x, b1[S][j].y);
+                Bs[buf][sp * BN + 2 * q + 1] = u32x4_make(b0[S][j].z, b0[S][j].w, b1[S][j].z, b1[S][j].w);
             }
         };
 
@@ -177,75 +299,160 @@ namespace vkhip {
         const int lrow = lane & 31; // A row / B column inside a 32x32 fragment
         const int lk   = lane >> 5; // which 8-wide K group of the 16-wide MFMA step
 
-        if (ks_begin < ks_end) {
-            load_tiles(ks_begin);
-            store_tiles(0);
+        // Fragment double buffer: the next 16-K step's A/B fragments are read from LDS while the
+        // current step's MFMAs run.
+        half8 fa[2][FM], fb[2][FN];
+        auto read_frags = [&](int buf, int kk, int fbuf) __attribute__((always_inline)) {
+            const half_t *Ab = reinterpret_cast<const half_t *>(As[buf]);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                fa[fbuf][i] = *reinterpret_cast<const half8 *>(Ab + (wm0 + i * 32 + lrow) * kAStride + kk * 16 + lk * 8);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                fb[fbuf][j] = *reinterpret_cast<const half8 *>(&Bs[buf][(kk * 2 + lk) * BN + wn0 + j * 32 + lrow]);
+        };
+
+        // Stage pipeline (LDS double buffer, two register prefetch sets):
+        //   step 0 of stage ks : write the set holding stage ks+1 into the idle LDS buffer;
+        //   step 1             : issue the global loads of stage ks+3 into that (now free) set;
+        //   steps 0..3         : read the next 16-K fragments while the current MFMAs run;
+        //   end                : barrier, read the first fragments of stage ks+1.
+        // The stage loop runs in pairs (register sets are compile-time indices); a trailing odd
+        // stage and all prefetches past ks_end read zeros, so they add nothing to the sums.
+        constexpr int NM = FM * FN, NR = FM + FN, NW = ALOADS + 2 * BITEMS, NV = ALOADS + 4 * BITEMS;
+        auto mfmas = [&](int fbuf) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[fbuf][i], fb[fbuf][j], acc[i][j], 0, 0, 0);
+        };
+        auto stage = [&](int ks, int buf, auto set_c) __attribute__((always_inline)) {
+            read_frags(buf, 1, 1);
+            store_tiles(buf ^ 1, set_c);
+            mfmas(0);
+            Interleave<0, NM, NR, NW, 0>::apply();
+            __builtin_amdgcn_sched_barrier(0);
+            read_frags(buf, 2, 0);
+            load_tiles(ks + 3, set_c);
+            mfmas(1);
+            Interleave<0, NM, NR, 0, NV>::apply();
+            __builtin_amdgcn_sched_barrier(0);
+            read_frags(buf, 3, 1);
+            mfmas(0);
+            Interleave<0, NM, NR, 0, 0>::apply();
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(1);
             __syncthreads();
-            for (int ks = ks_begin; ks < ks_end; ++ks) {
-                const int  buf  = (ks - ks_begin) & 1;
-                const bool more = ks + 1 < ks_end;
-                if (more) load_tiles(ks + 1);
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    half8 af[FM], bf[FN];
-#pragma unroll
-                    for (int i = 0; i < FM; ++i)
-                        af[i] = *reinterpret_cast<const half8 *>(&As[buf][(wm0 + i * 32 + lrow) * kAStride + kk * 16 + lk * 8]);
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        bf[j] = *reinterpret_cast<const half8 *>(&Bs[buf][(kk * 2 + lk) * BN + wn0 + j * 32 + lrow]);
-#pragma unroll
-                    for (int i = 0; i < FM; ++i)
-#pragma unroll
-                        for (int j = 0; j < FN; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-                }
-                if (more) store_tiles(buf ^ 1);
-                __syncthreads();
+            read_frags(buf ^ 1, 0, 0);
+        };
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        if (ks_begin < ks_end) {
+            load_tiles(ks_begin, S0 {});
+            store_tiles(0, S0 {});
+            __syncthreads();
+            load_tiles(ks_begin + 1, S1 {});
+            load_tiles(ks_begin + 2, S0 {});
+            read_frags(0, 0, 0);
+            for (int ks = ks_begin; ks < ks_end; ks += 2) {
+                stage(ks, 0, S1 {});
+                stage(ks + 1, 1, S0 {});
             }
         }
 
         // ---- epilogue. D layout of a 32x32 fragment: lane l holds column l%32, register r holds
         // row 8*(r/4) + 4*(l/32) + r%4, so registers 4q..4q+3 are one 4-channel block.
-        uint2   *Y  = a.y + bz * a.y_bstride;
+        // Pass 1 issues every bias / residual load of the tile, pass 2 computes and stores; rows or
+        // pixels outside the tensor get an out-of-range offset, so their loads read zero and their
+        // stores are dropped by the buffer unit.
+        unsigned yoff[FN][FM][4];
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-            const int px = n0 + wn0 + j * 32 + lrow;
-            if (px >= a.P) continue;
-            const int pn = px / a.OHW;
-            const int pr = px - pn * a.OHW;
+            const int  px = n0 + wn0 + j * 32 + lrow;
+            const bool pok = px < a.P;
+            const int  pn  = px / a.OHW;
+            const int  pr  = px - pn * a.OHW;
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int oc  = m0 + wm0 + i * 32 + q * 8 + lk * 4;
-                    const int ocb = oc >> 2;
-                    if (ocb >= a.Coutb) continue;
-                    float4v v;
-                    v.x = acc[i][j][q * 4 + 0];
-                    v.y = acc[i][j][q * 4 + 1];
-                    v.z = acc[i][j][q * 4 + 2];
-                    v.w = acc[i][j][q * 4 + 3];
-                    if (a.omode == OMODE_PARTIAL) {
-                        a.part[((long long) split * a.Coutb + ocb) * a.P + px] = v;
-                        continue;
-                    }
-                    const long long yi = ((long long) pn * a.Coutb + ocb) * a.OHW + pr;
-                    if (a.omode == OMODE_EPILOGUE) {
-                        float4v b = *reinterpret_cast<const float4v *>(a.bias + oc);
-                        v += b;
-                        if (a.has_res) v += h4_to_f4(u2_as_h4(a.res[yi]));
-                        v.x = apply_act(v.x, a.act, a.lo, a.hi);
-                        v.y = apply_act(v.y, a.act, a.lo, a.hi);
-                        v.z = apply_act(v.z, a.act, a.lo, a.hi);
-                        v.w = apply_act(v.w, a.act, a.lo, a.hi);
-                    }
-                    if (oc + 0 >= a.Cout) v.x = 0.f;
-                    if (oc + 1 >= a.Cout) v.y = 0.f;
-                    if (oc + 2 >= a.Cout) v.z = 0.f;
-                    if (oc + 3 >= a.Cout) v.w = 0.f;
-                    Y[yi] = h4_as_u2(f4_to_h4(v));
+                for (int qq = 0; qq < 4; ++qq) {
+                    const int ocb = (m0 + wm0 + i * 32 + qq * 8 + lk * 4) >> 2;
+                    const bool ok = pok & (ocb < a.Coutb);
+                    if (a.omode == OMODE_PARTIAL) yoff[j][i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + px) * 16) : kInvalid;
+                    else yoff[j][i][qq] = ok ? (unsigned) (((pn * a.Coutb + ocb) * a.OHW + pr) * 8) : kInvalid;
                 }
+        }
+        if (a.omode == OMODE_PARTIAL) {
+            const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc((void *) a.part, (short) 0, 0x7FFFFFFF, 0x00020000);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) {
+                        float4v v = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs, yoff[j][i][qq], 0, 0);
+                    }
+        } else {
+            uint2 *Y = a.y + bz * a.y_bstride;
+            const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc((void *) Y, (short) 0, (int) a.y_bytes, 0x00020000);
+            const bool  epi = a.omode == OMODE_EPILOGUE;
+            float4v     bia[FM][4];
+            u32x2       rv[FN][FM][4];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int qq = 0; qq < 4; ++qq) {
+                    const int oc = m0 + wm0 + i * 32 + qq * 8 + lk * 4;
+                    bia[i][qq]   = epi ? *reinterpret_cast<const float4v *>(a.bias + oc) : float4v {0.f, 0.f, 0.f, 0.f};
+                }
+            if (epi && a.has_res) {
+                const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc((void *) (a.res + bz * a.y_bstride), (short) 0, (int) a.y_bytes, 0x00020000);
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+#pragma unroll
+                        for (int qq = 0; qq < 4; ++qq) rv[j][i][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[j][i][qq], 0, 0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+#pragma unroll
+                        for (int qq = 0; qq < 4; ++qq) rv[j][i][qq] = u32x2 {0u, 0u};
+            }
+            auto finish = [&](auto act_c) __attribute__((always_inline)) {
+                constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+#pragma unroll
+                        for (int qq = 0; qq < 4; ++qq) {
+                            const int oc = m0 + wm0 + i * 32 + qq * 8 + lk * 4;
+                            float4v   v  = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
+                            v += bia[i][qq];
+                            v += h4_to_f4(__builtin_bit_cast(half4, rv[j][i][qq]));
+                            v.x = apply_act(v.x, ACT, a.lo, a.hi);
+                            v.y = apply_act(v.y, ACT, a.lo, a.hi);
+                            v.z = apply_act(v.z, ACT, a.lo, a.hi);
+                            v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                            if (oc + 0 >= a.Cout) v.x = 0.f;
+                            if (oc + 1 >= a.Cout) v.y = 0.f;
+                            if (oc + 2 >= a.Cout) v.z = 0.f;
+                            if (oc + 3 >= a.Cout) v.w = 0.f;
+                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff[j][i][qq], 0, 0);
+                        }
+            };
+            switch (epi ? a.act : 0) {
+                case VKHIP_ACT_RELU: finish(std::integral_constant<int, VKHIP_ACT_RELU> {}); break;
+                case VKHIP_ACT_RELU6: finish(std::integral_constant<int, VKHIP_ACT_RELU6> {}); break;
+                case VKHIP_ACT_CLIP: finish(std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
+                case VKHIP_ACT_HARDSWISH: finish(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
+                case VKHIP_ACT_SILU: finish(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
+                default: finish(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
             }
         }
     }
@@ -486,6 +693,8 @@ namespace vkhip {
         switch (bmode) {
             case BMODE_1X1: return conv_gemm_kernel<BM, BN, WM, WN, BMODE_1X1>;
             case BMODE_ALIGNED: return conv_gemm_kernel<BM, BN, WM, WN, BMODE_ALIGNED>;
+            case BMODE_1X1_P16: return conv_gemm_kernel<BM, BN, WM, WN, BMODE_1X1_P16>;
+            case BMODE_ALIGNED_P16: return conv_gemm_kernel<BM, BN, WM, WN, BMODE_ALIGNED_P16>;
             default: return conv_gemm_kernel<BM, BN, WM, WN, BMODE_GENERAL>;
         }
     }
@@ -526,19 +735,28 @@ namespace vkhip {
             int64_t nT = (int64_t) d->N * ceil_div(d->OH, 2) * ceil_div(d->OW, 2);
             g.Kslots   = g.Cinb;
             g.P        = nT;
-            g.bmode    = BMODE_1X1;
+            g.bmode    = nT % 2 == 0 ? BMODE_1X1_P16 : BMODE_1X1;
         } else {
             g.Kslots = (int64_t) d->KH * d->KW * g.Cinb;
             g.P      = (int64_t) d->N * d->OH * d->OW;
-            bool one = d->KH == 1 && d->KW == 1 && d->PT == 0 && d->PL == 0;
-            g.bmode  = one ? BMODE_1X1 : (g.Cinb % 8 == 0 ? BMODE_ALIGNED : BMODE_GENERAL);
+            const bool one  = d->KH == 1 && d->KW == 1 && d->PT == 0 && d->PL == 0;
+            const bool unit = d->SW == 1 && d->DW == 1;
+            if (one) g.bmode = (d->SH == 1 && d->SW == 1 && (d->OH * d->OW) % 2 == 0) ? BMODE_1X1_P16 : BMODE_1X1;
+            else if (g.Cinb % 8 == 0) g.bmode = (unit && d->OW % 2 == 0) ? BMODE_ALIGNED_P16 : BMODE_ALIGNED;
+            else g.bmode = BMODE_GENERAL;
         }
-        g.Kp      = round_up(g.Kslots * 4, 32);
-        g.nsteps  = g.Kp / 32;
+        g.Kp      = round_up(g.Kslots * 4, kBK);
+        g.nsteps  = g.Kp / kBK;
         g.m_tiles = ceil_div(g.Coutb * 4, t.BM);
         g.Coutp   = g.m_tiles * t.BM;
         g.n_tiles = ceil_div(g.P, t.BN);
         return g;
+    }
+
+    // Position of weight (oc, k) in the tiled layout [m_tile][k_stage][BM][64]: one K stage of one
+    // M tile is a contiguous BM*64-half block, read linearly by the kernel.
+    static inline int64_t tiled_index(const ConvGeom &g, int BM, int64_t oc, int64_t k) {
+        return ((oc / BM) * g.nsteps + k / kBK) * (int64_t) (BM * kBK) + (oc % BM) * kBK + k % kBK;
     }
 
     static int default_tile(const vkhip_conv_desc *d, bool wino) {
@@ -574,8 +792,11 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
         return set_error(VKHIP_ERR_INVALID, "conv_plan_make: bad geometry");
     if ((d->OH - 1) * d->SH - d->PT + (d->KH - 1) * d->DH < 0 || (d->OW - 1) * d->SW - d->PL + (d->KW - 1) * d->DW < 0)
         return set_error(VKHIP_ERR_INVALID, "conv_plan_make: output does not overlap the input");
-    if ((int64_t) d->N * d->OH * d->OW >= (1LL << 31) || (int64_t) d->N * ceil_div(d->Cin, 4) * d->H * d->W >= (1LL << 40))
-        return set_error(VKHIP_ERR_INVALID, "conv_plan_make: tensor too large");
+    // the GEMM gathers address the input through a buffer resource with 31-bit byte offsets
+    if ((int64_t) d->N * d->OH * d->OW >= (1LL << 31) || (int64_t) d->N * ceil_div(d->Cin, 4) * d->H * d->W * 8 >= (1LL << 31) ||
+        (int64_t) d->N * ceil_div(d->Cout, 4) * d->OH * d->OW * 8 >= (1LL << 31) ||
+        (int64_t) 16 * d->N * ceil_div(std::max(d->Cin, d->Cout), 4) * ceil_div(d->OH, 2) * ceil_div(d->OW, 2) * 8 >= (1LL << 31))
+        return set_error(VKHIP_ERR_INVALID, "conv_plan_make: input tensor >= 2 GiB (split the batch)");
     std::memset(plan, 0, sizeof(*plan));
     const bool dw = is_depthwise(d);
     if (dw) {
@@ -612,6 +833,7 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
         }
         if (ksplit < 1) ksplit = 1;
         if (ksplit > g.nsteps) ksplit = (int) g.nsteps;
+        while (ksplit > 1 && (int64_t) ksplit * g.Coutb * g.P * 16 >= (1LL << 31)) --ksplit;
         plan->ksplit          = ksplit;
         plan->workspace_bytes = (size_t) ksplit * g.Coutb * g.P * 16;
     } else if (wino) {
@@ -648,7 +870,7 @@ int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
                 for (int ky = 0; ky < d->KH; ++ky)
                     for (int kx = 0; kx < d->KW; ++kx) {
                         int64_t slot = ((int64_t) ky * d->KW + kx) * g.Cinb + ic / 4;
-                        wp[(int64_t) oc * g.Kp + slot * 4 + ic % 4] = (half_t) w[(((int64_t) oc * d->Cin + ic) * d->KH + ky) * d->KW + kx];
+                        wp[tiled_index(g, kTiles[plan->tile].BM, oc, slot * 4 + ic % 4)] = (half_t) w[(((int64_t) oc * d->Cin + ic) * d->KH + ky) * d->KW + kx];
                     }
         return VKHIP_OK;
     }
@@ -664,7 +886,7 @@ int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
             for (int i = 0; i < 4; ++i)
                 for (int j = 0; j < 4; ++j) {
                     float u = Gg[i][0] * G[j][0] + Gg[i][1] * G[j][1] + Gg[i][2] * G[j][2];
-                    wp[(i * 4 + j) * plane + (int64_t) oc * g.Kp + ic] = (half_t) u;
+                    wp[(i * 4 + j) * plane + tiled_index(g, kTiles[plan->tile].BM, oc, ic)] = (half_t) u;
                 }
         }
     return VKHIP_OK;
@@ -714,7 +936,6 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     a.Cout   = d->Cout;
     a.P      = (int) g.P;
     a.Kslots = (int) g.Kslots;
-    a.Kp     = (int) g.Kp;
     a.nsteps = (int) g.nsteps;
     a.steps_per_split = (int) g.nsteps;
     a.act    = d->act;
@@ -733,6 +954,8 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
         int rc = check_launch("wino_input");
         if (rc) return rc;
         a.x = V;
+        a.x_bytes = (unsigned) (g.Cinb * nT * 8);
+        a.y_bytes = (unsigned) (g.Coutb * nT * 8);
         a.y = M;
         a.H = 1; a.W = nT; a.HW = nT;
         a.OW = nT; a.OHW = nT;
@@ -751,6 +974,8 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     }
 
     a.x  = (const uint2 *) x;
+    a.x_bytes = (unsigned) ((int64_t) d->N * g.Cinb * d->H * d->W * 8);
+    a.y_bytes = (unsigned) ((int64_t) d->N * g.Coutb * d->OH * d->OW * 8);
     a.y  = (uint2 *) y;
     a.res = (const uint2 *) res;
     a.has_res = d->has_res;
