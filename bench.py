@@ -130,14 +130,16 @@ def main():
     img_s = args.batch * args.steps / wall
     log(f"b{args.batch}: {ms_step:.3f} ms/step wall, {ev / args.steps * 1e3:.3f} ms/step events, {img_s:.1f} img/s")
 
-    # ---- batch-1 latency
-    s1 = V.Session(args.model, 1, seed=7, options=args.options)
-    x1 = V.DeviceBuffer.from_array(x[:1])
-    s1.bind_device_input(x1.ptr)
-    wall1, _ = time_steps(s1, args.b1_steps, 10)
-    b1_ms = wall1 / args.b1_steps * 1e3
-    s1.close()
-    log(f"b1: {b1_ms:.3f} ms/img")
+    # ---- batch-1 latency (skipped with --b1-steps 0, e.g. under a profiler)
+    b1_ms = None
+    if args.b1_steps > 0:
+        s1 = V.Session(args.model, 1, seed=7, options=args.options)
+        x1 = V.DeviceBuffer.from_array(x[:1])
+        s1.bind_device_input(x1.ptr)
+        wall1, _ = time_steps(s1, args.b1_steps, 10)
+        b1_ms = wall1 / args.b1_steps * 1e3
+        s1.close()
+        log(f"b1: {b1_ms:.3f} ms/img")
 
     # ---- per-op roofline (separate profiled session, same graph and tuned plans)
     extra = {}
@@ -183,8 +185,8 @@ def main():
                    "batch": args.batch, "input": "x".join(map(str, sess.in_shape[1:])),
                    "layout": "NC4HW4 fp16", "options": args.options or "default",
                    "tflops_per_step": round(flops_img * args.batch / 1e12, 4)},
-        "b1_ms_per_img": round(b1_ms, 4),
-        "b1_img_per_s": round(1000.0 / b1_ms, 1),
+        "b1_ms_per_img": round(b1_ms, 4) if b1_ms else None,
+        "b1_img_per_s": round(1000.0 / b1_ms, 1) if b1_ms else None,
         "tflops": round(flops_img * img_s / 1e12, 2),
         "roofline": roof,
         "cpu_baseline": cpu,
