@@ -77,6 +77,17 @@ def profile_ops(model, batch, x_dev, options="", reps=3):
     return list(acc.values()), plan
 
 
+def profiled_traffic():
+    """Conv-kernel HBM bytes per step from the committed rocprofv3 PMC summary (FETCH_SIZE and
+    WRITE_SIZE, calibrated), or None when that summary is absent."""
+    import re
+    path = os.path.join(ROOT, "profiles", "resnet50_b64_traffic.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"conv kernels read ([0-9.]+) MB and wrote ([0-9.]+) MB", open(path).read())
+    return None if not m else (float(m.group(1)) + float(m.group(2))) * 1e6
+
+
 def cpu_baseline(model, seconds_budget=20.0):
     """The reference CPU backend (oracle/_ref, compiled from the reference sources) or, where that
     library is absent, the oracle restatement: single thread, batch 1, whole images until the
@@ -108,6 +119,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--b1-steps", type=int, default=100)
+    ap.add_argument("--traffic-probe", type=int, default=0, metavar="MELEMS",
+                    help="only run the flat fp32->fp16 convert over MELEMS million elements 5 times (known HBM "
+                         "traffic: 6 bytes per element), to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (--gpus {args.gpus} refused). "
@@ -116,6 +130,15 @@ def main():
 
     import vknn_amd as V
     V.require_gpu()
+    if args.traffic_probe:
+        n = args.traffic_probe * 1000000
+        src, dst = V.DeviceBuffer(4 * n), V.DeviceBuffer(2 * n)
+        src.zero()
+        for _ in range(5):
+            V.check(V.vkhip().vkhip_pack_flat_f32(src.ptr, dst.ptr, n, None))
+        V.check(V.vkhip().vkhip_device_sync())
+        print(json.dumps({"traffic_probe": "pack_flat_kernel", "read_bytes": 4 * n, "write_bytes": 2 * n, "launches": 5}))
+        return
     flops_img = V.vknn().vknn_model_flops(args.model.encode())
 
     # ---- batch-B throughput (the headline)
@@ -152,9 +175,12 @@ def main():
         all_ms = sum(o["gpu_ms"] for o in ops)
         achieved = conv_fl / (conv_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+                "traffic": profiled_traffic() if (args.model, args.batch) == ("resnet50", 64) else None,
+                "traffic_unit": "HBM bytes per step, all conv launches (profiles/resnet50_b64_traffic.md)",
                 "kernel": "conv_gemm_kernel (all conv/FC launches of one step)",
-                "launch_ms": round(conv_ms, 4), "flops_per_step": conv_fl}
+                "launch_ms": round(conv_ms, 4), "flops_per_step": conv_fl,
+                "algorithmic_bytes_per_step": sum(o["bytes"] for o in conv)}
         pw = [o for o in conv if "conv" in o["name"] and o["bytes"] > 0]
         one = [o for o in pw if o["flops"] / max(o["bytes"], 1) < 315]  # layers below the ridge
         if one:

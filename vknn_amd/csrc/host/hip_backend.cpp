@@ -12,6 +12,7 @@
 // MI355X-specific: the launch sequence of a segment is captured once into a HIP graph and replayed.
 #include "hip_backend.h"
 #include "vkhip.h"
+#include "vknn/profiler.h"
 #include <algorithm>
 #include <chrono>
 #include <cmath>
