@@ -118,7 +118,11 @@ def test_conv_auto(gpu, case):
     assert_parity(got, ref, f"conv {case} algo={plan.algo} tile={plan.tile}")
 
 
-@pytest.mark.parametrize("tile", range(8))
+NUM_TILES = V.vkhip().vkhip_conv_tile_count()
+BD_TILES = list(range(8, NUM_TILES))  # conv_bd_kernel tiles (A via LDS DMA, B gathered into registers)
+
+
+@pytest.mark.parametrize("tile", range(NUM_TILES))
 def test_conv_every_tile(gpu, tile):
     r = rng(10 + tile)
     x = round_half(r.standard_normal((2, 48, 17, 19)))
@@ -129,13 +133,41 @@ def test_conv_every_tile(gpu, tile):
     assert_parity(got, ref, f"tile {tile}")
 
 
-@pytest.mark.parametrize("tile", [0, 3, 6])
+@pytest.mark.parametrize("tile", [0, 3, 6] + BD_TILES)
 def test_conv_every_tile_1x1_aligned(gpu, tile):
     r = rng(20 + tile)
     x = round_half(r.standard_normal((3, 64, 9, 9)))
     w = (r.standard_normal((96, 64, 1, 1)) * 0.1).astype(np.float32)
     got, _, _ = gpu_conv(x, w, None, act=0, algo=V.CONV_GEMM, tile=tile)
     assert_parity(got, oracle_conv(x, w), f"1x1 tile {tile}")
+
+
+@pytest.mark.parametrize("tile", BD_TILES)
+def test_conv_bd_general_gather_residual(gpu, tile):
+    """Channel counts that are not a multiple of 16 (per-slot tap decode), stride 2, a K tail,
+    ragged output channels and pixels, residual + ReLU6 epilogue."""
+    r = rng(40 + tile)
+    x = round_half(r.standard_normal((3, 22, 13, 11)))
+    w = (r.standard_normal((70, 22, 3, 3)) * 0.1).astype(np.float32)
+    b = (r.standard_normal(70) * 0.1).astype(np.float32)
+    res = round_half(r.standard_normal((3, 70, 7, 6)))
+    got, plan, _ = gpu_conv(x, w, b, (2, 2), (1, 1, 1, 1), act=2, res=res, algo=V.CONV_GEMM, tile=tile)
+    ref = oracle_conv(x, w, b, (2, 2), (1, 1, 1, 1), res=res, act=2)
+    assert_parity(got, ref, f"bd general tile {tile}")
+
+
+@pytest.mark.parametrize("tile", [8, 10])
+def test_conv_bd_splitk_and_winograd(gpu, tile):
+    r = rng(60 + tile)
+    x = round_half(r.standard_normal((1, 256, 7, 7)))
+    w = (r.standard_normal((128, 256, 3, 3)) * 0.05).astype(np.float32)
+    b = (r.standard_normal(128) * 0.1).astype(np.float32)
+    ref = oracle_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1)
+    got, plan, _ = gpu_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1, algo=V.CONV_SPLITK, tile=tile, ksplit=6)
+    assert plan.ksplit == 6
+    assert_parity(got, ref, f"bd split-K tile {tile}")
+    got, plan, _ = gpu_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1, algo=V.CONV_WINOGRAD, tile=tile)
+    assert_parity(got, ref, f"bd winograd tile {tile}")
 
 
 @pytest.mark.parametrize("ksplit", [2, 3, 8, 16])

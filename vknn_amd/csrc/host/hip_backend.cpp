@@ -161,15 +161,21 @@ namespace vknn {
                 vkhip_conv_plan base;
                 check(vkhip_conv_plan_make(&d, VKHIP_CONV_AUTO, -1, 0, &base), "conv plan");
                 int64_t pixels = (int64_t) d.N * d.OH * d.OW;
-                if (pixels <= 4096 || base.algo == VKHIP_CONV_SPLITK) {
-                    for (int t: {3, 6, 1})
-                        for (int ks: {2, 4, 8, 16}) cands.push_back({VKHIP_CONV_SPLITK, t, ks});
+                // Split-K when the direct grid cannot fill the device (fewer than ~2 workgroups per CU
+                // with the big tiles) and the reduction is deep enough to split.
+                const int64_t kdepth = (int64_t) d.KH * d.KW * ((d.Cin + 3) / 4) * 4;
+                if (pixels <= 4096 || base.algo == VKHIP_CONV_SPLITK || (pixels * (int64_t) d.Cout <= (int64_t) 512 * 128 * 256 && kdepth >= 512)) {
+                    for (int t: {3, 6, 1, 8, 10})
+                        for (int ks: {2, 3, 4, 8, 16}) cands.push_back({VKHIP_CONV_SPLITK, t, ks});
                 }
                 if (tuning != (int) Mode::Thorough) {
-                    // Fast: the heuristic pick, its neighbours and the split-K set.
+                    // Fast: the heuristic pick, the tiles that win somewhere on the config shapes, and
+                    // the split-K set.
                     std::vector<std::array<int32_t, 3>> keep;
                     for (auto &c: cands)
-                        if (c[0] == VKHIP_CONV_SPLITK || c[1] == base.tile || c[1] == 0 || c[1] == 1 || c[1] == 3 || c[1] == 5 || c[1] == 7) keep.push_back(c);
+                        if (c[0] == VKHIP_CONV_SPLITK || c[1] == base.tile || c[1] == 0 || c[1] == 1 || c[1] == 3 || c[1] == 5 ||
+                            c[1] == 7 || c[1] >= 8)
+                            keep.push_back(c);
                     cands = keep;
                 }
                 double                 best = 1e30, bestDirect = 1e30;

@@ -457,6 +457,308 @@ namespace vkhip {
         }
     }
 
+    // ------------------------------------------------------------------ B-direct GEMM kernel
+    // Second main loop for the same implicit GEMM, built to cut LDS traffic per MFMA:
+    //   * A (weights) is prepacked on the host in MFMA fragment order ([m_tile][stage][kk][m_frag]
+    //     [lane][8 halves]) and copied global -> LDS by the buffer unit itself (buffer_load ... lds,
+    //     16 bytes per lane), three stages deep; no VGPR staging, no ds_write;
+    //   * B (activation pixels) never touches LDS: every lane gathers the two NC4HW4 slots of its own
+    //     fragment column straight into the MFMA operand registers, one stage ahead;
+    //   * each wave owns a (32*FM) x (32*FN) block; the 4 waves tile the workgroup WM x WN.
+    // LDS reads per 16-K step and wave are FM fragments (the A operand) for FM*FN MFMAs.
+    template <int I, int N, typename F>
+    __device__ __forceinline__ void static_for(F &&f) {
+        if constexpr (I < N) {
+            f(std::integral_constant<int, I> {});
+            static_for<I + 1, N>(f);
+        }
+    }
+
+    // D = prefetch distance in stages: stage ks+D is issued while stage ks computes (D+1 register
+    // sets for B, D+2 LDS buffers for A).
+    template <int FM, int FN, int WM, int WN, int BMODE, int D>
+    __global__ __launch_bounds__(kThreads, (16 * FM * FN + 16 * FN * (D + 1) + 4 * FM + 40 <= 256) ? 2 : 1) void conv_bd_kernel(GemmArgs a) {
+        static_assert(WM * WN == 4, "4 waves");
+        static_assert(BMODE == BMODE_1X1 || BMODE == BMODE_ALIGNED || BMODE == BMODE_GENERAL, "B mode");
+        constexpr int BM     = WM * 32 * FM;
+        constexpr int MF     = BM / 32;            // m fragments per tile
+        constexpr int ASTAGE = BM * kBK * 2;       // bytes of one A stage
+        constexpr int NA     = ASTAGE / (kThreads * 16); // LDS DMA instructions per thread and stage
+        constexpr int NB     = 4 * FN * 2;         // B loads per lane and stage
+        constexpr int NBUF   = D + 2;
+        static_assert(NA >= 1 && ASTAGE % (kThreads * 16) == 0, "A stage");
+        __shared__ __attribute__((aligned(16))) unsigned char As[NBUF][ASTAGE];
+
+        const int tid  = threadIdx.x;
+        const int lane = tid & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int wmi  = wave / WN;
+        const int wni  = wave % WN;
+
+        const int lin    = xcd_remap(blockIdx.x, gridDim.x);
+        const int m_tile = lin % a.m_tiles;
+        const int n_tile = lin / a.m_tiles;
+        const int m0     = m_tile * BM;
+        const int n0     = n_tile * (WN * 32 * FN);
+        const int split  = blockIdx.y;
+        const int bz     = blockIdx.z;
+        const int wm0    = wmi * 32 * FM;
+        const int wn0    = wni * 32 * FN;
+
+        const uint2         *X  = a.x + bz * a.x_bstride;
+        const unsigned char *Wt = reinterpret_cast<const unsigned char *>(a.w + bz * a.w_bstride) + (long long) m_tile * a.nsteps * ASTAGE;
+
+        const int ks_begin = split * a.steps_per_split;
+        const int ks_end   = min(a.nsteps, ks_begin + a.steps_per_split);
+
+        // Buffer resources. Range checks apply to the per-lane offset; every guard (padding tap,
+        // pixel past P, K tail, stage past ks_end) therefore lives in the VGPR offset, while the
+        // wave-uniform part of each address (channel slot, tap shift, stage) goes in the SGPR
+        // offset. The activation resource is rebased by `lead` bytes so per-lane pixel offsets,
+        // which include the top/left padding shift, are never negative.
+        const int lead = (a.PT * a.W + a.PL) * 8;
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *) ((const char *) X - lead), (short) 0,
+                                                                             (int) a.x_bytes + lead, 0x00020000);
+        const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *) Wt, (short) 0, ks_end * ASTAGE, 0x00020000);
+        constexpr unsigned kInvalid = 0x80000000u;
+        const int hw8    = a.HW * 8;
+        const int kslots = min(a.Kslots, ks_end * 16);
+        const int g      = lane >> 5; // which pair of slots of a 16-K step this lane supplies
+
+        // this lane's fragment columns (output pixels): offset of (n, slot 2g, iy0, ix0) and, for
+        // the shared-tap gather, the set of taps that land inside the image
+        unsigned pbase[FN];
+        unsigned tapok[FN];
+        int      piy[FN], pix[FN];
+        bool     pv[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int p  = n0 + wn0 + 32 * j + (lane & 31);
+            pv[j]        = p < a.P;
+            const int pp = pv[j] ? p : 0;
+            const int n  = pp / a.OHW;
+            const int r  = pp - n * a.OHW;
+            const int oy = r / a.OW;
+            const int ox = r - oy * a.OW;
+            piy[j]       = oy * a.SH - a.PT;
+            pix[j]       = ox * a.SW - a.PL;
+            pbase[j]     = (unsigned) ((n * a.Cinb * a.HW + piy[j] * a.W + pix[j]) * 8 + lead + 2 * g * hw8);
+            tapok[j]     = 0;
+            if constexpr (BMODE == BMODE_ALIGNED) {
+                for (int t = 0; t < a.Kslots / a.Cinb; ++t) {
+                    const int ky = t / a.KW, kx = t - (t / a.KW) * a.KW;
+                    const bool ok = pv[j] & ((unsigned) (piy[j] + ky * a.DH) < (unsigned) a.H) & ((unsigned) (pix[j] + kx * a.DW) < (unsigned) a.W);
+                    tapok[j] |= (ok ? 1u : 0u) << t;
+                }
+            }
+            if (!pv[j]) pbase[j] = kInvalid;
+        }
+
+        u32x2 breg[D + 1][4][FN][2];
+
+        auto issue_a = [&](int ks) __attribute__((always_inline)) {
+            unsigned char *dst = As[ks % NBUF];
+#pragma unroll
+            for (int r = 0; r < NA; ++r) {
+                const int chunk = (r * 4 + wave) * 1024; // wave-uniform LDS base of this 1 KB piece
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (__attribute__((address_space(3))) void *) (dst + chunk), 16,
+                                                         (unsigned) (chunk + lane * 16) + (unsigned) (ks * ASTAGE), 0, 0, 0);
+            }
+        };
+        auto issue_b = [&](int ks, auto set_c) __attribute__((always_inline)) {
+            constexpr int S = decltype(set_c)::value;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int s0 = ks * 16 + kk * 4; // first slot of this 16-K step (wave-uniform)
+                if constexpr (BMODE == BMODE_1X1) {
+                    const unsigned so = (unsigned) (s0 * hw8);
+                    if (s0 + 4 <= kslots) {
+#pragma unroll
+                        for (int j = 0; j < FN; ++j) {
+                            breg[S][kk][j][0] = __builtin_amdgcn_raw_buffer_load_b64(xrs, pbase[j], so, 0);
+                            breg[S][kk][j][1] = __builtin_amdgcn_raw_buffer_load_b64(xrs, pbase[j], so + hw8, 0);
+                        }
+                    } else { // K tail: slots past Kslots read zero
+                        const bool k0 = s0 + 2 * g < kslots, k1 = s0 + 2 * g + 1 < kslots;
+#pragma unroll
+                        for (int j = 0; j < FN; ++j) {
+                            breg[S][kk][j][0] = __builtin_amdgcn_raw_buffer_load_b64(xrs, k0 ? pbase[j] : kInvalid, so, 0);
+                            breg[S][kk][j][1] = __builtin_amdgcn_raw_buffer_load_b64(xrs, k1 ? pbase[j] : kInvalid, so + hw8, 0);
+                        }
+                    }
+                } else if constexpr (BMODE == BMODE_ALIGNED) {
+                    // Cinb % 4 == 0: the 4 slots of the step share one tap
+                    const int tap = s0 / a.Cinb;
+                    const int cb  = s0 - tap * a.Cinb;
+                    const int ky  = tap / a.KW;
+                    const int kx  = tap - ky * a.KW;
+                    const unsigned so = (unsigned) (cb * hw8 + (ky * a.DH * a.W + kx * a.DW) * 8);
+                    const bool kin = s0 < kslots;
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+                        const unsigned vo = (kin && ((tapok[j] >> tap) & 1u)) ? pbase[j] : kInvalid;
+                        breg[S][kk][j][0] = __builtin_amdgcn_raw_buffer_load_b64(xrs, vo, so, 0);
+                        breg[S][kk][j][1] = __builtin_amdgcn_raw_buffer_load_b64(xrs, vo, so + hw8, 0);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int slot = s0 + 2 * g + e;
+                        const int tap  = slot / a.Cinb;
+                        const int cb   = slot - tap * a.Cinb;
+                        const int ky   = tap / a.KW;
+                        const int kx   = tap - ky * a.KW;
+                        const int dy = ky * a.DH, dx = kx * a.DW;
+                        const int o  = (cb - 2 * g) * hw8 + (dy * a.W + dx) * 8;
+#pragma unroll
+                        for (int j = 0; j < FN; ++j) {
+                            const bool ok = (slot < kslots) & pv[j] & ((unsigned) (piy[j] + dy) < (unsigned) a.H) & ((unsigned) (pix[j] + dx) < (unsigned) a.W);
+                            breg[S][kk][j][e] = __builtin_amdgcn_raw_buffer_load_b64(xrs, ok ? pbase[j] + (unsigned) o : kInvalid, 0, 0);
+                        }
+                    }
+                }
+            }
+        };
+
+        float16v acc[FM][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+        // vmcnt wait immediate (gfx9 encoding: vmcnt[3:0] | expcnt[6:4]=7 | lgkmcnt[11:8]=15 | vmcnt[5:4] at [15:14])
+        constexpr int kAhead     = D * (NA + NB) < 63 ? D * (NA + NB) : 63; // loads that may stay in flight
+        constexpr int kWaitStage = (kAhead & 15) | (7 << 4) | (15 << 8) | ((kAhead >> 4) << 14);
+        constexpr int kWaitAll   = (7 << 4) | (15 << 8);
+
+        // A fragments are double buffered: step kk+1's LDS reads are in flight while step kk's
+        // MFMAs issue.
+        auto compute = [&](int ks, auto set_c) __attribute__((always_inline)) {
+            constexpr int S = decltype(set_c)::value;
+            const unsigned char *Ab = As[ks % NBUF] + ((wmi * FM) * 64 + lane) * 16;
+            half8 fa[2][FM];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) fa[0][i] = *reinterpret_cast<const half8 *>(Ab + i * 1024);
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                if (kk < 3) {
+#pragma unroll
+                    for (int i = 0; i < FM; ++i) fa[(kk + 1) & 1][i] = *reinterpret_cast<const half8 *>(Ab + ((kk + 1) * MF + i) * 1024);
+                }
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const u32x4 bv = u32x4_make(breg[S][kk][j][0].x, breg[S][kk][j][0].y, breg[S][kk][j][1].x, breg[S][kk][j][1].y);
+                    const half8 fb = __builtin_bit_cast(half8, bv);
+#pragma unroll
+                    for (int i = 0; i < FM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk & 1][i], fb, acc[i][j], 0, 0, 0);
+                }
+            }
+        };
+
+        // Stage ks: issue stage ks+1 (A into LDS buffer (ks+1)%3, B into the other register set),
+        // wait until stage ks has landed, barrier (every wave's share of A is in LDS and every wave
+        // is done with stage ks-1, so the next issue may reuse buffer (ks+2)%3 = (ks-1)%3), compute.
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        // The loop runs whole groups of D+1 stages (register sets are compile-time indices) and has a
+        // single exit, so the accumulators stay in place; the last < D+1 stages run after it. Each
+        // stage issues stage ks+D (A into LDS buffer (ks+D)%(D+2), B into the set freed by stage
+        // ks-1), waits until stage ks has landed, then barriers: every wave's share of A is in LDS
+        // and every wave is done with stage ks-1, whose buffer the next issue reuses. Issues past
+        // ks_end read zeros (out-of-range buffer offsets) into idle buffers.
+        if (ks_begin < ks_end) {
+            static_for<0, D>([&](auto p) {
+                issue_a(ks_begin + p.value);
+                issue_b(ks_begin + p.value, p);
+            });
+            int ks = ks_begin;
+            for (; ks + (D + 1) <= ks_end; ks += D + 1) {
+                static_for<0, D + 1>([&](auto p) {
+                    constexpr int P = decltype(p)::value;
+                    issue_a(ks + P + D);
+                    issue_b(ks + P + D, std::integral_constant<int, (P + D) % (D + 1)> {});
+                    __builtin_amdgcn_s_waitcnt(kWaitStage);
+                    __asm__ volatile("s_barrier" ::: "memory");
+                    compute(ks + P, p);
+                });
+            }
+            static_for<0, D>([&](auto p) {
+                if (ks + p.value < ks_end) {
+                    __builtin_amdgcn_s_waitcnt(kWaitAll);
+                    __asm__ volatile("s_barrier" ::: "memory");
+                    compute(ks + p.value, p);
+                }
+            });
+        }
+
+        // ---- epilogue (same D-fragment layout and stores as conv_gemm_kernel), one fragment column
+        // j at a time so only that column's residual loads and offsets are live next to the sums.
+        const int lrow = lane & 31;
+        const int lk   = lane >> 5;
+        uint2    *Y    = a.y + bz * a.y_bstride;
+        const bool epi = a.omode == OMODE_EPILOGUE;
+        const bool use_res = epi && a.has_res;
+        const __amdgpu_buffer_rsrc_t yrs = a.omode == OMODE_PARTIAL
+            ? __builtin_amdgcn_make_buffer_rsrc((void *) a.part, (short) 0, 0x7FFFFFFF, 0x00020000)
+            : __builtin_amdgcn_make_buffer_rsrc((void *) Y, (short) 0, (int) a.y_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc((void *) (use_res ? a.res + bz * a.y_bstride : Y), (short) 0,
+                                                                             use_res ? (int) a.y_bytes : 0, 0x00020000);
+        auto finish = [&](auto act_c) __attribute__((always_inline)) {
+            constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int  px  = n0 + wn0 + j * 32 + lrow;
+                const bool pok = px < a.P;
+                const int  pn  = px / a.OHW;
+                const int  pr  = px - pn * a.OHW;
+                unsigned   yoff[FM][4];
+                u32x2      rv[FM][4];
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) {
+                        const int  ocb = (m0 + wm0 + i * 32 + qq * 8 + lk * 4) >> 2;
+                        const bool ok  = pok & (ocb < a.Coutb);
+                        if (a.omode == OMODE_PARTIAL) yoff[i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + px) * 16) : kInvalid;
+                        else yoff[i][qq] = ok ? (unsigned) (((pn * a.Coutb + ocb) * a.OHW + pr) * 8) : kInvalid;
+                        rv[i][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[i][qq], 0, 0);
+                    }
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) {
+                        const int oc = m0 + wm0 + i * 32 + qq * 8 + lk * 4;
+                        float4v   v  = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
+                        if (a.omode == OMODE_PARTIAL) {
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yrs, yoff[i][qq], 0, 0);
+                            continue;
+                        }
+                        if (epi) v += *reinterpret_cast<const float4v *>(a.bias + oc);
+                        v += h4_to_f4(__builtin_bit_cast(half4, rv[i][qq]));
+                        v.x = apply_act(v.x, ACT, a.lo, a.hi);
+                        v.y = apply_act(v.y, ACT, a.lo, a.hi);
+                        v.z = apply_act(v.z, ACT, a.lo, a.hi);
+                        v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                        if (oc + 0 >= a.Cout) v.x = 0.f;
+                        if (oc + 1 >= a.Cout) v.y = 0.f;
+                        if (oc + 2 >= a.Cout) v.z = 0.f;
+                        if (oc + 3 >= a.Cout) v.w = 0.f;
+                        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff[i][qq], 0, 0);
+                    }
+            }
+        };
+        switch (epi ? a.act : 0) {
+            case VKHIP_ACT_RELU: finish(std::integral_constant<int, VKHIP_ACT_RELU> {}); break;
+            case VKHIP_ACT_RELU6: finish(std::integral_constant<int, VKHIP_ACT_RELU6> {}); break;
+            case VKHIP_ACT_CLIP: finish(std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
+            case VKHIP_ACT_HARDSWISH: finish(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
+            case VKHIP_ACT_SILU: finish(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
+            default: finish(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
+        }
+    }
+
     // Split-K reduce: y = act(sum_s part[s] + bias (+res)).
     __global__ void splitk_reduce_kernel(const float4v *part, const float *bias, const uint2 *res, uint2 *y, int ksplit,
                                          int Coutb, int Cout, int P, int OHW, int act, float lo, float hi, int has_res) {
@@ -671,20 +973,25 @@ namespace vkhip {
     }
 
     // ------------------------------------------------------------------ host side: tiles & plans
+    // kind 0: conv_gemm_kernel (A and B staged through LDS), WM x WN waves over a BM x BN tile.
+    // kind 1: conv_bd_kernel (A via LDS DMA, B straight into registers), waves of (32FM) x (32FN).
     struct TileCfg {
-        int BM, BN, WM, WN;
+        int BM, BN, WM, WN, kind, FM, FN;
     };
     static const TileCfg kTiles[] = {
-        {128, 128, 2, 2}, // 0
-        {64, 128, 2, 2},  // 1
-        {128, 64, 2, 2},  // 2
-        {64, 64, 2, 2},   // 3
-        {256, 128, 2, 2}, // 4
-        {128, 256, 2, 2}, // 5
-        {32, 128, 1, 4},  // 6
-        {64, 256, 1, 4},  // 7
+        {128, 128, 2, 2, 0, 0, 0}, // 0
+        {64, 128, 2, 2, 0, 0, 0},  // 1
+        {128, 64, 2, 2, 0, 0, 0},  // 2
+        {64, 64, 2, 2, 0, 0, 0},   // 3
+        {256, 128, 2, 2, 0, 0, 0}, // 4
+        {128, 256, 2, 2, 0, 0, 0}, // 5
+        {32, 128, 1, 4, 0, 0, 0},  // 6
+        {64, 256, 1, 4, 0, 0, 0},  // 7
+        {128, 256, 1, 4, 1, 4, 2}, // 8
+        {128, 128, 2, 2, 1, 2, 2}, // 9
+        {64, 256, 1, 4, 1, 2, 2},  // 10
     };
-    constexpr int kNumTiles = 8;
+    constexpr int kNumTiles = 11;
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
@@ -699,6 +1006,15 @@ namespace vkhip {
         }
     }
 
+    template <int FM, int FN, int WM, int WN, int D>
+    static GemmKernelFn pick_bd(int bmode) {
+        switch (bmode) {
+            case BMODE_1X1: return conv_bd_kernel<FM, FN, WM, WN, BMODE_1X1, D>;
+            case BMODE_ALIGNED: return conv_bd_kernel<FM, FN, WM, WN, BMODE_ALIGNED, D>;
+            default: return conv_bd_kernel<FM, FN, WM, WN, BMODE_GENERAL, D>;
+        }
+    }
+
     static GemmKernelFn gemm_kernel_for(int tile, int bmode) {
         switch (tile) {
             case 0: return pick_bmode<128, 128, 2, 2>(bmode);
@@ -709,6 +1025,9 @@ namespace vkhip {
             case 5: return pick_bmode<128, 256, 2, 2>(bmode);
             case 6: return pick_bmode<32, 128, 1, 4>(bmode);
             case 7: return pick_bmode<64, 256, 1, 4>(bmode);
+            case 8: return pick_bd<4, 2, 1, 4, 1>(bmode);
+            case 9: return pick_bd<2, 2, 2, 2, 1>(bmode);
+            case 10: return pick_bd<2, 2, 1, 4, 1>(bmode);
         }
         return nullptr;
     }
@@ -735,13 +1054,14 @@ namespace vkhip {
             int64_t nT = (int64_t) d->N * ceil_div(d->OH, 2) * ceil_div(d->OW, 2);
             g.Kslots   = g.Cinb;
             g.P        = nT;
-            g.bmode    = nT % 2 == 0 ? BMODE_1X1_P16 : BMODE_1X1;
+            g.bmode    = (t.kind == 0 && nT % 2 == 0) ? BMODE_1X1_P16 : BMODE_1X1;
         } else {
             g.Kslots = (int64_t) d->KH * d->KW * g.Cinb;
             g.P      = (int64_t) d->N * d->OH * d->OW;
             const bool one  = d->KH == 1 && d->KW == 1 && d->PT == 0 && d->PL == 0;
             const bool unit = d->SW == 1 && d->DW == 1;
-            if (one) g.bmode = (d->SH == 1 && d->SW == 1 && (d->OH * d->OW) % 2 == 0) ? BMODE_1X1_P16 : BMODE_1X1;
+            if (t.kind == 1) g.bmode = one ? BMODE_1X1 : ((g.Cinb % 4 == 0 && d->KH * d->KW <= 32) ? BMODE_ALIGNED : BMODE_GENERAL);
+            else if (one) g.bmode = (d->SH == 1 && d->SW == 1 && (d->OH * d->OW) % 2 == 0) ? BMODE_1X1_P16 : BMODE_1X1;
             else if (g.Cinb % 8 == 0) g.bmode = (unit && d->OW % 2 == 0) ? BMODE_ALIGNED_P16 : BMODE_ALIGNED;
             else g.bmode = BMODE_GENERAL;
         }
@@ -755,8 +1075,15 @@ namespace vkhip {
 
     // Position of weight (oc, k) in the tiled layout [m_tile][k_stage][BM][64]: one K stage of one
     // M tile is a contiguous BM*64-half block, read linearly by the kernel.
-    static inline int64_t tiled_index(const ConvGeom &g, int BM, int64_t oc, int64_t k) {
-        return ((oc / BM) * g.nsteps + k / kBK) * (int64_t) (BM * kBK) + (oc % BM) * kBK + k % kBK;
+    // kind 1 tiles store each stage in MFMA A-fragment order instead: [kk (16-K step)][m fragment]
+    // [lane][8 halves], lane = (k%16)/8*32 + row%32, so the LDS image is the global image.
+    static inline int64_t tiled_index(const ConvGeom &g, const TileCfg &t, int64_t oc, int64_t k) {
+        const int     BM   = t.BM;
+        const int64_t base = ((oc / BM) * g.nsteps + k / kBK) * (int64_t) (BM * kBK);
+        if (t.kind == 0) return base + (oc % BM) * kBK + k % kBK;
+        const int64_t r = oc % BM, kr = k % kBK;
+        const int64_t kk = kr / 16, l = ((kr % 16) / 8) * 32 + r % 32;
+        return base + ((kk * (BM / 32) + r / 32) * 64 + l) * 8 + kr % 8;
     }
 
     static int default_tile(const vkhip_conv_desc *d, bool wino) {
@@ -870,7 +1197,7 @@ int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
                 for (int ky = 0; ky < d->KH; ++ky)
                     for (int kx = 0; kx < d->KW; ++kx) {
                         int64_t slot = ((int64_t) ky * d->KW + kx) * g.Cinb + ic / 4;
-                        wp[tiled_index(g, kTiles[plan->tile].BM, oc, slot * 4 + ic % 4)] = (half_t) w[(((int64_t) oc * d->Cin + ic) * d->KH + ky) * d->KW + kx];
+                        wp[tiled_index(g, kTiles[plan->tile], oc, slot * 4 + ic % 4)] = (half_t) w[(((int64_t) oc * d->Cin + ic) * d->KH + ky) * d->KW + kx];
                     }
         return VKHIP_OK;
     }
@@ -886,7 +1213,7 @@ int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
             for (int i = 0; i < 4; ++i)
                 for (int j = 0; j < 4; ++j) {
                     float u = Gg[i][0] * G[j][0] + Gg[i][1] * G[j][1] + Gg[i][2] * G[j][2];
-                    wp[(i * 4 + j) * plane + tiled_index(g, kTiles[plan->tile].BM, oc, ic)] = (half_t) u;
+                    wp[(i * 4 + j) * plane + tiled_index(g, kTiles[plan->tile], oc, ic)] = (half_t) u;
                 }
         }
     return VKHIP_OK;
