@@ -119,6 +119,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--b1-steps", type=int, default=100)
+    ap.add_argument("--dw-batch", type=int, default=128, help="batch of the MobileNetV3-Large depthwise measurement (0 = skip)")
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="MELEMS",
                     help="only run the flat fp32->fp16 convert over MELEMS million elements 5 times (known HBM "
                          "traffic: 6 bytes per element), to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -191,6 +192,22 @@ def main():
         extra["op_time_share"] = {"conv_ms": round(conv_ms, 4), "all_ops_ms": round(all_ms, 4)}
         with open(os.path.join(ROOT, "gpurun_out", "bench_ops.json") if os.path.isdir(os.path.join(ROOT, "gpurun_out")) else os.devnull, "w") as f:
             json.dump({"ops": ops, "plan": plan}, f, indent=1)
+
+    # ---- bandwidth-bound kernels: depthwise convs of MobileNetV3-Large (config 3) at batch 128
+    if not args.no_profile and args.dw_batch > 0:
+        xs, _ = V.model_io("mobilenetv3_large", args.dw_batch)
+        xd = V.DeviceBuffer.from_array(np.random.default_rng(1).standard_normal(xs).astype(np.float32))
+        dops, dplan = profile_ops("mobilenetv3_large", args.dw_batch, xd, "")
+        kinds = {ln.split()[0]: ln.split()[1] for ln in dplan.splitlines() if len(ln.split()) > 1}
+        dw = [o for o in dops if kinds.get(o["name"]) == "[dwconv]" and o["bytes"] > 0]
+        if dw:
+            b_ms = sum(o["gpu_ms"] for o in dw)
+            b_bytes = sum(o["bytes"] for o in dw)
+            extra["depthwise"] = {"workload": f"mobilenetv3_large b{args.dw_batch}, {len(dw)} depthwise 3x3/5x5 convs",
+                                  "achieved_GBs": round(b_bytes / (b_ms * 1e-3) / 1e9, 1), "peak_GBs": PEAK_HBM_GBS,
+                                  "frac": round(b_bytes / (b_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                                  "launch_ms": round(b_ms, 4), "bytes_per_step": b_bytes}
+        xd.close()
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.model)
 

@@ -92,3 +92,46 @@ def test_batch_items_independent(gpu):
         y1 = s1.run(x[k:k + 1])
         rel, cos = parity(yb[k], y1)
         assert rel <= 5e-3 and cos >= 0.99999, (k, rel, cos)
+
+
+def check_batch_items(model, batch, items, seed, opts=""):
+    """Batched session on the HIP path; selected items against the oracle run at batch 1 on the
+    same images (the conv path is independent across the batch)."""
+    sess = V.Session(model, batch, seed=seed, options=opts)
+    x = make_input(sess.in_shape, 100 + batch)
+    got = sess.run(x)
+    per_item = [n // batch for n in sess.out_elems]
+    for k in items:
+        ref = oracle_model_run(model, 1, seed, x[k:k + 1])
+        g = np.concatenate([got[sum(sess.out_elems[:o]):sum(sess.out_elems[:o + 1])].reshape(batch, -1)[k]
+                            for o in range(len(per_item))])
+        check_outputs(g, ref, per_item, f"{model} b{batch}[{opts}] item {k}")
+
+
+def test_config1_mnv2_block_b32(gpu):
+    check_batch_items("mnv2_block", 32, (0, 31), 7)
+
+
+def test_config2_resnet50_b64_items(gpu):
+    check_batch_items("resnet50", 64, (0, 63), 7)
+
+
+@pytest.mark.parametrize("opts", ["", "fuse_se=1;fuse_dwpw=1"])
+def test_config3_mobilenetv3_large(gpu, opts):
+    sess = V.Session("mobilenetv3_large", 1, seed=7, options=opts)
+    x = make_input(sess.in_shape, 3)
+    check_outputs(sess.run(x), oracle_model_run("mobilenetv3_large", 1, 7, x), sess.out_elems, f"config3[{opts}]")
+
+
+def test_config3_mobilenetv3_large_b128_items(gpu):
+    check_batch_items("mobilenetv3_large", 128, (0, 127), 7, "fuse_se=1;fuse_dwpw=1")
+
+
+def test_config4_yolov8n(gpu):
+    sess = V.Session("yolov8n", 1, seed=7)
+    x = make_input(sess.in_shape, 4)
+    check_outputs(sess.run(x), oracle_model_run("yolov8n", 1, 7, x), sess.out_elems, "config4")
+
+
+def test_config4_yolov8n_b16_items(gpu):
+    check_batch_items("yolov8n", 16, (0, 15), 7)
