@@ -972,6 +972,142 @@ namespace vkhip {
         }
     }
 
+    // LDS-tiled depthwise conv for fixed KHxKW / stride with unit dilation. A workgroup owns PP
+    // consecutive (n, channel block) planes x RT output rows x the full output width: it copies
+    // the input rows those outputs need into LDS once (zero halo for padding, 16-byte loads where
+    // rows are 16-byte aligned). Each thread then owns one output column of one plane and computes
+    // its RT outputs as a vertical strip: the plane's KHxKW weights stay in registers, and every
+    // input row is read from LDS once and added into all the outputs whose window covers it
+    // (fp16 taps feed fp32 FMAs through v_fma_mix). HBM traffic is one read of the input (plus the
+    // KH - S halo rows per strip) and one coalesced write of the output.
+    struct DwTile {
+        int PP, IR, IWp, PLA; // planes per WG, LDS rows per plane, LDS row pitch (pixels), LDS column of ix=0
+        int row_tiles, plane_groups;
+    };
+
+    template <int KH, int KW, int S, int RT>
+    __global__ __launch_bounds__(256) void dwconv_lds_kernel(DwArgs a, DwTile t) {
+        extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
+        constexpr int IR = (RT - 1) * S + KH; // input rows of one strip
+        uint2 *tile = reinterpret_cast<uint2 *>(dsm); // [PP][IR][IWp]
+        const int tid = threadIdx.x;
+        const int rt  = blockIdx.x % t.row_tiles;
+        const int pg  = blockIdx.x / t.row_tiles;
+        const int NCb = a.N * a.Cb;
+        const int p0  = pg * t.PP;
+        const int np  = min(t.PP, NCb - p0);
+        const int oy0 = rt * RT;
+        const int iy0 = oy0 * S - a.PT;
+        const int IWp = t.IWp, PLA = t.PLA;
+
+        // input rows -> LDS: each thread keeps one column and steps down the rows (plane-major)
+        const int W = a.W, H = a.H;
+        const bool v16 = (W % 2 == 0) && (PLA % 2 == 0);
+        {
+            const int cols = v16 ? IWp / 2 : IWp; // 16- or 8-byte units per LDS row
+            const int rpp  = 256 / cols;
+            const int col  = tid % cols;
+            const int ix   = (v16 ? 2 * col : col) - PLA;
+            const bool cok = ix >= 0 && ix < W;
+            int r2 = tid / cols;
+            if (r2 < rpp) {
+                int pl = r2 / IR, r = r2 - pl * IR;
+                while (pl < np) {
+                    const int  iy = iy0 + r;
+                    const bool ok = cok && (unsigned) iy < (unsigned) H;
+                    const long long gi = ((long long) (p0 + pl) * H + iy) * W + ix;
+                    if (v16) {
+                        u32x4 v = u32x4_make(0u, 0u, 0u, 0u);
+                        if (ok) v = *reinterpret_cast<const u32x4 *>(a.x + gi);
+                        reinterpret_cast<u32x4 *>(tile)[(pl * IR + r) * cols + col] = v;
+                    } else {
+                        uint2 v = make_uint2(0u, 0u);
+                        if (ok) v = a.x[gi];
+                        tile[(pl * IR + r) * IWp + col] = v;
+                    }
+                    r += rpp;
+                    while (r >= IR) { r -= IR; ++pl; }
+                }
+            }
+        }
+        __syncthreads();
+
+        const int OW = a.OW;
+        const int ox = tid % OW;
+        const int pl = tid / OW;
+        if (pl >= np) return;
+        const int p  = p0 + pl;
+        const int cb = p % a.Cb;
+        float4v   w[KH * KW];
+#pragma unroll
+        for (int k = 0; k < KH * KW; ++k) w[k] = reinterpret_cast<const float4v *>(a.w)[(long long) cb * KH * KW + k];
+        const float4v b0 = *reinterpret_cast<const float4v *>(a.bias + cb * 4);
+        float4v acc[RT];
+#pragma unroll
+        for (int r = 0; r < RT; ++r) acc[r] = b0;
+        const uint2 *src = tile + pl * IR * IWp + ox * S + (PLA - a.PL);
+#pragma unroll
+        for (int ir = 0; ir < IR; ++ir) {
+            float4v tap[KW];
+#pragma unroll
+            for (int kx = 0; kx < KW; ++kx) tap[kx] = h4_to_f4(u2_as_h4(src[ir * IWp + kx]));
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const int ky = ir - r * S;
+                if (ky < 0 || ky >= KH) continue;
+#pragma unroll
+                for (int kx = 0; kx < KW; ++kx) acc[r] += tap[kx] * w[ky * KW + kx];
+            }
+        }
+        const int       nrows = min(RT, a.OH - oy0);
+        const long long yb    = ((long long) p * a.OH + oy0) * OW + ox;
+        const int       c     = cb * 4;
+        auto finish = [&](auto act_c) __attribute__((always_inline)) {
+            constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                if (r >= nrows) break;
+                float4v v = acc[r];
+                if (a.has_res) v += h4_to_f4(u2_as_h4(a.res[yb + (long long) r * OW]));
+                v.x = apply_act(v.x, ACT, a.lo, a.hi);
+                v.y = apply_act(v.y, ACT, a.lo, a.hi);
+                v.z = apply_act(v.z, ACT, a.lo, a.hi);
+                v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                if (c + 0 >= a.C) v.x = 0.f;
+                if (c + 1 >= a.C) v.y = 0.f;
+                if (c + 2 >= a.C) v.z = 0.f;
+                if (c + 3 >= a.C) v.w = 0.f;
+                a.y[yb + (long long) r * OW] = h4_as_u2(f4_to_h4(v));
+            }
+        };
+        switch (a.act) {
+            case VKHIP_ACT_RELU: finish(std::integral_constant<int, VKHIP_ACT_RELU> {}); break;
+            case VKHIP_ACT_RELU6: finish(std::integral_constant<int, VKHIP_ACT_RELU6> {}); break;
+            case VKHIP_ACT_CLIP: finish(std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
+            case VKHIP_ACT_HARDSWISH: finish(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
+            case VKHIP_ACT_SILU: finish(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
+            default: finish(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
+        }
+    }
+
+    // Tile geometry for dwconv_lds_kernel: as many planes as fill 256 threads with one output
+    // column each; RT output rows per strip.
+    static bool dw_tile(const vkhip_conv_desc *d, int64_t NCb, int RT, DwTile &t) {
+        const int S = d->SH;
+        if (d->OW > 256) return false;
+        t.PLA = (d->PL + 1) & ~1;
+        const int need_w = std::max<int>((d->OW - 1) * S + d->KW - d->PL + t.PLA, t.PLA + d->W);
+        t.IWp = (need_w + 1) & ~1;
+        if (t.IWp > 256) return false;
+        t.IR = (RT - 1) * S + d->KH;
+        t.PP = (int) std::max<int64_t>(1, std::min<int64_t>(NCb, 256 / d->OW));
+        while (t.PP > 1 && (size_t) t.PP * t.IR * t.IWp * 8 > 48 * 1024) --t.PP;
+        if ((size_t) t.PP * t.IR * t.IWp * 8 > 48 * 1024) return false;
+        t.row_tiles    = (int) ceil_div(d->OH, RT);
+        t.plane_groups = (int) ceil_div(NCb, t.PP);
+        return true;
+    }
+
     // ------------------------------------------------------------------ host side: tiles & plans
     // kind 0: conv_gemm_kernel (A and B staged through LDS), WM x WN waves over a BM x BN tile.
     // kind 1: conv_bd_kernel (A via LDS DMA, B straight into registers), waves of (32FM) x (32FN).
@@ -1237,10 +1373,24 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
         a.N = d->N; a.Cb = (int) Cb; a.C = d->Cin; a.H = d->H; a.W = d->W; a.OH = d->OH; a.OW = d->OW;
         a.KH = d->KH; a.KW = d->KW; a.SH = d->SH; a.SW = d->SW; a.PT = d->PT; a.PL = d->PL; a.DH = d->DH; a.DW = d->DW;
         a.act = d->act; a.lo = d->act_lo; a.hi = d->act_hi; a.has_res = d->has_res;
+        bool unit = d->DH == 1 && d->DW == 1 && d->SH == d->SW;
+        DwTile t;
+        const int RT = d->OH % 7 == 0 ? 7 : 4;
+        if (unit && d->KH == d->KW && (d->KH == 3 || d->KH == 5) && (d->SH == 1 || d->SH == 2) && dw_tile(d, (int64_t) d->N * Cb, RT, t)) {
+            const size_t sm = (size_t) t.PP * t.IR * t.IWp * 8;
+            dim3 g2((unsigned) ((int64_t) t.row_tiles * t.plane_groups));
+#define VKHIP_DW_LAUNCH(K, S_)                                                                                 \
+    (RT == 7 ? dwconv_lds_kernel<K, K, S_, 7><<<g2, 256, sm, st>>>(a, t) : dwconv_lds_kernel<K, K, S_, 4><<<g2, 256, sm, st>>>(a, t))
+            if (d->KH == 3 && d->SH == 1) VKHIP_DW_LAUNCH(3, 1);
+            else if (d->KH == 3) VKHIP_DW_LAUNCH(3, 2);
+            else if (d->SH == 1) VKHIP_DW_LAUNCH(5, 1);
+            else VKHIP_DW_LAUNCH(5, 2);
+#undef VKHIP_DW_LAUNCH
+            return check_launch("dwconv_lds");
+        }
         constexpr int OXT = 4;
         int64_t total = (int64_t) d->N * Cb * d->OH * ceil_div(d->OW, OXT);
         dim3 grid((unsigned) ceil_div(total, 256));
-        bool unit = d->DH == 1 && d->DW == 1 && d->SH == d->SW;
         if (unit && d->KH == 3 && d->KW == 3 && d->SH == 1) dwconv_kernel<3, 3, 1, OXT><<<grid, 256, 0, st>>>(a);
         else if (unit && d->KH == 3 && d->KW == 3 && d->SH == 2) dwconv_kernel<3, 3, 2, OXT><<<grid, 256, 0, st>>>(a);
         else if (unit && d->KH == 5 && d->KW == 5 && d->SH == 1) dwconv_kernel<5, 5, 1, OXT><<<grid, 256, 0, st>>>(a);
