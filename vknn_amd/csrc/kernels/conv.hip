@@ -1038,9 +1038,11 @@ namespace vkhip {
         if (pl >= np) return;
         const int p  = p0 + pl;
         const int cb = p % a.Cb;
-        float4v   w[KH * KW];
+        // weights held as fp16 (the storage precision of every GPU weight on this path): half the
+        // registers of fp32, and v_fma_mix takes fp16 x fp16 products into the fp32 sums
+        half4 w[KH * KW];
 #pragma unroll
-        for (int k = 0; k < KH * KW; ++k) w[k] = reinterpret_cast<const float4v *>(a.w)[(long long) cb * KH * KW + k];
+        for (int k = 0; k < KH * KW; ++k) w[k] = f4_to_h4(reinterpret_cast<const float4v *>(a.w)[(long long) cb * KH * KW + k]);
         const float4v b0 = *reinterpret_cast<const float4v *>(a.bias + cb * 4);
         float4v acc[RT];
 #pragma unroll
@@ -1048,15 +1050,21 @@ namespace vkhip {
         const uint2 *src = tile + pl * IR * IWp + ox * S + (PLA - a.PL);
 #pragma unroll
         for (int ir = 0; ir < IR; ++ir) {
-            float4v tap[KW];
+            half4 tap[KW];
 #pragma unroll
-            for (int kx = 0; kx < KW; ++kx) tap[kx] = h4_to_f4(u2_as_h4(src[ir * IWp + kx]));
+            for (int kx = 0; kx < KW; ++kx) tap[kx] = u2_as_h4(src[ir * IWp + kx]);
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
                 const int ky = ir - r * S;
                 if (ky < 0 || ky >= KH) continue;
 #pragma unroll
-                for (int kx = 0; kx < KW; ++kx) acc[r] += tap[kx] * w[ky * KW + kx];
+                for (int kx = 0; kx < KW; ++kx) {
+                    const half4 wv = w[ky * KW + kx];
+                    acc[r].x = __builtin_fmaf((float) tap[kx].x, (float) wv.x, acc[r].x);
+                    acc[r].y = __builtin_fmaf((float) tap[kx].y, (float) wv.y, acc[r].y);
+                    acc[r].z = __builtin_fmaf((float) tap[kx].z, (float) wv.z, acc[r].z);
+                    acc[r].w = __builtin_fmaf((float) tap[kx].w, (float) wv.w, acc[r].w);
+                }
             }
         }
         const int       nrows = min(RT, a.OH - oy0);
