@@ -119,10 +119,12 @@ def test_conv_auto(gpu, case):
 
 
 NUM_TILES = V.vkhip().vkhip_conv_tile_count()
-BD_TILES = list(range(8, NUM_TILES))  # conv_bd_kernel tiles (A via LDS DMA, B gathered into registers)
+BD_TILES = [8, 9, 10]            # conv_bd_kernel tiles (A via LDS DMA, B gathered into registers)
+DMA_TILES = [11, 12, 13, 14, 15]     # conv_dma_kernel tiles (A and B via LDS DMA; dense B only)
+GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES]
 
 
-@pytest.mark.parametrize("tile", range(NUM_TILES))
+@pytest.mark.parametrize("tile", GATHER_TILES)
 def test_conv_every_tile(gpu, tile):
     r = rng(10 + tile)
     x = round_half(r.standard_normal((2, 48, 17, 19)))
@@ -154,6 +156,48 @@ def test_conv_bd_general_gather_residual(gpu, tile):
     got, plan, _ = gpu_conv(x, w, b, (2, 2), (1, 1, 1, 1), act=2, res=res, algo=V.CONV_GEMM, tile=tile)
     ref = oracle_conv(x, w, b, (2, 2), (1, 1, 1, 1), res=res, act=2)
     assert_parity(got, ref, f"bd general tile {tile}")
+
+
+@pytest.mark.parametrize("tile", DMA_TILES)
+@pytest.mark.parametrize("shape", [(3, 72, 6, 10, 70), (2, 256, 14, 14, 300), (1, 24, 8, 8, 8)])
+def test_conv_dma_1x1(gpu, tile, shape):
+    """Dense-B kernel: K tail (Cin not a multiple of 64), ragged output channels, pixel tiles
+    crossing image boundaries and the end of the batch, residual + ReLU epilogue."""
+    N, C, H, W, Cout = shape
+    r = rng(80 + tile + C)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, 1, 1)) * 0.1).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    res = round_half(r.standard_normal((N, Cout, H, W)))
+    got, plan, _ = gpu_conv(x, w, b, act=1, res=res, algo=V.CONV_GEMM, tile=tile)
+    assert plan.tile == tile
+    assert_parity(got, oracle_conv(x, w, b, res=res, act=1), f"dma 1x1 tile {tile} {shape}")
+
+
+@pytest.mark.parametrize("tile", [11, 14])
+def test_conv_dma_winograd_and_splitk(gpu, tile):
+    r = rng(90 + tile)
+    x = round_half(r.standard_normal((2, 128, 14, 14)))
+    w = (r.standard_normal((96, 128, 3, 3)) * 0.05).astype(np.float32)
+    b = (r.standard_normal(96) * 0.1).astype(np.float32)
+    ref = oracle_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1)
+    got, plan, _ = gpu_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1, algo=V.CONV_WINOGRAD, tile=tile)
+    assert_parity(got, ref, f"dma winograd tile {tile}")
+    x1 = round_half(r.standard_normal((1, 512, 8, 8)))
+    w1 = (r.standard_normal((256, 512, 1, 1)) * 0.05).astype(np.float32)
+    got, plan, _ = gpu_conv(x1, w1, None, act=0, algo=V.CONV_SPLITK, tile=tile, ksplit=4)
+    assert plan.ksplit == 4
+    assert_parity(got, oracle_conv(x1, w1), f"dma split-K tile {tile}")
+
+
+def test_conv_dma_rejects_gather_shapes(gpu):
+    """The dense-B tiles refuse shapes whose B operand is a gather (3x3, stride 2, odd pixel count)."""
+    lib = V.vkhip()
+    plan = V.ConvPlan()
+    for xs, ws, st, pd in [((1, 8, 8, 8), (8, 8, 3, 3), (1, 1), (1, 1, 1, 1)), ((1, 8, 8, 8), (8, 8, 1, 1), (2, 2), (0, 0, 0, 0)),
+                           ((1, 8, 7, 7), (8, 8, 1, 1), (1, 1), (0, 0, 0, 0))]:
+        d, _ = conv_desc(xs, ws, st, pd)
+        assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, 11, 0, ctypes.byref(plan)) != 0
 
 
 @pytest.mark.parametrize("tile", [8, 10])

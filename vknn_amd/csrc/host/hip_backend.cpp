@@ -165,7 +165,7 @@ namespace vknn {
                 // with the big tiles) and the reduction is deep enough to split.
                 const int64_t kdepth = (int64_t) d.KH * d.KW * ((d.Cin + 3) / 4) * 4;
                 if (pixels <= 4096 || base.algo == VKHIP_CONV_SPLITK || (pixels * (int64_t) d.Cout <= (int64_t) 512 * 128 * 256 && kdepth >= 512)) {
-                    for (int t: {3, 6, 1, 8, 10})
+                    for (int t: {3, 6, 1, 8, 10, 14})
                         for (int ks: {2, 3, 4, 8, 16}) cands.push_back({VKHIP_CONV_SPLITK, t, ks});
                 }
                 if (tuning != (int) Mode::Thorough) {
@@ -195,13 +195,21 @@ namespace vknn {
                 }
                 bestDirect = best;
                 if (wino_ok && wino != (int) Mode::Off) {
-                    vkhip_conv_plan p;
-                    if (!vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, -1, 0, &p)) {
+                    // the position GEMMs on the heuristic tile and on the register-/DMA-fed tiles
+                    double bestWino = 1e30;
+                    std::array<int32_t, 3> wpick {};
+                    for (int t: {-1, 8, 10, 14, 12}) {
+                        vkhip_conv_plan p;
+                        if (vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, t, 0, &p)) continue;
                         double ms = timePlan(p, w, b, x->ptr, yb->ptr);
-                        // Winograd must win by 3% (reference ops/conv.cpp:16 kWinoMargin) so timing noise
-                        // cannot flip a near-tie between kernels that round differently.
-                        if (ms < bestDirect * 0.97) pick = {p.algo, p.tile, p.ksplit};
+                        if (ms < bestWino) {
+                            bestWino = ms;
+                            wpick    = {p.algo, p.tile, p.ksplit};
+                        }
                     }
+                    // Winograd must win by 3% (reference ops/conv.cpp:16 kWinoMargin) so timing noise
+                    // cannot flip a near-tie between kernels that round differently.
+                    if (bestWino < bestDirect * 0.97) pick = wpick;
                 }
                 {
                     std::lock_guard<std::mutex> lk(g_tune_mu);

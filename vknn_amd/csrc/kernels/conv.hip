@@ -466,6 +466,102 @@ namespace vkhip {
     //     fragment column straight into the MFMA operand registers, one stage ahead;
     //   * each wave owns a (32*FM) x (32*FN) block; the 4 waves tile the workgroup WM x WN.
     // LDS reads per 16-K step and wave are FM fragments (the A operand) for FM*FN MFMAs.
+    // Epilogue shared by the register-tile kernels: the D layout of a 32x32 fragment puts output
+    // column l%32 in lane l and rows 8*(r/4) + 4*(l/32) + r%4 in register r, so registers 4q..4q+3
+    // are one NC4HW4 channel block and each store is one 8-byte write. One fragment column j at a
+    // time: its residual loads and offsets are the only extra registers live next to the sums.
+    // Rows or pixels outside the tensor get an out-of-range offset (loads read zero, stores drop).
+    // Schedule of one 16-K step: NM MFMAs; the next step's NR LDS reads go out between the first
+    // half of them, the NV register moves that assemble B fragments between the last quarter (so
+    // the moves find their reads complete instead of stalling the MFMA issue).
+    // NG global (LDS-DMA) loads, when given, go out one per MFMA from the first one on.
+    template <int I, int NM, int NR, int NV, int NG = 0>
+    struct StepSchedule {
+        static __device__ __forceinline__ void apply() {
+            if constexpr (I < NM) {
+                constexpr int H = NM / 2 > 0 ? NM / 2 : 1;
+                constexpr int Q = NM - (3 * NM) / 4 > 0 ? NM - (3 * NM) / 4 : 1;
+                constexpr int r = I < H ? NR * (I + 1) / H - NR * I / H : 0;
+                constexpr int J = I - (NM - Q);
+                constexpr int v = J >= 0 ? NV * (J + 1) / Q - NV * J / Q : 0;
+                constexpr int gl = NG * (I + 1) / NM - NG * I / NM;
+                __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+                if constexpr (gl > 0) __builtin_amdgcn_sched_group_barrier(SG_VMEM_READ, gl, 0);
+                if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(SG_DS_READ, r, 0);
+                if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(SG_VALU, v, 0);
+                StepSchedule<I + 1, NM, NR, NV, NG>::apply();
+            }
+        }
+    };
+
+    template <int FM, int FN>
+    __device__ __forceinline__ void gemm_epilogue(const GemmArgs &a, float16v (&acc)[FM][FN], int mw0, int nw0, int split, int bz,
+                                                  int lane) {
+        constexpr unsigned kInvalid = 0x80000000u;
+        const int  lrow = lane & 31;
+        const int  lk   = lane >> 5;
+        uint2     *Y    = a.y + bz * a.y_bstride;
+        const bool epi  = a.omode == OMODE_EPILOGUE;
+        const bool use_res = epi && a.has_res;
+        const __amdgpu_buffer_rsrc_t yrs = a.omode == OMODE_PARTIAL
+            ? __builtin_amdgcn_make_buffer_rsrc((void *) a.part, (short) 0, 0x7FFFFFFF, 0x00020000)
+            : __builtin_amdgcn_make_buffer_rsrc((void *) Y, (short) 0, (int) a.y_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc((void *) (use_res ? a.res + bz * a.y_bstride : Y), (short) 0,
+                                                                             use_res ? (int) a.y_bytes : 0, 0x00020000);
+        auto finish = [&](auto act_c) __attribute__((always_inline)) {
+            constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int  px  = nw0 + j * 32 + lrow;
+                const bool pok = px < a.P;
+                const int  pn  = px / a.OHW;
+                const int  pr  = px - pn * a.OHW;
+                unsigned   yoff[FM][4];
+                u32x2      rv[FM][4];
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) {
+                        const int  ocb = (mw0 + i * 32 + qq * 8 + lk * 4) >> 2;
+                        const bool ok  = pok & (ocb < a.Coutb);
+                        if (a.omode == OMODE_PARTIAL) yoff[i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + px) * 16) : kInvalid;
+                        else yoff[i][qq] = ok ? (unsigned) (((pn * a.Coutb + ocb) * a.OHW + pr) * 8) : kInvalid;
+                        rv[i][qq] = use_res ? __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[i][qq], 0, 0) : u32x2 {0u, 0u};
+                    }
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) {
+                        const int oc = mw0 + i * 32 + qq * 8 + lk * 4;
+                        float4v   v  = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
+                        if (a.omode == OMODE_PARTIAL) {
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yrs, yoff[i][qq], 0, 0);
+                            continue;
+                        }
+                        if (epi) v += *reinterpret_cast<const float4v *>(a.bias + oc);
+                        v += h4_to_f4(__builtin_bit_cast(half4, rv[i][qq]));
+                        v.x = apply_act(v.x, ACT, a.lo, a.hi);
+                        v.y = apply_act(v.y, ACT, a.lo, a.hi);
+                        v.z = apply_act(v.z, ACT, a.lo, a.hi);
+                        v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                        if (oc + 0 >= a.Cout) v.x = 0.f;
+                        if (oc + 1 >= a.Cout) v.y = 0.f;
+                        if (oc + 2 >= a.Cout) v.z = 0.f;
+                        if (oc + 3 >= a.Cout) v.w = 0.f;
+                        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff[i][qq], 0, 0);
+                    }
+            }
+        };
+        switch (epi ? a.act : 0) {
+            case VKHIP_ACT_RELU: finish(std::integral_constant<int, VKHIP_ACT_RELU> {}); break;
+            case VKHIP_ACT_RELU6: finish(std::integral_constant<int, VKHIP_ACT_RELU6> {}); break;
+            case VKHIP_ACT_CLIP: finish(std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
+            case VKHIP_ACT_HARDSWISH: finish(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
+            case VKHIP_ACT_SILU: finish(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
+            default: finish(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
+        }
+    }
+
     template <int I, int N, typename F>
     __device__ __forceinline__ void static_for(F &&f) {
         if constexpr (I < N) {
@@ -641,6 +737,7 @@ namespace vkhip {
             half8 fa[2][FM];
 #pragma unroll
             for (int i = 0; i < FM; ++i) fa[0][i] = *reinterpret_cast<const half8 *>(Ab + i * 1024);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 if (kk < 3) {
@@ -654,6 +751,8 @@ namespace vkhip {
 #pragma unroll
                     for (int i = 0; i < FM; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk & 1][i], fb, acc[i][j], 0, 0, 0);
                 }
+                if (kk < 3) Interleave<0, FM * FN, FM, 0, 0>::apply();
+                __builtin_amdgcn_sched_barrier(0);
             }
         };
 
@@ -693,70 +792,149 @@ namespace vkhip {
             });
         }
 
-        // ---- epilogue (same D-fragment layout and stores as conv_gemm_kernel), one fragment column
-        // j at a time so only that column's residual loads and offsets are live next to the sums.
-        const int lrow = lane & 31;
-        const int lk   = lane >> 5;
-        uint2    *Y    = a.y + bz * a.y_bstride;
-        const bool epi = a.omode == OMODE_EPILOGUE;
-        const bool use_res = epi && a.has_res;
-        const __amdgpu_buffer_rsrc_t yrs = a.omode == OMODE_PARTIAL
-            ? __builtin_amdgcn_make_buffer_rsrc((void *) a.part, (short) 0, 0x7FFFFFFF, 0x00020000)
-            : __builtin_amdgcn_make_buffer_rsrc((void *) Y, (short) 0, (int) a.y_bytes, 0x00020000);
-        const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc((void *) (use_res ? a.res + bz * a.y_bstride : Y), (short) 0,
-                                                                             use_res ? (int) a.y_bytes : 0, 0x00020000);
-        auto finish = [&](auto act_c) __attribute__((always_inline)) {
-            constexpr int ACT = decltype(act_c)::value;
+        gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, bz, lane);
+    }
+
+    // ------------------------------------------------------------------ LDS-DMA GEMM kernel
+    // Third main loop, for dense B operands: 1x1 stride-1 convs over images with an even pixel
+    // count, and the Winograd position GEMMs. Both operands reach LDS through the buffer unit
+    // (buffer_load ... lds, 16 bytes per lane) with no VGPR staging:
+    //   A  prepacked weights in MFMA fragment order ([m_tile][stage][kk][m_frag][lane][8 halves]);
+    //   B  [slot][pixel] stage of 16 NC4HW4 channel slots x BN pixels, one lane per pixel pair of
+    //      one slot (a pair never straddles two images because the pixel count per image is even).
+    // Four waves in a 2x2 grid, each owning a (32FM) x (32FN) block; with FM = FN = 4 the
+    // workgroup tile is 256 x 256, which keeps the operand bytes per MFMA (and so the address-unit
+    // and LDS traffic) low enough for the matrix cores. Two LDS stages: stage ks+1 streams in while
+    // stage ks computes (one barrier per stage). A fragments read with ds_read_b128, B fragments
+    // with two ds_read_b64 (slots 2g and 2g+1 of the lane's pixel), both double buffered across
+    // the 16-K steps.
+    template <int FM, int FN, int NS, int WM, int WN>
+    __global__ __launch_bounds__(64 * WM * WN, 1) void conv_dma_kernel(GemmArgs a) {
+        constexpr int NW     = WM * WN; // waves
+        constexpr int BM     = 32 * FM * WM;
+        constexpr int BN     = 32 * FN * WN;
+        constexpr int MF     = BM / 32;
+        constexpr int ASTAGE = BM * kBK * 2;
+        constexpr int BSTAGE = BN * kBK * 2;
+        constexpr int NA     = ASTAGE / (NW * 1024);
+        constexpr int NB     = BSTAGE / (NW * 1024);
+        static_assert(NA >= 1 && NB >= 1 && ASTAGE % (NW * 1024) == 0 && BSTAGE % (NW * 1024) == 0, "stage split");
+        constexpr int BPB    = BN / 128; // 1 KB pixel blocks per slot row of the B stage
+        __shared__ __attribute__((aligned(16))) unsigned char sm[NS][ASTAGE + BSTAGE];
+
+        const int tid  = threadIdx.x;
+        const int lane = tid & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int wmi  = wave / WN;
+        const int wni  = wave % WN;
+
+        const int lin    = xcd_remap(blockIdx.x, gridDim.x);
+        const int m_tile = lin % a.m_tiles;
+        const int n_tile = lin / a.m_tiles;
+        const int m0     = m_tile * BM;
+        const int n0     = n_tile * BN;
+        const int split  = blockIdx.y;
+        const int bz     = blockIdx.z;
+        const int wm0    = wmi * 32 * FM;
+        const int wn0    = wni * 32 * FN;
+
+        const uint2         *X  = a.x + bz * a.x_bstride;
+        const unsigned char *Wt = reinterpret_cast<const unsigned char *>(a.w + bz * a.w_bstride) + (long long) m_tile * a.nsteps * ASTAGE;
+        const int ks_begin = split * a.steps_per_split;
+        const int ks_end   = min(a.nsteps, ks_begin + a.steps_per_split);
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *) X, (short) 0, (int) a.x_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *) Wt, (short) 0, ks_end * ASTAGE, 0x00020000);
+        constexpr unsigned kInvalid = 0x80000000u;
+        const int hw8 = a.HW * 8;
+
+        // B copy: instruction r of this wave fills 1 KB chunk c = r*NW + wave of the stage, i.e.
+        // slot c / BPB, pixels (c % BPB)*128 + 2*lane (+1). Per-lane pixel bases are fixed.
+        unsigned pbase[BPB];
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int  px  = n0 + wn0 + j * 32 + lrow;
-                const bool pok = px < a.P;
-                const int  pn  = px / a.OHW;
-                const int  pr  = px - pn * a.OHW;
-                unsigned   yoff[FM][4];
-                u32x2      rv[FM][4];
+        for (int pb = 0; pb < BPB; ++pb) {
+            const int p = n0 + pb * 128 + 2 * lane;
+            const int n = p / a.HW;
+            pbase[pb]   = p < a.P ? (unsigned) ((n * a.Cinb * a.HW + (p - n * a.HW)) * 8) : kInvalid;
+        }
+        auto issue = [&](int ks, int buf) __attribute__((always_inline)) {
+            unsigned char *dst = sm[buf];
 #pragma unroll
-                for (int i = 0; i < FM; ++i)
+            for (int r = 0; r < NA; ++r) {
+                const int chunk = (r * NW + wave) * 1024;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (__attribute__((address_space(3))) void *) (dst + chunk), 16,
+                                                         (unsigned) (chunk + lane * 16) + (unsigned) (ks * ASTAGE), 0, 0, 0);
+            }
 #pragma unroll
-                    for (int qq = 0; qq < 4; ++qq) {
-                        const int  ocb = (m0 + wm0 + i * 32 + qq * 8 + lk * 4) >> 2;
-                        const bool ok  = pok & (ocb < a.Coutb);
-                        if (a.omode == OMODE_PARTIAL) yoff[i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + px) * 16) : kInvalid;
-                        else yoff[i][qq] = ok ? (unsigned) (((pn * a.Coutb + ocb) * a.OHW + pr) * 8) : kInvalid;
-                        rv[i][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[i][qq], 0, 0);
-                    }
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int qq = 0; qq < 4; ++qq) {
-                        const int oc = m0 + wm0 + i * 32 + qq * 8 + lk * 4;
-                        float4v   v  = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
-                        if (a.omode == OMODE_PARTIAL) {
-                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yrs, yoff[i][qq], 0, 0);
-                            continue;
-                        }
-                        if (epi) v += *reinterpret_cast<const float4v *>(a.bias + oc);
-                        v += h4_to_f4(__builtin_bit_cast(half4, rv[i][qq]));
-                        v.x = apply_act(v.x, ACT, a.lo, a.hi);
-                        v.y = apply_act(v.y, ACT, a.lo, a.hi);
-                        v.z = apply_act(v.z, ACT, a.lo, a.hi);
-                        v.w = apply_act(v.w, ACT, a.lo, a.hi);
-                        if (oc + 0 >= a.Cout) v.x = 0.f;
-                        if (oc + 1 >= a.Cout) v.y = 0.f;
-                        if (oc + 2 >= a.Cout) v.z = 0.f;
-                        if (oc + 3 >= a.Cout) v.w = 0.f;
-                        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff[i][qq], 0, 0);
-                    }
+            for (int r = 0; r < NB; ++r) {
+                const int c    = r * NW + wave;
+                const int slot = ks * 16 + c / BPB; // wave-uniform
+                const unsigned vo = slot < a.Kslots ? pbase[c % BPB] : kInvalid;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void *) (dst + ASTAGE + c * 1024), 16, vo,
+                                                         (unsigned) (slot * hw8), 0, 0);
             }
         };
-        switch (epi ? a.act : 0) {
-            case VKHIP_ACT_RELU: finish(std::integral_constant<int, VKHIP_ACT_RELU> {}); break;
-            case VKHIP_ACT_RELU6: finish(std::integral_constant<int, VKHIP_ACT_RELU6> {}); break;
-            case VKHIP_ACT_CLIP: finish(std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
-            case VKHIP_ACT_HARDSWISH: finish(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
-            case VKHIP_ACT_SILU: finish(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
-            default: finish(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
+
+        float16v acc[FM][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+        const int g = lane >> 5;
+        auto compute = [&](int buf, int next_ks, int next_buf) __attribute__((always_inline)) {
+            const unsigned char *Ab = sm[buf] + ((wmi * FM) * 64 + lane) * 16;
+            const unsigned char *Bb = sm[buf] + ASTAGE + (2 * g * BN + wn0 + (lane & 31)) * 8;
+            half8 fa[2][FM], fb[2][FN];
+            auto rd = [&](int kk, int d) __attribute__((always_inline)) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const u32x2 lo = *reinterpret_cast<const u32x2 *>(Bb + (kk * 4 * BN + 32 * j) * 8);
+                    const u32x2 hi = *reinterpret_cast<const u32x2 *>(Bb + ((kk * 4 + 1) * BN + 32 * j) * 8);
+                    fb[d][j] = __builtin_bit_cast(half8, u32x4_make(lo.x, lo.y, hi.x, hi.y));
+                }
+#pragma unroll
+                for (int i = 0; i < FM; ++i) fa[d][i] = *reinterpret_cast<const half8 *>(Ab + (kk * MF + i) * 1024);
+            };
+            // Each 16-K step issues its MFMAs with the next step's LDS reads interleaved between
+            // them (the scheduler would otherwise reuse one fragment register and wait on every read).
+            rd(0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                // the copies of a later stage go out between the first step's MFMAs
+                if (kk == 0 && next_ks >= 0) issue(next_ks, next_buf);
+                if (kk < 3) rd(kk + 1, (kk + 1) & 1);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk & 1][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
+                if (kk == 0) StepSchedule<0, FM * FN, FM + 2 * FN, 4 * FN, NA + NB>::apply();
+                else if (kk < 3) StepSchedule<0, FM * FN, FM + 2 * FN, 4 * FN>::apply();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+
+        // NS LDS stages, prefetch distance NS-1: stage ks waits for its own copies (the NS-2 later
+        // stages may stay in flight), barriers (all waves' copies landed; all waves done with
+        // stage ks-1, whose buffer the next issue refills), issues stage ks+NS-1, computes.
+        constexpr int kAhead = (NS - 2) * (NA + NB) < 63 ? (NS - 2) * (NA + NB) : 63;
+        constexpr int kWait  = (kAhead & 15) | (7 << 4) | (15 << 8) | ((kAhead >> 4) << 14);
+        if (ks_begin < ks_end) {
+#pragma unroll
+            for (int d = 0; d < NS - 1; ++d)
+                if (ks_begin + d < ks_end) issue(ks_begin + d, d);
+            for (int ks = ks_begin; ks < ks_end; ++ks) {
+                const int rel = ks - ks_begin;
+                if (ks + NS - 2 < ks_end) __builtin_amdgcn_s_waitcnt(kWait);
+                else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); // tail: nothing later in flight
+                __asm__ volatile("s_barrier" ::: "memory");
+                compute(rel % NS, ks + NS - 1 < ks_end ? ks + NS - 1 : -1, (rel + NS - 1) % NS);
+            }
         }
+        gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, bz, lane);
     }
 
     // Split-K reduce: y = act(sum_s part[s] + bias (+res)).
@@ -1119,6 +1297,8 @@ namespace vkhip {
     // ------------------------------------------------------------------ host side: tiles & plans
     // kind 0: conv_gemm_kernel (A and B staged through LDS), WM x WN waves over a BM x BN tile.
     // kind 1: conv_bd_kernel (A via LDS DMA, B straight into registers), waves of (32FM) x (32FN).
+    // kind 2: conv_dma_kernel (A and B via LDS DMA; dense B only: 1x1 s1 with an even pixel count
+    //         per image, Winograd GEMMs with an even tile count), 2x2 waves of (32FM) x (32FN).
     struct TileCfg {
         int BM, BN, WM, WN, kind, FM, FN;
     };
@@ -1134,8 +1314,13 @@ namespace vkhip {
         {128, 256, 1, 4, 1, 4, 2}, // 8
         {128, 128, 2, 2, 1, 2, 2}, // 9
         {64, 256, 1, 4, 1, 2, 2},  // 10
+        {256, 256, 2, 2, 2, 4, 4}, // 11
+        {256, 256, 2, 4, 2, 4, 2}, // 12 (8 waves)
+        {256, 256, 4, 2, 2, 2, 4}, // 13 (8 waves)
+        {128, 128, 2, 2, 2, 2, 2}, // 14
+        {256, 128, 4, 2, 2, 2, 2}, // 15 (8 waves)
     };
-    constexpr int kNumTiles = 11;
+    constexpr int kNumTiles = 16;
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
@@ -1172,6 +1357,11 @@ namespace vkhip {
             case 8: return pick_bd<4, 2, 1, 4, 1>(bmode);
             case 9: return pick_bd<2, 2, 2, 2, 1>(bmode);
             case 10: return pick_bd<2, 2, 1, 4, 1>(bmode);
+            case 11: return conv_dma_kernel<4, 4, 2, 2, 2>;
+            case 12: return conv_dma_kernel<4, 2, 2, 2, 4>;
+            case 13: return conv_dma_kernel<2, 4, 2, 4, 2>;
+            case 14: return conv_dma_kernel<2, 2, 2, 2, 2>;
+            case 15: return conv_dma_kernel<2, 2, 2, 4, 2>;
         }
         return nullptr;
     }
@@ -1182,6 +1372,14 @@ namespace vkhip {
     };
 
     static bool is_depthwise(const vkhip_conv_desc *d) { return d->group > 1; }
+
+    // conv_dma_kernel copies B as pixel pairs of one channel slot: the GEMM columns must be dense
+    // NC4HW4 pixels (1x1, stride 1, no padding, or a Winograd V plane) with an even count per image.
+    static bool dma_eligible(const vkhip_conv_desc *d, bool wino) {
+        if (wino) return ((int64_t) d->N * ceil_div(d->OH, 2) * ceil_div(d->OW, 2)) % 2 == 0;
+        return d->KH == 1 && d->KW == 1 && d->SH == 1 && d->SW == 1 && d->PT == 0 && d->PL == 0 && d->OH == d->H && d->OW == d->W &&
+               (d->H * d->W) % 2 == 0;
+    }
 
     static bool wino_eligible(const vkhip_conv_desc *d) {
         return d->group == 1 && d->KH == 3 && d->KW == 3 && d->SH == 1 && d->SW == 1 && d->PT == 1 && d->PL == 1 &&
@@ -1224,7 +1422,7 @@ namespace vkhip {
     static inline int64_t tiled_index(const ConvGeom &g, const TileCfg &t, int64_t oc, int64_t k) {
         const int     BM   = t.BM;
         const int64_t base = ((oc / BM) * g.nsteps + k / kBK) * (int64_t) (BM * kBK);
-        if (t.kind == 0) return base + (oc % BM) * kBK + k % kBK;
+        if (t.kind == 0) return base + (oc % BM) * kBK + k % kBK; // kinds 1 and 2: fragment order
         const int64_t r = oc % BM, kr = k % kBK;
         const int64_t kk = kr / 16, l = ((kr % 16) / 8) * 32 + r % 32;
         return base + ((kk * (BM / 32) + r / 32) * 64 + l) * 8 + kr % 8;
@@ -1292,6 +1490,8 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
     const bool wino = algo == VKHIP_CONV_WINOGRAD;
     if (tile < 0) tile = (algo == VKHIP_CONV_SPLITK) ? (ceil_div(d->Cout, 4) * 4 <= 32 ? 6 : 3) : default_tile(d, wino);
     if (tile >= kNumTiles) return set_error(VKHIP_ERR_INVALID, "tile index %d out of range", tile);
+    if (kTiles[tile].kind == 2 && !dma_eligible(d, wino))
+        return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a dense B operand (1x1 stride 1 with an even pixel count, or Winograd)", tile);
     ConvGeom g = gemm_geom(d, tile, wino);
     plan->algo = algo;
     plan->tile = tile;
@@ -1450,7 +1650,7 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
         a.w_bstride = (long long) g.Coutp * g.Kp;
         a.y_bstride = (long long) g.Coutb * nT;
         dim3 grid((unsigned) (g.m_tiles * g.n_tiles), 1, 16);
-        fn<<<grid, kThreads, 0, st>>>(a);
+        fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
         if ((rc = check_launch("wino_gemm"))) return rc;
         int64_t nout = g.Coutb * nT;
         wino_output_kernel<<<dim3((unsigned) ceil_div(nout, 256)), 256, 0, st>>>(M, a.bias, (uint2 *) y, (int) g.Coutb, d->Cout, d->OH, d->OW,
@@ -1474,7 +1674,7 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
         a.omode = OMODE_PARTIAL;
         a.part  = (float4v *) workspace;
         dim3 grid((unsigned) (g.m_tiles * g.n_tiles), (unsigned) ks, 1);
-        fn<<<grid, kThreads, 0, st>>>(a);
+        fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
         int rc = check_launch("conv_gemm_splitk");
         if (rc) return rc;
         int64_t total = g.Coutb * g.P;
@@ -1485,7 +1685,7 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     }
     a.omode = OMODE_EPILOGUE;
     dim3 grid((unsigned) (g.m_tiles * g.n_tiles), 1, 1);
-    fn<<<grid, kThreads, 0, st>>>(a);
+    fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
     return check_launch("conv_gemm");
 }
 
