@@ -508,48 +508,57 @@ namespace vkhip {
             : __builtin_amdgcn_make_buffer_rsrc((void *) Y, (short) 0, (int) a.y_bytes, 0x00020000);
         const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc((void *) (use_res ? a.res + bz * a.y_bstride : Y), (short) 0,
                                                                              use_res ? (int) a.y_bytes : 0, 0x00020000);
+        // Offsets and residual loads: all fragment columns up front when that is at most 32
+        // registers of loads (the latency is paid once), one column at a time otherwise.
+        constexpr int JG = FM * FN <= 8 ? FN : 1; // fragment columns per group
         auto finish = [&](auto act_c) __attribute__((always_inline)) {
             constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int  px  = nw0 + j * 32 + lrow;
-                const bool pok = px < a.P;
-                const int  pn  = px / a.OHW;
-                const int  pr  = px - pn * a.OHW;
-                unsigned   yoff[FM][4];
-                u32x2      rv[FM][4];
+            for (int j0 = 0; j0 < FN; j0 += JG) {
+                unsigned yoff[JG][FM][4];
+                u32x2    rv[JG][FM][4];
 #pragma unroll
-                for (int i = 0; i < FM; ++i)
+                for (int jj = 0; jj < JG; ++jj) {
+                    const int  px  = nw0 + (j0 + jj) * 32 + lrow;
+                    const bool pok = px < a.P;
+                    const int  pn  = px / a.OHW;
+                    const int  pr  = px - pn * a.OHW;
 #pragma unroll
-                    for (int qq = 0; qq < 4; ++qq) {
-                        const int  ocb = (mw0 + i * 32 + qq * 8 + lk * 4) >> 2;
-                        const bool ok  = pok & (ocb < a.Coutb);
-                        if (a.omode == OMODE_PARTIAL) yoff[i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + px) * 16) : kInvalid;
-                        else yoff[i][qq] = ok ? (unsigned) (((pn * a.Coutb + ocb) * a.OHW + pr) * 8) : kInvalid;
-                        rv[i][qq] = use_res ? __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[i][qq], 0, 0) : u32x2 {0u, 0u};
-                    }
+                    for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int qq = 0; qq < 4; ++qq) {
-                        const int oc = mw0 + i * 32 + qq * 8 + lk * 4;
-                        float4v   v  = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
-                        if (a.omode == OMODE_PARTIAL) {
-                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yrs, yoff[i][qq], 0, 0);
-                            continue;
+                        for (int qq = 0; qq < 4; ++qq) {
+                            const int  ocb = (mw0 + i * 32 + qq * 8 + lk * 4) >> 2;
+                            const bool ok  = pok & (ocb < a.Coutb);
+                            if (a.omode == OMODE_PARTIAL) yoff[jj][i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + px) * 16) : kInvalid;
+                            else yoff[jj][i][qq] = ok ? (unsigned) (((pn * a.Coutb + ocb) * a.OHW + pr) * 8) : kInvalid;
+                            rv[jj][i][qq] = use_res ? __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[jj][i][qq], 0, 0) : u32x2 {0u, 0u};
                         }
-                        if (epi) v += *reinterpret_cast<const float4v *>(a.bias + oc);
-                        v += h4_to_f4(__builtin_bit_cast(half4, rv[i][qq]));
-                        v.x = apply_act(v.x, ACT, a.lo, a.hi);
-                        v.y = apply_act(v.y, ACT, a.lo, a.hi);
-                        v.z = apply_act(v.z, ACT, a.lo, a.hi);
-                        v.w = apply_act(v.w, ACT, a.lo, a.hi);
-                        if (oc + 0 >= a.Cout) v.x = 0.f;
-                        if (oc + 1 >= a.Cout) v.y = 0.f;
-                        if (oc + 2 >= a.Cout) v.z = 0.f;
-                        if (oc + 3 >= a.Cout) v.w = 0.f;
-                        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff[i][qq], 0, 0);
-                    }
+                }
+#pragma unroll
+                for (int jj = 0; jj < JG; ++jj)
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+#pragma unroll
+                        for (int qq = 0; qq < 4; ++qq) {
+                            const int j  = j0 + jj;
+                            const int oc = mw0 + i * 32 + qq * 8 + lk * 4;
+                            float4v   v  = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
+                            if (a.omode == OMODE_PARTIAL) {
+                                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yrs, yoff[jj][i][qq], 0, 0);
+                                continue;
+                            }
+                            if (epi) v += *reinterpret_cast<const float4v *>(a.bias + oc);
+                            v += h4_to_f4(__builtin_bit_cast(half4, rv[jj][i][qq]));
+                            v.x = apply_act(v.x, ACT, a.lo, a.hi);
+                            v.y = apply_act(v.y, ACT, a.lo, a.hi);
+                            v.z = apply_act(v.z, ACT, a.lo, a.hi);
+                            v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                            if (oc + 0 >= a.Cout) v.x = 0.f;
+                            if (oc + 1 >= a.Cout) v.y = 0.f;
+                            if (oc + 2 >= a.Cout) v.z = 0.f;
+                            if (oc + 3 >= a.Cout) v.w = 0.f;
+                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff[jj][i][qq], 0, 0);
+                        }
             }
         };
         switch (epi ? a.act : 0) {
