@@ -120,8 +120,9 @@ def test_conv_auto(gpu, case):
 
 NUM_TILES = V.vkhip().vkhip_conv_tile_count()
 BD_TILES = [8, 9, 10]            # conv_bd_kernel tiles (A via LDS DMA, B gathered into registers)
-DMA_TILES = [11, 12, 13, 14, 15]     # conv_dma_kernel tiles (A and B via LDS DMA; dense B only)
-GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES]
+DMA_TILES = [11, 12, 13, 14, 15, 16, 17, 18]     # conv_dma_kernel tiles (A and B via LDS DMA; dense B only)
+HALO_TILES = [19, 20, 21]         # conv_halo_kernel tiles (3x3 s1 p1: input band staged once for all taps)
+GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES and t not in HALO_TILES]
 
 
 @pytest.mark.parametrize("tile", GATHER_TILES)
@@ -198,6 +199,49 @@ def test_conv_dma_rejects_gather_shapes(gpu):
                            ((1, 8, 7, 7), (8, 8, 1, 1), (1, 1), (0, 0, 0, 0))]:
         d, _ = conv_desc(xs, ws, st, pd)
         assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, 11, 0, ctypes.byref(plan)) != 0
+
+
+@pytest.mark.parametrize("tile", HALO_TILES)
+@pytest.mark.parametrize("shape", [(2, 64, 14, 14, 72), (1, 32, 8, 10, 40), (3, 128, 6, 6, 128), (1, 64, 56, 56, 64),
+                                   (2, 96, 28, 28, 100)])
+def test_conv_halo_3x3(gpu, tile, shape):
+    """Band-staged 3x3 kernel: pixel tiles crossing one or several image boundaries (zero rows
+    between images), the end of the batch, ragged output channels, residual + ReLU epilogue."""
+    N, C, H, W, Cout = shape
+    r = rng(120 + tile + C + H)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    res = round_half(r.standard_normal((N, Cout, H, W)))
+    got, plan, _ = gpu_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1, res=res, algo=V.CONV_GEMM, tile=tile)
+    assert plan.tile == tile
+    ref = oracle_conv(x, w, b, (1, 1), (1, 1, 1, 1), res=res, act=1)
+    assert_parity(got, ref, f"halo tile {tile} {shape}")
+
+
+@pytest.mark.parametrize("tile", [19, 20])
+def test_conv_halo_splitk(gpu, tile):
+    r = rng(130 + tile)
+    x = round_half(r.standard_normal((2, 256, 14, 14)))
+    w = (r.standard_normal((128, 256, 3, 3)) * 0.03).astype(np.float32)
+    b = (r.standard_normal(128) * 0.1).astype(np.float32)
+    got, plan, _ = gpu_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1, algo=V.CONV_SPLITK, tile=tile, ksplit=4)
+    assert plan.ksplit == 4 and plan.tile == tile
+    assert_parity(got, oracle_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1), f"halo split-K tile {tile}")
+
+
+def test_conv_halo_rejects_other_shapes(gpu):
+    """The halo tiles refuse stride 2, odd width, 1x1, Cin not a multiple of 16 and Winograd."""
+    lib = V.vkhip()
+    plan = V.ConvPlan()
+    for xs, ws, st, pd in [((1, 16, 8, 8), (8, 16, 3, 3), (2, 2), (1, 1, 1, 1)), ((1, 16, 7, 7), (8, 16, 3, 3), (1, 1), (1, 1, 1, 1)),
+                           ((1, 16, 8, 8), (8, 16, 1, 1), (1, 1), (0, 0, 0, 0)), ((1, 24, 8, 8), (8, 24, 3, 3), (1, 1), (1, 1, 1, 1))]:
+        d, _ = conv_desc(xs, ws, st, pd)
+        for t in HALO_TILES:
+            assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, t, 0, ctypes.byref(plan)) != 0
+    d, _ = conv_desc((1, 16, 8, 8), (8, 16, 3, 3), (1, 1), (1, 1, 1, 1))
+    assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_WINOGRAD, 19, 0, ctypes.byref(plan)) != 0
+    assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, 19, 0, ctypes.byref(plan)) == 0
 
 
 @pytest.mark.parametrize("tile", [8, 10])

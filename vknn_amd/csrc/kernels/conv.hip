@@ -929,9 +929,19 @@ namespace vkhip {
         // NS LDS stages, prefetch distance NS-1: stage ks waits for its own copies (the NS-2 later
         // stages may stay in flight), barriers (all waves' copies landed; all waves done with
         // stage ks-1, whose buffer the next issue refills), issues stage ks+NS-1, computes.
-        constexpr int kAhead = (NS - 2) * (NA + NB) < 63 ? (NS - 2) * (NA + NB) : 63;
+        constexpr int kAhead = NS < 2 ? 0 : ((NS - 2) * (NA + NB) < 63 ? (NS - 2) * (NA + NB) : 63);
         constexpr int kWait  = (kAhead & 15) | (7 << 4) | (15 << 8) | ((kAhead >> 4) << 14);
-        if (ks_begin < ks_end) {
+        if constexpr (NS == 1) {
+            // one stage (GEMMs with a single K stage per split): copy, wait, compute; no LDS ring,
+            // so several workgroups fit on a CU and overlap each other's copies and epilogues
+            for (int ks = ks_begin; ks < ks_end; ++ks) {
+                if (ks > ks_begin) __asm__ volatile("s_barrier" ::: "memory");
+                issue(ks, 0);
+                __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+                __asm__ volatile("s_barrier" ::: "memory");
+                compute(0, -1, 0);
+            }
+        } else if (ks_begin < ks_end) {
 #pragma unroll
             for (int d = 0; d < NS - 1; ++d)
                 if (ks_begin + d < ks_end) issue(ks_begin + d, d);
@@ -944,6 +954,196 @@ namespace vkhip {
             }
         }
         gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, bz, lane);
+    }
+
+    // ------------------------------------------------------------------ 3x3 halo-tile GEMM kernel
+    // Direct 3x3 stride-1 pad-1 convolution (Cin a multiple of 16*KK, even W) that reads each input
+    // pixel once per workgroup instead of once per tap: the workgroup's BN consecutive output
+    // pixels (row-major over n, oy, ox, free to cross image boundaries) need a band of input rows;
+    // per channel slot the band is copied global->LDS by buffer-load-to-LDS, 16 bytes (a pixel pair)
+    // per lane, into rows of W + 2 pixels: W data pixels then two zero pixels, so the left
+    // neighbour of column 0 is the previous row's last zero pixel (for the first band row: the
+    // previous slot's zero tail, or a zero guard before slot 0) and the right neighbour of
+    // column W-1 is the first one. Each image contributes H + 2 band rows (its zero rows above and
+    // below), so the band row of (n, iy) is (n - n_first)(H + 2) + iy + 1 - oy_first. Rows outside
+    // the image, pad pairs and lanes past the band get an out-of-range offset and write zeros.
+    // The 9 taps of a 16-channel K step then read their B fragments from the same band at a
+    // shift of (ky - 1)(W + 2) + (kx - 1) pixels. A (weights) arrives by LDS DMA too, prepacked as
+    // [m_tile][stage][tap][kk][m_frag][lane][8 halves].
+    //   FM x FN fragments per wave, WM x WN waves; KK 16-channel K steps per LDS stage; NS stages
+    //   in the ring; NBI 1 KB DMA chunks per channel slot of the band (rows * (W + 2) / 2 lanes).
+    template <int FM, int FN, int WM, int WN, int KK, int NS, int NBI>
+    __global__ __launch_bounds__(64 * WM * WN, 1) void conv_halo_kernel(GemmArgs a) {
+        constexpr int NW     = WM * WN;
+        constexpr int BM     = 32 * FM * WM;
+        constexpr int BN     = 32 * FN * WN;
+        constexpr int MF     = BM / 32;
+        constexpr int SLOTS  = 4 * KK;                 // channel slots per stage
+        constexpr int SS     = NBI * 1024;             // LDS bytes per slot of the band
+        constexpr int ASTAGE = 9 * KK * MF * 1024;     // A bytes per stage
+        constexpr int BOFF   = ASTAGE + 32;            // band start (32 zero guard bytes before it)
+        constexpr int STAGE  = BOFF + SLOTS * SS;
+        constexpr int NA     = ASTAGE / 1024;          // 1 KB A chunks per stage
+        constexpr int NB     = SLOTS * NBI;            // 1 KB band chunks per stage
+        // every wave issues the same number of copies per stage (the vmcnt waits count them): A
+        // chunks are rounded up to a multiple of the wave count, the surplus ones copy zeros into
+        // a spare 1 KB after the ring
+        constexpr int NAW = (NA + NW - 1) / NW;
+        constexpr int SPARE = NA % NW ? 1024 : 0;
+        static_assert(NS * STAGE + SPARE <= 160 * 1024, "LDS budget");
+        static_assert(NB % NW == 0, "band copies per wave");
+        __shared__ __attribute__((aligned(16))) unsigned char sm[NS * STAGE + SPARE];
+
+        const int tid  = threadIdx.x;
+        const int lane = tid & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int wmi  = wave / WN;
+        const int wni  = wave % WN;
+
+        const int lin    = xcd_remap(blockIdx.x, gridDim.x);
+        const int m_tile = lin % a.m_tiles;
+        const int n_tile = lin / a.m_tiles;
+        const int m0     = m_tile * BM;
+        const int n0     = n_tile * BN;
+        const int split  = blockIdx.y;
+        const int wm0    = wmi * 32 * FM;
+        const int wn0    = wni * 32 * FN;
+
+        const int W   = a.W, H = a.H, HW = a.HW;
+        const int PW  = (W + 2) >> 1; // pixel pairs per band row
+        const int nf  = n0 / HW;
+        const int oyf = (n0 - nf * HW) / W;
+        const int NI  = a.P / HW;
+        // band rows of this workgroup: up to the row below its last pixel's row; lanes past them
+        // copy zeros, so the last 8 bytes of every slot are zero (the left neighbour of the next
+        // slot's first pixel)
+        const int pl    = min(a.P, n0 + BN) - 1;
+        const int nl    = pl / HW;
+        const int nrows = (nl - nf) * (H + 2) + (pl - nl * HW) / W + 1 - oyf + 2;
+
+        const unsigned char *Wt = reinterpret_cast<const unsigned char *>(a.w) + (long long) m_tile * a.nsteps * ASTAGE;
+        const int ks_begin = split * a.steps_per_split;
+        const int ks_end   = min(a.nsteps, ks_begin + a.steps_per_split);
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) a.x_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *) Wt, (short) 0, ks_end * ASTAGE, 0x00020000);
+        constexpr unsigned kInvalid = 0x80000000u;
+
+        // zero guards in front of every stage's band (never written by the copies)
+        if (tid < NS * 2) *reinterpret_cast<u32x4 *>(&sm[(tid >> 1) * STAGE + ASTAGE + (tid & 1) * 16]) = u32x4 {0u, 0u, 0u, 0u};
+
+        // Band copy chunks: chunk c = r*NW + wave of the stage covers slot c / NBI, lanes
+        // (c % NBI)*64 + lane of that slot's band; the per-lane source offsets repeat for every slot.
+        constexpr int NBW = NB / NW; // band chunks per wave per stage
+        unsigned bsrc[NBI];
+#pragma unroll
+        for (int i = 0; i < NBI; ++i) {
+            const int k    = i * 64 + lane;
+            const int vrow = k / PW;
+            const int pc   = k - vrow * PW;
+            const int vabs = vrow + oyf;
+            const int n    = nf + vabs / (H + 2);
+            const int iy   = vabs % (H + 2) - 1;
+            const bool ok  = 2 * pc < W && iy >= 0 && iy < H && n < NI && vrow < nrows;
+            bsrc[i]        = ok ? (unsigned) (((n * a.Cinb) * HW + iy * W + 2 * pc) * 8) : kInvalid;
+        }
+        const unsigned hw8 = (unsigned) HW * 8u;
+        auto issue = [&](int ks, int buf) __attribute__((always_inline)) {
+            unsigned char *dst = sm + buf * STAGE;
+#pragma unroll
+            for (int r = 0; r < NAW; ++r) {
+                const int  c    = r * NW + wave;
+                const bool real = NA % NW == 0 || c < NA;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (__attribute__((address_space(3))) void *) (real ? dst + c * 1024 : sm + NS * STAGE), 16,
+                                                         real ? (unsigned) (c * 1024 + lane * 16) + (unsigned) (ks * ASTAGE) : kInvalid, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < NBW; ++r) {
+                const int c  = r * NW + wave;
+                const int sl = c / NBI;
+                const unsigned vo = bsrc[c % NBI]; // (a local: the host pass rejects the array element as a builtin operand)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void *) (dst + BOFF + sl * SS + (c % NBI) * 1024),
+                                                         16, vo, (unsigned) (ks * SLOTS + sl) * hw8, 0, 0);
+            }
+        };
+
+        // B fragment pixel of each fragment column: LDS pixel index of the centre tap.
+        const int g = lane >> 5;
+        int       qb[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int p = n0 + wn0 + 32 * j + (lane & 31);
+            int       q = W + 3; // any interior position: columns past P read the band harmlessly
+            if (p < a.P) {
+                const int n  = p / HW;
+                const int r  = p - n * HW;
+                const int oy = r / W;
+                q            = ((n - nf) * (H + 2) + oy + 1 - oyf) * (W + 2) + (r - oy * W);
+            }
+            qb[j] = BOFF + (2 * g) * SS + q * 8;
+        }
+        int tapoff[9];
+#pragma unroll
+        for (int t = 0; t < 9; ++t) tapoff[t] = ((t / 3 - 1) * (W + 2) + (t % 3 - 1)) * 8;
+
+        float16v acc[FM][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+        auto compute = [&](int buf, int next_ks, int next_buf) __attribute__((always_inline)) {
+            const unsigned char *S  = sm + buf * STAGE;
+            const unsigned char *Ab = S + ((wmi * FM) * 64 + lane) * 16;
+            half8 fa[2][FM], fb[2][FN];
+            // step s = kk * 9 + tap
+            auto rd = [&](int s, int d) __attribute__((always_inline)) {
+                const int kk = s / 9, t = s % 9;
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const unsigned char *bp = S + qb[j] + tapoff[t] + kk * 4 * SS;
+                    const u32x2 lo = *reinterpret_cast<const u32x2 *>(bp);
+                    const u32x2 hi = *reinterpret_cast<const u32x2 *>(bp + SS);
+                    fb[d][j] = __builtin_bit_cast(half8, u32x4_make(lo.x, lo.y, hi.x, hi.y));
+                }
+#pragma unroll
+                for (int i = 0; i < FM; ++i) fa[d][i] = *reinterpret_cast<const half8 *>(Ab + ((t * KK + kk) * MF + i) * 1024);
+            };
+            rd(0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < 9 * KK; ++s) {
+                if (s == 0 && next_ks >= 0) issue(next_ks, next_buf);
+                if (s + 1 < 9 * KK) rd(s + 1, (s + 1) & 1);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[s & 1][i], fb[s & 1][j], acc[i][j], 0, 0, 0);
+                if (s == 0) StepSchedule<0, FM * FN, FM + 2 * FN, 4 * FN, NAW + NBW>::apply();
+                else if (s + 1 < 9 * KK) StepSchedule<0, FM * FN, FM + 2 * FN, 4 * FN>::apply();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+
+        constexpr int NPW    = NAW + NBW; // copies per wave per stage
+        constexpr int kAhead = NS < 2 ? 0 : ((NS - 2) * NPW < 63 ? (NS - 2) * NPW : 63);
+        constexpr int kWait  = (kAhead & 15) | (7 << 4) | (15 << 8) | ((kAhead >> 4) << 14);
+        __syncthreads(); // guards written
+        if (ks_begin < ks_end) {
+#pragma unroll
+            for (int d = 0; d < NS - 1; ++d)
+                if (ks_begin + d < ks_end) issue(ks_begin + d, d);
+            for (int ks = ks_begin; ks < ks_end; ++ks) {
+                const int rel = ks - ks_begin;
+                if (ks + NS - 2 < ks_end) __builtin_amdgcn_s_waitcnt(kWait);
+                else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+                __asm__ volatile("s_barrier" ::: "memory");
+                compute(rel % NS, ks + NS - 1 < ks_end ? ks + NS - 1 : -1, (rel + NS - 1) % NS);
+            }
+        }
+        gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, 0, lane);
     }
 
     // Split-K reduce: y = act(sum_s part[s] + bias (+res)).
@@ -1308,8 +1508,10 @@ namespace vkhip {
     // kind 1: conv_bd_kernel (A via LDS DMA, B straight into registers), waves of (32FM) x (32FN).
     // kind 2: conv_dma_kernel (A and B via LDS DMA; dense B only: 1x1 s1 with an even pixel count
     //         per image, Winograd GEMMs with an even tile count), 2x2 waves of (32FM) x (32FN).
+    // kind 3: conv_halo_kernel (3x3 stride-1 pad-1 only: input band staged once in LDS for all 9
+    //         taps), KK 16-channel K steps per LDS stage.
     struct TileCfg {
-        int BM, BN, WM, WN, kind, FM, FN;
+        int BM, BN, WM, WN, kind, FM, FN, KK;
     };
     static const TileCfg kTiles[] = {
         {128, 128, 2, 2, 0, 0, 0}, // 0
@@ -1328,8 +1530,15 @@ namespace vkhip {
         {256, 256, 4, 2, 2, 2, 4}, // 13 (8 waves)
         {128, 128, 2, 2, 2, 2, 2}, // 14
         {256, 128, 4, 2, 2, 2, 2}, // 15 (8 waves)
+        {128, 128, 2, 2, 2, 2, 2}, // 16 (4-stage LDS ring)
+        {256, 128, 4, 2, 2, 2, 2}, // 17 (8 waves, 3-stage ring)
+        {128, 256, 2, 2, 2, 2, 4}, // 18 (3-stage ring)
+        {128, 128, 2, 2, 3, 2, 2, 1}, // 19 (3-stage ring)
+        {64, 256, 1, 4, 3, 2, 2, 1},  // 20 (2-stage ring, two workgroups per CU)
+        {128, 256, 2, 2, 3, 2, 4, 1}, // 21 (2-stage ring)
     };
-    constexpr int kNumTiles = 16;
+    constexpr int kNumTiles = 22;
+    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 5, 10};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
@@ -1353,7 +1562,25 @@ namespace vkhip {
         }
     }
 
-    static GemmKernelFn gemm_kernel_for(int tile, int bmode) {
+    // conv_dma_kernel with its LDS ring cut to the number of K stages one split runs (fewer stages
+    // need no deeper ring; the smaller LDS footprint lets more workgroups share a CU).
+    template <int FM, int FN, int NS, int WM, int WN>
+    static GemmKernelFn pick_dma(int steps) {
+        if constexpr (NS > 1) {
+            if (steps < NS) return pick_dma<FM, FN, NS - 1, WM, WN>(steps);
+        }
+        return conv_dma_kernel<FM, FN, NS, WM, WN>;
+    }
+
+    // the smallest band-size instantiation (NBIS ascending) that holds nbi chunks per slot
+    template <int FM, int FN, int WM, int WN, int KK, int NS, int NBI0, int... NBIS>
+    static GemmKernelFn pick_halo(int nbi) {
+        if (nbi <= NBI0) return conv_halo_kernel<FM, FN, WM, WN, KK, NS, NBI0>;
+        if constexpr (sizeof...(NBIS) > 0) return pick_halo<FM, FN, WM, WN, KK, NS, NBIS...>(nbi);
+        return nullptr;
+    }
+
+    static GemmKernelFn gemm_kernel_for(int tile, int bmode, int steps, int nbi = 0) {
         switch (tile) {
             case 0: return pick_bmode<128, 128, 2, 2>(bmode);
             case 1: return pick_bmode<64, 128, 2, 2>(bmode);
@@ -1366,11 +1593,17 @@ namespace vkhip {
             case 8: return pick_bd<4, 2, 1, 4, 1>(bmode);
             case 9: return pick_bd<2, 2, 2, 2, 1>(bmode);
             case 10: return pick_bd<2, 2, 1, 4, 1>(bmode);
-            case 11: return conv_dma_kernel<4, 4, 2, 2, 2>;
-            case 12: return conv_dma_kernel<4, 2, 2, 2, 4>;
-            case 13: return conv_dma_kernel<2, 4, 2, 4, 2>;
-            case 14: return conv_dma_kernel<2, 2, 2, 2, 2>;
-            case 15: return conv_dma_kernel<2, 2, 2, 4, 2>;
+            case 11: return pick_dma<4, 4, 2, 2, 2>(steps);
+            case 12: return pick_dma<4, 2, 2, 2, 4>(steps);
+            case 13: return pick_dma<2, 4, 2, 4, 2>(steps);
+            case 14: return pick_dma<2, 2, 2, 2, 2>(steps);
+            case 15: return pick_dma<2, 2, 2, 4, 2>(steps);
+            case 16: return pick_dma<2, 2, 4, 2, 2>(steps);
+            case 17: return pick_dma<2, 2, 3, 4, 2>(steps);
+            case 18: return pick_dma<2, 4, 3, 2, 2>(steps);
+            case 19: return pick_halo<2, 2, 2, 2, 1, 3, 1, 2, 3, 4>(nbi);
+            case 20: return pick_halo<2, 2, 1, 4, 1, 2, 1, 2, 3, 4, 5>(nbi);
+            case 21: return pick_halo<2, 4, 2, 2, 1, 2, 2, 3, 4, 5, 6, 8, 10>(nbi);
         }
         return nullptr;
     }
@@ -1388,6 +1621,31 @@ namespace vkhip {
         if (wino) return ((int64_t) d->N * ceil_div(d->OH, 2) * ceil_div(d->OW, 2)) % 2 == 0;
         return d->KH == 1 && d->KW == 1 && d->SH == 1 && d->SW == 1 && d->PT == 0 && d->PL == 0 && d->OH == d->H && d->OW == d->W &&
                (d->H * d->W) % 2 == 0;
+    }
+
+    // conv_halo_kernel: 3x3, stride 1, pad 1, dilation 1, same-size output, even W (pixel pairs),
+    // Cin a multiple of the stage's 16*KK channels.
+    static bool halo_shape_ok(const vkhip_conv_desc *d, const TileCfg &t) {
+        return d->group == 1 && d->KH == 3 && d->KW == 3 && d->SH == 1 && d->SW == 1 && d->PT == 1 && d->PL == 1 && d->DH == 1 &&
+               d->DW == 1 && d->OH == d->H && d->OW == d->W && d->W % 2 == 0 && d->Cin % (16 * t.KK) == 0;
+    }
+
+    // 1 KB copy chunks per channel slot of the largest input band any workgroup of a halo tile
+    // needs: band rows run from the row above the first output pixel's row to the row below the
+    // last one's, with two extra (zero) rows per image boundary crossed; W/2 + 1 pixel pairs a row.
+    static int halo_nbi(const vkhip_conv_desc *d, const TileCfg &t) {
+        const int64_t HW = (int64_t) d->H * d->W, P = (int64_t) d->N * HW, PW = d->W / 2 + 1;
+        int64_t       rows = 0;
+        for (int64_t p0 = 0; p0 < P; p0 += t.BN) {
+            const int64_t p1 = std::min(P, p0 + t.BN) - 1;
+            const int64_t nf = p0 / HW, oyf = (p0 % HW) / d->W;
+            const int64_t nl = p1 / HW, oyl = (p1 % HW) / d->W;
+            rows = std::max(rows, (nl - nf) * (d->H + 2) + oyl + 1 - oyf + 2);
+        }
+        int nbi = (int) ceil_div(rows * PW, 64);
+        const int nw = t.WM * t.WN;
+        while ((4 * t.KK * nbi) % nw) ++nbi;
+        return nbi;
     }
 
     static bool wino_eligible(const vkhip_conv_desc *d) {
@@ -1418,6 +1676,10 @@ namespace vkhip {
         }
         g.Kp      = round_up(g.Kslots * 4, kBK);
         g.nsteps  = g.Kp / kBK;
+        if (t.kind == 3) { // 9 taps x Cin, stages of 16*KK channels (all 9 taps each)
+            g.Kp     = 9 * (int64_t) d->Cin;
+            g.nsteps = d->Cin / (16 * t.KK);
+        }
         g.m_tiles = ceil_div(g.Coutb * 4, t.BM);
         g.Coutp   = g.m_tiles * t.BM;
         g.n_tiles = ceil_div(g.P, t.BN);
@@ -1432,6 +1694,14 @@ namespace vkhip {
         const int     BM   = t.BM;
         const int64_t base = ((oc / BM) * g.nsteps + k / kBK) * (int64_t) (BM * kBK);
         if (t.kind == 0) return base + (oc % BM) * kBK + k % kBK; // kinds 1 and 2: fragment order
+        if (t.kind == 3) {
+            // [m_tile][stage][tap][kk][m_frag][lane][8 halves]; k = (tap*Cinb + cb)*4 + c%4
+            const int64_t tap = (k / 4) / g.Cinb, c = ((k / 4) % g.Cinb) * 4 + k % 4;
+            const int64_t SK = 16 * t.KK, stage = c / SK, kk = (c % SK) / 16, kr = c % 16, r = oc % BM;
+            const int64_t l = (kr / 8) * 32 + r % 32;
+            const int64_t hb = ((oc / BM) * g.nsteps + stage) * (int64_t) (9 * SK * BM);
+            return hb + (((tap * t.KK + kk) * (BM / 32) + r / 32) * 64 + l) * 8 + kr % 8;
+        }
         const int64_t r = oc % BM, kr = k % kBK;
         const int64_t kk = kr / 16, l = ((kr % 16) / 8) * 32 + r % 32;
         return base + ((kk * (BM / 32) + r / 32) * 64 + l) * 8 + kr % 8;
@@ -1499,6 +1769,9 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
     const bool wino = algo == VKHIP_CONV_WINOGRAD;
     if (tile < 0) tile = (algo == VKHIP_CONV_SPLITK) ? (ceil_div(d->Cout, 4) * 4 <= 32 ? 6 : 3) : default_tile(d, wino);
     if (tile >= kNumTiles) return set_error(VKHIP_ERR_INVALID, "tile index %d out of range", tile);
+    if (kTiles[tile].kind == 3 && (wino || !halo_shape_ok(d, kTiles[tile]) || halo_nbi(d, kTiles[tile]) > kHaloMaxNBI[tile]))
+        return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a 3x3 stride-1 pad-1 conv with even W, Cin %% %d == 0 and a band that fits LDS", tile,
+                         16 * kTiles[tile].KK);
     if (kTiles[tile].kind == 2 && !dma_eligible(d, wino))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a dense B operand (1x1 stride 1 with an even pixel count, or Winograd)", tile);
     ConvGeom g = gemm_geom(d, tile, wino);
@@ -1636,7 +1909,9 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     a.lo     = d->act_lo;
     a.hi     = d->act_hi;
     a.m_tiles = (int) g.m_tiles;
-    GemmKernelFn fn = gemm_kernel_for(plan->tile, g.bmode);
+    const int split_steps = plan->algo == VKHIP_CONV_SPLITK ? (int) ceil_div(g.nsteps, plan->ksplit) : (int) g.nsteps;
+    GemmKernelFn fn = gemm_kernel_for(plan->tile, g.bmode, split_steps, t.kind == 3 ? halo_nbi(d, t) : 0);
+    if (!fn) return set_error(VKHIP_ERR_INVALID, "conv_forward: no kernel for tile %d", plan->tile);
 
     if (wino) {
         const int nTH = (int) ceil_div(d->OH, 2), nTW = (int) ceil_div(d->OW, 2);
