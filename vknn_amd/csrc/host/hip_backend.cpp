@@ -165,7 +165,7 @@ namespace vknn {
                 // with the big tiles) and the reduction is deep enough to split.
                 const int64_t kdepth = (int64_t) d.KH * d.KW * ((d.Cin + 3) / 4) * 4;
                 if (pixels <= 4096 || base.algo == VKHIP_CONV_SPLITK || (pixels * (int64_t) d.Cout <= (int64_t) 512 * 128 * 256 && kdepth >= 512)) {
-                    for (int t: {3, 6, 1, 8, 10, 14, 16, 19, 20})
+                    for (int t: {3, 6, 1, 8, 10, 14, 16, 17, 18, 20})
                         for (int ks: {2, 3, 4, 8, 16}) cands.push_back({VKHIP_CONV_SPLITK, t, ks});
                 }
                 if (tuning != (int) Mode::Thorough) {
@@ -198,7 +198,7 @@ namespace vknn {
                     // the position GEMMs on the heuristic tile and on the register-/DMA-fed tiles
                     double bestWino = 1e30;
                     std::array<int32_t, 3> wpick {};
-                    for (int t: {-1, 8, 10, 14, 12, 16, 17}) {
+                    for (int t: {-1, 8, 10, 14, 12, 16}) {
                         vkhip_conv_plan p;
                         if (vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, t, 0, &p)) continue;
                         double ms = timePlan(p, w, b, x->ptr, yb->ptr);

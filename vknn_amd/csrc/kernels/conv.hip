@@ -501,22 +501,32 @@ namespace vkhip {
         const int  lrow = lane & 31;
         const int  lk   = lane >> 5;
         uint2     *Y    = a.y + bz * a.y_bstride;
-        const bool epi  = a.omode == OMODE_EPILOGUE;
-        const bool use_res = epi && a.has_res;
-        const __amdgpu_buffer_rsrc_t yrs = a.omode == OMODE_PARTIAL
-            ? __builtin_amdgcn_make_buffer_rsrc((void *) a.part, (short) 0, 0x7FFFFFFF, 0x00020000)
-            : __builtin_amdgcn_make_buffer_rsrc((void *) Y, (short) 0, (int) a.y_bytes, 0x00020000);
-        const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc((void *) (use_res ? a.res + bz * a.y_bstride : Y), (short) 0,
-                                                                             use_res ? (int) a.y_bytes : 0, 0x00020000);
         // Offsets and residual loads: all fragment columns up front when that is at most 32
-        // registers of loads (the latency is paid once), one column at a time otherwise.
+        // registers of loads (the latency is paid once), one column at a time otherwise, the
+        // next column's loads issued before this column's stores. Every load of the epilogue
+        // goes out before the stores it could queue behind: the vector memory counter retires in
+        // order, so waiting for a load issued after a store also waits for that store.
+        // MODE (compile time, so the element loop has no branches): 0 split-K partials (fp32, raw),
+        // 1 raw fp16 (Winograd M), 2 bias + act, 3 bias + residual + act.
         constexpr int JG = FM * FN <= 8 ? FN : 1; // fragment columns per group
-        auto finish = [&](auto act_c) __attribute__((always_inline)) {
-            constexpr int ACT = decltype(act_c)::value;
+        constexpr int NG = FN / JG;
+        auto finish = [&](auto mode_c, auto act_c) __attribute__((always_inline)) {
+            constexpr int MODE = decltype(mode_c)::value;
+            constexpr int ACT  = decltype(act_c)::value;
+            const __amdgpu_buffer_rsrc_t yrs = MODE == 0 ? __builtin_amdgcn_make_buffer_rsrc((void *) a.part, (short) 0, 0x7FFFFFFF, 0x00020000)
+                                                         : __builtin_amdgcn_make_buffer_rsrc((void *) Y, (short) 0, (int) a.y_bytes, 0x00020000);
+            const __amdgpu_buffer_rsrc_t rrs =
+                __builtin_amdgcn_make_buffer_rsrc((void *) (MODE == 3 ? a.res + bz * a.y_bstride : Y), (short) 0, (int) a.y_bytes, 0x00020000);
+            float4v bv[FM][4];
+            if constexpr (MODE >= 2) {
 #pragma unroll
-            for (int j0 = 0; j0 < FN; j0 += JG) {
-                unsigned yoff[JG][FM][4];
-                u32x2    rv[JG][FM][4];
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) bv[i][qq] = *reinterpret_cast<const float4v *>(a.bias + mw0 + i * 32 + qq * 8 + lk * 4);
+            }
+            unsigned yoff[NG > 1 ? 2 : 1][JG][FM][4];
+            u32x2    rv[NG > 1 ? 2 : 1][JG][FM][4];
+            auto prep = [&](int j0, int b) __attribute__((always_inline)) {
 #pragma unroll
                 for (int jj = 0; jj < JG; ++jj) {
                     const int  px  = nw0 + (j0 + jj) * 32 + lrow;
@@ -529,11 +539,17 @@ namespace vkhip {
                         for (int qq = 0; qq < 4; ++qq) {
                             const int  ocb = (mw0 + i * 32 + qq * 8 + lk * 4) >> 2;
                             const bool ok  = pok & (ocb < a.Coutb);
-                            if (a.omode == OMODE_PARTIAL) yoff[jj][i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + px) * 16) : kInvalid;
-                            else yoff[jj][i][qq] = ok ? (unsigned) (((pn * a.Coutb + ocb) * a.OHW + pr) * 8) : kInvalid;
-                            rv[jj][i][qq] = use_res ? __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[jj][i][qq], 0, 0) : u32x2 {0u, 0u};
+                            if constexpr (MODE == 0) yoff[b][jj][i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + px) * 16) : kInvalid;
+                            else yoff[b][jj][i][qq] = ok ? (unsigned) (((pn * a.Coutb + ocb) * a.OHW + pr) * 8) : kInvalid;
+                            if constexpr (MODE == 3) rv[b][jj][i][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[b][jj][i][qq], 0, 0);
                         }
                 }
+            };
+            prep(0, 0);
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                const int j0 = g * JG, b = g & 1;
+                if (g + 1 < NG) prep(j0 + JG, b ^ 1);
 #pragma unroll
                 for (int jj = 0; jj < JG; ++jj)
 #pragma unroll
@@ -543,12 +559,12 @@ namespace vkhip {
                             const int j  = j0 + jj;
                             const int oc = mw0 + i * 32 + qq * 8 + lk * 4;
                             float4v   v  = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
-                            if (a.omode == OMODE_PARTIAL) {
-                                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yrs, yoff[jj][i][qq], 0, 0);
+                            if constexpr (MODE == 0) {
+                                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yrs, yoff[b][jj][i][qq], 0, 0);
                                 continue;
                             }
-                            if (epi) v += *reinterpret_cast<const float4v *>(a.bias + oc);
-                            v += h4_to_f4(__builtin_bit_cast(half4, rv[jj][i][qq]));
+                            if constexpr (MODE >= 2) v += bv[i][qq];
+                            if constexpr (MODE == 3) v += h4_to_f4(__builtin_bit_cast(half4, rv[b][jj][i][qq]));
                             v.x = apply_act(v.x, ACT, a.lo, a.hi);
                             v.y = apply_act(v.y, ACT, a.lo, a.hi);
                             v.z = apply_act(v.z, ACT, a.lo, a.hi);
@@ -557,18 +573,25 @@ namespace vkhip {
                             if (oc + 1 >= a.Cout) v.y = 0.f;
                             if (oc + 2 >= a.Cout) v.z = 0.f;
                             if (oc + 3 >= a.Cout) v.w = 0.f;
-                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff[jj][i][qq], 0, 0);
+                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff[b][jj][i][qq], 0, 0);
                         }
             }
         };
-        switch (epi ? a.act : 0) {
-            case VKHIP_ACT_RELU: finish(std::integral_constant<int, VKHIP_ACT_RELU> {}); break;
-            case VKHIP_ACT_RELU6: finish(std::integral_constant<int, VKHIP_ACT_RELU6> {}); break;
-            case VKHIP_ACT_CLIP: finish(std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
-            case VKHIP_ACT_HARDSWISH: finish(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
-            case VKHIP_ACT_SILU: finish(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
-            default: finish(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
-        }
+        using I = std::integral_constant<int, 0>;
+        if (a.omode == OMODE_PARTIAL) return finish(I {}, I {});
+        if (a.omode == OMODE_RAW) return finish(std::integral_constant<int, 1> {}, I {});
+        auto with_act = [&](auto mode_c) __attribute__((always_inline)) {
+            switch (a.act) {
+                case VKHIP_ACT_RELU: finish(mode_c, std::integral_constant<int, VKHIP_ACT_RELU> {}); break;
+                case VKHIP_ACT_RELU6: finish(mode_c, std::integral_constant<int, VKHIP_ACT_RELU6> {}); break;
+                case VKHIP_ACT_CLIP: finish(mode_c, std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
+                case VKHIP_ACT_HARDSWISH: finish(mode_c, std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
+                case VKHIP_ACT_SILU: finish(mode_c, std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
+                default: finish(mode_c, std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
+            }
+        };
+        if (a.has_res) with_act(std::integral_constant<int, 3> {});
+        else with_act(std::integral_constant<int, 2> {});
     }
 
     template <int I, int N, typename F>
@@ -1131,7 +1154,16 @@ namespace vkhip {
         constexpr int kAhead = NS < 2 ? 0 : ((NS - 2) * NPW < 63 ? (NS - 2) * NPW : 63);
         constexpr int kWait  = (kAhead & 15) | (7 << 4) | (15 << 8) | ((kAhead >> 4) << 14);
         __syncthreads(); // guards written
-        if (ks_begin < ks_end) {
+        if constexpr (NS == 1) {
+            // one LDS stage: copy, wait, compute (the workgroups sharing a CU overlap each other)
+            for (int ks = ks_begin; ks < ks_end; ++ks) {
+                if (ks > ks_begin) __asm__ volatile("s_barrier" ::: "memory");
+                issue(ks, 0);
+                __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+                __asm__ volatile("s_barrier" ::: "memory");
+                compute(0, -1, 0);
+            }
+        } else if (ks_begin < ks_end) {
 #pragma unroll
             for (int d = 0; d < NS - 1; ++d)
                 if (ks_begin + d < ks_end) issue(ks_begin + d, d);
@@ -1530,15 +1562,14 @@ namespace vkhip {
         {256, 256, 4, 2, 2, 2, 4}, // 13 (8 waves)
         {128, 128, 2, 2, 2, 2, 2}, // 14
         {256, 128, 4, 2, 2, 2, 2}, // 15 (8 waves)
-        {128, 128, 2, 2, 2, 2, 2}, // 16 (4-stage LDS ring)
-        {256, 128, 4, 2, 2, 2, 2}, // 17 (8 waves, 3-stage ring)
-        {128, 256, 2, 2, 2, 2, 4}, // 18 (3-stage ring)
-        {128, 128, 2, 2, 3, 2, 2, 1}, // 19 (3-stage ring)
-        {64, 256, 1, 4, 3, 2, 2, 1},  // 20 (2-stage ring, two workgroups per CU)
-        {128, 256, 2, 2, 3, 2, 4, 1}, // 21 (2-stage ring)
+        {128, 128, 2, 2, 2, 2, 2},    // 16 (4-stage LDS ring)
+        {128, 128, 2, 2, 3, 2, 2, 1}, // 17 (3-stage ring)
+        {64, 256, 1, 4, 3, 2, 2, 1},  // 18 (2-stage ring, two workgroups per CU)
+        {128, 256, 2, 2, 3, 2, 4, 1}, // 19 (2-stage ring)
+        {64, 128, 1, 4, 3, 2, 1, 1},  // 20 (one stage, several workgroups per CU)
     };
-    constexpr int kNumTiles = 22;
-    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 5, 10};
+    constexpr int kNumTiles = 21;
+    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 5, 10, 8};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
@@ -1599,11 +1630,10 @@ namespace vkhip {
             case 14: return pick_dma<2, 2, 2, 2, 2>(steps);
             case 15: return pick_dma<2, 2, 2, 4, 2>(steps);
             case 16: return pick_dma<2, 2, 4, 2, 2>(steps);
-            case 17: return pick_dma<2, 2, 3, 4, 2>(steps);
-            case 18: return pick_dma<2, 4, 3, 2, 2>(steps);
-            case 19: return pick_halo<2, 2, 2, 2, 1, 3, 1, 2, 3, 4>(nbi);
-            case 20: return pick_halo<2, 2, 1, 4, 1, 2, 1, 2, 3, 4, 5>(nbi);
-            case 21: return pick_halo<2, 4, 2, 2, 1, 2, 2, 3, 4, 5, 6, 8, 10>(nbi);
+            case 17: return pick_halo<2, 2, 2, 2, 1, 3, 1, 2, 3, 4>(nbi);
+            case 18: return pick_halo<2, 2, 1, 4, 1, 2, 1, 2, 3, 4, 5>(nbi);
+            case 19: return pick_halo<2, 4, 2, 2, 1, 2, 2, 3, 4, 5, 6, 8, 10>(nbi);
+            case 20: return pick_halo<2, 1, 1, 4, 1, 1, 1, 2, 3, 4, 5, 6, 8>(nbi);
         }
         return nullptr;
     }
