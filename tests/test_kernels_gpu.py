@@ -219,6 +219,30 @@ def test_conv_halo_3x3(gpu, tile, shape):
     assert_parity(got, ref, f"halo tile {tile} {shape}")
 
 
+@pytest.mark.parametrize("tile", HALO_TILES)
+@pytest.mark.parametrize("shape", [(2, 64, 56, 56, 64), (3, 32, 14, 14, 40), (2, 128, 28, 28, 100), (5, 64, 14, 10, 64),
+                                   (2, 48, 7, 8, 32)])
+def test_conv_halo_3x3_stride2(gpu, tile, shape):
+    """Stride-2 band: two input rows per output row, output rows from odd input heights (the last
+    centre row's lower neighbour is the zero row), odd output widths, several images per tile."""
+    N, C, H, W, Cout = shape
+    r = rng(140 + tile + C + H + W)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    OH, OW = (H - 1) // 2 + 1, (W - 1) // 2 + 1
+    res = round_half(r.standard_normal((N, Cout, OH, OW)))
+    lib = V.vkhip()
+    plan = V.ConvPlan()
+    d, _ = conv_desc((N, C, H, W), (Cout, C, 3, 3), (2, 2), (1, 1, 1, 1))
+    if lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, tile, 0, ctypes.byref(plan)) != 0:
+        pytest.skip("band does not fit this tile's LDS budget")
+    got, plan, _ = gpu_conv(x, w, b, (2, 2), (1, 1, 1, 1), act=1, res=res, algo=V.CONV_GEMM, tile=tile)
+    assert plan.tile == tile
+    ref = oracle_conv(x, w, b, (2, 2), (1, 1, 1, 1), res=res, act=1)
+    assert_parity(got, ref, f"halo s2 tile {tile} {shape}")
+
+
 @pytest.mark.parametrize("tile", [17, 18, 20])
 def test_conv_halo_splitk(gpu, tile):
     r = rng(130 + tile)
@@ -231,10 +255,10 @@ def test_conv_halo_splitk(gpu, tile):
 
 
 def test_conv_halo_rejects_other_shapes(gpu):
-    """The halo tiles refuse stride 2, odd width, 1x1, Cin not a multiple of 16 and Winograd."""
+    """The halo tiles refuse stride 3, odd width, 1x1, Cin not a multiple of 16 and Winograd."""
     lib = V.vkhip()
     plan = V.ConvPlan()
-    for xs, ws, st, pd in [((1, 16, 8, 8), (8, 16, 3, 3), (2, 2), (1, 1, 1, 1)), ((1, 16, 7, 7), (8, 16, 3, 3), (1, 1), (1, 1, 1, 1)),
+    for xs, ws, st, pd in [((1, 16, 9, 9), (8, 16, 3, 3), (3, 3), (1, 1, 1, 1)), ((1, 16, 7, 7), (8, 16, 3, 3), (1, 1), (1, 1, 1, 1)),
                            ((1, 16, 8, 8), (8, 16, 1, 1), (1, 1), (0, 0, 0, 0)), ((1, 24, 8, 8), (8, 24, 3, 3), (1, 1), (1, 1, 1, 1))]:
         d, _ = conv_desc(xs, ws, st, pd)
         for t in HALO_TILES:

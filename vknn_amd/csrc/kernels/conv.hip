@@ -980,15 +980,16 @@ namespace vkhip {
     }
 
     // ------------------------------------------------------------------ 3x3 halo-tile GEMM kernel
-    // Direct 3x3 stride-1 pad-1 convolution (Cin a multiple of 16*KK, even W) that reads each input
-    // pixel once per workgroup instead of once per tap: the workgroup's BN consecutive output
-    // pixels (row-major over n, oy, ox, free to cross image boundaries) need a band of input rows;
+    // Direct 3x3 pad-1 convolution, stride 1 or 2 (Cin a multiple of 16*KK, even input width W),
+    // that reads each input pixel once per workgroup instead of once per tap: the workgroup's BN
+    // consecutive output pixels (row-major over n, oy, ox, free to cross image boundaries) need a
+    // band of input rows (rows S*oy - 1 .. S*oy + 1 of each output row oy);
     // per channel slot the band is copied global->LDS by buffer-load-to-LDS, 16 bytes (a pixel pair)
     // per lane, into rows of W + 2 pixels: W data pixels then two zero pixels, so the left
     // neighbour of column 0 is the previous row's last zero pixel (for the first band row: the
     // previous slot's zero tail, or a zero guard before slot 0) and the right neighbour of
     // column W-1 is the first one. Each image contributes H + 2 band rows (its zero rows above and
-    // below), so the band row of (n, iy) is (n - n_first)(H + 2) + iy + 1 - oy_first. Rows outside
+    // below), so the band row of (n, iy) is (n - n_first)(H + 2) + iy + 1 - S*oy_first. Rows outside
     // the image, pad pairs and lanes past the band get an out-of-range offset and write zeros.
     // The 9 taps of a 16-channel K step then read their B fragments from the same band at a
     // shift of (ky - 1)(W + 2) + (kx - 1) pixels. A (weights) arrives by LDS DMA too, prepacked as
@@ -1032,17 +1033,17 @@ namespace vkhip {
         const int wm0    = wmi * 32 * FM;
         const int wn0    = wni * 32 * FN;
 
-        const int W   = a.W, H = a.H, HW = a.HW;
+        const int W   = a.W, H = a.H, HW = a.HW, OW = a.OW, OHW = a.OHW, S = a.SH;
         const int PW  = (W + 2) >> 1; // pixel pairs per band row
-        const int nf  = n0 / HW;
-        const int oyf = (n0 - nf * HW) / W;
-        const int NI  = a.P / HW;
-        // band rows of this workgroup: up to the row below its last pixel's row; lanes past them
-        // copy zeros, so the last 8 bytes of every slot are zero (the left neighbour of the next
-        // slot's first pixel)
+        const int nf  = n0 / OHW;
+        const int iyf = S * ((n0 - nf * OHW) / OW); // input row of the first pixel's centre tap
+        const int NI  = a.P / OHW;
+        // band rows of this workgroup: up to the row below its last pixel's centre row; lanes past
+        // them copy zeros, so the last 8 bytes of every slot are zero (the left neighbour of the
+        // next slot's first pixel)
         const int pl    = min(a.P, n0 + BN) - 1;
-        const int nl    = pl / HW;
-        const int nrows = (nl - nf) * (H + 2) + (pl - nl * HW) / W + 1 - oyf + 2;
+        const int nl    = pl / OHW;
+        const int nrows = (nl - nf) * (H + 2) + S * ((pl - nl * OHW) / OW) + 1 - iyf + 2;
 
         const unsigned char *Wt = reinterpret_cast<const unsigned char *>(a.w) + (long long) m_tile * a.nsteps * ASTAGE;
         const int ks_begin = split * a.steps_per_split;
@@ -1063,7 +1064,7 @@ namespace vkhip {
             const int k    = i * 64 + lane;
             const int vrow = k / PW;
             const int pc   = k - vrow * PW;
-            const int vabs = vrow + oyf;
+            const int vabs = vrow + iyf;
             const int n    = nf + vabs / (H + 2);
             const int iy   = vabs % (H + 2) - 1;
             const bool ok  = 2 * pc < W && iy >= 0 && iy < H && n < NI && vrow < nrows;
@@ -1097,10 +1098,10 @@ namespace vkhip {
             const int p = n0 + wn0 + 32 * j + (lane & 31);
             int       q = W + 3; // any interior position: columns past P read the band harmlessly
             if (p < a.P) {
-                const int n  = p / HW;
-                const int r  = p - n * HW;
-                const int oy = r / W;
-                q            = ((n - nf) * (H + 2) + oy + 1 - oyf) * (W + 2) + (r - oy * W);
+                const int n  = p / OHW;
+                const int r  = p - n * OHW;
+                const int oy = r / OW;
+                q            = ((n - nf) * (H + 2) + S * oy + 1 - iyf) * (W + 2) + S * (r - oy * OW);
             }
             qb[j] = BOFF + (2 * g) * SS + q * 8;
         }
@@ -1540,7 +1541,7 @@ namespace vkhip {
     // kind 1: conv_bd_kernel (A via LDS DMA, B straight into registers), waves of (32FM) x (32FN).
     // kind 2: conv_dma_kernel (A and B via LDS DMA; dense B only: 1x1 s1 with an even pixel count
     //         per image, Winograd GEMMs with an even tile count), 2x2 waves of (32FM) x (32FN).
-    // kind 3: conv_halo_kernel (3x3 stride-1 pad-1 only: input band staged once in LDS for all 9
+    // kind 3: conv_halo_kernel (3x3 pad-1, stride 1 or 2: input band staged once in LDS for all 9
     //         taps), KK 16-channel K steps per LDS stage.
     struct TileCfg {
         int BM, BN, WM, WN, kind, FM, FN, KK;
@@ -1569,7 +1570,7 @@ namespace vkhip {
         {64, 128, 1, 4, 3, 2, 1, 1},  // 20 (one stage, several workgroups per CU)
     };
     constexpr int kNumTiles = 21;
-    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 5, 10, 8};
+    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
@@ -1631,9 +1632,9 @@ namespace vkhip {
             case 15: return pick_dma<2, 2, 2, 4, 2>(steps);
             case 16: return pick_dma<2, 2, 4, 2, 2>(steps);
             case 17: return pick_halo<2, 2, 2, 2, 1, 3, 1, 2, 3, 4>(nbi);
-            case 18: return pick_halo<2, 2, 1, 4, 1, 2, 1, 2, 3, 4, 5>(nbi);
+            case 18: return pick_halo<2, 2, 1, 4, 1, 2, 1, 2, 3, 4, 5, 6, 8, 10, 12, 15>(nbi);
             case 19: return pick_halo<2, 4, 2, 2, 1, 2, 2, 3, 4, 5, 6, 8, 10>(nbi);
-            case 20: return pick_halo<2, 1, 1, 4, 1, 1, 1, 2, 3, 4, 5, 6, 8>(nbi);
+            case 20: return pick_halo<2, 1, 1, 4, 1, 1, 1, 2, 3, 4, 5, 6, 8, 10, 12, 16>(nbi);
         }
         return nullptr;
     }
@@ -1653,24 +1654,26 @@ namespace vkhip {
                (d->H * d->W) % 2 == 0;
     }
 
-    // conv_halo_kernel: 3x3, stride 1, pad 1, dilation 1, same-size output, even W (pixel pairs),
-    // Cin a multiple of the stage's 16*KK channels.
+    // conv_halo_kernel: 3x3, stride 1 or 2 (both axes), pad 1, dilation 1, output (H - 1)/S + 1,
+    // even input width W (pixel pairs), Cin a multiple of the stage's 16*KK channels.
     static bool halo_shape_ok(const vkhip_conv_desc *d, const TileCfg &t) {
-        return d->group == 1 && d->KH == 3 && d->KW == 3 && d->SH == 1 && d->SW == 1 && d->PT == 1 && d->PL == 1 && d->DH == 1 &&
-               d->DW == 1 && d->OH == d->H && d->OW == d->W && d->W % 2 == 0 && d->Cin % (16 * t.KK) == 0;
+        const int S = d->SH;
+        return d->group == 1 && d->KH == 3 && d->KW == 3 && (S == 1 || S == 2) && d->SW == S && d->PT == 1 && d->PL == 1 &&
+               d->DH == 1 && d->DW == 1 && d->OH == (d->H - 1) / S + 1 && d->OW == (d->W - 1) / S + 1 && d->W % 2 == 0 &&
+               d->Cin % (16 * t.KK) == 0;
     }
 
     // 1 KB copy chunks per channel slot of the largest input band any workgroup of a halo tile
     // needs: band rows run from the row above the first output pixel's row to the row below the
     // last one's, with two extra (zero) rows per image boundary crossed; W/2 + 1 pixel pairs a row.
     static int halo_nbi(const vkhip_conv_desc *d, const TileCfg &t) {
-        const int64_t HW = (int64_t) d->H * d->W, P = (int64_t) d->N * HW, PW = d->W / 2 + 1;
+        const int64_t OHW = (int64_t) d->OH * d->OW, P = (int64_t) d->N * OHW, PW = d->W / 2 + 1, S = d->SH;
         int64_t       rows = 0;
         for (int64_t p0 = 0; p0 < P; p0 += t.BN) {
             const int64_t p1 = std::min(P, p0 + t.BN) - 1;
-            const int64_t nf = p0 / HW, oyf = (p0 % HW) / d->W;
-            const int64_t nl = p1 / HW, oyl = (p1 % HW) / d->W;
-            rows = std::max(rows, (nl - nf) * (d->H + 2) + oyl + 1 - oyf + 2);
+            const int64_t nf = p0 / OHW, oyf = (p0 % OHW) / d->OW;
+            const int64_t nl = p1 / OHW, oyl = (p1 % OHW) / d->OW;
+            rows = std::max(rows, (nl - nf) * (d->H + 2) + S * (oyl - oyf) + 1 + 2);
         }
         int nbi = (int) ceil_div(rows * PW, 64);
         const int nw = t.WM * t.WN;
@@ -1800,7 +1803,7 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
     if (tile < 0) tile = (algo == VKHIP_CONV_SPLITK) ? (ceil_div(d->Cout, 4) * 4 <= 32 ? 6 : 3) : default_tile(d, wino);
     if (tile >= kNumTiles) return set_error(VKHIP_ERR_INVALID, "tile index %d out of range", tile);
     if (kTiles[tile].kind == 3 && (wino || !halo_shape_ok(d, kTiles[tile]) || halo_nbi(d, kTiles[tile]) > kHaloMaxNBI[tile]))
-        return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a 3x3 stride-1 pad-1 conv with even W, Cin %% %d == 0 and a band that fits LDS", tile,
+        return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a 3x3 stride-1/2 pad-1 conv with even W, Cin %% %d == 0 and a band that fits LDS", tile,
                          16 * kTiles[tile].KK);
     if (kTiles[tile].kind == 2 && !dma_eligible(d, wino))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a dense B operand (1x1 stride 1 with an even pixel count, or Winograd)", tile);
