@@ -122,7 +122,8 @@ NUM_TILES = V.vkhip().vkhip_conv_tile_count()
 BD_TILES = [8, 9, 10]            # conv_bd_kernel tiles (A via LDS DMA, B gathered into registers)
 DMA_TILES = [11, 12, 13, 14, 15, 16]     # conv_dma_kernel tiles (A and B via LDS DMA; dense B only)
 HALO_TILES = [17, 18, 19, 20]         # conv_halo_kernel tiles (3x3 s1 p1: input band staged once for all taps)
-GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES and t not in HALO_TILES]
+STEM_TILES = [21, 22, 23]                 # conv_stem_kernel tiles (3x3/7x7 over at most 4 input channels)
+GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES + HALO_TILES + STEM_TILES]
 
 
 @pytest.mark.parametrize("tile", GATHER_TILES)
@@ -241,6 +242,36 @@ def test_conv_halo_3x3_stride2(gpu, tile, shape):
     assert plan.tile == tile
     ref = oracle_conv(x, w, b, (2, 2), (1, 1, 1, 1), res=res, act=1)
     assert_parity(got, ref, f"halo s2 tile {tile} {shape}")
+
+
+@pytest.mark.parametrize("tile", STEM_TILES)
+@pytest.mark.parametrize("case", [(2, 3, 224, 224, 64, 7, 2), (3, 3, 32, 30, 16, 3, 2), (2, 4, 20, 18, 40, 3, 1),
+                                  (1, 3, 40, 38, 24, 7, 1), (2, 1, 16, 16, 8, 7, 2), (5, 2, 9, 10, 70, 3, 2)])
+def test_conv_stem(gpu, tile, case):
+    """Stem kernel: 3 or fewer channels padded to one slot, 7x7 and 3x3 taps packed four to an
+    MFMA step, stride 1/2, odd heights, ragged output channels, tiles across images, residual."""
+    N, C, H, W, Cout, K, S = case
+    r = rng(150 + tile + H + K)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, K, K)) * np.sqrt(2.0 / (K * K * C))).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    p = K // 2
+    OH, OW = (H + 2 * p - K) // S + 1, (W + 2 * p - K) // S + 1
+    res = round_half(r.standard_normal((N, Cout, OH, OW)))
+    got, plan, _ = gpu_conv(x, w, b, (S, S), (p, p, p, p), act=1, res=res, algo=V.CONV_GEMM, tile=tile)
+    assert plan.tile == tile
+    ref = oracle_conv(x, w, b, (S, S), (p, p, p, p), res=res, act=1)
+    assert_parity(got, ref, f"stem tile {tile} {case}")
+
+
+def test_conv_stem_rejects_other_shapes(gpu):
+    lib = V.vkhip()
+    plan = V.ConvPlan()
+    for xs, ws, st, pd in [((1, 5, 8, 8), (8, 5, 3, 3), (1, 1), (1, 1, 1, 1)), ((1, 3, 8, 8), (8, 3, 5, 5), (1, 1), (2, 2, 2, 2)),
+                           ((1, 3, 9, 9), (8, 3, 3, 3), (2, 2), (1, 1, 1, 1)), ((1, 3, 8, 8), (8, 3, 3, 3), (1, 1), (0, 0, 0, 0))]:
+        d, _ = conv_desc(xs, ws, st, pd)
+        for t in STEM_TILES:
+            assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, t, 0, ctypes.byref(plan)) != 0
 
 
 @pytest.mark.parametrize("tile", [17, 18, 20])

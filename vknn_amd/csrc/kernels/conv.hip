@@ -1179,6 +1179,144 @@ namespace vkhip {
         gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, 0, lane);
     }
 
+    // ------------------------------------------------------------------ stem kernel (Cin <= 4)
+    // KxK convolution (K = 3 or 7, stride 1 or 2, pad K/2) over at most 4 input channels, i.e. the
+    // first layer of a CNN on an RGB image. The whole reduction is KxK taps x 4 channels, so one
+    // 16-deep MFMA K step holds 4 taps (lanes 0-31 taps 4s and 4s+1, lanes 32-63 taps 4s+2 and
+    // 4s+3, 4 channels each; taps past K*K have zero weights) and all KT = ceil(K*K/4) steps fit
+    // one LDS stage: the workgroup copies its input band (one channel slot) and the prepacked
+    // weights [m_tile][step][m_frag][lane][8 halves] once, waits, and runs every step from LDS.
+    // Band layout as in the halo kernel with rows of W + K - 1 pixels (W data, K - 1 zeros that
+    // serve as the right pad of this row and the left pad of the next) and H + K - 1 band rows per
+    // image (K/2 zero rows above and below).
+    template <int K, int FM, int FN, int WM, int WN, int NBI>
+    __global__ __launch_bounds__(64 * WM * WN) void conv_stem_kernel(GemmArgs a) {
+        constexpr int NW     = WM * WN;
+        constexpr int BM     = 32 * FM * WM;
+        constexpr int BN     = 32 * FN * WN;
+        constexpr int MF     = BM / 32;
+        constexpr int KT     = (K * K + 3) / 4; // 16-deep K steps
+        constexpr int KH2    = K / 2;
+        constexpr int NA     = KT * MF;         // 1 KB A chunks
+        constexpr int BOFF   = NA * 1024 + 32;  // band start (32 zero guard bytes before it)
+        constexpr int NC     = NA + NBI;        // chunks per workgroup
+        constexpr int NCW    = (NC + NW - 1) / NW;
+        constexpr int SPARE  = BOFF + NBI * 1024;
+        static_assert(SPARE + 1024 <= 160 * 1024, "LDS budget");
+        __shared__ __attribute__((aligned(16))) unsigned char sm[SPARE + 1024];
+
+        const int tid  = threadIdx.x;
+        const int lane = tid & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int wmi  = wave / WN;
+        const int wni  = wave % WN;
+        const int lin    = xcd_remap(blockIdx.x, gridDim.x);
+        const int m_tile = lin % a.m_tiles;
+        const int n0     = (lin / a.m_tiles) * BN;
+        const int m0     = m_tile * BM;
+        const int wm0    = wmi * 32 * FM;
+        const int wn0    = wni * 32 * FN;
+
+        const int W = a.W, H = a.H, OW = a.OW, OHW = a.OHW, S = a.SH;
+        const int RS  = W + K - 1;  // band row stride in pixels (even: W even, K odd)
+        const int VR  = H + K - 1;  // band rows per image
+        const int nf  = n0 / OHW;
+        const int iyf = S * ((n0 - nf * OHW) / OW);
+        const int NI  = a.P / OHW;
+        const int pl  = min(a.P, n0 + BN) - 1;
+        const int nl  = pl / OHW;
+        const int nrows = (nl - nf) * VR + S * ((pl - nl * OHW) / OW) + 2 * KH2 + 1 - iyf;
+
+        const unsigned char *Wt = reinterpret_cast<const unsigned char *>(a.w) + (long long) m_tile * NA * 1024;
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) a.x_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *) Wt, (short) 0, NA * 1024, 0x00020000);
+        constexpr unsigned kInvalid = 0x80000000u;
+        if (tid < 2) *reinterpret_cast<u32x4 *>(&sm[NA * 1024 + tid * 16]) = u32x4 {0u, 0u, 0u, 0u};
+
+        // copies: chunk c = r*NW + wave; chunks < NA are weights, then NBI band chunks, the rest
+        // (every wave issues the same count) copy zeros into the spare KB
+#pragma unroll
+        for (int r = 0; r < NCW; ++r) {
+            const int c = r * NW + wave;
+            if (c < NA) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (__attribute__((address_space(3))) void *) (sm + c * 1024), 16,
+                                                         (unsigned) (c * 1024 + lane * 16), 0, 0, 0);
+            } else {
+                const int  k    = (c - NA) * 64 + lane;
+                const int  vrow = k / (RS >> 1);
+                const int  pc   = k - vrow * (RS >> 1);
+                const int  vabs = vrow + iyf;
+                const int  n    = nf + vabs / VR;
+                const int  iy   = vabs % VR - KH2;
+                const bool ok   = c < NC && 2 * pc < W && iy >= 0 && iy < H && n < NI && vrow < nrows;
+                const unsigned vo = ok ? (unsigned) ((n * a.HW + iy * W + 2 * pc) * 8) : kInvalid;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void *) (c < NC ? sm + BOFF + (c - NA) * 1024 : sm + SPARE),
+                                                         16, vo, 0, 0, 0);
+            }
+        }
+
+        // per lane: centre pixel of each fragment column, and the two tap offsets of every step
+        const int g = lane >> 5;
+        int       qb[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int p = n0 + wn0 + 32 * j + (lane & 31);
+            int       q = KH2 * RS + KH2; // any interior position for columns past P
+            if (p < a.P) {
+                const int n  = p / OHW;
+                const int rr = p - n * OHW;
+                const int oy = rr / OW;
+                q            = ((n - nf) * VR + S * oy + KH2 - iyf) * RS + S * (rr - oy * OW);
+            }
+            qb[j] = BOFF + q * 8;
+        }
+        int toff[KT][2];
+#pragma unroll
+        for (int s = 0; s < KT; ++s)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int t = 4 * s + 2 * g + h;
+                toff[s][h]  = t < K * K ? ((t / K - KH2) * RS + (t % K - KH2)) * 8 : 0;
+            }
+
+        float16v acc[FM][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+        __syncthreads();
+        const unsigned char *Ab = sm + ((wmi * FM) * 64 + lane) * 16;
+        half8 fa[2][FM], fb[2][FN];
+        auto rd = [&](int s, int d) __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const u32x2 lo = *reinterpret_cast<const u32x2 *>(sm + qb[j] + toff[s][0]);
+                const u32x2 hi = *reinterpret_cast<const u32x2 *>(sm + qb[j] + toff[s][1]);
+                fb[d][j] = __builtin_bit_cast(half8, u32x4_make(lo.x, lo.y, hi.x, hi.y));
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i) fa[d][i] = *reinterpret_cast<const half8 *>(Ab + (s * MF + i) * 1024);
+        };
+        rd(0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < KT; ++s) {
+            if (s + 1 < KT) rd(s + 1, (s + 1) & 1);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[s & 1][i], fb[s & 1][j], acc[i][j], 0, 0, 0);
+            if (s + 1 < KT) StepSchedule<0, FM * FN, FM + 2 * FN, 4 * FN>::apply();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, 0, 0, lane);
+    }
+
     // Split-K reduce: y = act(sum_s part[s] + bias (+res)).
     __global__ void splitk_reduce_kernel(const float4v *part, const float *bias, const uint2 *res, uint2 *y, int ksplit,
                                          int Coutb, int Cout, int P, int OHW, int act, float lo, float hi, int has_res) {
@@ -1543,6 +1681,7 @@ namespace vkhip {
     //         per image, Winograd GEMMs with an even tile count), 2x2 waves of (32FM) x (32FN).
     // kind 3: conv_halo_kernel (3x3 pad-1, stride 1 or 2: input band staged once in LDS for all 9
     //         taps), KK 16-channel K steps per LDS stage.
+    // kind 4: conv_stem_kernel (3x3 or 7x7, stride 1 or 2, pad K/2, at most 4 input channels).
     struct TileCfg {
         int BM, BN, WM, WN, kind, FM, FN, KK;
     };
@@ -1568,9 +1707,12 @@ namespace vkhip {
         {64, 256, 1, 4, 3, 2, 2, 1},  // 18 (2-stage ring, two workgroups per CU)
         {128, 256, 2, 2, 3, 2, 4, 1}, // 19 (2-stage ring)
         {64, 128, 1, 4, 3, 2, 1, 1},  // 20 (one stage, several workgroups per CU)
+        {64, 256, 1, 4, 4, 2, 2},     // 21 stem
+        {64, 128, 1, 4, 4, 2, 1},     // 22 stem
+        {32, 256, 1, 4, 4, 1, 2},     // 23 stem (few output channels)
     };
-    constexpr int kNumTiles = 21;
-    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16};
+    constexpr int kNumTiles = 24;
+    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
@@ -1612,6 +1754,14 @@ namespace vkhip {
         return nullptr;
     }
 
+    template <int K, int FM, int FN, int WM, int WN, int NBI0, int... NBIS>
+    static GemmKernelFn pick_stem(int nbi) {
+        if (nbi <= NBI0) return conv_stem_kernel<K, FM, FN, WM, WN, NBI0>;
+        if constexpr (sizeof...(NBIS) > 0) return pick_stem<K, FM, FN, WM, WN, NBIS...>(nbi);
+        return nullptr;
+    }
+
+    // bmode carries the kernel size for the stem tiles
     static GemmKernelFn gemm_kernel_for(int tile, int bmode, int steps, int nbi = 0) {
         switch (tile) {
             case 0: return pick_bmode<128, 128, 2, 2>(bmode);
@@ -1635,6 +1785,12 @@ namespace vkhip {
             case 18: return pick_halo<2, 2, 1, 4, 1, 2, 1, 2, 3, 4, 5, 6, 8, 10, 12, 15>(nbi);
             case 19: return pick_halo<2, 4, 2, 2, 1, 2, 2, 3, 4, 5, 6, 8, 10>(nbi);
             case 20: return pick_halo<2, 1, 1, 4, 1, 1, 1, 2, 3, 4, 5, 6, 8, 10, 12, 16>(nbi);
+            case 21:
+                return bmode == 7 ? pick_stem<7, 2, 2, 1, 4, 8, 16, 24, 32, 48>(nbi) : pick_stem<3, 2, 2, 1, 4, 4, 8, 16, 24, 32, 48>(nbi);
+            case 22:
+                return bmode == 7 ? pick_stem<7, 2, 1, 1, 4, 8, 16, 24, 32, 48>(nbi) : pick_stem<3, 2, 1, 1, 4, 4, 8, 16, 24, 32, 48>(nbi);
+            case 23:
+                return bmode == 7 ? pick_stem<7, 1, 2, 1, 4, 8, 16, 24, 32, 48>(nbi) : pick_stem<3, 1, 2, 1, 4, 4, 8, 16, 24, 32, 48>(nbi);
         }
         return nullptr;
     }
@@ -1681,6 +1837,30 @@ namespace vkhip {
         return nbi;
     }
 
+    // conv_stem_kernel: at most 4 input channels, square 3x3 or 7x7 kernel, stride 1 or 2 (both
+    // axes), pad K/2, dilation 1, even input width.
+    static bool stem_shape_ok(const vkhip_conv_desc *d) {
+        const int K = d->KH, S = d->SH;
+        return d->group == 1 && d->Cin <= 4 && (K == 3 || K == 7) && d->KW == K && (S == 1 || S == 2) && d->SW == S &&
+               d->PT == K / 2 && d->PL == K / 2 && d->DH == 1 && d->DW == 1 && d->OH == (d->H + 2 * (K / 2) - K) / S + 1 &&
+               d->OW == (d->W + 2 * (K / 2) - K) / S + 1 && d->W % 2 == 0;
+    }
+
+    // 1 KB copy chunks of the largest input band a stem workgroup needs (rows of W + K - 1 pixels,
+    // H + K - 1 band rows per image).
+    static int stem_nbi(const vkhip_conv_desc *d, const TileCfg &t) {
+        const int64_t OHW = (int64_t) d->OH * d->OW, P = (int64_t) d->N * OHW, S = d->SH, K = d->KH;
+        const int64_t RS = d->W + K - 1, VR = d->H + K - 1;
+        int64_t       rows = 0;
+        for (int64_t p0 = 0; p0 < P; p0 += t.BN) {
+            const int64_t p1 = std::min(P, p0 + t.BN) - 1;
+            const int64_t nf = p0 / OHW, oyf = (p0 % OHW) / d->OW;
+            const int64_t nl = p1 / OHW, oyl = (p1 % OHW) / d->OW;
+            rows = std::max(rows, (nl - nf) * VR + S * (oyl - oyf) + 2 * (K / 2) + 1);
+        }
+        return (int) ceil_div(rows * (RS / 2), 64);
+    }
+
     static bool wino_eligible(const vkhip_conv_desc *d) {
         return d->group == 1 && d->KH == 3 && d->KW == 3 && d->SH == 1 && d->SW == 1 && d->PT == 1 && d->PL == 1 &&
                d->DH == 1 && d->DW == 1 && d->OH == d->H && d->OW == d->W;
@@ -1709,6 +1889,11 @@ namespace vkhip {
         }
         g.Kp      = round_up(g.Kslots * 4, kBK);
         g.nsteps  = g.Kp / kBK;
+        if (t.kind == 4) { // all K*K taps x 4 channels in one stage of ceil(K*K/4) 16-deep steps
+            g.Kp     = ceil_div((int64_t) d->KH * d->KW, 4) * 16;
+            g.nsteps = 1;
+            g.bmode  = d->KH;
+        }
         if (t.kind == 3) { // 9 taps x Cin, stages of 16*KK channels (all 9 taps each)
             g.Kp     = 9 * (int64_t) d->Cin;
             g.nsteps = d->Cin / (16 * t.KK);
@@ -1727,6 +1912,12 @@ namespace vkhip {
         const int     BM   = t.BM;
         const int64_t base = ((oc / BM) * g.nsteps + k / kBK) * (int64_t) (BM * kBK);
         if (t.kind == 0) return base + (oc % BM) * kBK + k % kBK; // kinds 1 and 2: fragment order
+        if (t.kind == 4) {
+            // [m_tile][step][m_frag][lane][8 halves]; Cinb = 1, so k = tap*4 + c and step = tap/4
+            const int64_t tap = k / 4, kr = (tap % 4) * 4 + k % 4, r = oc % BM;
+            const int64_t l = (kr / 8) * 32 + r % 32;
+            return (oc / BM) * g.Kp * BM + (((tap / 4) * (BM / 32) + r / 32) * 64 + l) * 8 + kr % 8;
+        }
         if (t.kind == 3) {
             // [m_tile][stage][tap][kk][m_frag][lane][8 halves]; k = (tap*Cinb + cb)*4 + c%4
             const int64_t tap = (k / 4) / g.Cinb, c = ((k / 4) % g.Cinb) * 4 + k % 4;
@@ -1805,6 +1996,8 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
     if (kTiles[tile].kind == 3 && (wino || !halo_shape_ok(d, kTiles[tile]) || halo_nbi(d, kTiles[tile]) > kHaloMaxNBI[tile]))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a 3x3 stride-1/2 pad-1 conv with even W, Cin %% %d == 0 and a band that fits LDS", tile,
                          16 * kTiles[tile].KK);
+    if (kTiles[tile].kind == 4 && (wino || !stem_shape_ok(d) || stem_nbi(d, kTiles[tile]) > kHaloMaxNBI[tile]))
+        return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a 3x3/7x7 stride-1/2 pad-K/2 conv over at most 4 channels with even W", tile);
     if (kTiles[tile].kind == 2 && !dma_eligible(d, wino))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a dense B operand (1x1 stride 1 with an even pixel count, or Winograd)", tile);
     ConvGeom g = gemm_geom(d, tile, wino);
@@ -1943,7 +2136,7 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     a.hi     = d->act_hi;
     a.m_tiles = (int) g.m_tiles;
     const int split_steps = plan->algo == VKHIP_CONV_SPLITK ? (int) ceil_div(g.nsteps, plan->ksplit) : (int) g.nsteps;
-    GemmKernelFn fn = gemm_kernel_for(plan->tile, g.bmode, split_steps, t.kind == 3 ? halo_nbi(d, t) : 0);
+    GemmKernelFn fn = gemm_kernel_for(plan->tile, g.bmode, split_steps, t.kind == 3 ? halo_nbi(d, t) : (t.kind == 4 ? stem_nbi(d, t) : 0));
     if (!fn) return set_error(VKHIP_ERR_INVALID, "conv_forward: no kernel for tile %d", plan->tile);
 
     if (wino) {
