@@ -180,14 +180,30 @@ namespace vknn {
                 }
                 double                 best = 1e30, bestDirect = 1e30;
                 std::array<int32_t, 3> pick = {base.algo, base.tile, base.ksplit};
-                auto x  = std::make_shared<DevBuf>(nc4Bytes({d.N, d.Cin, d.H, d.W}));
-                auto yb = std::make_shared<DevBuf>(nc4Bytes({d.N, d.Cout, d.OH, d.OW}));
-                check(vkhip_fill_zero(x->ptr, x->bytes, nullptr), "tune fill");
-                check(vkhip_fill_zero(yb->ptr, yb->bytes, nullptr), "tune fill");
+                // Candidates run as the network runs them (with the residual read when the conv has
+                // one) on rotating buffer sets whose total exceeds the GPU's 256 MB last-level
+                // cache, so memory-bound layers are timed from HBM like in a full forward pass
+                // rather than from cache-resident repeats of one input.
+                const size_t xbytes = nc4Bytes({d.N, d.Cin, d.H, d.W}), ybytes = nc4Bytes({d.N, d.Cout, d.OH, d.OW});
+                const size_t set_bytes = xbytes + ybytes * (d.has_res ? 2 : 1);
+                const int    nset      = (int) std::min<size_t>(6, std::max<size_t>(1, ((size_t) 640 << 20) / std::max<size_t>(set_bytes, 1) + 1));
+                std::vector<TuneSet> sets;
+                for (int k = 0; k < nset; ++k) {
+                    TuneSet t;
+                    t.x = std::make_shared<DevBuf>(xbytes);
+                    t.y = std::make_shared<DevBuf>(ybytes);
+                    check(vkhip_fill_zero(t.x->ptr, xbytes, nullptr), "tune fill");
+                    check(vkhip_fill_zero(t.y->ptr, ybytes, nullptr), "tune fill");
+                    if (d.has_res) {
+                        t.r = std::make_shared<DevBuf>(ybytes);
+                        check(vkhip_fill_zero(t.r->ptr, ybytes, nullptr), "tune fill");
+                    }
+                    sets.push_back(t);
+                }
                 for (auto &c: cands) {
                     vkhip_conv_plan p;
                     if (vkhip_conv_plan_make(&d, c[0], c[1], c[2], &p)) continue;
-                    double ms = timePlan(p, w, b, x->ptr, yb->ptr);
+                    double ms = timePlan(p, w, b, sets);
                     if (ms < best) {
                         best = ms;
                         pick = {p.algo, p.tile, p.ksplit};
@@ -201,7 +217,7 @@ namespace vknn {
                     for (int t: {-1, 8, 10, 14, 12, 16}) {
                         vkhip_conv_plan p;
                         if (vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, t, 0, &p)) continue;
-                        double ms = timePlan(p, w, b, x->ptr, yb->ptr);
+                        double ms = timePlan(p, w, b, sets);
                         if (ms < bestWino) {
                             bestWino = ms;
                             wpick    = {p.algo, p.tile, p.ksplit};
@@ -219,22 +235,29 @@ namespace vknn {
                 build(w, b);
             }
 
-            // min over 3 timings of 4 back-to-back launches on scratch buffers
-            double timePlan(const vkhip_conv_plan &p, const float *w, const float *b, void *x, void *y) {
+            struct TuneSet {
+                std::shared_ptr<DevBuf> x, y, r;
+            };
+
+            // min over 3 timings of 6 back-to-back launches, each on the next buffer set
+            double timePlan(const vkhip_conv_plan &p, const float *w, const float *b, const std::vector<TuneSet> &sets) {
                 std::vector<uint8_t> host(p.weight_bytes);
                 if (vkhip_conv_pack_weights(&d, &p, w, b, host.data())) return 1e30;
                 auto   bl  = upload(host.data(), host.size());
                 auto   wsb = p.workspace_bytes ? std::make_shared<DevBuf>(p.workspace_bytes) : nullptr;
-                vkhip_conv_desc dd = d;
-                dd.has_res = 0;
+                size_t k   = 0;
+                auto   run = [&]() {
+                    const TuneSet &t = sets[k++ % sets.size()];
+                    return vkhip_conv_forward(&d, &p, t.x->ptr, bl->ptr, t.r ? t.r->ptr : nullptr, t.y->ptr, wsb ? wsb->ptr : nullptr, nullptr);
+                };
                 vkhip_event_t e0, e1;
                 check(vkhip_event_create(&e0), "event");
                 check(vkhip_event_create(&e1), "event");
                 double best = 1e30;
-                if (vkhip_conv_forward(&dd, &p, x, bl->ptr, nullptr, y, wsb ? wsb->ptr : nullptr, nullptr) == VKHIP_OK) {
+                if (run() == VKHIP_OK) {
                     for (int r = 0; r < 3; ++r) {
                         vkhip_event_record(e0, nullptr);
-                        for (int k = 0; k < 4; ++k) vkhip_conv_forward(&dd, &p, x, bl->ptr, nullptr, y, wsb ? wsb->ptr : nullptr, nullptr);
+                        for (int i = 0; i < 6; ++i) run();
                         vkhip_event_record(e1, nullptr);
                         vkhip_event_sync(e1);
                         float ms = 0;

@@ -1710,9 +1710,11 @@ namespace vkhip {
         {64, 256, 1, 4, 4, 2, 2},     // 21 stem
         {64, 128, 1, 4, 4, 2, 1},     // 22 stem
         {32, 256, 1, 4, 4, 1, 2},     // 23 stem (few output channels)
+        {64, 128, 2, 2, 2, 1, 2},     // 24
+        {64, 256, 1, 4, 2, 2, 2},     // 25
     };
-    constexpr int kNumTiles = 24;
-    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48};
+    constexpr int kNumTiles = 26;
+    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
@@ -1791,6 +1793,8 @@ namespace vkhip {
                 return bmode == 7 ? pick_stem<7, 2, 1, 1, 4, 8, 16, 24, 32, 48>(nbi) : pick_stem<3, 2, 1, 1, 4, 4, 8, 16, 24, 32, 48>(nbi);
             case 23:
                 return bmode == 7 ? pick_stem<7, 1, 2, 1, 4, 8, 16, 24, 32, 48>(nbi) : pick_stem<3, 1, 2, 1, 4, 4, 8, 16, 24, 32, 48>(nbi);
+            case 24: return pick_dma<1, 2, 2, 2, 2>(steps);
+            case 25: return pick_dma<2, 2, 2, 1, 4>(steps);
         }
         return nullptr;
     }
