@@ -161,10 +161,12 @@ def test_conv_bd_general_gather_residual(gpu, tile):
 
 
 @pytest.mark.parametrize("tile", DMA_TILES)
-@pytest.mark.parametrize("shape", [(3, 72, 6, 10, 70), (2, 256, 14, 14, 300), (1, 24, 8, 8, 8)])
+@pytest.mark.parametrize("shape", [(3, 72, 6, 10, 70), (2, 256, 14, 14, 300), (1, 24, 8, 8, 8), (3, 72, 7, 7, 70),
+                                   (5, 64, 5, 9, 40)])
 def test_conv_dma_1x1(gpu, tile, shape):
     """Dense-B kernel: K tail (Cin not a multiple of 64), ragged output channels, pixel tiles
-    crossing image boundaries and the end of the batch, residual + ReLU epilogue."""
+    crossing image boundaries and the end of the batch, odd pixel counts per image (one padding
+    column per image), residual + ReLU epilogue."""
     N, C, H, W, Cout = shape
     r = rng(80 + tile + C)
     x = round_half(r.standard_normal((N, C, H, W)))
@@ -185,6 +187,10 @@ def test_conv_dma_winograd_and_splitk(gpu, tile):
     ref = oracle_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1)
     got, plan, _ = gpu_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1, algo=V.CONV_WINOGRAD, tile=tile)
     assert_parity(got, ref, f"dma winograd tile {tile}")
+    xo = round_half(r.standard_normal((1, 32, 6, 6)))   # 9 Winograd tiles: odd column count
+    wo = (r.standard_normal((40, 32, 3, 3)) * 0.1).astype(np.float32)
+    got, plan, _ = gpu_conv(xo, wo, None, (1, 1), (1, 1, 1, 1), act=0, algo=V.CONV_WINOGRAD, tile=tile)
+    assert_parity(got, oracle_conv(xo, wo, None, (1, 1), (1, 1, 1, 1)), f"dma winograd odd tiles {tile}")
     x1 = round_half(r.standard_normal((1, 512, 8, 8)))
     w1 = (r.standard_normal((256, 512, 1, 1)) * 0.05).astype(np.float32)
     got, plan, _ = gpu_conv(x1, w1, None, act=0, algo=V.CONV_SPLITK, tile=tile, ksplit=4)
@@ -193,11 +199,11 @@ def test_conv_dma_winograd_and_splitk(gpu, tile):
 
 
 def test_conv_dma_rejects_gather_shapes(gpu):
-    """The dense-B tiles refuse shapes whose B operand is a gather (3x3, stride 2, odd pixel count)."""
+    """The dense-B tiles refuse shapes whose B operand is a gather (3x3, stride 2, padded 1x1)."""
     lib = V.vkhip()
     plan = V.ConvPlan()
     for xs, ws, st, pd in [((1, 8, 8, 8), (8, 8, 3, 3), (1, 1), (1, 1, 1, 1)), ((1, 8, 8, 8), (8, 8, 1, 1), (2, 2), (0, 0, 0, 0)),
-                           ((1, 8, 7, 7), (8, 8, 1, 1), (1, 1), (0, 0, 0, 0))]:
+                           ((1, 8, 7, 7), (8, 8, 1, 1), (1, 1), (1, 1, 1, 1))]:
         d, _ = conv_desc(xs, ws, st, pd)
         assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, 11, 0, ctypes.byref(plan)) != 0
 

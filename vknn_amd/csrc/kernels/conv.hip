@@ -38,6 +38,8 @@ namespace vkhip {
         int           Coutb, Cout, OW, OHW;
         int           KW, SH, SW, PT, PL, DH, DW;
         int           P, Kslots, nsteps, steps_per_split;
+        int           Pv, OHWp; // GEMM columns and columns per image: P and OH*OW, or with one padding
+                                // column per image when the dense-B kernel needs an even count
         int           act;
         float         lo, hi;
         int           has_res, omode, m_tiles;
@@ -530,16 +532,17 @@ namespace vkhip {
 #pragma unroll
                 for (int jj = 0; jj < JG; ++jj) {
                     const int  px  = nw0 + (j0 + jj) * 32 + lrow;
-                    const bool pok = px < a.P;
-                    const int  pn  = px / a.OHW;
-                    const int  pr  = px - pn * a.OHW;
+                    const int  pn  = px / a.OHWp;
+                    const int  pr  = px - pn * a.OHWp;
+                    const bool pok = (px < a.Pv) & (pr < a.OHW);
 #pragma unroll
                     for (int i = 0; i < FM; ++i)
 #pragma unroll
                         for (int qq = 0; qq < 4; ++qq) {
                             const int  ocb = (mw0 + i * 32 + qq * 8 + lk * 4) >> 2;
                             const bool ok  = pok & (ocb < a.Coutb);
-                            if constexpr (MODE == 0) yoff[b][jj][i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + px) * 16) : kInvalid;
+                            if constexpr (MODE == 0)
+                                yoff[b][jj][i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + pn * a.OHW + pr) * 16) : kInvalid;
                             else yoff[b][jj][i][qq] = ok ? (unsigned) (((pn * a.Coutb + ocb) * a.OHW + pr) * 8) : kInvalid;
                             if constexpr (MODE == 3) rv[b][jj][i][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[b][jj][i][qq], 0, 0);
                         }
@@ -884,9 +887,11 @@ namespace vkhip {
         unsigned pbase[BPB];
 #pragma unroll
         for (int pb = 0; pb < BPB; ++pb) {
+            // virtual columns: OHWp per image (the padding column of an odd image reads the next
+            // 8 bytes, whatever they hold; its outputs are never stored)
             const int p = n0 + pb * 128 + 2 * lane;
-            const int n = p / a.HW;
-            pbase[pb]   = p < a.P ? (unsigned) ((n * a.Cinb * a.HW + (p - n * a.HW)) * 8) : kInvalid;
+            const int n = p / a.OHWp;
+            pbase[pb]   = p < a.Pv ? (unsigned) ((n * a.Cinb * a.HW + (p - n * a.OHWp)) * 8) : kInvalid;
         }
         auto issue = [&](int ks, int buf) __attribute__((always_inline)) {
             unsigned char *dst = sm[buf];
@@ -1801,17 +1806,18 @@ namespace vkhip {
 
     struct ConvGeom {
         int64_t Cinb, Coutb, Kslots, Kp, nsteps, Coutp, P, m_tiles, n_tiles;
+        int64_t Pv, HWp; // GEMM columns and columns per image (see GemmArgs::Pv)
         int     bmode;
     };
 
     static bool is_depthwise(const vkhip_conv_desc *d) { return d->group > 1; }
 
     // conv_dma_kernel copies B as pixel pairs of one channel slot: the GEMM columns must be dense
-    // NC4HW4 pixels (1x1, stride 1, no padding, or a Winograd V plane) with an even count per image.
+    // NC4HW4 pixels (1x1, stride 1, no padding, or a Winograd V plane); an odd pixel count per
+    // image gets one padding column per image (gemm_geom).
     static bool dma_eligible(const vkhip_conv_desc *d, bool wino) {
-        if (wino) return ((int64_t) d->N * ceil_div(d->OH, 2) * ceil_div(d->OW, 2)) % 2 == 0;
-        return d->KH == 1 && d->KW == 1 && d->SH == 1 && d->SW == 1 && d->PT == 0 && d->PL == 0 && d->OH == d->H && d->OW == d->W &&
-               (d->H * d->W) % 2 == 0;
+        if (wino) return true;
+        return d->KH == 1 && d->KW == 1 && d->SH == 1 && d->SW == 1 && d->PT == 0 && d->PL == 0 && d->OH == d->H && d->OW == d->W;
     }
 
     // conv_halo_kernel: 3x3, stride 1 or 2 (both axes), pad 1, dilation 1, output (H - 1)/S + 1,
@@ -1904,7 +1910,10 @@ namespace vkhip {
         }
         g.m_tiles = ceil_div(g.Coutb * 4, t.BM);
         g.Coutp   = g.m_tiles * t.BM;
-        g.n_tiles = ceil_div(g.P, t.BN);
+        g.HWp     = wino ? g.P : (int64_t) d->OH * d->OW;
+        if (t.kind == 2) g.HWp += g.HWp & 1;
+        g.Pv      = wino ? g.HWp : (int64_t) d->N * g.HWp;
+        g.n_tiles = ceil_div(g.Pv, t.BN);
         return g;
     }
 
@@ -2132,6 +2141,8 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     a.Coutb  = (int) g.Coutb;
     a.Cout   = d->Cout;
     a.P      = (int) g.P;
+    a.Pv     = (int) g.Pv;
+    a.OHWp   = (int) g.HWp;
     a.Kslots = (int) g.Kslots;
     a.nsteps = (int) g.nsteps;
     a.steps_per_split = (int) g.nsteps;
