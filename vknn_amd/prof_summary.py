@@ -16,7 +16,7 @@ import csv
 import re
 from collections import OrderedDict
 
-CONV_PREFIX = ("conv_gemm", "conv_bd", "conv_dma", "splitk_reduce", "wino_", "dwconv", "dwpw")
+CONV_PREFIX = ("conv_gemm", "conv_bd", "conv_dma", "conv_halo", "conv_stem", "splitk_reduce", "wino_", "dwconv", "dwpw")
 
 
 def family(name):
@@ -67,7 +67,7 @@ def cmd_trace(a):
     fam, span_ns, n = summarise(a.trace, a.steps)
     total = sum(v[1] for v in fam.values())
     conv = sum(v[1] for k, v in fam.items() if k.startswith(CONV_PREFIX))
-    gemm = sum(v[1] for k, v in fam.items() if k.startswith(("conv_gemm", "conv_bd", "conv_dma")))
+    gemm = sum(v[1] for k, v in fam.items() if k.startswith(("conv_gemm", "conv_bd", "conv_dma", "conv_halo", "conv_stem")))
     print(f"# {a.title}\n")
     if a.command:
         print(f"Command: `{a.command}`\n")
@@ -77,7 +77,7 @@ def cmd_trace(a):
     for k, (c, d) in sorted(fam.items(), key=lambda kv: -kv[1][1]):
         print(f"| `{k}` | {c / a.steps:.1f} | {d / c / 1e3:.2f} | {d / a.steps / 1e3:.1f} | {100 * d / total:.1f}% |")
     print(f"\nSum of kernel time per step: {total / a.steps / 1e3:.1f} us; conv kernels (gemm, split-K reduce, "
-          f"Winograd transforms, depthwise): {conv / a.steps / 1e3:.1f} us; implicit-GEMM kernels (conv_gemm, conv_bd, conv_dma) alone: {gemm / a.steps / 1e3:.1f} us")
+          f"Winograd transforms, depthwise): {conv / a.steps / 1e3:.1f} us; implicit-GEMM kernels (conv_gemm, conv_bd, conv_dma, conv_halo, conv_stem) alone: {gemm / a.steps / 1e3:.1f} us")
 
 
 def cmd_traffic(a):
