@@ -178,6 +178,24 @@ def test_conv_dma_1x1(gpu, tile, shape):
     assert_parity(got, oracle_conv(x, w, b, res=res, act=1), f"dma 1x1 tile {tile} {shape}")
 
 
+@pytest.mark.parametrize("tile", [14, 15, 24, 25])
+@pytest.mark.parametrize("shape", [(2, 64, 14, 14, 128), (3, 72, 9, 11, 70), (1, 256, 28, 28, 512)])
+def test_conv_dma_1x1_stride2(gpu, tile, shape):
+    """Stride-2 1x1 (ResNet downsample) on the dense-B kernel: one pixel per copy lane with its
+    unused right neighbour, odd input sizes (the last column's neighbour is the next row's first
+    pixel), residual + ReLU."""
+    N, C, H, W, Cout = shape
+    r = rng(160 + tile + C + H)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, 1, 1)) * 0.1).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    OH, OW = (H - 1) // 2 + 1, (W - 1) // 2 + 1
+    res = round_half(r.standard_normal((N, Cout, OH, OW)))
+    got, plan, _ = gpu_conv(x, w, b, (2, 2), act=1, res=res, algo=V.CONV_GEMM, tile=tile)
+    assert plan.tile == tile
+    assert_parity(got, oracle_conv(x, w, b, (2, 2), res=res, act=1), f"dma 1x1 s2 tile {tile} {shape}")
+
+
 @pytest.mark.parametrize("tile", [11, 14])
 def test_conv_dma_winograd_and_splitk(gpu, tile):
     r = rng(90 + tile)

@@ -843,18 +843,21 @@ namespace vkhip {
     // stage ks computes (one barrier per stage). A fragments read with ds_read_b128, B fragments
     // with two ds_read_b64 (slots 2g and 2g+1 of the lane's pixel), both double buffered across
     // the 16-K steps.
-    template <int FM, int FN, int NS, int WM, int WN>
+    // PS = 16: stride-2 1x1 convs. Each lane copies one output pixel's input pixel (2oy, 2ox)
+    // together with its right neighbour (16 bytes, the neighbour unused), so B columns sit 16 bytes
+    // apart in LDS.
+    template <int FM, int FN, int NS, int WM, int WN, int PS = 8>
     __global__ __launch_bounds__(64 * WM * WN, 1) void conv_dma_kernel(GemmArgs a) {
         constexpr int NW     = WM * WN; // waves
         constexpr int BM     = 32 * FM * WM;
         constexpr int BN     = 32 * FN * WN;
         constexpr int MF     = BM / 32;
         constexpr int ASTAGE = BM * kBK * 2;
-        constexpr int BSTAGE = BN * kBK * 2;
+        constexpr int BSTAGE = BN * kBK * 2 * PS / 8;
         constexpr int NA     = ASTAGE / (NW * 1024);
         constexpr int NB     = BSTAGE / (NW * 1024);
         static_assert(NA >= 1 && NB >= 1 && ASTAGE % (NW * 1024) == 0 && BSTAGE % (NW * 1024) == 0, "stage split");
-        constexpr int BPB    = BN / 128; // 1 KB pixel blocks per slot row of the B stage
+        constexpr int BPB    = BN * PS / 1024; // 1 KB pixel blocks per slot row of the B stage
         __shared__ __attribute__((aligned(16))) unsigned char sm[NS][ASTAGE + BSTAGE];
 
         const int tid  = threadIdx.x;
@@ -889,9 +892,17 @@ namespace vkhip {
         for (int pb = 0; pb < BPB; ++pb) {
             // virtual columns: OHWp per image (the padding column of an odd image reads the next
             // 8 bytes, whatever they hold; its outputs are never stored)
-            const int p = n0 + pb * 128 + 2 * lane;
-            const int n = p / a.OHWp;
-            pbase[pb]   = p < a.Pv ? (unsigned) ((n * a.Cinb * a.HW + (p - n * a.OHWp)) * 8) : kInvalid;
+            if constexpr (PS == 8) {
+                const int p = n0 + pb * 128 + 2 * lane;
+                const int n = p / a.OHWp;
+                pbase[pb]   = p < a.Pv ? (unsigned) ((n * a.Cinb * a.HW + (p - n * a.OHWp)) * 8) : kInvalid;
+            } else {
+                const int p  = n0 + pb * 64 + lane;
+                const int n  = p / a.OHW;
+                const int r  = p - n * a.OHW;
+                const int oy = r / a.OW;
+                pbase[pb]    = p < a.P ? (unsigned) ((n * a.Cinb * a.HW + (a.SH * oy) * a.W + a.SW * (r - oy * a.OW)) * 8) : kInvalid;
+            }
         }
         auto issue = [&](int ks, int buf) __attribute__((always_inline)) {
             unsigned char *dst = sm[buf];
@@ -922,13 +933,13 @@ namespace vkhip {
         const int g = lane >> 5;
         auto compute = [&](int buf, int next_ks, int next_buf) __attribute__((always_inline)) {
             const unsigned char *Ab = sm[buf] + ((wmi * FM) * 64 + lane) * 16;
-            const unsigned char *Bb = sm[buf] + ASTAGE + (2 * g * BN + wn0 + (lane & 31)) * 8;
+            const unsigned char *Bb = sm[buf] + ASTAGE + (2 * g * BN + wn0 + (lane & 31)) * PS;
             half8 fa[2][FM], fb[2][FN];
             auto rd = [&](int kk, int d) __attribute__((always_inline)) {
 #pragma unroll
                 for (int j = 0; j < FN; ++j) {
-                    const u32x2 lo = *reinterpret_cast<const u32x2 *>(Bb + (kk * 4 * BN + 32 * j) * 8);
-                    const u32x2 hi = *reinterpret_cast<const u32x2 *>(Bb + ((kk * 4 + 1) * BN + 32 * j) * 8);
+                    const u32x2 lo = *reinterpret_cast<const u32x2 *>(Bb + (kk * 4 * BN + 32 * j) * PS);
+                    const u32x2 hi = *reinterpret_cast<const u32x2 *>(Bb + ((kk * 4 + 1) * BN + 32 * j) * PS);
                     fb[d][j] = __builtin_bit_cast(half8, u32x4_make(lo.x, lo.y, hi.x, hi.y));
                 }
 #pragma unroll
@@ -1745,12 +1756,22 @@ namespace vkhip {
 
     // conv_dma_kernel with its LDS ring cut to the number of K stages one split runs (fewer stages
     // need no deeper ring; the smaller LDS footprint lets more workgroups share a CU).
-    template <int FM, int FN, int NS, int WM, int WN>
-    static GemmKernelFn pick_dma(int steps) {
+    template <int FM, int FN, int NS, int WM, int WN, int PS = 8>
+    static GemmKernelFn pick_dma_ps(int steps) {
         if constexpr (NS > 1) {
-            if (steps < NS) return pick_dma<FM, FN, NS - 1, WM, WN>(steps);
+            if (steps < NS) return pick_dma_ps<FM, FN, NS - 1, WM, WN, PS>(steps);
         }
-        return conv_dma_kernel<FM, FN, NS, WM, WN>;
+        return conv_dma_kernel<FM, FN, NS, WM, WN, PS>;
+    }
+    // bmode 2 = stride-2 columns (16 bytes per B column)
+    template <int FM, int FN, int NS, int WM, int WN>
+    static GemmKernelFn pick_dma(int steps, int bmode) {
+        constexpr int lds16 = NS * (32 * FM * WM + 2 * 32 * FN * WN) * kBK * 2; // LDS of the 16-byte-column variant
+        if (bmode == 2) {
+            if constexpr (lds16 <= 160 * 1024) return pick_dma_ps<FM, FN, NS, WM, WN, 16>(steps);
+            else return nullptr;
+        }
+        return pick_dma_ps<FM, FN, NS, WM, WN, 8>(steps);
     }
 
     // the smallest band-size instantiation (NBIS ascending) that holds nbi chunks per slot
@@ -1782,12 +1803,12 @@ namespace vkhip {
             case 8: return pick_bd<4, 2, 1, 4, 1>(bmode);
             case 9: return pick_bd<2, 2, 2, 2, 1>(bmode);
             case 10: return pick_bd<2, 2, 1, 4, 1>(bmode);
-            case 11: return pick_dma<4, 4, 2, 2, 2>(steps);
-            case 12: return pick_dma<4, 2, 2, 2, 4>(steps);
-            case 13: return pick_dma<2, 4, 2, 4, 2>(steps);
-            case 14: return pick_dma<2, 2, 2, 2, 2>(steps);
-            case 15: return pick_dma<2, 2, 2, 4, 2>(steps);
-            case 16: return pick_dma<2, 2, 4, 2, 2>(steps);
+            case 11: return pick_dma<4, 4, 2, 2, 2>(steps, bmode);
+            case 12: return pick_dma<4, 2, 2, 2, 4>(steps, bmode);
+            case 13: return pick_dma<2, 4, 2, 4, 2>(steps, bmode);
+            case 14: return pick_dma<2, 2, 2, 2, 2>(steps, bmode);
+            case 15: return pick_dma<2, 2, 2, 4, 2>(steps, bmode);
+            case 16: return pick_dma<2, 2, 4, 2, 2>(steps, bmode);
             case 17: return pick_halo<2, 2, 2, 2, 1, 3, 1, 2, 3, 4>(nbi);
             case 18: return pick_halo<2, 2, 1, 4, 1, 2, 1, 2, 3, 4, 5, 6, 8, 10, 12, 15>(nbi);
             case 19: return pick_halo<2, 4, 2, 2, 1, 2, 2, 3, 4, 5, 6, 8, 10>(nbi);
@@ -1798,8 +1819,8 @@ namespace vkhip {
                 return bmode == 7 ? pick_stem<7, 2, 1, 1, 4, 8, 16, 24, 32, 48>(nbi) : pick_stem<3, 2, 1, 1, 4, 4, 8, 16, 24, 32, 48>(nbi);
             case 23:
                 return bmode == 7 ? pick_stem<7, 1, 2, 1, 4, 8, 16, 24, 32, 48>(nbi) : pick_stem<3, 1, 2, 1, 4, 4, 8, 16, 24, 32, 48>(nbi);
-            case 24: return pick_dma<1, 2, 2, 2, 2>(steps);
-            case 25: return pick_dma<2, 2, 2, 1, 4>(steps);
+            case 24: return pick_dma<1, 2, 2, 2, 2>(steps, bmode);
+            case 25: return pick_dma<2, 2, 2, 1, 4>(steps, bmode);
         }
         return nullptr;
     }
@@ -1817,7 +1838,9 @@ namespace vkhip {
     // image gets one padding column per image (gemm_geom).
     static bool dma_eligible(const vkhip_conv_desc *d, bool wino) {
         if (wino) return true;
-        return d->KH == 1 && d->KW == 1 && d->SH == 1 && d->SW == 1 && d->PT == 0 && d->PL == 0 && d->OH == d->H && d->OW == d->W;
+        const int S = d->SH;
+        return d->KH == 1 && d->KW == 1 && (S == 1 || S == 2) && d->SW == S && d->PT == 0 && d->PL == 0 && d->OH == (d->H - 1) / S + 1 &&
+               d->OW == (d->W - 1) / S + 1;
     }
 
     // conv_halo_kernel: 3x3, stride 1 or 2 (both axes), pad 1, dilation 1, output (H - 1)/S + 1,
@@ -1911,7 +1934,8 @@ namespace vkhip {
         g.m_tiles = ceil_div(g.Coutb * 4, t.BM);
         g.Coutp   = g.m_tiles * t.BM;
         g.HWp     = wino ? g.P : (int64_t) d->OH * d->OW;
-        if (t.kind == 2) g.HWp += g.HWp & 1;
+        if (t.kind == 2 && !wino && d->SH == 2) g.bmode = 2; // stride-2 columns: one pixel per lane, no pairing
+        else if (t.kind == 2) g.HWp += g.HWp & 1;
         g.Pv      = wino ? g.HWp : (int64_t) d->N * g.HWp;
         g.n_tiles = ceil_div(g.Pv, t.BN);
         return g;
@@ -2011,6 +2035,8 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
                          16 * kTiles[tile].KK);
     if (kTiles[tile].kind == 4 && (wino || !stem_shape_ok(d) || stem_nbi(d, kTiles[tile]) > kHaloMaxNBI[tile]))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a 3x3/7x7 stride-1/2 pad-K/2 conv over at most 4 channels with even W", tile);
+    if (kTiles[tile].kind == 2 && dma_eligible(d, wino) && !gemm_kernel_for(tile, gemm_geom(d, tile, wino).bmode, 1))
+        return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d has no stride-2 variant (LDS)", tile);
     if (kTiles[tile].kind == 2 && !dma_eligible(d, wino))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a dense B operand (1x1 stride 1 with an even pixel count, or Winograd)", tile);
     ConvGeom g = gemm_geom(d, tile, wino);
