@@ -200,6 +200,8 @@ def main():
         dops, dplan = profile_ops("mobilenetv3_large", args.dw_batch, xd, "")
         kinds = {ln.split()[0]: ln.split()[1] for ln in dplan.splitlines() if len(ln.split()) > 1}
         dw = [o for o in dops if kinds.get(o["name"]) == "[dwconv]" and o["bytes"] > 0]
+        with open(os.path.join(ROOT, "gpurun_out", "bench_dw_ops.json") if os.path.isdir(os.path.join(ROOT, "gpurun_out")) else os.devnull, "w") as f:
+            json.dump({"ops": dops, "plan": dplan}, f, indent=1)
         if dw:
             b_ms = sum(o["gpu_ms"] for o in dw)
             b_bytes = sum(o["bytes"] for o in dw)

@@ -1454,11 +1454,11 @@ namespace vkhip {
     }
 
     // ------------------------------------------------------------------ depthwise
-    // Thread = (n, cb, oy, OXT consecutive ox) of one 4-channel block; fp32 weights [Cb][KH][KW][4]
+    // Thread = (n, cb, oy, OXT consecutive ox) of one 4-channel block; fp16 weights [Cb][KH][KW][4]
     // and bias [Cb*4]. Reference semantics: ConvCpu with group == C (conv.cpp:40-80).
     struct DwArgs {
         const uint2 *x;
-        const float *w;
+        const half4 *w;    // fp16 weights [Cb][KH][KW] x 4 channels
         const float *bias;
         const uint2 *res;
         uint2       *y;
@@ -1492,7 +1492,7 @@ namespace vkhip {
 #pragma unroll
         for (int o = 0; o < OXT; ++o) acc[o] = b;
         const uint2 *src = a.x + ((long long) n * a.Cb + cb) * a.H * a.W;
-        const float4v *wv = reinterpret_cast<const float4v *>(a.w) + (long long) cb * kh * kw;
+        const half4 *wv = a.w + (long long) cb * kh * kw;
         const int iy0 = oy * sh - a.PT;
         const int ix0 = ox0 * sw - a.PL;
         for (int ky = 0; ky < kh; ++ky) {
@@ -1510,13 +1510,13 @@ namespace vkhip {
                 }
 #pragma unroll
                 for (int kx = 0; kx < KW; ++kx) {
-                    float4v wk = wv[ky * KW + kx];
+                    float4v wk = h4_to_f4(wv[ky * KW + kx]);
 #pragma unroll
                     for (int o = 0; o < OXT; ++o) acc[o] += seg[o * S + kx] * wk;
                 }
             } else {
                 for (int kx = 0; kx < kw; ++kx) {
-                    float4v wk = wv[ky * kw + kx];
+                    float4v wk = h4_to_f4(wv[ky * kw + kx]);
 #pragma unroll
                     for (int o = 0; o < OXT; ++o) {
                         int ix = ix0 + o * sw + kx * dw;
@@ -1574,50 +1574,62 @@ namespace vkhip {
         const int iy0 = oy0 * S - a.PT;
         const int IWp = t.IWp, PLA = t.PLA;
 
-        // input rows -> LDS: each thread keeps one column and steps down the rows (plane-major)
+        // The thread's output column and plane; its weights and bias are loaded first so their
+        // latency overlaps the input copy.
+        const int OW = a.OW;
+        const int ox = tid % OW;
+        const int pl = tid / OW;
+        const int p  = p0 + min(pl, np - 1);
+        const int cb = p % a.Cb;
+        // weights stored and held as fp16 (the storage precision of every GPU weight on this path):
+        // half the registers of fp32, and v_fma_mix takes fp16 x fp16 products into the fp32 sums
+        half4 w[KH * KW];
+#pragma unroll
+        for (int k = 0; k < KH * KW; ++k) w[k] = a.w[(long long) cb * KH * KW + k];
+        const float4v b0 = *reinterpret_cast<const float4v *>(a.bias + cb * 4);
+
+        // input rows -> LDS: each thread keeps one column and steps down the rows (plane-major),
+        // U rows per round with all U loads issued before any LDS write, so a round costs one
+        // memory latency instead of U (most tiles need a single round)
         const int W = a.W, H = a.H;
         const bool v16 = (W % 2 == 0) && (PLA % 2 == 0);
         {
-            const int cols = v16 ? IWp / 2 : IWp; // 16- or 8-byte units per LDS row
-            const int rpp  = 256 / cols;
-            const int col  = tid % cols;
-            const int ix   = (v16 ? 2 * col : col) - PLA;
-            const bool cok = ix >= 0 && ix < W;
-            int r2 = tid / cols;
+            constexpr int U = 16;
+            const int cols  = v16 ? IWp / 2 : IWp; // 16- or 8-byte units per LDS row
+            const int rpp   = 256 / cols;
+            const int col   = tid % cols;
+            const int ix    = (v16 ? 2 * col : col) - PLA;
+            const bool cok  = ix >= 0 && ix < W;
+            const int rows  = np * IR;
+            const int r2    = tid / cols;
             if (r2 < rpp) {
-                int pl = r2 / IR, r = r2 - pl * IR;
-                while (pl < np) {
-                    const int  iy = iy0 + r;
-                    const bool ok = cok && (unsigned) iy < (unsigned) H;
-                    const long long gi = ((long long) (p0 + pl) * H + iy) * W + ix;
-                    if (v16) {
-                        u32x4 v = u32x4_make(0u, 0u, 0u, 0u);
-                        if (ok) v = *reinterpret_cast<const u32x4 *>(a.x + gi);
-                        reinterpret_cast<u32x4 *>(tile)[(pl * IR + r) * cols + col] = v;
-                    } else {
-                        uint2 v = make_uint2(0u, 0u);
-                        if (ok) v = a.x[gi];
-                        tile[(pl * IR + r) * IWp + col] = v;
+                auto copy = [&](auto vec_c) __attribute__((always_inline)) {
+                    using T = decltype(vec_c);
+                    for (int base = r2; base < rows; base += U * rpp) {
+                        T v[U];
+#pragma unroll
+                        for (int u = 0; u < U; ++u) {
+                            const int  row = base + u * rpp;
+                            const int  pl  = row / IR, r = row - pl * IR; // IR is a compile-time constant
+                            const int  iy  = iy0 + r;
+                            const bool ok  = row < rows && cok && (unsigned) iy < (unsigned) H;
+                            v[u] = T {};
+                            if (ok) v[u] = *reinterpret_cast<const T *>(a.x + ((long long) (p0 + pl) * H + iy) * W + ix);
+                        }
+#pragma unroll
+                        for (int u = 0; u < U; ++u) {
+                            const int row = base + u * rpp;
+                            if (row < rows) reinterpret_cast<T *>(tile)[row * cols + col] = v[u];
+                        }
                     }
-                    r += rpp;
-                    while (r >= IR) { r -= IR; ++pl; }
-                }
+                };
+                if (v16) copy(u32x4 {});
+                else copy(u32x2 {});
             }
         }
         __syncthreads();
 
-        const int OW = a.OW;
-        const int ox = tid % OW;
-        const int pl = tid / OW;
         if (pl >= np) return;
-        const int p  = p0 + pl;
-        const int cb = p % a.Cb;
-        // weights held as fp16 (the storage precision of every GPU weight on this path): half the
-        // registers of fp32, and v_fma_mix takes fp16 x fp16 products into the fp32 sums
-        half4 w[KH * KW];
-#pragma unroll
-        for (int k = 0; k < KH * KW; ++k) w[k] = f4_to_h4(reinterpret_cast<const float4v *>(a.w)[(long long) cb * KH * KW + k]);
-        const float4v b0 = *reinterpret_cast<const float4v *>(a.bias + cb * 4);
         float4v acc[RT];
 #pragma unroll
         for (int r = 0; r < RT; ++r) acc[r] = b0;
@@ -2015,7 +2027,7 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
             return set_error(VKHIP_ERR_INVALID, "depthwise conv only runs the depthwise algorithm");
         int64_t Cb         = ceil_div(d->Cin, 4);
         plan->algo         = VKHIP_CONV_DEPTHWISE;
-        plan->weight_bytes = align256((size_t) Cb * 4 * 4) + (size_t) Cb * d->KH * d->KW * 16;
+        plan->weight_bytes = align256((size_t) Cb * 4 * 4) + (size_t) Cb * d->KH * d->KW * 8;
         return VKHIP_OK;
     }
     if (d->group != 1) return set_error(VKHIP_ERR_UNSUPPORTED, "grouped conv");
@@ -2067,12 +2079,12 @@ int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
     if (plan->algo == VKHIP_CONV_DEPTHWISE) {
         int64_t Cb = ceil_div(d->Cin, 4);
         float  *b  = (float *) blob;
-        float  *wp = (float *) ((char *) blob + align256((size_t) Cb * 16));
+        half_t *wp = (half_t *) ((char *) blob + align256((size_t) Cb * 16));
         for (int c = 0; c < d->Cin; ++c) {
             if (bias) b[c] = bias[c];
             for (int ky = 0; ky < d->KH; ++ky)
                 for (int kx = 0; kx < d->KW; ++kx)
-                    wp[(((int64_t) (c / 4) * d->KH + ky) * d->KW + kx) * 4 + c % 4] = w[((int64_t) c * d->KH + ky) * d->KW + kx];
+                    wp[(((int64_t) (c / 4) * d->KH + ky) * d->KW + kx) * 4 + c % 4] = (half_t) w[((int64_t) c * d->KH + ky) * d->KW + kx];
         }
         return VKHIP_OK;
     }
@@ -2122,7 +2134,7 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
         int64_t Cb = ceil_div(d->Cin, 4);
         a.x = (const uint2 *) x;
         a.bias = (const float *) blob;
-        a.w = (const float *) ((const char *) blob + align256((size_t) Cb * 16));
+        a.w = (const half4 *) ((const char *) blob + align256((size_t) Cb * 16));
         a.res = (const uint2 *) res;
         a.y = (uint2 *) y;
         a.N = d->N; a.Cb = (int) Cb; a.C = d->Cin; a.H = d->H; a.W = d->W; a.OH = d->OH; a.OW = d->OW;
