@@ -200,13 +200,23 @@ namespace vknn {
                     }
                     sets.push_back(t);
                 }
+                // two rounds: every candidate briefly, then the four fastest again with more
+                // repetitions, so near-ties are decided on a steadier measurement
+                std::vector<std::pair<double, std::array<int32_t, 3>>> timed;
                 for (auto &c: cands) {
                     vkhip_conv_plan p;
                     if (vkhip_conv_plan_make(&d, c[0], c[1], c[2], &p)) continue;
-                    double ms = timePlan(p, w, b, sets);
+                    timed.push_back({timePlan(p, w, b, sets, 2), {p.algo, p.tile, p.ksplit}});
+                }
+                std::sort(timed.begin(), timed.end(), [](const auto &x, const auto &y) { return x.first < y.first; });
+                for (size_t i = 0; i < timed.size() && i < 4; ++i) {
+                    vkhip_conv_plan p;
+                    const auto &c = timed[i].second;
+                    if (vkhip_conv_plan_make(&d, c[0], c[1], c[2], &p)) continue;
+                    const double ms = std::min(timed[i].first, timePlan(p, w, b, sets, 6));
                     if (ms < best) {
                         best = ms;
-                        pick = {p.algo, p.tile, p.ksplit};
+                        pick = c;
                     }
                 }
                 bestDirect = best;
@@ -217,7 +227,7 @@ namespace vknn {
                     for (int t: {-1, 8, 10, 14, 12, 16}) {
                         vkhip_conv_plan p;
                         if (vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, t, 0, &p)) continue;
-                        double ms = timePlan(p, w, b, sets);
+                        double ms = timePlan(p, w, b, sets, 6);
                         if (ms < bestWino) {
                             bestWino = ms;
                             wpick    = {p.algo, p.tile, p.ksplit};
@@ -239,8 +249,8 @@ namespace vknn {
                 std::shared_ptr<DevBuf> x, y, r;
             };
 
-            // min over 3 timings of 6 back-to-back launches, each on the next buffer set
-            double timePlan(const vkhip_conv_plan &p, const float *w, const float *b, const std::vector<TuneSet> &sets) {
+            // min over reps timings of 6 back-to-back launches, each on the next buffer set
+            double timePlan(const vkhip_conv_plan &p, const float *w, const float *b, const std::vector<TuneSet> &sets, int reps) {
                 std::vector<uint8_t> host(p.weight_bytes);
                 if (vkhip_conv_pack_weights(&d, &p, w, b, host.data())) return 1e30;
                 auto   bl  = upload(host.data(), host.size());
@@ -255,7 +265,7 @@ namespace vknn {
                 check(vkhip_event_create(&e1), "event");
                 double best = 1e30;
                 if (run() == VKHIP_OK) {
-                    for (int r = 0; r < 3; ++r) {
+                    for (int r = 0; r < reps; ++r) {
                         vkhip_event_record(e0, nullptr);
                         for (int i = 0; i < 6; ++i) run();
                         vkhip_event_record(e1, nullptr);

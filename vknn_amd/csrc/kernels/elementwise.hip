@@ -25,18 +25,20 @@ namespace vkhip {
     }
 
     // NCHW fp32 -> NC4HW4 fp16; thread = one (n, cb, pixel) 4-lane vector.
-    __global__ void pack_kernel(const float *src, uint2 *dst, int64_t C, int64_t HW, int64_t Cb, int64_t total) {
-        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    // I = 32-bit indices when the tensor allows them (64-bit division costs ~10x a 32-bit one)
+    template <typename I>
+    __global__ void pack_kernel(const float *src, uint2 *dst, I C, I HW, I Cb, I total) {
+        I i = (I) blockIdx.x * blockDim.x + threadIdx.x;
         if (i >= total) return;
-        int64_t p  = i % HW;
-        int64_t t  = i / HW;
-        int64_t cb = t % Cb;
-        int64_t n  = t / Cb;
+        I p  = i % HW;
+        I t  = i / HW;
+        I cb = t % Cb;
+        I n  = t / Cb;
         uint16_t h[4];
 #pragma unroll
         for (int l = 0; l < 4; ++l) {
-            int64_t c = cb * 4 + l;
-            h[l]      = c < C ? ref_float_to_half(src[(n * C + c) * HW + p]) : (uint16_t) 0;
+            I c  = cb * 4 + l;
+            h[l] = c < C ? ref_float_to_half(src[(n * C + c) * HW + p]) : (uint16_t) 0;
         }
         dst[i] = make_uint2((uint32_t) h[0] | ((uint32_t) h[1] << 16), (uint32_t) h[2] | ((uint32_t) h[3] << 16));
     }
@@ -191,14 +193,15 @@ namespace vkhip {
     }
 
     // Max pool over NC4HW4; out-of-image taps are skipped (reference maxpool.cpp semantics).
-    __global__ void maxpool_kernel(vkhip_pool_desc d, const uint2 *x, uint2 *y, int64_t total) {
-        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    template <typename I>
+    __global__ void maxpool_kernel(vkhip_pool_desc d, const uint2 *x, uint2 *y, I total) {
+        I i = (I) blockIdx.x * blockDim.x + threadIdx.x;
         if (i >= total) return;
-        int     ox = (int) (i % d.OW);
-        int64_t t  = i / d.OW;
-        int     oy = (int) (t % d.OH);
-        int64_t nc = t / d.OH;
-        const uint2 *src = x + nc * d.H * d.W;
+        int ox = (int) (i % (I) d.OW);
+        I   t  = i / (I) d.OW;
+        int oy = (int) (t % (I) d.OH);
+        I   nc = t / (I) d.OH;
+        const uint2 *src = x + (int64_t) nc * d.H * d.W;
         float4v m = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
         for (int ky = 0; ky < d.KH; ++ky) {
             int iy = oy * d.SH - d.PT + ky;
@@ -272,7 +275,10 @@ extern "C" {
 int vkhip_pack_nchw_f32(const float *src, void *dst, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s) {
     if (!src || !dst || N <= 0 || C <= 0 || H <= 0 || W <= 0) return set_error(VKHIP_ERR_INVALID, "pack: bad arguments");
     int64_t Cb = ceil_div(C, 4), total = N * Cb * H * W;
-    pack_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>(src, (uint2 *) dst, C, H * W, Cb, total);
+    if (total * 4 < INT32_MAX && N * Cb * 4 * H * W < INT32_MAX)
+        pack_kernel<int><<<grid1(total), 256, 0, resolve_stream(s)>>>(src, (uint2 *) dst, (int) C, (int) (H * W), (int) Cb, (int) total);
+    else
+        pack_kernel<int64_t><<<grid1(total), 256, 0, resolve_stream(s)>>>(src, (uint2 *) dst, C, H * W, Cb, total);
     return check_launch("pack");
 }
 
@@ -361,7 +367,10 @@ int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream
     if (!d || !x || !y || d->N <= 0 || d->C <= 0 || d->OH <= 0 || d->OW <= 0 || d->KH <= 0 || d->KW <= 0 || d->SH <= 0 || d->SW <= 0)
         return set_error(VKHIP_ERR_INVALID, "maxpool: bad arguments");
     int64_t total = (int64_t) d->N * ceil_div(d->C, 4) * d->OH * d->OW;
-    maxpool_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>(*d, (const uint2 *) x, (uint2 *) y, total);
+    if ((int64_t) d->N * ceil_div(d->C, 4) * d->H * d->W < INT32_MAX)
+        maxpool_kernel<int><<<grid1(total), 256, 0, resolve_stream(s)>>>(*d, (const uint2 *) x, (uint2 *) y, (int) total);
+    else
+        maxpool_kernel<int64_t><<<grid1(total), 256, 0, resolve_stream(s)>>>(*d, (const uint2 *) x, (uint2 *) y, total);
     return check_launch("maxpool");
 }
 
