@@ -57,10 +57,12 @@ def time_steps(sess, steps, warmup):
     return wall, ms.value / 1e3
 
 
-def profile_ops(model, batch, x_dev, options="", reps=3):
-    """Per-op device times (HIP events around each op's launches on the segment stream)."""
+def profile_ops(model, batch, x_dev, options="", reps=3, launches=5):
+    """Per-op device times: HIP events on the segment stream around `launches` back-to-back
+    launches of each op (their average; one launch per event pair would add the event overhead,
+    several microseconds, to every short kernel)."""
     import vknn_amd as V
-    sess = V.Session(model, batch, seed=7, options=(options + ";profile=1").lstrip(";"))
+    sess = V.Session(model, batch, seed=7, options=(options + f";profile=1;profile_reps={launches}").lstrip(";"))
     sess.bind_device_input(x_dev.ptr)
     sess.run_device()
     sess.sync()
@@ -170,6 +172,12 @@ def main():
     roof = None
     if not args.no_profile:
         ops, plan = profile_ops(args.model, args.batch, x_dev, args.options)
+        # Per-op times come from back-to-back replays of each op (warmer caches, no gaps); scale
+        # them so they add up to the measured graph step, i.e. every op's share of the real pass.
+        scale = ms_step / sum(o["gpu_ms"] for o in ops)
+        for o in ops:
+            o["replay_ms"] = o["gpu_ms"]
+            o["gpu_ms"] = o["gpu_ms"] * scale
         conv = [o for o in ops if o["type"] in ("Conv", "Gemm", "FusedDwPw") and o["flops"] > 0]
         conv_ms = sum(o["gpu_ms"] for o in conv)
         conv_fl = sum(o["flops"] for o in conv)
@@ -189,7 +197,8 @@ def main():
             b_bytes = sum(o["bytes"] for o in one)
             extra["hbm_bound_convs"] = {"count": len(one), "achieved_GBs": round(b_bytes / (b_ms * 1e-3) / 1e9, 1),
                                         "peak_GBs": PEAK_HBM_GBS, "frac": round(b_bytes / (b_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
-        extra["op_time_share"] = {"conv_ms": round(conv_ms, 4), "all_ops_ms": round(all_ms, 4)}
+        extra["op_time_share"] = {"conv_ms": round(conv_ms, 4), "all_ops_ms": round(all_ms, 4),
+                                  "replay_to_step_scale": round(scale, 4)}
         with open(os.path.join(ROOT, "gpurun_out", "bench_ops.json") if os.path.isdir(os.path.join(ROOT, "gpurun_out")) else os.devnull, "w") as f:
             json.dump({"ops": ops, "plan": plan}, f, indent=1)
 
@@ -198,6 +207,14 @@ def main():
         xs, _ = V.model_io("mobilenetv3_large", args.dw_batch)
         xd = V.DeviceBuffer.from_array(np.random.default_rng(1).standard_normal(xs).astype(np.float32))
         dops, dplan = profile_ops("mobilenetv3_large", args.dw_batch, xd, "")
+        ds = V.Session("mobilenetv3_large", args.dw_batch, seed=7)
+        ds.bind_device_input(xd.ptr)
+        dwall, _ = time_steps(ds, 10, 3)
+        ds.close()
+        dscale = dwall / 10 * 1e3 / sum(o["gpu_ms"] for o in dops)
+        for o in dops:
+            o["replay_ms"] = o["gpu_ms"]
+            o["gpu_ms"] = o["gpu_ms"] * dscale
         kinds = {ln.split()[0]: ln.split()[1] for ln in dplan.splitlines() if len(ln.split()) > 1}
         dw = [o for o in dops if kinds.get(o["name"]) == "[dwconv]" and o["bytes"] > 0]
         with open(os.path.join(ROOT, "gpurun_out", "bench_dw_ops.json") if os.path.isdir(os.path.join(ROOT, "gpurun_out")) else os.devnull, "w") as f:
@@ -208,7 +225,8 @@ def main():
             extra["depthwise"] = {"workload": f"mobilenetv3_large b{args.dw_batch}, {len(dw)} depthwise 3x3/5x5 convs",
                                   "achieved_GBs": round(b_bytes / (b_ms * 1e-3) / 1e9, 1), "peak_GBs": PEAK_HBM_GBS,
                                   "frac": round(b_bytes / (b_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                                  "launch_ms": round(b_ms, 4), "bytes_per_step": b_bytes}
+                                  "launch_ms": round(b_ms, 4), "bytes_per_step": b_bytes,
+                                  "replay_to_step_scale": round(dscale, 4)}
         xd.close()
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.model)

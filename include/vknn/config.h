@@ -63,6 +63,9 @@ namespace vknn {
         // HIP backend: capture each segment's launch sequence into a HIP graph after the first run
         // and replay it (the analogue of the reference's pre-recorded command buffer).
         bool hipGraphs = true;
+        // HIP backend, profiling only: launches per op between its two timing events (the op's
+        // time is their average; amortizes the event overhead on short kernels).
+        int profileReps = 1;
         // Fusion passes the reference exposes only as compiler flags (passes.h:33-40).
         bool fuseDwPw          = false;
         bool fuseSqueezeExcite = false;

@@ -4,6 +4,8 @@
 #include "model_zoo.h"
 #include "vknn/session.h"
 #include <cstring>
+#include <algorithm>
+#include <cstdlib>
 #include <sstream>
 #include <string>
 
@@ -39,6 +41,7 @@ namespace {
                 else if (k == "tuning") cfg.setHint(Hint::Tuning, tuningFromStr(v));
                 else if (k == "graphs") cfg.hipGraphs = v != "0";
                 else if (k == "profile") cfg.profile = v != "0";
+                else if (k == "profile_reps") cfg.profileReps = std::max(1, std::atoi(v.c_str()));
                 else if (k == "fuse_dwpw") cfg.fuseDwPw = v != "0";
                 else if (k == "fuse_se") cfg.fuseSqueezeExcite = v != "0";
             }

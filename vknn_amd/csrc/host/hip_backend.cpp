@@ -688,7 +688,7 @@ namespace vknn {
             }
             for (size_t k = 0; k < ops_.size(); ++k) {
                 if (timed) vkhip_event_record(events_[2 * k], stream_);
-                ops_[k]->record(env_, stream_);
+                for (int r = 0; r < (timed ? cfg_.profileReps : 1); ++r) ops_[k]->record(env_, stream_);
                 if (timed) vkhip_event_record(events_[2 * k + 1], stream_);
             }
             for (TensorId t: boundaryOutputs) {
@@ -759,7 +759,7 @@ namespace vknn {
                     r.backend = "HIP";
                     float ms  = 0;
                     vkhip_event_elapsed_ms(events_[2 * k], events_[2 * k + 1], &ms);
-                    r.gpuMs   = ms;
+                    r.gpuMs   = ms / cfg_.profileReps;
                     r.flops   = ops_[k]->flops;
                     r.bytesIO = ops_[k]->bytes;
                     r.cpuMs   = std::chrono::duration<double, std::milli>(t1 - t0).count() / (double) ops_.size();
