@@ -136,22 +136,25 @@ namespace vkhip {
         y[i]       = h4_as_u2(f4_to_h4(v * sc));
     }
 
-    // One wave per (n, cb): mean over HW pixels of 4 channels (fp32 sums).
-    __global__ void gap_kernel(const uint2 *x, uint2 *y, int64_t NCb, int64_t HW) {
-        int64_t w    = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-        int     lane = threadIdx.x & 63;
-        if (w >= NCb) return;
-        const uint2 *src = x + w * HW;
-        float4v      s   = {0.f, 0.f, 0.f, 0.f};
-        for (int64_t p = lane; p < HW; p += 64) s += h4_to_f4(u2_as_h4(src[p]));
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
+    // L lanes per (n, cb) plane (L a power of two from 8 to 64, about one lane per 8 pixels): mean
+    // over HW pixels of 4 channels (fp32 sums), lane partials reduced with shuffles. Small planes
+    // (7x7 before a classifier) would leave most of a full wave idle.
+    __global__ void gap_kernel(const uint2 *x, uint2 *y, int64_t NCb, int64_t HW, int L) {
+        const int64_t t    = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+        const int64_t w    = t / L;
+        const int     lane = (int) (t % L);
+        float4v       s    = {0.f, 0.f, 0.f, 0.f};
+        if (w < NCb) {
+            const uint2 *src = x + w * HW;
+            for (int64_t p = lane; p < HW; p += L) s += h4_to_f4(u2_as_h4(src[p]));
+        }
+        for (int off = L >> 1; off > 0; off >>= 1) {
             s.x += __shfl_xor(s.x, off);
             s.y += __shfl_xor(s.y, off);
             s.z += __shfl_xor(s.z, off);
             s.w += __shfl_xor(s.w, off);
         }
-        if (lane == 0) y[w] = h4_as_u2(f4_to_h4(s / (float) HW));
+        if (w < NCb && lane == 0) y[w] = h4_as_u2(f4_to_h4(s / (float) HW));
     }
 
     // Fused SE middle, one workgroup per image: s1 = relu(W1 avg + b1); s = clamp(alpha*(W2 s1 +
@@ -336,7 +339,9 @@ int vkhip_channel_scale(const void *x, const void *scale, void *y, int64_t N, in
 int vkhip_global_avg_pool(const void *x, void *y, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s) {
     if (!x || !y || N <= 0 || C <= 0 || H <= 0 || W <= 0) return set_error(VKHIP_ERR_INVALID, "gap: bad arguments");
     int64_t NCb = N * ceil_div(C, 4);
-    gap_kernel<<<grid1(NCb * 64), 256, 0, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, NCb, H * W);
+    int L = 8;
+    while (L < 64 && L * 8 < H * W) L <<= 1;
+    gap_kernel<<<grid1(NCb * L), 256, 0, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, NCb, H * W, L);
     return check_launch("global_avg_pool");
 }
 
