@@ -123,7 +123,7 @@ BD_TILES = [8, 9, 10]            # conv_bd_kernel tiles (A via LDS DMA, B gather
 DMA_TILES = [11, 12, 13, 14, 15, 16, 24, 25]     # conv_dma_kernel tiles (A and B via LDS DMA; dense B only)
 HALO_TILES = [17, 18, 19, 20]         # conv_halo_kernel tiles (3x3 s1 p1: input band staged once for all taps)
 STEM_TILES = [21, 22, 23]                 # conv_stem_kernel tiles (3x3/7x7 over at most 4 input channels)
-GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES + HALO_TILES + STEM_TILES + [26]]
+GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES + HALO_TILES + STEM_TILES]
 
 
 @pytest.mark.parametrize("tile", GATHER_TILES)
@@ -176,39 +176,6 @@ def test_conv_dma_1x1(gpu, tile, shape):
     got, plan, _ = gpu_conv(x, w, b, act=1, res=res, algo=V.CONV_GEMM, tile=tile)
     assert plan.tile == tile
     assert_parity(got, oracle_conv(x, w, b, res=res, act=1), f"dma 1x1 tile {tile} {shape}")
-
-
-KG_TILES = [26]   # conv_dma_kernel with two K groups of waves (deep-K 1x1)
-
-
-@pytest.mark.parametrize("tile", KG_TILES)
-@pytest.mark.parametrize("shape", [(2, 512, 14, 14, 256), (1, 300, 7, 9, 70), (3, 256, 5, 6, 40)])
-def test_conv_dma_two_k_groups(gpu, tile, shape):
-    """Two wave groups split the K stages and reduce through LDS: even and odd stage counts (the
-    group with one stage fewer idles through the last barrier), a K tail, odd pixel counts,
-    ragged output channels, residual + ReLU; and split-K on top."""
-    N, C, H, W, Cout = shape
-    r = rng(170 + tile + C)
-    x = round_half(r.standard_normal((N, C, H, W)))
-    w = (r.standard_normal((Cout, C, 1, 1)) * 0.05).astype(np.float32)
-    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
-    res = round_half(r.standard_normal((N, Cout, H, W)))
-    got, plan, _ = gpu_conv(x, w, b, act=1, res=res, algo=V.CONV_GEMM, tile=tile)
-    assert plan.tile == tile
-    ref = oracle_conv(x, w, b, res=res, act=1)
-    assert_parity(got, ref, f"dma K groups tile {tile} {shape}")
-    if C >= 512:
-        got, plan, _ = gpu_conv(x, w, b, act=1, res=res, algo=V.CONV_SPLITK, tile=tile, ksplit=2)
-        assert plan.ksplit == 2
-        assert_parity(got, ref, f"dma K groups split-K tile {tile} {shape}")
-
-
-def test_conv_dma_two_k_groups_rejects_shallow_k(gpu):
-    lib = V.vkhip()
-    plan = V.ConvPlan()
-    d, _ = conv_desc((1, 128, 8, 8), (64, 128, 1, 1))
-    for t in KG_TILES:
-        assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, t, 0, ctypes.byref(plan)) != 0
 
 
 @pytest.mark.parametrize("tile", [14, 15, 24, 25])

@@ -846,13 +846,8 @@ namespace vkhip {
     // PS = 16: stride-2 1x1 convs. Each lane copies one output pixel's input pixel (2oy, 2ox)
     // together with its right neighbour (16 bytes, the neighbour unused), so B columns sit 16 bytes
     // apart in LDS.
-    // KG = 2: two groups of WM x WN waves share the workgroup's tile and split its K stages (first
-    // and second half, each group with its own LDS ring), so every SIMD runs two waves on one
-    // tile; at the end the second group adds its sums into the first through LDS and the first
-    // group runs the epilogue. For deep-K, few-tile GEMMs (1x1 reductions) whose single wave per
-    // SIMD would otherwise sit idle on every copy and barrier.
-    template <int FM, int FN, int NS, int WM, int WN, int PS = 8, int KG = 1>
-    __global__ __launch_bounds__(64 * WM * WN * KG, 1) void conv_dma_kernel(GemmArgs a) {
+    template <int FM, int FN, int NS, int WM, int WN, int PS = 8>
+    __global__ __launch_bounds__(64 * WM * WN, 1) void conv_dma_kernel(GemmArgs a) {
         constexpr int NW     = WM * WN; // waves
         constexpr int BM     = 32 * FM * WM;
         constexpr int BN     = 32 * FN * WN;
@@ -863,18 +858,13 @@ namespace vkhip {
         constexpr int NB     = BSTAGE / (NW * 1024);
         static_assert(NA >= 1 && NB >= 1 && ASTAGE % (NW * 1024) == 0 && BSTAGE % (NW * 1024) == 0, "stage split");
         constexpr int BPB    = BN * PS / 1024; // 1 KB pixel blocks per slot row of the B stage
-        static_assert(KG == 1 || NS >= 2, "K groups need a ring");
-        static_assert(KG == 1 || KG * NS * (ASTAGE + BSTAGE) >= NW * FM * FN * 16 * 64 * 4, "reduction buffer");
-        __shared__ __attribute__((aligned(16))) unsigned char smk[KG][NS][ASTAGE + BSTAGE];
+        __shared__ __attribute__((aligned(16))) unsigned char sm[NS][ASTAGE + BSTAGE];
 
         const int tid  = threadIdx.x;
         const int lane = tid & 63;
-        const int wv   = __builtin_amdgcn_readfirstlane(tid >> 6);
-        const int kg   = wv / NW;       // K group
-        const int wave = wv - kg * NW;  // wave within the group
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const int wmi  = wave / WN;
         const int wni  = wave % WN;
-        unsigned char (*sm)[ASTAGE + BSTAGE] = smk[kg];
 
         const int lin    = xcd_remap(blockIdx.x, gridDim.x);
         const int m_tile = lin % a.m_tiles;
@@ -888,13 +878,10 @@ namespace vkhip {
 
         const uint2         *X  = a.x + bz * a.x_bstride;
         const unsigned char *Wt = reinterpret_cast<const unsigned char *>(a.w + bz * a.w_bstride) + (long long) m_tile * a.nsteps * ASTAGE;
-        const int sp_begin = split * a.steps_per_split;
-        const int sp_end   = min(a.nsteps, sp_begin + a.steps_per_split);
-        const int half     = (sp_end - sp_begin + KG - 1) / KG; // stages per K group (the last may have one fewer)
-        const int ks_begin = min(sp_end, sp_begin + kg * half);
-        const int ks_end   = min(sp_end, ks_begin + half);
+        const int ks_begin = split * a.steps_per_split;
+        const int ks_end   = min(a.nsteps, ks_begin + a.steps_per_split);
         const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *) X, (short) 0, (int) a.x_bytes, 0x00020000);
-        const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *) Wt, (short) 0, sp_end * ASTAGE, 0x00020000);
+        const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *) Wt, (short) 0, ks_end * ASTAGE, 0x00020000);
         constexpr unsigned kInvalid = 0x80000000u;
         const int hw8 = a.HW * 8;
 
@@ -993,41 +980,17 @@ namespace vkhip {
                 __asm__ volatile("s_barrier" ::: "memory");
                 compute(0, -1, 0);
             }
-        } else if (KG > 1 || ks_begin < ks_end) {
+        } else if (ks_begin < ks_end) {
 #pragma unroll
             for (int d = 0; d < NS - 1; ++d)
                 if (ks_begin + d < ks_end) issue(ks_begin + d, d);
-            // every group runs `half` iterations so the workgroup barriers pair up; a group with
-            // fewer stages idles through its last one
-            for (int rel = 0; rel < half; ++rel) {
-                const int  ks  = ks_begin + rel;
-                const bool act = ks < ks_end;
-                if (act && ks + NS - 2 < ks_end) __builtin_amdgcn_s_waitcnt(kWait);
+            for (int ks = ks_begin; ks < ks_end; ++ks) {
+                const int rel = ks - ks_begin;
+                if (ks + NS - 2 < ks_end) __builtin_amdgcn_s_waitcnt(kWait);
                 else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); // tail: nothing later in flight
                 __asm__ volatile("s_barrier" ::: "memory");
-                if (act) compute(rel % NS, ks + NS - 1 < ks_end ? ks + NS - 1 : -1, (rel + NS - 1) % NS);
+                compute(rel % NS, ks + NS - 1 < ks_end ? ks + NS - 1 : -1, (rel + NS - 1) % NS);
             }
-        }
-        if constexpr (KG > 1) {
-            // group 1 hands its sums to group 0 through the (now idle) LDS rings
-            float *red = reinterpret_cast<float *>(&smk[0][0][0]);
-            __syncthreads();
-            if (kg == 1) {
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) red[(((wave * FM + i) * FN + j) * 16 + r) * 64 + lane] = acc[i][j][r];
-            }
-            __syncthreads();
-            if (kg == 1) return;
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[i][j][r] += red[(((wave * FM + i) * FN + j) * 16 + r) * 64 + lane];
         }
         gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, bz, lane);
     }
@@ -1742,8 +1705,8 @@ namespace vkhip {
     // ------------------------------------------------------------------ host side: tiles & plans
     // kind 0: conv_gemm_kernel (A and B staged through LDS), WM x WN waves over a BM x BN tile.
     // kind 1: conv_bd_kernel (A via LDS DMA, B straight into registers), waves of (32FM) x (32FN).
-    // kind 2: conv_dma_kernel (A and B via LDS DMA; dense B only: 1x1 s1/s2, Winograd GEMMs),
-    //         WM x WN waves of (32FM) x (32FN); KK = 2 marks two K groups (twice the waves).
+    // kind 2: conv_dma_kernel (A and B via LDS DMA; dense B only: 1x1 s1 with an even pixel count
+    //         per image, Winograd GEMMs with an even tile count), 2x2 waves of (32FM) x (32FN).
     // kind 3: conv_halo_kernel (3x3 pad-1, stride 1 or 2: input band staged once in LDS for all 9
     //         taps), KK 16-channel K steps per LDS stage.
     // kind 4: conv_stem_kernel (3x3 or 7x7, stride 1 or 2, pad K/2, at most 4 input channels).
@@ -1777,10 +1740,9 @@ namespace vkhip {
         {32, 256, 1, 4, 4, 1, 2},     // 23 stem (few output channels)
         {64, 128, 2, 2, 2, 1, 2},     // 24
         {64, 256, 1, 4, 2, 2, 2},     // 25
-        {128, 128, 2, 2, 2, 2, 2, 2}, // 26 (two K groups: 8 waves)
     };
-    constexpr int kNumTiles = 27;
-    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 0};
+    constexpr int kNumTiles = 26;
+    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
@@ -1822,14 +1784,6 @@ namespace vkhip {
             else return nullptr;
         }
         return pick_dma_ps<FM, FN, NS, WM, WN, 8>(steps);
-    }
-
-    // Two K groups need at least two stages each; shallower splits run the one-group kernel.
-    static inline int dma_kgroups(int kk_field, int steps) { return (kk_field == 2 && steps >= 4) ? 2 : 1; }
-    template <int FM, int FN, int NS, int WM, int WN>
-    static GemmKernelFn pick_dma_kg(int steps, int bmode) {
-        if (dma_kgroups(2, steps) == 1 || bmode == 2) return nullptr;
-        return conv_dma_kernel<FM, FN, NS, WM, WN, 8, 2>;
     }
 
     // the smallest band-size instantiation (NBIS ascending) that holds nbi chunks per slot
@@ -1879,7 +1833,6 @@ namespace vkhip {
                 return bmode == 7 ? pick_stem<7, 1, 2, 1, 4, 8, 16, 24, 32, 48>(nbi) : pick_stem<3, 1, 2, 1, 4, 4, 8, 16, 24, 32, 48>(nbi);
             case 24: return pick_dma<1, 2, 2, 2, 2>(steps, bmode);
             case 25: return pick_dma<2, 2, 2, 1, 4>(steps, bmode);
-            case 26: return pick_dma_kg<2, 2, 2, 2, 2>(steps, bmode);
         }
         return nullptr;
     }
@@ -2094,15 +2047,11 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
                          16 * kTiles[tile].KK);
     if (kTiles[tile].kind == 4 && (wino || !stem_shape_ok(d) || stem_nbi(d, kTiles[tile]) > kHaloMaxNBI[tile]))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a 3x3/7x7 stride-1/2 pad-K/2 conv over at most 4 channels with even W", tile);
-    if (kTiles[tile].kind == 2 && dma_eligible(d, wino) && !gemm_kernel_for(tile, gemm_geom(d, tile, wino).bmode, kTiles[tile].KK == 2 ? 1 << 20 : 1))
+    if (kTiles[tile].kind == 2 && dma_eligible(d, wino) && !gemm_kernel_for(tile, gemm_geom(d, tile, wino).bmode, 1))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d has no stride-2 variant (LDS)", tile);
     if (kTiles[tile].kind == 2 && !dma_eligible(d, wino))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a dense B operand (1x1 stride 1 with an even pixel count, or Winograd)", tile);
     ConvGeom g = gemm_geom(d, tile, wino);
-    if (kTiles[tile].kind == 2 && kTiles[tile].KK == 2) {
-        const int64_t ks = algo == VKHIP_CONV_SPLITK ? std::max<int64_t>(1, std::min<int64_t>(ksplit > 0 ? ksplit : 1, g.nsteps)) : 1;
-        if (ceil_div(g.nsteps, ks) < 4) return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d splits K across two wave groups: needs >= 4 K stages", tile);
-    }
     plan->algo = algo;
     plan->tile = tile;
     size_t wb  = (size_t) g.Coutp * g.Kp * 2;
@@ -2242,7 +2191,6 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     const int split_steps = plan->algo == VKHIP_CONV_SPLITK ? (int) ceil_div(g.nsteps, plan->ksplit) : (int) g.nsteps;
     GemmKernelFn fn = gemm_kernel_for(plan->tile, g.bmode, split_steps, t.kind == 3 ? halo_nbi(d, t) : (t.kind == 4 ? stem_nbi(d, t) : 0));
     if (!fn) return set_error(VKHIP_ERR_INVALID, "conv_forward: no kernel for tile %d", plan->tile);
-    const int threads = 64 * t.WM * t.WN * (t.kind == 2 ? dma_kgroups(t.KK, split_steps) : 1);
 
     if (wino) {
         const int nTH = (int) ceil_div(d->OH, 2), nTW = (int) ceil_div(d->OW, 2);
@@ -2265,7 +2213,7 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
         a.w_bstride = (long long) g.Coutp * g.Kp;
         a.y_bstride = (long long) g.Coutb * nT;
         dim3 grid((unsigned) (g.m_tiles * g.n_tiles), 1, 16);
-        fn<<<grid, threads, 0, st>>>(a);
+        fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
         if ((rc = check_launch("wino_gemm"))) return rc;
         int64_t nout = g.Coutb * nT;
         wino_output_kernel<<<dim3((unsigned) ceil_div(nout, 256)), 256, 0, st>>>(M, a.bias, (uint2 *) y, (int) g.Coutb, d->Cout, d->OH, d->OW,
@@ -2289,7 +2237,7 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
         a.omode = OMODE_PARTIAL;
         a.part  = (float4v *) workspace;
         dim3 grid((unsigned) (g.m_tiles * g.n_tiles), (unsigned) ks, 1);
-        fn<<<grid, threads, 0, st>>>(a);
+        fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
         int rc = check_launch("conv_gemm_splitk");
         if (rc) return rc;
         int64_t total = g.Coutb * g.P;
@@ -2300,7 +2248,7 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     }
     a.omode = OMODE_EPILOGUE;
     dim3 grid((unsigned) (g.m_tiles * g.n_tiles), 1, 1);
-    fn<<<grid, threads, 0, st>>>(a);
+    fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
     return check_launch("conv_gemm");
 }
 
