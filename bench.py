@@ -229,6 +229,26 @@ def main():
                                   "replay_to_step_scale": round(dscale, 4)}
         xd.close()
 
+    # ---- fused dw+pw (config 1: the MobileNetV2 block with the dw+pw fusion pass) at batch 128
+    if not args.no_profile and args.dw_batch > 0:
+        xs, _ = V.model_io("mnv2_block", args.dw_batch)
+        xd = V.DeviceBuffer.from_array(np.random.default_rng(2).standard_normal(xs).astype(np.float32))
+        fops, _ = profile_ops("mnv2_block", args.dw_batch, xd, "fuse_dwpw=1")
+        fs = V.Session("mnv2_block", args.dw_batch, seed=7, options="fuse_dwpw=1")
+        fs.bind_device_input(xd.ptr)
+        fwall, _ = time_steps(fs, 10, 3)
+        fs.close()
+        fscale = fwall / 10 * 1e3 / sum(o["gpu_ms"] for o in fops)
+        fused = [o for o in fops if o["type"] == "FusedDwPw" and o["bytes"] > 0]
+        if fused:
+            f_ms = sum(o["gpu_ms"] for o in fused) * fscale
+            f_bytes = sum(o["bytes"] for o in fused)
+            extra["fused_dwpw"] = {"workload": f"config-1 MobileNetV2 block (24-144-24 @56x56) b{args.dw_batch} (fuse_dwpw=1), {len(fused)} fused dw+pw op(s)",
+                                   "achieved_GBs": round(f_bytes / (f_ms * 1e-3) / 1e9, 1), "peak_GBs": PEAK_HBM_GBS,
+                                   "frac": round(f_bytes / (f_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                                   "launch_ms": round(f_ms, 4), "bytes_per_step": f_bytes, "replay_to_step_scale": round(fscale, 4)}
+        xd.close()
+
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.model)
 
     out = {

@@ -424,7 +424,10 @@ def test_depthwise_dilated_generic(gpu):
 @pytest.mark.parametrize("N,E,H,k,s,Cout,dw_act,act,res", [(2, 144, 14, 3, 1, 24, 2, 0, True),
                                                            (1, 960, 7, 5, 1, 160, 1, 0, False),
                                                            (3, 72, 11, 3, 2, 40, 0, 1, False),
-                                                           (1, 22, 9, 3, 1, 10, 2, 3, True)])
+                                                           (1, 22, 9, 3, 1, 10, 2, 3, True),
+                                                           (2, 144, 56, 3, 1, 24, 2, 0, True),
+                                                           (1, 96, 40, 5, 2, 64, 1, 0, True),
+                                                           (1, 40, 130, 3, 2, 24, 2, 0, False)])
 def test_fused_dwpw(gpu, N, E, H, k, s, Cout, dw_act, act, res):
     lib = V.vkhip()
     r = rng(E + Cout + H)
