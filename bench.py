@@ -233,7 +233,7 @@ def main():
     if not args.no_profile and args.dw_batch > 0:
         xs, _ = V.model_io("mnv2_block", args.dw_batch)
         xd = V.DeviceBuffer.from_array(np.random.default_rng(2).standard_normal(xs).astype(np.float32))
-        fops, _ = profile_ops("mnv2_block", args.dw_batch, xd, "fuse_dwpw=1")
+        fops, fplan = profile_ops("mnv2_block", args.dw_batch, xd, "fuse_dwpw=1")
         fs = V.Session("mnv2_block", args.dw_batch, seed=7, options="fuse_dwpw=1")
         fs.bind_device_input(xd.ptr)
         fwall, _ = time_steps(fs, 10, 3)
@@ -246,7 +246,8 @@ def main():
             extra["fused_dwpw"] = {"workload": f"config-1 MobileNetV2 block (24-144-24 @56x56) b{args.dw_batch} (fuse_dwpw=1), {len(fused)} fused dw+pw op(s)",
                                    "achieved_GBs": round(f_bytes / (f_ms * 1e-3) / 1e9, 1), "peak_GBs": PEAK_HBM_GBS,
                                    "frac": round(f_bytes / (f_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                                   "launch_ms": round(f_ms, 4), "bytes_per_step": f_bytes, "replay_to_step_scale": round(fscale, 4)}
+                                   "launch_ms": round(f_ms, 4), "bytes_per_step": f_bytes, "replay_to_step_scale": round(fscale, 4),
+                                   "execution": [ln for ln in fplan.splitlines() if "[dwpw]" in ln]}
         xd.close()
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.model)

@@ -296,8 +296,14 @@ namespace vknn {
         // ------------------------------------------------------------ fused dw + pw
         struct DwPwOp: HipOp {
             vkhip_dwpw_desc         d {};
-            std::shared_ptr<DevBuf> blob;
+            std::shared_ptr<DevBuf> blob, mid;
             TensorId                in, out, res = kNoTensor;
+            // Either the fused kernel, or the depthwise and projection convs back to back on the
+            // tuned single-op kernels with the E-channel intermediate in HBM: the fused kernel
+            // keeps that intermediate on chip but its depthwise stage is slower than the tiled
+            // depthwise kernel, so prepare() times both on the real shape and keeps the faster.
+            bool                    split = false;
+            ConvOp                  dwc, pwc;
             void prepare(const Node &node, SegEnv &env) override {
                 const Graph &g = *env.graph;
                 in  = node.inputs[0];
@@ -312,18 +318,65 @@ namespace vknn {
                 c.DH = (int) dil[0]; c.DW = (int) dil[1]; c.group = (int) x.c; c.act = node.subOp; c.act_lo = 0; c.act_hi = 6;
                 d.Cout = (int) y.c; d.act = (int) node.fusedAct; d.act_lo = node.actLo; d.act_hi = node.actHi; d.has_res = res != kNoTensor;
                 if (!vkhip_dwpw_supported(&d)) throw Error(Status::Unsupported, "FusedDwPw shape not supported: " + name);
+                const float *dw_w = initF32(g, node.inputs[1]), *dw_b = initF32(g, node.inputs[2]);
+                const float *pw_w = initF32(g, node.inputs[3]), *pw_b = initF32(g, node.inputs[4]);
                 std::vector<uint8_t> host(vkhip_dwpw_weight_bytes(&d));
-                check(vkhip_dwpw_pack_weights(&d, initF32(g, node.inputs[1]), initF32(g, node.inputs[2]), initF32(g, node.inputs[3]),
-                                              initF32(g, node.inputs[4]), host.data()),
-                      "dwpw pack");
+                check(vkhip_dwpw_pack_weights(&d, dw_w, dw_b, pw_w, pw_b, host.data()), "dwpw pack");
                 blob  = upload(host.data(), host.size());
                 kind  = "dwpw";
                 flops = 2.0 * c.N * c.OH * c.OW * ((double) c.Cin * c.KH * c.KW + (double) c.Cin * d.Cout);
                 bytes = (int64_t) (nc4Bytes(g.desc(in).shape) + nc4Bytes(g.desc(out).shape) * (d.has_res ? 2 : 1));
+
+                // the split alternative: depthwise conv (+ its activation), then the 1x1 projection
+                // (+ residual + activation), both planned like standalone convs
+                dwc.d = c;
+                dwc.d.has_res = 0;
+                pwc.d = vkhip_conv_desc {};
+                pwc.d.N = c.N; pwc.d.Cin = c.Cin; pwc.d.H = c.OH; pwc.d.W = c.OW; pwc.d.Cout = d.Cout; pwc.d.OH = c.OH; pwc.d.OW = c.OW;
+                pwc.d.KH = 1; pwc.d.KW = 1; pwc.d.SH = 1; pwc.d.SW = 1; pwc.d.DH = 1; pwc.d.DW = 1; pwc.d.group = 1;
+                pwc.d.act = d.act; pwc.d.act_lo = d.act_lo; pwc.d.act_hi = d.act_hi; pwc.d.has_res = d.has_res;
+                if (!env.tunable) return; // untuned sessions keep the fused kernel
+                dwc.choosePlan(env, dw_w, dw_b);
+                pwc.choosePlan(env, pw_w, pw_b);
+                mid = std::make_shared<DevBuf>(nc4Bytes({c.N, c.Cin, c.OH, c.OW}));
+                auto xb = std::make_shared<DevBuf>(nc4Bytes({c.N, c.Cin, c.H, c.W}));
+                auto yb = std::make_shared<DevBuf>(nc4Bytes({c.N, d.Cout, c.OH, c.OW}));
+                auto rb = d.has_res ? std::make_shared<DevBuf>(nc4Bytes({c.N, d.Cout, c.OH, c.OW})) : nullptr;
+                check(vkhip_fill_zero(xb->ptr, xb->bytes, nullptr), "dwpw tune fill");
+                if (rb) check(vkhip_fill_zero(rb->ptr, rb->bytes, nullptr), "dwpw tune fill");
+                auto timeIt = [&](bool sp) {
+                    vkhip_event_t e0, e1;
+                    check(vkhip_event_create(&e0), "event");
+                    check(vkhip_event_create(&e1), "event");
+                    double best = 1e30;
+                    for (int r = 0; r < 4; ++r) {
+                        vkhip_event_record(e0, nullptr);
+                        for (int k = 0; k < 3; ++k) launch(sp, xb->ptr, rb ? rb->ptr : nullptr, yb->ptr, nullptr);
+                        vkhip_event_record(e1, nullptr);
+                        vkhip_event_sync(e1);
+                        float ms = 0;
+                        vkhip_event_elapsed_ms(e0, e1, &ms);
+                        if (r > 0) best = std::min(best, (double) ms); // first round warms up
+                    }
+                    vkhip_event_destroy(e0);
+                    vkhip_event_destroy(e1);
+                    return best;
+                };
+                split = timeIt(true) < timeIt(false);
+                if (!split) mid.reset();
+            }
+            void launch(bool sp, const void *x, const void *r, void *y, vkhip_stream_t s) {
+                if (!sp) {
+                    check(vkhip_dwpw_forward(&d, x, blob->ptr, r, y, s), "dwpw " + name);
+                    return;
+                }
+                check(vkhip_conv_forward(&dwc.d, &dwc.plan, x, dwc.blob->ptr, nullptr, mid->ptr, dwc.ws ? dwc.ws->ptr : nullptr, s), "dwpw dw " + name);
+                check(vkhip_conv_forward(&pwc.d, &pwc.plan, mid->ptr, pwc.blob->ptr, r, y, pwc.ws ? pwc.ws->ptr : nullptr, s), "dwpw pw " + name);
             }
             void record(SegEnv &env, vkhip_stream_t s) override {
-                check(vkhip_dwpw_forward(&d, env.dev(in), blob->ptr, res != kNoTensor ? env.dev(res) : nullptr, env.dev(out), s), "dwpw " + name);
+                launch(split, env.dev(in), res != kNoTensor ? env.dev(res) : nullptr, env.dev(out), s);
             }
+            std::string describe() const override { return split ? "split: dw + 1x1" : "fused kernel"; }
         };
 
         // ------------------------------------------------------------ fused SE middle
