@@ -228,7 +228,7 @@ def test_conv_dma_rejects_gather_shapes(gpu):
 
 @pytest.mark.parametrize("tile", HALO_TILES)
 @pytest.mark.parametrize("shape", [(2, 64, 14, 14, 72), (1, 32, 8, 10, 40), (3, 128, 6, 6, 128), (1, 64, 56, 56, 64),
-                                   (2, 96, 28, 28, 100)])
+                                   (2, 96, 28, 28, 100), (2, 64, 7, 7, 64), (3, 32, 9, 11, 40)])
 def test_conv_halo_3x3(gpu, tile, shape):
     """Band-staged 3x3 kernel: pixel tiles crossing one or several image boundaries (zero rows
     between images), the end of the batch, ragged output channels, residual + ReLU epilogue."""
@@ -246,7 +246,7 @@ def test_conv_halo_3x3(gpu, tile, shape):
 
 @pytest.mark.parametrize("tile", HALO_TILES)
 @pytest.mark.parametrize("shape", [(2, 64, 56, 56, 64), (3, 32, 14, 14, 40), (2, 128, 28, 28, 100), (5, 64, 14, 10, 64),
-                                   (2, 48, 7, 8, 32)])
+                                   (2, 48, 7, 8, 32), (2, 32, 9, 9, 32), (1, 64, 15, 13, 48)])
 def test_conv_halo_3x3_stride2(gpu, tile, shape):
     """Stride-2 band: two input rows per output row, output rows from odd input heights (the last
     centre row's lower neighbour is the zero row), odd output widths, several images per tile."""
@@ -310,10 +310,13 @@ def test_conv_halo_splitk(gpu, tile):
 
 
 def test_conv_halo_rejects_other_shapes(gpu):
-    """The halo tiles refuse stride 3, odd width, 1x1, Cin not a multiple of 16 and Winograd."""
+    """The halo tiles refuse stride 3, dilation 2, 1x1, Cin not a multiple of 16 and Winograd."""
     lib = V.vkhip()
     plan = V.ConvPlan()
-    for xs, ws, st, pd in [((1, 16, 9, 9), (8, 16, 3, 3), (3, 3), (1, 1, 1, 1)), ((1, 16, 7, 7), (8, 16, 3, 3), (1, 1), (1, 1, 1, 1)),
+    d, _ = conv_desc((1, 16, 9, 9), (8, 16, 3, 3), (1, 1), (2, 2, 2, 2), dil=(2, 2))
+    for t in HALO_TILES:
+        assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, t, 0, ctypes.byref(plan)) != 0
+    for xs, ws, st, pd in [((1, 16, 9, 9), (8, 16, 3, 3), (3, 3), (1, 1, 1, 1)),
                            ((1, 16, 8, 8), (8, 16, 1, 1), (1, 1), (0, 0, 0, 0)), ((1, 24, 8, 8), (8, 24, 3, 3), (1, 1), (1, 1, 1, 1))]:
         d, _ = conv_desc(xs, ws, st, pd)
         for t in HALO_TILES:

@@ -1001,7 +1001,7 @@ namespace vkhip {
     // consecutive output pixels (row-major over n, oy, ox, free to cross image boundaries) need a
     // band of input rows (rows S*oy - 1 .. S*oy + 1 of each output row oy);
     // per channel slot the band is copied global->LDS by buffer-load-to-LDS, 16 bytes (a pixel pair)
-    // per lane, into rows of W + 2 pixels: W data pixels then two zero pixels, so the left
+    // per lane, into rows of W + 2 pixels (W + 3 for odd W): W data pixels then zero pixels, so the left
     // neighbour of column 0 is the previous row's last zero pixel (for the first band row: the
     // previous slot's zero tail, or a zero guard before slot 0) and the right neighbour of
     // column W-1 is the first one. Each image contributes H + 2 band rows (its zero rows above and
@@ -1012,7 +1012,11 @@ namespace vkhip {
     // [m_tile][stage][tap][kk][m_frag][lane][8 halves].
     //   FM x FN fragments per wave, WM x WN waves; KK 16-channel K steps per LDS stage; NS stages
     //   in the ring; NBI 1 KB DMA chunks per channel slot of the band (rows * (W + 2) / 2 lanes).
-    template <int FM, int FN, int WM, int WN, int KK, int NS, int NBI>
+    //   ODD: odd input width. Band rows are then W + 3 pixels (pairs stay 16-byte aligned) and the
+    //   pair that holds pixel W-1 also copies the next image row's first pixel into column W, the
+    //   right pad; the B fragments of the right-hand taps are zeroed in registers for the output
+    //   columns whose right neighbour is that pad.
+    template <int FM, int FN, int WM, int WN, int KK, int NS, int NBI, bool ODD = false>
     __global__ __launch_bounds__(64 * WM * WN, 1) void conv_halo_kernel(GemmArgs a) {
         constexpr int NW     = WM * WN;
         constexpr int BM     = 32 * FM * WM;
@@ -1050,7 +1054,8 @@ namespace vkhip {
         const int wn0    = wni * 32 * FN;
 
         const int W   = a.W, H = a.H, HW = a.HW, OW = a.OW, OHW = a.OHW, S = a.SH;
-        const int PW  = (W + 2) >> 1; // pixel pairs per band row
+        const int RS  = (W + 3) & ~1; // band row stride in pixels: W data + 1 or 2 zero pads (even)
+        const int PW  = RS >> 1;      // pixel pairs per band row
         const int nf  = n0 / OHW;
         const int iyf = S * ((n0 - nf * OHW) / OW); // input row of the first pixel's centre tap
         const int NI  = a.P / OHW;
@@ -1109,6 +1114,7 @@ namespace vkhip {
         // B fragment pixel of each fragment column: LDS pixel index of the centre tap.
         const int g = lane >> 5;
         int       qb[FN];
+        bool      redge[FN] = {}; // right neighbour is column W (not zero when W is odd)
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const int p = n0 + wn0 + 32 * j + (lane & 31);
@@ -1117,13 +1123,14 @@ namespace vkhip {
                 const int n  = p / OHW;
                 const int r  = p - n * OHW;
                 const int oy = r / OW;
-                q            = ((n - nf) * (H + 2) + S * oy + 1 - iyf) * (W + 2) + S * (r - oy * OW);
+                q            = ((n - nf) * (H + 2) + S * oy + 1 - iyf) * RS + S * (r - oy * OW);
+                if constexpr (ODD) redge[j] = S * (r - oy * OW) + 1 == W;
             }
             qb[j] = BOFF + (2 * g) * SS + q * 8;
         }
         int tapoff[9];
 #pragma unroll
-        for (int t = 0; t < 9; ++t) tapoff[t] = ((t / 3 - 1) * (W + 2) + (t % 3 - 1)) * 8;
+        for (int t = 0; t < 9; ++t) tapoff[t] = ((t / 3 - 1) * RS + (t % 3 - 1)) * 8;
 
         float16v acc[FM][FN];
 #pragma unroll
@@ -1143,8 +1150,14 @@ namespace vkhip {
 #pragma unroll
                 for (int j = 0; j < FN; ++j) {
                     const unsigned char *bp = S + qb[j] + tapoff[t] + kk * 4 * SS;
-                    const u32x2 lo = *reinterpret_cast<const u32x2 *>(bp);
-                    const u32x2 hi = *reinterpret_cast<const u32x2 *>(bp + SS);
+                    u32x2 lo = *reinterpret_cast<const u32x2 *>(bp);
+                    u32x2 hi = *reinterpret_cast<const u32x2 *>(bp + SS);
+                    if constexpr (ODD) {
+                        if (t % 3 == 2) {
+                            lo = redge[j] ? u32x2 {0u, 0u} : lo;
+                            hi = redge[j] ? u32x2 {0u, 0u} : hi;
+                        }
+                    }
                     fb[d][j] = __builtin_bit_cast(half8, u32x4_make(lo.x, lo.y, hi.x, hi.y));
                 }
 #pragma unroll
@@ -1787,9 +1800,12 @@ namespace vkhip {
     }
 
     // the smallest band-size instantiation (NBIS ascending) that holds nbi chunks per slot
+    // nbi < 0: odd input width (the ODD variant), |nbi| chunks
     template <int FM, int FN, int WM, int WN, int KK, int NS, int NBI0, int... NBIS>
     static GemmKernelFn pick_halo(int nbi) {
-        if (nbi <= NBI0) return conv_halo_kernel<FM, FN, WM, WN, KK, NS, NBI0>;
+        const bool odd = nbi < 0;
+        const int  n   = odd ? -nbi : nbi;
+        if (n <= NBI0) return odd ? conv_halo_kernel<FM, FN, WM, WN, KK, NS, NBI0, true> : conv_halo_kernel<FM, FN, WM, WN, KK, NS, NBI0>;
         if constexpr (sizeof...(NBIS) > 0) return pick_halo<FM, FN, WM, WN, KK, NS, NBIS...>(nbi);
         return nullptr;
     }
@@ -1856,19 +1872,18 @@ namespace vkhip {
     }
 
     // conv_halo_kernel: 3x3, stride 1 or 2 (both axes), pad 1, dilation 1, output (H - 1)/S + 1,
-    // even input width W (pixel pairs), Cin a multiple of the stage's 16*KK channels.
+    // Cin a multiple of the stage's 16*KK channels (odd input widths take the ODD variant).
     static bool halo_shape_ok(const vkhip_conv_desc *d, const TileCfg &t) {
         const int S = d->SH;
         return d->group == 1 && d->KH == 3 && d->KW == 3 && (S == 1 || S == 2) && d->SW == S && d->PT == 1 && d->PL == 1 &&
-               d->DH == 1 && d->DW == 1 && d->OH == (d->H - 1) / S + 1 && d->OW == (d->W - 1) / S + 1 && d->W % 2 == 0 &&
-               d->Cin % (16 * t.KK) == 0;
+               d->DH == 1 && d->DW == 1 && d->OH == (d->H - 1) / S + 1 && d->OW == (d->W - 1) / S + 1 && d->Cin % (16 * t.KK) == 0;
     }
 
     // 1 KB copy chunks per channel slot of the largest input band any workgroup of a halo tile
     // needs: band rows run from the row above the first output pixel's row to the row below the
     // last one's, with two extra (zero) rows per image boundary crossed; W/2 + 1 pixel pairs a row.
     static int halo_nbi(const vkhip_conv_desc *d, const TileCfg &t) {
-        const int64_t OHW = (int64_t) d->OH * d->OW, P = (int64_t) d->N * OHW, PW = d->W / 2 + 1, S = d->SH;
+        const int64_t OHW = (int64_t) d->OH * d->OW, P = (int64_t) d->N * OHW, PW = ((d->W + 3) & ~1) / 2, S = d->SH;
         int64_t       rows = 0;
         for (int64_t p0 = 0; p0 < P; p0 += t.BN) {
             const int64_t p1 = std::min(P, p0 + t.BN) - 1;
@@ -2043,7 +2058,7 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
     if (tile < 0) tile = (algo == VKHIP_CONV_SPLITK) ? (ceil_div(d->Cout, 4) * 4 <= 32 ? 6 : 3) : default_tile(d, wino);
     if (tile >= kNumTiles) return set_error(VKHIP_ERR_INVALID, "tile index %d out of range", tile);
     if (kTiles[tile].kind == 3 && (wino || !halo_shape_ok(d, kTiles[tile]) || halo_nbi(d, kTiles[tile]) > kHaloMaxNBI[tile]))
-        return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a 3x3 stride-1/2 pad-1 conv with even W, Cin %% %d == 0 and a band that fits LDS", tile,
+        return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a 3x3 stride-1/2 pad-1 conv with Cin %% %d == 0 and a band that fits LDS", tile,
                          16 * kTiles[tile].KK);
     if (kTiles[tile].kind == 4 && (wino || !stem_shape_ok(d) || stem_nbi(d, kTiles[tile]) > kHaloMaxNBI[tile]))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a 3x3/7x7 stride-1/2 pad-K/2 conv over at most 4 channels with even W", tile);
@@ -2189,7 +2204,8 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     a.hi     = d->act_hi;
     a.m_tiles = (int) g.m_tiles;
     const int split_steps = plan->algo == VKHIP_CONV_SPLITK ? (int) ceil_div(g.nsteps, plan->ksplit) : (int) g.nsteps;
-    GemmKernelFn fn = gemm_kernel_for(plan->tile, g.bmode, split_steps, t.kind == 3 ? halo_nbi(d, t) : (t.kind == 4 ? stem_nbi(d, t) : 0));
+    GemmKernelFn fn = gemm_kernel_for(plan->tile, g.bmode, split_steps,
+                                      t.kind == 3 ? halo_nbi(d, t) * (d->W % 2 ? -1 : 1) : (t.kind == 4 ? stem_nbi(d, t) : 0));
     if (!fn) return set_error(VKHIP_ERR_INVALID, "conv_forward: no kernel for tile %d", plan->tile);
 
     if (wino) {
