@@ -49,6 +49,22 @@ int vknn_session_count_ops(vknn_session s, const char *op_type_name);
  * node list, one node per line: "<OpType> <name> act=<ActType> res=<0|1> out=<shape>". */
 int vknn_graph_after_passes(const char *model, int64_t batch, const char *options, char *buf, int64_t cap);
 
+/* Persistent autotune table (the tune section of the reference's unified cache file "VKNNCAC1",
+ * src/backend/vulkan/vk_backend.cpp:30-150 and :440-545). A session created with the option
+ * "cache_file=<path>" (and cache_mode tune or full, the default full) merges the file's table
+ * before compiling and writes it back afterwards when it changed. These calls reach the same
+ * process-wide table directly; none needs a device.
+ *   load: merge a file's entries (once per path), returns the number read (0 if absent/unknown)
+ *   save: write the table (untouched when the bytes are unchanged); get: 0 found, 1 absent */
+int vknn_tune_cache_load(const char *path);
+int vknn_tune_cache_save(const char *path);
+int vknn_tune_cache_put(const char *key, int32_t value);
+int vknn_tune_cache_get(const char *key, int32_t *value);
+int vknn_tune_cache_clear(void);
+int vknn_tune_cache_stats(int64_t *entries, int64_t *hits, int64_t *misses);
+/* The key namespace of this device ("hip-<arch>-<CUs>cu"); needs the device. */
+int vknn_tune_cache_gpu_tag(char *buf, int64_t cap);
+
 #ifdef __cplusplus
 }
 #endif

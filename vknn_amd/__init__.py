@@ -120,6 +120,13 @@ VKNN_API = {
     "vknn_session_describe": (c_int, [c_vp, c_char_p, c_i64]),
     "vknn_session_count_ops": (c_int, [c_vp, c_char_p]),
     "vknn_graph_after_passes": (c_int, [c_char_p, c_i64, c_char_p, c_char_p, c_i64]),
+    "vknn_tune_cache_load": (c_int, [c_char_p]),
+    "vknn_tune_cache_save": (c_int, [c_char_p]),
+    "vknn_tune_cache_put": (c_int, [c_char_p, c_i32]),
+    "vknn_tune_cache_get": (c_int, [c_char_p, P(c_i32)]),
+    "vknn_tune_cache_clear": (c_int, []),
+    "vknn_tune_cache_stats": (c_int, [P(c_i64), P(c_i64), P(c_i64)]),
+    "vknn_tune_cache_gpu_tag": (c_int, [c_char_p, c_i64]),
 }
 
 _libs = {}

@@ -1,6 +1,7 @@
 // C ABI over Session + the HIP backend (declared in include/vknn_c.h).
 #include "vknn_c.h"
 #include "hip_backend.h"
+#include "tune_cache.h"
 #include "model_zoo.h"
 #include "vknn/session.h"
 #include <cstring>
@@ -44,6 +45,8 @@ namespace {
                 else if (k == "profile_reps") cfg.profileReps = std::max(1, std::atoi(v.c_str()));
                 else if (k == "fuse_dwpw") cfg.fuseDwPw = v != "0";
                 else if (k == "fuse_se") cfg.fuseSqueezeExcite = v != "0";
+                else if (k == "cache_file") cfg.cacheFile = v;
+                else if (k == "cache_mode") cfg.cacheMode = v == "off" ? CacheMode::Off : v == "tune" ? CacheMode::Tune : CacheMode::Full;
             }
             // setHint resizes the hint table with zeros; keep unset knobs at their defaults.
             if (cfg.hints.size() > (size_t) Hint::Tuning && !std::strstr(str.c_str(), "tuning=")) cfg.setHint(Hint::Tuning, Mode::Fast);
@@ -217,6 +220,44 @@ int vknn_graph_after_passes(const char *model, int64_t batch, const char *option
     } catch (const std::exception &e) {
         return fail(e.what());
     }
+}
+
+int vknn_tune_cache_load(const char *path) { return path ? hipbe::TuneCache::instance().load(path) : 0; }
+
+int vknn_tune_cache_save(const char *path) {
+    if (!path || hipbe::TuneCache::instance().save(path)) return fail(std::string("cannot write cache file ") + (path ? path : "(null)"));
+    return 0;
+}
+
+int vknn_tune_cache_put(const char *key, int32_t value) {
+    if (!key) return fail("tune cache: null key");
+    hipbe::TuneCache::instance().put(key, value);
+    return 0;
+}
+
+int vknn_tune_cache_get(const char *key, int32_t *value) {
+    int32_t v = 0;
+    if (!key || !hipbe::TuneCache::instance().get(key, v)) return 1;
+    if (value) *value = v;
+    return 0;
+}
+
+int vknn_tune_cache_clear(void) {
+    hipbe::TuneCache::instance().clear();
+    return 0;
+}
+
+int vknn_tune_cache_stats(int64_t *entries, int64_t *hits, int64_t *misses) {
+    auto &c = hipbe::TuneCache::instance();
+    if (entries) *entries = (int64_t) c.size();
+    if (hits) *hits = c.hits();
+    if (misses) *misses = c.misses();
+    return 0;
+}
+
+int vknn_tune_cache_gpu_tag(char *buf, int64_t cap) {
+    copyOut(hipbe::gpuTag(), buf, cap);
+    return 0;
 }
 
 } // extern "C"

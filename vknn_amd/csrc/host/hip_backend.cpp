@@ -11,6 +11,7 @@
 //   other ops              ops/fused_dwpw.cpp, ops/fused_se.cpp, ops/add.cpp, ops/binary.cpp
 // MI355X-specific: the launch sequence of a segment is captured once into a HIP graph and replayed.
 #include "hip_backend.h"
+#include "tune_cache.h"
 #include "vkhip.h"
 #include "vknn/profiler.h"
 #include <algorithm>
@@ -69,18 +70,18 @@ namespace vknn {
         size_t nc4Bytes(const Shape &s) { return (size_t) formatElems(TensorFormat::NC4HW4, NCHW::from(s)) * 2; }
 
         // ------------------------------------------------------------ conv autotune cache
-        // Keyed by the conv geometry; the chosen (algo, tile, ksplit) survives across sessions in
-        // the process, like the reference's in-memory tuned table (vk_backend.cpp WeightCache).
-        struct TuneKey {
-            std::vector<int32_t> k;
-            bool operator<(const TuneKey &o) const { return k < o.k; }
-        };
-        static std::map<TuneKey, std::array<int32_t, 3>> g_tuned;
-        static std::mutex                                g_tune_mu;
-
-        static TuneKey keyOf(const vkhip_conv_desc &d, int mode) {
-            return TuneKey {{d.N, d.Cin, d.H, d.W, d.Cout, d.OH, d.OW, d.KH, d.KW, d.SH, d.SW, d.PT, d.PL, d.DH, d.DW, d.group, d.has_res, mode}};
+        // Keyed by the conv geometry under the per-GPU tag; the chosen (algo, tile, ksplit) lives in
+        // the process-wide TuneCache, which Config::cacheFile persists across processes (the
+        // reference's tune table: ops/conv.cpp:195-238 keys, vk_backend.cpp:30-150 storage).
+        static std::string keyOf(const vkhip_conv_desc &d, int mode) {
+            std::string k = gpuTag() + "/conv";
+            for (int v: {d.N, d.Cin, d.H, d.W, d.Cout, d.OH, d.OW, d.KH, d.KW, d.SH, d.SW, d.PT, d.PL, d.DH, d.DW, d.group, d.has_res, mode})
+                k += "_" + std::to_string(v);
+            return k;
         }
+        // (algo, tile, ksplit) <-> one i32 table value: algo in bits 0-7, tile+1 in 8-15, ksplit in 16-23
+        static int32_t encodePick(const std::array<int32_t, 3> &p) { return (p[0] & 0xff) | (((p[1] + 1) & 0xff) << 8) | ((p[2] & 0xff) << 16); }
+        static std::array<int32_t, 3> decodePick(int32_t v) { return {v & 0xff, ((v >> 8) & 0xff) - 1, (v >> 16) & 0xff}; }
 
         // ------------------------------------------------------------ conv
         struct ConvOp: HipOp {
@@ -144,12 +145,12 @@ namespace vknn {
                     build(w, b);
                     return;
                 }
-                TuneKey key = keyOf(d, tuning * 4 + wino);
-                {
-                    std::lock_guard<std::mutex> lk(g_tune_mu);
-                    auto it = g_tuned.find(key);
-                    if (it != g_tuned.end()) {
-                        check(vkhip_conv_plan_make(&d, it->second[0], it->second[1], it->second[2], &plan), "conv plan");
+                const std::string key = keyOf(d, tuning * 4 + wino);
+                int32_t           cached = 0;
+                if (TuneCache::instance().get(key, cached)) {
+                    // an entry that no longer makes a plan (e.g. written by another build) is re-tuned
+                    const auto c = decodePick(cached);
+                    if (vkhip_conv_plan_make(&d, c[0], c[1], c[2], &plan) == VKHIP_OK) {
                         build(w, b);
                         return;
                     }
@@ -237,10 +238,7 @@ namespace vknn {
                     // cannot flip a near-tie between kernels that round differently.
                     if (bestWino < bestDirect * 0.97) pick = wpick;
                 }
-                {
-                    std::lock_guard<std::mutex> lk(g_tune_mu);
-                    g_tuned[key] = pick;
-                }
+                TuneCache::instance().put(key, encodePick(pick));
                 check(vkhip_conv_plan_make(&d, pick[0], pick[1], pick[2], &plan), "conv plan");
                 build(w, b);
             }
@@ -339,6 +337,15 @@ namespace vknn {
                 dwc.choosePlan(env, dw_w, dw_b);
                 pwc.choosePlan(env, pw_w, pw_b);
                 mid = std::make_shared<DevBuf>(nc4Bytes({c.N, c.Cin, c.OH, c.OW}));
+                std::string key = gpuTag() + "/dwpw";
+                for (int v: {c.N, c.Cin, c.H, c.W, c.OH, c.OW, c.KH, c.KW, c.SH, c.SW, c.PT, c.PL, d.Cout, d.has_res})
+                    key += "_" + std::to_string(v);
+                int32_t cached = 0;
+                if (TuneCache::instance().get(key, cached)) {
+                    split = cached != 0;
+                    if (!split) mid.reset();
+                    return;
+                }
                 auto xb = std::make_shared<DevBuf>(nc4Bytes({c.N, c.Cin, c.H, c.W}));
                 auto yb = std::make_shared<DevBuf>(nc4Bytes({c.N, d.Cout, c.OH, c.OW}));
                 auto rb = d.has_res ? std::make_shared<DevBuf>(nc4Bytes({c.N, d.Cout, c.OH, c.OW})) : nullptr;
@@ -363,6 +370,7 @@ namespace vknn {
                     return best;
                 };
                 split = timeIt(true) < timeIt(false);
+                TuneCache::instance().put(key, split ? 1 : 0);
                 if (!split) mid.reset();
             }
             void launch(bool sp, const void *x, const void *r, void *y, vkhip_stream_t s) {
@@ -902,10 +910,22 @@ namespace vknn {
         }
 
         std::unique_ptr<Segment> HipBackend::compileSegment(const std::vector<int> &idx, Graph &g, const Config &cfg) {
+            // warm start: the tune table of the unified cache file (reference vk_backend.cpp:440-509)
+            if (cfg.cachesTuning() && !cfg.cacheFile.empty()) {
+                cacheFile_ = cfg.cacheFile;
+                TuneCache::instance().load(cacheFile_);
+            }
             auto s     = std::make_unique<HipSegment>(idx, g, cfg);
             s->backend = this;
             segs_.push_back(s.get());
             return s;
+        }
+
+        // Writes the tune table back when it changed (reference saveCaches, vk_backend.cpp:510-545;
+        // an unchanged warm session leaves the file untouched).
+        void HipBackend::finalize() {
+            if (!cacheFile_.empty() && TuneCache::instance().save(cacheFile_))
+                throw Error(Status::RuntimeError, "cannot write cache file " + cacheFile_);
         }
 
         void HipBackend::toHost(RtTensor &rt, ExecContext &) {

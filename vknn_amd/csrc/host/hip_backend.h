@@ -92,11 +92,13 @@ namespace vknn {
             bool        supportsNode(const Graph &g, const Node &nd, DType dt) const override;
             void        toHost(RtTensor &rt, ExecContext &ctx) override;
             std::unique_ptr<Segment> compileSegment(const std::vector<int> &idx, Graph &g, const Config &cfg) override;
+            void        finalize() override;
 
           private:
             std::string               disabled_;
             bool                      high_ = false;
             std::vector<HipSegment *> segs_;
+            std::string               cacheFile_;
         };
 
     } // namespace hipbe

@@ -1,0 +1,58 @@
+// Persistent autotune table in the reference's unified cache-file container.
+//
+// File layout (reference src/backend/vulkan/vk_backend.cpp:445-545 for the container, :30-126 for
+// the weight/tune section):
+//   "VKNNCAC1" | u32 pipeLen | pipe bytes | u32 wLen | w bytes
+//   w = u32 nWeights {u32 klen | key | u32 nfloats | floats}  u32 nTune {u32 klen | key | i32 val}
+// The HIP backend has no pipeline cache (its code objects live in libvkhip.so) and keeps no
+// prepacked weights (packing is a cheap host pass), so it writes pipeLen = 0 and nWeights = 0 and
+// fills only the tune table. A file written by the reference is read too: its weight blobs are
+// skipped and its pipeline section is kept verbatim so a rewrite does not drop it. Keys are
+// namespaced by a per-GPU tag ("<tag>/<signature>"), like the reference's gpuTag, so tables from
+// other devices never apply.
+#pragma once
+#include <cstdint>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace vknn {
+    namespace hipbe {
+
+        class TuneCache {
+          public:
+            static TuneCache &instance();
+
+            // Merge the tune entries of `path` (once per path; absent or unrecognised files are
+            // ignored, as in the reference). Returns the number of entries read.
+            int  load(const std::string &path);
+            // Write the table to `path` unless the bytes equal what the file already holds.
+            // Returns 0 on success (written or unchanged), -1 when the file cannot be written.
+            int  save(const std::string &path);
+            bool get(const std::string &key, int32_t &val);
+            void put(const std::string &key, int32_t val);
+            void clear();
+            size_t size();
+            // Lookups that found / did not find an entry since the last clear().
+            int64_t hits() const { return hits_; }
+            int64_t misses() const { return misses_; }
+
+            // Serialisation of the container (exposed for tests).
+            std::vector<uint8_t> serialize();
+            bool parse(const std::vector<uint8_t> &bytes, std::map<std::string, int32_t> &tune, std::vector<char> *pipe);
+
+          private:
+            std::mutex                          mu_;
+            std::map<std::string, int32_t>      tune_;
+            std::map<std::string, bool>         loaded_;
+            std::map<std::string, std::vector<uint8_t>> fileBytes_;
+            std::vector<char>                   pipe_;
+            int64_t                             hits_ = 0, misses_ = 0;
+        };
+
+        // The per-GPU key namespace: "hip-<arch>-<CUs>cu".
+        std::string gpuTag();
+
+    } // namespace hipbe
+} // namespace vknn
