@@ -31,4 +31,12 @@ namespace vknn {
         std::string dump() const;
     };
 
+    // The ".vxm" model file (reference include/vknn/graph.h:46-47, src/core/model_io.cpp): an
+    // optimized graph with its weights in the reference's VXM2 byte layout. load returns false on
+    // a missing, foreign, truncated or inconsistent file and then says why in `why`.
+    bool                 saveGraphBin(const Graph &g, const std::string &path);
+    bool                 loadGraphBin(Graph &g, const std::string &path, std::string *why = nullptr);
+    std::vector<uint8_t> serializeGraphBin(const Graph &g);
+    bool                 parseGraphBin(Graph &g, const uint8_t *data, size_t size, std::string *why = nullptr);
+
 } // namespace vknn

@@ -39,6 +39,13 @@ namespace vknn {
         // standard passes run first; `passOpt` overrides the default pass options.
         static std::unique_ptr<Session> create(Graph &&g, const Config &cfg);
         static std::unique_ptr<Session> create(Graph &&g, const Config &cfg, const PassOptions &passOpt);
+        // Load a pre-optimized ".vxm" graph: the passes are already applied and do not run again.
+        // An empty cfg.cacheFile becomes "<model path without extension>.cache" (reference
+        // session.cpp:133-155). Throws Error(RuntimeError) when the file cannot be loaded.
+        static std::unique_ptr<Session> createFromVxm(const std::string &path, const Config &cfg);
+        // Write the planned (post-pass) graph and its weights as ".vxm" (reference session.cpp:157-159).
+        // Needs the host weights, so it fails once they were released (cfg.freeWeightsAfterUpload).
+        bool saveOptimized(const std::string &path) const;
 
         Status run(const std::vector<IOTensor> &inputs, std::vector<IOTensor> &outputs);
         Status run(const std::vector<std::vector<float>> &inputData, std::vector<IOTensor> &outputs);
@@ -65,6 +72,8 @@ namespace vknn {
 
         Graph    graph_;
         Config   cfg_;
+        bool     graphOptimized_ = false; // loaded from .vxm: passes already baked in
+        bool     weightsReleased_ = false;
         Profiler profiler_;
         std::vector<std::unique_ptr<Backend>> backends_;
         std::map<BackendKind, Backend *>      byKind_;

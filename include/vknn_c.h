@@ -49,6 +49,19 @@ int vknn_session_count_ops(vknn_session s, const char *op_type_name);
  * node list, one node per line: "<OpType> <name> act=<ActType> res=<0|1> out=<shape>". */
 int vknn_graph_after_passes(const char *model, int64_t batch, const char *options, char *buf, int64_t cap);
 
+/* The ".vxm" model file (reference VXM2 layout, src/core/model_io.cpp; Session::createFromVxm and
+ * saveOptimized, src/core/session.cpp:133-159).
+ *   save_vxm: build a zoo model, run the standard passes (options: fuse_dwpw, fuse_se; passes=0
+ *             skips them) and write the graph with its weights; host only.
+ *   vxm_describe: load a .vxm and write its node list in the vknn_graph_after_passes format; host only.
+ *   session_create_vxm: plan a session from a .vxm (passes are not re-run); an empty cache_file
+ *             option means "<path without extension>.cache", as in the reference.
+ *   session_save_optimized: write a session's planned graph; needs "keep_weights=1" at creation. */
+int vknn_model_save_vxm(const char *model, int64_t batch, uint64_t seed, const char *options, const char *path);
+int vknn_vxm_describe(const char *path, char *buf, int64_t cap);
+int vknn_session_create_vxm(const char *path, const char *options, vknn_session *out);
+int vknn_session_save_optimized(vknn_session s, const char *path);
+
 /* Persistent autotune table (the tune section of the reference's unified cache file "VKNNCAC1",
  * src/backend/vulkan/vk_backend.cpp:30-150 and :440-545). A session created with the option
  * "cache_file=<path>" (and cache_mode tune or full, the default full) merges the file's table

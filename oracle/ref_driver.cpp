@@ -107,6 +107,44 @@ REF_API int ref_model_run(const char *name, int64_t batch, uint64_t seed, const 
     return runSession(std::move(g), {std::vector<float>(x, x + nx)}, y, ny, nullptr);
 }
 
+// The reference's own ".vxm" writer and reader (src/core/model_io.cpp), to pin this build's VXM2
+// implementation byte for byte. optimized = 0: the zoo graph as built; 1: after the reference
+// session's passes (Session::create on the CPU backend, then Session::saveOptimized).
+REF_API int ref_save_vxm(const char *name, int64_t batch, uint64_t seed, int optimized, const char *path) {
+    Graph g = vknn_zoo::build(name, batch, seed);
+    if (g.nodes.empty()) {
+        g_err = "unknown model";
+        return 1;
+    }
+    if (!optimized) return saveGraphBin(g, path) ? 0 : (g_err = "saveGraphBin failed", 1);
+    Config cfg;
+    cfg.backend   = BackendKind::Cpu;
+    cfg.fallback  = {};
+    cfg.cacheMode = CacheMode::Off;
+    cfg.verbosity = 0;
+    try {
+        auto s = Session::create(std::move(g), cfg);
+        if (!s || !s->saveOptimized(path)) {
+            g_err = "saveOptimized failed";
+            return 1;
+        }
+    } catch (const std::exception &e) {
+        g_err = e.what();
+        return 1;
+    }
+    return 0;
+}
+
+// Load a .vxm with the reference reader and write it back with the reference writer.
+REF_API int ref_vxm_resave(const char *in, const char *out) {
+    Graph g;
+    if (!loadGraphBin(g, in)) {
+        g_err = "loadGraphBin failed";
+        return 1;
+    }
+    return saveGraphBin(g, out) ? 0 : (g_err = "saveGraphBin failed", 1);
+}
+
 // One node of type `op` (vknn OpType code) through the reference Session on the CPU backend.
 // Input 0 is the graph input; inputs 1.. are initializers (is_init[k] = 1) — or, with is_init[k]
 // = 0, a second graph input is not supported (all extra inputs are constants). Shapes: 4 dims per

@@ -120,6 +120,10 @@ VKNN_API = {
     "vknn_session_describe": (c_int, [c_vp, c_char_p, c_i64]),
     "vknn_session_count_ops": (c_int, [c_vp, c_char_p]),
     "vknn_graph_after_passes": (c_int, [c_char_p, c_i64, c_char_p, c_char_p, c_i64]),
+    "vknn_model_save_vxm": (c_int, [c_char_p, c_i64, c_u64, c_char_p, c_char_p]),
+    "vknn_vxm_describe": (c_int, [c_char_p, c_char_p, c_i64]),
+    "vknn_session_create_vxm": (c_int, [c_char_p, c_char_p, P(c_vp)]),
+    "vknn_session_save_optimized": (c_int, [c_vp, c_char_p]),
     "vknn_tune_cache_load": (c_int, [c_char_p]),
     "vknn_tune_cache_save": (c_int, [c_char_p]),
     "vknn_tune_cache_put": (c_int, [c_char_p, c_i32]),
@@ -234,6 +238,25 @@ class Session:
             raise VkhipError("session create: " + lib.vknn_last_error().decode())
         self.h = h.value
         self.in_shape, self.out_elems = model_io(model, batch)
+
+    @classmethod
+    def from_vxm(cls, path, model, batch, options=""):
+        """A session planned from a .vxm file; `model`/`batch` name the zoo model it was saved
+        from, which fixes the input and output sizes."""
+        lib = vknn()
+        require_gpu()
+        self = cls.__new__(cls)
+        self.model, self.batch = model, batch
+        h = c_vp()
+        if lib.vknn_session_create_vxm(str(path).encode(), options.encode(), ctypes.byref(h)):
+            raise VkhipError("session create: " + lib.vknn_last_error().decode())
+        self.h = h.value
+        self.in_shape, self.out_elems = model_io(model, batch)
+        return self
+
+    def save_optimized(self, path):
+        if vknn().vknn_session_save_optimized(self.h, str(path).encode()):
+            raise VkhipError(vknn().vknn_last_error().decode())
 
     def run(self, x):
         lib = vknn()

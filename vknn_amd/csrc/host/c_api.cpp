@@ -29,6 +29,7 @@ namespace {
 
     struct Opts {
         Config cfg;
+        bool   passes = true; // vknn_model_save_vxm: "passes=0" writes the graph as built
         Opts(const char *s) {
             cfg.backend = BackendKind::Hip;
             std::string str = s ? s : "";
@@ -46,6 +47,8 @@ namespace {
                 else if (k == "fuse_dwpw") cfg.fuseDwPw = v != "0";
                 else if (k == "fuse_se") cfg.fuseSqueezeExcite = v != "0";
                 else if (k == "cache_file") cfg.cacheFile = v;
+                else if (k == "passes") passes = v != "0";
+                else if (k == "keep_weights") cfg.freeWeightsAfterUpload = v == "0";
                 else if (k == "cache_mode") cfg.cacheMode = v == "off" ? CacheMode::Off : v == "tune" ? CacheMode::Tune : CacheMode::Full;
             }
             // setHint resizes the hint table with zeros; keep unset knobs at their defaults.
@@ -87,10 +90,10 @@ int vknn_session_create_model(const char *model, int64_t batch, uint64_t seed, c
         Graph g = vknn_zoo::build(model, batch, seed);
         if (g.nodes.empty()) return fail(std::string("unknown model ") + model);
         Opts o(options);
-        auto s   = new vknn_session_s();
+        std::unique_ptr<vknn_session_s> s(new vknn_session_s());
         s->model = model;
         s->sess  = Session::create(std::move(g), o.cfg);
-        *out     = s;
+        *out     = s.release();
         return 0;
     } catch (const std::exception &e) {
         return fail(e.what());
@@ -200,26 +203,73 @@ int vknn_session_count_ops(vknn_session s, const char *op) {
     return n;
 }
 
+static std::string nodeList(const Graph &g) {
+    std::string d;
+    for (const Node &nd: g.nodes)
+        d += std::string(opTypeName(nd.type)) + " " + nd.name + " act=" + std::to_string((int) nd.fusedAct) +
+             " res=" + std::to_string(nd.fusedResidual != kNoTensor ? 1 : 0) + " out=" + shapeStr(g.desc(nd.outputs[0]).shape) + "\n";
+    return d;
+}
+
+static Graph optimizedZooGraph(const char *model, int64_t batch, uint64_t seed, const char *options) {
+    Graph g = vknn_zoo::build(model, batch, seed);
+    if (g.nodes.empty()) throw Error(Status::InvalidArgument, std::string("unknown model ") + model);
+    Opts o(options);
+    if (!o.passes) return g;
+    PassOptions po;
+    po.batch             = batch;
+    po.fuseDwPw          = o.cfg.fuseDwPw;
+    po.fuseSqueezeExcite = o.cfg.fuseSqueezeExcite;
+    runStandardPasses(g, po);
+    g.topoSort();
+    return g;
+}
+
 int vknn_graph_after_passes(const char *model, int64_t batch, const char *options, char *buf, int64_t cap) {
     try {
-        Graph g = vknn_zoo::build(model, batch, 1);
-        if (g.nodes.empty()) return fail(std::string("unknown model ") + model);
-        Opts        o(options);
-        PassOptions po;
-        po.batch             = batch;
-        po.fuseDwPw          = o.cfg.fuseDwPw;
-        po.fuseSqueezeExcite = o.cfg.fuseSqueezeExcite;
-        runStandardPasses(g, po);
-        g.topoSort();
-        std::string d;
-        for (const Node &nd: g.nodes)
-            d += std::string(opTypeName(nd.type)) + " " + nd.name + " act=" + std::to_string((int) nd.fusedAct) +
-                 " res=" + std::to_string(nd.fusedResidual != kNoTensor ? 1 : 0) + " out=" + shapeStr(g.desc(nd.outputs[0]).shape) + "\n";
-        copyOut(d, buf, cap);
+        copyOut(nodeList(optimizedZooGraph(model, batch, 1, options)), buf, cap);
         return 0;
     } catch (const std::exception &e) {
         return fail(e.what());
     }
+}
+
+int vknn_model_save_vxm(const char *model, int64_t batch, uint64_t seed, const char *options, const char *path) {
+    try {
+        if (!path) return fail("save_vxm: null path");
+        if (!saveGraphBin(optimizedZooGraph(model, batch, seed, options), path)) return fail(std::string("cannot write ") + path);
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+int vknn_vxm_describe(const char *path, char *buf, int64_t cap) {
+    Graph       g;
+    std::string why;
+    if (!path || !loadGraphBin(g, path, &why)) return fail(std::string("failed to load .vxm ") + (path ? path : "(null)") + ": " + why);
+    copyOut(nodeList(g), buf, cap);
+    return 0;
+}
+
+int vknn_session_create_vxm(const char *path, const char *options, vknn_session *out) {
+    try {
+        if (!path || !out) return fail("create_vxm: null argument");
+        Opts o(options);
+        std::unique_ptr<vknn_session_s> s(new vknn_session_s());
+        s->model = path;
+        s->sess  = Session::createFromVxm(path, o.cfg);
+        *out     = s.release();
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+int vknn_session_save_optimized(vknn_session s, const char *path) {
+    if (!s || !path) return fail("save_optimized: null argument");
+    if (!s->sess->saveOptimized(path)) return fail(std::string("cannot save the optimized graph to ") + path + " (host weights released: create the session with keep_weights=1)");
+    return 0;
 }
 
 int vknn_tune_cache_load(const char *path) { return path ? hipbe::TuneCache::instance().load(path) : 0; }

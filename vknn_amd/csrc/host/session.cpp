@@ -32,8 +32,30 @@ namespace vknn {
         return s;
     }
 
+    std::unique_ptr<Session> Session::createFromVxm(const std::string &path, const Config &cfg) {
+        Graph       g;
+        std::string why;
+        if (!loadGraphBin(g, path, &why)) throw Error(Status::RuntimeError, "failed to load .vxm " + path + ": " + why);
+        std::unique_ptr<Session> s(new Session());
+        s->graph_          = std::move(g);
+        s->cfg_            = cfg;
+        s->graphOptimized_ = true;
+        if (s->cfg_.cacheFile.empty()) {
+            const size_t slash = path.find_last_of("/\\"), dot = path.find_last_of('.');
+            const bool   ext   = dot != std::string::npos && (slash == std::string::npos || dot > slash);
+            s->cfg_.cacheFile  = (ext ? path.substr(0, dot) : path) + ".cache";
+        }
+        s->plan(PassOptions {});
+        return s;
+    }
+
+    bool Session::saveOptimized(const std::string &path) const {
+        if (weightsReleased_) return false;
+        return saveGraphBin(graph_, path);
+    }
+
     void Session::plan(const PassOptions &opt) {
-        runStandardPasses(graph_, opt);
+        if (!graphOptimized_) runStandardPasses(graph_, opt);
         graph_.topoSort();
 
         std::vector<BackendKind> order = {cfg_.backend};
@@ -112,6 +134,7 @@ namespace vknn {
                 if (keep.count(it->first)) ++it;
                 else it = graph_.initializers.erase(it);
             }
+            weightsReleased_ = true;
         }
         profiler_.setEnabled(cfg_.profile);
     }
