@@ -179,7 +179,9 @@ typedef struct vkhip_pool_desc {
 } vkhip_pool_desc;
 int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s);
 /* Fully connected y[N,M] = act(x[N,K] W^T + b): x/y are [N,C,1,1] NC4HW4 fp16 tensors.
- * Blob: fp16 W[M][K padded to 8] followed by fp32 b[M] (vkhip_fc_weight_bytes). */
+ * Blob: fp16 W[Mp][Kp] followed by fp32 b[Mp], Mp = M rounded up to 16, Kp = K rounded up to 32,
+ * zero padded (vkhip_fc_weight_bytes). One skinny-GEMM kernel: 16 x 16/32 output tiles, K split
+ * over 8 waves. */
 size_t vkhip_fc_weight_bytes(int64_t K, int64_t M);
 int    vkhip_fc_pack_weights(int64_t K, int64_t M, const float *w, int32_t transB, const float *b, float alpha, float beta, void *blob);
 int    vkhip_fc(const void *x, const void *blob, void *y, int64_t N, int64_t K, int64_t M, int32_t act, float lo, float hi,

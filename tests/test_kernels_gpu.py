@@ -543,10 +543,32 @@ def test_maxpool(gpu):
         assert np.array_equal(got, ref), f"maxpool k{k}"  # max of fp16 values is exact
 
 
-def test_fc(gpu):
+@pytest.mark.parametrize("shape,pb", [((2, 9, 18, 18), 1), ((1, 8, 16, 20), 1), ((3, 5, 15, 20), 0), ((2, 4, 15, 12), 1),
+                                      ((1, 64, 112, 112), 1), ((2, 7, 2, 2), 1), ((1, 4, 1, 6), 1)])
+def test_maxpool_3x3_s2_pairs(gpu, shape, pb):
+    """The stem-pool kernel (3x3 s2, pad 1 left/top, even W): odd and even output widths and
+    heights, bottom/right pad 0 or 1, a single-row input. Exact against the oracle, including the
+    -inf-free edges (every output has at least one in-image tap)."""
     lib = V.vkhip()
-    r = rng(100)
-    N, K, M = 5, 2048, 1000
+    N, C, H, W = shape
+    x = round_half(rng(91 + H + W).standard_normal(shape) * 3)
+    OH, OW = (H + 1 + pb - 3) // 2 + 1, (W + 1 + pb - 3) // 2 + 1
+    d = V.PoolDesc(N=N, C=C, H=H, W=W, OH=OH, OW=OW, KH=3, KW=3, SH=2, SW=2, PT=1, PL=1)
+    dx = to_device_nc4(x)
+    dy = DeviceBuffer(V.nc4_elems(N, C, OH, OW) * 2)
+    check(lib.vkhip_maxpool(ctypes.byref(d), dx.ptr, dy.ptr, None))
+    ref = np.zeros((N, C, OH, OW), np.float32)
+    oracle().oracle_maxpool(x.ctypes.data, ref.ctypes.data, N, C, H, W, 3, 3, 2, 2, 1, 1, OH, OW)
+    got = from_device_nc4(dy, (N, C, OH, OW))
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("N,K,M,act", [(5, 2048, 1000, 0), (64, 2048, 1000, 0), (33, 1000, 37, 1), (1, 7, 3, 2), (130, 1280, 1000, 0)])
+def test_fc(gpu, N, K, M, act):
+    """Skinny GEMM kernel: partial n tiles (N % 32), K not a multiple of 16 or 4, M not a
+    multiple of 16 or 4, fused ReLU / ReLU6."""
+    lib = V.vkhip()
+    r = rng(100 + N + K)
     x = round_half(r.standard_normal((N, K)))
     w = (r.standard_normal((M, K)) * 0.02).astype(np.float32)
     b = (r.standard_normal(M) * 0.1).astype(np.float32)
@@ -555,10 +577,15 @@ def test_fc(gpu):
     dblob = DeviceBuffer.from_array(blob)
     dx = to_device_nc4(x.reshape(N, K, 1, 1))
     dy = DeviceBuffer(V.nc4_elems(N, M, 1, 1) * 2)
-    check(lib.vkhip_fc(dx.ptr, dblob.ptr, dy.ptr, N, K, M, 0, 0.0, 0.0, None))
+    check(lib.vkhip_fc(dx.ptr, dblob.ptr, dy.ptr, N, K, M, act, 0.0, 6.0, None))
     ref = np.zeros((N, M), np.float32)
-    oracle().oracle_gemm(x.ctypes.data, w.ctypes.data, b.ctypes.data, ref.ctypes.data, N, K, M, 1, 1.0, 1.0, 0, 0, 0)
+    oracle().oracle_gemm(x.ctypes.data, w.ctypes.data, b.ctypes.data, ref.ctypes.data, N, K, M, 1, 1.0, 1.0, act, 0.0, 6.0)
     assert_parity(from_device_nc4(dy, (N, M, 1, 1)).reshape(N, M), ref, "fc")
+    # the padding lanes of the last channel block are zero
+    if M % 4:
+        check(lib.vkhip_stream_sync(None))
+        raw = dy.download(np.uint16, V.nc4_elems(N, M, 1, 1)).reshape(N, -1)
+        assert not raw[:, M:].any()
 
 
 def test_concat_slice_resize(gpu):

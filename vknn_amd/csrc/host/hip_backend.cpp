@@ -435,18 +435,71 @@ namespace vknn {
                 }
                 conv        = std::make_unique<ConvOp>();
                 conv->name  = name;
-                conv->in    = node.inputs[0];
-                conv->out   = node.outputs[0];
+                conv->in    = in  = node.inputs[0];
+                conv->out   = out = node.outputs[0];
                 vkhip_conv_desc &d = conv->d;
                 d.N = (int) M; d.Cin = (int) K; d.H = d.W = 1; d.Cout = (int) Nn; d.OH = d.OW = 1; d.KH = d.KW = 1;
                 d.SH = d.SW = d.DH = d.DW = 1; d.group = 1; d.act = (int) node.fusedAct; d.act_lo = node.actLo; d.act_hi = node.actHi;
-                conv->choosePlan(env, w.data(), b.data());
                 kind  = "gemm";
                 flops = 2.0 * M * K * Nn;
                 bytes = (M * K + M * Nn + K * Nn) * 2;
+                // the skinny-GEMM kernel (weights read once, K split over the waves of a workgroup)
+                // or the conv GEMM path; tuned sessions time both and keep the faster
+                rows = M; depth = K; cols = Nn;
+                act = d.act; lo = d.act_lo; hi = d.act_hi;
+                std::vector<uint8_t> host(vkhip_fc_weight_bytes(K, Nn));
+                check(vkhip_fc_pack_weights(K, Nn, w.data(), 1, b.data(), 1.f, 1.f, host.data()), "fc pack");
+                fcblob = upload(host.data(), host.size());
+                if (!env.tunable || env.config->hint(Hint::Tuning, (int) Mode::Fast) == (int) Mode::NoTune) return;
+                conv->choosePlan(env, w.data(), b.data());
+                std::string key = gpuTag() + "/gemm";
+                for (int64_t v: {M, K, Nn, (int64_t) d.act}) key += "_" + std::to_string(v);
+                int32_t cached = 0;
+                if (TuneCache::instance().get(key, cached)) {
+                    useConv = cached != 0;
+                } else {
+                    auto xb = std::make_shared<DevBuf>(nc4Bytes({M, K, 1, 1}));
+                    auto yb = std::make_shared<DevBuf>(nc4Bytes({M, Nn, 1, 1}));
+                    check(vkhip_fill_zero(xb->ptr, xb->bytes, nullptr), "gemm tune fill");
+                    auto timeIt = [&](bool cv) {
+                        vkhip_event_t e0, e1;
+                        check(vkhip_event_create(&e0), "event");
+                        check(vkhip_event_create(&e1), "event");
+                        double best = 1e30;
+                        for (int r = 0; r < 4; ++r) {
+                            vkhip_event_record(e0, nullptr);
+                            for (int k = 0; k < 5; ++k) launch(cv, xb->ptr, yb->ptr, nullptr);
+                            vkhip_event_record(e1, nullptr);
+                            vkhip_event_sync(e1);
+                            float ms = 0;
+                            vkhip_event_elapsed_ms(e0, e1, &ms);
+                            if (r > 0) best = std::min(best, (double) ms);
+                        }
+                        vkhip_event_destroy(e0);
+                        vkhip_event_destroy(e1);
+                        return best;
+                    };
+                    useConv = timeIt(true) < timeIt(false);
+                    TuneCache::instance().put(key, useConv ? 1 : 0);
+                }
+                if (!useConv) conv.reset();
             }
-            void record(SegEnv &env, vkhip_stream_t s) override { conv->record(env, s); }
-            std::string describe() const override { return conv->describe(); }
+            void launch(bool cv, const void *x, void *y, vkhip_stream_t s) {
+                if (cv) {
+                    check(vkhip_conv_forward(&conv->d, &conv->plan, x, conv->blob->ptr, nullptr, y, conv->ws ? conv->ws->ptr : nullptr, s), "gemm " + name);
+                    return;
+                }
+                check(vkhip_fc(x, fcblob->ptr, y, rows, depth, cols, act, lo, hi, s), "fc " + name);
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override { launch(useConv, env.dev(conv ? conv->in : in), env.dev(conv ? conv->out : out), s); }
+            std::string describe() const override { return useConv ? conv->describe() : "fc kernel"; }
+
+            std::shared_ptr<DevBuf> fcblob;
+            bool                    useConv = false;
+            int64_t                 rows = 0, depth = 0, cols = 0;
+            int                     act  = 0;
+            float                   lo = 0, hi = 0;
+            TensorId                in = kNoTensor, out = kNoTensor;
         };
 
         // ------------------------------------------------------------ element-wise & data movement

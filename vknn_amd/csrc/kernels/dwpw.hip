@@ -140,6 +140,89 @@ namespace vkhip {
         return g;
     }
 
+
+    // y[n][m] = act(b[m] + sum_k x[n][k] w[m][k]) for a small batch N: one workgroup computes a
+    // 16 (m) x 16*NF (n) tile with v_mfma_f32_16x16x16f16; its 8 waves take interleaved 32-deep K
+    // chunks and reduce their partial tiles through LDS. Fragments go straight from global memory
+    // to registers, all U chunks of a wave issued before the first MFMA: weights are read once, x
+    // (N*K fp16, small) is served from L2. Lane l of a 16x16x16 MFMA holds A[l%16][4(l/16)..+3],
+    // B[4(l/16)..+3][l%16] and D rows 4(l/16)..+3 of column l%16. Within a 32-deep chunk lane
+    // group q loads the 8 contiguous k at 8q..8q+7 of its row/column and feeds the low four to one
+    // MFMA and the high four to the next: the same permutation of k on A and B, so the sum is the
+    // same. X16: x rows are 16-byte aligned (round_up(K,4) % 8 == 0) and loaded 16 bytes at once.
+    template <int NF, bool X16>
+    __global__ __launch_bounds__(512) void fc_kernel(const uint2 *x, const half_t *w, const float *b, uint2 *y, int N, int Kb,
+                                                     int Kp, int M, int Mb, int act, float lo, float hi) {
+        constexpr int U = 8;
+        __shared__ float4v red[8][NF][64];
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        const int r = lane & 15, q = lane >> 4;
+        const int m0 = blockIdx.x * 16, n0 = blockIdx.y * (16 * NF);
+        const half_t *wrow = w + (size_t) (m0 + r) * Kp + 8 * q;
+        const uint2  *xrow[NF];
+        bool          nok[NF];
+        for (int f = 0; f < NF; ++f) {
+            const int n = n0 + f * 16 + r;
+            nok[f]      = n < N;
+            xrow[f]     = x + (size_t) (nok[f] ? n : 0) * Kb + 2 * q;
+        }
+        float4v acc[NF];
+        for (int f = 0; f < NF; ++f) acc[f] = float4v {0.f, 0.f, 0.f, 0.f};
+        const int chunks = Kp >> 5;
+        for (int c0 = wave; c0 < chunks; c0 += 8 * U) {
+            half8 a[U], bv[U][NF];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + 8 * u;
+                a[u]        = half8 {0, 0, 0, 0, 0, 0, 0, 0};
+                if (c < chunks) a[u] = *(const half8 *) (wrow + c * 32);
+#pragma unroll
+                for (int f = 0; f < NF; ++f) {
+                    const int kb = c * 8 + 2 * q; // first 4-element block of this lane's 8
+                    half4     lo4 = {0, 0, 0, 0}, hi4 = {0, 0, 0, 0};
+                    if (c < chunks && nok[f]) {
+                        if (X16) {
+                            if (kb < Kb) {
+                                const uint4 v = *(const uint4 *) (xrow[f] + c * 8);
+                                lo4 = u2_as_h4(uint2 {v.x, v.y});
+                                hi4 = u2_as_h4(uint2 {v.z, v.w});
+                            }
+                        } else {
+                            if (kb < Kb) lo4 = u2_as_h4(xrow[f][c * 8]);
+                            if (kb + 1 < Kb) hi4 = u2_as_h4(xrow[f][c * 8 + 1]);
+                        }
+                    }
+                    bv[u][f] = half8 {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int f = 0; f < NF; ++f) {
+                    const half4 alo = {a[u][0], a[u][1], a[u][2], a[u][3]}, ahi = {a[u][4], a[u][5], a[u][6], a[u][7]};
+                    const half4 blo = {bv[u][f][0], bv[u][f][1], bv[u][f][2], bv[u][f][3]};
+                    const half4 bhi = {bv[u][f][4], bv[u][f][5], bv[u][f][6], bv[u][f][7]};
+                    acc[f] = __builtin_amdgcn_mfma_f32_16x16x16f16(alo, blo, acc[f], 0, 0, 0);
+                    acc[f] = __builtin_amdgcn_mfma_f32_16x16x16f16(ahi, bhi, acc[f], 0, 0, 0);
+                }
+        }
+        for (int f = 0; f < NF; ++f) red[wave][f][lane] = acc[f];
+        __syncthreads();
+        if (threadIdx.x >= NF * 64) return;
+        const int f = threadIdx.x >> 6;
+        float4v   v = red[0][f][lane];
+        for (int k = 1; k < 8; ++k) v += red[k][f][lane];
+        const int n  = n0 + f * 16 + r;
+        const int mb = (m0 >> 2) + q; // output channel block: rows m0+4q .. +3
+        if (n >= N || mb >= Mb) return;
+        float4v o;
+        for (int j = 0; j < 4; ++j) {
+            const int m = mb * 4 + j;
+            o[j]        = m < M ? apply_act(v[j] + b[m], act, lo, hi) : 0.f;
+        }
+        y[(size_t) n * Mb + mb] = h4_as_u2(f4_to_h4(o));
+    }
+
 } // namespace vkhip
 
 using namespace vkhip;
@@ -207,48 +290,59 @@ int vkhip_dwpw_forward(const vkhip_dwpw_desc *d, const void *x, const void *blob
     return check_launch("dwpw");
 }
 
-// ---------------------------------------------------------------- fully connected via the conv GEMM
-static vkhip_conv_desc fc_desc(int64_t N, int64_t K, int64_t M) {
-    vkhip_conv_desc d;
-    std::memset(&d, 0, sizeof(d));
-    d.N = (int) N; d.Cin = (int) K; d.H = 1; d.W = 1; d.Cout = (int) M; d.OH = 1; d.OW = 1;
-    d.KH = 1; d.KW = 1; d.SH = 1; d.SW = 1; d.DH = 1; d.DW = 1; d.group = 1;
-    return d;
+// ---------------------------------------------------------------- fully connected (skinny GEMM)
+// Blob: fp16 W[Mp][Kp] (rows padded to Mp = M rounded up to 16, K to Kp = K rounded up to 32,
+// zeros in the padding) followed by fp32 b[Mp].
+static void fc_geom(int64_t K, int64_t M, int64_t &Kp, int64_t &Mp) {
+    Kp = round_up(K, 32);
+    Mp = round_up(M, 16);
 }
 
 size_t vkhip_fc_weight_bytes(int64_t K, int64_t M) {
-    vkhip_conv_desc d = fc_desc(1, K, M);
-    vkhip_conv_plan p;
-    if (vkhip_conv_plan_make(&d, VKHIP_CONV_GEMM, 3, 0, &p)) return 0;
-    return p.weight_bytes;
+    if (K <= 0 || M <= 0) return 0;
+    int64_t Kp, Mp;
+    fc_geom(K, M, Kp, Mp);
+    return (size_t) (Mp * Kp * 2 + Mp * 4);
 }
 
 int vkhip_fc_pack_weights(int64_t K, int64_t M, const float *w, int32_t transB, const float *b, float alpha, float beta, void *blob) {
     if (!w || !blob || K <= 0 || M <= 0) return set_error(VKHIP_ERR_INVALID, "fc_pack: bad arguments");
-    vkhip_conv_desc d = fc_desc(1, K, M);
-    vkhip_conv_plan p;
-    int rc = vkhip_conv_plan_make(&d, VKHIP_CONV_GEMM, 3, 0, &p);
-    if (rc) return rc;
-    // conv weights are [M][K]; Gemm B is [K][M] unless transB.
-    float *wt = new float[(size_t) K * M];
-    float *bb = new float[(size_t) M];
+    int64_t Kp, Mp;
+    fc_geom(K, M, Kp, Mp);
+    std::memset(blob, 0, vkhip_fc_weight_bytes(K, M));
+    half_t *wp = (half_t *) blob;
+    float  *bp = (float *) ((char *) blob + Mp * Kp * 2);
+    // Gemm B is [K][M] unless transB ([M][K]); alpha scales it and beta the bias, in fp32 before
+    // the fp16 conversion (reference cpu/ops/gemm.cpp applies them to the fp32 product).
     for (int64_t m = 0; m < M; ++m) {
-        for (int64_t k = 0; k < K; ++k) wt[m * K + k] = alpha * (transB ? w[m * K + k] : w[k * M + m]);
-        bb[m] = b ? beta * b[m] : 0.f;
+        for (int64_t k = 0; k < K; ++k) wp[m * Kp + k] = (half_t) (alpha * (transB ? w[m * K + k] : w[k * M + m]));
+        bp[m] = b ? beta * b[m] : 0.f;
     }
-    rc = vkhip_conv_pack_weights(&d, &p, wt, bb, blob);
-    delete[] wt;
-    delete[] bb;
-    return rc;
+    return VKHIP_OK;
 }
 
 int vkhip_fc(const void *x, const void *blob, void *y, int64_t N, int64_t K, int64_t M, int32_t act, float lo, float hi, vkhip_stream_t s) {
-    vkhip_conv_desc d = fc_desc(N, K, M);
-    d.act = act; d.act_lo = lo; d.act_hi = hi;
-    vkhip_conv_plan p;
-    int rc = vkhip_conv_plan_make(&d, VKHIP_CONV_GEMM, 3, 0, &p);
-    if (rc) return rc;
-    return vkhip_conv_forward(&d, &p, x, blob, nullptr, y, nullptr, s);
+    if (!x || !blob || !y || N <= 0 || K <= 0 || M <= 0) return set_error(VKHIP_ERR_INVALID, "fc: bad arguments");
+    if (N * round_up(K, 4) >= (1LL << 31) || N * round_up(M, 4) >= (1LL << 31)) return set_error(VKHIP_ERR_UNSUPPORTED, "fc: tensor too large");
+    int64_t Kp, Mp;
+    fc_geom(K, M, Kp, Mp);
+    const half_t *wp = (const half_t *) blob;
+    const float  *bp = (const float *) ((const char *) blob + Mp * Kp * 2);
+    const int Kb = (int) (round_up(K, 4) / 4), Mb = (int) (round_up(M, 4) / 4);
+    // n tiles of 16 while the grid is small (more workgroups pulling weights), else 32
+    const bool nf1 = (Mp / 16) * ceil_div(N, 16) <= 512;
+    dim3       grid((unsigned) (Mp / 16), (unsigned) ceil_div(N, nf1 ? 16 : 32));
+    hipStream_t st = resolve_stream(s);
+    const uint2 *xx = (const uint2 *) x;
+    uint2       *yy = (uint2 *) y;
+    if (nf1) {
+        if (Kb % 2 == 0) fc_kernel<1, true><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi);
+        else fc_kernel<1, false><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi);
+    } else {
+        if (Kb % 2 == 0) fc_kernel<2, true><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi);
+        else fc_kernel<2, false><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi);
+    }
+    return check_launch("fc");
 }
 
 } // extern "C"

@@ -222,6 +222,73 @@ namespace vkhip {
         y[i] = h4_as_u2(f4_to_h4(m));
     }
 
+    // 3x3 stride-2 max pool with pad 1 on the left/top (the ResNet stem pool), even W. One thread
+    // computes a 2x2 block of outputs of one 4-channel plane: rows 2oy0-1 .. 2oy0+3 and columns
+    // 2ox0-2 .. 2ox0+3 of the input, read as three 16-byte pixel pairs per row (pair p holds
+    // pixels 2p, 2p+1), 15 loads for 4 outputs instead of 36. Maxima are taken on packed fp16
+    // pairs (exact, like the fp32 max of fp16 values); taps outside the image are skipped.
+    typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+    template <typename I>
+    __global__ void maxpool3s2_kernel(const uint4 *x, uint4 *y2, uint2 *y, int H, int Wp, int OH, int OW, int OHq, int OWq, I total) {
+        I i = (I) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return;
+        const int oxq = (int) (i % (I) OWq);
+        I         t   = i / (I) OWq;
+        const int oyq = (int) (t % (I) OHq);
+        const I   nc  = t / (I) OHq;
+        const int ox0 = 2 * oxq, oy0 = 2 * oyq;
+        const uint4 *src = x + (int64_t) nc * H * Wp;
+        const half2v ninf = __builtin_bit_cast(half2v, 0xFC00FC00u);
+        // m[r][c][h]: output (oy0+r, ox0+c), channel half h (channels 0-1, 2-3)
+        half2v m[2][2][2];
+        for (int r = 0; r < 2; ++r)
+            for (int c = 0; c < 2; ++c) m[r][c][0] = m[r][c][1] = ninf;
+        const bool left = ox0 > 0, right = ox0 + 1 < Wp;
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+            const int iy = 2 * oy0 - 1 + k;
+            if (iy < 0 || iy >= H) continue;
+            const uint4 *row = src + (int64_t) iy * Wp;
+            uint4 A = {0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u}, C = A;
+            if (left) A = row[ox0 - 1];
+            const uint4 B = row[ox0];
+            if (right) C = row[ox0 + 1];
+            // pixel halves: A.zw = pixel 2ox0-1; B.xy = 2ox0, B.zw = 2ox0+1; C.xy = 2ox0+2, C.zw = 2ox0+3
+            half2v c0[2], c1[2];
+            const unsigned a1[2] = {A.z, A.w}, b0[2] = {B.x, B.y}, b1[2] = {B.z, B.w}, cc0[2] = {C.x, C.y}, cc1[2] = {C.z, C.w};
+            for (int h = 0; h < 2; ++h) {
+                const half2v vb1 = __builtin_bit_cast(half2v, b1[h]);
+                c0[h] = __builtin_elementwise_max(__builtin_elementwise_max(__builtin_bit_cast(half2v, a1[h]), __builtin_bit_cast(half2v, b0[h])), vb1);
+                c1[h] = __builtin_elementwise_max(__builtin_elementwise_max(vb1, __builtin_bit_cast(half2v, cc0[h])), __builtin_bit_cast(half2v, cc1[h]));
+            }
+            // input row k feeds output row 0 for k = 0..2 and output row 1 for k = 2..4
+            for (int h = 0; h < 2; ++h) {
+                if (k <= 2) {
+                    m[0][0][h] = __builtin_elementwise_max(m[0][0][h], c0[h]);
+                    m[0][1][h] = __builtin_elementwise_max(m[0][1][h], c1[h]);
+                }
+                if (k >= 2) {
+                    m[1][0][h] = __builtin_elementwise_max(m[1][0][h], c0[h]);
+                    m[1][1][h] = __builtin_elementwise_max(m[1][1][h], c1[h]);
+                }
+            }
+        }
+        uint2 *dst = y + (int64_t) nc * OH * OW;
+        for (int r = 0; r < 2; ++r) {
+            const int oy = oy0 + r;
+            if (oy >= OH) break;
+            const uint2 v0 = {__builtin_bit_cast(unsigned, m[r][0][0]), __builtin_bit_cast(unsigned, m[r][0][1])};
+            const uint2 v1 = {__builtin_bit_cast(unsigned, m[r][1][0]), __builtin_bit_cast(unsigned, m[r][1][1])};
+            if (y2 && ox0 + 1 < OW) {
+                y2[((int64_t) nc * OH * OW + (int64_t) oy * OW + ox0) >> 1] = uint4 {v0.x, v0.y, v1.x, v1.y};
+            } else {
+                dst[oy * OW + ox0] = v0;
+                if (ox0 + 1 < OW) dst[oy * OW + ox0 + 1] = v1;
+            }
+        }
+    }
+
     // Channel concat / slice at 4-channel granularity when aligned, element granularity otherwise.
     __global__ void copy_channels_kernel(const half_t *x, half_t *y, int64_t Cx, int64_t Cy, int64_t cx0, int64_t cy0,
                                          int64_t C, int64_t HW, int64_t total) {
@@ -371,6 +438,20 @@ int vkhip_fused_se(const void *avg, const void *blob, void *y, int64_t N, int64_
 int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s) {
     if (!d || !x || !y || d->N <= 0 || d->C <= 0 || d->OH <= 0 || d->OW <= 0 || d->KH <= 0 || d->KW <= 0 || d->SH <= 0 || d->SW <= 0)
         return set_error(VKHIP_ERR_INVALID, "maxpool: bad arguments");
+    // the stem pool shape: 3x3 stride 2, pad 1 left/top, even W (pixel pairs 16-byte aligned), and
+    // the output width the padding implies (right pad 0 or 1)
+    if (d->KH == 3 && d->KW == 3 && d->SH == 2 && d->SW == 2 && d->PT == 1 && d->PL == 1 && d->W % 2 == 0 && d->OW == d->W / 2 &&
+        d->OH <= (d->H + 1) / 2 + 1 && d->OH >= 1) {
+        const int     OHq = (d->OH + 1) / 2, OWq = (d->OW + 1) / 2;
+        const int64_t tq  = (int64_t) d->N * ceil_div(d->C, 4) * OHq * OWq;
+        // 16-byte stores when every output row starts 16-byte aligned
+        uint4 *y2 = d->OW % 2 == 0 ? (uint4 *) y : nullptr;
+        if ((int64_t) d->N * ceil_div(d->C, 4) * d->H * d->W < INT32_MAX)
+            maxpool3s2_kernel<int><<<grid1(tq), 256, 0, resolve_stream(s)>>>((const uint4 *) x, y2, (uint2 *) y, d->H, d->W / 2, d->OH, d->OW, OHq, OWq, (int) tq);
+        else
+            maxpool3s2_kernel<int64_t><<<grid1(tq), 256, 0, resolve_stream(s)>>>((const uint4 *) x, y2, (uint2 *) y, d->H, d->W / 2, d->OH, d->OW, OHq, OWq, tq);
+        return check_launch("maxpool");
+    }
     int64_t total = (int64_t) d->N * ceil_div(d->C, 4) * d->OH * d->OW;
     if ((int64_t) d->N * ceil_div(d->C, 4) * d->H * d->W < INT32_MAX)
         maxpool_kernel<int><<<grid1(total), 256, 0, resolve_stream(s)>>>(*d, (const uint2 *) x, (uint2 *) y, (int) total);
