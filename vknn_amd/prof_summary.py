@@ -16,15 +16,28 @@ import csv
 import re
 from collections import OrderedDict
 
-CONV_PREFIX = ("conv_gemm", "conv_bd", "conv_dma", "conv_halo", "conv_stem", "splitk_reduce", "wino_", "dwconv", "dwpw")
+CONV_PREFIX = ("conv_gemm", "conv_bd", "conv_dma", "conv_halo", "conv_stem", "splitk_reduce", "wino_", "dwconv", "dwpw", "fc_kernel")
 
 
 def family(name):
     m = re.search(r"vkhip::(\w+)(<[^>(]*>)?\(", name)
     if m:
         return m.group(1) + (m.group(2) or "").replace(" ", "")
-    m = re.search(r"_ZN5vkhip\d+(\w+?)E", name)
-    return m.group(1) if m else name[:40]
+    # mangled (the tool could not demangle it): _ZN5vkhip<len><name>[I<args>E]...; integer and bool
+    # template arguments are Li<n>E / Lb<0|1>E
+    m = re.match(r"_ZN5vkhip(\d+)", name)
+    if m:
+        n = int(m.group(1))
+        base = name[m.end():m.end() + n]
+        rest = name[m.end() + n:]
+        if rest.startswith("I"):
+            args = []
+            for am in re.finditer(r"L([ib])(\d+)E", rest[1:rest.find("EE") + 1] if "EE" in rest else ""):
+                args.append(am.group(2) if am.group(1) == "i" else ("true" if am.group(2) == "1" else "false"))
+            if args:
+                return base + "<" + ",".join(args) + ">"
+        return base
+    return name[:40]
 
 
 def timed_rows(rows, steps):
@@ -77,7 +90,7 @@ def cmd_trace(a):
     for k, (c, d) in sorted(fam.items(), key=lambda kv: -kv[1][1]):
         print(f"| `{k}` | {c / a.steps:.1f} | {d / c / 1e3:.2f} | {d / a.steps / 1e3:.1f} | {100 * d / total:.1f}% |")
     print(f"\nSum of kernel time per step: {total / a.steps / 1e3:.1f} us; conv kernels (gemm, split-K reduce, "
-          f"Winograd transforms, depthwise): {conv / a.steps / 1e3:.1f} us; implicit-GEMM kernels (conv_gemm, conv_bd, conv_dma, conv_halo, conv_stem) alone: {gemm / a.steps / 1e3:.1f} us")
+          f"Winograd transforms, depthwise, FC): {conv / a.steps / 1e3:.1f} us; implicit-GEMM kernels (conv_gemm, conv_bd, conv_dma, conv_halo, conv_stem) alone: {gemm / a.steps / 1e3:.1f} us")
 
 
 def cmd_traffic(a):
