@@ -11,6 +11,7 @@
 // namespaced by a per-GPU tag ("<tag>/<signature>"), like the reference's gpuTag, so tables from
 // other devices never apply.
 #pragma once
+#include <atomic>
 #include <cstdint>
 #include <map>
 #include <mutex>
@@ -35,20 +36,20 @@ namespace vknn {
             void clear();
             size_t size();
             // Lookups that found / did not find an entry since the last clear().
-            int64_t hits() const { return hits_; }
-            int64_t misses() const { return misses_; }
+            int64_t hits() const { return hits_.load(); }
+            int64_t misses() const { return misses_.load(); }
 
-            // Serialisation of the container (exposed for tests).
-            std::vector<uint8_t> serialize();
-            bool parse(const std::vector<uint8_t> &bytes, std::map<std::string, int32_t> &tune, std::vector<char> *pipe);
+            // Parse a container's tune entries (and its pipeline bytes) without touching the table.
+            static bool parse(const std::vector<uint8_t> &bytes, std::map<std::string, int32_t> &tune, std::vector<char> *pipe);
 
           private:
+            std::vector<uint8_t> serialize(); // caller holds mu_
             std::mutex                          mu_;
             std::map<std::string, int32_t>      tune_;
             std::map<std::string, bool>         loaded_;
             std::map<std::string, std::vector<uint8_t>> fileBytes_;
             std::vector<char>                   pipe_;
-            int64_t                             hits_ = 0, misses_ = 0;
+            std::atomic<int64_t>                hits_ {0}, misses_ {0};
         };
 
         // The per-GPU key namespace: "hip-<arch>-<CUs>cu".
