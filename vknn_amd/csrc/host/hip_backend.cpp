@@ -166,7 +166,7 @@ namespace vknn {
                 // with the big tiles) and the reduction is deep enough to split.
                 const int64_t kdepth = (int64_t) d.KH * d.KW * ((d.Cin + 3) / 4) * 4;
                 if (pixels <= 4096 || base.algo == VKHIP_CONV_SPLITK || (pixels * (int64_t) d.Cout <= (int64_t) 512 * 128 * 256 && kdepth >= 512)) {
-                    for (int t: {3, 6, 1, 8, 10, 14, 16, 17, 18, 20})
+                    for (int t: {3, 6, 1, 8, 10, 14, 16, 17, 18, 20, 26})
                         for (int ks: {2, 3, 4, 8, 16}) cands.push_back({VKHIP_CONV_SPLITK, t, ks});
                 }
                 if (tuning != (int) Mode::Thorough) {

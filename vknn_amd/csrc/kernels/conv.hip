@@ -1753,9 +1753,10 @@ namespace vkhip {
         {32, 256, 1, 4, 4, 1, 2},     // 23 stem (few output channels)
         {64, 128, 2, 2, 2, 1, 2},     // 24
         {64, 256, 1, 4, 2, 2, 2},     // 25
+        {64, 128, 1, 4, 3, 2, 1, 1},  // 26 halo (2-stage ring, two workgroups per CU for small bands)
     };
-    constexpr int kNumTiles = 26;
-    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0};
+    constexpr int kNumTiles = 27;
+    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
@@ -1849,6 +1850,7 @@ namespace vkhip {
                 return bmode == 7 ? pick_stem<7, 1, 2, 1, 4, 8, 16, 24, 32, 48>(nbi) : pick_stem<3, 1, 2, 1, 4, 4, 8, 16, 24, 32, 48>(nbi);
             case 24: return pick_dma<1, 2, 2, 2, 2>(steps, bmode);
             case 25: return pick_dma<2, 2, 2, 1, 4>(steps, bmode);
+            case 26: return pick_halo<2, 1, 1, 4, 1, 2, 1, 2, 3, 4, 5, 6, 8>(nbi);
         }
         return nullptr;
     }
