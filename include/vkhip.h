@@ -63,6 +63,9 @@ int vkhip_event_create(vkhip_event_t *e);
 int vkhip_event_destroy(vkhip_event_t e);
 int vkhip_event_record(vkhip_event_t e, vkhip_stream_t s);
 int vkhip_event_sync(vkhip_event_t e);
+/* Work issued to s after this call waits for e's last record (also inside graph capture, where it
+ * forks/joins a second stream into the captured graph). */
+int vkhip_stream_wait_event(vkhip_stream_t s, vkhip_event_t e);
 int vkhip_event_elapsed_ms(vkhip_event_t start, vkhip_event_t stop, float *ms);
 
 /* Stream capture into an executable graph (the analogue of a pre-recorded command buffer). */

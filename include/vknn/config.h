@@ -63,6 +63,10 @@ namespace vknn {
         // HIP backend: capture each segment's launch sequence into a HIP graph after the first run
         // and replay it (the analogue of the reference's pre-recorded command buffer).
         bool hipGraphs = true;
+        // HIP backend: issue a node whose inputs do not depend on the node recorded just before it
+        // (e.g. a residual block's projection shortcut) on a second stream, joined back by events,
+        // so independent branches of a segment overlap. false keeps one in-order stream.
+        bool hipBranches = true;
         // HIP backend, profiling only: launches per op between its two timing events (the op's
         // time is their average; amortizes the event overhead on short kernels).
         int profileReps = 1;

@@ -135,3 +135,21 @@ def test_config4_yolov8n(gpu):
 
 def test_config4_yolov8n_b16_items(gpu):
     check_batch_items("yolov8n", 16, (0, 15), 7)
+
+
+@pytest.mark.parametrize("model,batch,opts", [("resnet_tiny", 2, ""), ("mnv3_tiny", 2, "fuse_se=1"), ("yolo_tiny", 1, ""),
+                                              ("resnet50", 4, "")])
+@pytest.mark.parametrize("graphs", ["1", "0"])
+def test_side_stream_branches_match_single_stream(gpu, model, batch, opts, graphs):
+    """Independent branches on a second stream (projection shortcuts, SE branches, YOLO concat
+    inputs) give bit-identical outputs to one in-order stream: same plans (the in-process tune
+    table is shared), same kernels, only the overlap differs. Run twice to cover the captured
+    graph's replay and the eager first run."""
+    base = f"{opts};graphs={graphs}"
+    s1 = V.Session(model, batch, seed=9, options=base + ";branches=0")
+    s2 = V.Session(model, batch, seed=9, options=base + ";branches=1")
+    assert s1.describe() == s2.describe()
+    rng = np.random.default_rng(4)
+    for _ in range(3):
+        x = rng.standard_normal(int(np.prod(s1.in_shape))).astype(np.float32)
+        np.testing.assert_array_equal(s2.run(x), s1.run(x))

@@ -68,6 +68,7 @@ VKHIP_API = {
     "vkhip_event_create": (c_int, [P(c_vp)]),
     "vkhip_event_destroy": (c_int, [c_vp]),
     "vkhip_event_record": (c_int, [c_vp, c_vp]),
+    "vkhip_stream_wait_event": (c_int, [c_vp, c_vp]),
     "vkhip_event_sync": (c_int, [c_vp]),
     "vkhip_event_elapsed_ms": (c_int, [c_vp, c_vp, P(c_f)]),
     "vkhip_graph_begin": (c_int, [c_vp]),

@@ -741,6 +741,7 @@ namespace vknn {
                 for (TensorId t: nd.outputs)
                     if (t != kNoTensor && !bufs_.count(t)) bufs_[t] = std::make_shared<DevBuf>(nc4Bytes(g.desc(t).shape));
             }
+            std::vector<std::vector<TensorId>> ins, outs;
             for (int i: idx) {
                 const Node &nd = g.nodes[i];
                 auto        op = makeOp(g, nd);
@@ -749,13 +750,84 @@ namespace vknn {
                 op->type = nd.type;
                 op->prepare(nd, env_);
                 ops_.push_back(std::move(op));
+                // data the op's launches read and write (alias ops launch nothing)
+                std::vector<TensorId> in, out;
+                if (!isAliasOp(g, nd)) {
+                    for (TensorId t: nd.inputs)
+                        if (t != kNoTensor && !g.isInitializer(t)) in.push_back(resolve(t));
+                    if (nd.fusedResidual != kNoTensor) in.push_back(resolve(nd.fusedResidual));
+                    for (TensorId t: nd.outputs)
+                        if (t != kNoTensor) out.push_back(resolve(t));
+                }
+                ins.push_back(in);
+                outs.push_back(out);
             }
             check(vkhip_stream_sync(nullptr), "prepare sync");
+            if (cfg.hipBranches) planStreams(ins, outs);
+        }
+
+        // Two-stream list schedule over the recorded op order. Every activation has its own buffer
+        // and is written by one op, so only read-after-write dependencies order ops. An op goes on
+        // the main stream when it consumes the output of the op last placed there (the common
+        // chain); an op that does not (a branch that only needs older tensors, such as a residual
+        // block's projection shortcut) goes on the side stream, so the two overlap. Dependencies
+        // that cross streams become event waits, and the side stream is joined back into the main
+        // one before the boundary outputs are unpacked. The same sequence is what the HIP graph
+        // captures (the first event wait forks the side stream into the capture).
+        void HipSegment::planStreams(const std::vector<std::vector<TensorId>> &ins, const std::vector<std::vector<TensorId>> &outs) {
+            const int            n = (int) ops_.size();
+            std::map<TensorId, int> producer; // tensor -> op index
+            for (int k = 0; k < n; ++k)
+                for (TensorId t: outs[k]) producer[t] = k;
+            opStream_.assign(n, 0);
+            opWaits_.assign(n, {});
+            opSignals_.assign(n, 0);
+            int tail[2]      = {-1, -1};  // last op placed on each stream (-1: the pack / nothing)
+            int waited[2][2] = {{-2, -2}, {-2, -2}}; // waited[s][o]: latest op of stream o that s waited for
+            bool any_side    = false;
+            for (int k = 0; k < n; ++k) {
+                if (ins[k].empty() && outs[k].empty()) continue; // alias: nothing launched
+                std::vector<int> deps;
+                for (TensorId t: ins[k]) {
+                    auto it = producer.find(t);
+                    deps.push_back(it != producer.end() && it->second < k ? it->second : -1);
+                }
+                const bool on_main_tail = tail[0] < 0 || std::find(deps.begin(), deps.end(), tail[0]) != deps.end();
+                const bool on_side_tail = tail[1] >= 0 && std::find(deps.begin(), deps.end(), tail[1]) != deps.end();
+                const int  st           = on_main_tail ? 0 : (on_side_tail || !deps.empty() ? 1 : 0);
+                opStream_[k]            = st;
+                any_side |= st == 1;
+                for (int d: deps) {
+                    const int ds = d < 0 ? 0 : opStream_[d];
+                    if (ds == st) continue;
+                    if (d <= waited[st][ds]) continue; // an earlier wait already covers it
+                    waited[st][ds] = d;
+                    opWaits_[k].push_back(d);
+                    if (d >= 0) opSignals_[d] = 1;
+                }
+                tail[st] = k;
+            }
+            useSide_ = any_side;
+            if (!useSide_) return;
+            check(vkhip_stream_create(&side_), "side stream");
+            opEvents_.assign(n, nullptr);
+            for (int k = 0; k < n; ++k)
+                if (opSignals_[k]) check(vkhip_event_create(&opEvents_[k]), "event");
+            check(vkhip_event_create(&packEvent_), "event");
+            check(vkhip_event_create(&joinEvent_), "event");
         }
 
         HipSegment::~HipSegment() {
             if (graph_) vkhip_graph_destroy(graph_);
             for (auto &e: events_) vkhip_event_destroy(e);
+            if (side_) {
+                vkhip_stream_sync(side_);
+                vkhip_stream_destroy(side_);
+            }
+            for (auto &e: opEvents_)
+                if (e) vkhip_event_destroy(e);
+            if (packEvent_) vkhip_event_destroy(packEvent_);
+            if (joinEvent_) vkhip_event_destroy(joinEvent_);
             if (stream_) {
                 vkhip_stream_sync(stream_);
                 vkhip_stream_destroy(stream_);
@@ -800,10 +872,24 @@ namespace vknn {
                 const float *src = extIn_.count(t) ? extIn_[t] : (const float *) staging_[t]->ptr;
                 check(vkhip_pack_nchw_f32(src, dev(t), x.n, x.c, x.h, x.w, stream_), "pack");
             }
-            for (size_t k = 0; k < ops_.size(); ++k) {
-                if (timed) vkhip_event_record(events_[2 * k], stream_);
-                for (int r = 0; r < (timed ? cfg_.profileReps : 1); ++r) ops_[k]->record(env_, stream_);
-                if (timed) vkhip_event_record(events_[2 * k + 1], stream_);
+            if (timed || !useSide_) {
+                // one in-order stream (profiling times each op between its own two events)
+                for (size_t k = 0; k < ops_.size(); ++k) {
+                    if (timed) vkhip_event_record(events_[2 * k], stream_);
+                    for (int r = 0; r < (timed ? cfg_.profileReps : 1); ++r) ops_[k]->record(env_, stream_);
+                    if (timed) vkhip_event_record(events_[2 * k + 1], stream_);
+                }
+            } else {
+                check(vkhip_event_record(packEvent_, stream_), "event");
+                for (size_t k = 0; k < ops_.size(); ++k) {
+                    vkhip_stream_t s = opStream_[k] ? side_ : stream_;
+                    for (int d: opWaits_[k]) check(vkhip_stream_wait_event(s, d < 0 ? packEvent_ : opEvents_[d]), "stream wait");
+                    ops_[k]->record(env_, s);
+                    if (opSignals_[k]) check(vkhip_event_record(opEvents_[k], s), "event");
+                }
+                // join: everything on the side stream completes before the main stream goes on
+                check(vkhip_event_record(joinEvent_, side_), "event");
+                check(vkhip_stream_wait_event(stream_, joinEvent_), "stream wait");
             }
             for (TensorId t: boundaryOutputs) {
                 NCHW y = NCHW::from(g_.desc(t).shape);

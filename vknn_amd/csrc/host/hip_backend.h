@@ -65,6 +65,7 @@ namespace vknn {
 
           private:
             TensorId resolve(TensorId t) const;
+            void     planStreams(const std::vector<std::vector<TensorId>> &ins, const std::vector<std::vector<TensorId>> &outs);
             void     recordAll(bool timed);
             void     launch(bool profile);
             void     dropGraph();
@@ -80,6 +81,16 @@ namespace vknn {
             std::map<TensorId, TensorId>                   alias_;
             std::map<TensorId, const float *>              extIn_;
             std::vector<vkhip_event_t>                     events_;
+            // Two-stream schedule (see planStreams): per op its stream (0 main, 1 side), the ops
+            // whose completion events it waits for (-1 = the boundary pack), and whether its own
+            // completion event is needed.
+            vkhip_stream_t                                 side_ = nullptr;
+            std::vector<int>                               opStream_;
+            std::vector<std::vector<int>>                  opWaits_;
+            std::vector<char>                              opSignals_;
+            std::vector<vkhip_event_t>                     opEvents_;
+            vkhip_event_t                                  packEvent_ = nullptr, joinEvent_ = nullptr;
+            bool                                           useSide_ = false;
         };
 
         class HipBackend: public Backend {

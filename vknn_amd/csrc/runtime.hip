@@ -172,6 +172,10 @@ int vkhip_event_destroy(vkhip_event_t e) { return e ? hip_check(hipEventDestroy(
 
 int vkhip_event_record(vkhip_event_t e, vkhip_stream_t s) { return hip_check(hipEventRecord((hipEvent_t) e, resolve_stream(s)), "hipEventRecord"); }
 
+int vkhip_stream_wait_event(vkhip_stream_t s, vkhip_event_t e) {
+    return hip_check(hipStreamWaitEvent(resolve_stream(s), (hipEvent_t) e, 0), "hipStreamWaitEvent");
+}
+
 int vkhip_event_sync(vkhip_event_t e) { return hip_check(hipEventSynchronize((hipEvent_t) e), "hipEventSynchronize"); }
 
 int vkhip_event_elapsed_ms(vkhip_event_t a, vkhip_event_t b, float *ms) {
