@@ -43,6 +43,34 @@ namespace vkhip {
         dst[i] = make_uint2((uint32_t) h[0] | ((uint32_t) h[1] << 16), (uint32_t) h[2] | ((uint32_t) h[3] << 16));
     }
 
+    // The same conversion, four consecutive pixels per thread (HW % 4 == 0): one 16-byte load per
+    // channel plane, two 16-byte stores.
+    template <typename I>
+    __global__ void pack4_kernel(const float4 *src, uint4 *dst, I C, I HW4, I Cb, I total) {
+        I i = (I) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return;
+        I p  = i % HW4;
+        I t  = i / HW4;
+        I cb = t % Cb;
+        I n  = t / Cb;
+        float v[4][4]; // [channel lane][pixel]
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            I c = cb * 4 + l;
+            float4 f = c < C ? src[(n * C + c) * HW4 + p] : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[l][0] = f.x; v[l][1] = f.y; v[l][2] = f.z; v[l][3] = f.w;
+        }
+        uint32_t w[4][2]; // [pixel][channel pair]
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            w[k][0] = (uint32_t) ref_float_to_half(v[0][k]) | ((uint32_t) ref_float_to_half(v[1][k]) << 16);
+            w[k][1] = (uint32_t) ref_float_to_half(v[2][k]) | ((uint32_t) ref_float_to_half(v[3][k]) << 16);
+        }
+        // padding lanes of a partial channel block hold +0 (ref_float_to_half(0) == 0)
+        dst[2 * i]     = make_uint4(w[0][0], w[0][1], w[1][0], w[1][1]);
+        dst[2 * i + 1] = make_uint4(w[2][0], w[2][1], w[3][0], w[3][1]);
+    }
+
     // NC4HW4 fp16 -> NCHW fp32 (exact); thread = one NCHW element, reads are 2-byte gathers.
     __global__ void unpack_kernel(const half_t *src, float *dst, int64_t C, int64_t HW, int64_t Cb, int64_t total) {
         int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
@@ -345,6 +373,15 @@ extern "C" {
 int vkhip_pack_nchw_f32(const float *src, void *dst, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s) {
     if (!src || !dst || N <= 0 || C <= 0 || H <= 0 || W <= 0) return set_error(VKHIP_ERR_INVALID, "pack: bad arguments");
     int64_t Cb = ceil_div(C, 4), total = N * Cb * H * W;
+    // four pixels per thread when every plane starts 16-byte aligned
+    if ((H * W) % 4 == 0 && ((uintptr_t) src & 15) == 0 && ((uintptr_t) dst & 15) == 0) {
+        const int64_t t4 = total / 4;
+        if (N * Cb * 4 * H * W < INT32_MAX)
+            pack4_kernel<int><<<grid1(t4), 256, 0, resolve_stream(s)>>>((const float4 *) src, (uint4 *) dst, (int) C, (int) (H * W / 4), (int) Cb, (int) t4);
+        else
+            pack4_kernel<int64_t><<<grid1(t4), 256, 0, resolve_stream(s)>>>((const float4 *) src, (uint4 *) dst, C, H * W / 4, Cb, t4);
+        return check_launch("pack");
+    }
     if (total * 4 < INT32_MAX && N * Cb * 4 * H * W < INT32_MAX)
         pack_kernel<int><<<grid1(total), 256, 0, resolve_stream(s)>>>(src, (uint2 *) dst, (int) C, (int) (H * W), (int) Cb, (int) total);
     else
