@@ -774,6 +774,8 @@ namespace vknn {
         // that cross streams become event waits, and the side stream is joined back into the main
         // one before the boundary outputs are unpacked. The same sequence is what the HIP graph
         // captures (the first event wait forks the side stream into the capture).
+        static constexpr double kSideMinUs = 4.0;
+
         void HipSegment::planStreams(const std::vector<std::vector<TensorId>> &ins, const std::vector<std::vector<TensorId>> &outs) {
             const int            n = (int) ops_.size();
             std::map<TensorId, int> producer; // tensor -> op index
@@ -794,7 +796,12 @@ namespace vknn {
                 }
                 const bool on_main_tail = tail[0] < 0 || std::find(deps.begin(), deps.end(), tail[0]) != deps.end();
                 const bool on_side_tail = tail[1] >= 0 && std::find(deps.begin(), deps.end(), tail[1]) != deps.end();
-                const int  st           = on_main_tail ? 0 : (on_side_tail || !deps.empty() ? 1 : 0);
+                // Only ops long enough to gain from overlap go to the side stream: each cross-stream
+                // wait costs a few microseconds of dependency latency in the graph, which small ops
+                // (batch 1) do not recover. Estimated time at 6 TB/s or 1.5 PFLOP/s.
+                const double est_us     = std::max((double) ops_[k]->bytes / 6e6, ops_[k]->flops / 1.5e9);
+                const bool   worth      = est_us >= kSideMinUs;
+                const int    st         = on_main_tail ? 0 : (on_side_tail || (!deps.empty() && worth) ? 1 : 0);
                 opStream_[k]            = st;
                 any_side |= st == 1;
                 for (int d: deps) {
@@ -977,7 +984,11 @@ namespace vknn {
 
         std::string HipSegment::describe() const {
             std::string s;
-            for (auto &op: ops_) s += op->name + " [" + op->kind + "] " + op->describe() + "\n";
+            for (size_t k = 0; k < ops_.size(); ++k) {
+                s += ops_[k]->name + " [" + ops_[k]->kind + "] " + ops_[k]->describe();
+                if (useSide_ && opStream_[k] == 1) s += " (side stream)";
+                s += "\n";
+            }
             return s;
         }
 
