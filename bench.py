@@ -187,7 +187,7 @@ def main():
                 "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
                 "traffic": profiled_traffic() if (args.model, args.batch) == ("resnet50", 64) else None,
                 "traffic_unit": "HBM bytes per step, all conv launches (profiles/resnet50_b64_traffic.md)",
-                "kernel": "all conv/FC kernels of one step (conv_gemm, conv_bd, conv_dma, conv_halo, conv_stem, split-K reduce, Winograd transforms)",
+                "kernel": "all conv/FC kernels of one step (conv_gemm, conv_bd, conv_dma, conv_halo, conv_stem, split-K reduce, Winograd transforms, fc_kernel)",
                 "launch_ms": round(conv_ms, 4), "flops_per_step": conv_fl,
                 "algorithmic_bytes_per_step": sum(o["bytes"] for o in conv)}
         pw = [o for o in conv if "conv" in o["name"] and o["bytes"] > 0]

@@ -42,7 +42,7 @@ def family(name):
 
 def timed_rows(rows, steps):
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-    packs = [i for i, r in enumerate(rows) if family(r["Kernel_Name"]).startswith("pack_kernel")]
+    packs = [i for i, r in enumerate(rows) if family(r["Kernel_Name"]).startswith(("pack_kernel", "pack4_kernel"))]
     if len(packs) < steps:
         raise SystemExit(f"found {len(packs)} pack dispatches, need {steps}")
     return rows[packs[-steps]:]
