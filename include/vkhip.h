@@ -93,6 +93,17 @@ int vkhip_unpack_nchw_f32(const void *src, float *dst, int64_t N, int64_t C, int
 /* Flat (row-major) variants: a straight element-wise convert (vk_backend.cpp:559-575, 637-651). */
 int vkhip_pack_flat_f32(const float *src, void *dst, int64_t n, vkhip_stream_t s);
 int vkhip_unpack_flat_f32(const void *src, float *dst, int64_t n, vkhip_stream_t s);
+/* NC4HW4 <-> flat row-major NCHW of one element type (elem_bytes 2: fp16, 4: fp32), a pure copy;
+ * dir 0: NC4HW4 -> flat, 1: flat -> NC4HW4 (padding lanes of the last channel block written 0).
+ * Replaces ops/convert_layout.cpp + shaders/convert_layout.comp:1-33 (node.subOp = dir). */
+int vkhip_convert_layout(const void *src, void *dst, int64_t N, int64_t C, int64_t H, int64_t W, int32_t dir, int32_t elem_bytes,
+                         vkhip_stream_t s);
+/* Layout + dtype conversion between declared boundary formats, one destination element per
+ * thread: fmt 0 NCHW, 1 NHWC, 2 NC4HW4 (padding lanes written 0); f16 = 1 for fp16 storage, 0 for
+ * fp32. fp32 -> fp16 rounds to nearest even (unlike the host codec above), fp16 -> fp32 is exact.
+ * Replaces ops/boundary_convert.{h,cpp} + shaders/boundary_convert.comp:1-58. */
+int vkhip_boundary_convert(const void *src, int32_t src_fmt, int32_t src_f16, void *dst, int32_t dst_fmt, int32_t dst_f16, int64_t N,
+                           int64_t C, int64_t H, int64_t W, vkhip_stream_t s);
 
 /* ---------------------------------------------------------------- convolution
  * One descriptor covers dense (group 1) and depthwise (group == Cin == Cout) 2-D convolution

@@ -63,6 +63,63 @@ float oracle_half_to_float(uint16_t h) {
 void oracle_float_to_half_n(const float *src, uint16_t *dst, int64_t n) {
     for (int64_t i = 0; i < n; ++i) dst[i] = oracle_float_to_half(src[i]);
 }
+/* IEEE-754 binary32 -> binary16, round to nearest, ties to even (not the reference host codec:
+ * this is what the reference's GLSL float16_t conversion does on the boundary converter). */
+uint16_t oracle_float_to_half_rne(float v) {
+    uint32_t x;
+    memcpy(&x, &v, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ex   = (x >> 23) & 0xFFu;
+    uint32_t       m    = x & 0x7FFFFFu;
+    if (ex == 0xFFu) return (uint16_t) (sign | 0x7C00u | (m ? 0x200u | (m >> 13) : 0u)); /* inf / quiet NaN */
+    const int e = (int) ex - 127 + 15;
+    if (e >= 31) return (uint16_t) (sign | 0x7C00u);                                    /* overflow */
+    if (e <= 0) {                                                                         /* subnormal or zero */
+        if (e < -10) return (uint16_t) sign;
+        m |= 0x800000u;                      /* implicit bit */
+        const int      shift = 14 - e;       /* 24-bit significand -> 10-bit field at exponent -14 */
+        const uint32_t half  = 1u << (shift - 1);
+        uint32_t       q     = m >> shift;
+        const uint32_t rem   = m & ((1u << shift) - 1u);
+        if (rem > half || (rem == half && (q & 1u))) ++q; /* may carry into the smallest normal */
+        return (uint16_t) (sign | q);
+    }
+    uint32_t       q   = ((uint32_t) e << 10) | (m >> 13);
+    const uint32_t rem = m & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) ++q; /* carry may reach the exponent, even inf */
+    return (uint16_t) (sign | q);
+}
+
+static int64_t oracle_layout_offset(int fmt, int64_t n, int64_t c, int64_t h, int64_t w, int64_t C, int64_t H, int64_t W) {
+    if (fmt == 1) return ((n * H + h) * W + w) * C + c;
+    if (fmt == 2) return (((n * ((C + 3) / 4) + c / 4) * H + h) * W + w) * 4 + c % 4;
+    return ((n * C + c) * H + h) * W + w;
+}
+
+void oracle_boundary_convert(const void *src, int src_fmt, int src_f16, void *dst, int dst_fmt, int dst_f16, int64_t N, int64_t C,
+                             int64_t H, int64_t W) {
+    const int64_t Cd = dst_fmt == 2 ? (C + 3) / 4 * 4 : C; /* destination channel extent incl. padding */
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t c = 0; c < Cd; ++c)
+            for (int64_t h = 0; h < H; ++h)
+                for (int64_t w = 0; w < W; ++w) {
+                    const int64_t di = dst_fmt == 2 ? oracle_layout_offset(2, n, c, h, w, C, H, W) : oracle_layout_offset(dst_fmt, n, c, h, w, C, H, W);
+                    float         v  = 0.f;
+                    uint16_t      hv = 0;
+                    if (c < C) {
+                        const int64_t si = oracle_layout_offset(src_fmt, n, c, h, w, C, H, W);
+                        if (src_f16) {
+                            hv = ((const uint16_t *) src)[si];
+                            v  = oracle_half_to_float(hv);
+                        } else {
+                            v = ((const float *) src)[si];
+                        }
+                    }
+                    if (dst_f16) ((uint16_t *) dst)[di] = c < C ? (src_f16 ? hv : oracle_float_to_half_rne(v)) : 0;
+                    else ((float *) dst)[di] = v;
+                }
+}
+
 void oracle_half_to_float_n(const uint16_t *src, float *dst, int64_t n) {
     for (int64_t i = 0; i < n; ++i) dst[i] = oracle_half_to_float(src[i]);
 }

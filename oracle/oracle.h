@@ -17,6 +17,8 @@
  *   add/mul/unary/act/gap/ oracle/_ref single-op graphs + closed forms
  *   maxpool/gemm/concat/
  *   resize/bn_fold
+ *   boundary_convert       numpy: astype(float16) (IEEE round-to-nearest-even) and
+ *                          reshape/transpose constructions of NHWC and NC4HW4
  */
 #ifndef VKNN_ORACLE_H
 #define VKNN_ORACLE_H
@@ -31,6 +33,14 @@ uint16_t oracle_float_to_half(float v);
 float    oracle_half_to_float(uint16_t h);
 void     oracle_float_to_half_n(const float *src, uint16_t *dst, int64_t n);
 void     oracle_half_to_float_n(const uint16_t *src, float *dst, int64_t n);
+/* fp32 -> fp16 with IEEE round-to-nearest-even (the GPU boundary converter's rounding,
+ * shaders/boundary_convert.comp, as opposed to the host codec above). */
+uint16_t oracle_float_to_half_rne(float v);
+/* shaders/boundary_convert.comp:20-58 (also shaders/convert_layout.comp for the same-type case):
+ * fmt 0 NCHW, 1 NHWC, 2 NC4HW4; *_f16 selects fp16 (uint16 bits) or fp32 storage. One destination
+ * element at a time, NC4HW4 padding lanes 0. */
+void     oracle_boundary_convert(const void *src, int src_fmt, int src_f16, void *dst, int dst_fmt, int dst_f16, int64_t N, int64_t C,
+                                 int64_t H, int64_t W);
 
 /* src/backend/vulkan/vk_backend.cpp:576-611 (fp16 NC4HW4 pack) and :652-673 (unpack) */
 void oracle_pack_nc4hw4(const float *src, uint16_t *dst, int64_t N, int64_t C, int64_t H, int64_t W);

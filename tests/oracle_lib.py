@@ -36,6 +36,8 @@ ORACLE_API = {
     "oracle_slice_channels": (None, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "oracle_resize_nearest": (None, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_int]),
     "oracle_fold_bn": (None, [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_f]),
+    "oracle_float_to_half_rne": (ctypes.c_uint16, [c_f]),
+    "oracle_boundary_convert": (None, [c_vp, ctypes.c_int, ctypes.c_int, c_vp, ctypes.c_int, ctypes.c_int, c_i64, c_i64, c_i64, c_i64]),
     "oracle_last_error": (c_char_p, []),
     "oracle_model_run": (ctypes.c_int, [c_char_p, c_i64, c_u64, c_vp, c_i64, c_vp, c_i64]),
     "oracle_model_io": (ctypes.c_int, [c_char_p, c_i64, P(c_i64), P(c_i64), P(c_i32), c_i32]),

@@ -686,7 +686,10 @@ namespace vknn {
         };
 
         static bool isAliasOp(const Graph &g, const Node &nd) {
-            if (nd.type == OpType::Identity) return true;
+            // ConvertLayout (reference ops/convert_layout.cpp) changes only the physical layout of
+            // the same logical NCHW tensor; this backend keeps every activation NC4HW4 fp16, so
+            // in a HIP segment it is the identity (vkhip_convert_layout serves boundary callers).
+            if (nd.type == OpType::Identity || nd.type == OpType::ConvertLayout) return true;
             if (nd.type == OpType::Flatten || nd.type == OpType::Reshape || nd.type == OpType::Squeeze || nd.type == OpType::Unsqueeze) {
                 // [N,C,1,1] <-> [N,C]: the NC4HW4 bytes are identical.
                 NCHW a = NCHW::from(g.desc(nd.inputs[0]).shape), b = NCHW::from(g.desc(nd.outputs[0]).shape);
@@ -1007,7 +1010,7 @@ namespace vknn {
                 case OpType::Conv: case OpType::FusedDwPw: case OpType::FusedSE: case OpType::Gemm: case OpType::Add: case OpType::Binary:
                 case OpType::Unary: case OpType::Relu: case OpType::Clip: case OpType::GlobalAvgPool: case OpType::MaxPool:
                 case OpType::Concat: case OpType::Split: case OpType::Resize: case OpType::Flatten: case OpType::Reshape:
-                case OpType::Identity: case OpType::Squeeze: case OpType::Unsqueeze:
+                case OpType::Identity: case OpType::Squeeze: case OpType::Unsqueeze: case OpType::ConvertLayout:
                     return true;
                 default: return false;
             }

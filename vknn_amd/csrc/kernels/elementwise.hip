@@ -71,6 +71,43 @@ namespace vkhip {
         dst[2 * i + 1] = make_uint4(w[2][0], w[2][1], w[3][0], w[3][1]);
     }
 
+    // Element offset of logical (n, c, h, w) in layout fmt (0 NCHW, 1 NHWC, 2 NC4HW4).
+    __device__ __forceinline__ int64_t layout_offset(int fmt, int64_t n, int64_t c, int64_t h, int64_t w, int64_t C, int64_t H, int64_t W) {
+        if (fmt == 1) return ((n * H + h) * W + w) * C + c;
+        if (fmt == 2) return (((n * ((C + 3) >> 2) + (c >> 2)) * H + h) * W + w) * 4 + (c & 3);
+        return ((n * C + c) * H + h) * W + w;
+    }
+
+    // One destination element per thread: decode (n, c, h, w) from the destination layout, read
+    // the source element from the source layout (0 for an NC4HW4 padding lane), convert the type.
+    template <typename TS, typename TD>
+    __global__ void layout_convert_kernel(const TS *src, int sfmt, TD *dst, int dfmt, int64_t C, int64_t H, int64_t W, int64_t total) {
+        int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return;
+        int64_t n, c, h, w, t;
+        if (dfmt == 2) {
+            const int64_t Cb = (C + 3) >> 2;
+            const int64_t l  = i & 3;
+            t = i >> 2;
+            w = t % W; t /= W;
+            h = t % H; t /= H;
+            const int64_t cb = t % Cb;
+            n = t / Cb;
+            c = cb * 4 + l;
+        } else if (dfmt == 1) {
+            c = i % C; t = i / C;
+            w = t % W; t /= W;
+            h = t % H;
+            n = t / H;
+        } else {
+            w = i % W; t = i / W;
+            h = t % H; t /= H;
+            c = t % C;
+            n = t / C;
+        }
+        dst[i] = c < C ? (TD) src[layout_offset(sfmt, n, c, h, w, C, H, W)] : (TD) 0;
+    }
+
     // NC4HW4 fp16 -> NCHW fp32 (exact); thread = one NCHW element, reads are 2-byte gathers.
     __global__ void unpack_kernel(const half_t *src, float *dst, int64_t C, int64_t HW, int64_t Cb, int64_t total) {
         int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
@@ -394,6 +431,31 @@ int vkhip_unpack_nchw_f32(const void *src, float *dst, int64_t N, int64_t C, int
     int64_t Cb = ceil_div(C, 4), total = N * C * H * W;
     unpack_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>((const half_t *) src, dst, C, H * W, Cb, total);
     return check_launch("unpack");
+}
+
+static int64_t layout_elems(int fmt, int64_t N, int64_t C, int64_t H, int64_t W) {
+    return fmt == 2 ? N * ceil_div(C, 4) * 4 * H * W : N * C * H * W;
+}
+
+int vkhip_boundary_convert(const void *src, int32_t src_fmt, int32_t src_f16, void *dst, int32_t dst_fmt, int32_t dst_f16, int64_t N,
+                           int64_t C, int64_t H, int64_t W, vkhip_stream_t s) {
+    if (!src || !dst || N <= 0 || C <= 0 || H <= 0 || W <= 0 || src_fmt < 0 || src_fmt > 2 || dst_fmt < 0 || dst_fmt > 2)
+        return set_error(VKHIP_ERR_INVALID, "boundary_convert: bad arguments");
+    const int64_t total = layout_elems(dst_fmt, N, C, H, W);
+    hipStream_t   st    = resolve_stream(s);
+    dim3          g     = grid1(total);
+    if (src_f16 && dst_f16) layout_convert_kernel<half_t, half_t><<<g, 256, 0, st>>>((const half_t *) src, src_fmt, (half_t *) dst, dst_fmt, C, H, W, total);
+    else if (src_f16) layout_convert_kernel<half_t, float><<<g, 256, 0, st>>>((const half_t *) src, src_fmt, (float *) dst, dst_fmt, C, H, W, total);
+    else if (dst_f16) layout_convert_kernel<float, half_t><<<g, 256, 0, st>>>((const float *) src, src_fmt, (half_t *) dst, dst_fmt, C, H, W, total);
+    else layout_convert_kernel<float, float><<<g, 256, 0, st>>>((const float *) src, src_fmt, (float *) dst, dst_fmt, C, H, W, total);
+    return check_launch("boundary_convert");
+}
+
+int vkhip_convert_layout(const void *src, void *dst, int64_t N, int64_t C, int64_t H, int64_t W, int32_t dir, int32_t elem_bytes,
+                         vkhip_stream_t s) {
+    if ((dir != 0 && dir != 1) || (elem_bytes != 2 && elem_bytes != 4)) return set_error(VKHIP_ERR_INVALID, "convert_layout: bad dir or element size");
+    const int f16 = elem_bytes == 2;
+    return dir == 0 ? vkhip_boundary_convert(src, 2, f16, dst, 0, f16, N, C, H, W, s) : vkhip_boundary_convert(src, 0, f16, dst, 2, f16, N, C, H, W, s);
 }
 
 int vkhip_pack_flat_f32(const float *src, void *dst, int64_t n, vkhip_stream_t s) {
