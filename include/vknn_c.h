@@ -34,6 +34,10 @@ int vknn_session_run_host(vknn_session s, const float *x, int64_t nx, float *y, 
 /* Device path: the input is read from device memory (NCHW fp32, e.g. from vkhip_malloc); the run
  * is enqueued on the session stream and returns without waiting. */
 int vknn_session_bind_device_input(vknn_session s, const float *dev_x);
+/* Same, from a declared layout (0 NCHW, 1 NHWC, 2 NC4HW4) and element type (f16 = 1: fp16,
+ * 0: fp32), converted on the device by vkhip_boundary_convert (fp32 -> fp16 rounds to nearest
+ * even), like the reference's declared-format dma-buf input (vk_backend.cpp:1218-1318). */
+int vknn_session_bind_device_input_as(vknn_session s, const void *dev_x, int32_t fmt, int32_t f16);
 int vknn_session_run_device(vknn_session s);
 int vknn_session_sync(vknn_session s);
 /* Device pointer of output k (NCHW fp32, valid after a run completes). */

@@ -82,6 +82,27 @@ def test_device_input_path_matches_host_path(gpu):
         assert np.array_equal(sess.read_outputs(), host)
 
 
+@pytest.mark.parametrize("fmt", [0, 1, 2])
+@pytest.mark.parametrize("f16", [False, True])
+def test_declared_format_device_input(gpu, fmt, f16):
+    """A device input declared as NCHW/NHWC/NC4HW4 in fp32 or fp16 gives the host path's bits when
+    the values are fp16-representable (then the boundary converter's round-to-nearest-even and the
+    host codec agree)."""
+    from tests.test_boundary_convert import to_fmt
+    sess = V.Session("resnet_tiny", 2, seed=3)
+    x16 = make_input(sess.in_shape, 11).astype(np.float16)
+    host = sess.run(x16.astype(np.float32))
+    src = x16.view(np.uint16) if f16 else x16.astype(np.float32)
+    dx = V.DeviceBuffer.from_array(to_fmt(src.reshape(sess.in_shape), fmt))
+    sess.bind_device_input_as(dx.ptr, fmt, f16)
+    for _ in range(2):
+        sess.run_device()
+        sess.sync()
+        assert np.array_equal(sess.read_outputs(), host)
+    with pytest.raises(V.VkhipError, match="declared input layout"):
+        sess.bind_device_input_as(dx.ptr, 3, f16)
+
+
 def test_batch_items_independent(gpu):
     """Item k of a batched run equals a batch-1 run on image k (convs are per-image)."""
     sb = V.Session("resnet_tiny", 4, seed=3)

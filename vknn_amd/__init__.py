@@ -114,6 +114,7 @@ VKNN_API = {
     "vknn_session_destroy": (c_int, [c_vp]),
     "vknn_session_run_host": (c_int, [c_vp, c_vp, c_i64, c_vp, c_i64]),
     "vknn_session_bind_device_input": (c_int, [c_vp, c_vp]),
+    "vknn_session_bind_device_input_as": (c_int, [c_vp, c_vp, c_i32, c_i32]),
     "vknn_session_run_device": (c_int, [c_vp]),
     "vknn_session_sync": (c_int, [c_vp]),
     "vknn_session_device_output": (c_vp, [c_vp, c_i32]),
@@ -271,6 +272,11 @@ class Session:
 
     def bind_device_input(self, ptr):
         if vknn().vknn_session_bind_device_input(self.h, ptr):
+            raise VkhipError(vknn().vknn_last_error().decode())
+
+    def bind_device_input_as(self, ptr, fmt, f16):
+        """Device input in a declared layout (0 NCHW, 1 NHWC, 2 NC4HW4) and type (fp16 if f16)."""
+        if vknn().vknn_session_bind_device_input_as(self.h, ptr, fmt, int(f16)):
             raise VkhipError(vknn().vknn_last_error().decode())
 
     def run_device(self):

@@ -135,6 +135,16 @@ int vknn_session_bind_device_input(vknn_session s, const float *dev_x) {
     }
 }
 
+int vknn_session_bind_device_input_as(vknn_session s, const void *dev_x, int32_t fmt, int32_t f16) {
+    try {
+        auto *seg = onlySegment(s);
+        seg->bindDeviceInputAs(s->sess->graph().inputs[0], dev_x, fmt, f16 != 0);
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
 int vknn_session_run_device(vknn_session s) {
     Status st = s->sess->runSegments();
     return st == Status::Ok ? 0 : fail(std::string("run failed: ") + statusStr(st));

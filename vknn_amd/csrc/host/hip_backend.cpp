@@ -862,8 +862,20 @@ namespace vknn {
         void *SegEnv::dev(TensorId t) { return seg->dev(t); }
 
         void HipSegment::bindDeviceInput(TensorId t, const float *devNchw) {
-            if (extIn_[t] != devNchw) {
+            if (extIn_[t] != devNchw || extFmt_.count(t)) {
                 extIn_[t] = devNchw;
+                extFmt_.erase(t);
+                dropGraph();
+            }
+        }
+
+        void HipSegment::bindDeviceInputAs(TensorId t, const void *dev, int fmt, bool f16) {
+            if (fmt < 0 || fmt > 2) throw Error(Status::InvalidArgument, "declared input layout must be 0 (NCHW), 1 (NHWC) or 2 (NC4HW4)");
+            const auto decl = std::make_pair(fmt, f16);
+            auto       it   = extFmt_.find(t);
+            if (extIn_[t] != dev || it == extFmt_.end() || it->second != decl) {
+                extIn_[t]  = (const float *) dev;
+                extFmt_[t] = decl;
                 dropGraph();
             }
         }
@@ -880,7 +892,11 @@ namespace vknn {
                 const Shape &s = g_.desc(t).shape;
                 NCHW         x = NCHW::from(s);
                 const float *src = extIn_.count(t) ? extIn_[t] : (const float *) staging_[t]->ptr;
-                check(vkhip_pack_nchw_f32(src, dev(t), x.n, x.c, x.h, x.w, stream_), "pack");
+                auto         fit = extFmt_.find(t);
+                if (fit != extFmt_.end())
+                    check(vkhip_boundary_convert(src, fit->second.first, fit->second.second ? 1 : 0, dev(t), 2, 1, x.n, x.c, x.h, x.w, stream_),
+                          "boundary convert");
+                else check(vkhip_pack_nchw_f32(src, dev(t), x.n, x.c, x.h, x.w, stream_), "pack");
             }
             if (timed || !useSide_) {
                 // one in-order stream (profiling times each op between its own two events)

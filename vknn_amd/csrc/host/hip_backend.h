@@ -55,6 +55,10 @@ namespace vknn {
             void       *dev(TensorId t);
             // Read a boundary input straight from device memory (NCHW fp32) instead of host data.
             void        bindDeviceInput(TensorId t, const float *devNchw);
+            // Same, from a declared layout (0 NCHW, 1 NHWC, 2 NC4HW4) and dtype (fp16 or fp32),
+            // converted by the boundary converter (fp32 -> fp16 rounds to nearest even), as the
+            // reference does for a declared-format dma-buf input.
+            void        bindDeviceInputAs(TensorId t, const void *dev, int fmt, bool f16);
             // Copy a boundary output (already unpacked to NCHW fp32 on the device) to the host.
             void        download(TensorId t, float *dst);
             const float *deviceOutput(TensorId t) const;
@@ -80,6 +84,7 @@ namespace vknn {
             std::map<TensorId, std::shared_ptr<DevBuf>>    bufs_, staging_, outStaging_;
             std::map<TensorId, TensorId>                   alias_;
             std::map<TensorId, const float *>              extIn_;
+            std::map<TensorId, std::pair<int, bool>>       extFmt_; // declared (layout, fp16) of a bound input
             std::vector<vkhip_event_t>                     events_;
             // Two-stream schedule (see planStreams): per op its stream (0 main, 1 side), the ops
             // whose completion events it waits for (-1 = the boundary pack), and whether its own
