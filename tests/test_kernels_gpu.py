@@ -364,6 +364,21 @@ def test_conv_winograd(gpu, shape):
     assert_parity(got, oracle_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1), f"winograd {shape}")
 
 
+@pytest.mark.parametrize("shape", [(1, 128, 15, 7, 31), (2, 64, 14, 14, 64)])
+def test_conv_winograd_residual(gpu, shape):
+    """Winograd with a fused residual: added after the bias and before the activation in the
+    output transform (a regression: the output transform once dropped it)."""
+    N, C, H, W, Cout = shape
+    r = rng(sum(shape) + 1)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    res = round_half(r.standard_normal((N, Cout, H, W)))
+    got, plan, _ = gpu_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=5, res=res, algo=V.CONV_WINOGRAD)
+    assert plan.algo == V.CONV_WINOGRAD
+    assert_parity(got, oracle_conv(x, w, b, (1, 1), (1, 1, 1, 1), res=res, act=5), f"winograd+res {shape}")
+
+
 def test_conv_dilation(gpu):
     r = rng(40)
     x = round_half(r.standard_normal((1, 16, 15, 15)))

@@ -1418,7 +1418,9 @@ namespace vkhip {
     }
 
     // Y = A^T M A (A^T = [[1,1,1,0],[0,1,-1,-1]]) + bias, activation, scatter into NC4HW4 fp16.
-    __global__ void wino_output_kernel(const uint2 *M, const float *bias, uint2 *y, int Coutb, int Cout, int OH, int OW,
+    // res: the fused residual (same layout as y) or null; added after the bias, before the
+    // activation, like every conv epilogue.
+    __global__ void wino_output_kernel(const uint2 *M, const float *bias, const uint2 *res, uint2 *y, int Coutb, int Cout, int OH, int OW,
                                        int nTH, int nTW, int nT, int act, float lo, float hi) {
         long long idx = (long long) blockIdx.x * blockDim.x + threadIdx.x;
         if (idx >= (long long) Coutb * nT) return;
@@ -1439,7 +1441,8 @@ namespace vkhip {
             s[1][j] = m[1][j] - m[2][j] - m[3][j];
         }
         float4v b = *reinterpret_cast<const float4v *>(bias + ocb * 4);
-        uint2  *dst = y + ((long long) n * Coutb + ocb) * OH * OW;
+        uint2       *dst  = y + ((long long) n * Coutb + ocb) * OH * OW;
+        const uint2 *rsrc = res ? res + ((long long) n * Coutb + ocb) * OH * OW : nullptr;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             float4v o[2];
@@ -1452,6 +1455,7 @@ namespace vkhip {
                 int ox = 2 * tw + j;
                 if (ox >= OW) continue;
                 float4v v = o[j];
+                if (rsrc) v += h4_to_f4(u2_as_h4(rsrc[oy * OW + ox]));
                 v.x = apply_act(v.x, act, lo, hi);
                 v.y = apply_act(v.y, act, lo, hi);
                 v.z = apply_act(v.z, act, lo, hi);
@@ -2234,7 +2238,8 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
         fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
         if ((rc = check_launch("wino_gemm"))) return rc;
         int64_t nout = g.Coutb * nT;
-        wino_output_kernel<<<dim3((unsigned) ceil_div(nout, 256)), 256, 0, st>>>(M, a.bias, (uint2 *) y, (int) g.Coutb, d->Cout, d->OH, d->OW,
+        wino_output_kernel<<<dim3((unsigned) ceil_div(nout, 256)), 256, 0, st>>>(M, a.bias, d->has_res ? (const uint2 *) res : nullptr, (uint2 *) y,
+                                                                               (int) g.Coutb, d->Cout, d->OH, d->OW,
                                                                                nTH, nTW, nT, d->act, d->act_lo, d->act_hi);
         return check_launch("wino_output");
     }
