@@ -80,3 +80,52 @@ def test_conv_sweep(gpu, seed):
         got, plan, _ = gpu_conv(x, w, b, (c["S"], c["S"]), c["pads"], (c["D"], c["D"]), c["group"], c["act"], 0.0, 6.0, res, algo, tile, ks)
         rel, cos = parity(got, ref)
         assert rel <= REL_TOL and cos >= COS_TOL, (seed, c, algo, tile, ks, rel, cos)
+
+
+def draw_dwpw(seed):
+    r = np.random.default_rng(5000 + seed)
+    k = int(r.choice([3, 5]))
+    s = int(r.choice([1, 2]))
+    return dict(N=int(r.integers(1, 4)), E=int(r.integers(4, 200)), H=int(r.integers(2, 30)), W=int(r.integers(2, 30)), k=k, s=s,
+                pads=tuple(int(r.integers(0, k // 2 + 1)) for _ in range(4)), Cout=int(r.integers(1, 120)),
+                dw_act=int(r.choice([0, 1, 2])), act=int(r.integers(0, 6)), res=bool(r.random() < 0.4))
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_fused_dwpw_sweep(gpu, seed):
+    """The fused dw+pw kernel over seeded geometries (ragged channel counts, odd sizes,
+    asymmetric pads, stride 2, every activation pair, residual) against the oracle."""
+    from tests.gpu_helpers import DeviceBuffer, check, from_device_nc4, to_device_nc4
+    from tests.oracle_lib import oracle_dwpw
+    lib = V.vkhip()
+    c = draw_dwpw(seed)
+    N, E, H, W, k, s, pads, Cout = c["N"], c["E"], c["H"], c["W"], c["k"], c["s"], c["pads"], c["Cout"]
+    OH, OW = (H + pads[0] + pads[2] - k) // s + 1, (W + pads[1] + pads[3] - k) // s + 1
+    if OH < 1 or OW < 1:
+        pytest.skip("empty output")
+    r = np.random.default_rng(seed)
+    x = round_half(r.standard_normal((N, E, H, W)))
+    dw_w = (r.standard_normal((E, 1, k, k)) * 0.3).astype(np.float32)
+    dw_b = (r.standard_normal(E) * 0.1).astype(np.float32)
+    pw_w = (r.standard_normal((Cout, E)) * np.sqrt(1.0 / E)).astype(np.float32)
+    pw_b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    resid = round_half(r.standard_normal((N, Cout, OH, OW))) if c["res"] else None
+    lo, hi = (-0.3, 0.4) if c["act"] == 3 else (0.0, 6.0)
+    dwd, _ = conv_desc(x.shape, (E, 1, k, k), (s, s), pads, group=E, act=c["dw_act"], lo=0.0, hi=6.0)
+    d = V.DwPwDesc(dw=dwd, Cout=Cout, act=c["act"], act_lo=lo, act_hi=hi, has_res=int(c["res"]))
+    print(f"dwpw case {seed}: {c}", flush=True)
+    if lib.vkhip_dwpw_supported(ctypes.byref(d)) != 1:
+        pytest.skip("shape outside the fused kernel")
+    blob = np.zeros(lib.vkhip_dwpw_weight_bytes(ctypes.byref(d)), np.uint8)
+    check(lib.vkhip_dwpw_pack_weights(ctypes.byref(d), dw_w.ctypes.data, dw_b.ctypes.data, pw_w.ctypes.data, pw_b.ctypes.data,
+                                      blob.ctypes.data))
+    dblob = DeviceBuffer.from_array(blob)
+    dx = to_device_nc4(x)
+    dres = to_device_nc4(resid) if resid is not None else None
+    dy = DeviceBuffer(V.nc4_elems(N, Cout, OH, OW) * 2)
+    check(lib.vkhip_dwpw_forward(ctypes.byref(d), dx.ptr, dblob.ptr, dres.ptr if dres else None, dy.ptr, None))
+    check(lib.vkhip_stream_sync(None))
+    got = from_device_nc4(dy, (N, Cout, OH, OW))
+    ref = oracle_dwpw(x, dw_w, dw_b, pw_w, pw_b, (s, s), pads, dw_act=c["dw_act"], res=resid, act=c["act"], lo=lo, hi=hi)
+    rel, cos = parity(got, ref)
+    assert rel <= REL_TOL and cos >= COS_TOL, (seed, c, rel, cos)
