@@ -129,3 +129,55 @@ def test_fused_dwpw_sweep(gpu, seed):
     ref = oracle_dwpw(x, dw_w, dw_b, pw_w, pw_b, (s, s), pads, dw_act=c["dw_act"], res=resid, act=c["act"], lo=lo, hi=hi)
     rel, cos = parity(got, ref)
     assert rel <= REL_TOL and cos >= COS_TOL, (seed, c, rel, cos)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_pool_fc_sweep(gpu, seed):
+    """Max pool (the generic and the 3x3/s2 pixel-pair kernels), global average pool (lane counts
+    8..64 by plane size) and the skinny-GEMM FC over seeded shapes against the oracle: pools
+    bit-exact (a max of fp16 values is exact; the mean within the conv tolerance), FC within it."""
+    from tests.gpu_helpers import DeviceBuffer, check, from_device_nc4, to_device_nc4
+    from tests.oracle_lib import oracle
+    lib, o = V.vkhip(), oracle()
+    r = np.random.default_rng(9000 + seed)
+    N, C = int(r.integers(1, 5)), int(r.integers(1, 80))
+    H, W = int(r.integers(1, 40)), int(r.integers(1, 40))
+    if seed % 2 == 0:  # the stem-pool shape family: 3x3 s2, pad 1 left/top, even W
+        k, s, pt, pl = 3, 2, 1, 1
+        W += W % 2
+    else:
+        k, s = int(r.choice([1, 2, 3, 5])), int(r.choice([1, 2, 3]))
+        pt, pl = int(r.integers(0, k // 2 + 1)), int(r.integers(0, k // 2 + 1))
+    pb, pr = int(r.integers(0, k // 2 + 1)), int(r.integers(0, k // 2 + 1))
+    OH, OW = (H + pt + pb - k) // s + 1, (W + pl + pr - k) // s + 1
+    x = round_half(r.standard_normal((N, C, H, W)) * 2)
+    dx = to_device_nc4(x)
+    print(f"pool/fc case {seed}: N={N} C={C} H={H} W={W} k={k} s={s} pads={pt, pl, pb, pr}", flush=True)
+    if OH >= 1 and OW >= 1 and pt < k and pl < k:
+        d = V.PoolDesc(N=N, C=C, H=H, W=W, OH=OH, OW=OW, KH=k, KW=k, SH=s, SW=s, PT=pt, PL=pl)
+        dy = DeviceBuffer(V.nc4_elems(N, C, OH, OW) * 2)
+        check(lib.vkhip_maxpool(ctypes.byref(d), dx.ptr, dy.ptr, None))
+        ref = np.zeros((N, C, OH, OW), np.float32)
+        o.oracle_maxpool(x.ctypes.data, ref.ctypes.data, N, C, H, W, k, k, s, s, pt, pl, OH, OW)
+        assert np.array_equal(from_device_nc4(dy, (N, C, OH, OW)), ref), ("maxpool", seed)
+    davg = DeviceBuffer(V.nc4_elems(N, C, 1, 1) * 2)
+    check(lib.vkhip_global_avg_pool(dx.ptr, davg.ptr, N, C, H, W, None))
+    avg_ref = np.zeros((N, C), np.float32)
+    o.oracle_global_avg_pool(x.ctypes.data, avg_ref.ctypes.data, N, C, H * W)
+    avg = from_device_nc4(davg, (N, C, 1, 1)).reshape(N, C)
+    rel, cos = parity(avg, avg_ref)
+    assert rel <= REL_TOL and cos >= COS_TOL, ("gap", seed, rel, cos)
+    M, act = int(r.integers(1, 300)), int(r.integers(0, 3))
+    w = (r.standard_normal((M, C)) / np.sqrt(C)).astype(np.float32)
+    b = (r.standard_normal(M) * 0.1).astype(np.float32)
+    blob = np.zeros(lib.vkhip_fc_weight_bytes(C, M), np.uint8)
+    check(lib.vkhip_fc_pack_weights(C, M, w.ctypes.data, 1, b.ctypes.data, 1.0, 1.0, blob.ctypes.data))
+    dblob = DeviceBuffer.from_array(blob)
+    a16 = round_half(avg)
+    dfc = DeviceBuffer(V.nc4_elems(N, M, 1, 1) * 2)
+    check(lib.vkhip_fc(davg.ptr, dblob.ptr, dfc.ptr, N, C, M, act, 0.0, 6.0, None))
+    check(lib.vkhip_stream_sync(None))
+    fc_ref = np.zeros((N, M), np.float32)
+    o.oracle_gemm(a16.ctypes.data, w.ctypes.data, b.ctypes.data, fc_ref.ctypes.data, N, C, M, 1, 1.0, 1.0, act, 0.0, 6.0)
+    rel, cos = parity(from_device_nc4(dfc, (N, M, 1, 1)).reshape(N, M), fc_ref)
+    assert rel <= REL_TOL and cos >= COS_TOL, ("fc", seed, rel, cos)
