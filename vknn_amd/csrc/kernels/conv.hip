@@ -1758,9 +1758,10 @@ namespace vkhip {
         {64, 128, 2, 2, 2, 1, 2},     // 24
         {64, 256, 1, 4, 2, 2, 2},     // 25
         {64, 128, 1, 4, 3, 2, 1, 1},  // 26 halo (2-stage ring, two workgroups per CU for small bands)
+        {64, 256, 1, 4, 3, 2, 2, 1},  // 27 halo (one stage: workgroups overlap each other instead of a ring)
     };
-    constexpr int kNumTiles = 27;
-    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8};
+    constexpr int kNumTiles = 28;
+    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8, 15};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
@@ -1855,6 +1856,7 @@ namespace vkhip {
             case 24: return pick_dma<1, 2, 2, 2, 2>(steps, bmode);
             case 25: return pick_dma<2, 2, 2, 1, 4>(steps, bmode);
             case 26: return pick_halo<2, 1, 1, 4, 1, 2, 1, 2, 3, 4, 5, 6, 8>(nbi);
+            case 27: return pick_halo<2, 2, 1, 4, 1, 1, 2, 4, 6, 8, 10, 12, 15>(nbi);
         }
         return nullptr;
     }
