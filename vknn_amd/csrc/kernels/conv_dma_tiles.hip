@@ -1,0 +1,42 @@
+// Tile instantiations of conv_dma_kernel (tiles 11-16, 24, 25: dense B operands via LDS DMA).
+#include "conv_kernels.h"
+
+namespace vkhip {
+
+    // conv_dma_kernel with its LDS ring cut to the number of K stages one split runs (fewer stages
+    // need no deeper ring; the smaller LDS footprint lets more workgroups share a CU).
+    template <int FM, int FN, int NS, int WM, int WN, int PS = 8>
+    static GemmKernelFn pick_dma_ps(int steps) {
+        if constexpr (NS > 1) {
+            if (steps < NS) return pick_dma_ps<FM, FN, NS - 1, WM, WN, PS>(steps);
+        }
+        return conv_dma_kernel<FM, FN, NS, WM, WN, PS>;
+    }
+    // bmode 2 = stride-2 columns (16 bytes per B column)
+    template <int FM, int FN, int NS, int WM, int WN>
+    static GemmKernelFn pick_dma(int steps, int bmode) {
+        constexpr int lds16 = NS * (32 * FM * WM + 2 * 32 * FN * WN) * kBK * 2; // LDS of the 16-byte-column variant
+        if (bmode == 2) {
+            if constexpr (lds16 <= 160 * 1024) return pick_dma_ps<FM, FN, NS, WM, WN, 16>(steps);
+            else return nullptr;
+        }
+        return pick_dma_ps<FM, FN, NS, WM, WN, 8>(steps);
+    }
+
+    // the smallest band-size instantiation (NBIS ascending) that holds nbi chunks per slot
+    // nbi < 0: odd input width (the ODD variant), |nbi| chunks
+    GemmKernelFn dma_tile_kernel(int tile, int bmode, int steps) {
+        switch (tile) {
+            case 11: return pick_dma<4, 4, 2, 2, 2>(steps, bmode);
+            case 12: return pick_dma<4, 2, 2, 2, 4>(steps, bmode);
+            case 13: return pick_dma<2, 4, 2, 4, 2>(steps, bmode);
+            case 14: return pick_dma<2, 2, 2, 2, 2>(steps, bmode);
+            case 15: return pick_dma<2, 2, 2, 4, 2>(steps, bmode);
+            case 16: return pick_dma<2, 2, 4, 2, 2>(steps, bmode);
+            case 24: return pick_dma<1, 2, 2, 2, 2>(steps, bmode);
+            case 25: return pick_dma<2, 2, 2, 1, 4>(steps, bmode);
+        }
+        return nullptr;
+    }
+
+} // namespace vkhip
