@@ -65,6 +65,8 @@ namespace vknn {
         std::vector<RtTensor>                 &pool() { return pool_; }
         std::vector<std::unique_ptr<Segment>> &segments() { return segments_; }
         Status                                 runSegments();
+        // Message of the exception behind the last non-Ok status of run()/runSegments().
+        const std::string                     &lastError() const { return lastError_; }
 
       private:
         Session() = default;
@@ -80,6 +82,7 @@ namespace vknn {
         std::vector<int>                      nodeBackendIdx_;
         std::vector<std::unique_ptr<Segment>> segments_;
         std::vector<RtTensor>                 pool_;
+        std::string                           lastError_;
     };
 
 } // namespace vknn

@@ -349,3 +349,13 @@ def test_config0_vs_ref():
     in_shape, _ = O.model_io("conv3x3_bn_relu", 1)
     x = np.random.default_rng(0).uniform(-1, 1, in_shape).astype(np.float32)
     assert bits_equal(O.oracle_model_run("conv3x3_bn_relu", 1, 7, x), O.ref_model_run("conv3x3_bn_relu", 1, 7, x))
+
+
+@needs_ref
+@pytest.mark.parametrize("name", ["mnv2_block", "resnet50", "mobilenetv3_large", "yolov8n"])
+def test_full_config_vs_ref(name):
+    """Configs 1-4 at N=1 and full size: the oracle graph runner equals the reference Session (the
+    reference CPU backend compiled from its sources) bit for bit on the same seeded graph."""
+    in_shape, _ = O.model_io(name, 1)
+    x = np.random.default_rng(1).standard_normal(in_shape).astype(np.float32)
+    assert bits_equal(O.oracle_model_run(name, 1, 7, x), O.ref_model_run(name, 1, 7, x))

@@ -84,7 +84,14 @@ int vknn_model_io(const char *model, int64_t batch, int64_t *in_shape4, int64_t 
     return 0;
 }
 
-double vknn_model_flops(const char *model) { return vknn_zoo::conv_flops_per_image(model); }
+double vknn_model_flops(const char *model) {
+    try {
+        return vknn_zoo::conv_flops_per_image(model);
+    } catch (const std::exception &e) {
+        fail(e.what());
+        return 0.0;
+    }
+}
 
 int vknn_session_create_model(const char *model, int64_t batch, uint64_t seed, const char *options, vknn_session *out) {
     try {
@@ -102,8 +109,12 @@ int vknn_session_create_model(const char *model, int64_t batch, uint64_t seed, c
 }
 
 int vknn_session_destroy(vknn_session s) {
-    delete s;
-    return 0;
+    try {
+        delete s;
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 int vknn_session_run_host(vknn_session s, const float *x, int64_t nx, float *y, int64_t ny) {
@@ -111,7 +122,7 @@ int vknn_session_run_host(vknn_session s, const float *x, int64_t nx, float *y, 
         std::vector<float> in(x, x + nx);
         std::vector<IOTensor> outs;
         Status st = s->sess->run(std::vector<std::vector<float>> {in}, outs);
-        if (st != Status::Ok) return fail(std::string("run failed: ") + statusStr(st));
+        if (st != Status::Ok) return fail(std::string("run failed: ") + statusStr(st) + ": " + s->sess->lastError());
         int64_t off = 0;
         for (auto &o: outs) {
             int64_t n = numElements(o.shape);
@@ -146,8 +157,9 @@ int vknn_session_bind_device_input_as(vknn_session s, const void *dev_x, int32_t
 }
 
 int vknn_session_run_device(vknn_session s) {
+    if (!s) return fail("run_device: null session");
     Status st = s->sess->runSegments();
-    return st == Status::Ok ? 0 : fail(std::string("run failed: ") + statusStr(st));
+    return st == Status::Ok ? 0 : fail(std::string("run failed: ") + statusStr(st) + ": " + s->sess->lastError());
 }
 
 int vknn_session_sync(vknn_session s) {
@@ -194,24 +206,36 @@ void *vknn_session_stream(vknn_session s) {
 }
 
 int vknn_session_profile_json(vknn_session s, char *buf, int64_t cap) {
-    copyOut(s->sess->profiler().toJson(), buf, cap);
-    s->sess->profiler().clear();
-    return 0;
+    try {
+        copyOut(s->sess->profiler().toJson(), buf, cap);
+        s->sess->profiler().clear();
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 int vknn_session_describe(vknn_session s, char *buf, int64_t cap) {
-    std::string d;
-    for (auto &seg: s->sess->segments())
-        if (auto *h = dynamic_cast<hipbe::HipSegment *>(seg.get())) d += h->describe();
-    copyOut(d, buf, cap);
-    return 0;
+    try {
+        std::string d;
+        for (auto &seg: s->sess->segments())
+            if (auto *h = dynamic_cast<hipbe::HipSegment *>(seg.get())) d += h->describe();
+        copyOut(d, buf, cap);
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 int vknn_session_count_ops(vknn_session s, const char *op) {
-    int n = 0;
-    for (const Node &nd: s->sess->graph().nodes)
-        if (std::string(opTypeName(nd.type)) == op) ++n;
-    return n;
+    try {
+        int n = 0;
+        for (const Node &nd: s->sess->graph().nodes)
+            if (std::string(opTypeName(nd.type)) == op) ++n;
+        return n;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 static std::string nodeList(const Graph &g) {
@@ -256,11 +280,15 @@ int vknn_model_save_vxm(const char *model, int64_t batch, uint64_t seed, const c
 }
 
 int vknn_vxm_describe(const char *path, char *buf, int64_t cap) {
-    Graph       g;
-    std::string why;
-    if (!path || !loadGraphBin(g, path, &why)) return fail(std::string("failed to load .vxm ") + (path ? path : "(null)") + ": " + why);
-    copyOut(nodeList(g), buf, cap);
-    return 0;
+    try {
+        Graph       g;
+        std::string why;
+        if (!path || !loadGraphBin(g, path, &why)) return fail(std::string("failed to load .vxm ") + (path ? path : "(null)") + ": " + why);
+        copyOut(nodeList(g), buf, cap);
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 int vknn_session_create_vxm(const char *path, const char *options, vknn_session *out) {
@@ -278,47 +306,82 @@ int vknn_session_create_vxm(const char *path, const char *options, vknn_session 
 }
 
 int vknn_session_save_optimized(vknn_session s, const char *path) {
-    if (!s || !path) return fail("save_optimized: null argument");
-    if (!s->sess->saveOptimized(path)) return fail(std::string("cannot save the optimized graph to ") + path + " (host weights released: create the session with keep_weights=1)");
-    return 0;
+    try {
+        if (!s || !path) return fail("save_optimized: null argument");
+        if (!s->sess->saveOptimized(path)) return fail(std::string("cannot save the optimized graph to ") + path + " (host weights released: create the session with keep_weights=1)");
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
-int vknn_tune_cache_load(const char *path) { return path ? hipbe::TuneCache::instance().load(path) : 0; }
+int vknn_tune_cache_load(const char *path) {
+    try {
+        return path ? hipbe::TuneCache::instance().load(path) : 0;
+    } catch (const std::exception &e) {
+        fail(e.what());
+        return 0;
+    }
+}
 
 int vknn_tune_cache_save(const char *path) {
-    if (!path || hipbe::TuneCache::instance().save(path)) return fail(std::string("cannot write cache file ") + (path ? path : "(null)"));
-    return 0;
+    try {
+        if (!path || hipbe::TuneCache::instance().save(path)) return fail(std::string("cannot write cache file ") + (path ? path : "(null)"));
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 int vknn_tune_cache_put(const char *key, int32_t value) {
-    if (!key) return fail("tune cache: null key");
-    hipbe::TuneCache::instance().put(key, value);
-    return 0;
+    try {
+        if (!key) return fail("tune cache: null key");
+        hipbe::TuneCache::instance().put(key, value);
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 int vknn_tune_cache_get(const char *key, int32_t *value) {
-    int32_t v = 0;
-    if (!key || !hipbe::TuneCache::instance().get(key, v)) return 1;
-    if (value) *value = v;
-    return 0;
+    try {
+        int32_t v = 0;
+        if (!key || !hipbe::TuneCache::instance().get(key, v)) return 1;
+        if (value) *value = v;
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 int vknn_tune_cache_clear(void) {
-    hipbe::TuneCache::instance().clear();
-    return 0;
+    try {
+        hipbe::TuneCache::instance().clear();
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 int vknn_tune_cache_stats(int64_t *entries, int64_t *hits, int64_t *misses) {
-    auto &c = hipbe::TuneCache::instance();
-    if (entries) *entries = (int64_t) c.size();
-    if (hits) *hits = c.hits();
-    if (misses) *misses = c.misses();
-    return 0;
+    try {
+        auto &c = hipbe::TuneCache::instance();
+        if (entries) *entries = (int64_t) c.size();
+        if (hits) *hits = c.hits();
+        if (misses) *misses = c.misses();
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 int vknn_tune_cache_gpu_tag(char *buf, int64_t cap) {
-    copyOut(hipbe::gpuTag(), buf, cap);
-    return 0;
+    try {
+        copyOut(hipbe::gpuTag(), buf, cap);
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 } // extern "C"

@@ -950,7 +950,16 @@ namespace vknn {
             }
             if (!graph_) {
                 check(vkhip_graph_begin(stream_), "graph capture");
-                recordAll(false);
+                try {
+                    recordAll(false);
+                } catch (...) {
+                    // end the capture so the stream leaves capture mode, drop the partial graph,
+                    // and start over eagerly on the next run
+                    vkhip_graph_t partial = nullptr;
+                    if (vkhip_graph_end(stream_, &partial) == VKHIP_OK && partial) vkhip_graph_destroy(partial);
+                    replay_ = 0;
+                    throw;
+                }
                 check(vkhip_graph_end(stream_, &graph_), "graph capture");
             }
             check(vkhip_graph_launch(graph_, stream_), "graph launch");

@@ -116,7 +116,8 @@ namespace vknn {
             }
             for (TensorId t: produced)
                 if (usedOutside.count(t)) bout.push_back(t);
-            // boundary sets are known before compile so the segment can size its staging buffers
+            // the boundary sets are attached once compileSegment returns; the segment reads them
+            // when it first runs (staging buffers are sized then)
             auto seg = be->compileSegment(r, graph_, cfg_);
             seg->nodeIdx         = r;
             seg->boundaryInputs  = bin;
@@ -156,8 +157,10 @@ namespace vknn {
                 seg->run(ctx);
             }
         } catch (const Error &e) {
+            lastError_ = e.what();
             return e.status();
-        } catch (const std::exception &) {
+        } catch (const std::exception &e) {
+            lastError_ = e.what();
             return Status::RuntimeError;
         }
         return Status::Ok;
@@ -202,7 +205,11 @@ namespace vknn {
                 outputs.push_back(std::move(o));
             }
         } catch (const Error &e) {
+            lastError_ = e.what();
             return e.status();
+        } catch (const std::exception &e) {
+            lastError_ = e.what();
+            return Status::RuntimeError;
         }
         return Status::Ok;
     }
