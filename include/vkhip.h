@@ -147,6 +147,17 @@ int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
 /* y = act(conv(x) + bias (+ res)). x, y, res: NC4HW4 fp16 device tensors. */
 int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob,
                        const void *res, void *y, void *workspace, vkhip_stream_t s);
+/* vkhip_conv_forward without a workspace argument and without any allocation: the split-K
+ * partials or Winograd V/M planes go to a fixed device-resident scratch array of
+ * VKHIP_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends. No counterpart in the
+ * reference; it exists for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Plans whose workspace_bytes
+ * exceed the maximum are rejected with VKHIP_ERR_INVALID. Every call on one GPU shares that GPU's
+ * scratch, which keeps the last call's contents: calls that overlap in time on one GPU (two
+ * streams, or two host threads) race and must be serialised by the caller. */
+#define VKHIP_NOALLOC_SCRATCH_BYTES ((size_t) 64 << 20)
+int vkhip_conv_forward_noalloc(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob,
+                               const void *res, void *y, vkhip_stream_t s);
 
 /* ---------------------------------------------------------------- fused depthwise + 1x1 project
  * Reference FusedDwPw (src/backend/cpu/ops/fused_dwpw.cpp:10-87): t = dw_act(dwconv(x) + dw_b)

@@ -85,6 +85,7 @@ VKHIP_API = {
     "vkhip_conv_tile_count": (c_int, []),
     "vkhip_conv_pack_weights": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp]),
     "vkhip_conv_forward": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "vkhip_conv_forward_noalloc": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_dwpw_supported": (c_int, [P(DwPwDesc)]),
     "vkhip_dwpw_weight_bytes": (c_sz, [P(DwPwDesc)]),
     "vkhip_dwpw_pack_weights": (c_int, [P(DwPwDesc), c_vp, c_vp, c_vp, c_vp, c_vp]),

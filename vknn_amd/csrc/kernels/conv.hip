@@ -16,6 +16,7 @@
 // Winograd F(2,3) matrices (G, B^T, A^T) and the fp16 storage of V and M; the split-K reduce
 // (shaders/conv1x1_reduce_fp16.comp) for partial sums + bias + residual + activation.
 #include "conv_kernels.h"
+#include <mutex>
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -574,6 +575,32 @@ namespace vkhip {
 
     static size_t align256(size_t v) { return (v + 255) & ~(size_t) 255; }
 
+    // Scratch of the allocation-free forward entry point: one copy per GPU (a __device__ array
+    // lives in every device's memory at its own address). Host code never passes the array's name
+    // to a kernel: it is only a host-side handle, so the per-device address comes from
+    // hipGetSymbolAddress, taken once per device with that device current.
+    static __device__ __align__(256) unsigned char scratch[VKHIP_NOALLOC_SCRATCH_BYTES];
+    constexpr int kMaxDevices = 64;
+
+    static int scratch_ptr(void **out) {
+        static std::mutex mu;
+        static void      *ptrs[kMaxDevices] = {};
+        int               dev             = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+            return set_error(VKHIP_ERR_RUNTIME, "conv_forward_noalloc: no current device");
+        std::lock_guard<std::mutex> lock(mu);
+        if (!ptrs[dev]) {
+            void      *p  = nullptr;
+            hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (rc != hipSuccess || !p)
+                return set_error(VKHIP_ERR_RUNTIME, "conv_forward_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                                 hipGetErrorString(rc));
+            ptrs[dev] = p;
+        }
+        *out = ptrs[dev];
+        return VKHIP_OK;
+    }
+
 } // namespace vkhip
 
 using namespace vkhip;
@@ -828,6 +855,21 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     dim3 grid((unsigned) (g.m_tiles * g.n_tiles), 1, 1);
     fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
     return check_launch("conv_gemm");
+}
+
+int vkhip_conv_forward_noalloc(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob,
+                               const void *res, void *y, vkhip_stream_t s) {
+    if (!d || !plan) return set_error(VKHIP_ERR_INVALID, "conv_forward_noalloc: null argument");
+    if (plan->workspace_bytes > VKHIP_NOALLOC_SCRATCH_BYTES)
+        return set_error(VKHIP_ERR_INVALID, "conv_forward_noalloc: the plan needs %zu bytes of workspace, more than the %zu-byte scratch",
+                         plan->workspace_bytes, (size_t) VKHIP_NOALLOC_SCRATCH_BYTES);
+    void *ws = nullptr;
+    if (plan->workspace_bytes) {
+        int rc = vkhip_init();
+        if (rc) return rc;
+        if ((rc = scratch_ptr(&ws))) return rc;
+    }
+    return vkhip_conv_forward(d, plan, x, blob, res, y, ws, s);
 }
 
 } // extern "C"
