@@ -81,6 +81,7 @@ int vkhip_graph_destroy(vkhip_graph_t g);
 #define VKHIP_ACT_CLIP 3
 #define VKHIP_ACT_HARDSWISH 4
 #define VKHIP_ACT_SILU 5
+#define VKHIP_ACT_HARDSIGMOID 6 /* clamp(lo*v + hi, 0, 1): the squeeze-excite gate (alpha = lo, beta = hi) */
 
 /* ---------------------------------------------------------------- pack / unpack
  * NCHW fp32 (host or device memory the kernel can read) <-> NC4HW4 fp16 on the device.
@@ -117,6 +118,8 @@ typedef struct vkhip_conv_desc {
     int32_t act;
     float   act_lo, act_hi;
     int32_t has_res; /* residual tensor of the output's shape is added before the activation */
+    int32_t in_scale; /* 1: the input is first multiplied by a per-(image, input channel) scale
+                       * (vkhip_conv_forward_scaled; dense 1x1 stride-1 pad-0 convs only) */
 } vkhip_conv_desc;
 
 /* Algorithms. GEMM is the implicit-GEMM MFMA kernel (any KHxKW/stride/pad/dilation, group 1);
@@ -147,6 +150,14 @@ int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
 /* y = act(conv(x) + bias (+ res)). x, y, res: NC4HW4 fp16 device tensors. */
 int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob,
                        const void *res, void *y, void *workspace, vkhip_stream_t s);
+/* y = act(conv(x * xs) + bias (+ res)) for a plan made with d->in_scale = 1: xs is the
+ * [N][C][1][1] channel scale as an NC4HW4 fp16 device tensor (N rows of ceil(Cin/4)*4 halves, the
+ * output of a squeeze-excite branch). The product x * xs is rounded to fp16 before the
+ * convolution, exactly like a separate channel-broadcast Mul (ops/binary.cpp:32-43) writing fp16,
+ * so the result equals Mul followed by the conv; the scaled tensor itself never reaches memory. */
+int vkhip_conv_forward_scaled(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *xs,
+                              const void *blob, const void *res, void *y, void *workspace, vkhip_stream_t s);
+
 /* vkhip_conv_forward without a workspace argument and without any allocation: the split-K
  * partials or Winograd V/M planes go to a fixed device-resident scratch array of
  * VKHIP_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends. No counterpart in the
@@ -181,11 +192,14 @@ int    vkhip_dwpw_forward(const vkhip_dwpw_desc *d, const void *x, const void *b
 int vkhip_global_avg_pool(const void *x, void *y, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s);
 /* Fused SE middle (reference FusedSE, src/backend/cpu/ops/fused_se.cpp:9-47):
  * s = clamp(alpha*(W2 relu(W1 avg + b1) + b2) + beta, 0, 1). avg/y: NC4HW4 fp16 [N,C,1,1].
- * Blob: fp32 W1[Cr][C], b1[Cr], W2[C][Cr], b2[C] (vkhip_se_weight_bytes). */
+ * Two skinny-GEMM launches over the whole batch (the vkhip_fc kernel): relu(W1 avg + b1) into the
+ * workspace ([N,Cr,1,1] fp16, vkhip_se_workspace_bytes), then the gated W2 product into y. w1 is
+ * [Cr][C], w2 [C][Cr] (fp32, rounded to fp16 by the pack); the blob holds both fc blobs. */
 size_t vkhip_se_weight_bytes(int64_t C, int64_t Cr);
+size_t vkhip_se_workspace_bytes(int64_t N, int64_t Cr);
 int    vkhip_se_pack_weights(int64_t C, int64_t Cr, const float *w1, const float *b1, const float *w2, const float *b2, void *blob);
 int    vkhip_fused_se(const void *avg, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr, float alpha, float beta,
-                      vkhip_stream_t s);
+                      void *workspace, vkhip_stream_t s);
 /* y = x * scale[n,c] (channel broadcast; reference Binary Mul BCAST, ops/binary.cpp:32-43). */
 int vkhip_channel_scale(const void *x, const void *scale, void *y, int64_t N, int64_t C, int64_t HW, vkhip_stream_t s);
 

@@ -477,11 +477,11 @@ def test_fused_dwpw(gpu, N, E, H, k, s, Cout, dw_act, act, res):
 
 
 # ---------------------------------------------------------------- SE + pooling + element-wise
-def test_gap_se_scale(gpu):
+@pytest.mark.parametrize("N,C,H,Cr", [(3, 120, 14, 32), (128, 960, 7, 240), (5, 72, 9, 24)])
+def test_gap_se_scale(gpu, N, C, H, Cr):
     lib = V.vkhip()
     o = oracle()
     r = rng(60)
-    N, C, H, Cr = 3, 120, 14, 32
     x = round_half(r.standard_normal((N, C, H, H)))
     dx = to_device_nc4(x)
     davg = DeviceBuffer(V.nc4_elems(N, C, 1, 1) * 2)
@@ -498,7 +498,8 @@ def test_gap_se_scale(gpu):
     check(lib.vkhip_se_pack_weights(C, Cr, w1.ctypes.data, b1.ctypes.data, w2.ctypes.data, b2.ctypes.data, blob.ctypes.data))
     dblob = DeviceBuffer.from_array(blob)
     ds = DeviceBuffer(V.nc4_elems(N, C, 1, 1) * 2)
-    check(lib.vkhip_fused_se(davg.ptr, dblob.ptr, ds.ptr, N, C, Cr, 1.0 / 6.0, 0.5, None))
+    dws = DeviceBuffer(lib.vkhip_se_workspace_bytes(N, Cr))
+    check(lib.vkhip_fused_se(davg.ptr, dblob.ptr, ds.ptr, N, C, Cr, 1.0 / 6.0, 0.5, dws.ptr, None))
     avg16 = round_half(avg)
     s_ref = np.zeros((N, C), np.float32)
     o.oracle_fused_se(avg16.ctypes.data, N, C, w1.ctypes.data, Cr, b1.ctypes.data, w2.ctypes.data, b2.ctypes.data,
@@ -687,3 +688,56 @@ def test_invalid_arguments_rejected(gpu):
     assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_AUTO, -1, 0, ctypes.byref(plan)) == 1
     d2, _ = conv_desc((1, 8, 5, 5), (8, 8, 3, 3), (2, 2), (1, 1, 1, 1))
     assert lib.vkhip_conv_plan_make(ctypes.byref(d2), V.CONV_WINOGRAD, -1, 0, ctypes.byref(plan)) == 1
+
+
+XS_TILES = [14, 16, 24, 25]  # conv_dma_kernel tiles with the input-scale (squeeze-excite) variant
+
+
+@pytest.mark.parametrize("tile", XS_TILES)
+@pytest.mark.parametrize("shape", [(3, 72, 14, 14, 40), (5, 960, 7, 7, 160), (2, 120, 28, 28, 40), (7, 36, 5, 9, 24)])
+def test_conv_input_scale(gpu, tile, shape):
+    """1x1 conv on x * s with s of shape [N,C,1,1] (a squeeze-excite scale folded into the conv):
+    equals the separate channel-broadcast Mul (fp16 store) followed by the same conv plan, bit for
+    bit, and the oracle conv of the fp16-rounded product within the tolerance. Shapes cover odd
+    pixel counts per image (padding columns), several images per tile, K tails, residual."""
+    lib = V.vkhip()
+    N, C, H, W, Co = shape
+    r = rng(700 + tile + C)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    s = round_half(r.uniform(0.0, 1.0, (N, C, 1, 1)))
+    w = (r.standard_normal((Co, C, 1, 1)) * 0.1).astype(np.float32)
+    b = (r.standard_normal(Co) * 0.1).astype(np.float32)
+    res = round_half(r.standard_normal((N, Co, H, W)))
+    d, yshape = conv_desc(x.shape, w.shape, act=1, has_res=1)
+    d.in_scale = 1
+    plan = V.ConvPlan()
+    rc = lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, tile, 0, ctypes.byref(plan))
+    if rc:
+        pytest.skip(f"tile {tile} takes no input scale at {shape}: {lib.vkhip_last_error().decode()}")
+    blob = np.zeros(plan.weight_bytes, np.uint8)
+    check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(plan), w.ctypes.data, b.ctypes.data, blob.ctypes.data))
+    dblob = DeviceBuffer.from_array(blob)
+    dx, ds, dres = to_device_nc4(x), to_device_nc4(s), to_device_nc4(res)
+    nbytes = V.nc4_elems(*yshape) * 2
+    dy = DeviceBuffer(nbytes)
+    check(lib.vkhip_conv_forward_scaled(ctypes.byref(d), ctypes.byref(plan), dx.ptr, ds.ptr, dblob.ptr, dres.ptr, dy.ptr, None, None))
+    # the unfused pair: channel-broadcast Mul into an fp16 tensor, then the same plan without scale
+    dt = DeviceBuffer(V.nc4_elems(N, C, H, W) * 2)
+    check(lib.vkhip_channel_scale(dx.ptr, ds.ptr, dt.ptr, N, C, H * W, None))
+    d0, _ = conv_desc(x.shape, w.shape, act=1, has_res=1)
+    dy0 = DeviceBuffer(nbytes)
+    check(lib.vkhip_conv_forward(ctypes.byref(d0), ctypes.byref(plan), dt.ptr, dblob.ptr, dres.ptr, dy0.ptr, None, None))
+    check(lib.vkhip_stream_sync(None))
+    a, u = dy.download(np.uint16, nbytes // 2), dy0.download(np.uint16, nbytes // 2)
+    assert np.array_equal(a, u), f"{np.count_nonzero(a != u)} of {a.size} fp16 values differ from Mul + conv"
+    got = from_device_nc4(dy, yshape)
+    assert_parity(got, oracle_conv(round_half(x * s), w, b, res=res, act=1), f"input-scale conv tile {tile} {shape}")
+
+
+def test_conv_input_scale_rejects_other_shapes(gpu):
+    lib = V.vkhip()
+    for wshape, stride in [((8, 16, 3, 3), (1, 1)), ((8, 16, 1, 1), (2, 2))]:
+        d, _ = conv_desc((2, 16, 8, 8), wshape, stride=stride, pads=(1, 1, 1, 1) if wshape[2] == 3 else (0, 0, 0, 0))
+        d.in_scale = 1
+        plan = V.ConvPlan()
+        assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_AUTO, -1, 0, ctypes.byref(plan)) == 2

@@ -144,6 +144,22 @@ def test_config3_mobilenetv3_large(gpu, opts):
     check_outputs(sess.run(x), oracle_model_run("mobilenetv3_large", 1, 7, x), sess.out_elems, f"config3[{opts}]")
 
 
+@pytest.mark.parametrize("opts", ["", "fuse_se=1"])
+def test_se_scale_folded_into_projection(gpu, opts, monkeypatch):
+    """The squeeze-excite channel scale of every MobileNetV3 block is folded into its projection
+    conv (no separate Mul launch) and the result matches both the oracle and the unfolded session."""
+    sess = V.Session("mobilenetv3_large", 2, seed=7, options=opts)
+    plan = sess.describe()
+    assert plan.count("+input scale") == 8 and plan.count("scale folded into") == 8, plan
+    x = make_input(sess.in_shape, 4)
+    got = sess.run(x)
+    check_outputs(got, oracle_model_run("mobilenetv3_large", 2, 7, x), sess.out_elems, f"config3 b2 folded[{opts}]")
+    monkeypatch.setenv("VKNN_HIP_FOLD_SCALE", "0")
+    plain = V.Session("mobilenetv3_large", 2, seed=7, options=opts)
+    assert "+input scale" not in plain.describe()
+    check_outputs(got, plain.run(x), sess.out_elems, f"config3 b2 folded vs unfolded[{opts}]")
+
+
 def test_config3_mobilenetv3_large_b128_items(gpu):
     check_batch_items("mobilenetv3_large", 128, (0, 127), 7, "fuse_se=1;fuse_dwpw=1")
 

@@ -30,7 +30,7 @@ CONV_AUTO, CONV_GEMM, CONV_SPLITK, CONV_WINOGRAD, CONV_DEPTHWISE = 0, 1, 2, 3, 4
 class ConvDesc(ctypes.Structure):
     _fields_ = [(n, c_i32) for n in ("N", "Cin", "H", "W", "Cout", "OH", "OW", "KH", "KW", "SH", "SW", "PT",
                                      "PL", "DH", "DW", "group", "act")] + \
-               [("act_lo", c_f), ("act_hi", c_f), ("has_res", c_i32)]
+               [("act_lo", c_f), ("act_hi", c_f), ("has_res", c_i32), ("in_scale", c_i32)]
 
 
 class ConvPlan(ctypes.Structure):
@@ -86,6 +86,7 @@ VKHIP_API = {
     "vkhip_conv_pack_weights": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp]),
     "vkhip_conv_forward": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_forward_noalloc": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "vkhip_conv_forward_scaled": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_dwpw_supported": (c_int, [P(DwPwDesc)]),
     "vkhip_dwpw_weight_bytes": (c_sz, [P(DwPwDesc)]),
     "vkhip_dwpw_pack_weights": (c_int, [P(DwPwDesc), c_vp, c_vp, c_vp, c_vp, c_vp]),
@@ -93,7 +94,8 @@ VKHIP_API = {
     "vkhip_global_avg_pool": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "vkhip_se_weight_bytes": (c_sz, [c_i64, c_i64]),
     "vkhip_se_pack_weights": (c_int, [c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
-    "vkhip_fused_se": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_f, c_f, c_vp]),
+    "vkhip_se_workspace_bytes": (c_sz, [c_i64, c_i64]),
+    "vkhip_fused_se": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_f, c_f, c_vp, c_vp]),
     "vkhip_channel_scale": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp]),
     "vkhip_add": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i32, c_f, c_f, c_vp]),
     "vkhip_unary": (c_int, [c_vp, c_vp, c_i64, c_i32, c_f, c_f, c_vp]),

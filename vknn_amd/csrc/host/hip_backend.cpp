@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -77,6 +78,7 @@ namespace vknn {
             std::string k = gpuTag() + "/conv";
             for (int v: {d.N, d.Cin, d.H, d.W, d.Cout, d.OH, d.OW, d.KH, d.KW, d.SH, d.SW, d.PT, d.PL, d.DH, d.DW, d.group, d.has_res, mode})
                 k += "_" + std::to_string(v);
+            if (d.in_scale) k += "_xs";
             return k;
         }
         // (algo, tile, ksplit) <-> one i32 table value: algo in bits 0-7, tile+1 in 8-15, ksplit in 16-23
@@ -89,10 +91,14 @@ namespace vknn {
             vkhip_conv_plan         plan {};
             std::shared_ptr<DevBuf> blob, ws;
             TensorId                in = kNoTensor, out = kNoTensor, res = kNoTensor;
+            // Set by the segment before prepare when a channel-broadcast Mul (the squeeze-excite
+            // scale) is folded into this conv: the conv reads the Mul's unscaled operand `scaledIn`
+            // and multiplies it by `xscale` ([N,C,1,1]) on the way into the GEMM.
+            TensorId                scaledIn = kNoTensor, xscale = kNoTensor;
 
             void prepare(const Node &node, SegEnv &env) override {
                 const Graph &g = *env.graph;
-                in             = node.inputs[0];
+                in             = scaledIn != kNoTensor ? scaledIn : node.inputs[0];
                 out            = node.outputs[0];
                 res            = node.fusedResidual;
                 NCHW         x  = NCHW::from(g.desc(in).shape);
@@ -108,6 +114,7 @@ namespace vknn {
                 d.group = (int) node.attr.geti("group", 1);
                 d.act = (int) node.fusedAct; d.act_lo = node.actLo; d.act_hi = node.actHi;
                 d.has_res = res != kNoTensor;
+                d.in_scale = xscale != kNoTensor;
                 kind  = d.group > 1 ? "dwconv" : "conv";
                 flops = 2.0 * d.N * d.Cout * (double) (d.Cin / d.group) * d.KH * d.KW * d.OH * d.OW;
                 bytes = (int64_t) (nc4Bytes(g.desc(in).shape) + nc4Bytes(g.desc(out).shape) * (d.has_res ? 2 : 1)) +
@@ -199,6 +206,10 @@ namespace vknn {
                         t.r = std::make_shared<DevBuf>(ybytes);
                         check(vkhip_fill_zero(t.r->ptr, ybytes, nullptr), "tune fill");
                     }
+                    if (d.in_scale) {
+                        t.s = std::make_shared<DevBuf>(nc4Bytes({d.N, d.Cin, 1, 1}));
+                        check(vkhip_fill_zero(t.s->ptr, t.s->bytes, nullptr), "tune fill");
+                    }
                     sets.push_back(t);
                 }
                 // two rounds: every candidate briefly, then the four fastest again with more
@@ -244,7 +255,7 @@ namespace vknn {
             }
 
             struct TuneSet {
-                std::shared_ptr<DevBuf> x, y, r;
+                std::shared_ptr<DevBuf> x, y, r, s;
             };
 
             // min over reps timings of 6 back-to-back launches, each on the next buffer set
@@ -256,7 +267,7 @@ namespace vknn {
                 size_t k   = 0;
                 auto   run = [&]() {
                     const TuneSet &t = sets[k++ % sets.size()];
-                    return vkhip_conv_forward(&d, &p, t.x->ptr, bl->ptr, t.r ? t.r->ptr : nullptr, t.y->ptr, wsb ? wsb->ptr : nullptr, nullptr);
+                    return forward(p, t.x->ptr, t.s ? t.s->ptr : nullptr, bl->ptr, t.r ? t.r->ptr : nullptr, t.y->ptr, wsb ? wsb->ptr : nullptr, nullptr);
                 };
                 vkhip_event_t e0, e1;
                 check(vkhip_event_create(&e0), "event");
@@ -279,15 +290,20 @@ namespace vknn {
                 return best;
             }
 
+            int forward(const vkhip_conv_plan &p, const void *x, const void *xs, const void *bl, const void *r, void *y, void *w, vkhip_stream_t s) {
+                return d.in_scale ? vkhip_conv_forward_scaled(&d, &p, x, xs, bl, r, y, w, s) : vkhip_conv_forward(&d, &p, x, bl, r, y, w, s);
+            }
+
             void record(SegEnv &env, vkhip_stream_t s) override {
-                check(vkhip_conv_forward(&d, &plan, env.dev(in), blob->ptr, res != kNoTensor ? env.dev(res) : nullptr, env.dev(out),
-                                         ws ? ws->ptr : nullptr, s),
+                check(forward(plan, env.dev(in), xscale != kNoTensor ? env.dev(xscale) : nullptr, blob->ptr,
+                              res != kNoTensor ? env.dev(res) : nullptr, env.dev(out), ws ? ws->ptr : nullptr, s),
                       "conv " + name);
             }
 
             std::string describe() const override {
                 static const char *algos[] = {"auto", "gemm", "splitk", "winograd", "depthwise"};
-                return std::string(algos[plan.algo]) + " tile=" + std::to_string(plan.tile) + " ksplit=" + std::to_string(plan.ksplit);
+                return std::string(algos[plan.algo]) + " tile=" + std::to_string(plan.tile) + " ksplit=" + std::to_string(plan.ksplit) +
+                       (d.in_scale ? " +input scale" : "");
             }
         };
 
@@ -389,7 +405,7 @@ namespace vknn {
 
         // ------------------------------------------------------------ fused SE middle
         struct SeOp: HipOp {
-            std::shared_ptr<DevBuf> blob;
+            std::shared_ptr<DevBuf> blob, ws;
             TensorId                in, out;
             int64_t                 N, C, Cr;
             float                   alpha, beta;
@@ -405,11 +421,12 @@ namespace vknn {
                                             initF32(g, node.inputs[4]), host.data()),
                       "se pack");
                 blob  = upload(host.data(), host.size());
+                ws    = std::make_shared<DevBuf>(vkhip_se_workspace_bytes(N, Cr));
                 kind  = "se";
                 flops = 4.0 * N * C * Cr;
             }
             void record(SegEnv &env, vkhip_stream_t s) override {
-                check(vkhip_fused_se(env.dev(in), blob->ptr, env.dev(out), N, C, Cr, alpha, beta, s), "fused_se " + name);
+                check(vkhip_fused_se(env.dev(in), blob->ptr, env.dev(out), N, C, Cr, alpha, beta, ws->ptr, s), "fused_se " + name);
             }
         };
 
@@ -685,6 +702,62 @@ namespace vknn {
             void record(SegEnv &, vkhip_stream_t) override {}
         };
 
+        // A channel-broadcast Mul folded into the conv that consumes it (ConvOp::xscale): no launch.
+        struct FoldedMulOp: HipOp {
+            std::string into;
+            void        prepare(const Node &, SegEnv &) override { kind = "folded"; }
+            void        record(SegEnv &, vkhip_stream_t) override {}
+            std::string describe() const override { return "scale folded into " + into; }
+        };
+
+        // Squeeze-excite scale folding: y = Mul(h, s) with s of shape [N,C,1,1] (the SE branch output)
+        // whose only reader is a dense 1x1 stride-1 pad-0 conv of the same segment becomes that conv's
+        // input scale, so h*s is never written (the reference runs the Mul as its own Binary op,
+        // ops/binary.cpp:32-43; the product is rounded to fp16 exactly as that op's store does).
+        // Returns conv node -> (h, s) and the set of folded Mul nodes.
+        static void planScaleFolds(const Graph &g, const std::vector<int> &idx, std::map<int, std::pair<TensorId, TensorId>> &conv,
+                                   std::set<int> &muls) {
+            std::set<int>           inSeg(idx.begin(), idx.end());
+            std::map<TensorId, int> readers;
+            for (const Node &nd: g.nodes) {
+                for (TensorId t: nd.inputs)
+                    if (t != kNoTensor) ++readers[t];
+                if (nd.fusedResidual != kNoTensor && std::find(nd.inputs.begin(), nd.inputs.end(), nd.fusedResidual) == nd.inputs.end())
+                    ++readers[nd.fusedResidual];
+            }
+            for (TensorId t: g.outputs) readers[t] += 1000; // a graph output is never folded away
+            for (int i: idx) {
+                const Node &m = g.nodes[i];
+                if (m.type != OpType::Binary || m.subOp != (int) BinaryType::Mul || m.inputs.size() != 2) continue;
+                TensorId     h = m.inputs[0], sc = m.inputs[1];
+                const Shape &sh = g.desc(h).shape, &ss = g.desc(sc).shape;
+                if (g.isInitializer(h) || g.isInitializer(sc) || sh.size() != 4 || ss.size() != 4) continue;
+                const Shape *ph = &sh, *ps = &ss;
+                if (sh[2] * sh[3] == 1 && ss[2] * ss[3] != 1) std::swap(h, sc), std::swap(ph, ps);
+                if ((*ph)[0] != (*ps)[0] || (*ph)[1] != (*ps)[1] || (*ps)[2] * (*ps)[3] != 1 || (*ph)[2] * (*ph)[3] == 1) continue;
+                const TensorId t = m.outputs[0];
+                if (readers[t] != 1) continue;
+                for (int j: idx) {
+                    const Node &c = g.nodes[j];
+                    if (c.type != OpType::Conv || c.inputs.empty() || c.inputs[0] != t || c.fusedResidual == t) continue;
+                    const Shape &w = g.desc(c.inputs[1]).shape;
+                    auto st = attrInts(c, "strides", {1, 1}), pad = attrInts(c, "pads", {0, 0, 0, 0});
+                    if (c.attr.geti("group", 1) != 1 || w.size() != 4 || w[2] != 1 || w[3] != 1 || st[0] != 1 || st[1] != 1 ||
+                        pad[0] != 0 || pad[1] != 0 || pad[2] != 0 || pad[3] != 0 || !inSeg.count(j))
+                        break;
+                    vkhip_conv_desc d {};
+                    NCHW x = NCHW::from(sh);
+                    d.N = (int) x.n; d.Cin = (int) x.c; d.H = d.OH = (int) x.h; d.W = d.OW = (int) x.w; d.Cout = (int) w[0];
+                    d.KH = d.KW = d.SH = d.SW = d.DH = d.DW = d.group = 1; d.in_scale = 1;
+                    vkhip_conv_plan p;
+                    if (vkhip_conv_plan_make(&d, VKHIP_CONV_GEMM, -1, 0, &p) != VKHIP_OK) break; // shape the scaled kernel does not take
+                    conv[j] = {h, sc};
+                    muls.insert(i);
+                    break;
+                }
+            }
+        }
+
         static bool isAliasOp(const Graph &g, const Node &nd) {
             // ConvertLayout (reference ops/convert_layout.cpp) changes only the physical layout of
             // the same logical NCHW tensor; this backend keeps every activation NC4HW4 fp16, so
@@ -744,20 +817,51 @@ namespace vknn {
                 for (TensorId t: nd.outputs)
                     if (t != kNoTensor && !bufs_.count(t)) bufs_[t] = std::make_shared<DevBuf>(nc4Bytes(g.desc(t).shape));
             }
+            std::map<int, std::pair<TensorId, TensorId>> scaled;
+            std::set<int>                                folded;
+            // VKNN_HIP_FOLD_SCALE=0 keeps every Mul as its own launch (A/B measurements)
+            const char *fold_env = std::getenv("VKNN_HIP_FOLD_SCALE");
+            if (!fold_env || std::string(fold_env) != "0") planScaleFolds(g, idx, scaled, folded);
+            std::map<int, std::string> foldedInto;
+            for (auto &kv: scaled)
+                for (int m: folded)
+                    if (g.nodes[m].outputs[0] == g.nodes[kv.first].inputs[0]) foldedInto[m] = g.nodes[kv.first].name;
             std::vector<std::vector<TensorId>> ins, outs;
             for (int i: idx) {
                 const Node &nd = g.nodes[i];
-                auto        op = makeOp(g, nd);
+                std::unique_ptr<HipOp> op;
+                if (folded.count(i)) {
+                    auto f  = std::make_unique<FoldedMulOp>();
+                    f->into = foldedInto[i];
+                    op      = std::move(f);
+                } else op = makeOp(g, nd);
                 if (!op) throw Error(Status::Unsupported, std::string("HIP backend has no kernel for ") + opTypeName(nd.type) + " (" + nd.name + ")");
+                auto sit = scaled.find(i);
+                if (sit != scaled.end()) {
+                    auto *c     = static_cast<ConvOp *>(op.get());
+                    c->scaledIn = sit->second.first;
+                    c->xscale   = sit->second.second;
+                }
                 op->name = nd.name;
                 op->type = nd.type;
                 op->prepare(nd, env_);
                 ops_.push_back(std::move(op));
-                // data the op's launches read and write (alias ops launch nothing)
+                // data the op's launches read and write (alias and folded ops launch nothing)
                 std::vector<TensorId> in, out;
+                if (folded.count(i)) {
+                    ins.push_back(in);
+                    outs.push_back(out);
+                    continue;
+                }
                 if (!isAliasOp(g, nd)) {
-                    for (TensorId t: nd.inputs)
+                    if (sit != scaled.end()) {
+                        in.push_back(resolve(sit->second.first));
+                        in.push_back(resolve(sit->second.second));
+                    }
+                    for (size_t k = sit != scaled.end() ? 1 : 0; k < nd.inputs.size(); ++k) {
+                        TensorId t = nd.inputs[k];
                         if (t != kNoTensor && !g.isInitializer(t)) in.push_back(resolve(t));
+                    }
                     if (nd.fusedResidual != kNoTensor) in.push_back(resolve(nd.fusedResidual));
                     for (TensorId t: nd.outputs)
                         if (t != kNoTensor) out.push_back(resolve(t));

@@ -25,6 +25,7 @@ namespace vkhip {
                 return v * c / 6.f;
             }
             case VKHIP_ACT_SILU: return v / (1.f + __expf(-v));
+            case VKHIP_ACT_HARDSIGMOID: return fminf(fmaxf(lo * v + hi, 0.f), 1.f);
             default: return v;
         }
     }

@@ -403,12 +403,12 @@ namespace vkhip {
     // ------------------------------------------------------------------ host side: plans
 
     // the kernel of tile `tile` (kTiles), by family
-    static GemmKernelFn gemm_kernel_for(int tile, int bmode, int steps, int nbi = 0) {
+    static GemmKernelFn gemm_kernel_for(int tile, int bmode, int steps, int nbi = 0, bool xs = false) {
         if (tile < 0 || tile >= kNumTiles) return nullptr;
         switch (kTiles[tile].kind) {
             case 0: return gemm_tile_kernel(tile, bmode);
             case 1: return bd_tile_kernel(tile, bmode);
-            case 2: return dma_tile_kernel(tile, bmode, steps);
+            case 2: return dma_tile_kernel(tile, bmode, steps, xs);
             case 3: return halo_tile_kernel(tile, nbi);
             case 4: return stem_tile_kernel(tile, bmode, nbi);
         }
@@ -635,6 +635,20 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
     }
     if (d->group != 1) return set_error(VKHIP_ERR_UNSUPPORTED, "grouped conv");
     if (algo == VKHIP_CONV_DEPTHWISE) return set_error(VKHIP_ERR_INVALID, "depthwise algorithm on a dense conv");
+    if (d->in_scale) {
+        // the scale rides on the dense-B (LDS-DMA) kernel: 1x1, stride 1, no padding, no split-K
+        if (d->KH != 1 || d->KW != 1 || d->SH != 1 || d->SW != 1 || d->PT != 0 || d->PL != 0 || d->OH != d->H || d->OW != d->W)
+            return set_error(VKHIP_ERR_UNSUPPORTED, "input scale needs a 1x1 stride-1 pad-0 conv");
+        if (algo == VKHIP_CONV_AUTO) algo = VKHIP_CONV_GEMM;
+        if (algo != VKHIP_CONV_GEMM) return set_error(VKHIP_ERR_UNSUPPORTED, "input scale runs the GEMM algorithm only");
+        if (tile < 0) tile = 14;
+        if (tile >= kNumTiles || kTiles[tile].kind != 2 || !dma_tile_kernel(tile, 0, 1, true))
+            return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d has no input-scale variant", tile);
+        // a workgroup's columns may cover at most 8 images (the scale slice of a stage)
+        const int64_t hwp = (int64_t) d->OH * d->OW + ((int64_t) d->OH * d->OW & 1);
+        if (ceil_div(kTiles[tile].BN - 1, hwp) > 7)
+            return set_error(VKHIP_ERR_UNSUPPORTED, "input scale: tile %d spans more than 8 images of %lld pixels", tile, (long long) hwp);
+    }
     if (algo == VKHIP_CONV_WINOGRAD && !wino_eligible(d))
         return set_error(VKHIP_ERR_INVALID, "Winograd F(2,3) needs 3x3 stride 1 pad 1 dilation 1");
     if (algo == VKHIP_CONV_AUTO) {
@@ -725,8 +739,11 @@ int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
     return VKHIP_OK;
 }
 
-int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res,
-                       void *y, void *workspace, vkhip_stream_t s) {
+} // extern "C"
+
+// The forward pass of every conv algorithm; xs is the input scale of an in_scale plan (or null).
+static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *xs, const void *blob,
+                             const void *res, void *y, void *workspace, vkhip_stream_t s) {
     if (!d || !plan || !x || !blob || !y) return set_error(VKHIP_ERR_INVALID, "conv_forward: null argument");
     if (d->has_res && !res) return set_error(VKHIP_ERR_INVALID, "conv_forward: has_res without a residual tensor");
     if (plan->workspace_bytes && !workspace) return set_error(VKHIP_ERR_INVALID, "conv_forward: plan needs a workspace");
@@ -793,7 +810,7 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     a.m_tiles = (int) g.m_tiles;
     const int split_steps = plan->algo == VKHIP_CONV_SPLITK ? (int) ceil_div(g.nsteps, plan->ksplit) : (int) g.nsteps;
     GemmKernelFn fn = gemm_kernel_for(plan->tile, g.bmode, split_steps,
-                                      t.kind == 3 ? halo_nbi(d, t) * (d->W % 2 ? -1 : 1) : (t.kind == 4 ? stem_nbi(d, t) : 0));
+                                      t.kind == 3 ? halo_nbi(d, t) * (d->W % 2 ? -1 : 1) : (t.kind == 4 ? stem_nbi(d, t) : 0), d->in_scale != 0);
     if (!fn) return set_error(VKHIP_ERR_INVALID, "conv_forward: no kernel for tile %d", plan->tile);
 
     if (wino) {
@@ -827,6 +844,8 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     }
 
     a.x  = (const uint2 *) x;
+    a.xs = (const uint2 *) xs;
+    a.xs_bytes = (unsigned) ((int64_t) d->N * g.Cinb * 8);
     a.x_bytes = (unsigned) ((int64_t) d->N * g.Cinb * d->H * d->W * 8);
     a.y_bytes = (unsigned) ((int64_t) d->N * g.Coutb * d->OH * d->OW * 8);
     a.y  = (uint2 *) y;
@@ -855,6 +874,20 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
     dim3 grid((unsigned) (g.m_tiles * g.n_tiles), 1, 1);
     fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
     return check_launch("conv_gemm");
+}
+
+extern "C" {
+
+int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res,
+                       void *y, void *workspace, vkhip_stream_t s) {
+    if (d && d->in_scale) return set_error(VKHIP_ERR_INVALID, "conv_forward: an in_scale plan runs through vkhip_conv_forward_scaled");
+    return conv_forward_impl(d, plan, x, nullptr, blob, res, y, workspace, s);
+}
+
+int vkhip_conv_forward_scaled(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *xs, const void *blob,
+                              const void *res, void *y, void *workspace, vkhip_stream_t s) {
+    if (!d || !xs || !d->in_scale) return set_error(VKHIP_ERR_INVALID, "conv_forward_scaled: needs an in_scale plan and a scale tensor");
+    return conv_forward_impl(d, plan, x, xs, blob, res, y, workspace, s);
 }
 
 int vkhip_conv_forward_noalloc(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob,

@@ -5,12 +5,12 @@ namespace vkhip {
 
     // conv_dma_kernel with its LDS ring cut to the number of K stages one split runs (fewer stages
     // need no deeper ring; the smaller LDS footprint lets more workgroups share a CU).
-    template <int FM, int FN, int NS, int WM, int WN, int PS = 8>
+    template <int FM, int FN, int NS, int WM, int WN, int PS = 8, bool XS = false>
     static GemmKernelFn pick_dma_ps(int steps) {
         if constexpr (NS > 1) {
-            if (steps < NS) return pick_dma_ps<FM, FN, NS - 1, WM, WN, PS>(steps);
+            if (steps < NS) return pick_dma_ps<FM, FN, NS - 1, WM, WN, PS, XS>(steps);
         }
-        return conv_dma_kernel<FM, FN, NS, WM, WN, PS>;
+        return conv_dma_kernel<FM, FN, NS, WM, WN, PS, XS>;
     }
     // bmode 2 = stride-2 columns (16 bytes per B column)
     template <int FM, int FN, int NS, int WM, int WN>
@@ -25,7 +25,18 @@ namespace vkhip {
 
     // the smallest band-size instantiation (NBIS ascending) that holds nbi chunks per slot
     // nbi < 0: odd input width (the ODD variant), |nbi| chunks
-    GemmKernelFn dma_tile_kernel(int tile, int bmode, int steps) {
+    // xs: the input-scale variant (only the tiles that win on squeeze-excite projections)
+    GemmKernelFn dma_tile_kernel(int tile, int bmode, int steps, bool xs) {
+        if (xs) {
+            if (bmode == 2) return nullptr;
+            switch (tile) {
+                case 14: return pick_dma_ps<2, 2, 2, 2, 2, 8, true>(steps);
+                case 16: return pick_dma_ps<2, 2, 4, 2, 2, 8, true>(steps);
+                case 24: return pick_dma_ps<1, 2, 2, 2, 2, 8, true>(steps);
+                case 25: return pick_dma_ps<2, 2, 2, 1, 4, 8, true>(steps);
+            }
+            return nullptr;
+        }
         switch (tile) {
             case 11: return pick_dma<4, 4, 2, 2, 2>(steps, bmode);
             case 12: return pick_dma<4, 2, 2, 2, 4>(steps, bmode);

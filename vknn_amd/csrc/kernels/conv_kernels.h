@@ -51,6 +51,8 @@ namespace vkhip {
         long long     x_bstride, w_bstride, y_bstride; // batch (blockIdx.z) strides: uint2 / half / uint2
         unsigned      x_bytes;                         // bytes of one batch slice of x (< 2 GiB)
         unsigned      y_bytes;                         // bytes of one batch slice of y (< 2 GiB)
+        const uint2  *xs;                              // input channel scale [N][Cinb] x 4 fp16 (in_scale)
+        unsigned      xs_bytes;                        // bytes of xs
     };
 
     enum { OMODE_EPILOGUE = 0, OMODE_RAW = 1, OMODE_PARTIAL = 2 };
@@ -851,7 +853,12 @@ namespace vkhip {
     // PS = 16: stride-2 1x1 convs. Each lane copies one output pixel's input pixel (2oy, 2ox)
     // together with its right neighbour (16 bytes, the neighbour unused), so B columns sit 16 bytes
     // apart in LDS.
-    template <int FM, int FN, int NS, int WM, int WN, int PS = 8>
+    // XS: the input is scaled per (image, channel) first (a squeeze-excite scale folded into the
+    // conv that consumes it). Each stage then also copies the scale slice of its 64 K values for
+    // up to 8 consecutive images (lane l: image l/8, halves (l%8)*8..+7) into 1 KB after the B
+    // stage, and every B fragment is multiplied by the scales of its column's image before the
+    // MFMA (fp16 products, rounded like the separate Mul's fp16 store).
+    template <int FM, int FN, int NS, int WM, int WN, int PS = 8, bool XS = false>
     __global__ __launch_bounds__(64 * WM * WN, 1) void conv_dma_kernel(GemmArgs a) {
         constexpr int NW     = WM * WN; // waves
         constexpr int BM     = 32 * FM * WM;
@@ -863,7 +870,10 @@ namespace vkhip {
         constexpr int NB     = BSTAGE / (NW * 1024);
         static_assert(NA >= 1 && NB >= 1 && ASTAGE % (NW * 1024) == 0 && BSTAGE % (NW * 1024) == 0, "stage split");
         constexpr int BPB    = BN * PS / 1024; // 1 KB pixel blocks per slot row of the B stage
-        __shared__ __attribute__((aligned(16))) unsigned char sm[NS][ASTAGE + BSTAGE];
+        constexpr int SSTAGE = XS ? 1024 : 0;  // scale slice of the stage
+        constexpr int STAGE  = ASTAGE + BSTAGE + SSTAGE;
+        static_assert(!XS || PS == 8, "input scale on dense stride-1 columns only");
+        __shared__ __attribute__((aligned(16))) unsigned char sm[NS * STAGE + (XS ? 1024 : 0)]; // + spare for the idle scale copies
 
         const int tid  = threadIdx.x;
         const int lane = tid & 63;
@@ -909,8 +919,14 @@ namespace vkhip {
                 pbase[pb]    = p < a.P ? (unsigned) ((n * a.Cinb * a.HW + (a.SH * oy) * a.W + a.SW * (r - oy * a.OW)) * 8) : kInvalid;
             }
         }
+        // XS: images n_first .. n_first+7 of the scale table; lane l copies image n_first + l/8
+        const int      n_first = n0 / a.OHWp;
+        const unsigned xs_row  = (unsigned) a.Cinb * 8u;
+        const int      img     = n_first + (lane >> 3);
+        const unsigned sbase   = XS && img * a.OHWp < a.Pv ? (unsigned) img * xs_row : kInvalid;
+        const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc((void *) (XS ? a.xs : a.x), (short) 0, XS ? (int) a.xs_bytes : 0, 0x00020000);
         auto issue = [&](int ks, int buf) __attribute__((always_inline)) {
-            unsigned char *dst = sm[buf];
+            unsigned char *dst = sm + buf * STAGE;
 #pragma unroll
             for (int r = 0; r < NA; ++r) {
                 const int chunk = (r * NW + wave) * 1024;
@@ -925,6 +941,14 @@ namespace vkhip {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void *) (dst + ASTAGE + c * 1024), 16, vo,
                                                          (unsigned) (slot * hw8), 0, 0);
             }
+            if constexpr (XS) {
+                // every wave issues one copy so the per-wave copy counts (the vmcnt waits) stay
+                // equal; waves other than 0 copy nothing into the spare block
+                const int  k0  = ks * kBK + (lane & 7) * 8;
+                const bool ok  = wave == 0 && sbase != kInvalid && k0 < a.Kslots * 4;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (__attribute__((address_space(3))) void *) (wave == 0 ? dst + ASTAGE + BSTAGE : sm + NS * STAGE),
+                                                         16, ok ? sbase + (unsigned) (k0 * 2) : kInvalid, 0, 0, 0);
+            }
         };
 
         float16v acc[FM][FN];
@@ -936,9 +960,17 @@ namespace vkhip {
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
         const int g = lane >> 5;
+        // XS: byte offset of each fragment column's image row in the stage's scale slice
+        int simg[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int p = n0 + wn0 + 32 * j + (lane & 31);
+            simg[j]     = (p < a.Pv ? p / a.OHWp - n_first : 0) * (kBK * 2) + g * 16;
+        }
         auto compute = [&](int buf, int next_ks, int next_buf) __attribute__((always_inline)) {
-            const unsigned char *Ab = sm[buf] + ((wmi * FM) * 64 + lane) * 16;
-            const unsigned char *Bb = sm[buf] + ASTAGE + (2 * g * BN + wn0 + (lane & 31)) * PS;
+            const unsigned char *Ab = sm + buf * STAGE + ((wmi * FM) * 64 + lane) * 16;
+            const unsigned char *Bb = sm + buf * STAGE + ASTAGE + (2 * g * BN + wn0 + (lane & 31)) * PS;
+            const unsigned char *Sb = sm + buf * STAGE + ASTAGE + BSTAGE;
             half8 fa[2][FM], fb[2][FN];
             auto rd = [&](int kk, int d) __attribute__((always_inline)) {
 #pragma unroll
@@ -946,6 +978,8 @@ namespace vkhip {
                     const u32x2 lo = *reinterpret_cast<const u32x2 *>(Bb + (kk * 4 * BN + 32 * j) * PS);
                     const u32x2 hi = *reinterpret_cast<const u32x2 *>(Bb + ((kk * 4 + 1) * BN + 32 * j) * PS);
                     fb[d][j] = __builtin_bit_cast(half8, u32x4_make(lo.x, lo.y, hi.x, hi.y));
+                    // halves (kk*4 + 2g)*4 .. +8 of the column's image: slots 2g, 2g+1 of step kk
+                    if constexpr (XS) fb[d][j] *= *reinterpret_cast<const half8 *>(Sb + simg[j] + kk * 32);
                 }
 #pragma unroll
                 for (int i = 0; i < FM; ++i) fa[d][i] = *reinterpret_cast<const half8 *>(Ab + (kk * MF + i) * 1024);
@@ -964,8 +998,8 @@ namespace vkhip {
 #pragma unroll
                     for (int j = 0; j < FN; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk & 1][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
-                if (kk == 0) StepSchedule<0, FM * FN, FM + 2 * FN, 4 * FN, NA + NB>::apply();
-                else if (kk < 3) StepSchedule<0, FM * FN, FM + 2 * FN, 4 * FN>::apply();
+                if (kk == 0) StepSchedule<0, FM * FN, FM + (XS ? 3 : 2) * FN, (XS ? 8 : 4) * FN, NA + NB + (XS ? 1 : 0)>::apply();
+                else if (kk < 3) StepSchedule<0, FM * FN, FM + (XS ? 3 : 2) * FN, (XS ? 8 : 4) * FN>::apply();
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
@@ -973,7 +1007,8 @@ namespace vkhip {
         // NS LDS stages, prefetch distance NS-1: stage ks waits for its own copies (the NS-2 later
         // stages may stay in flight), barriers (all waves' copies landed; all waves done with
         // stage ks-1, whose buffer the next issue refills), issues stage ks+NS-1, computes.
-        constexpr int kAhead = NS < 2 ? 0 : ((NS - 2) * (NA + NB) < 63 ? (NS - 2) * (NA + NB) : 63);
+        constexpr int NPW    = NA + NB + (XS ? 1 : 0); // copies per wave per stage
+        constexpr int kAhead = NS < 2 ? 0 : ((NS - 2) * NPW < 63 ? (NS - 2) * NPW : 63);
         constexpr int kWait  = (kAhead & 15) | (7 << 4) | (15 << 8) | ((kAhead >> 4) << 14);
         if constexpr (NS == 1) {
             // one stage (GEMMs with a single K stage per split): copy, wait, compute; no LDS ring,
@@ -1401,7 +1436,7 @@ namespace vkhip {
     // template instantiations compile in parallel). bmode / steps / nbi as in gemm_kernel_for.
     GemmKernelFn gemm_tile_kernel(int tile, int bmode);
     GemmKernelFn bd_tile_kernel(int tile, int bmode);
-    GemmKernelFn dma_tile_kernel(int tile, int bmode, int steps);
+    GemmKernelFn dma_tile_kernel(int tile, int bmode, int steps, bool xs);
     GemmKernelFn halo_tile_kernel(int tile, int nbi);
     GemmKernelFn stem_tile_kernel(int tile, int bmode, int nbi);
 

@@ -222,44 +222,6 @@ namespace vkhip {
         if (w < NCb && lane == 0) y[w] = h4_as_u2(f4_to_h4(s / (float) HW));
     }
 
-    // Fused SE middle, one workgroup per image: s1 = relu(W1 avg + b1); s = clamp(alpha*(W2 s1 +
-    // b2) + beta, 0, 1). Dot products are split across the wave and reduced with shuffles.
-    __global__ __launch_bounds__(256) void fused_se_kernel(const half_t *avg, const float *blob, half_t *y, int C, int Cr,
-                                                           float alpha, float beta) {
-        extern __shared__ float sm[];
-        float *a  = sm;      // [C]
-        float *s1 = sm + C;  // [Cr]
-        const int    n  = blockIdx.x;
-        const int    Cp = ((C + 3) / 4) * 4;
-        const float *W1 = blob;
-        const float *b1 = W1 + (int64_t) Cr * C;
-        const float *W2 = b1 + Cr;
-        const float *b2 = W2 + (int64_t) C * Cr;
-        for (int c = threadIdx.x; c < C; c += blockDim.x) a[c] = (float) avg[(int64_t) n * Cp + c];
-        __syncthreads();
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-        for (int j = wave; j < Cr; j += nw) {
-            float acc = 0.f;
-            for (int c = lane; c < C; c += 64) acc += W1[(int64_t) j * C + c] * a[c];
-            for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-            if (lane == 0) {
-                float v = acc + b1[j];
-                s1[j]   = v > 0.f ? v : 0.f;
-            }
-        }
-        __syncthreads();
-        for (int k = wave; k < C; k += nw) {
-            float acc = 0.f;
-            for (int j = lane; j < Cr; j += 64) acc += W2[(int64_t) k * Cr + j] * s1[j];
-            for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-            if (lane == 0) {
-                float v = fminf(fmaxf(alpha * (acc + b2[k]) + beta, 0.f), 1.f);
-                y[(int64_t) n * Cp + k] = (half_t) v;
-            }
-        }
-        for (int k = C + threadIdx.x; k < Cp; k += blockDim.x) y[(int64_t) n * Cp + k] = (half_t) 0.f;
-    }
-
     // Max pool over NC4HW4; out-of-image taps are skipped (reference maxpool.cpp semantics).
     template <typename I>
     __global__ void maxpool_kernel(vkhip_pool_desc d, const uint2 *x, uint2 *y, I total) {
@@ -511,27 +473,28 @@ int vkhip_global_avg_pool(const void *x, void *y, int64_t N, int64_t C, int64_t 
     return check_launch("global_avg_pool");
 }
 
-size_t vkhip_se_weight_bytes(int64_t C, int64_t Cr) { return (size_t) (2 * C * Cr + Cr + C) * 4; }
+// Fused SE middle as two batched skinny GEMMs (vkhip_fc): the blob is the fc blob of W1 (K = C,
+// M = Cr) at offset 0 and that of W2 (K = Cr, M = C) at a 256-byte aligned offset.
+static size_t se_w2_offset(int64_t C, int64_t Cr) { return (vkhip_fc_weight_bytes(C, Cr) + 255) & ~(size_t) 255; }
+
+size_t vkhip_se_weight_bytes(int64_t C, int64_t Cr) { return C > 0 && Cr > 0 ? se_w2_offset(C, Cr) + vkhip_fc_weight_bytes(Cr, C) : 0; }
+
+size_t vkhip_se_workspace_bytes(int64_t N, int64_t Cr) { return N > 0 && Cr > 0 ? (size_t) (N * round_up(Cr, 4) * 2) : 0; }
 
 int vkhip_se_pack_weights(int64_t C, int64_t Cr, const float *w1, const float *b1, const float *w2, const float *b2, void *blob) {
     if (!w1 || !w2 || !blob || C <= 0 || Cr <= 0) return set_error(VKHIP_ERR_INVALID, "se_pack: bad arguments");
-    float *p = (float *) blob;
-    std::memcpy(p, w1, (size_t) C * Cr * 4);
-    p += C * Cr;
-    for (int64_t j = 0; j < Cr; ++j) p[j] = b1 ? b1[j] : 0.f;
-    p += Cr;
-    std::memcpy(p, w2, (size_t) C * Cr * 4);
-    p += C * Cr;
-    for (int64_t k = 0; k < C; ++k) p[k] = b2 ? b2[k] : 0.f;
-    return VKHIP_OK;
+    std::memset(blob, 0, vkhip_se_weight_bytes(C, Cr));
+    int rc = vkhip_fc_pack_weights(C, Cr, w1, 1, b1, 1.f, 1.f, blob);
+    if (rc) return rc;
+    return vkhip_fc_pack_weights(Cr, C, w2, 1, b2, 1.f, 1.f, (char *) blob + se_w2_offset(C, Cr));
 }
 
-int vkhip_fused_se(const void *avg, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr, float alpha, float beta, vkhip_stream_t s) {
-    if (!avg || !blob || !y || N <= 0 || C <= 0 || Cr <= 0) return set_error(VKHIP_ERR_INVALID, "fused_se: bad arguments");
-    if (C + Cr > 16384) return set_error(VKHIP_ERR_UNSUPPORTED, "fused_se: C + Cr > 16384");
-    size_t sm = (size_t) (C + Cr) * 4;
-    fused_se_kernel<<<dim3((unsigned) N), 256, sm, resolve_stream(s)>>>((const half_t *) avg, (const float *) blob, (half_t *) y, (int) C, (int) Cr, alpha, beta);
-    return check_launch("fused_se");
+int vkhip_fused_se(const void *avg, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr, float alpha, float beta, void *workspace,
+                   vkhip_stream_t s) {
+    if (!avg || !blob || !y || !workspace || N <= 0 || C <= 0 || Cr <= 0) return set_error(VKHIP_ERR_INVALID, "fused_se: bad arguments");
+    int rc = vkhip_fc(avg, blob, workspace, N, C, Cr, VKHIP_ACT_RELU, 0.f, 0.f, s);
+    if (rc) return rc;
+    return vkhip_fc(workspace, (const char *) blob + se_w2_offset(C, Cr), y, N, Cr, C, VKHIP_ACT_HARDSIGMOID, alpha, beta, s);
 }
 
 int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s) {
