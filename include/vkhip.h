@@ -141,7 +141,9 @@ typedef struct vkhip_conv_plan {
     size_t  workspace_bytes; /* device scratch the forward call needs (0 = none) */
 } vkhip_conv_plan;
 
-/* Fill `plan` for `algo` (AUTO picks by shape heuristics). `tile` < 0 picks the default tile. */
+/* Fill `plan` for `algo` (AUTO picks by shape heuristics). `tile` < 0 picks the default tile; for
+ * a depthwise conv `tile` is the number of output rows per strip of the row-tiled kernel (4, 7 or
+ * 14; 0 or < 0: chosen by shape). */
 int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, int32_t ksplit, vkhip_conv_plan *plan);
 int vkhip_conv_tile_count(void);
 /* Host-side prepack: fp32 OIHW weights [Cout][Cin/group][KH][KW] and optional fp32 bias[Cout]

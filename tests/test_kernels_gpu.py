@@ -413,9 +413,11 @@ def test_depthwise(gpu, k, s, C, act):
 @pytest.mark.parametrize("shape,k,s,act,res", [((3, 20, 28, 28), 3, 1, 4, True), ((2, 24, 56, 56), 5, 2, 1, False),
                                                ((4, 160, 7, 7), 5, 1, 2, True), ((1, 16, 112, 112), 3, 2, 3, False),
                                                ((2, 6, 14, 13), 3, 1, 5, True)])
-def test_depthwise_tiled_shapes(gpu, shape, k, s, act, res):
+@pytest.mark.parametrize("rt", [4, 7, 14])
+def test_depthwise_tiled_shapes(gpu, shape, k, s, act, res, rt):
     """Even/odd widths (16- and 8-byte row copies), several planes per workgroup, row tiles with
-    halos, residual epilogue, ragged channel count."""
+    halos (4, 7 or 14 output rows per strip, the plan's tile), residual epilogue, ragged channel
+    count."""
     N, C, H, W = shape
     r = rng(70 + k + s + C)
     x = round_half(r.standard_normal(shape))
@@ -425,9 +427,10 @@ def test_depthwise_tiled_shapes(gpu, shape, k, s, act, res):
     OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
     rr = round_half(r.standard_normal((N, C, OH, OW))) if res else None
     lo, hi = (-0.5, 0.7) if act == 3 else (0.0, 0.0)
-    got, plan, _ = gpu_conv(x, w, b, (s, s), (p, p, p, p), group=C, act=act, lo=lo, hi=hi, res=rr)
+    got, plan, _ = gpu_conv(x, w, b, (s, s), (p, p, p, p), group=C, act=act, lo=lo, hi=hi, res=rr, algo=V.CONV_DEPTHWISE, tile=rt)
+    assert plan.tile == rt
     ref = oracle_conv(x, w, b, (s, s), (p, p, p, p), group=C, res=rr, act=act, lo=lo, hi=hi)
-    assert_parity(got, ref, f"dw {shape} k{k} s{s}")
+    assert_parity(got, ref, f"dw {shape} k{k} s{s} rows/strip {rt}")
 
 
 def test_depthwise_dilated_generic(gpu):

@@ -135,13 +135,14 @@ namespace vknn {
                 const Config &cfg    = *env.config;
                 const int     tuning = cfg.hint(Hint::Tuning, (int) Mode::Fast);
                 const int     wino   = cfg.hint(Hint::Winograd, (int) Mode::Auto);
-                if (d.group > 1) {
+                const bool dw = d.group > 1;
+                if (dw && (tuning == (int) Mode::NoTune || !env.tunable)) {
                     check(vkhip_conv_plan_make(&d, VKHIP_CONV_DEPTHWISE, -1, 0, &plan), "conv plan");
                     build(w, b);
                     return;
                 }
                 vkhip_conv_plan tmp;
-                const bool wino_ok = vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, -1, 0, &tmp) == VKHIP_OK && d.Cin >= 32 && d.Cout >= 32;
+                const bool wino_ok = !dw && vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, -1, 0, &tmp) == VKHIP_OK && d.Cin >= 32 && d.Cout >= 32;
                 if (wino == (int) Mode::On && wino_ok) {
                     check(vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, -1, 0, &plan), "conv plan");
                     build(w, b);
@@ -164,15 +165,17 @@ namespace vknn {
                 }
                 // Candidates: every GEMM tile, split-K for low-parallelism shapes, Winograd if eligible.
                 std::vector<std::array<int32_t, 3>> cands;
-                const int ntiles = vkhip_conv_tile_count();
+                const int ntiles = dw ? 0 : vkhip_conv_tile_count();
                 for (int t = 0; t < ntiles; ++t) cands.push_back({VKHIP_CONV_GEMM, t, 0});
+                if (dw) // the depthwise kernel's rows per strip
+                    for (int rt: {4, 7, 14}) cands.push_back({VKHIP_CONV_DEPTHWISE, rt, 0});
                 vkhip_conv_plan base;
                 check(vkhip_conv_plan_make(&d, VKHIP_CONV_AUTO, -1, 0, &base), "conv plan");
                 int64_t pixels = (int64_t) d.N * d.OH * d.OW;
                 // Split-K when the direct grid cannot fill the device (fewer than ~2 workgroups per CU
                 // with the big tiles) and the reduction is deep enough to split.
                 const int64_t kdepth = (int64_t) d.KH * d.KW * ((d.Cin + 3) / 4) * 4;
-                if (pixels <= 4096 || base.algo == VKHIP_CONV_SPLITK || (pixels * (int64_t) d.Cout <= (int64_t) 512 * 128 * 256 && kdepth >= 512)) {
+                if (!dw && (pixels <= 4096 || base.algo == VKHIP_CONV_SPLITK || (pixels * (int64_t) d.Cout <= (int64_t) 512 * 128 * 256 && kdepth >= 512))) {
                     for (int t: {3, 6, 1, 8, 10, 14, 16, 17, 18, 20, 26})
                         for (int ks: {2, 3, 4, 8, 16}) cands.push_back({VKHIP_CONV_SPLITK, t, ks});
                 }
@@ -181,7 +184,7 @@ namespace vknn {
                     // the split-K set.
                     std::vector<std::array<int32_t, 3>> keep;
                     for (auto &c: cands)
-                        if (c[0] == VKHIP_CONV_SPLITK || c[1] == base.tile || c[1] == 0 || c[1] == 1 || c[1] == 3 || c[1] == 5 ||
+                        if (c[0] == VKHIP_CONV_SPLITK || c[0] == VKHIP_CONV_DEPTHWISE || c[1] == base.tile || c[1] == 0 || c[1] == 1 || c[1] == 3 || c[1] == 5 ||
                             c[1] == 7 || c[1] >= 8)
                             keep.push_back(c);
                     cands = keep;

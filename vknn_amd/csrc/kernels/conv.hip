@@ -628,8 +628,11 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
             return set_error(VKHIP_ERR_UNSUPPORTED, "grouped conv with group=%d (Cin=%d Cout=%d) is not depthwise", d->group, d->Cin, d->Cout);
         if (algo != VKHIP_CONV_AUTO && algo != VKHIP_CONV_DEPTHWISE)
             return set_error(VKHIP_ERR_INVALID, "depthwise conv only runs the depthwise algorithm");
+        if (tile > 0 && tile != 4 && tile != 7 && tile != 14)
+            return set_error(VKHIP_ERR_INVALID, "depthwise tile %d: the rows per strip are 4, 7 or 14 (0 or -1: by shape)", tile);
         int64_t Cb         = ceil_div(d->Cin, 4);
         plan->algo         = VKHIP_CONV_DEPTHWISE;
+        plan->tile         = tile > 0 ? tile : 0;
         plan->weight_bytes = align256((size_t) Cb * 4 * 4) + (size_t) Cb * d->KH * d->KW * 8;
         return VKHIP_OK;
     }
@@ -762,12 +765,12 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
         a.act = d->act; a.lo = d->act_lo; a.hi = d->act_hi; a.has_res = d->has_res;
         bool unit = d->DH == 1 && d->DW == 1 && d->SH == d->SW;
         DwTile t;
-        const int RT = d->OH % 7 == 0 ? 7 : 4;
+        const int RT = plan->tile > 0 ? plan->tile : (d->OH % 7 == 0 ? 7 : 4);
         if (unit && d->KH == d->KW && (d->KH == 3 || d->KH == 5) && (d->SH == 1 || d->SH == 2) && dw_tile(d, (int64_t) d->N * Cb, RT, t)) {
             const size_t sm = (size_t) t.PP * t.IR * t.IWp * 8;
             dim3 g2((unsigned) ((int64_t) t.row_tiles * t.plane_groups));
 #define VKHIP_DW_LAUNCH(K, S_)                                                                                 \
-    (RT == 7 ? dwconv_lds_kernel<K, K, S_, 7><<<g2, 256, sm, st>>>(a, t) : dwconv_lds_kernel<K, K, S_, 4><<<g2, 256, sm, st>>>(a, t))
+    (RT == 14 ? dwconv_lds_kernel<K, K, S_, 14><<<g2, 256, sm, st>>>(a, t) : RT == 7 ? dwconv_lds_kernel<K, K, S_, 7><<<g2, 256, sm, st>>>(a, t) : dwconv_lds_kernel<K, K, S_, 4><<<g2, 256, sm, st>>>(a, t))
             if (d->KH == 3 && d->SH == 1) VKHIP_DW_LAUNCH(3, 1);
             else if (d->KH == 3) VKHIP_DW_LAUNCH(3, 2);
             else if (d->SH == 1) VKHIP_DW_LAUNCH(5, 1);
