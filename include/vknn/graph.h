@@ -31,6 +31,14 @@ namespace vknn {
         std::string dump() const;
     };
 
+    // ONNX import (reference include/vknn/graph.h:42): the graph of an ONNX model file as the
+    // reference's importer builds it, before any pass. Weights stored outside the model are read
+    // relative to the model's folder. Throws Error(IoError) for an unreadable file and
+    // Error(InvalidArgument) for a malformed one.
+    Graph importOnnx(const std::string &path);
+    // The same from an in-memory ModelProto; `baseDir` resolves external weight files.
+    Graph importOnnxBytes(const uint8_t *data, size_t size, const std::string &baseDir = "");
+
     // The ".vxm" model file (reference include/vknn/graph.h:46-47, src/core/model_io.cpp): an
     // optimized graph with its weights in the reference's VXM2 byte layout. load returns false on
     // a missing, foreign, truncated or inconsistent file and then says why in `why`.

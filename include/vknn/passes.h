@@ -7,6 +7,7 @@
 
 namespace vknn {
 
+    void foldConstantNodes(Graph &g);
     void inferShapes(Graph &g, int64_t batch = 1);
     void eliminateIdentity(Graph &g);
     void eliminateDeadNodes(Graph &g);

@@ -1,6 +1,5 @@
 // Top-level facade (reference include/vknn/runtime.h:10-35): load a model file with its unified
-// cache file. This build reads pre-optimized ".vxm" models; an ONNX path is reported as
-// unsupported (the ONNX importer is not part of this build).
+// cache file: a pre-optimized ".vxm" model, or any other path as an ONNX model.
 #pragma once
 #include "vknn/session.h"
 #include <memory>
@@ -15,8 +14,7 @@ namespace vknn {
             Config c    = cfg;
             c.cacheFile = cacheFile.empty() ? defaultCacheFile(path) : cacheFile;
             const bool vxm = path.size() >= 4 && path.compare(path.size() - 4, 4, ".vxm") == 0;
-            if (!vxm) throw Error(Status::Unsupported, "only .vxm models can be loaded by this build: " + path);
-            return Session::createFromVxm(path, c);
+            return vxm ? Session::createFromVxm(path, c) : Session::createFromOnnx(path, c);
         }
         static std::string defaultCacheFile(const std::string &modelPath) {
             const size_t slash = modelPath.find_last_of("/\\"), dot = modelPath.find_last_of('.');

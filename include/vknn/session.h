@@ -39,6 +39,9 @@ namespace vknn {
         // standard passes run first; `passOpt` overrides the default pass options.
         static std::unique_ptr<Session> create(Graph &&g, const Config &cfg);
         static std::unique_ptr<Session> create(Graph &&g, const Config &cfg, const PassOptions &passOpt);
+        // Import an ONNX model (importOnnx) and build a session from it; an empty cfg.cacheFile
+        // becomes "<model path without extension>.cache" (reference session.cpp:123-131).
+        static std::unique_ptr<Session> createFromOnnx(const std::string &path, const Config &cfg);
         // Load a pre-optimized ".vxm" graph: the passes are already applied and do not run again.
         // An empty cfg.cacheFile becomes "<model path without extension>.cache" (reference
         // session.cpp:133-155). Throws Error(RuntimeError) when the file cannot be loaded.

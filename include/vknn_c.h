@@ -66,6 +66,18 @@ int vknn_vxm_describe(const char *path, char *buf, int64_t cap);
 int vknn_session_create_vxm(const char *path, const char *options, vknn_session *out);
 int vknn_session_save_optimized(vknn_session s, const char *path);
 
+/* ONNX models (reference include/vknn/graph.h:42 importOnnx, src/core/session.cpp:123-131
+ * Session::createFromOnnx).
+ *   onnx_describe: import a model and write the graph as imported (before any pass) in full:
+ *             tensors, inputs, outputs, initializer hashes, nodes with attributes; host only.
+ *   onnx_after_passes: the node list after the standard passes (vknn_graph_after_passes format);
+ *             options fuse_dwpw, fuse_se; host only.
+ *   session_create_onnx: import and plan a session; an empty cache_file option means
+ *             "<path without extension>.cache", as in the reference. */
+int vknn_onnx_describe(const char *path, char *buf, int64_t cap);
+int vknn_onnx_after_passes(const char *path, const char *options, char *buf, int64_t cap);
+int vknn_session_create_onnx(const char *path, const char *options, vknn_session *out);
+
 /* Persistent autotune table (the tune section of the reference's unified cache file "VKNNCAC1",
  * src/backend/vulkan/vk_backend.cpp:30-150 and :440-545). A session created with the option
  * "cache_file=<path>" (and cache_mode tune or full, the default full) merges the file's table

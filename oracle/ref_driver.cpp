@@ -7,6 +7,7 @@
 #include "vknn/graph.h"
 #include "vknn/session.h"
 #include "model_zoo.h"
+#include "graph_text.h"
 #include <cstring>
 #include <sstream>
 #include <string>
@@ -203,4 +204,35 @@ REF_API int ref_single_node(int op, int sub_op, int fused_act, float act_lo, flo
             if (ids[k] == t) ins.emplace_back(data[k], data[k] + numElements(g.desc(t).shape));
     }
     return runSession(std::move(g), ins, y, ny, yshape);
+}
+
+// The reference's own ONNX importer (src/import/onnx/onnx_parser.cpp importOnnx) on a model file:
+// the imported graph in the full text form of graph_text.h, to compare node for node with this
+// build's importer.
+REF_API int ref_onnx_describe(const char *path, char *buf, int64_t cap) {
+    try {
+        std::string t = vknn_text::graph(importOnnx(path));
+        if ((int64_t) t.size() + 1 > cap) {
+            g_err = "buffer too small";
+            return 1;
+        }
+        std::memcpy(buf, t.c_str(), t.size() + 1);
+        return 0;
+    } catch (const std::exception &e) {
+        g_err = e.what();
+        return 1;
+    }
+}
+
+// Import an ONNX model with the reference importer and run it through the reference session on
+// its CPU backend (Session::create: the reference's full pass pipeline), one input.
+REF_API int ref_onnx_run(const char *path, const float *x, int64_t nx, float *y, int64_t ny) {
+    Graph g;
+    try {
+        g = importOnnx(path);
+    } catch (const std::exception &e) {
+        g_err = e.what();
+        return 1;
+    }
+    return runSession(std::move(g), {std::vector<float>(x, x + nx)}, y, ny, nullptr);
 }

@@ -49,6 +49,8 @@ REF_API = {
     "ref_float_to_half_n": (None, [c_vp, c_vp, c_i64]),
     "ref_half_to_float_n": (None, [c_vp, c_vp, c_i64]),
     "ref_model_run": (ctypes.c_int, [c_char_p, c_i64, c_u64, c_vp, c_i64, c_vp, c_i64]),
+    "ref_onnx_describe": (ctypes.c_int, [c_char_p, c_char_p, c_i64]),
+    "ref_onnx_run": (ctypes.c_int, [c_char_p, c_vp, c_i64, c_vp, c_i64]),
     "ref_single_node": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, c_f, c_f, c_char_p, ctypes.c_int, P(c_vp),
                                        P(c_i64), P(c_i32), ctypes.c_int, ctypes.c_int, c_vp, c_i64, P(c_i64)]),
 }

@@ -87,7 +87,7 @@ def test_config2_resnet50_structure():
     assert len(convs) == 53
     assert sum(n[3] for n in convs) == 16           # one fused residual per bottleneck (1x1 expand)
     assert all(n[2] == 1 for n in convs if n[3] == 1)  # ReLU moved onto the conv with the residual
-    assert [n[0] for n in ns if n[0] != "Conv"] == ["MaxPool", "GlobalAvgPool", "Flatten", "Gemm"]
+    assert [n[0] for n in ns if n[0] != "Conv"] == ["MaxPool", "GlobalAveragePool", "Flatten", "Gemm"]
     assert ns[-1][4] == "[64,1000]"
 
 

@@ -131,6 +131,9 @@ VKNN_API = {
     "vknn_vxm_describe": (c_int, [c_char_p, c_char_p, c_i64]),
     "vknn_session_create_vxm": (c_int, [c_char_p, c_char_p, P(c_vp)]),
     "vknn_session_save_optimized": (c_int, [c_vp, c_char_p]),
+    "vknn_onnx_describe": (c_int, [c_char_p, c_char_p, c_i64]),
+    "vknn_onnx_after_passes": (c_int, [c_char_p, c_char_p, c_char_p, c_i64]),
+    "vknn_session_create_onnx": (c_int, [c_char_p, c_char_p, P(c_vp)]),
     "vknn_tune_cache_load": (c_int, [c_char_p]),
     "vknn_tune_cache_save": (c_int, [c_char_p]),
     "vknn_tune_cache_put": (c_int, [c_char_p, c_i32]),
@@ -261,6 +264,21 @@ class Session:
         self.in_shape, self.out_elems = model_io(model, batch)
         return self
 
+    @classmethod
+    def from_onnx(cls, path, in_shape, out_elems, options=""):
+        """A session imported from an ONNX file with one input of `in_shape` and outputs of
+        `out_elems` elements each."""
+        lib = vknn()
+        require_gpu()
+        self = cls.__new__(cls)
+        self.model, self.batch = str(path), in_shape[0]
+        h = c_vp()
+        if lib.vknn_session_create_onnx(str(path).encode(), options.encode(), ctypes.byref(h)):
+            raise VkhipError("session create: " + lib.vknn_last_error().decode())
+        self.h = h.value
+        self.in_shape, self.out_elems = list(in_shape), list(out_elems)
+        return self
+
     def save_optimized(self, path):
         if vknn().vknn_session_save_optimized(self.h, str(path).encode()):
             raise VkhipError(vknn().vknn_last_error().decode())
@@ -333,6 +351,26 @@ def model_io(model, batch):
     if vknn().vknn_model_io(model.encode(), batch, in4, outs, ctypes.byref(n), 16):
         raise VkhipError(vknn().vknn_last_error().decode())
     return list(in4), list(outs)[:n.value]
+
+
+def _text(fn, *args, cap=1 << 24):
+    buf = ctypes.create_string_buffer(cap)
+    if fn(*args, buf, len(buf)):
+        raise VkhipError(vknn().vknn_last_error().decode())
+    out = buf.value.decode()
+    if len(out) >= cap - 1:
+        raise VkhipError("text output larger than %d bytes" % cap)
+    return out
+
+
+def onnx_describe(path):
+    """The graph an ONNX file imports to, before any pass, in full text form (host only)."""
+    return _text(vknn().vknn_onnx_describe, str(path).encode())
+
+
+def onnx_after_passes(path, options=""):
+    """Node list of an imported ONNX model after the standard passes (host only)."""
+    return _text(vknn().vknn_onnx_after_passes, str(path).encode(), options.encode())
 
 
 def graph_after_passes(model, batch=1, options=""):

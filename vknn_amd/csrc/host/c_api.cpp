@@ -3,6 +3,7 @@
 #include "hip_backend.h"
 #include "tune_cache.h"
 #include "model_zoo.h"
+#include "graph_text.h"
 #include "vknn/session.h"
 #include <cstring>
 #include <algorithm>
@@ -298,6 +299,47 @@ int vknn_session_create_vxm(const char *path, const char *options, vknn_session 
         std::unique_ptr<vknn_session_s> s(new vknn_session_s());
         s->model = path;
         s->sess  = Session::createFromVxm(path, o.cfg);
+        *out     = s.release();
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+int vknn_onnx_describe(const char *path, char *buf, int64_t cap) {
+    try {
+        if (!path) return fail("onnx_describe: null path");
+        copyOut(vknn_text::graph(importOnnx(path)), buf, cap);
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+int vknn_onnx_after_passes(const char *path, const char *options, char *buf, int64_t cap) {
+    try {
+        if (!path) return fail("onnx_after_passes: null path");
+        Graph g = importOnnx(path);
+        Opts  o(options);
+        PassOptions po;
+        po.fuseDwPw          = o.cfg.fuseDwPw;
+        po.fuseSqueezeExcite = o.cfg.fuseSqueezeExcite;
+        runStandardPasses(g, po);
+        g.topoSort();
+        copyOut(nodeList(g), buf, cap);
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+int vknn_session_create_onnx(const char *path, const char *options, vknn_session *out) {
+    try {
+        if (!path || !out) return fail("create_onnx: null argument");
+        Opts o(options);
+        std::unique_ptr<vknn_session_s> s(new vknn_session_s());
+        s->model = path;
+        s->sess  = Session::createFromOnnx(path, o.cfg);
         *out     = s.release();
         return 0;
     } catch (const std::exception &e) {

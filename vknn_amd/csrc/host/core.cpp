@@ -85,8 +85,8 @@ namespace vknn {
 
     const char *opTypeName(OpType t) {
         static const char *names[] = {
-            "Unknown", "Conv", "ConvTranspose", "Clip", "Relu", "Add", "GlobalAvgPool", "AvgPool", "MaxPool", "Gemm", "MatMul",
-            "Einsum", "Reshape", "Expand", "Tile", "Squeeze", "Flatten", "Softmax", "LayerNorm", "BatchNorm", "Concat", "Pad",
+            "Unknown", "Conv", "ConvTranspose", "Clip", "Relu", "Add", "GlobalAveragePool", "AveragePool", "MaxPool", "Gemm", "MatMul",
+            "Einsum", "Reshape", "Expand", "Tile", "Squeeze", "Flatten", "Softmax", "LayerNormalization", "BatchNormalization", "Concat", "Pad",
             "Identity", "Constant", "Shape", "Gather", "Unsqueeze", "Unary", "Binary", "PRelu", "Resize", "GridSample",
             "Transpose", "Slice", "Reduce", "DepthToSpace", "Cast", "Split", "Where", "Equal", "Greater", "GreaterEqual",
             "ConstantOfShape", "EyeLike", "ScatterND", "FusedSE", "FusedDwPw", "FusedPointwise", "ConvertLayout", "ConvertDtype"};

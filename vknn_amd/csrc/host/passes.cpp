@@ -1,5 +1,7 @@
 // Graph passes that shape the conv-path nodes the HIP backend executes. Same rewrites and
 // eligibility rules as the reference passes, implemented over a shared use-count helper:
+//   foldConstantNodes  the Constant case of src/import/const_fold.cpp:33 with the value emitted as
+//                      backend/cpu/ops/constant.cpp:8-38 does (dims kept, else a flat [n])
 //   inferShapes        src/import/infer_shapes.cpp (rules for the conv-path op set)
 //   foldBatchNorm      src/import/fold_batchnorm.cpp:5-131
 //   fuseActivations    src/import/fuse_activations.cpp:5-125 (Relu6 only when lo==0 && hi==6)
@@ -73,6 +75,45 @@ namespace vknn {
         }
         for (TensorId &t: g.outputs)
             if (t == from) t = to;
+    }
+
+    // Constant nodes (ONNX import) become initializers, so the parameters they carry (Clip bounds,
+    // Resize scales, Split sizes) are readable by the rules below and no backend runs them. The
+    // value comes from the "value" tensor attribute, or value_float(s) / value_int(s).
+    void foldConstantNodes(Graph &g) {
+        std::set<int> drop;
+        for (size_t i = 0; i < g.nodes.size(); ++i) {
+            const Node &n = g.nodes[i];
+            if (n.type != OpType::Constant || n.outputs.empty() || n.outputs[0] == kNoTensor) continue;
+            const Attr *a = nullptr;
+            for (const char *k: {"value", "value_floats", "value_ints", "value_float", "value_int"})
+                if (auto it = n.attr.map.find(k); it != n.attr.map.end()) {
+                    a = &it->second;
+                    break;
+                }
+            if (!a) continue;
+            const TensorId o = n.outputs[0];
+            TensorDesc    &d = g.desc(o);
+            HostBuffer     hb;
+            const bool     ints = a->kind == Attr::Ints || a->kind == Attr::Int;
+            std::vector<int64_t> iv = a->kind == Attr::Int ? std::vector<int64_t> {a->i} : a->ints;
+            std::vector<float>   fv = a->kind == Attr::Float ? std::vector<float> {a->f} : a->floats;
+            const size_t         cnt = ints ? iv.size() : fv.size();
+            d.shape = !a->shape.empty() ? a->shape : Shape {(int64_t) cnt};
+            if (ints) {
+                d.dtype = DType::Int64;
+                hb.resizeElems((int64_t) cnt, DType::Int64);
+                for (size_t k = 0; k < cnt; ++k) hb.i64()[k] = iv[k];
+            } else {
+                d.dtype = DType::Float32;
+                hb.resizeElems((int64_t) cnt, DType::Float32);
+                for (size_t k = 0; k < cnt; ++k) hb.f32()[k] = fv[k];
+            }
+            d.isInitializer   = true;
+            g.initializers[o] = std::move(hb);
+            drop.insert((int) i);
+        }
+        dropNodes(g, drop);
     }
 
     void inferShapes(Graph &g, int64_t batch) {
@@ -179,6 +220,11 @@ namespace vknn {
                     int64_t axis = nd.attr.geti("axis", 0);
                     if (axis < 0) axis += (int64_t) s0.size();
                     std::vector<int64_t> sp = nd.attr.getints("split");
+                    if (sp.empty() && nd.inputs.size() > 1 && nd.inputs[1] != kNoTensor && g.isInitializer(nd.inputs[1]) &&
+                        g.desc(nd.inputs[1]).dtype == DType::Int64) {
+                        const HostBuffer &hb = g.initializers[nd.inputs[1]];
+                        sp.assign(hb.i64(), hb.i64() + hb.bytes.size() / 8);
+                    }
                     if (sp.empty())
                         for (size_t k = 0; k < nd.outputs.size(); ++k) sp.push_back(s0[axis] / (int64_t) nd.outputs.size());
                     for (size_t k = 0; k < nd.outputs.size() && k < sp.size(); ++k) {
@@ -450,6 +496,7 @@ namespace vknn {
     }
 
     void runStandardPasses(Graph &g, const PassOptions &opt) {
+        foldConstantNodes(g);
         inferShapes(g, opt.batch);
         eliminateIdentity(g);
         foldBatchNorm(g);

@@ -4,6 +4,7 @@
 // whose supportsNode accepts it (else Unsupported) -> maximal same-backend runs become segments ->
 // boundary input/output sets -> host weights released. run = bind host inputs, run segments in
 // order, bring graph outputs to the host.
+#include "vknn/runtime.h"
 #include "vknn/session.h"
 #include <algorithm>
 #include <cstring>
@@ -30,6 +31,12 @@ namespace vknn {
         s->cfg_   = cfg;
         s->plan(opt);
         return s;
+    }
+
+    std::unique_ptr<Session> Session::createFromOnnx(const std::string &path, const Config &cfg) {
+        Config c = cfg;
+        if (c.cacheFile.empty()) c.cacheFile = Runtime::defaultCacheFile(path);
+        return create(importOnnx(path), c);
     }
 
     std::unique_ptr<Session> Session::createFromVxm(const std::string &path, const Config &cfg) {
