@@ -23,6 +23,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA (published)
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E (published)
+RIDGE = PEAK_FP16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)  # 312.5 flop/byte
 
 
 def log(*a):
@@ -79,15 +80,36 @@ def profile_ops(model, batch, x_dev, options="", reps=3, launches=5):
     return list(acc.values()), plan
 
 
-def profiled_traffic():
-    """Conv-kernel HBM bytes per step from the committed rocprofv3 PMC summary (FETCH_SIZE and
-    WRITE_SIZE, calibrated), or None when that summary is absent."""
+def plan_info(plan):
+    """op name -> kernel family ("conv_dma_kernel tile=14", or the op kind) from a session plan."""
     import re
-    path = os.path.join(ROOT, "profiles", "resnet50_b64_traffic.md")
+    out = {}
+    for ln in plan.splitlines():
+        m = re.match(r"(\S+) \[(\w+)\] ?(.*?) ?\{", ln)
+        if not m:
+            continue
+        k = re.search(r"kernel=(\S+)", m.group(3))
+        t = re.search(r"tile=(\d+)", m.group(3))
+        out[m.group(1)] = f"{k.group(1)} tile={t.group(1)}" if k and t else m.group(2)
+    return out
+
+
+def profiled_layer_traffic(model, batch, family, launches):
+    """Mean measured HBM bytes per launch of one kernel family, from the committed per-layer
+    rocprofv3 summary of this workload (profiles/<model>_b<batch>_layers.md), or None."""
+    path = os.path.join(ROOT, "profiles", f"{model}_b{batch}_layers.md")
     if not os.path.exists(path):
         return None
-    m = re.search(r"conv kernels read ([0-9.]+) MB and wrote ([0-9.]+) MB", open(path).read())
-    return None if not m else (float(m.group(1)) + float(m.group(2))) * 1e6
+    kernel, tile = family.split(" tile=") if " tile=" in family else (family, None)
+    vals = []
+    for ln in open(path):
+        c = [x.strip() for x in ln.split("|")]
+        if len(c) < 16 or not c[1].isdigit():
+            continue
+        plan, kern = c[4], c[5]
+        if kernel in kern and (tile is None or f"tile={tile} " in plan + " "):
+            vals.append(float(c[13]) * 1e6)
+    return round(sum(vals) / len(vals)) if vals and len(vals) == launches else None
 
 
 CPU_CONFIGS = [("conv3x3_bn_relu", "config 0"), ("mnv2_block", "config 1"), ("resnet50", "config 2"),
@@ -148,6 +170,8 @@ def main():
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--b1-steps", type=int, default=100)
     ap.add_argument("--dw-batch", type=int, default=128, help="batch of the MobileNetV3-Large depthwise measurement (0 = skip)")
+    ap.add_argument("--plan-out", default="", help="write the timed session's plan (one line per op with its flops and "
+                                                   "bytes) to this file, for vknn_amd.prof_summary layers")
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="MELEMS",
                     help="only run the flat fp32->fp16 convert over MELEMS million elements 5 times (known HBM "
                          "traffic: 6 bytes per element), to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -181,6 +205,9 @@ def main():
     ms_step = wall / args.steps * 1e3
     img_s = args.batch * args.steps / wall
     log(f"b{args.batch}: {ms_step:.3f} ms/step wall, {ev / args.steps * 1e3:.3f} ms/step events, {img_s:.1f} img/s")
+    if args.plan_out:
+        with open(args.plan_out, "w") as f:
+            f.write(sess.describe())
 
     # ---- batch-1 latency (skipped with --b1-steps 0, e.g. under a profiler)
     b1_ms = None
@@ -208,16 +235,48 @@ def main():
         conv_ms = sum(o["gpu_ms"] for o in conv)
         conv_fl = sum(o["flops"] for o in conv)
         all_ms = sum(o["gpu_ms"] for o in ops)
+        # the kernel family (kernel + tile) with the most device time in the step is the "dominant
+        # kernel"; its roofline is MFMA or HBM by its arithmetic intensity against the ridge point
+        info = plan_info(plan)
+        fams = {}
+        for o in ops:
+            fam = info.get(o["name"])
+            if fam and o["gpu_ms"] > 0:
+                e = fams.setdefault(fam, dict(n=0, ms=0.0, flops=0.0, bytes=0, names=[]))
+                e["n"] += 1
+                e["ms"] += o["gpu_ms"]
+                e["flops"] += o["flops"]
+                e["bytes"] += o["bytes"]
+                e["names"].append(o["name"])
+        dom = max(fams, key=lambda k: fams[k]["ms"])
+        d = fams[dom]
+        hbm = d["bytes"] > 0 and d["flops"] / d["bytes"] <= RIDGE
+        launch_s = d["ms"] / d["n"] * 1e-3
+        if hbm:
+            ach, peak, unit = d["bytes"] / d["n"] / launch_s / 1e9, PEAK_HBM_GBS, "GB/s"
+        else:
+            ach, peak, unit = d["flops"] / d["n"] / launch_s / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s"
+        roof = {"bound": "hbm" if hbm else "mfma", "achieved": round(ach, 2), "peak": peak, "unit": unit,
+                "frac": round(ach / peak, 4),
+                "traffic": profiled_layer_traffic(args.model, args.batch, dom, d["n"]),
+                "traffic_unit": "HBM bytes per launch (FETCH_SIZE x2 + WRITE_SIZE x1, profiles/<model>_b<batch>_layers.md), null if not profiled",
+                "kernel": f"{dom}: {d['n']} launches per step ({', '.join(d['names'])})",
+                "launch_us": round(launch_s * 1e6, 3),
+                "algorithmic_bytes_per_launch": round(d["bytes"] / d["n"]), "flops_per_launch": round(d["flops"] / d["n"]),
+                "intensity_flop_per_byte": round(d["flops"] / max(d["bytes"], 1), 1), "ridge_flop_per_byte": RIDGE}
+        # every op against its own roofline: the step's attainable time (sum over ops of
+        # max(flops / MFMA peak, algorithmic bytes / HBM peak)) over the measured op time
+        lb_ms = sum(max(o["flops"] / (PEAK_FP16_TFLOPS * 1e12), o["bytes"] / (PEAK_HBM_GBS * 1e9)) * 1e3 for o in ops)
+        extra["step_roofline"] = {"attainable_ms": round(lb_ms, 4), "op_ms": round(all_ms, 4), "frac": round(lb_ms / all_ms, 4),
+                                  "mfma_bound_ops": sum(1 for o in ops if o["bytes"] and o["flops"] / o["bytes"] > RIDGE),
+                                  "hbm_bound_ops": sum(1 for o in ops if o["bytes"] and o["flops"] / o["bytes"] <= RIDGE)}
         achieved = conv_fl / (conv_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
-                "traffic": profiled_traffic() if (args.model, args.batch) == ("resnet50", 64) else None,
-                "traffic_unit": "HBM bytes per step, all conv launches (profiles/resnet50_b64_traffic.md)",
-                "kernel": "all conv/FC kernels of one step (conv_gemm, conv_bd, conv_dma, conv_halo, conv_stem, split-K reduce, Winograd transforms, fc_kernel)",
-                "launch_ms": round(conv_ms, 4), "flops_per_step": conv_fl,
-                "algorithmic_bytes_per_step": sum(o["bytes"] for o in conv)}
+        extra["conv_mfma"] = {"achieved_TFLOPs": round(achieved, 2), "peak_TFLOPs": PEAK_FP16_TFLOPS,
+                              "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "conv_ms": round(conv_ms, 4), "flops_per_step": conv_fl,
+                              "note": "all conv/FC flops over all conv/FC time against the MFMA peak, including the layers whose "
+                                      "intensity puts them under the HBM roof"}
         pw = [o for o in conv if "conv" in o["name"] and o["bytes"] > 0]
-        one = [o for o in pw if o["flops"] / max(o["bytes"], 1) < 315]  # layers below the ridge
+        one = [o for o in pw if o["flops"] / max(o["bytes"], 1) <= RIDGE]  # layers below the ridge
         if one:
             b_ms = sum(o["gpu_ms"] for o in one)
             b_bytes = sum(o["bytes"] for o in one)

@@ -91,6 +91,10 @@ int vkhip_graph_destroy(vkhip_graph_t g);
  * (vk_backend.cpp:576-611) bit for bit. Unpack is exact. */
 int vkhip_pack_nchw_f32(const float *src, void *dst, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s);
 int vkhip_unpack_nchw_f32(const void *src, float *dst, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s);
+/* Profiling aid, no counterpart in the reference: enqueue one empty single-wave dispatch
+ * (dispatch_marker_kernel) so that a kernel trace can be cut into the launches of each operator.
+ * The vknn session records one before every operator when VKNN_HIP_OP_MARKERS=1. */
+int vkhip_dispatch_marker(int32_t id, vkhip_stream_t s);
 /* Flat (row-major) variants: a straight element-wise convert (vk_backend.cpp:559-575, 637-651). */
 int vkhip_pack_flat_f32(const float *src, void *dst, int64_t n, vkhip_stream_t s);
 int vkhip_unpack_flat_f32(const void *src, float *dst, int64_t n, vkhip_stream_t s);
@@ -146,6 +150,9 @@ typedef struct vkhip_conv_plan {
  * 14; 0 or < 0: chosen by shape). */
 int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, int32_t ksplit, vkhip_conv_plan *plan);
 int vkhip_conv_tile_count(void);
+/* Name of the kernel family a plan launches (e.g. "conv_dma_kernel"; Winograd names its three
+ * kernels joined by '+'), as a profiler shows it; for reports, no reference counterpart. */
+const char *vkhip_conv_plan_kernel(const vkhip_conv_plan *plan);
 /* Host-side prepack: fp32 OIHW weights [Cout][Cin/group][KH][KW] and optional fp32 bias[Cout]
  * into the blob the plan's kernel reads (bias stays fp32; weights become fp16, RNE). */
 int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const float *w, const float *bias, void *blob);

@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -306,7 +307,7 @@ namespace vknn {
             std::string describe() const override {
                 static const char *algos[] = {"auto", "gemm", "splitk", "winograd", "depthwise"};
                 return std::string(algos[plan.algo]) + " tile=" + std::to_string(plan.tile) + " ksplit=" + std::to_string(plan.ksplit) +
-                       (d.in_scale ? " +input scale" : "");
+                       (d.in_scale ? " +input scale" : "") + " kernel=" + vkhip_conv_plan_kernel(&plan);
             }
         };
 
@@ -427,6 +428,7 @@ namespace vknn {
                 ws    = std::make_shared<DevBuf>(vkhip_se_workspace_bytes(N, Cr));
                 kind  = "se";
                 flops = 4.0 * N * C * Cr;
+                bytes = (int64_t) (host.size() + (size_t) N * ((C + 3) / 4 * 4) * 2 * 2);
             }
             void record(SegEnv &env, vkhip_stream_t s) override {
                 check(vkhip_fused_se(env.dev(in), blob->ptr, env.dev(out), N, C, Cr, alpha, beta, ws->ptr, s), "fused_se " + name);
@@ -801,6 +803,8 @@ namespace vknn {
             env_.config  = &cfg;
             env_.tunable = true;
             env_.seg     = this;
+            const char *mk = std::getenv("VKNN_HIP_OP_MARKERS");
+            markers_       = mk && std::strcmp(mk, "1") == 0;
             // Tensors this segment touches, in first-use order.
             std::set<TensorId> produced;
             for (int i: idx) {
@@ -1005,9 +1009,11 @@ namespace vknn {
                           "boundary convert");
                 else check(vkhip_pack_nchw_f32(src, dev(t), x.n, x.c, x.h, x.w, stream_), "pack");
             }
-            if (timed || !useSide_) {
-                // one in-order stream (profiling times each op between its own two events)
+            if (timed || !useSide_ || markers_) {
+                // one in-order stream (profiling times each op between its own two events; trace
+                // markers need the launches in plan order)
                 for (size_t k = 0; k < ops_.size(); ++k) {
+                    if (markers_) check(vkhip_dispatch_marker((int32_t) k, stream_), "marker");
                     if (timed) vkhip_event_record(events_[2 * k], stream_);
                     for (int r = 0; r < (timed ? cfg_.profileReps : 1); ++r) ops_[k]->record(env_, stream_);
                     if (timed) vkhip_event_record(events_[2 * k + 1], stream_);
@@ -1121,7 +1127,10 @@ namespace vknn {
             std::string s;
             for (size_t k = 0; k < ops_.size(); ++k) {
                 s += ops_[k]->name + " [" + ops_[k]->kind + "] " + ops_[k]->describe();
-                if (useSide_ && opStream_[k] == 1) s += " (side stream)";
+                if (useSide_ && opStream_[k] == 1 && !markers_) s += " (side stream)";
+                char fb[64];
+                std::snprintf(fb, sizeof fb, " {flops=%.6g bytes=%lld}", ops_[k]->flops, (long long) ops_[k]->bytes);
+                s += fb;
                 s += "\n";
             }
             return s;

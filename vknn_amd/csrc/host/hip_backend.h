@@ -96,6 +96,9 @@ namespace vknn {
             std::vector<vkhip_event_t>                     opEvents_;
             vkhip_event_t                                  packEvent_ = nullptr, joinEvent_ = nullptr;
             bool                                           useSide_ = false;
+            // VKNN_HIP_OP_MARKERS=1: an empty marker dispatch before every op, all ops on one
+            // stream, so a kernel trace splits into per-op launches (vknn_amd/prof_summary.py layers)
+            bool                                           markers_ = false;
         };
 
         class HipBackend: public Backend {

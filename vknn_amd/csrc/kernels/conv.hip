@@ -609,6 +609,15 @@ extern "C" {
 
 int vkhip_conv_tile_count(void) { return kNumTiles; }
 
+const char *vkhip_conv_plan_kernel(const vkhip_conv_plan *plan) {
+    static const char *kinds[] = {"conv_gemm_kernel", "conv_bd_kernel", "conv_dma_kernel", "conv_halo_kernel", "conv_stem_kernel"};
+    if (!plan) return "?";
+    if (plan->algo == VKHIP_CONV_DEPTHWISE) return "dwconv_lds_kernel";
+    if (plan->tile < 0 || plan->tile >= kNumTiles) return "?";
+    if (plan->algo == VKHIP_CONV_WINOGRAD) return "wino_input_kernel+conv_gemm_kernel+wino_output_kernel";
+    return kinds[kTiles[plan->tile].kind];
+}
+
 int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, int32_t ksplit, vkhip_conv_plan *plan) {
     if (!d || !plan) return set_error(VKHIP_ERR_INVALID, "conv_plan_make: null argument");
     if (d->N <= 0 || d->Cin <= 0 || d->H <= 0 || d->W <= 0 || d->Cout <= 0 || d->OH <= 0 || d->OW <= 0 || d->KH <= 0 ||

@@ -119,6 +119,10 @@ namespace vkhip {
         dst[i]    = (float) src[((n * Cb + c / 4) * HW + p) * 4 + (c & 3)];
     }
 
+    // An empty one-wave dispatch: a separator in profiler traces between the launches of
+    // consecutive operators (the id argument is not read).
+    __global__ void dispatch_marker_kernel(int) {}
+
     __global__ void pack_flat_kernel(const float *src, uint16_t *dst, int64_t n) {
         int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
         if (i < n) dst[i] = ref_float_to_half(src[i]);
@@ -418,6 +422,11 @@ int vkhip_convert_layout(const void *src, void *dst, int64_t N, int64_t C, int64
     if ((dir != 0 && dir != 1) || (elem_bytes != 2 && elem_bytes != 4)) return set_error(VKHIP_ERR_INVALID, "convert_layout: bad dir or element size");
     const int f16 = elem_bytes == 2;
     return dir == 0 ? vkhip_boundary_convert(src, 2, f16, dst, 0, f16, N, C, H, W, s) : vkhip_boundary_convert(src, 0, f16, dst, 2, f16, N, C, H, W, s);
+}
+
+int vkhip_dispatch_marker(int32_t id, vkhip_stream_t s) {
+    dispatch_marker_kernel<<<1, 64, 0, resolve_stream(s)>>>(id);
+    return check_launch("dispatch_marker");
 }
 
 int vkhip_pack_flat_f32(const float *src, void *dst, int64_t n, vkhip_stream_t s) {

@@ -3,6 +3,8 @@
 Kernel time:   python -m vknn_amd.prof_summary trace <run_kernel_trace.csv> --steps K
 HBM traffic:   python -m vknn_amd.prof_summary traffic <fetch counter csv> <write counter csv> --steps K
                    --fetch-scale F --write-scale W
+Per layer:     python -m vknn_amd.prof_summary layers <run_kernel_trace.csv> <plan.txt> --steps K
+                   [--fetch <csv> --write <csv> --fetch-scale F --write-scale W]
 
 The timed region of bench.py is K forward passes, each starting with one NCHW->NC4HW4 pack
 dispatch; the last K pack dispatches therefore delimit the timed steps (session creation,
@@ -10,6 +12,15 @@ autotuning and warm-up come before them). Per kernel family the tables give disp
 mean duration / per-step time, or per-step HBM bytes read and written. FETCH_SIZE and WRITE_SIZE
 (KiB per dispatch) are multiplied by the calibration factors measured on a kernel of known traffic
 (`bench.py --traffic-probe`), so the totals are bytes that crossed the HBM interface.
+
+The per-layer table needs a run with VKNN_HIP_OP_MARKERS=1 (the session then enqueues an empty
+dispatch_marker_kernel before each operator, all operators on one stream) and the plan that
+`bench.py --plan-out` writes: one line per operator, in launch order, ending in
+"{flops=F bytes=B}" (the operator's algorithmic work). Each step's dispatches are cut at the
+markers, the i-th group belongs to the i-th plan line, and every operator gets its kernels, mean
+device time per step, achieved TFLOP/s and GB/s, and the fraction of the roofline that bounds it:
+MFMA fp16 (2500 TFLOP/s dense) above the ridge of 2.5e15 / 8e12 = 312.5 flop/byte, HBM (8 TB/s)
+below it. With the PMC runs of the same command, each operator's measured HBM bytes are added.
 """
 import argparse
 import csv
@@ -116,6 +127,114 @@ def cmd_traffic(a):
           f"{conv_r / 1e6:.1f} MB and wrote {conv_w / 1e6:.1f} MB (total {(conv_r + conv_w) / 1e6:.1f} MB)")
 
 
+PEAK_TFLOPS, PEAK_GBS = 2500.0, 8000.0
+RIDGE = PEAK_TFLOPS * 1e12 / (PEAK_GBS * 1e9)
+BOUNDARY = ("pack_kernel", "pack4_kernel", "unpack_kernel", "boundary_convert")
+
+
+def read_plan(path):
+    ops = []
+    for ln in open(path):
+        m = re.match(r"(\S+) \[(\w+)\] ?(.*?) ?\{flops=([0-9.eE+-]+) bytes=(\d+)\}\s*$", ln.rstrip("\n"))
+        if m:
+            ops.append(dict(name=m.group(1), kind=m.group(2), plan=m.group(3), flops=float(m.group(4)), bytes=int(m.group(5))))
+    return ops
+
+
+def marker_groups(rows, steps, n_ops):
+    """Per timed step, the dispatch rows of each operator (cut at the markers)."""
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    starts = [i for i, r in enumerate(rows) if family(r["Kernel_Name"]).startswith(("pack_kernel", "pack4_kernel"))]
+    if len(starts) < steps:
+        raise SystemExit(f"found {len(starts)} pack dispatches, need {steps}")
+    out = []
+    for s_i, beg in enumerate(starts[-steps:]):
+        end = starts[starts.index(beg) + 1] if starts.index(beg) + 1 < len(starts) else len(rows)
+        groups = []
+        for r in rows[beg:end]:
+            f = family(r["Kernel_Name"])
+            if f.startswith("dispatch_marker"):
+                groups.append([])
+            elif groups and not f.startswith(BOUNDARY):
+                groups[-1].append(r)
+        if len(groups) != n_ops:
+            raise SystemExit(f"step {s_i}: {len(groups)} marker groups for {n_ops} plan lines (run with VKNN_HIP_OP_MARKERS=1)")
+        out.append(groups)
+    return out
+
+
+def counters_by_dispatch(path, counter):
+    vals, rows = {}, {}
+    for r in csv.DictReader(open(path)):
+        if r["Counter_Name"] != counter:
+            continue
+        vals[r["Dispatch_Id"]] = vals.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"]) * 1024.0
+        rows.setdefault(r["Dispatch_Id"], r)
+    return vals, list(rows.values())
+
+
+def cmd_layers(a):
+    ops = read_plan(a.plan)
+    steps = marker_groups(list(csv.DictReader(open(a.trace))), a.steps, len(ops))
+    measured = None
+    if a.fetch and a.write:
+        fv, frows = counters_by_dispatch(a.fetch, "FETCH_SIZE")
+        wv, wrows = counters_by_dispatch(a.write, "WRITE_SIZE")
+        fsteps = marker_groups(frows, a.steps, len(ops))
+        wsteps = marker_groups(wrows, a.steps, len(ops))
+        measured = []
+        for k in range(len(ops)):
+            rd = sum(fv[r["Dispatch_Id"]] for st in fsteps for r in st[k]) * a.fetch_scale / a.steps
+            wr = sum(wv[r["Dispatch_Id"]] for st in wsteps for r in st[k]) * a.write_scale / a.steps
+            measured.append((rd, wr))
+    print(f"# {a.title}\n")
+    if a.command:
+        print(f"Command: `{a.command}`\n")
+    print(f"Timed steps: {a.steps}. Roofline: MFMA fp16 {PEAK_TFLOPS:.0f} TFLOP/s above {RIDGE:.1f} flop/B, HBM {PEAK_GBS:.0f} GB/s below."
+          + (f" Measured HBM bytes: FETCH_SIZE x {a.fetch_scale} + WRITE_SIZE x {a.write_scale}." if measured else "") + "\n")
+    head = "| # | op | kind | plan | kernels | us | GFLOP | alg. MB | TFLOP/s | GB/s | bound | frac |"
+    sep = "|---:|---|---|---|---|---:|---:|---:|---:|---:|---|---:|"
+    if measured:
+        head += " HBM MB | HBM/alg |"
+        sep += "---:|---:|"
+    print(head)
+    print(sep)
+    tot = dict(mfma=[0.0, 0.0], hbm=[0.0, 0.0])
+    all_us = 0.0
+    for k, op in enumerate(ops):
+        rows = [r for st in steps for r in st[k]]
+        us = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rows) / a.steps / 1e3
+        all_us += us
+        fams = OrderedDict()
+        for r in steps[-1][k]:
+            f = family(r["Kernel_Name"])
+            fams[f] = fams.get(f, 0) + 1
+        kern = ", ".join(f"`{f}`" + (f" x{c}" if c > 1 else "") for f, c in fams.items()) or "-"
+        line = f"| {k} | {op['name']} | {op['kind']} | {op['plan']} | {kern} | {us:.2f} |"
+        if us > 0 and (op["flops"] > 0 or op["bytes"] > 0):
+            tf = op["flops"] / (us * 1e-6) / 1e12
+            gbs = op["bytes"] / (us * 1e-6) / 1e9
+            bound = "mfma" if op["bytes"] == 0 or op["flops"] / op["bytes"] > RIDGE else "hbm"
+            frac = tf / PEAK_TFLOPS if bound == "mfma" else gbs / PEAK_GBS
+            tot[bound][0] += op["flops"] if bound == "mfma" else op["bytes"]
+            tot[bound][1] += us
+            line += f" {op['flops'] / 1e9:.2f} | {op['bytes'] / 1e6:.2f} | {tf:.1f} | {gbs:.0f} | {bound} | {frac:.3f} |"
+        else:
+            line += f" {op['flops'] / 1e9:.2f} | {op['bytes'] / 1e6:.2f} | - | - | - | - |"
+        if measured:
+            rd, wr = measured[k]
+            line += f" {(rd + wr) / 1e6:.2f} | " + (f"{(rd + wr) / op['bytes']:.2f} |" if op["bytes"] else "- |")
+        print(line)
+    mf, hb = tot["mfma"], tot["hbm"]
+    print(f"\nPer step: {all_us:.1f} us of operator kernels.")
+    if mf[1]:
+        print(f"MFMA-bound operators: {mf[0] / 1e9:.1f} GFLOP in {mf[1]:.1f} us = {mf[0] / (mf[1] * 1e-6) / 1e12:.1f} TFLOP/s, "
+              f"{mf[0] / (mf[1] * 1e-6) / 1e12 / PEAK_TFLOPS:.3f} of peak.")
+    if hb[1]:
+        print(f"HBM-bound operators: {hb[0] / 1e6:.1f} MB in {hb[1]:.1f} us = {hb[0] / (hb[1] * 1e-6) / 1e9:.0f} GB/s, "
+              f"{hb[0] / (hb[1] * 1e-6) / 1e9 / PEAK_GBS:.3f} of peak.")
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -126,12 +245,19 @@ def main():
     c.add_argument("write")
     c.add_argument("--fetch-scale", type=float, default=1.0)
     c.add_argument("--write-scale", type=float, default=1.0)
-    for p in (t, c):
+    lay = sub.add_parser("layers")
+    lay.add_argument("trace")
+    lay.add_argument("plan")
+    lay.add_argument("--fetch", default="")
+    lay.add_argument("--write", default="")
+    lay.add_argument("--fetch-scale", type=float, default=1.0)
+    lay.add_argument("--write-scale", type=float, default=1.0)
+    for p in (t, c, lay):
         p.add_argument("--steps", type=int, required=True)
         p.add_argument("--title", default="kernel time per forward pass")
         p.add_argument("--command", default="")
     a = ap.parse_args()
-    cmd_trace(a) if a.cmd == "trace" else cmd_traffic(a)
+    {"trace": cmd_trace, "traffic": cmd_traffic, "layers": cmd_layers}[a.cmd](a)
 
 
 if __name__ == "__main__":
