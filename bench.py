@@ -94,7 +94,7 @@ def plan_info(plan):
     return out
 
 
-def profiled_layer_traffic(model, batch, family, launches):
+def profiled_layer_traffic(model, batch, family):
     """Mean measured HBM bytes per launch of one kernel family, from the committed per-layer
     rocprofv3 summary of this workload (profiles/<model>_b<batch>_layers.md), or None."""
     path = os.path.join(ROOT, "profiles", f"{model}_b{batch}_layers.md")
@@ -109,7 +109,7 @@ def profiled_layer_traffic(model, batch, family, launches):
         plan, kern = c[4], c[5]
         if kernel in kern and (tile is None or f"tile={tile} " in plan + " "):
             vals.append(float(c[13]) * 1e6)
-    return round(sum(vals) / len(vals)) if vals and len(vals) == launches else None
+    return round(sum(vals) / len(vals)) if vals else None
 
 
 CPU_CONFIGS = [("conv3x3_bn_relu", "config 0"), ("mnv2_block", "config 1"), ("resnet50", "config 2"),
@@ -258,7 +258,7 @@ def main():
             ach, peak, unit = d["flops"] / d["n"] / launch_s / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s"
         roof = {"bound": "hbm" if hbm else "mfma", "achieved": round(ach, 2), "peak": peak, "unit": unit,
                 "frac": round(ach / peak, 4),
-                "traffic": profiled_layer_traffic(args.model, args.batch, dom, d["n"]),
+                "traffic": profiled_layer_traffic(args.model, args.batch, dom),
                 "traffic_unit": "HBM bytes per launch (FETCH_SIZE x2 + WRITE_SIZE x1, profiles/<model>_b<batch>_layers.md), null if not profiled",
                 "kernel": f"{dom}: {d['n']} launches per step ({', '.join(d['names'])})",
                 "launch_us": round(launch_s * 1e6, 3),
