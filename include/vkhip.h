@@ -48,6 +48,17 @@ const char *vkhip_build_info(void);
 
 int vkhip_malloc(void **p, size_t bytes);
 int vkhip_free(void *p);
+
+/* dma-buf interop (the reference's zero-copy I/O: IOTensor.dmaBufFd bound as the boundary buffer,
+ * src/backend/vulkan/vk_backend.cpp:1218-1318, src/core/ion.cpp).
+ *   import: map a caller's dma-buf fd (`bytes` long) into device memory; the caller keeps fd (the
+ *           runtime imports a duplicate). *dev_ptr addresses the buffer until release.
+ *   export: a dma-buf fd for `bytes` of device memory from vkhip_malloc (page-aligned size); the
+ *           caller closes it. */
+typedef struct vkhip_dmabuf_s *vkhip_dmabuf;
+int vkhip_dmabuf_import(int fd, size_t bytes, vkhip_dmabuf *out, void **dev_ptr);
+int vkhip_dmabuf_release(vkhip_dmabuf h);
+int vkhip_dmabuf_export(const void *dev_ptr, size_t bytes, int *fd);
 int vkhip_memcpy_h2d(void *dst, const void *src, size_t bytes, vkhip_stream_t s);
 int vkhip_memcpy_d2h(void *dst, const void *src, size_t bytes, vkhip_stream_t s);
 int vkhip_memcpy_d2d(void *dst, const void *src, size_t bytes, vkhip_stream_t s);

@@ -35,7 +35,8 @@ namespace vknn {
         BackendKind              backend          = BackendKind::Hip;
         std::vector<BackendKind> fallback         = {};
         // The HIP build ships no CPU backend: a node the HIP backend cannot run is an Unsupported
-        // error, never a silent host fallback.
+        // error, never a silent host fallback. A host backend registered by the caller (the
+        // tests' oracle/test_cpu_backend.cpp) takes such nodes only when this is set.
         bool                     allowCpuFallback = false;
 
         Precision precision = Precision::Low;

@@ -31,6 +31,14 @@ int vknn_session_create_model(const char *model, int64_t batch, uint64_t seed, c
 int vknn_session_destroy(vknn_session s);
 /* Host path: x (NCHW fp32) in, all outputs (NCHW fp32, concatenated in graph order) out. */
 int vknn_session_run_host(vknn_session s, const float *x, int64_t nx, float *y, int64_t ny);
+/* Zero-copy run (reference IOTensor.dmaBufFd, io_tensor.h:10-23, Session::run output bindings,
+ * session_class.h:34-37): the single input is read from the dma-buf `in_fd`, converted from its
+ * declared layout (0 NCHW, 1 NHWC, 2 NC4HW4, 3 device-native = NC4HW4 fp16) and dtype (in_f16);
+ * with out_fd >= 0 the first output is written into that dma-buf in its declared layout, and the
+ * run returns once it is there; other outputs (or all, with out_fd < 0) land in y as fp32 NCHW.
+ * Imports are cached while the same buffer comes back. */
+int vknn_session_run_dmabuf(vknn_session s, int32_t in_fd, int32_t in_fmt, int32_t in_f16, int32_t out_fd, int32_t out_fmt, int32_t out_f16,
+                            float *y, int64_t ny);
 /* Device path: the input is read from device memory (NCHW fp32, e.g. from vkhip_malloc); the run
  * is enqueued on the session stream and returns without waiting. */
 int vknn_session_bind_device_input(vknn_session s, const float *dev_x);
@@ -47,6 +55,8 @@ void *vknn_session_stream(vknn_session s);
 /* Per-op profile of the last profiled run (JSON array) and the per-op kernel plan (text). */
 int vknn_session_profile_json(vknn_session s, char *buf, int64_t cap);
 int vknn_session_describe(vknn_session s, char *buf, int64_t cap);
+/* The session's segments in run order, one line each: "<backend> nodes=<n> in=<names,> out=<names,>". */
+int vknn_session_segments(vknn_session s, char *buf, int64_t cap);
 /* Number of nodes of one op type (e.g. "Conv", "FusedDwPw") in the session's planned graph. */
 int vknn_session_count_ops(vknn_session s, const char *op_type_name);
 /* Host only (no device needed): run the standard passes on a zoo model and write the resulting

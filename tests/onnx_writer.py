@@ -395,3 +395,41 @@ DTYPES_EXTRA = [("h16", np.array([0.5, -1.25, 3.0e-5, 65504.0]), FLOAT16, "typed
                 ("i8", np.array([-128, 5], np.int8), INT8, "raw")]
 
 IMPORT_CASES = ["ssa", "defaults", "unnamed", "inputs_inits", "dtypes", "const_attrs", "value_info"]
+
+
+def mixed_model(path, seed=5):
+    """A network whose graph alternates between ops the HIP backend runs (Conv, Add, global pool)
+    and ops it does not (LeakyRelu, Tanh, Elu), so a session with a host backend splits it into
+    HIP -> CPU -> HIP -> CPU -> HIP -> CPU -> HIP segments. x [2,8,10,10] -> y [2,8,1,1]."""
+    r = _rng(seed)
+    wa = (r.standard_normal((12, 8, 3, 3)) * 0.2).astype(np.float32)
+    ba = (r.standard_normal(12) * 0.1).astype(np.float32)
+    wb = (r.standard_normal((12, 12, 1, 1)) * 0.3).astype(np.float32)
+    bb = (r.standard_normal(12) * 0.1).astype(np.float32)
+    wc = (r.standard_normal((8, 12, 1, 1)) * 0.3).astype(np.float32)
+    inits = [tensor("wa", wa), tensor("ba", ba), tensor("wb", wb), tensor("bb", bb), tensor("wc", wc)]
+    nodes = [
+        node("Conv", ["x", "wa", "ba"], ["a"], name="conv_a", kernel_shape=[3, 3], pads=[1, 1, 1, 1]),
+        node("LeakyRelu", ["a"], ["l"], name="leaky", alpha=0.1),
+        node("Conv", ["l", "wb", "bb"], ["b"], name="conv_b", kernel_shape=[1, 1]),
+        node("Tanh", ["b"], ["t"], name="tanh"),
+        node("Add", ["t", "a"], ["s"], name="add"),
+        node("Elu", ["s"], ["e"], name="elu", alpha=0.7),
+        node("Conv", ["e", "wc"], ["c"], name="conv_c", kernel_shape=[1, 1]),
+        node("GlobalAveragePool", ["c"], ["y"], name="gap"),
+    ]
+    g = graph(nodes, [value_info("x", [2, 8, 10, 10])], [value_info("y", [2, 8, 1, 1])], inits)
+    with open(path, "wb") as f:
+        f.write(model(g))
+    return path
+
+
+def host_only_model(path):
+    """Ops the test host backend runs alone: x [2,3,4,5] -> LeakyRelu -> Tanh -> Add x -> Elu -> GAP."""
+    nodes = [node("LeakyRelu", ["x"], ["l"], name="leaky", alpha=0.2), node("Tanh", ["l"], ["t"], name="tanh"),
+             node("Add", ["t", "x"], ["s"], name="add"), node("Elu", ["s"], ["e"], name="elu"),
+             node("GlobalAveragePool", ["e"], ["y"], name="gap")]
+    g = graph(nodes, [value_info("x", [2, 3, 4, 5])], [value_info("y", [2, 3, 1, 1])])
+    with open(path, "wb") as f:
+        f.write(model(g))
+    return path

@@ -57,6 +57,9 @@ VKHIP_API = {
     "vkhip_build_info": (c_char_p, []),
     "vkhip_malloc": (c_int, [P(c_vp), c_sz]),
     "vkhip_free": (c_int, [c_vp]),
+    "vkhip_dmabuf_import": (c_int, [c_int, c_sz, P(c_vp), P(c_vp)]),
+    "vkhip_dmabuf_release": (c_int, [c_vp]),
+    "vkhip_dmabuf_export": (c_int, [c_vp, c_sz, P(c_int)]),
     "vkhip_memcpy_h2d": (c_int, [c_vp, c_vp, c_sz, c_vp]),
     "vkhip_memcpy_d2h": (c_int, [c_vp, c_vp, c_sz, c_vp]),
     "vkhip_memcpy_d2d": (c_int, [c_vp, c_vp, c_sz, c_vp]),
@@ -126,6 +129,8 @@ VKNN_API = {
     "vknn_session_profile_json": (c_int, [c_vp, c_char_p, c_i64]),
     "vknn_session_describe": (c_int, [c_vp, c_char_p, c_i64]),
     "vknn_session_count_ops": (c_int, [c_vp, c_char_p]),
+    "vknn_session_segments": (c_int, [c_vp, c_char_p, c_i64]),
+    "vknn_session_run_dmabuf": (c_int, [c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64]),
     "vknn_graph_after_passes": (c_int, [c_char_p, c_i64, c_char_p, c_char_p, c_i64]),
     "vknn_model_save_vxm": (c_int, [c_char_p, c_i64, c_u64, c_char_p, c_char_p]),
     "vknn_vxm_describe": (c_int, [c_char_p, c_char_p, c_i64]),
@@ -328,6 +333,16 @@ class Session:
         buf = ctypes.create_string_buffer(1 << 20)
         vknn().vknn_session_describe(self.h, buf, len(buf))
         return buf.value.decode()
+
+    def segments(self):
+        """[(backend, nodes, inputs, outputs)] per segment, in run order."""
+        out = []
+        for ln in _text(vknn().vknn_session_segments, self.h).splitlines():
+            be, rest = ln.split(" nodes=")
+            n, rest = rest.split(" in=")
+            ins, outs = rest.split(" out=")
+            out.append((be, int(n), [t for t in ins.split(",") if t], [t for t in outs.split(",") if t]))
+        return out
 
     def count_ops(self, op):
         return vknn().vknn_session_count_ops(self.h, op.encode())

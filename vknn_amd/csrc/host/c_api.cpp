@@ -50,6 +50,7 @@ namespace {
                 else if (k == "fuse_se") cfg.fuseSqueezeExcite = v != "0";
                 else if (k == "cache_file") cfg.cacheFile = v;
                 else if (k == "passes") passes = v != "0";
+                else if (k == "cpu_fallback") cfg.allowCpuFallback = v != "0";
                 else if (k == "keep_weights") cfg.freeWeightsAfterUpload = v == "0";
                 else if (k == "cache_mode") cfg.cacheMode = v == "off" ? CacheMode::Off : v == "tune" ? CacheMode::Tune : CacheMode::Full;
             }
@@ -128,6 +129,50 @@ int vknn_session_run_host(vknn_session s, const float *x, int64_t nx, float *y, 
         for (auto &o: outs) {
             int64_t n = numElements(o.shape);
             if (off + n > ny) return fail("output buffer too small");
+            std::memcpy(y + off, o.f32(), (size_t) n * 4);
+            off += n;
+        }
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+int vknn_session_run_dmabuf(vknn_session s, int32_t in_fd, int32_t in_fmt, int32_t in_f16, int32_t out_fd, int32_t out_fmt, int32_t out_f16,
+                            float *y, int64_t ny) {
+    try {
+        if (!s) return fail("run_dmabuf: null session");
+        auto layout = [](int32_t f) {
+            if (f < 0 || f > 3) throw Error(Status::InvalidArgument, "dma-buf layout must be 0 NCHW, 1 NHWC, 2 NC4HW4 or 3 device-native");
+            return (TensorFormat) f;
+        };
+        const Graph &g = s->sess->graph();
+        if (g.inputs.size() != 1 || g.outputs.empty()) return fail("run_dmabuf: the model must have one input");
+        std::vector<IOTensor> ins(1), outs;
+        ins[0].name  = g.desc(g.inputs[0]).name;
+        ins[0].shape = g.desc(g.inputs[0]).shape;
+        if (in_fd >= 0) {
+            ins[0].dmaBufFd     = in_fd;
+            ins[0].dmaBufFormat = layout(in_fmt);
+            ins[0].dmaBufDtype  = in_f16 ? DType::Float16 : DType::Float32;
+        } else {
+            return fail("run_dmabuf: no input fd");
+        }
+        if (out_fd >= 0) {
+            IOTensor o;
+            o.name         = g.desc(g.outputs[0]).name;
+            o.dmaBufFd     = out_fd;
+            o.dmaBufFormat = layout(out_fmt);
+            o.dmaBufDtype  = out_f16 ? DType::Float16 : DType::Float32;
+            outs.push_back(o);
+        }
+        Status st = s->sess->run(ins, outs);
+        if (st != Status::Ok) return fail(std::string("run failed: ") + statusStr(st) + ": " + s->sess->lastError());
+        int64_t off = 0;
+        for (auto &o: outs) {
+            if (o.dmaBufFd >= 0) continue;
+            int64_t n = numElements(o.shape);
+            if (!y || off + n > ny) return fail("output buffer too small");
             std::memcpy(y + off, o.f32(), (size_t) n * 4);
             off += n;
         }
@@ -221,6 +266,24 @@ int vknn_session_describe(vknn_session s, char *buf, int64_t cap) {
         std::string d;
         for (auto &seg: s->sess->segments())
             if (auto *h = dynamic_cast<hipbe::HipSegment *>(seg.get())) d += h->describe();
+        copyOut(d, buf, cap);
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+int vknn_session_segments(vknn_session s, char *buf, int64_t cap) {
+    try {
+        if (!s) return fail("segments: null session");
+        std::string d;
+        for (auto &seg: s->sess->segments()) {
+            d += std::string(seg->backend ? seg->backend->name() : "?") + " nodes=" + std::to_string(seg->nodeIdx.size()) + " in=";
+            for (TensorId t: seg->boundaryInputs) d += s->sess->graph().desc(t).name + ",";
+            d += " out=";
+            for (TensorId t: seg->boundaryOutputs) d += s->sess->graph().desc(t).name + ",";
+            d += "\n";
+        }
         copyOut(d, buf, cap);
         return 0;
     } catch (const std::exception &e) {

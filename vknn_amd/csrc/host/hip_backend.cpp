@@ -19,6 +19,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <sys/stat.h>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -953,6 +954,76 @@ namespace vknn {
                 vkhip_stream_sync(stream_);
                 vkhip_stream_destroy(stream_);
             }
+            for (auto &kv: dma_) vkhip_dmabuf_release(kv.second.h);
+        }
+
+        void *HipSegment::importDmaBuf(TensorId t, int fd, size_t bytes) {
+            struct stat st {};
+            const uint64_t id = ::fstat(fd, &st) == 0 ? ((uint64_t) st.st_dev << 40) ^ (uint64_t) st.st_ino : 0;
+            DmaImport &imp = dma_[t];
+            if (imp.h && imp.bytes == bytes && (id ? imp.id == id : imp.fd == fd)) return imp.ptr;
+            if (imp.h) {
+                check(vkhip_stream_sync(stream_), "sync");
+                dropGraph(); // a captured graph holds the old address
+                vkhip_dmabuf_release(imp.h);
+                imp = DmaImport {};
+            }
+            vkhip_dmabuf h   = nullptr;
+            void        *ptr = nullptr;
+            check(vkhip_dmabuf_import(fd, bytes, &h, &ptr), "dma-buf import of " + g_.desc(t).name);
+            imp = DmaImport {id, fd, bytes, h, ptr};
+            return ptr;
+        }
+
+        // Layout code of the boundary converter for a declared dma-buf format; Auto means the
+        // device-native NC4HW4 fp16.
+        static std::pair<int, bool> dmaLayout(const RtTensor &rt) {
+            if (rt.dmaBufFormat == TensorFormat::Auto) return {2, true};
+            if (rt.dmaBufFormat != TensorFormat::NCHW && rt.dmaBufFormat != TensorFormat::NHWC && rt.dmaBufFormat != TensorFormat::NC4HW4)
+                throw Error(Status::InvalidArgument, "dma-buf layout must be NCHW, NHWC, NC4HW4 or Auto");
+            if (rt.dmaBufDtype != DType::Float32 && rt.dmaBufDtype != DType::Float16)
+                throw Error(Status::InvalidArgument, "dma-buf dtype must be fp32 or fp16");
+            return {(int) rt.dmaBufFormat, rt.dmaBufDtype == DType::Float16};
+        }
+
+        static size_t dmaBytes(const Shape &s, std::pair<int, bool> fmt) {
+            NCHW         x = NCHW::from(s);
+            const size_t c = fmt.first == 2 ? (size_t) (x.c + 3) / 4 * 4 : (size_t) x.c;
+            return (size_t) x.n * c * x.h * x.w * (fmt.second ? 2 : 4);
+        }
+
+        // Bind (or unbind) this run's dma-buf inputs and outputs (reference vk_backend.cpp:1218-1318):
+        // an input fd becomes the source of the boundary pack, converted from its declared layout;
+        // an output fd receives the boundary tensor in its declared layout instead of the host path.
+        void HipSegment::bindDmaBufs(ExecContext &ctx) {
+            for (TensorId t: boundaryInputs) {
+                const RtTensor &rt = ctx.t(t);
+                if (rt.dmaBufFd >= 0) {
+                    const auto fmt = dmaLayout(rt);
+                    void      *ptr = importDmaBuf(t, rt.dmaBufFd, dmaBytes(g_.desc(t).shape, fmt));
+                    bindDeviceInputAs(t, ptr, fmt.first, fmt.second);
+                    dmaIn_.insert(t);
+                } else if (dmaIn_.count(t)) {
+                    extIn_.erase(t);
+                    extFmt_.erase(t);
+                    dmaIn_.erase(t);
+                    dropGraph();
+                }
+            }
+            for (TensorId t: boundaryOutputs) {
+                const RtTensor &rt = ctx.t(t);
+                if (rt.dmaBufFd >= 0) {
+                    const auto fmt = dmaLayout(rt);
+                    void      *ptr = importDmaBuf(t, rt.dmaBufFd, dmaBytes(g_.desc(t).shape, fmt));
+                    auto       it  = extOut_.find(t);
+                    if (it == extOut_.end() || it->second.first != ptr || it->second.second != fmt) {
+                        extOut_[t] = {ptr, fmt};
+                        dropGraph();
+                    }
+                } else if (extOut_.erase(t)) {
+                    dropGraph();
+                }
+            }
         }
 
         TensorId HipSegment::resolve(TensorId t) const {
@@ -1031,8 +1102,13 @@ namespace vknn {
                 check(vkhip_stream_wait_event(stream_, joinEvent_), "stream wait");
             }
             for (TensorId t: boundaryOutputs) {
-                NCHW y = NCHW::from(g_.desc(t).shape);
-                check(vkhip_unpack_nchw_f32(dev(t), (float *) outStaging_[t]->ptr, y.n, y.c, y.h, y.w, stream_), "unpack");
+                NCHW y  = NCHW::from(g_.desc(t).shape);
+                auto xo = extOut_.find(t);
+                if (xo != extOut_.end())
+                    check(vkhip_boundary_convert(dev(t), 2, 1, xo->second.first, xo->second.second.first, xo->second.second.second ? 1 : 0, y.n,
+                                                 y.c, y.h, y.w, stream_),
+                          "boundary convert (dma-buf output)");
+                else check(vkhip_unpack_nchw_f32(dev(t), (float *) outStaging_[t]->ptr, y.n, y.c, y.h, y.w, stream_), "unpack");
             }
         }
 
@@ -1081,6 +1157,7 @@ namespace vknn {
         void HipSegment::run(ExecContext &ctx) {
             const bool profile = ctx.profiler && ctx.profiler->enabled();
             auto       t0      = std::chrono::high_resolution_clock::now();
+            bindDmaBufs(ctx);
             for (TensorId t: boundaryInputs) {
                 RtTensor &rt = ctx.t(t);
                 if (extIn_.count(t)) continue;
@@ -1089,6 +1166,8 @@ namespace vknn {
                 check(vkhip_memcpy_h2d(staging_[t]->ptr, rt.host.f32(), (size_t) rt.elems() * 4, stream_), "input upload");
             }
             launch(profile);
+            // a dma-buf output is complete when the run returns: the caller reads the buffer next
+            if (!extOut_.empty()) check(vkhip_stream_sync(stream_), "sync (dma-buf output)");
             for (TensorId t: boundaryOutputs) {
                 RtTensor &rt = ctx.t(t);
                 rt.shape       = g_.desc(t).shape;

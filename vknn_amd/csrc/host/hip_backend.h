@@ -3,6 +3,7 @@
 #include "vkhip.h"
 #include "vknn/backend.h"
 #include <map>
+#include <set>
 #include <memory>
 #include <string>
 #include <vector>
@@ -73,6 +74,10 @@ namespace vknn {
             void     recordAll(bool timed);
             void     launch(bool profile);
             void     dropGraph();
+            // dma-buf boundaries (IOTensor.dmaBufFd): import the fd of tensor t, reusing the last
+            // import while the same buffer and size come back; returns the device address
+            void    *importDmaBuf(TensorId t, int fd, size_t bytes);
+            void     bindDmaBufs(ExecContext &ctx);
 
             Graph                                         &g_;
             const Config                                  &cfg_;
@@ -85,6 +90,16 @@ namespace vknn {
             std::map<TensorId, TensorId>                   alias_;
             std::map<TensorId, const float *>              extIn_;
             std::map<TensorId, std::pair<int, bool>>       extFmt_; // declared (layout, fp16) of a bound input
+            struct DmaImport {
+                uint64_t     id    = 0; // st_dev:st_ino of the fd's file, or 0
+                int          fd    = -1;
+                size_t       bytes = 0;
+                vkhip_dmabuf h     = nullptr;
+                void        *ptr   = nullptr;
+            };
+            std::map<TensorId, DmaImport>                  dma_;
+            std::set<TensorId>                             dmaIn_;  // inputs bound to an imported dma-buf
+            std::map<TensorId, std::pair<void *, std::pair<int, bool>>> extOut_; // outputs written to a dma-buf
             std::vector<vkhip_event_t>                     events_;
             // Two-stream schedule (see planStreams): per op its stream (0 main, 1 side), the ops
             // whose completion events it waits for (-1 = the boundary pack), and whether its own

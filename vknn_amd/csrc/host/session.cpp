@@ -126,6 +126,7 @@ namespace vknn {
             // the boundary sets are attached once compileSegment returns; the segment reads them
             // when it first runs (staging buffers are sized then)
             auto seg = be->compileSegment(r, graph_, cfg_);
+            seg->backend         = be;
             seg->nodeIdx         = r;
             seg->boundaryInputs  = bin;
             seg->boundaryOutputs = bout;
@@ -175,16 +176,39 @@ namespace vknn {
 
     Status Session::run(const std::vector<IOTensor> &inputs, std::vector<IOTensor> &outputs) {
         try {
+            // dma-buf bindings hold for one run: clear the last run's, then take this run's inputs
+            // and the outputs the caller pre-filled with a name and an fd (reference
+            // session_class.h:34-37)
+            for (TensorId t: graph_.inputs) pool_[t].dmaBufFd = -1;
+            for (TensorId t: graph_.outputs) pool_[t].dmaBufFd = -1;
+            for (const IOTensor &io: outputs) {
+                if (io.dmaBufFd < 0) continue;
+                TensorId id = kNoTensor;
+                for (TensorId t: graph_.outputs)
+                    if (graph_.desc(t).name == io.name || (outputs.size() == 1 && graph_.outputs.size() == 1)) id = t;
+                if (id == kNoTensor) throw Error(Status::NotFound, "no graph output named " + io.name);
+                pool_[id].dmaBufFd     = io.dmaBufFd;
+                pool_[id].dmaBufFormat = io.dmaBufFormat;
+                pool_[id].dmaBufDtype  = io.dmaBufDtype;
+            }
             for (const IOTensor &io: inputs) {
                 TensorId id = graph_.find(io.name);
                 if (id == kNoTensor && inputs.size() == 1 && graph_.inputs.size() == 1) id = graph_.inputs[0];
                 if (id == kNoTensor) throw Error(Status::NotFound, "no graph input named " + io.name);
                 RtTensor &rt = pool_[id];
+                rt.shape     = graph_.desc(id).shape;
+                if (io.dmaBufFd >= 0) {
+                    rt.dmaBufFd     = io.dmaBufFd;
+                    rt.dmaBufFormat = io.dmaBufFormat;
+                    rt.dmaBufDtype  = io.dmaBufDtype;
+                    rt.hostValid    = false;
+                    rt.deviceValid  = false;
+                    continue;
+                }
                 if (io.dtype != DType::Float32) throw Error(Status::InvalidArgument, "inputs must be fp32");
                 if ((int64_t) io.data.size() != numElements(graph_.desc(id).shape) * 4)
                     throw Error(Status::InvalidArgument, "input " + io.name + " has " + std::to_string(io.data.size() / 4) + " values, expected " +
                                                              std::to_string(numElements(graph_.desc(id).shape)));
-                rt.shape = graph_.desc(id).shape;
                 rt.dtype = DType::Float32;
                 rt.host.bytes = io.data;
                 rt.hostValid   = true;
@@ -199,6 +223,16 @@ namespace vknn {
             outputs.clear();
             for (TensorId t: graph_.outputs) {
                 RtTensor &rt = pool_[t];
+                if (rt.dmaBufFd >= 0) { // written into the caller's buffer; no host data
+                    IOTensor o;
+                    o.name         = graph_.desc(t).name;
+                    o.shape        = graph_.desc(t).shape;
+                    o.dmaBufFd     = rt.dmaBufFd;
+                    o.dmaBufFormat = rt.dmaBufFormat;
+                    o.dmaBufDtype  = rt.dmaBufDtype;
+                    outputs.push_back(std::move(o));
+                    continue;
+                }
                 if (!rt.hostValid)
                     for (auto &b: backends_) {
                         b->toHost(rt, ctx);

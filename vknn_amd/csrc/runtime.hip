@@ -7,6 +7,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <unistd.h>
 
 namespace vkhip {
 
@@ -112,6 +113,66 @@ int vkhip_malloc(void **p, size_t bytes) {
 int vkhip_free(void *p) {
     if (!p) return VKHIP_OK;
     return hip_check(hipFree(p), "hipFree");
+}
+
+// ------------------------------------------------------------------ dma-buf interop
+struct vkhip_dmabuf_s {
+    hipExternalMemory_t mem = nullptr;
+    void               *ptr = nullptr;
+};
+
+int vkhip_dmabuf_import(int fd, size_t bytes, vkhip_dmabuf *out, void **dev_ptr) {
+    int rc = vkhip_init();
+    if (rc) return rc;
+    if (fd < 0 || !bytes || !out || !dev_ptr) return set_error(VKHIP_ERR_INVALID, "dmabuf_import: bad arguments");
+    *out     = nullptr;
+    *dev_ptr = nullptr;
+    // the runtime may take the descriptor it imports: give it a duplicate, the caller keeps fd
+    const int dup_fd = ::dup(fd);
+    if (dup_fd < 0) return set_error(VKHIP_ERR_INVALID, "dmabuf_import: dup failed");
+    hipExternalMemoryHandleDesc hd {};
+    hd.type      = hipExternalMemoryHandleTypeOpaqueFd;
+    hd.handle.fd = dup_fd;
+    hd.size      = bytes;
+    hipExternalMemory_t mem = nullptr;
+    if (hipImportExternalMemory(&mem, &hd) != hipSuccess) {
+        ::close(dup_fd);
+        (void) hipGetLastError();
+        return set_error(VKHIP_ERR_RUNTIME, "dmabuf_import: hipImportExternalMemory failed");
+    }
+    hipExternalMemoryBufferDesc bd {};
+    bd.offset = 0;
+    bd.size   = bytes;
+    void *p   = nullptr;
+    if (hipExternalMemoryGetMappedBuffer(&p, mem, &bd) != hipSuccess) {
+        (void) hipGetLastError();
+        hipDestroyExternalMemory(mem);
+        return set_error(VKHIP_ERR_RUNTIME, "dmabuf_import: hipExternalMemoryGetMappedBuffer failed");
+    }
+    *out     = new vkhip_dmabuf_s {mem, p};
+    *dev_ptr = p;
+    return VKHIP_OK;
+}
+
+int vkhip_dmabuf_release(vkhip_dmabuf h) {
+    if (!h) return VKHIP_OK;
+    int rc = VKHIP_OK;
+    if (h->ptr && hipFree(h->ptr) != hipSuccess) rc = set_error(VKHIP_ERR_RUNTIME, "dmabuf_release: hipFree of the mapping failed");
+    if (h->mem && hipDestroyExternalMemory(h->mem) != hipSuccess) rc = set_error(VKHIP_ERR_RUNTIME, "dmabuf_release: hipDestroyExternalMemory failed");
+    delete h;
+    return rc;
+}
+
+int vkhip_dmabuf_export(const void *dev_ptr, size_t bytes, int *fd) {
+    if (!dev_ptr || !bytes || !fd) return set_error(VKHIP_ERR_INVALID, "dmabuf_export: bad arguments");
+    *fd = -1;
+    int h = -1;
+    if (hipMemGetHandleForAddressRange(&h, (hipDeviceptr_t) dev_ptr, bytes, hipMemRangeHandleTypeDmaBufFd, 0) != hipSuccess || h < 0) {
+        (void) hipGetLastError();
+        return set_error(VKHIP_ERR_RUNTIME, "dmabuf_export: hipMemGetHandleForAddressRange failed");
+    }
+    *fd = h;
+    return VKHIP_OK;
 }
 
 int vkhip_memcpy_h2d(void *dst, const void *src, size_t bytes, vkhip_stream_t s) {
