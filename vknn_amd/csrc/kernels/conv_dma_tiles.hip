@@ -1,4 +1,4 @@
-// Tile instantiations of conv_dma_kernel (tiles 11-16, 24, 25: dense B operands via LDS DMA).
+// Tile instantiations of conv_dma_kernel (tiles 11-16, 24, 25, 28-31: dense B operands via LDS DMA).
 #include "conv_kernels.h"
 
 namespace vkhip {
@@ -46,6 +46,10 @@ namespace vkhip {
             case 16: return pick_dma<2, 2, 4, 2, 2>(steps, bmode);
             case 24: return pick_dma<1, 2, 2, 2, 2>(steps, bmode);
             case 25: return pick_dma<2, 2, 2, 1, 4>(steps, bmode);
+            case 28: return pick_dma<1, 2, 3, 2, 2>(steps, bmode);
+            case 29: return pick_dma<2, 2, 3, 2, 2>(steps, bmode);
+            case 30: return pick_dma<2, 2, 3, 1, 4>(steps, bmode);
+            case 31: return pick_dma<1, 2, 4, 2, 2>(steps, bmode);
         }
         return nullptr;
     }

@@ -1426,9 +1426,13 @@ namespace vkhip {
         {64, 256, 1, 4, 2, 2, 2},     // 25
         {64, 128, 1, 4, 3, 2, 1, 1},  // 26 halo (2-stage ring, two workgroups per CU for small bands)
         {64, 256, 1, 4, 3, 2, 2, 1},  // 27 halo (one stage: workgroups overlap each other instead of a ring)
+        {64, 128, 2, 2, 2, 1, 2},     // 28 tile 24 with a 3-stage ring (two K stages in flight)
+        {128, 128, 2, 2, 2, 2, 2},    // 29 tile 14 with a 3-stage ring
+        {64, 256, 1, 4, 2, 2, 2},     // 30 tile 25 with a 3-stage ring
+        {64, 128, 2, 2, 2, 1, 2},     // 31 tile 24 with a 4-stage ring
     };
-    constexpr int kNumTiles = 28;
-    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8, 15};
+    constexpr int kNumTiles = 32;
+    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8, 15, 0, 0, 0, 0};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 

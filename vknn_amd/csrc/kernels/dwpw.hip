@@ -8,6 +8,7 @@
 // Also hosts the fully-connected helper (a 1x1 conv over [N,K,1,1]).
 #include "common.h"
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 
 namespace vkhip {
@@ -115,6 +116,236 @@ namespace vkhip {
         }
     }
 
+    // Strip-tiled fused dw + pw: a workgroup owns RT whole output rows of one image (BN = RT * OW
+    // pixels, contiguous in every NC4HW4 plane) and walks the E expanded channels in chunks of CB
+    // channel blocks (CB/4 16-deep MFMA K steps; CB * OW <= 256, so each thread owns one
+    // (channel block, output column) of a chunk — two when OW > 64):
+    //   1. the chunk's input rows ((RT-1)*S + K of them, zero columns left and right) and the
+    //      chunk's slice of the packed projection weights are copied into LDS, each thread issuing
+    //      all of its loads before its first LDS write, so a chunk costs one memory latency and
+    //      every input pixel is read from L2 once per workgroup; the thread's depthwise weights go
+    //      to registers as fp16;
+    //   2. the thread walks the IR input rows of its column once, K taps per row, adding each into
+    //      the RT output rows it feeds (RT independent fp32 accumulators, v_fma_mix with fp16
+    //      operands), then applies bias and the dw activation and stores the RT outputs as fp16
+    //      into an LDS chunk laid out as MFMA B fragments (16-byte channel-block pairs per pixel);
+    //   3. each wave accumulates the projection of its 32-pixel fragments over the chunk's K steps
+    //      with v_mfma_f32_32x32x16_f16, A and B from LDS.
+    // The E-channel intermediate lives only in LDS. After the last chunk the epilogue adds bias (+
+    // residual), applies the activation and stores fp16 NC4HW4.
+    //   K: kernel size (3 or 5, square), S: stride (1 or 2), MF: 32-row output fragments (Cout <=
+    //   32 * MF <= 64), RT: output rows per strip (BN = RT * OW <= 256, two pixel fragments per wave).
+    struct DwStrip {
+        int BN, IWp, PLA, NF, CB;
+    };
+
+    // LDS of one chunk: [A: MF*32 rows x CB/2 16-byte k groups | dw weights: CB x K*K float4 |
+    // dw bias: CB float4][B chunk: CB/2 pairs x NF*32 pixels x 16 B][input: CB planes x IR rows x
+    // IWp x 8 B]
+    __host__ __device__ inline size_t dwpw_strip_a_bytes(int MF, int K, const DwStrip &t) {
+        return (size_t) MF * 32 * t.CB * 8 + (size_t) t.CB * K * K * 16 + (size_t) t.CB * 16;
+    }
+    __host__ __device__ inline size_t dwpw_strip_lds(int MF, int K, int IR, const DwStrip &t) {
+        return dwpw_strip_a_bytes(MF, K, t) + (size_t) t.CB / 2 * t.NF * 32 * 16 + (size_t) t.CB * IR * t.IWp * 8;
+    }
+
+
+    template <int K, int S, int MF, int RT>
+    __global__ __launch_bounds__(256, (K == 3 && MF == 1 && RT <= 4) ? 4 : (K == 3 && RT <= 4) ? 3 : 2) void dwpw_strip_kernel(DwPwArgs a, DwStrip t) {
+        constexpr int IR  = (RT - 1) * S + K;
+        constexpr int NFW = 2;
+        extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
+        const size_t ab = dwpw_strip_a_bytes(MF, K, t);
+        uint4 *asm_ = reinterpret_cast<uint4 *>(dsm);                                              // [MF*32][CB/2], weights, bias
+        uint4 *bch  = reinterpret_cast<uint4 *>(dsm + ab);                                         // [CB/2][NF*32]
+        uint2 *stg  = reinterpret_cast<uint2 *>(dsm + ab + (size_t) t.CB / 2 * t.NF * 32 * 16);    // [CB][IR][IWp]
+        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+        const int row_tiles = (a.OH + RT - 1) / RT;
+        const int n     = blockIdx.x / row_tiles;
+        const int oy0   = (blockIdx.x - n * row_tiles) * RT;
+        const int nrows = min(RT, a.OH - oy0);
+        const int npx   = nrows * a.OW;
+        const int iy0   = oy0 * S - a.PT;
+        const int OHW = a.OH * a.OW, HW = a.H * a.W;
+        const int BNF = t.NF * 32, CB = t.CB, KG = CB / 2;
+        const int IWp = t.IWp;
+        const int items = CB * a.OW;
+
+        // input copy geometry: each thread keeps one column and steps down rows (plane-major)
+        const int  rpp  = 256 / IWp;
+        const int  ccol = tid % IWp;
+        const int  crow = tid / IWp;
+        const int  cix  = ccol - t.PLA;
+        const bool cok  = (unsigned) cix < (unsigned) a.W && crow < rpp;
+
+        float16v acc[MF][NFW];
+#pragma unroll
+        for (int m = 0; m < MF; ++m)
+#pragma unroll
+            for (int f = 0; f < NFW; ++f)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[m][f][r] = 0.f;
+
+        const int chunks = (a.Ebp + CB - 1) / CB;
+        const int rows   = CB * IR;                 // input rows of a chunk
+        const int na     = MF * 32 * KG, nw = CB * K * K, n16 = na + nw + CB; // 16-byte units
+        // 1. a chunk's data goes global -> registers -> LDS with a batch of loads in flight per
+        //    thread before its LDS writes (other workgroups on the CU compute meanwhile): input rows
+        //    (8-byte units; each thread keeps one column and steps down the rows), then the
+        //    projection weights, depthwise weights and bias (16-byte units, contiguous in LDS)
+        for (int ch = 0; ch < chunks; ++ch) {
+            const int cb0 = ch * CB;
+            {
+                constexpr int U = 6;
+                for (int base = crow; base < rows; base += U * rpp) {
+                    uint2 v[U];
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const int row = base + u * rpp;
+                        const int pl = row / IR, r = row - pl * IR; // IR is a compile-time constant
+                        const int cb = cb0 + pl, iy = iy0 + r;
+                        v[u] = uint2 {0u, 0u};
+                        if (row < rows && cok && cb < a.Eb && (unsigned) iy < (unsigned) a.H)
+                            v[u] = a.x[((long long) n * a.Eb + cb) * HW + (long long) iy * a.W + cix];
+                    }
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const int row = base + u * rpp;
+                        if (row < rows && crow < rpp) stg[row * IWp + ccol] = v[u];
+                    }
+                }
+            }
+            for (int i = tid; i < n16; i += 256) {
+                const uint4 *src = nullptr;
+                if (i < na) {
+                    const int row = i / KG, k0 = cb0 * 4 + (i - row * KG) * 8;
+                    if (k0 < a.Kp) src = reinterpret_cast<const uint4 *>(a.pw_w + (long long) row * a.Kp + k0);
+                } else if (i < na + nw) {
+                    if (cb0 + (i - na) / (K * K) < a.Eb) src = reinterpret_cast<const uint4 *>(a.dw_w) + (long long) cb0 * K * K + (i - na);
+                } else if (cb0 + (i - na - nw) < a.Eb) {
+                    src = reinterpret_cast<const uint4 *>(a.dw_b) + cb0 + (i - na - nw);
+                }
+                asm_[i] = src ? *src : uint4 {0u, 0u, 0u, 0u};
+            }
+            __syncthreads();
+            const float4v *wsm = reinterpret_cast<const float4v *>(asm_ + na);
+            const float4v *bsm = wsm + nw;
+            // 2. depthwise for this thread's (channel block, column) items
+            for (int it = tid; it < items; it += 256) {
+                const int cbl = it / a.OW;
+                const int ox  = it - cbl * a.OW;
+                const int cb  = cb0 + cbl;
+                uint2    *dst = reinterpret_cast<uint2 *>(&bch[(cbl >> 1) * BNF + ox]) + (cbl & 1);
+                if (cb >= a.Eb) {
+#pragma unroll
+                    for (int r = 0; r < RT; ++r)
+                        if (r < nrows) dst[2 * r * a.OW] = uint2 {0u, 0u};
+                    continue;
+                }
+                half4 w[K * K];
+#pragma unroll
+                for (int k = 0; k < K * K; ++k) w[k] = f4_to_h4(wsm[cbl * K * K + k]);
+                const float4v b = bsm[cbl];
+                float4v acc4[RT];
+#pragma unroll
+                for (int r = 0; r < RT; ++r) acc4[r] = b;
+                const uint2 *src = stg + cbl * IR * IWp + ox * S + (t.PLA - a.PL);
+#pragma unroll
+                for (int ir = 0; ir < IR; ++ir) {
+                    half4 tap[K];
+#pragma unroll
+                    for (int kx = 0; kx < K; ++kx) tap[kx] = u2_as_h4(src[ir * IWp + kx]);
+#pragma unroll
+                    for (int r = 0; r < RT; ++r) {
+                        const int ky = ir - r * S;
+                        if (ky < 0 || ky >= K) continue;
+#pragma unroll
+                        for (int kx = 0; kx < K; ++kx) {
+                            const half4 wv = w[ky * K + kx];
+                            acc4[r].x = __builtin_fmaf((float) tap[kx].x, (float) wv.x, acc4[r].x);
+                            acc4[r].y = __builtin_fmaf((float) tap[kx].y, (float) wv.y, acc4[r].y);
+                            acc4[r].z = __builtin_fmaf((float) tap[kx].z, (float) wv.z, acc4[r].z);
+                            acc4[r].w = __builtin_fmaf((float) tap[kx].w, (float) wv.w, acc4[r].w);
+                        }
+                    }
+                }
+                const int c = cb * 4;
+                auto finish = [&](auto act_c) __attribute__((always_inline)) {
+                    constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+                    for (int r = 0; r < RT; ++r) {
+                        if (r >= nrows) break;
+                        float4v v = acc4[r];
+                        v.x = apply_act(v.x, ACT, 0.f, 6.f);
+                        v.y = apply_act(v.y, ACT, 0.f, 6.f);
+                        v.z = apply_act(v.z, ACT, 0.f, 6.f);
+                        v.w = apply_act(v.w, ACT, 0.f, 6.f);
+                        if (c + 0 >= a.E) v.x = 0.f;
+                        if (c + 1 >= a.E) v.y = 0.f;
+                        if (c + 2 >= a.E) v.z = 0.f;
+                        if (c + 3 >= a.E) v.w = 0.f;
+                        dst[2 * r * a.OW] = h4_as_u2(f4_to_h4(v));
+                    }
+                };
+                if (a.dw_act == VKHIP_ACT_RELU) finish(std::integral_constant<int, VKHIP_ACT_RELU> {});
+                else if (a.dw_act == VKHIP_ACT_RELU6) finish(std::integral_constant<int, VKHIP_ACT_RELU6> {});
+                else finish(std::integral_constant<int, VKHIP_ACT_NONE> {});
+            }
+            // pixels past the strip's last row (fragment padding) read as zero
+            for (int i = tid; i < KG * BNF; i += 256)
+                if (i % BNF >= npx) bch[i] = uint4 {0u, 0u, 0u, 0u};
+            __syncthreads();
+            // 3. projection: the chunk's K steps for every fragment of this wave
+            for (int ks = 0; ks < CB / 4; ++ks) {
+                const int kg = ks * 2 + (lane >> 5);
+#pragma unroll
+                for (int f = 0; f < NFW; ++f) {
+                    const int fr = wave + 4 * f;
+                    if (fr >= t.NF) break;
+                    const half8 bf = *reinterpret_cast<const half8 *>(&bch[kg * BNF + fr * 32 + (lane & 31)]);
+#pragma unroll
+                    for (int m = 0; m < MF; ++m) {
+                        const half8 af = *reinterpret_cast<const half8 *>(&asm_[(m * 32 + (lane & 31)) * KG + kg]);
+                        acc[m][f]      = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[m][f], 0, 0, 0);
+                    }
+                }
+            }
+            __syncthreads(); // the next chunk overwrites every LDS region
+        }
+
+        // epilogue: bias (+ residual) + activation, fp16 NC4HW4 store
+        const int lk = lane >> 5;
+#pragma unroll
+        for (int f = 0; f < NFW; ++f) {
+            const int fr = wave + 4 * f;
+            if (fr >= t.NF) break;
+            const int px = fr * 32 + (lane & 31);
+            if (px >= npx) continue;
+            const long long pix = (long long) oy0 * a.OW + px; // within the image's plane
+#pragma unroll
+            for (int m = 0; m < MF; ++m)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int oc  = m * 32 + q * 8 + lk * 4;
+                    const int ocb = oc >> 2;
+                    if (ocb >= a.Coutb) continue;
+                    float4v v = {acc[m][f][q * 4 + 0], acc[m][f][q * 4 + 1], acc[m][f][q * 4 + 2], acc[m][f][q * 4 + 3]};
+                    v += *reinterpret_cast<const float4v *>(a.pw_b + oc);
+                    const long long yi = ((long long) n * a.Coutb + ocb) * OHW + pix;
+                    if (a.has_res) v += h4_to_f4(u2_as_h4(a.res[yi]));
+                    v.x = apply_act(v.x, a.act, a.lo, a.hi);
+                    v.y = apply_act(v.y, a.act, a.lo, a.hi);
+                    v.z = apply_act(v.z, a.act, a.lo, a.hi);
+                    v.w = apply_act(v.w, a.act, a.lo, a.hi);
+                    if (oc + 0 >= a.Cout) v.x = 0.f;
+                    if (oc + 1 >= a.Cout) v.y = 0.f;
+                    if (oc + 2 >= a.Cout) v.z = 0.f;
+                    if (oc + 3 >= a.Cout) v.w = 0.f;
+                    a.y[yi] = h4_as_u2(f4_to_h4(v));
+                }
+        }
+    }
+
     struct DwPwGeom {
         int64_t Eb, Ebp, Kp, Coutb, Coutp, m_frags;
         size_t  off_dwb, off_dww, off_pwb, off_pww, bytes;
@@ -122,6 +353,61 @@ namespace vkhip {
     };
 
     static size_t a256(size_t v) { return (v + 255) & ~(size_t) 255; }
+
+
+    typedef void (*GemmStripFn)(DwPwArgs, DwStrip);
+    constexpr int kStripRT[] = {14, 8, 7, 4, 2}; // rows per strip the kernel is built for
+    template <int K, int S, int MF>
+    static GemmStripFn strip_rt(int rt) {
+        switch (rt) {
+            case 14: return dwpw_strip_kernel<K, S, MF, 14>;
+            case 8: return dwpw_strip_kernel<K, S, MF, 8>;
+            case 7: return dwpw_strip_kernel<K, S, MF, 7>;
+            case 4: return dwpw_strip_kernel<K, S, MF, 4>;
+            case 2: return dwpw_strip_kernel<K, S, MF, 2>;
+        }
+        return nullptr;
+    }
+    static GemmStripFn dwpw_strip_fn(int K, int S, int mf, int rt) {
+        if (mf != 1 && mf != 2) return nullptr;
+        if (K == 3) {
+            if (S == 1) return mf == 1 ? strip_rt<3, 1, 1>(rt) : strip_rt<3, 1, 2>(rt);
+            return mf == 1 ? strip_rt<3, 2, 1>(rt) : strip_rt<3, 2, 2>(rt);
+        }
+        if (S == 1) return mf == 1 ? strip_rt<5, 1, 1>(rt) : strip_rt<5, 1, 2>(rt);
+        return mf == 1 ? strip_rt<5, 2, 1>(rt) : strip_rt<5, 2, 2>(rt);
+    }
+
+    // The strip kernel takes square 3x3 / 5x5 kernels at stride 1 or 2 without dilation, up to 64
+    // output channels and rows of at most 128 pixels. Rows per strip: the largest built RT with
+    // RT * OW <= 256 (and no more than the output has, unless none fits); channel blocks per chunk:
+    // the largest multiple of 4 with CB * OW <= 256 (at least 4), at most the padded channel count,
+    // halved until the chunk fits 64 KB of LDS (room for a second workgroup per CU).
+    static bool dwpw_strip_fits(const vkhip_dwpw_desc *d, const DwPwGeom &g, DwStrip &t, int &RT) {
+        const vkhip_conv_desc &c = d->dw;
+        if (c.KH != c.KW || (c.KH != 3 && c.KH != 5) || c.SH != c.SW || (c.SH != 1 && c.SH != 2) || c.DH != 1 || c.DW != 1) return false;
+        if (g.m_frags > 2 || c.PL < 0 || c.PT < 0 || c.OW > 128) return false;
+        RT = 0;
+        for (int rt: kStripRT)
+            if (rt * c.OW <= 256 && (rt <= c.OH || RT == 0)) {
+                RT = rt;
+                if (rt <= c.OH) break;
+            }
+        if (!RT) return false;
+        t.BN  = RT * c.OW;
+        t.NF  = (int) ceil_div(t.BN, 32);
+        if (t.NF > 8) return false;
+        t.PLA = c.PL;
+        t.IWp = std::max((c.OW - 1) * c.SW + c.KW, c.W + c.PL);
+        if (t.IWp > 256) return false;
+        t.CB = (int) std::max<int64_t>(4, (256 / c.OW) / 4 * 4);
+        t.CB = (int) std::min<int64_t>(t.CB, g.Ebp);
+        const int IR = (RT - 1) * c.SH + c.KH;
+        auto fits = [&]() { return dwpw_strip_lds((int) g.m_frags, c.KH, IR, t) <= 64 * 1024; };
+        while (t.CB > 4 && !fits()) t.CB -= 4;
+        if (t.CB % 4) return false;
+        return fits();
+    }
 
     static DwPwGeom dwpw_geom(const vkhip_dwpw_desc *d) {
         DwPwGeom g;
@@ -283,6 +569,23 @@ int vkhip_dwpw_forward(const vkhip_dwpw_desc *d, const void *x, const void *blob
     a.Cout = d->Cout; a.Coutb = (int) g.Coutb; a.m_frags = (int) g.m_frags; a.Kp = (int) g.Kp;
     a.P = c.N * c.OH * c.OW;
     a.act = d->act; a.lo = d->act_lo; a.hi = d->act_hi; a.has_res = d->has_res;
+    DwStrip t;
+    int     RT = 0;
+    // VKHIP_DWPW_STRIP=0 keeps the untiled kernel (A/B measurements)
+    static const bool strip_on = [] {
+        const char *e = std::getenv("VKHIP_DWPW_STRIP");
+        return !(e && e[0] == '0');
+    }();
+    if (strip_on && dwpw_strip_fits(d, g, t, RT)) {
+        const size_t sm = dwpw_strip_lds((int) g.m_frags, c.KH, (RT - 1) * c.SH + c.KH, t);
+        dim3         grid((unsigned) (c.N * ceil_div(c.OH, RT)));
+        hipStream_t  st = resolve_stream(s);
+        GemmStripFn  fn = dwpw_strip_fn(c.KH, c.SH, (int) g.m_frags, RT);
+        if (fn) {
+            fn<<<grid, 256, sm, st>>>(a, t);
+            return check_launch("dwpw_strip");
+        }
+    }
     size_t sm = (size_t) g.Ebp / 2 * g.BN * 16;
     dim3   grid((unsigned) ceil_div(a.P, g.BN));
     if (g.BN == 64) dwpw_kernel<64><<<grid, 256, sm, resolve_stream(s)>>>(a);
