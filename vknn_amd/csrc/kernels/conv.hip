@@ -286,43 +286,73 @@ namespace vkhip {
         for (int k = 0; k < KH * KW; ++k) w[k] = a.w[(long long) cb * KH * KW + k];
         const float4v b0 = *reinterpret_cast<const float4v *>(a.bias + cb * 4);
 
-        // input rows -> LDS: each thread keeps one column and steps down the rows (plane-major),
-        // U rows per round with all U loads issued before any LDS write, so a round costs one
-        // memory latency instead of U (most tiles need a single round)
         const int W = a.W, H = a.H;
-        const bool v16 = (W % 2 == 0) && (PLA % 2 == 0);
-        {
-            constexpr int U = 16;
-            const int cols  = v16 ? IWp / 2 : IWp; // 16- or 8-byte units per LDS row
-            const int rpp   = 256 / cols;
-            const int col   = tid % cols;
-            const int ix    = (v16 ? 2 * col : col) - PLA;
-            const bool cok  = ix >= 0 && ix < W;
-            const int rows  = np * IR;
-            const int r2    = tid / cols;
-            if (r2 < rpp) {
-                auto copy = [&](auto vec_c) __attribute__((always_inline)) {
-                    using T = decltype(vec_c);
-                    for (int base = r2; base < rows; base += U * rpp) {
-                        T v[U];
+        if (t.row_tiles == 1) {
+            // One strip covers every output row, so the workgroup's planes are one contiguous range
+            // of the input (np * H * W pixels from plane p0): zero the LDS tile, then copy the range
+            // linearly — fully coalesced, all of a thread's loads in flight at once — and drop each
+            // pixel at its padded tile position (row iy + PT, column ix + PLA).
+            const int tile_units = np * IR * IWp;
+            for (int i = tid; i < tile_units; i += 256) tile[i] = uint2 {0u, 0u};
+            __syncthreads();
+            constexpr int U    = 16;
+            const int     HW   = H * W;
+            const int     tot  = np * HW;
+            const uint2  *base = a.x + (long long) p0 * HW;
+            for (int b0 = tid; b0 < tot; b0 += 256 * U) {
+                uint2 v[U];
 #pragma unroll
-                        for (int u = 0; u < U; ++u) {
-                            const int  row = base + u * rpp;
-                            const int  pl  = row / IR, r = row - pl * IR; // IR is a compile-time constant
-                            const int  iy  = iy0 + r;
-                            const bool ok  = row < rows && cok && (unsigned) iy < (unsigned) H;
-                            v[u] = T {};
-                            if (ok) v[u] = *reinterpret_cast<const T *>(a.x + ((long long) (p0 + pl) * H + iy) * W + ix);
-                        }
+                for (int u = 0; u < U; ++u) {
+                    const int e = b0 + u * 256;
+                    v[u]        = e < tot ? base[e] : uint2 {0u, 0u};
+                }
 #pragma unroll
-                        for (int u = 0; u < U; ++u) {
-                            const int row = base + u * rpp;
-                            if (row < rows) reinterpret_cast<T *>(tile)[row * cols + col] = v[u];
+                for (int u = 0; u < U; ++u) {
+                    const int e = b0 + u * 256;
+                    if (e >= tot) break;
+                    const int pl = e / HW, pix = e - pl * HW;
+                    const int iy = pix / W, ix = pix - iy * W;
+                    tile[(pl * IR + iy + a.PT) * IWp + ix + PLA] = v[u];
+                }
+            }
+        } else {
+            // input rows -> LDS: each thread keeps one column and steps down the rows (plane-major),
+            // U rows per round with all U loads issued before any LDS write, so a round costs one
+            // memory latency instead of U (most tiles need a single round)
+            const bool v16 = (W % 2 == 0) && (PLA % 2 == 0);
+            {
+                constexpr int U = 16;
+                const int cols  = v16 ? IWp / 2 : IWp; // 16- or 8-byte units per LDS row
+                const int rpp   = 256 / cols;
+                const int col   = tid % cols;
+                const int ix    = (v16 ? 2 * col : col) - PLA;
+                const bool cok  = ix >= 0 && ix < W;
+                const int rows  = np * IR;
+                const int r2    = tid / cols;
+                if (r2 < rpp) {
+                    auto copy = [&](auto vec_c) __attribute__((always_inline)) {
+                        using T = decltype(vec_c);
+                        for (int base = r2; base < rows; base += U * rpp) {
+                            T v[U];
+    #pragma unroll
+                            for (int u = 0; u < U; ++u) {
+                                const int  row = base + u * rpp;
+                                const int  pl  = row / IR, r = row - pl * IR; // IR is a compile-time constant
+                                const int  iy  = iy0 + r;
+                                const bool ok  = row < rows && cok && (unsigned) iy < (unsigned) H;
+                                v[u] = T {};
+                                if (ok) v[u] = *reinterpret_cast<const T *>(a.x + ((long long) (p0 + pl) * H + iy) * W + ix);
+                            }
+    #pragma unroll
+                            for (int u = 0; u < U; ++u) {
+                                const int row = base + u * rpp;
+                                if (row < rows) reinterpret_cast<T *>(tile)[row * cols + col] = v[u];
+                            }
                         }
-                    }
-                };
-                if (v16) copy(u32x4 {});
-                else copy(u32x2 {});
+                    };
+                    if (v16) copy(u32x4 {});
+                    else copy(u32x2 {});
+                }
             }
         }
         __syncthreads();
