@@ -237,6 +237,15 @@ typedef struct vkhip_pool_desc {
     int32_t N, C, H, W, OH, OW, KH, KW, SH, SW, PT, PL;
 } vkhip_pool_desc;
 int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s);
+/* A first-layer conv (at most 4 input channels, 3x3 or 7x7, stride 1 or 2, pad K/2, <= 64 output
+ * channels, no residual) followed by a 3x3 stride-2 pad-1 max pool over its output, in one
+ * kernel: y = maxpool(act(conv(x) + bias)), bit-identical to vkhip_conv_forward then
+ * vkhip_maxpool, without the conv output in memory. The plan must be a stem-kernel plan with
+ * 64-row tiles (vkhip_conv_plan_make with tile 21 or 22) and its packed blob. No counterpart in the
+ * reference, which runs the two as separate ops (ops/conv.cpp, ops/pool.cpp). */
+int vkhip_conv_maxpool_supported(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const vkhip_pool_desc *p);
+int vkhip_conv_maxpool_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const vkhip_pool_desc *p, const void *x, const void *blob,
+                               void *y, vkhip_stream_t s);
 /* Fully connected y[N,M] = act(x[N,K] W^T + b): x/y are [N,C,1,1] NC4HW4 fp16 tensors.
  * Blob: fp16 W[Mp][Kp] followed by fp32 b[Mp], Mp = M rounded up to 16, Kp = K rounded up to 32,
  * zero padded (vkhip_fc_weight_bytes). One skinny-GEMM kernel: 16 x 16/32 output tiles, K split

@@ -288,6 +288,64 @@ def test_conv_stem(gpu, tile, case):
     assert_parity(got, ref, f"stem tile {tile} {case}")
 
 
+@pytest.mark.parametrize("tile", [21, 22])
+@pytest.mark.parametrize("case", [(2, 3, 224, 224, 64, 7, 2, 1), (1, 3, 33, 40, 64, 7, 2, 0), (3, 4, 30, 46, 48, 3, 2, 2),
+                                  (2, 1, 17, 18, 20, 7, 1, 1), (1, 3, 9, 250, 64, 7, 2, 1)])
+def test_conv_maxpool_fused(gpu, tile, case):
+    """Stem conv + 3x3/s2/p1 max pool in one kernel: bit-identical to the conv kernel followed by
+    the max-pool kernel (odd heights, ragged output channels, stride 1 and 2, wide rows with one
+    pooled row per workgroup), and the pool of the oracle conv within the fp16 tolerance."""
+    lib = V.vkhip()
+    N, C, H, W, Cout, K, S, act = case
+    r = rng(170 + tile + H + K)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, K, K)) * np.sqrt(2.0 / (K * K * C))).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    p = K // 2
+    lo, hi = (0.0, 6.0) if act == 2 else (0.0, 0.0)
+    d, (_, _, OH, OW) = conv_desc(x.shape, w.shape, (S, S), (p, p, p, p), act=act, lo=lo, hi=hi)
+    POH, POW = (OH - 1) // 2 + 1, (OW - 1) // 2 + 1
+    pd = V.PoolDesc(N=N, C=Cout, H=OH, W=OW, OH=POH, OW=POW, KH=3, KW=3, SH=2, SW=2, PT=1, PL=1)
+    plan = V.ConvPlan()
+    check(lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, tile, 0, ctypes.byref(plan)), "plan")
+    assert lib.vkhip_conv_maxpool_supported(ctypes.byref(d), ctypes.byref(plan), ctypes.byref(pd)) == 1
+    blob = np.zeros(plan.weight_bytes, np.uint8)
+    check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(plan), w.ctypes.data, b.ctypes.data, blob.ctypes.data))
+    dblob = DeviceBuffer.from_array(blob)
+    dx = to_device_nc4(x)
+    dconv = DeviceBuffer(V.nc4_elems(N, Cout, OH, OW) * 2)
+    dpool = DeviceBuffer(V.nc4_elems(N, Cout, POH, POW) * 2)
+    dfused = DeviceBuffer(V.nc4_elems(N, Cout, POH, POW) * 2)
+    print(f"conv+maxpool tile {tile} case {case}", flush=True)
+    check(lib.vkhip_conv_forward(ctypes.byref(d), ctypes.byref(plan), dx.ptr, dblob.ptr, None, dconv.ptr, None, None))
+    check(lib.vkhip_maxpool(ctypes.byref(pd), dconv.ptr, dpool.ptr, None))
+    check(lib.vkhip_conv_maxpool_forward(ctypes.byref(d), ctypes.byref(plan), ctypes.byref(pd), dx.ptr, dblob.ptr, dfused.ptr, None))
+    check(lib.vkhip_stream_sync(None))
+    assert np.array_equal(raw_nc4(dfused, (N, Cout, POH, POW)), raw_nc4(dpool, (N, Cout, POH, POW)))
+    conv_ref = oracle_conv(x, w, b, (S, S), (p, p, p, p), act=act, lo=lo, hi=hi)
+    ref = np.zeros((N, Cout, POH, POW), np.float32)
+    oracle().oracle_maxpool(np.ascontiguousarray(conv_ref).ctypes.data, ref.ctypes.data, N, Cout, OH, OW, 3, 3, 2, 2, 1, 1, POH, POW)
+    assert_parity(from_device_nc4(dfused, (N, Cout, POH, POW)), ref, f"conv+maxpool {case}")
+
+
+def test_conv_maxpool_rejects_other_shapes(gpu):
+    lib = V.vkhip()
+    plan = V.ConvPlan()
+    d, (_, _, OH, OW) = conv_desc((1, 3, 32, 32), (64, 3, 7, 7), (2, 2), (3, 3, 3, 3), act=1)
+    ok = V.PoolDesc(N=1, C=64, H=OH, W=OW, OH=(OH - 1) // 2 + 1, OW=(OW - 1) // 2 + 1, KH=3, KW=3, SH=2, SW=2, PT=1, PL=1)
+    check(lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, 21, 0, ctypes.byref(plan)))
+    assert lib.vkhip_conv_maxpool_supported(ctypes.byref(d), ctypes.byref(plan), ctypes.byref(ok)) == 1
+    for field, val in [("KH", 2), ("SH", 1), ("PT", 0), ("OH", ok.OH + 1), ("C", 32)]:
+        bad = V.PoolDesc(**{f: getattr(ok, f) for f, _ in V.PoolDesc._fields_})
+        setattr(bad, field, val)
+        assert lib.vkhip_conv_maxpool_supported(ctypes.byref(d), ctypes.byref(plan), ctypes.byref(bad)) == 0, field
+    wide, _ = conv_desc((1, 3, 32, 32), (96, 3, 7, 7), (2, 2), (3, 3, 3, 3))
+    assert lib.vkhip_conv_plan_make(ctypes.byref(wide), V.CONV_GEMM, 21, 0, ctypes.byref(plan)) != 0 or \
+        lib.vkhip_conv_maxpool_supported(ctypes.byref(wide), ctypes.byref(plan), ctypes.byref(ok)) == 0
+    check(lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, 0, 0, ctypes.byref(plan)))
+    assert lib.vkhip_conv_maxpool_supported(ctypes.byref(d), ctypes.byref(plan), ctypes.byref(ok)) == 0
+
+
 def test_conv_stem_rejects_other_shapes(gpu):
     lib = V.vkhip()
     plan = V.ConvPlan()

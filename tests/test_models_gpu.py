@@ -194,3 +194,23 @@ def test_side_stream_branches_match_single_stream(gpu, model, batch, opts, graph
     for _ in range(3):
         x = rng.standard_normal(int(np.prod(s1.in_shape))).astype(np.float32)
         np.testing.assert_array_equal(s2.run(x), s1.run(x))
+
+
+@pytest.mark.parametrize("model,batch", [("resnet_tiny", 3), ("resnet50", 2)])
+def test_stem_maxpool_fused(gpu, model, batch, monkeypatch):
+    """With VKNN_HIP_FUSE_POOL=1 the ResNet stem conv and its 3x3/s2 max pool run as one kernel
+    (the pool node folded into the conv): outputs within the tolerance of the session that runs
+    them apart (default), and of the oracle."""
+    monkeypatch.setenv("VKNN_HIP_FUSE_POOL", "1")
+    sess = V.Session(model, batch, seed=7)
+    plan = sess.describe()
+    assert plan.count("+max pool") == 1 and plan.count("max pool folded into") == 1, plan
+    x = make_input(sess.in_shape, 6)
+    got = sess.run(x)
+    monkeypatch.setenv("VKNN_HIP_FUSE_POOL", "0")
+    plain = V.Session(model, batch, seed=7)
+    assert "+max pool" not in plain.describe()
+    ref = plain.run(x)
+    # the two sessions may pick different tiles for the other convs, so compare at the tolerance
+    check_outputs(got, ref, sess.out_elems, f"{model} fused stem pool vs apart")
+    check_outputs(got, oracle_model_run(model, batch, 7, x), sess.out_elems, f"{model} fused stem pool vs oracle")

@@ -58,6 +58,8 @@ VKHIP_API = {
     "vkhip_malloc": (c_int, [P(c_vp), c_sz]),
     "vkhip_free": (c_int, [c_vp]),
     "vkhip_dispatch_marker": (c_int, [c_i32, c_vp]),
+    "vkhip_conv_maxpool_supported": (c_int, [c_vp, c_vp, c_vp]),
+    "vkhip_conv_maxpool_forward": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_plan_kernel": (c_char_p, [c_vp]),
     "vkhip_dmabuf_import": (c_int, [c_int, c_sz, P(c_vp), P(c_vp)]),
     "vkhip_dmabuf_release": (c_int, [c_vp]),

@@ -97,6 +97,11 @@ namespace vknn {
             // scale) is folded into this conv: the conv reads the Mul's unscaled operand `scaledIn`
             // and multiplies it by `xscale` ([N,C,1,1]) on the way into the GEMM.
             TensorId                scaledIn = kNoTensor, xscale = kNoTensor;
+            // Set by the segment when the 3x3 stride-2 max pool that is this conv's only reader is
+            // fused into it (a first-layer conv): the conv writes the pooled tensor `poolOut` and
+            // its own output never exists in memory.
+            TensorId                poolOut = kNoTensor;
+            vkhip_pool_desc         pd {};
 
             void prepare(const Node &node, SegEnv &env) override {
                 const Graph &g = *env.graph;
@@ -123,6 +128,16 @@ namespace vknn {
                         (int64_t) d.Cout * (d.Cin / d.group) * d.KH * d.KW * 2;
                 const float *w = initF32(g, node.inputs[1]);
                 const float *b = initF32(g, biasOf(node));
+                if (poolOut != kNoTensor) {
+                    // the fused stem + pool kernel runs the 64-row stem tiles
+                    bool ok = false;
+                    for (int t: {21, 22})
+                        if (!ok && vkhip_conv_plan_make(&d, VKHIP_CONV_GEMM, t, 0, &plan) == VKHIP_OK && vkhip_conv_maxpool_supported(&d, &plan, &pd)) ok = true;
+                    if (!ok) throw Error(Status::RuntimeError, "conv + max pool fusion planned for an unsupported shape: " + name);
+                    bytes = (int64_t) (nc4Bytes(g.desc(in).shape) + nc4Bytes(g.desc(poolOut).shape)) + (int64_t) d.Cout * d.Cin * d.KH * d.KW * 2;
+                    build(w, b);
+                    return;
+                }
                 choosePlan(env, w, b);
             }
 
@@ -300,6 +315,10 @@ namespace vknn {
             }
 
             void record(SegEnv &env, vkhip_stream_t s) override {
+                if (poolOut != kNoTensor) {
+                    check(vkhip_conv_maxpool_forward(&d, &plan, &pd, env.dev(in), blob->ptr, env.dev(poolOut), s), "conv + max pool " + name);
+                    return;
+                }
                 check(forward(plan, env.dev(in), xscale != kNoTensor ? env.dev(xscale) : nullptr, blob->ptr,
                               res != kNoTensor ? env.dev(res) : nullptr, env.dev(out), ws ? ws->ptr : nullptr, s),
                       "conv " + name);
@@ -308,7 +327,8 @@ namespace vknn {
             std::string describe() const override {
                 static const char *algos[] = {"auto", "gemm", "splitk", "winograd", "depthwise"};
                 return std::string(algos[plan.algo]) + " tile=" + std::to_string(plan.tile) + " ksplit=" + std::to_string(plan.ksplit) +
-                       (d.in_scale ? " +input scale" : "") + " kernel=" + vkhip_conv_plan_kernel(&plan);
+                       (d.in_scale ? " +input scale" : "") + (poolOut != kNoTensor ? " +max pool" : "") + " kernel=" +
+                       (poolOut != kNoTensor ? std::string("stem_pool_kernel") : std::string(vkhip_conv_plan_kernel(&plan)));
             }
         };
 
@@ -708,13 +728,62 @@ namespace vknn {
             void record(SegEnv &, vkhip_stream_t) override {}
         };
 
-        // A channel-broadcast Mul folded into the conv that consumes it (ConvOp::xscale): no launch.
+        // A node folded into a conv (a channel-broadcast Mul into the conv that consumes it,
+        // ConvOp::xscale; a max pool into the conv it reads, ConvOp::poolOut): no launch.
         struct FoldedMulOp: HipOp {
-            std::string into;
+            std::string into, what = "scale";
             void        prepare(const Node &, SegEnv &) override { kind = "folded"; }
             void        record(SegEnv &, vkhip_stream_t) override {}
-            std::string describe() const override { return "scale folded into " + into; }
+            std::string describe() const override { return what + " folded into " + into; }
         };
+
+        // Stem + pool fusion: a MaxPool 3x3 stride 2 pad 1 whose input is the output of a conv of the
+        // same segment that nothing else reads, and that conv a first layer the fused kernel takes
+        // (vkhip_conv_maxpool_supported on its stem plan). Returns conv node -> pool node.
+        static void planPoolFolds(const Graph &g, const std::vector<int> &idx, std::map<int, int> &convPool) {
+            std::set<int>           inSeg(idx.begin(), idx.end());
+            std::map<TensorId, int> readers, producer;
+            for (size_t i = 0; i < g.nodes.size(); ++i) {
+                const Node &nd = g.nodes[i];
+                for (TensorId t: nd.inputs)
+                    if (t != kNoTensor) ++readers[t];
+                if (nd.fusedResidual != kNoTensor) ++readers[nd.fusedResidual];
+                for (TensorId t: nd.outputs)
+                    if (t != kNoTensor) producer[t] = (int) i;
+            }
+            for (TensorId t: g.outputs) readers[t] += 1000;
+            for (int i: idx) {
+                const Node &p = g.nodes[i];
+                if (p.type != OpType::MaxPool || p.inputs.empty()) continue;
+                auto k = attrInts(p, "kernel_shape", {1, 1}), st = attrInts(p, "strides", {1, 1}), pad = attrInts(p, "pads", {0, 0, 0, 0});
+                auto dl = attrInts(p, "dilations", {1, 1});
+                if (k[0] != 3 || k[1] != 3 || st[0] != 2 || st[1] != 2 || pad[0] != 1 || pad[1] != 1 || pad[2] != 1 || pad[3] != 1 ||
+                    p.attr.geti("ceil_mode", 0) || dl[0] != 1 || dl[1] != 1)
+                    continue;
+                const TensorId t = p.inputs[0];
+                auto           pit = producer.find(t);
+                if (pit == producer.end() || !inSeg.count(pit->second) || readers[t] != 1) continue;
+                const Node &c = g.nodes[pit->second];
+                if (c.type != OpType::Conv || c.fusedResidual != kNoTensor || c.inputs.size() < 2 || !g.isInitializer(c.inputs[1])) continue;
+                const Shape &ws = g.desc(c.inputs[1]).shape;
+                NCHW         x = NCHW::from(g.desc(c.inputs[0]).shape), y = NCHW::from(g.desc(t).shape), z = NCHW::from(g.desc(p.outputs[0]).shape);
+                auto cst = attrInts(c, "strides", {1, 1}), cpad = attrInts(c, "pads", {0, 0, 0, 0}), cdl = attrInts(c, "dilations", {1, 1});
+                if (ws.size() != 4) continue;
+                vkhip_conv_desc d {};
+                d.N = (int) x.n; d.Cin = (int) x.c; d.H = (int) x.h; d.W = (int) x.w; d.Cout = (int) ws[0]; d.OH = (int) y.h; d.OW = (int) y.w;
+                d.KH = (int) ws[2]; d.KW = (int) ws[3]; d.SH = (int) cst[0]; d.SW = (int) cst[1]; d.PT = (int) cpad[0]; d.PL = (int) cpad[1];
+                d.DH = (int) cdl[0]; d.DW = (int) cdl[1]; d.group = (int) c.attr.geti("group", 1); d.act = (int) c.fusedAct;
+                if (cpad[2] != cpad[0] || cpad[3] != cpad[1]) continue;
+                vkhip_pool_desc pd {};
+                pd.N = (int) y.n; pd.C = (int) y.c; pd.H = (int) y.h; pd.W = (int) y.w; pd.OH = (int) z.h; pd.OW = (int) z.w;
+                pd.KH = pd.KW = 3; pd.SH = pd.SW = 2; pd.PT = pd.PL = 1;
+                vkhip_conv_plan plan;
+                bool            ok = false;
+                for (int tile: {21, 22})
+                    if (!ok && vkhip_conv_plan_make(&d, VKHIP_CONV_GEMM, tile, 0, &plan) == VKHIP_OK && vkhip_conv_maxpool_supported(&d, &plan, &pd)) ok = true;
+                if (ok) convPool[pit->second] = i;
+            }
+        }
 
         // Squeeze-excite scale folding: y = Mul(h, s) with s of shape [N,C,1,1] (the SE branch output)
         // whose only reader is a dense 1x1 stride-1 pad-0 conv of the same segment becomes that conv's
@@ -834,13 +903,26 @@ namespace vknn {
             for (auto &kv: scaled)
                 for (int m: folded)
                     if (g.nodes[m].outputs[0] == g.nodes[kv.first].inputs[0]) foldedInto[m] = g.nodes[kv.first].name;
+            // VKNN_HIP_FUSE_POOL=1 runs a stem conv and its max pool as one kernel. Off by default:
+            // on the ResNet-50 stem the fused kernel (70 us at b64) only matches the two kernels it
+            // replaces (49 + 25 us), because it recomputes the shared conv rows at the stem's low
+            // MFMA rate and holds one workgroup per CU.
+            std::map<int, int> convPool;
+            std::set<int>      pools;
+            const char        *pool_env = std::getenv("VKNN_HIP_FUSE_POOL");
+            if (pool_env && std::string(pool_env) == "1") planPoolFolds(g, idx, convPool);
+            for (auto &kv: convPool) {
+                pools.insert(kv.second);
+                foldedInto[kv.second] = g.nodes[kv.first].name;
+            }
             std::vector<std::vector<TensorId>> ins, outs;
             for (int i: idx) {
                 const Node &nd = g.nodes[i];
                 std::unique_ptr<HipOp> op;
-                if (folded.count(i)) {
+                if (folded.count(i) || pools.count(i)) {
                     auto f  = std::make_unique<FoldedMulOp>();
                     f->into = foldedInto[i];
+                    if (pools.count(i)) f->what = "max pool";
                     op      = std::move(f);
                 } else op = makeOp(g, nd);
                 if (!op) throw Error(Status::Unsupported, std::string("HIP backend has no kernel for ") + opTypeName(nd.type) + " (" + nd.name + ")");
@@ -850,13 +932,22 @@ namespace vknn {
                     c->scaledIn = sit->second.first;
                     c->xscale   = sit->second.second;
                 }
+                auto pit = convPool.find(i);
+                if (pit != convPool.end()) {
+                    auto       *c  = static_cast<ConvOp *>(op.get());
+                    const Node &pn = g.nodes[pit->second];
+                    NCHW        y  = NCHW::from(g.desc(pn.inputs[0]).shape), z = NCHW::from(g.desc(pn.outputs[0]).shape);
+                    c->poolOut     = pn.outputs[0];
+                    c->pd.N = (int) y.n; c->pd.C = (int) y.c; c->pd.H = (int) y.h; c->pd.W = (int) y.w; c->pd.OH = (int) z.h; c->pd.OW = (int) z.w;
+                    c->pd.KH = c->pd.KW = 3; c->pd.SH = c->pd.SW = 2; c->pd.PT = c->pd.PL = 1;
+                }
                 op->name = nd.name;
                 op->type = nd.type;
                 op->prepare(nd, env_);
                 ops_.push_back(std::move(op));
                 // data the op's launches read and write (alias and folded ops launch nothing)
                 std::vector<TensorId> in, out;
-                if (folded.count(i)) {
+                if (folded.count(i) || pools.count(i)) {
                     ins.push_back(in);
                     outs.push_back(out);
                     continue;
@@ -871,8 +962,10 @@ namespace vknn {
                         if (t != kNoTensor && !g.isInitializer(t)) in.push_back(resolve(t));
                     }
                     if (nd.fusedResidual != kNoTensor) in.push_back(resolve(nd.fusedResidual));
-                    for (TensorId t: nd.outputs)
-                        if (t != kNoTensor) out.push_back(resolve(t));
+                    if (pit != convPool.end()) out.push_back(resolve(g.nodes[pit->second].outputs[0]));
+                    else
+                        for (TensorId t: nd.outputs)
+                            if (t != kNoTensor) out.push_back(resolve(t));
                 }
                 ins.push_back(in);
                 outs.push_back(out);

@@ -783,6 +783,73 @@ int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
 
 } // extern "C"
 
+// ---------------------------------------------------------------- stem conv + max pool
+namespace vkhip {
+    // Pooled rows per workgroup and band chunks of the fused stem + pool kernel, or false when the
+    // pair does not fit it: a stem-kernel plan with 64-row tiles (one M tile: Cout <= 64), no
+    // residual, a 3x3 stride-2 pad-1 pool over exactly the conv output, and a band that fits LDS
+    // next to the weights.
+    // Configuration: the 1024-column workgroups (several pooled rows per tile, so the recomputed
+    // shared conv row costs least), else the 384-column ones.
+    static bool stem_pool_geom(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const vkhip_pool_desc *p, int &PR, int &NBI, int &cfg) {
+        if (!d || !plan || !p) return false;
+        if (plan->algo != VKHIP_CONV_GEMM || plan->tile < 0 || plan->tile >= kNumTiles) return false;
+        const TileCfg &t = kTiles[plan->tile];
+        if (t.kind != 4 || t.BM != 64 || d->Cout > 64 || d->has_res || d->in_scale || !stem_shape_ok(d)) return false;
+        if (p->N != d->N || p->C != d->Cout || p->H != d->OH || p->W != d->OW || p->KH != 3 || p->KW != 3 || p->SH != 2 || p->SW != 2 ||
+            p->PT != 1 || p->PL != 1 || p->OH != (d->OH - 1) / 2 + 1 || p->OW != (d->OW - 1) / 2 + 1)
+            return false;
+        const int K = d->KH, S = d->SH, RS = d->W + K - 1, KT = (K * K + 3) / 4;
+        for (cfg = 0; cfg < 2; ++cfg) {
+            const int bn = cfg == 0 ? stem_pool_bn(kSP0FN, kSP0WN) : stem_pool_bn(kSP1FN, kSP1WN);
+            const int lds = cfg == 0 ? stem_pool_lds(kSP0FN, kSP0WN) : stem_pool_lds(kSP1FN, kSP1WN);
+            PR = (bn / d->OW - 1) / 2;
+            if (PR < 1) continue;
+            const int R = 2 * PR + 1, VRB = S * (R - 1) + K;
+            NBI = (int) ceil_div((int64_t) VRB * (RS / 2), 64);
+            if ((KT * 2 + NBI) * 1024 + 32 <= lds - 1024) return true;
+        }
+        return false;
+    }
+} // namespace vkhip
+
+extern "C" {
+
+int vkhip_conv_maxpool_supported(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const vkhip_pool_desc *p) {
+    int PR, NBI, cfg;
+    return stem_pool_geom(d, plan, p, PR, NBI, cfg) ? 1 : 0;
+}
+
+int vkhip_conv_maxpool_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const vkhip_pool_desc *p, const void *x, const void *blob,
+                               void *y, vkhip_stream_t s) {
+    if (!d || !plan || !p || !x || !blob || !y) return set_error(VKHIP_ERR_INVALID, "conv_maxpool: null argument");
+    int PR = 0, NBI = 0, cfg = 0;
+    if (!stem_pool_geom(d, plan, p, PR, NBI, cfg)) return set_error(VKHIP_ERR_UNSUPPORTED, "conv_maxpool: shape or plan not supported");
+    StemPoolFn fn = stem_pool_kernel_for(d->KH, cfg);
+    if (!fn) return set_error(VKHIP_ERR_UNSUPPORTED, "conv_maxpool: kernel size");
+    ConvGeom g = gemm_geom(d, plan->tile, false);
+    GemmArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.w      = (const half_t *) ((const char *) blob + align256((size_t) g.Coutp * 4));
+    a.bias   = (const float *) blob;
+    a.Cinb   = (int) g.Cinb;
+    a.Coutb  = (int) g.Coutb;
+    a.Cout   = d->Cout;
+    a.act    = d->act;
+    a.lo     = d->act_lo;
+    a.hi     = d->act_hi;
+    a.x      = (const uint2 *) x;
+    a.x_bytes = (unsigned) ((int64_t) d->N * g.Cinb * d->H * d->W * 8);
+    a.H  = d->H; a.W = d->W; a.HW = d->H * d->W;
+    a.OW = d->OW; a.OHW = d->OH * d->OW;
+    a.SH = d->SH; a.SW = d->SW; a.PT = d->PT; a.PL = d->PL;
+    const int groups = (int) ceil_div(p->OH, PR);
+    fn<<<dim3((unsigned) (d->N * groups)), 64 * (cfg == 0 ? kSP0WN : kSP1WN), 0, resolve_stream(s)>>>(a, (uint2 *) y, p->OH, p->OW, PR, NBI);
+    return check_launch("stem_pool");
+}
+
+} // extern "C"
+
 // The forward pass of every conv algorithm; xs is the input scale of an in_scale plan (or null).
 static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *xs, const void *blob,
                              const void *res, void *y, void *workspace, vkhip_stream_t s) {

@@ -1442,6 +1442,17 @@ namespace vkhip {
     GemmKernelFn bd_tile_kernel(int tile, int bmode);
     GemmKernelFn dma_tile_kernel(int tile, int bmode, int steps, bool xs);
     GemmKernelFn halo_tile_kernel(int tile, int nbi);
+    // stem conv + 3x3/s2 max pool (stem_pool.hip): FM = 2 (64 output channels), WM = 1, WN waves
+    // over FN fragments each, so BN = 32 FN WN GEMM columns = up to BN / OW conv rows; LDS holds the
+    // conv tile (16 channel blocks x BN columns) plus a spare KB. Two configurations: 0 = 8 waves x
+    // 4 fragments (1024 columns, one workgroup per CU), 1 = 4 waves x 3 fragments (384 columns,
+    // three workgroups per CU). Arguments: conv args, pooled output, POH, POW, pooled rows per
+    // workgroup, band chunks.
+    constexpr int kSP0FN = 4, kSP0WN = 8, kSP1FN = 3, kSP1WN = 4;
+    constexpr int stem_pool_bn(int fn, int wn) { return 32 * fn * wn; }
+    constexpr int stem_pool_lds(int fn, int wn) { return 16 * stem_pool_bn(fn, wn) * 8 + 1024; }
+    typedef void (*StemPoolFn)(GemmArgs, uint2 *, int, int, int, int);
+    StemPoolFn stem_pool_kernel_for(int K, int cfg);
     GemmKernelFn stem_tile_kernel(int tile, int bmode, int nbi);
 
 } // namespace vkhip
