@@ -207,3 +207,33 @@ def test_edge_fixture_is_pinned(tmp_path):
     if O.ref_available():
         from tests.golden.make_onnx_golden import ref_onnx_run
         assert np.array_equal(ref_onnx_run(tmp_path / "edge.onnx", z["x"], z["y"].size), z["y"])
+
+
+def test_corrupted_files_never_crash(tmp_path):
+    """Seeded truncations, byte flips and spliced bytes of valid models either import or raise
+    the library's error — the reader checks every length against its buffer, so nothing reads past
+    the end or crashes the process."""
+    rng = np.random.default_rng(123)
+    blobs = [open(W.import_case(str(tmp_path / f"{c}.onnx"), c), "rb").read() for c in ("const_attrs", "dtypes", "ssa")]
+    blobs.append(open(W.edge_model(str(tmp_path / "edge.onnx")), "rb").read())
+    outcomes = {"ok": 0, "error": 0}
+    p = tmp_path / "fuzz.onnx"
+    for i in range(300):
+        b = bytearray(blobs[i % len(blobs)])
+        kind = i % 3
+        if kind == 0:
+            b = b[:int(rng.integers(0, len(b)))]
+        elif kind == 1:
+            for _ in range(int(rng.integers(1, 6))):
+                b[int(rng.integers(0, len(b)))] = int(rng.integers(0, 256))
+        else:
+            at = int(rng.integers(0, len(b)))
+            b[at:at] = bytes(rng.integers(0, 256, int(rng.integers(1, 12)), dtype=np.uint8))
+        p.write_bytes(bytes(b))
+        try:
+            V.onnx_describe(p)
+            outcomes["ok"] += 1
+        except V.VkhipError as e:
+            assert "InvalidArgument" in str(e) or "IoError" in str(e), str(e)
+            outcomes["error"] += 1
+    assert outcomes["error"] > 50, outcomes
