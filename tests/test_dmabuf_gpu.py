@@ -21,7 +21,7 @@ ALIGN = 2 << 20
 def _export(buf):
     fd = ctypes.c_int(-1)
     if V.vkhip().vkhip_dmabuf_export(buf.ptr, buf.nbytes, ctypes.byref(fd)):
-        pytest.skip("dma-buf export unavailable here: " + V.vkhip().vkhip_last_error().decode(errors="replace"))
+        pytest.skip("dma-buf export unavailable here: " + V.vkhip().vkhip_last_error().decode(errors='replace'))
     return fd.value
 
 
@@ -57,7 +57,7 @@ def test_dmabuf_io_matches_host_path(gpu, model, batch):
             y = np.zeros(n_out, np.float32)
             for _ in range(2):  # the second run reuses the cached imports (and a captured graph)
                 rc = lib.vknn_session_run_dmabuf(s.h, in_fd, ifmt, if16, out_fd, ofmt, of16, y.ctypes.data, y.size)
-                assert rc == 0, lib.vknn_last_error().decode(errors="replace")
+                assert rc == 0, lib.vknn_last_error().decode(errors='replace')
                 got = outb.download(odt, s.out_elems[0])
                 want = conv(ref[:s.out_elems[0]])
                 assert np.array_equal(got.view(np.uint16 if odt == np.float16 else np.uint32),

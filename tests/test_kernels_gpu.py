@@ -774,7 +774,7 @@ def test_conv_input_scale(gpu, tile, shape):
     plan = V.ConvPlan()
     rc = lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, tile, 0, ctypes.byref(plan))
     if rc:
-        pytest.skip(f"tile {tile} takes no input scale at {shape}: {lib.vkhip_last_error().decode(errors="replace")}")
+        pytest.skip(f"tile {tile} takes no input scale at {shape}: {lib.vkhip_last_error().decode(errors='replace')}")
     blob = np.zeros(plan.weight_bytes, np.uint8)
     check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(plan), w.ctypes.data, b.ctypes.data, blob.ctypes.data))
     dblob = DeviceBuffer.from_array(blob)

@@ -40,7 +40,7 @@ def host_backend():
 def _session(path, options):
     h = ctypes.c_void_p()
     if V.vknn().vknn_session_create_onnx(str(path).encode(), options.encode(), ctypes.byref(h)):
-        raise V.VkhipError(V.vknn().vknn_last_error().decode(errors="replace"))
+        raise V.VkhipError(V.vknn().vknn_last_error().decode(errors='replace'))
     s = V.Session.__new__(V.Session)
     s.h = h.value
     return s
@@ -50,7 +50,7 @@ def _run(s, x, n):
     y = np.zeros(n, np.float32)
     x = np.ascontiguousarray(x, np.float32)
     if V.vknn().vknn_session_run_host(s.h, x.ctypes.data, x.size, y.ctypes.data, y.size):
-        raise V.VkhipError(V.vknn().vknn_last_error().decode(errors="replace"))
+        raise V.VkhipError(V.vknn().vknn_last_error().decode(errors='replace'))
     return y
 
 

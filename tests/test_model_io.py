@@ -38,7 +38,7 @@ def describe(path):
     lib = V.vknn()
     buf = ctypes.create_string_buffer(1 << 20)
     rc = lib.vknn_vxm_describe(str(path).encode(), buf, len(buf))
-    return (buf.value.decode() if rc == 0 else None), lib.vknn_last_error().decode(errors="replace")
+    return (buf.value.decode() if rc == 0 else None), lib.vknn_last_error().decode(errors='replace')
 
 
 @needs_ref

@@ -188,13 +188,13 @@ class VkhipError(RuntimeError):
 
 def check(rc, what="vkhip"):
     if rc != 0:
-        raise VkhipError(f"{what} failed ({rc}): {vkhip().vkhip_last_error().decode(errors="replace")}")
+        raise VkhipError(f"{what} failed ({rc}): {vkhip().vkhip_last_error().decode(errors='replace')}")
 
 
 def require_gpu():
     lib = vkhip()
     if lib.vkhip_available() != 1:
-        raise VkhipError("no gfx950 device: " + lib.vkhip_last_error().decode(errors="replace"))
+        raise VkhipError("no gfx950 device: " + lib.vkhip_last_error().decode(errors='replace'))
     return lib
 
 
@@ -254,7 +254,7 @@ class Session:
         h = c_vp()
         rc = lib.vknn_session_create_model(model.encode(), batch, seed, options.encode(), ctypes.byref(h))
         if rc:
-            raise VkhipError("session create: " + lib.vknn_last_error().decode(errors="replace"))
+            raise VkhipError("session create: " + lib.vknn_last_error().decode(errors='replace'))
         self.h = h.value
         self.in_shape, self.out_elems = model_io(model, batch)
 
@@ -268,7 +268,7 @@ class Session:
         self.model, self.batch = model, batch
         h = c_vp()
         if lib.vknn_session_create_vxm(str(path).encode(), options.encode(), ctypes.byref(h)):
-            raise VkhipError("session create: " + lib.vknn_last_error().decode(errors="replace"))
+            raise VkhipError("session create: " + lib.vknn_last_error().decode(errors='replace'))
         self.h = h.value
         self.in_shape, self.out_elems = model_io(model, batch)
         return self
@@ -283,44 +283,44 @@ class Session:
         self.model, self.batch = str(path), in_shape[0]
         h = c_vp()
         if lib.vknn_session_create_onnx(str(path).encode(), options.encode(), ctypes.byref(h)):
-            raise VkhipError("session create: " + lib.vknn_last_error().decode(errors="replace"))
+            raise VkhipError("session create: " + lib.vknn_last_error().decode(errors='replace'))
         self.h = h.value
         self.in_shape, self.out_elems = list(in_shape), list(out_elems)
         return self
 
     def save_optimized(self, path):
         if vknn().vknn_session_save_optimized(self.h, str(path).encode()):
-            raise VkhipError(vknn().vknn_last_error().decode(errors="replace"))
+            raise VkhipError(vknn().vknn_last_error().decode(errors='replace'))
 
     def run(self, x):
         lib = vknn()
         x = np.ascontiguousarray(x, dtype=np.float32).ravel()
         y = np.empty(sum(self.out_elems), np.float32)
         if lib.vknn_session_run_host(self.h, x.ctypes.data, x.size, y.ctypes.data, y.size):
-            raise VkhipError("run: " + lib.vknn_last_error().decode(errors="replace"))
+            raise VkhipError("run: " + lib.vknn_last_error().decode(errors='replace'))
         return y
 
     def bind_device_input(self, ptr):
         if vknn().vknn_session_bind_device_input(self.h, ptr):
-            raise VkhipError(vknn().vknn_last_error().decode(errors="replace"))
+            raise VkhipError(vknn().vknn_last_error().decode(errors='replace'))
 
     def bind_device_input_as(self, ptr, fmt, f16):
         """Device input in a declared layout (0 NCHW, 1 NHWC, 2 NC4HW4) and type (fp16 if f16)."""
         if vknn().vknn_session_bind_device_input_as(self.h, ptr, fmt, int(f16)):
-            raise VkhipError(vknn().vknn_last_error().decode(errors="replace"))
+            raise VkhipError(vknn().vknn_last_error().decode(errors='replace'))
 
     def run_device(self):
         if vknn().vknn_session_run_device(self.h):
-            raise VkhipError(vknn().vknn_last_error().decode(errors="replace"))
+            raise VkhipError(vknn().vknn_last_error().decode(errors='replace'))
 
     def sync(self):
         if vknn().vknn_session_sync(self.h):
-            raise VkhipError(vknn().vknn_last_error().decode(errors="replace"))
+            raise VkhipError(vknn().vknn_last_error().decode(errors='replace'))
 
     def read_outputs(self):
         y = np.empty(sum(self.out_elems), np.float32)
         if vknn().vknn_session_read_outputs(self.h, y.ctypes.data, y.size):
-            raise VkhipError(vknn().vknn_last_error().decode(errors="replace"))
+            raise VkhipError(vknn().vknn_last_error().decode(errors='replace'))
         return y
 
     @property
@@ -368,15 +368,15 @@ def model_io(model, batch):
     outs = (c_i64 * 16)()
     n = c_i32()
     if vknn().vknn_model_io(model.encode(), batch, in4, outs, ctypes.byref(n), 16):
-        raise VkhipError(vknn().vknn_last_error().decode(errors="replace"))
+        raise VkhipError(vknn().vknn_last_error().decode(errors='replace'))
     return list(in4), list(outs)[:n.value]
 
 
 def _text(fn, *args, cap=1 << 24):
     buf = ctypes.create_string_buffer(cap)
     if fn(*args, buf, len(buf)):
-        raise VkhipError(vknn().vknn_last_error().decode(errors="replace"))
-    out = buf.value.decode(errors="replace")  # names come from the model file and need not be UTF-8
+        raise VkhipError(vknn().vknn_last_error().decode(errors='replace'))
+    out = buf.value.decode(errors='replace')  # names come from the model file and need not be UTF-8
     if len(buf.value) >= cap - 1:
         raise VkhipError("text output larger than %d bytes" % cap)
     return out
@@ -396,5 +396,5 @@ def graph_after_passes(model, batch=1, options=""):
     """Node list of a zoo model after the standard passes (host only, no device needed)."""
     buf = ctypes.create_string_buffer(1 << 20)
     if vknn().vknn_graph_after_passes(model.encode(), batch, options.encode(), buf, len(buf)):
-        raise VkhipError(vknn().vknn_last_error().decode(errors="replace"))
+        raise VkhipError(vknn().vknn_last_error().decode(errors='replace'))
     return buf.value.decode()
