@@ -91,12 +91,14 @@ def draw_dwpw(seed):
                 dw_act=int(r.choice([0, 1, 2])), act=int(r.integers(0, 6)), res=bool(r.random() < 0.4))
 
 
+@pytest.mark.parametrize("kernel", ["ring", "strip"])
 @pytest.mark.parametrize("seed", range(40))
-def test_fused_dwpw_sweep(gpu, seed):
+def test_fused_dwpw_sweep(gpu, monkeypatch, kernel, seed):
     """The fused dw+pw kernel over seeded geometries (ragged channel counts, odd sizes,
     asymmetric pads, stride 2, every activation pair, residual) against the oracle."""
     from tests.gpu_helpers import DeviceBuffer, check, from_device_nc4, to_device_nc4
     from tests.oracle_lib import oracle_dwpw
+    monkeypatch.setenv("VKHIP_DWPW_RING", "1" if kernel == "ring" else "0")
     lib = V.vkhip()
     c = draw_dwpw(seed)
     N, E, H, W, k, s, pads, Cout = c["N"], c["E"], c["H"], c["W"], c["k"], c["s"], c["pads"], c["Cout"]

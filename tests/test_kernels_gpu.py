@@ -507,7 +507,12 @@ def test_depthwise_dilated_generic(gpu):
                                                            (2, 144, 56, 3, 1, 24, 2, 0, True),
                                                            (1, 96, 40, 5, 2, 64, 1, 0, True),
                                                            (1, 40, 130, 3, 2, 24, 2, 0, False)])
-def test_fused_dwpw(gpu, N, E, H, k, s, Cout, dw_act, act, res):
+@pytest.mark.parametrize("kernel", ["ring", "strip", "untiled"])
+def test_fused_dwpw(gpu, monkeypatch, kernel, N, E, H, k, s, Cout, dw_act, act, res):
+    """Each fused kernel (the launcher takes the first that fits: ring-staged for even input
+    widths, strip-tiled, untiled; the environment switches the first two off) against the oracle."""
+    monkeypatch.setenv("VKHIP_DWPW_RING", "1" if kernel == "ring" else "0")
+    monkeypatch.setenv("VKHIP_DWPW_STRIP", "0" if kernel == "untiled" else "1")
     lib = V.vkhip()
     r = rng(E + Cout + H)
     x = round_half(r.standard_normal((N, E, H, H)))

@@ -346,9 +346,312 @@ namespace vkhip {
         }
     }
 
+    // Ring-staged fused dw + pw (even input width). Same work split and arithmetic as the strip
+    // kernel — a workgroup owns SR output rows of one image (SR = RG row groups of RTT rows, BN =
+    // SR * OW pixels) and walks the E expanded channels in chunks of CB channel blocks — but every
+    // chunk's operands reach LDS by buffer-load-to-LDS (16 bytes per lane, no VGPR staging) into a
+    // ring of NS stages, so chunk ch + NS - 1 streams in while chunk ch computes:
+    //   stage = [input band: CB planes x IR rows x IWp pixels, pixel pairs copied whole (input
+    //            column ix at LDS column ix + PLA, PLA even, zero pads from out-of-range lanes)]
+    //           [projection weights MF*32 x CB/2 16-byte k groups][dw weights CB x K*K, fp16 x 4]
+    //           [dw bias CB float4], T KB, copied in 1 KB units dealt round-robin to the 4
+    //           waves (lanes past the data copy zeros);
+    //   dw       thread item (channel block, row group, column): RTT outputs from (RTT-1)*S + K
+    //            band rows, fp16 taps and weights into fp32 sums, bias + dw activation, fp16 into
+    //            the B chunk (MFMA fragment layout, 16-byte channel-block pairs per pixel);
+    //   project  v_mfma_f32_32x32x16_f16 over the chunk's CB/4 K steps, A from the stage.
+    // Units of channel blocks at or past Eb (and projection k past Kp) copy zeros, so padded
+    // channels contribute exact zeros. Two barriers per chunk; the band is read from L2/HBM once.
+    struct DwRing {
+        int         SR, RG, IR, IWp, PLA, NF, CB; // strip rows, row groups, band rows, LDS row pitch (pixels), LDS column of ix=0, pixel fragments, blocks per chunk
+        int         NCI, T, na, nw;               // input KB per stage, KB per stage, A / dw-weight 16-byte units
+        int         x_bytes, blob_bytes, off_dwb, off_dww, off_pww;
+        const void *blob;
+    };
+
+    __device__ __forceinline__ void wait_vm_upto(int n) {
+        // s_waitcnt takes an immediate: vmcnt(n), expcnt and lgkmcnt left at their maxima
+        switch (n) {
+            case 0: __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8)); break;
+            case 1: __builtin_amdgcn_s_waitcnt(1 | (7 << 4) | (15 << 8)); break;
+            case 2: __builtin_amdgcn_s_waitcnt(2 | (7 << 4) | (15 << 8)); break;
+            case 3: __builtin_amdgcn_s_waitcnt(3 | (7 << 4) | (15 << 8)); break;
+            case 4: __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (15 << 8)); break;
+            case 5: __builtin_amdgcn_s_waitcnt(5 | (7 << 4) | (15 << 8)); break;
+            case 6: __builtin_amdgcn_s_waitcnt(6 | (7 << 4) | (15 << 8)); break;
+            case 7: __builtin_amdgcn_s_waitcnt(7 | (7 << 4) | (15 << 8)); break;
+            default: __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8)); break;
+        }
+    }
+
+    // copies per wave per stage: stages of at most 16 KB for the 3x3 single-fragment kernels (the
+    // register budget of four waves per SIMD), 24 KB otherwise
+    __host__ __device__ constexpr int ring_rmax(int K, int MF) { return K == 3 && MF == 1 ? 4 : 6; }
+
+    template <int K, int S, int MF, int RTT, int NS>
+    __global__ __launch_bounds__(256, (K == 3 && MF == 1) ? 4 : 2) void dwpw_ring_kernel(DwPwArgs a, DwRing t) {
+        constexpr int IRT = (RTT - 1) * S + K; // band rows one item reads
+        constexpr int NFW = 2;
+        constexpr unsigned kInvalid = 0x80000000u;
+        extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
+        const int STAGE = t.T * 1024;
+        uint4    *bch   = reinterpret_cast<uint4 *>(dsm + NS * STAGE); // [CB/2][NF*32]
+        const int tid = threadIdx.x, lane = tid & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int RW   = (t.T - wave + 3) / 4; // copies this wave issues per stage (units wave, wave + 4, ...)
+        const int row_tiles = (a.OH + t.SR - 1) / t.SR;
+        const int n     = blockIdx.x / row_tiles;
+        const int oy0   = (blockIdx.x - n * row_tiles) * t.SR;
+        const int nrows = min(t.SR, a.OH - oy0);
+        const int npx   = nrows * a.OW;
+        const int iy0   = oy0 * S - a.PT;
+        const int HW = a.H * a.W, OHW = a.OH * a.OW;
+        const int CB = t.CB, KG = CB / 2, BNF = t.NF * 32, IWp = t.IWp, PW = IWp >> 1;
+        const int chunks = (a.Ebp + CB - 1) / CB;
+        const int ni = CB * t.IR * PW; // input units of a stage
+
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, t.x_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc((void *) t.blob, (short) 0, t.blob_bytes, 0x00020000);
+
+        // per-lane copy plan, one word per copy: the source offset at chunk 0 (16-byte aligned) with
+        // bit 0 set when the unit is real for Eb / CB + 1 chunks instead of Eb / CB (its channel
+        // block within the chunk is below Eb % CB), or kInvalid for a unit that is always zero
+        // (padding, rows and columns outside the image, lanes past the data). The per-chunk
+        // advance depends only on the unit's region.
+        constexpr int RMAX = ring_rmax(K, MF);
+        unsigned      plan[RMAX];
+        const int rmd = a.Eb % CB;
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) {
+            const int c    = r * 4 + wave;
+            unsigned  base = kInvalid;
+            int       key  = 0; // the unit's channel block within the chunk
+            if (r < RW) {
+                if (c < t.NCI) {
+                    const int u = c * 64 + lane;
+                    if (u < ni) {
+                        const int pl = u / (t.IR * PW), rem = u - pl * (t.IR * PW);
+                        const int rr = rem / PW, j = rem - rr * PW;
+                        const int iy = iy0 + rr, ix = 2 * j - t.PLA;
+                        if ((unsigned) iy < (unsigned) a.H && ix >= 0 && ix < a.W) {
+                            base = (unsigned) ((((long long) n * a.Eb + pl) * HW + (long long) iy * a.W + ix) * 8);
+                            key  = pl;
+                        }
+                    }
+                } else {
+                    const int ua = (c - t.NCI) * 64 + lane;
+                    if (ua < t.na) {
+                        const int row = ua / KG, kg = ua - row * KG;
+                        base = (unsigned) (t.off_pww + (row * a.Kp + kg * 8) * 2);
+                        key  = 2 * kg;
+                    } else if (ua < t.na + t.nw) {
+                        const int uw = ua - t.na; // fp16 weights, two taps per unit
+                        base = (unsigned) (t.off_dww + uw * 16);
+                        key  = (2 * uw) / (K * K);
+                    } else if (ua < t.na + t.nw + CB) {
+                        const int ub = ua - t.na - t.nw;
+                        base = (unsigned) (t.off_dwb + ub * 16);
+                        key  = ub;
+                    }
+                }
+            }
+            plan[r] = base == kInvalid ? kInvalid : base | (key < rmd ? 1u : 0u);
+        }
+        const int      q0   = a.Eb / CB;
+        const unsigned xinc = (unsigned) CB * (unsigned) HW * 8u;
+        auto issue = [&](int ch, int buf) __attribute__((always_inline)) {
+            unsigned char *dst = dsm + buf * STAGE;
+#pragma unroll
+            for (int r = 0; r < RMAX; ++r) {
+                if (r >= RW) break;
+                const int      c    = r * 4 + wave;
+                const unsigned p    = plan[r];
+                const bool     real = !(p & kInvalid) && ch < q0 + (int) (p & 1u);
+                if (c < t.NCI) {
+                    const unsigned vo = real ? (p & ~1u) + (unsigned) ch * xinc : kInvalid;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void *) (dst + c * 1024), 16, vo, 0, 0, 0);
+                } else {
+                    const int      ua  = (c - t.NCI) * 64 + lane;
+                    const unsigned inc = ua < t.na ? (unsigned) CB * 8u : ua < t.na + t.nw ? (unsigned) (CB * K * K * 8) : (unsigned) CB * 16u;
+                    const unsigned vo  = real ? (p & ~1u) + (unsigned) ch * inc : kInvalid;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (__attribute__((address_space(3))) void *) (dst + c * 1024), 16, vo, 0, 0, 0);
+                }
+            }
+        };
+
+        float16v acc[MF][NFW];
+#pragma unroll
+        for (int m = 0; m < MF; ++m)
+#pragma unroll
+            for (int f = 0; f < NFW; ++f)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[m][f][r] = 0.f;
+
+        // fragment columns past the strip's pixels read as zero (never written by the dw phase)
+        for (int i = tid; i < KG * BNF; i += 256)
+            if (i % BNF >= npx) bch[i] = uint4 {0u, 0u, 0u, 0u};
+
+#pragma unroll
+        for (int d = 0; d < NS - 1; ++d)
+            if (d < chunks) issue(d, d);
+
+        // this thread's dw items (channel block, row group, column): it = tid and tid + 256,
+        // as LDS offsets: band pixel of the first tap, B-chunk half4 slot, weights, bias
+        int  isrc[2], idst[2], iw[2], ib[2], irw[2];
+        bool iok[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int it  = tid + 256 * k;
+            const int cbl = it / (t.RG * a.OW);
+            const int rem = it - cbl * (t.RG * a.OW);
+            const int rg  = rem / a.OW, ox = rem - rg * a.OW;
+            const int r0  = rg * RTT;
+            iok[k]  = cbl < CB && r0 < nrows;
+            isrc[k] = (cbl * t.IR + r0 * S) * IWp + ox * S + (t.PLA - a.PL);
+            idst[k] = ((cbl >> 1) * BNF + r0 * a.OW + ox) * 2 + (cbl & 1);
+            iw[k]   = cbl * K * K;
+            ib[k]   = cbl;
+            irw[k]  = nrows - r0;
+        }
+
+        const bool two_items = CB * t.RG * a.OW > 256;
+        for (int ch = 0; ch < chunks; ++ch) {
+            const int buf = ch % NS;
+            wait_vm_upto(min(NS - 2, chunks - 1 - ch) * RW);
+            __builtin_amdgcn_s_waitcnt(0xC07F); // and this wave's LDS writes
+            __asm__ volatile("s_barrier" ::: "memory");
+            if (ch + NS - 1 < chunks) issue(ch + NS - 1, (ch + NS - 1) % NS);
+
+            // LDS is accessed through ext-vector types only: the compiler then keeps the copies
+            // in flight across these accesses instead of waiting for them
+            const unsigned char *stg  = dsm + buf * STAGE;
+            const half8         *asm_ = reinterpret_cast<const half8 *>(stg + t.NCI * 1024);
+            const half4         *wsm  = reinterpret_cast<const half4 *>(asm_ + t.na);
+            const float4v       *bsm  = reinterpret_cast<const float4v *>(wsm + 2 * t.nw);
+            const half4         *inp  = reinterpret_cast<const half4 *>(stg);
+            half4               *bh   = reinterpret_cast<half4 *>(bch);
+            auto item = [&](const int k) __attribute__((always_inline)) {
+                if (!iok[k]) return;
+                half4 w[K * K];
+#pragma unroll
+                for (int q = 0; q < K * K; ++q) w[q] = wsm[iw[k] + q];
+                const float4v b = bsm[ib[k]];
+                float4v       acc4[RTT];
+#pragma unroll
+                for (int r = 0; r < RTT; ++r) acc4[r] = b;
+                const half4 *src = inp + isrc[k];
+#pragma unroll
+                for (int ir = 0; ir < IRT; ++ir) {
+                    half4 tap[K];
+#pragma unroll
+                    for (int kx = 0; kx < K; ++kx) tap[kx] = src[ir * IWp + kx];
+#pragma unroll
+                    for (int r = 0; r < RTT; ++r) {
+                        const int ky = ir - r * S;
+                        if (ky < 0 || ky >= K) continue;
+#pragma unroll
+                        for (int kx = 0; kx < K; ++kx) {
+                            const half4 wv = w[ky * K + kx];
+                            acc4[r].x = __builtin_fmaf((float) tap[kx].x, (float) wv.x, acc4[r].x);
+                            acc4[r].y = __builtin_fmaf((float) tap[kx].y, (float) wv.y, acc4[r].y);
+                            acc4[r].z = __builtin_fmaf((float) tap[kx].z, (float) wv.z, acc4[r].z);
+                            acc4[r].w = __builtin_fmaf((float) tap[kx].w, (float) wv.w, acc4[r].w);
+                        }
+                    }
+                }
+                const int c   = (ch * CB + ib[k]) * 4;
+                half4    *dst = bh + idst[k];
+                // channels past E are zeroed; only the chunk holding E's last block needs the test
+                auto finish = [&](auto act_c, auto mask_c) __attribute__((always_inline)) {
+                    constexpr int  ACT  = decltype(act_c)::value;
+                    constexpr bool MASK = decltype(mask_c)::value;
+#pragma unroll
+                    for (int r = 0; r < RTT; ++r) {
+                        if (r >= irw[k]) break;
+                        float4v v = acc4[r];
+                        v.x = apply_act(v.x, ACT, 0.f, 6.f);
+                        v.y = apply_act(v.y, ACT, 0.f, 6.f);
+                        v.z = apply_act(v.z, ACT, 0.f, 6.f);
+                        v.w = apply_act(v.w, ACT, 0.f, 6.f);
+                        if (MASK) {
+                            if (c + 0 >= a.E) v.x = 0.f;
+                            if (c + 1 >= a.E) v.y = 0.f;
+                            if (c + 2 >= a.E) v.z = 0.f;
+                            if (c + 3 >= a.E) v.w = 0.f;
+                        }
+                        dst[2 * r * a.OW] = f4_to_h4(v);
+                    }
+                };
+                using yes = std::true_type;
+                using no  = std::false_type;
+                const bool tail = (ch + 1) * CB * 4 > a.E;
+                if (a.dw_act == VKHIP_ACT_RELU) {
+                    if (tail) finish(std::integral_constant<int, VKHIP_ACT_RELU> {}, yes {});
+                    else finish(std::integral_constant<int, VKHIP_ACT_RELU> {}, no {});
+                } else if (a.dw_act == VKHIP_ACT_RELU6) {
+                    if (tail) finish(std::integral_constant<int, VKHIP_ACT_RELU6> {}, yes {});
+                    else finish(std::integral_constant<int, VKHIP_ACT_RELU6> {}, no {});
+                } else {
+                    if (tail) finish(std::integral_constant<int, VKHIP_ACT_NONE> {}, yes {});
+                    else finish(std::integral_constant<int, VKHIP_ACT_NONE> {}, no {});
+                }
+            };
+            item(0);
+            if (two_items) item(1); // a uniform branch: the two items are not interleaved
+            __builtin_amdgcn_s_waitcnt(0xC07F); // B chunk written (LDS), copies left in flight
+            __asm__ volatile("s_barrier" ::: "memory");
+            for (int ks = 0; ks < CB / 4; ++ks) {
+                const int kg = ks * 2 + (lane >> 5);
+#pragma unroll
+                for (int f = 0; f < NFW; ++f) {
+                    const int fr = wave + 4 * f;
+                    if (fr >= t.NF) break;
+                    const half8 bf = *reinterpret_cast<const half8 *>(&bch[kg * BNF + fr * 32 + (lane & 31)]);
+#pragma unroll
+                    for (int m = 0; m < MF; ++m) {
+                        const half8 af = *reinterpret_cast<const half8 *>(&asm_[(m * 32 + (lane & 31)) * KG + kg]);
+                        acc[m][f]      = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[m][f], 0, 0, 0);
+                    }
+                }
+            }
+        }
+
+        // epilogue: bias (+ residual) + activation, fp16 NC4HW4 store
+        const int lk = lane >> 5;
+#pragma unroll
+        for (int f = 0; f < NFW; ++f) {
+            const int fr = wave + 4 * f;
+            if (fr >= t.NF) break;
+            const int px = fr * 32 + (lane & 31);
+            if (px >= npx) continue;
+            const long long pix = (long long) oy0 * a.OW + px;
+#pragma unroll
+            for (int m = 0; m < MF; ++m)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int oc  = m * 32 + q * 8 + lk * 4;
+                    const int ocb = oc >> 2;
+                    if (ocb >= a.Coutb) continue;
+                    float4v v = {acc[m][f][q * 4 + 0], acc[m][f][q * 4 + 1], acc[m][f][q * 4 + 2], acc[m][f][q * 4 + 3]};
+                    v += *reinterpret_cast<const float4v *>(a.pw_b + oc);
+                    const long long yi = ((long long) n * a.Coutb + ocb) * OHW + pix;
+                    if (a.has_res) v += h4_to_f4(u2_as_h4(a.res[yi]));
+                    v.x = apply_act(v.x, a.act, a.lo, a.hi);
+                    v.y = apply_act(v.y, a.act, a.lo, a.hi);
+                    v.z = apply_act(v.z, a.act, a.lo, a.hi);
+                    v.w = apply_act(v.w, a.act, a.lo, a.hi);
+                    if (oc + 0 >= a.Cout) v.x = 0.f;
+                    if (oc + 1 >= a.Cout) v.y = 0.f;
+                    if (oc + 2 >= a.Cout) v.z = 0.f;
+                    if (oc + 3 >= a.Cout) v.w = 0.f;
+                    a.y[yi] = h4_as_u2(f4_to_h4(v));
+                }
+        }
+    }
+
     struct DwPwGeom {
         int64_t Eb, Ebp, Kp, Coutb, Coutp, m_frags;
-        size_t  off_dwb, off_dww, off_pwb, off_pww, bytes;
+        size_t  off_dwb, off_dww, off_dwh, off_pwb, off_pww, bytes;
         int     BN;
     };
 
@@ -409,6 +712,69 @@ namespace vkhip {
         return fits();
     }
 
+    typedef void (*RingFn)(DwPwArgs, DwRing);
+    template <int K, int S, int MF, int NS>
+    static RingFn ring_rtt(int rtt) {
+        switch (rtt) {
+            case 4: return dwpw_ring_kernel<K, S, MF, 4, NS>;
+            case 2: return dwpw_ring_kernel<K, S, MF, 2, NS>;
+            case 1: return dwpw_ring_kernel<K, S, MF, 1, NS>;
+        }
+        return nullptr;
+    }
+    template <int NS>
+    static RingFn ring_fn_ns(int K, int S, int mf, int rtt) {
+        if (K == 3) {
+            if (S == 1) return mf == 1 ? ring_rtt<3, 1, 1, NS>(rtt) : ring_rtt<3, 1, 2, NS>(rtt);
+            return mf == 1 ? ring_rtt<3, 2, 1, NS>(rtt) : ring_rtt<3, 2, 2, NS>(rtt);
+        }
+        if (S == 1) return mf == 1 ? ring_rtt<5, 1, 1, NS>(rtt) : ring_rtt<5, 1, 2, NS>(rtt);
+        return mf == 1 ? ring_rtt<5, 2, 1, NS>(rtt) : ring_rtt<5, 2, 2, NS>(rtt);
+    }
+
+    // LDS bytes of the ring kernel: NS stages of T KB plus the B chunk
+    static size_t dwpw_ring_lds(const DwRing &t, int NS) { return (size_t) NS * t.T * 1024 + (size_t) t.CB / 2 * t.NF * 32 * 16; }
+
+    // Ring-kernel geometry: square 3x3 / 5x5, stride 1 or 2, no dilation, Cout <= 64, even input
+    // width, 32-bit buffer offsets. Strip: RTT rows per item (4, else 2, else 1) and RG row groups,
+    // SR = RG * RTT rows with SR * OW <= 256 and no more rows than the output needs; CB the largest
+    // multiple of 4 (at least 4) with CB * RG * OW <= 256. Smaller strips are tried until a stage
+    // fits ring_rmax KB per wave and the workgroup 64 KB of LDS.
+    static bool dwpw_ring_fits(const vkhip_dwpw_desc *d, const DwPwGeom &g, int NS, DwRing &t, int &RTT) {
+        const vkhip_conv_desc &c = d->dw;
+        if (c.KH != c.KW || (c.KH != 3 && c.KH != 5) || c.SH != c.SW || (c.SH != 1 && c.SH != 2) || c.DH != 1 || c.DW != 1) return false;
+        if (g.m_frags > 2 || c.PL < 0 || c.PT < 0 || c.W % 2 || c.OW > 256) return false;
+        if ((int64_t) c.N * g.Eb * c.H * c.W * 8 >= (1LL << 31) || g.bytes >= (1ULL << 31)) return false;
+        const int K = c.KH, S = c.SH, OW = c.OW;
+        t.PLA = (c.PL + 1) & ~1;
+        t.IWp = std::max(t.PLA + c.W, (OW - 1) * S + K - c.PL + t.PLA);
+        t.IWp = (t.IWp + 1) & ~1;
+        const int SRmax = std::min(c.OH, 256 / OW);
+        if (SRmax < 1) return false;
+        for (int rtt: {4, 2, 1}) {
+            if (rtt > SRmax && rtt > 1) continue;
+            for (int rg = (SRmax + rtt - 1) / rtt; rg >= 1; --rg) {
+                if (rg * rtt * OW > 256) continue;
+                t.RG = rg;
+                t.SR = rg * rtt;
+                t.NF = (int) ceil_div((int64_t) t.SR * OW, 32);
+                if (t.NF > 8) continue;
+                t.CB = std::max(4, 256 / (rg * OW) / 4 * 4);
+                t.CB = (int) std::min<int64_t>(t.CB, g.Ebp);
+                t.IR  = (t.SR - 1) * S + K;
+                t.na  = (int) g.m_frags * 32 * t.CB / 2;
+                t.nw  = t.CB * K * K / 2;
+                t.NCI = (int) ceil_div((int64_t) t.CB * t.IR * (t.IWp / 2), 64);
+                const int nca = (int) ceil_div(t.na + t.nw + t.CB, 64);
+                t.T = t.NCI + nca;
+                if (t.T > 4 * ring_rmax(K, (int) g.m_frags) || dwpw_ring_lds(t, NS) > 64 * 1024) continue;
+                RTT = rtt;
+                return true;
+            }
+        }
+        return false;
+    }
+
     static DwPwGeom dwpw_geom(const vkhip_dwpw_desc *d) {
         DwPwGeom g;
         g.Eb      = ceil_div(d->dw.Cin, 4);
@@ -420,7 +786,8 @@ namespace vkhip {
         g.off_pwb = 0;
         g.off_dwb = a256((size_t) g.Coutp * 4);
         g.off_dww = g.off_dwb + a256((size_t) g.Eb * 16);
-        g.off_pww = g.off_dww + a256((size_t) g.Eb * d->dw.KH * d->dw.KW * 16);
+        g.off_dwh = g.off_dww + a256((size_t) g.Eb * d->dw.KH * d->dw.KW * 16);
+        g.off_pww = g.off_dwh + a256((size_t) g.Eb * d->dw.KH * d->dw.KW * 8);
         g.bytes   = g.off_pww + (size_t) g.Coutp * g.Kp * 2;
         g.BN      = (g.Ebp * 64 * 8 <= 65536) ? 64 : 32;
         return g;
@@ -534,12 +901,16 @@ int vkhip_dwpw_pack_weights(const vkhip_dwpw_desc *d, const float *dw_w, const f
     std::memset(blob, 0, g.bytes);
     char  *base = (char *) blob;
     float *pwb = (float *) (base + g.off_pwb), *dwb = (float *) (base + g.off_dwb), *dww = (float *) (base + g.off_dww);
-    half_t *pww = (half_t *) (base + g.off_pww);
+    half_t *pww = (half_t *) (base + g.off_pww), *dwh = (half_t *) (base + g.off_dwh);
     const int E = d->dw.Cin, KH = d->dw.KH, KW = d->dw.KW;
     for (int c = 0; c < E; ++c) {
         if (dw_b) dwb[c] = dw_b[c];
         for (int ky = 0; ky < KH; ++ky)
-            for (int kx = 0; kx < KW; ++kx) dww[(((int64_t) (c / 4) * KH + ky) * KW + kx) * 4 + c % 4] = dw_w[((int64_t) c * KH + ky) * KW + kx];
+            for (int kx = 0; kx < KW; ++kx) {
+                const int64_t i = (((int64_t) (c / 4) * KH + ky) * KW + kx) * 4 + c % 4;
+                dww[i] = dw_w[((int64_t) c * KH + ky) * KW + kx];
+                dwh[i] = (half_t) dww[i];
+            }
     }
     for (int oc = 0; oc < d->Cout; ++oc) {
         if (pw_b) pwb[oc] = pw_b[oc];
@@ -572,10 +943,29 @@ int vkhip_dwpw_forward(const vkhip_dwpw_desc *d, const void *x, const void *blob
     DwStrip t;
     int     RT = 0;
     // VKHIP_DWPW_STRIP=0 keeps the untiled kernel (A/B measurements)
-    static const bool strip_on = [] {
-        const char *e = std::getenv("VKHIP_DWPW_STRIP");
-        return !(e && e[0] == '0');
-    }();
+    const char *strip_env = std::getenv("VKHIP_DWPW_STRIP");
+    const bool  strip_on  = !(strip_env && strip_env[0] == '0');
+    // VKHIP_DWPW_RING=0 keeps the strip kernel (A/B measurements). Two LDS stages: measured
+    // faster than three on every shape, since the third stage costs a workgroup per CU.
+    const char *ring_env = std::getenv("VKHIP_DWPW_RING");
+    const bool  ring_on  = !(ring_env && ring_env[0] == '0');
+    constexpr int kRingNS = 2;
+    DwRing rt;
+    int    RTT = 0;
+    if (ring_on && dwpw_ring_fits(d, g, kRingNS, rt, RTT)) {
+        rt.x_bytes    = (int) (c.N * g.Eb * c.H * c.W * 8);
+        rt.blob_bytes = (int) g.bytes;
+        rt.off_dwb    = (int) g.off_dwb;
+        rt.off_dww    = (int) g.off_dwh;
+        rt.off_pww    = (int) g.off_pww;
+        rt.blob       = blob;
+        RingFn fn     = ring_fn_ns<kRingNS>(c.KH, c.SH, (int) g.m_frags, RTT);
+        if (fn) {
+            dim3 grid((unsigned) (c.N * ceil_div(c.OH, rt.SR)));
+            fn<<<grid, 256, dwpw_ring_lds(rt, kRingNS), resolve_stream(s)>>>(a, rt);
+            return check_launch("dwpw_ring");
+        }
+    }
     if (strip_on && dwpw_strip_fits(d, g, t, RT)) {
         const size_t sm = dwpw_strip_lds((int) g.m_frags, c.KH, (RT - 1) * c.SH + c.KH, t);
         dim3         grid((unsigned) (c.N * ceil_div(c.OH, RT)));
