@@ -254,14 +254,16 @@ namespace vkhip {
     // KH - S halo rows per strip) and one coalesced write of the output.
     struct DwTile {
         int PP, IR, IWp, PLA; // planes per WG, LDS rows per plane, LDS row pitch (pixels), LDS column of ix=0
+        int PS;               // LDS plane pitch (pixels): IR * IWp padded so consecutive planes start on different banks
         int row_tiles, plane_groups;
+        unsigned mHW, mW;     // ceil(2^32 / (H*W)), ceil(2^32 / W): n / d = umulhi(n, m) for n * d < 2^32 (0: divide)
     };
 
     template <int KH, int KW, int S, int RT>
     __global__ __launch_bounds__(256) void dwconv_lds_kernel(DwArgs a, DwTile t) {
         extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
         constexpr int IR = (RT - 1) * S + KH; // input rows of one strip
-        uint2 *tile = reinterpret_cast<uint2 *>(dsm); // [PP][IR][IWp]
+        uint2 *tile = reinterpret_cast<uint2 *>(dsm); // [PP][PS: IR x IWp + padding]
         const int tid = threadIdx.x;
         const int rt  = blockIdx.x % t.row_tiles;
         const int pg  = blockIdx.x / t.row_tiles;
@@ -292,7 +294,7 @@ namespace vkhip {
             // of the input (np * H * W pixels from plane p0): zero the LDS tile, then copy the range
             // linearly — fully coalesced, all of a thread's loads in flight at once — and drop each
             // pixel at its padded tile position (row iy + PT, column ix + PLA).
-            const int tile_units = np * IR * IWp;
+            const int tile_units = np * t.PS;
             for (int i = tid; i < tile_units; i += 256) tile[i] = uint2 {0u, 0u};
             __syncthreads();
             constexpr int U    = 16;
@@ -310,9 +312,10 @@ namespace vkhip {
                 for (int u = 0; u < U; ++u) {
                     const int e = b0 + u * 256;
                     if (e >= tot) break;
-                    const int pl = e / HW, pix = e - pl * HW;
-                    const int iy = pix / W, ix = pix - iy * W;
-                    tile[(pl * IR + iy + a.PT) * IWp + ix + PLA] = v[u];
+                    // e / HW and pix / W by multiply-high (exact: e * HW and pix * W stay below 2^32)
+                    const int pl = t.mHW ? (int) __umulhi((unsigned) e, t.mHW) : e / HW, pix = e - pl * HW;
+                    const int iy = t.mW ? (int) __umulhi((unsigned) pix, t.mW) : pix / W, ix = pix - iy * W;
+                    tile[pl * t.PS + (iy + a.PT) * IWp + ix + PLA] = v[u];
                 }
             }
         } else {
@@ -346,7 +349,8 @@ namespace vkhip {
     #pragma unroll
                             for (int u = 0; u < U; ++u) {
                                 const int row = base + u * rpp;
-                                if (row < rows) reinterpret_cast<T *>(tile)[row * cols + col] = v[u];
+                                const int pl = row / IR, r = row - pl * IR;
+                                if (row < rows) *reinterpret_cast<T *>(tile + pl * t.PS + r * IWp + (v16 ? 2 * col : col)) = v[u];
                             }
                         }
                     };
@@ -361,7 +365,7 @@ namespace vkhip {
         float4v acc[RT];
 #pragma unroll
         for (int r = 0; r < RT; ++r) acc[r] = b0;
-        const uint2 *src = tile + pl * IR * IWp + ox * S + (PLA - a.PL);
+        const uint2 *src = tile + pl * t.PS + ox * S + (PLA - a.PL);
 #pragma unroll
         for (int ir = 0; ir < IR; ++ir) {
             half4 tap[KW];
@@ -423,8 +427,18 @@ namespace vkhip {
         if (t.IWp > 256) return false;
         t.IR = (RT - 1) * S + d->KH;
         t.PP = (int) std::max<int64_t>(1, std::min<int64_t>(NCb, 256 / d->OW));
-        while (t.PP > 1 && (size_t) t.PP * t.IR * t.IWp * 8 > 48 * 1024) --t.PP;
-        if ((size_t) t.PP * t.IR * t.IWp * 8 > 48 * 1024) return false;
+        // plane pitch: the lanes of one plane read about OW * S consecutive 8-byte units, so a pitch
+        // of that many units modulo the 32 units of the 64 banks puts the next plane's lanes on the
+        // banks right after them
+        const int want = ((d->OW * S + 1) & ~1) % 32; // even: rows of a plane stay 16-byte aligned
+        t.PS = t.IR * t.IWp;
+        while (t.PS % 32 != want) ++t.PS;
+        while (t.PP > 1 && (size_t) t.PP * t.PS * 8 > 48 * 1024) --t.PP;
+        if ((size_t) t.PP * t.PS * 8 > 48 * 1024) return false;
+        const uint64_t HW = (uint64_t) d->H * d->W;
+        const uint64_t span = (uint64_t) t.PP * HW; // largest dividend of the plane split
+        t.mHW = HW > 1 && span * HW < (1ULL << 32) ? (unsigned) (((1ULL << 32) + HW - 1) / HW) : 0u;
+        t.mW  = d->W > 1 && HW * (uint64_t) d->W < (1ULL << 32) ? (unsigned) (((1ULL << 32) + d->W - 1) / d->W) : 0u;
         t.row_tiles    = (int) ceil_div(d->OH, RT);
         t.plane_groups = (int) ceil_div(NCb, t.PP);
         return true;
@@ -873,7 +887,7 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
         DwTile t;
         const int RT = plan->tile > 0 ? plan->tile : (d->OH % 7 == 0 ? 7 : 4);
         if (unit && d->KH == d->KW && (d->KH == 3 || d->KH == 5) && (d->SH == 1 || d->SH == 2) && dw_tile(d, (int64_t) d->N * Cb, RT, t)) {
-            const size_t sm = (size_t) t.PP * t.IR * t.IWp * 8;
+            const size_t sm = (size_t) t.PP * t.PS * 8;
             dim3 g2((unsigned) ((int64_t) t.row_tiles * t.plane_groups));
 #define VKHIP_DW_LAUNCH(K, S_)                                                                                 \
     (RT == 14 ? dwconv_lds_kernel<K, K, S_, 14><<<g2, 256, sm, st>>>(a, t) : RT == 7 ? dwconv_lds_kernel<K, K, S_, 7><<<g2, 256, sm, st>>>(a, t) : dwconv_lds_kernel<K, K, S_, 4><<<g2, 256, sm, st>>>(a, t))

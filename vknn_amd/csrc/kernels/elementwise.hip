@@ -151,7 +151,7 @@ namespace vkhip {
         switch (op) {
             case -1: return v < p0 ? p0 : (v > p1 ? p1 : v);      // clip
             case 0: return 1.f / (1.f + __expf(-v));               // Sigmoid
-            case 2: return v * fminf(fmaxf(v + 3.f, 0.f), 6.f) / 6.f; // HardSwish
+            case 2: return div6(v * fminf(fmaxf(v + 3.f, 0.f), 6.f)); // HardSwish
             case 3: return fmaxf(0.f, fminf(1.f, p0 * v + p1));    // HardSigmoid(alpha, beta)
             case 13: return v > 0.f ? v : 0.f;                     // Relu
             case 14: return v / (1.f + __expf(-v));                // SiLU
