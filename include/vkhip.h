@@ -187,6 +187,15 @@ int vkhip_conv_forward_scaled(const vkhip_conv_desc *d, const vkhip_conv_plan *p
  * scratch, which keeps the last call's contents: calls that overlap in time on one GPU (two
  * streams, or two host threads) race and must be serialised by the caller. */
 #define VKHIP_NOALLOC_SCRATCH_BYTES ((size_t) 64 << 20)
+/* Depthwise conv that also leaves, for a following global average pool, the sum of its stored fp16
+ * outputs per (plane, row tile): pool is [N*ceil(C/4)][R] x 4 fp32, R = vkhip_conv_pool_parts
+ * (0: the plan's kernel cannot; then use vkhip_conv_forward and vkhip_global_avg_pool). y is
+ * exactly what vkhip_conv_forward writes. No counterpart in the reference (its GlobalAveragePool
+ * re-reads the conv output, cpu/ops/global_avg_pool.cpp:7-28). */
+int vkhip_conv_pool_parts(const vkhip_conv_desc *d, const vkhip_conv_plan *plan);
+int vkhip_conv_forward_pooled(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res,
+                              void *y, void *pool, vkhip_stream_t s);
+
 int vkhip_conv_forward_noalloc(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob,
                                const void *res, void *y, vkhip_stream_t s);
 
@@ -220,6 +229,13 @@ size_t vkhip_se_workspace_bytes(int64_t N, int64_t Cr);
 int    vkhip_se_pack_weights(int64_t C, int64_t Cr, const float *w1, const float *b1, const float *w2, const float *b2, void *blob);
 int    vkhip_fused_se(const void *avg, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr, float alpha, float beta,
                       void *workspace, vkhip_stream_t s);
+/* vkhip_fused_se whose avg is not in memory: the squeeze input is formed from the R fp32 partial
+ * sums per (image, 4-channel block) that vkhip_conv_forward_pooled left ([N][ceil(C/4)][R] x 4
+ * floats), as fp16(sum / HW), the value vkhip_global_avg_pool would have stored. Folds the
+ * reference's GlobalAveragePool (cpu/ops/global_avg_pool.cpp) into the depthwise conv before it
+ * and the first FC after it; no counterpart of its own in the reference. */
+int    vkhip_fused_se_pooled(const void *part, int32_t R, int64_t HW, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr,
+                             float alpha, float beta, void *workspace, vkhip_stream_t s);
 /* y = x * scale[n,c] (channel broadcast; reference Binary Mul BCAST, ops/binary.cpp:32-43). */
 int vkhip_channel_scale(const void *x, const void *scale, void *y, int64_t N, int64_t C, int64_t HW, vkhip_stream_t s);
 
@@ -254,6 +270,10 @@ size_t vkhip_fc_weight_bytes(int64_t K, int64_t M);
 int    vkhip_fc_pack_weights(int64_t K, int64_t M, const float *w, int32_t transB, const float *b, float alpha, float beta, void *blob);
 int    vkhip_fc(const void *x, const void *blob, void *y, int64_t N, int64_t K, int64_t M, int32_t act, float lo, float hi,
                 vkhip_stream_t s);
+/* vkhip_fc with x formed from pooled partial sums as in vkhip_fused_se_pooled (K channels, R
+ * partials per 4-channel block, HW pixels per plane). */
+int    vkhip_fc_pooled(const void *part, int32_t R, int64_t HW, const void *blob, void *y, int64_t N, int64_t K, int64_t M, int32_t act,
+                       float lo, float hi, vkhip_stream_t s);
 /* Channel concat of `count` NC4HW4 inputs (any channel counts) into y. */
 int vkhip_concat_channels(const void *const *xs, const int64_t *cs, int32_t count, void *y, int64_t N, int64_t HW,
                           vkhip_stream_t s);

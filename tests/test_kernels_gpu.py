@@ -807,3 +807,68 @@ def test_conv_input_scale_rejects_other_shapes(gpu):
         d.in_scale = 1
         plan = V.ConvPlan()
         assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_AUTO, -1, 0, ctypes.byref(plan)) == 2
+
+
+# ---------------------------------------------------------------- depthwise + squeeze-excite pool sums
+@pytest.mark.parametrize("shape,k,s,rt", [((3, 72, 28, 28), 3, 2, 7), ((2, 120, 28, 28), 5, 1, 4), ((4, 960, 7, 7), 5, 1, 7),
+                                          ((2, 22, 14, 14), 3, 1, 14), ((5, 40, 56, 56), 5, 2, 4)])
+def test_depthwise_pool_sums(gpu, shape, k, s, rt):
+    """vkhip_conv_forward_pooled writes exactly the depthwise output of vkhip_conv_forward and the
+    per-(plane, row tile) sums of it; a squeeze-excite fed from those sums (vkhip_fused_se_pooled)
+    matches the one fed by vkhip_global_avg_pool on the stored output (the fp32 sums are formed in
+    another order, so the fp16 averages may differ by one rounding step)."""
+    lib = V.vkhip()
+    N, C, H, W = shape
+    r = rng(90 + C + k)
+    x = round_half(r.standard_normal(shape))
+    w = (r.standard_normal((C, 1, k, k)) * 0.3).astype(np.float32)
+    b = (r.standard_normal(C) * 0.1).astype(np.float32)
+    p = k // 2
+    ref, plan, dref = gpu_conv(x, w, b, (s, s), (p, p, p, p), group=C, act=4, algo=V.CONV_DEPTHWISE, tile=rt)
+    d, yshape = conv_desc(x.shape, w.shape, (s, s), (p, p, p, p), (1, 1), C, 4, 0.0, 0.0, 0)
+    R = lib.vkhip_conv_pool_parts(ctypes.byref(d), ctypes.byref(plan))
+    OH = yshape[2]
+    assert R == -(-OH // rt)
+    blob = np.zeros(plan.weight_bytes, np.uint8)
+    check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(plan), w.ctypes.data, b.ctypes.data, blob.ctypes.data))
+    dblob = DeviceBuffer.from_array(blob)
+    dx = to_device_nc4(x)
+    dy = DeviceBuffer(V.nc4_elems(*yshape) * 2)
+    Cb = (C + 3) // 4
+    dpart = DeviceBuffer(N * Cb * R * 16)
+    check(lib.vkhip_conv_forward_pooled(ctypes.byref(d), ctypes.byref(plan), dx.ptr, dblob.ptr, None, dy.ptr, dpart.ptr, None))
+    check(lib.vkhip_stream_sync(None))
+    assert np.array_equal(raw_nc4(dy, yshape), raw_nc4(dref, yshape))
+    part = dpart.download(np.float32, N * Cb * R * 4).reshape(N, Cb, R, 4)
+    y = from_device_nc4(dy, yshape).astype(np.float64)
+    sums = y.reshape(N, C, -1).sum(-1)
+    got = part.sum(2).reshape(N, Cb * 4)[:, :C]
+    np.testing.assert_allclose(got, sums, rtol=1e-5, atol=1e-3)
+    # squeeze-excite from the sums vs from the pooled tensor
+    Cr = max(8, C // 4)
+    w1 = (r.standard_normal((Cr, C)) * 0.2).astype(np.float32)
+    b1 = (r.standard_normal(Cr) * 0.1).astype(np.float32)
+    w2 = (r.standard_normal((C, Cr)) * 0.2).astype(np.float32)
+    b2 = (r.standard_normal(C) * 0.1).astype(np.float32)
+    sblob = np.zeros(lib.vkhip_se_weight_bytes(C, Cr), np.uint8)
+    check(lib.vkhip_se_pack_weights(C, Cr, w1.ctypes.data, b1.ctypes.data, w2.ctypes.data, b2.ctypes.data, sblob.ctypes.data))
+    dsb = DeviceBuffer.from_array(sblob)
+    davg = DeviceBuffer(V.nc4_elems(N, C, 1, 1) * 2)
+    check(lib.vkhip_global_avg_pool(dy.ptr, davg.ptr, N, C, OH, yshape[3], None))
+    ws = DeviceBuffer(lib.vkhip_se_workspace_bytes(N, Cr))
+    o1, o2 = DeviceBuffer(V.nc4_elems(N, C, 1, 1) * 2), DeviceBuffer(V.nc4_elems(N, C, 1, 1) * 2)
+    check(lib.vkhip_fused_se(davg.ptr, dsb.ptr, o1.ptr, N, C, Cr, 1.0 / 6, 0.5, ws.ptr, None))
+    check(lib.vkhip_fused_se_pooled(dpart.ptr, R, OH * yshape[3], dsb.ptr, o2.ptr, N, C, Cr, 1.0 / 6, 0.5, ws.ptr, None))
+    check(lib.vkhip_stream_sync(None))
+    a1 = from_device_nc4(o1, (N, C, 1, 1))
+    a2 = from_device_nc4(o2, (N, C, 1, 1))
+    np.testing.assert_allclose(a2, a1, atol=4e-3)
+    assert parity(a2, a1)[1] >= 0.99999
+
+
+def test_pool_sums_reject_untiled_plan(gpu):
+    lib = V.vkhip()
+    d, _ = conv_desc((1, 12, 16, 16), (12, 1, 3, 3), (1, 1), (2, 2, 2, 2), (2, 2), 12, 0, 0.0, 0.0, 0)
+    plan = V.ConvPlan()
+    check(lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_DEPTHWISE, -1, 0, ctypes.byref(plan)))
+    assert lib.vkhip_conv_pool_parts(ctypes.byref(d), ctypes.byref(plan)) == 0

@@ -94,6 +94,8 @@ VKHIP_API = {
     "vkhip_conv_forward": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_forward_noalloc": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_forward_scaled": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "vkhip_conv_pool_parts": (c_int, [P(ConvDesc), P(ConvPlan)]),
+    "vkhip_conv_forward_pooled": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_dwpw_supported": (c_int, [P(DwPwDesc)]),
     "vkhip_dwpw_weight_bytes": (c_sz, [P(DwPwDesc)]),
     "vkhip_dwpw_pack_weights": (c_int, [P(DwPwDesc), c_vp, c_vp, c_vp, c_vp, c_vp]),
@@ -103,6 +105,7 @@ VKHIP_API = {
     "vkhip_se_pack_weights": (c_int, [c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_se_workspace_bytes": (c_sz, [c_i64, c_i64]),
     "vkhip_fused_se": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_f, c_f, c_vp, c_vp]),
+    "vkhip_fused_se_pooled": (c_int, [c_vp, c_i32, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_f, c_f, c_vp, c_vp]),
     "vkhip_channel_scale": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp]),
     "vkhip_add": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i32, c_f, c_f, c_vp]),
     "vkhip_unary": (c_int, [c_vp, c_vp, c_i64, c_i32, c_f, c_f, c_vp]),
@@ -111,6 +114,7 @@ VKHIP_API = {
     "vkhip_fc_weight_bytes": (c_sz, [c_i64, c_i64]),
     "vkhip_fc_pack_weights": (c_int, [c_i64, c_i64, c_vp, c_i32, c_vp, c_f, c_f, c_vp]),
     "vkhip_fc": (c_int, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i32, c_f, c_f, c_vp]),
+    "vkhip_fc_pooled": (c_int, [c_vp, c_i32, c_i64, c_vp, c_vp, c_i64, c_i64, c_i64, c_i32, c_f, c_f, c_vp]),
     "vkhip_concat_channels": (c_int, [P(c_vp), P(c_i64), c_i32, c_vp, c_i64, c_i64, c_vp]),
     "vkhip_slice_channels": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "vkhip_resize_nearest": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp]),

@@ -102,6 +102,11 @@ namespace vknn {
             // its own output never exists in memory.
             TensorId                poolOut = kNoTensor;
             vkhip_pool_desc         pd {};
+            // Set by the segment after prepare when the global average pool of a squeeze-excite
+            // that reads this depthwise conv's output is folded into it: the conv also writes the
+            // per-(plane, row tile) sums of its output into `gapPart` (gapR partials per plane).
+            std::shared_ptr<DevBuf> gapPart;
+            int                     gapR = 0;
 
             void prepare(const Node &node, SegEnv &env) override {
                 const Graph &g = *env.graph;
@@ -319,6 +324,12 @@ namespace vknn {
                     check(vkhip_conv_maxpool_forward(&d, &plan, &pd, env.dev(in), blob->ptr, env.dev(poolOut), s), "conv + max pool " + name);
                     return;
                 }
+                if (gapPart) {
+                    check(vkhip_conv_forward_pooled(&d, &plan, env.dev(in), blob->ptr, res != kNoTensor ? env.dev(res) : nullptr, env.dev(out),
+                                                    gapPart->ptr, s),
+                          "conv + pool sums " + name);
+                    return;
+                }
                 check(forward(plan, env.dev(in), xscale != kNoTensor ? env.dev(xscale) : nullptr, blob->ptr,
                               res != kNoTensor ? env.dev(res) : nullptr, env.dev(out), ws ? ws->ptr : nullptr, s),
                       "conv " + name);
@@ -327,7 +338,7 @@ namespace vknn {
             std::string describe() const override {
                 static const char *algos[] = {"auto", "gemm", "splitk", "winograd", "depthwise"};
                 return std::string(algos[plan.algo]) + " tile=" + std::to_string(plan.tile) + " ksplit=" + std::to_string(plan.ksplit) +
-                       (d.in_scale ? " +input scale" : "") + (poolOut != kNoTensor ? " +max pool" : "") + " kernel=" +
+                       (d.in_scale ? " +input scale" : "") + (poolOut != kNoTensor ? " +max pool" : "") + (gapPart ? " +pool sums" : "") + " kernel=" +
                        (poolOut != kNoTensor ? std::string("stem_pool_kernel") : std::string(vkhip_conv_plan_kernel(&plan)));
             }
         };
@@ -451,9 +462,16 @@ namespace vknn {
                 flops = 4.0 * N * C * Cr;
                 bytes = (int64_t) (host.size() + (size_t) N * ((C + 3) / 4 * 4) * 2 * 2);
             }
+            // set by the segment when the average pool before this op is folded into the depthwise
+            // conv that feeds it: the squeeze input comes from that conv's partial sums
+            std::shared_ptr<DevBuf> part;
+            int                     R  = 0;
+            int64_t                 HW = 0;
             void record(SegEnv &env, vkhip_stream_t s) override {
-                check(vkhip_fused_se(env.dev(in), blob->ptr, env.dev(out), N, C, Cr, alpha, beta, ws->ptr, s), "fused_se " + name);
+                if (part) check(vkhip_fused_se_pooled(part->ptr, R, HW, blob->ptr, env.dev(out), N, C, Cr, alpha, beta, ws->ptr, s), "fused_se " + name);
+                else check(vkhip_fused_se(env.dev(in), blob->ptr, env.dev(out), N, C, Cr, alpha, beta, ws->ptr, s), "fused_se " + name);
             }
+            std::string describe() const override { return part ? "pool folded into the depthwise conv" : ""; }
         };
 
         // ------------------------------------------------------------ Gemm (FC head) as a 1x1 conv
@@ -915,11 +933,66 @@ namespace vknn {
                 pools.insert(kv.second);
                 foldedInto[kv.second] = g.nodes[kv.first].name;
             }
+            // Squeeze-excite pool folding: a GlobalAveragePool whose input is a depthwise conv of this
+            // segment and whose output only a FusedSE of this segment reads. The conv (once its
+            // plan is known) also leaves the pool sums, and the FusedSE forms its input from them,
+            // so the pool neither launches nor re-reads the conv output. VKNN_HIP_FOLD_GAP=0 keeps it.
+            std::map<int, int> gapConv; // GAP node -> depthwise conv node
+            std::map<int, int> seGap;   // FusedSE node -> GAP node
+            {
+                const char *gap_env = std::getenv("VKNN_HIP_FOLD_GAP");
+                if (!gap_env || std::string(gap_env) != "0") {
+                    std::set<int>           inSeg(idx.begin(), idx.end());
+                    std::map<TensorId, int> producer;
+                    std::map<TensorId, std::vector<int>> readers;
+                    for (size_t i = 0; i < g.nodes.size(); ++i) {
+                        for (TensorId t: g.nodes[i].inputs)
+                            if (t != kNoTensor) readers[t].push_back((int) i);
+                        if (g.nodes[i].fusedResidual != kNoTensor) readers[g.nodes[i].fusedResidual].push_back((int) i);
+                        for (TensorId t: g.nodes[i].outputs)
+                            if (t != kNoTensor) producer[t] = (int) i;
+                    }
+                    std::set<TensorId> gout(g.outputs.begin(), g.outputs.end());
+                    for (int i: idx) {
+                        const Node &p = g.nodes[i];
+                        if (p.type != OpType::GlobalAvgPool || p.inputs.empty() || gout.count(p.outputs[0])) continue;
+                        auto pit = producer.find(p.inputs[0]);
+                        if (pit == producer.end() || !inSeg.count(pit->second) || folded.count(pit->second)) continue;
+                        const Node &c = g.nodes[pit->second];
+                        if (c.type != OpType::Conv || c.attr.geti("group", 1) <= 1 || scaled.count(pit->second) || convPool.count(pit->second)) continue;
+                        const auto &rd = readers[p.outputs[0]];
+                        if (rd.size() != 1 || !inSeg.count(rd[0]) || g.nodes[rd[0]].type != OpType::FusedSE || g.nodes[rd[0]].inputs[0] != p.outputs[0])
+                            continue;
+                        gapConv[i]   = pit->second;
+                        seGap[rd[0]] = i;
+                    }
+                }
+            }
+            std::map<int, ConvOp *> convOps;       // node -> its ConvOp (pool-fold candidates)
+            std::map<int, std::shared_ptr<DevBuf>> gapParts; // folded GAP node -> partial sums
+            std::map<int, int>      gapR;
+            std::map<int, size_t>   opPos; // node -> index of its op
             std::vector<std::vector<TensorId>> ins, outs;
             for (int i: idx) {
                 const Node &nd = g.nodes[i];
                 std::unique_ptr<HipOp> op;
-                if (folded.count(i) || pools.count(i)) {
+                auto gc = gapConv.find(i);
+                if (gc != gapConv.end() && convOps.count(gc->second)) {
+                    ConvOp   *c = convOps[gc->second];
+                    const int R = vkhip_conv_pool_parts(&c->d, &c->plan);
+                    if (R > 0) {
+                        c->gapR    = R;
+                        c->gapPart = std::make_shared<DevBuf>((size_t) c->d.N * ((c->d.Cout + 3) / 4) * R * 16);
+                        gapParts[i] = c->gapPart;
+                        gapR[i]     = R;
+                        auto f  = std::make_unique<FoldedMulOp>();
+                        f->into = c->name;
+                        f->what = "global average pool";
+                        op      = std::move(f);
+                    }
+                }
+                if (op) {
+                } else if (folded.count(i) || pools.count(i)) {
                     auto f  = std::make_unique<FoldedMulOp>();
                     f->into = foldedInto[i];
                     if (pools.count(i)) f->what = "max pool";
@@ -943,10 +1016,30 @@ namespace vknn {
                 }
                 op->name = nd.name;
                 op->type = nd.type;
-                op->prepare(nd, env_);
+                const bool gapFolded = gapParts.count(i) > 0;
+                if (!gapFolded) op->prepare(nd, env_);
+                else op->kind = "folded";
+                if (gapConv.size() && nd.type == OpType::Conv) convOps[i] = static_cast<ConvOp *>(op.get());
+                auto sg = seGap.find(i);
+                if (sg != seGap.end() && gapParts.count(sg->second)) {
+                    auto       *se = static_cast<SeOp *>(op.get());
+                    const Node &gn = g.nodes[sg->second];
+                    NCHW        x  = NCHW::from(g.desc(gn.inputs[0]).shape);
+                    se->part = gapParts[sg->second];
+                    se->R    = gapR[sg->second];
+                    se->HW   = x.h * x.w;
+                }
+                opPos[i] = ops_.size();
                 ops_.push_back(std::move(op));
                 // data the op's launches read and write (alias and folded ops launch nothing)
                 std::vector<TensorId> in, out;
+                if (gapFolded) {
+                    // the pool's output stands for the sums the conv's launch writes
+                    outs[opPos[gapConv[i]]].push_back(resolve(nd.outputs[0]));
+                    ins.push_back(in);
+                    outs.push_back(out);
+                    continue;
+                }
                 if (folded.count(i) || pools.count(i)) {
                     ins.push_back(in);
                     outs.push_back(out);

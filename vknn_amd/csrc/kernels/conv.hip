@@ -164,6 +164,7 @@ namespace vkhip {
         int          act;
         float        lo, hi;
         int          has_res;
+        float4v     *pool; // dwconv_lds_kernel: per-(plane, row tile) sums of the stored outputs, or null
     };
 
     template <int KH, int KW, int S, int OXT>
@@ -361,11 +362,11 @@ namespace vkhip {
         }
         __syncthreads();
 
-        if (pl >= np) return;
+        const bool live = pl < np;
         float4v acc[RT];
 #pragma unroll
         for (int r = 0; r < RT; ++r) acc[r] = b0;
-        const uint2 *src = tile + pl * t.PS + ox * S + (PLA - a.PL);
+        const uint2 *src = tile + min(pl, np - 1) * t.PS + ox * S + (PLA - a.PL);
 #pragma unroll
         for (int ir = 0; ir < IR; ++ir) {
             half4 tap[KW];
@@ -385,9 +386,10 @@ namespace vkhip {
                 }
             }
         }
-        const int       nrows = min(RT, a.OH - oy0);
+        const int       nrows = live ? min(RT, a.OH - oy0) : 0;
         const long long yb    = ((long long) p * a.OH + oy0) * OW + ox;
         const int       c     = cb * 4;
+        float4v         psum  = {0.f, 0.f, 0.f, 0.f}; // this column's share of the plane sum (pool)
         auto finish = [&](auto act_c) __attribute__((always_inline)) {
             constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
@@ -403,7 +405,9 @@ namespace vkhip {
                 if (c + 1 >= a.C) v.y = 0.f;
                 if (c + 2 >= a.C) v.z = 0.f;
                 if (c + 3 >= a.C) v.w = 0.f;
-                a.y[yb + (long long) r * OW] = h4_as_u2(f4_to_h4(v));
+                const half4 h = f4_to_h4(v);
+                a.y[yb + (long long) r * OW] = h4_as_u2(h);
+                psum += h4_to_f4(h);
             }
         };
         switch (a.act) {
@@ -413,6 +417,20 @@ namespace vkhip {
             case VKHIP_ACT_HARDSWISH: finish(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
             case VKHIP_ACT_SILU: finish(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
             default: finish(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
+        }
+        if (a.pool) {
+            // the global-average-pool numerator of a following squeeze-excite, without reading the
+            // output back: sum of the fp16 values just stored, per plane of this row tile (columns
+            // in order, then the host-visible partials per row tile in order: deterministic)
+            __syncthreads(); // every wave is done with the input tile
+            float4v *red = reinterpret_cast<float4v *>(dsm);
+            red[tid] = psum;
+            __syncthreads();
+            if (tid < np) {
+                float4v sum = {0.f, 0.f, 0.f, 0.f};
+                for (int k = 0; k < OW; ++k) sum += red[tid * OW + k];
+                a.pool[(long long) (p0 + tid) * t.row_tiles + rt] = sum;
+            }
         }
     }
 
@@ -866,7 +884,7 @@ int vkhip_conv_maxpool_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *
 
 // The forward pass of every conv algorithm; xs is the input scale of an in_scale plan (or null).
 static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *xs, const void *blob,
-                             const void *res, void *y, void *workspace, vkhip_stream_t s) {
+                             const void *res, void *y, void *workspace, vkhip_stream_t s, void *pool = nullptr) {
     if (!d || !plan || !x || !blob || !y) return set_error(VKHIP_ERR_INVALID, "conv_forward: null argument");
     if (d->has_res && !res) return set_error(VKHIP_ERR_INVALID, "conv_forward: has_res without a residual tensor");
     if (plan->workspace_bytes && !workspace) return set_error(VKHIP_ERR_INVALID, "conv_forward: plan needs a workspace");
@@ -883,11 +901,12 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
         a.N = d->N; a.Cb = (int) Cb; a.C = d->Cin; a.H = d->H; a.W = d->W; a.OH = d->OH; a.OW = d->OW;
         a.KH = d->KH; a.KW = d->KW; a.SH = d->SH; a.SW = d->SW; a.PT = d->PT; a.PL = d->PL; a.DH = d->DH; a.DW = d->DW;
         a.act = d->act; a.lo = d->act_lo; a.hi = d->act_hi; a.has_res = d->has_res;
+        a.pool = (float4v *) pool;
         bool unit = d->DH == 1 && d->DW == 1 && d->SH == d->SW;
         DwTile t;
         const int RT = plan->tile > 0 ? plan->tile : (d->OH % 7 == 0 ? 7 : 4);
         if (unit && d->KH == d->KW && (d->KH == 3 || d->KH == 5) && (d->SH == 1 || d->SH == 2) && dw_tile(d, (int64_t) d->N * Cb, RT, t)) {
-            const size_t sm = (size_t) t.PP * t.PS * 8;
+            const size_t sm = std::max<size_t>((size_t) t.PP * t.PS * 8, pool ? 256 * 16 : 0); // the pool reduction reuses the tile
             dim3 g2((unsigned) ((int64_t) t.row_tiles * t.plane_groups));
 #define VKHIP_DW_LAUNCH(K, S_)                                                                                 \
     (RT == 14 ? dwconv_lds_kernel<K, K, S_, 14><<<g2, 256, sm, st>>>(a, t) : RT == 7 ? dwconv_lds_kernel<K, K, S_, 7><<<g2, 256, sm, st>>>(a, t) : dwconv_lds_kernel<K, K, S_, 4><<<g2, 256, sm, st>>>(a, t))
@@ -898,6 +917,7 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
 #undef VKHIP_DW_LAUNCH
             return check_launch("dwconv_lds");
         }
+        if (pool) return set_error(VKHIP_ERR_UNSUPPORTED, "conv_forward_pooled: the plan does not run the tiled depthwise kernel");
         constexpr int OXT = 4;
         int64_t total = (int64_t) d->N * Cb * d->OH * ceil_div(d->OW, OXT);
         dim3 grid((unsigned) ceil_div(total, 256));
@@ -1005,6 +1025,22 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
                        void *y, void *workspace, vkhip_stream_t s) {
     if (d && d->in_scale) return set_error(VKHIP_ERR_INVALID, "conv_forward: an in_scale plan runs through vkhip_conv_forward_scaled");
     return conv_forward_impl(d, plan, x, nullptr, blob, res, y, workspace, s);
+}
+
+int vkhip_conv_pool_parts(const vkhip_conv_desc *d, const vkhip_conv_plan *plan) {
+    if (!d || !plan || plan->algo != VKHIP_CONV_DEPTHWISE || d->in_scale) return 0;
+    const bool unit = d->DH == 1 && d->DW == 1 && d->SH == d->SW;
+    const int  RT   = plan->tile > 0 ? plan->tile : (d->OH % 7 == 0 ? 7 : 4);
+    DwTile     t;
+    if (!(unit && d->KH == d->KW && (d->KH == 3 || d->KH == 5) && (d->SH == 1 || d->SH == 2) && dw_tile(d, (int64_t) d->N * ceil_div(d->Cin, 4), RT, t)))
+        return 0;
+    return t.row_tiles;
+}
+
+int vkhip_conv_forward_pooled(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res,
+                              void *y, void *pool, vkhip_stream_t s) {
+    if (!pool || vkhip_conv_pool_parts(d, plan) <= 0) return set_error(VKHIP_ERR_UNSUPPORTED, "conv_forward_pooled: needs a tiled depthwise plan and a pool buffer");
+    return conv_forward_impl(d, plan, x, nullptr, blob, res, y, nullptr, s, pool);
 }
 
 int vkhip_conv_forward_scaled(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *xs, const void *blob,

@@ -803,9 +803,13 @@ namespace vkhip {
     // group q loads the 8 contiguous k at 8q..8q+7 of its row/column and feeds the low four to one
     // MFMA and the high four to the next: the same permutation of k on A and B, so the sum is the
     // same. X16: x rows are 16-byte aligned (round_up(K,4) % 8 == 0) and loaded 16 bytes at once.
-    template <int NF, bool X16>
+    // PART: x is not given; each 4-channel block of it is the global average pool of a depthwise
+    // output, fp16(sum of R fp32 partial sums [N][Kb][R] / HW) (what the pool kernel computes and
+    // stores), formed while loading.
+    template <int NF, bool X16, bool PART = false>
     __global__ __launch_bounds__(512) void fc_kernel(const uint2 *x, const half_t *w, const float *b, uint2 *y, int N, int Kb,
-                                                     int Kp, int M, int Mb, int act, float lo, float hi) {
+                                                     int Kp, int M, int Mb, int act, float lo, float hi, const float4v *part = nullptr,
+                                                     int R = 0, float hw = 1.f) {
         constexpr int U = 8;
         __shared__ float4v red[8][NF][64];
         const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -833,7 +837,17 @@ namespace vkhip {
                 for (int f = 0; f < NF; ++f) {
                     const int kb = c * 8 + 2 * q; // first 4-element block of this lane's 8
                     half4     lo4 = {0, 0, 0, 0}, hi4 = {0, 0, 0, 0};
-                    if (c < chunks && nok[f]) {
+                    if (PART) {
+                        const int n = n0 + f * 16 + r;
+                        auto pooled = [&](int k) __attribute__((always_inline)) {
+                            const float4v *q = part + ((long long) n * Kb + k) * R;
+                            float4v        s4 = {0.f, 0.f, 0.f, 0.f};
+                            for (int i = 0; i < R; ++i) s4 += q[i];
+                            return f4_to_h4(s4 / hw);
+                        };
+                        if (c < chunks && nok[f] && kb < Kb) lo4 = pooled(kb);
+                        if (c < chunks && nok[f] && kb + 1 < Kb) hi4 = pooled(kb + 1);
+                    } else if (c < chunks && nok[f]) {
                         if (X16) {
                             if (kb < Kb) {
                                 const uint4 v = *(const uint4 *) (xrow[f] + c * 8);
@@ -1014,8 +1028,10 @@ int vkhip_fc_pack_weights(int64_t K, int64_t M, const float *w, int32_t transB, 
     return VKHIP_OK;
 }
 
-int vkhip_fc(const void *x, const void *blob, void *y, int64_t N, int64_t K, int64_t M, int32_t act, float lo, float hi, vkhip_stream_t s) {
-    if (!x || !blob || !y || N <= 0 || K <= 0 || M <= 0) return set_error(VKHIP_ERR_INVALID, "fc: bad arguments");
+// fc launcher: x as fp16 rows, or (part != null) as the pooled partial sums described at fc_kernel
+static int fc_launch(const void *x, const float4v *part, int R, int HW, const void *blob, void *y, int64_t N, int64_t K, int64_t M, int32_t act,
+                     float lo, float hi, vkhip_stream_t s) {
+    if ((!x && !part) || !blob || !y || N <= 0 || K <= 0 || M <= 0) return set_error(VKHIP_ERR_INVALID, "fc: bad arguments");
     if (N * round_up(K, 4) >= (1LL << 31) || N * round_up(M, 4) >= (1LL << 31)) return set_error(VKHIP_ERR_UNSUPPORTED, "fc: tensor too large");
     int64_t Kp, Mp;
     fc_geom(K, M, Kp, Mp);
@@ -1028,7 +1044,11 @@ int vkhip_fc(const void *x, const void *blob, void *y, int64_t N, int64_t K, int
     hipStream_t st = resolve_stream(s);
     const uint2 *xx = (const uint2 *) x;
     uint2       *yy = (uint2 *) y;
-    if (nf1) {
+    const float  hw = (float) HW;
+    if (part) {
+        if (nf1) fc_kernel<1, false, true><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi, part, R, hw);
+        else fc_kernel<2, false, true><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi, part, R, hw);
+    } else if (nf1) {
         if (Kb % 2 == 0) fc_kernel<1, true><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi);
         else fc_kernel<1, false><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi);
     } else {
@@ -1036,6 +1056,17 @@ int vkhip_fc(const void *x, const void *blob, void *y, int64_t N, int64_t K, int
         else fc_kernel<2, false><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi);
     }
     return check_launch("fc");
+}
+
+int vkhip_fc(const void *x, const void *blob, void *y, int64_t N, int64_t K, int64_t M, int32_t act, float lo, float hi, vkhip_stream_t s) {
+    if (!x) return set_error(VKHIP_ERR_INVALID, "fc: bad arguments");
+    return fc_launch(x, nullptr, 0, 1, blob, y, N, K, M, act, lo, hi, s);
+}
+
+int vkhip_fc_pooled(const void *part, int32_t R, int64_t HW, const void *blob, void *y, int64_t N, int64_t K, int64_t M, int32_t act, float lo,
+                    float hi, vkhip_stream_t s) {
+    if (!part || R <= 0 || HW <= 0 || HW >= (1LL << 24)) return set_error(VKHIP_ERR_INVALID, "fc_pooled: bad arguments");
+    return fc_launch(nullptr, (const float4v *) part, R, (int) HW, blob, y, N, K, M, act, lo, hi, s);
 }
 
 } // extern "C"

@@ -506,6 +506,14 @@ int vkhip_fused_se(const void *avg, const void *blob, void *y, int64_t N, int64_
     return vkhip_fc(workspace, (const char *) blob + se_w2_offset(C, Cr), y, N, Cr, C, VKHIP_ACT_HARDSIGMOID, alpha, beta, s);
 }
 
+int vkhip_fused_se_pooled(const void *part, int32_t R, int64_t HW, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr, float alpha,
+                          float beta, void *workspace, vkhip_stream_t s) {
+    if (!part || !blob || !y || !workspace || N <= 0 || C <= 0 || Cr <= 0) return set_error(VKHIP_ERR_INVALID, "fused_se_pooled: bad arguments");
+    int rc = vkhip_fc_pooled(part, R, HW, blob, workspace, N, C, Cr, VKHIP_ACT_RELU, 0.f, 0.f, s);
+    if (rc) return rc;
+    return vkhip_fc(workspace, (const char *) blob + se_w2_offset(C, Cr), y, N, Cr, C, VKHIP_ACT_HARDSIGMOID, alpha, beta, s);
+}
+
 int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s) {
     if (!d || !x || !y || d->N <= 0 || d->C <= 0 || d->OH <= 0 || d->OW <= 0 || d->KH <= 0 || d->KW <= 0 || d->SH <= 0 || d->SW <= 0)
         return set_error(VKHIP_ERR_INVALID, "maxpool: bad arguments");
