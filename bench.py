@@ -168,6 +168,7 @@ def main():
     ap.add_argument("--options", default="")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config throughput section")
     ap.add_argument("--b1-steps", type=int, default=100)
     ap.add_argument("--dw-batch", type=int, default=128, help="batch of the MobileNetV3-Large depthwise measurement (0 = skip)")
     ap.add_argument("--plan-out", default="", help="write the timed session's plan (one line per op with its flops and "
@@ -338,6 +339,28 @@ def main():
                                    "frac_of_step_time": round(f_bytes / (f_ms * fscale * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                                    "execution": [ln for ln in fplan.splitlines() if "[dwpw]" in ln]}
         xd.close()
+
+    # ---- every config at its two batch sizes (img/s and TFLOP/s of whole forward passes, the
+    # default session options; the headline config is the line's value)
+    if not args.no_configs:
+        per = {}
+        for name, batches, opts in (("conv3x3_bn_relu", (1,), ""), ("mnv2_block", (1, 32), ""), ("mnv2_block", (32,), "fuse_dwpw=1"),
+                                     ("mobilenetv3_large", (1, 128), ""), ("mobilenetv3_large", (128,), "fuse_se=1"),
+                                     ("yolov8n", (1, 16), "")):
+            fl = V.vknn().vknn_model_flops(name.encode())
+            for b in batches:
+                cs = V.Session(name, b, seed=7, options=opts)
+                cx = V.DeviceBuffer.from_array(np.random.default_rng(3).standard_normal(cs.in_shape).astype(np.float32))
+                cs.bind_device_input(cx.ptr)
+                n = 50 if b == 1 else 20
+                cw, _ = time_steps(cs, n, 5)
+                cs.close()
+                cx.close()
+                key = name + (f" ({opts})" if opts else "")
+                per.setdefault(key, {})[f"b{b}"] = {"ms_per_step": round(cw / n * 1e3, 4), "img_per_s": round(b * n / cw, 1),
+                                                      "tflops": round(fl * b * n / cw / 1e12, 2)}
+                log(f"{key} b{b}: {cw / n * 1e3:.3f} ms/step")
+        extra["per_config"] = per
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.model)
 
