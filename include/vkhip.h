@@ -196,6 +196,15 @@ int vkhip_conv_pool_parts(const vkhip_conv_desc *d, const vkhip_conv_plan *plan)
 int vkhip_conv_forward_pooled(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res,
                               void *y, void *pool, vkhip_stream_t s);
 
+/* vkhip_conv_forward on views: x and y may point into wider NC4HW4 tensors, `x_pstride` /
+ * `y_pstride` channel blocks (4-channel planes) per image apart instead of ceil(Cin/4) /
+ * ceil(Cout/4) (0 = dense). This lets a conv read a channel slice of a tensor (a Split output) and
+ * write straight into its slice of a channel Concat, so neither is copied. GEMM and split-K plans
+ * only (not the stem tiles, Winograd or depthwise), no residual, no input scale. No counterpart in
+ * the reference, whose Concat and Split copy (ops/concat.cpp, ops/split.cpp). */
+int vkhip_conv_forward_view(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, int64_t x_pstride, const void *blob,
+                            void *y, int64_t y_pstride, void *workspace, vkhip_stream_t s);
+
 int vkhip_conv_forward_noalloc(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob,
                                const void *res, void *y, vkhip_stream_t s);
 
@@ -242,6 +251,10 @@ int vkhip_channel_scale(const void *x, const void *scale, void *y, int64_t N, in
 /* ---------------------------------------------------------------- element-wise
  * y = act(a + b) over `n` packed fp16 elements (reference Add same-shape path, add.cpp:67-86). */
 int vkhip_add(const void *a, const void *b, void *y, int64_t n, int32_t act, float lo, float hi, vkhip_stream_t s);
+/* vkhip_add over views (plane strides per image as in vkhip_conv_forward_view; 0 = dense) of
+ * N x C x HW NC4HW4 tensors. */
+int vkhip_add_view(const void *a, int64_t a_pstride, const void *b, int64_t b_pstride, void *y, int64_t y_pstride, int64_t N, int64_t C,
+                   int64_t HW, int32_t act, float lo, float hi, vkhip_stream_t s);
 /* y = op(x) on `n` packed fp16 elements; op is a vknn UnaryType code (Sigmoid 0, HardSwish 2,
  * HardSigmoid 3 with alpha/beta in p0/p1, Relu 13, SiLU 14) or, with unary = -1, a clip to [p0,p1]. */
 int vkhip_unary(const void *x, void *y, int64_t n, int32_t unary, float p0, float p1, vkhip_stream_t s);
@@ -253,6 +266,8 @@ typedef struct vkhip_pool_desc {
     int32_t N, C, H, W, OH, OW, KH, KW, SH, SW, PT, PL;
 } vkhip_pool_desc;
 int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s);
+/* vkhip_maxpool over views (plane strides per image; 0 = dense). */
+int vkhip_maxpool_view(const vkhip_pool_desc *d, const void *x, int64_t x_pstride, void *y, int64_t y_pstride, vkhip_stream_t s);
 /* A first-layer conv (at most 4 input channels, 3x3 or 7x7, stride 1 or 2, pad K/2, <= 64 output
  * channels, no residual) followed by a 3x3 stride-2 pad-1 max pool over its output, in one
  * kernel: y = maxpool(act(conv(x) + bias)), bit-identical to vkhip_conv_forward then
@@ -282,6 +297,9 @@ int vkhip_slice_channels(const void *x, void *y, int64_t N, int64_t Cx, int64_t 
 /* Nearest-neighbour resize (ONNX asymmetric/floor): y[oy,ox] = x[floor(oy*H/OH), floor(ox*W/OW)]. */
 int vkhip_resize_nearest(const void *x, void *y, int64_t N, int64_t C, int64_t H, int64_t W, int64_t OH, int64_t OW,
                          vkhip_stream_t s);
+/* vkhip_resize_nearest over views (plane strides per image; 0 = dense). */
+int vkhip_resize_nearest_view(const void *x, int64_t x_pstride, void *y, int64_t y_pstride, int64_t N, int64_t C, int64_t H, int64_t W,
+                              int64_t OH, int64_t OW, vkhip_stream_t s);
 
 #ifdef __cplusplus
 }

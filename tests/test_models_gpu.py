@@ -214,3 +214,26 @@ def test_stem_maxpool_fused(gpu, model, batch, monkeypatch):
     # the two sessions may pick different tiles for the other convs, so compare at the tolerance
     check_outputs(got, ref, sess.out_elems, f"{model} fused stem pool vs apart")
     check_outputs(got, oracle_model_run(model, batch, 7, x), sess.out_elems, f"{model} fused stem pool vs oracle")
+
+
+@pytest.mark.parametrize("model,batch", [("yolo_tiny", 2), ("yolov8n", 2)])
+def test_inplace_concat_split(gpu, model, batch, monkeypatch):
+    """Channel concats and splits done in place (producers write straight into their slice of the
+    concat's buffer, split outputs are views of the split input, views read and written with plane
+    strides by the conv, add, max pool and resize kernels): bit-identical to the session that copies
+    (same plans: tuning and Winograd off), across the eager run and graph replays, and within the
+    tolerance of the oracle."""
+    opts = "tuning=off;winograd=off;branches=0"
+    sess = V.Session(model, batch, seed=7, options=opts)
+    plan = sess.describe()
+    assert "concat in place" in plan and "split in place" in plan, plan
+    monkeypatch.setenv("VKNN_HIP_VIEWS", "0")
+    plain = V.Session(model, batch, seed=7, options=opts)
+    assert "in place" not in plain.describe()
+    rng = np.random.default_rng(8)
+    for k in range(3):
+        x = rng.standard_normal(int(np.prod(sess.in_shape))).astype(np.float32)
+        got = sess.run(x)
+        np.testing.assert_array_equal(got, plain.run(x))
+        if k == 0:
+            check_outputs(got, oracle_model_run(model, batch, 7, x), sess.out_elems, f"{model} in-place concat")

@@ -95,6 +95,10 @@ VKHIP_API = {
     "vkhip_conv_forward_noalloc": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_forward_scaled": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_pool_parts": (c_int, [P(ConvDesc), P(ConvPlan)]),
+    "vkhip_conv_forward_view": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp]),
+    "vkhip_add_view": (c_int, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64, c_i32, c_f, c_f, c_vp]),
+    "vkhip_maxpool_view": (c_int, [P(PoolDesc), c_vp, c_i64, c_vp, c_i64, c_vp]),
+    "vkhip_resize_nearest_view": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "vkhip_conv_forward_pooled": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_dwpw_supported": (c_int, [P(DwPwDesc)]),
     "vkhip_dwpw_weight_bytes": (c_sz, [P(DwPwDesc)]),

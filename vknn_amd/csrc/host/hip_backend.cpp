@@ -107,6 +107,9 @@ namespace vknn {
             // per-(plane, row tile) sums of its output into `gapPart` (gapR partials per plane).
             std::shared_ptr<DevBuf> gapPart;
             int                     gapR = 0;
+            // Set by the segment before prepare when the conv reads or writes a view (a slice of an
+            // in-place concat or split): the plan is then a GEMM or split-K one (no Winograd).
+            bool                    viewIO = false;
 
             void prepare(const Node &node, SegEnv &env) override {
                 const Graph &g = *env.graph;
@@ -147,6 +150,8 @@ namespace vknn {
             }
 
             void build(const float *w, const float *b) {
+                // a view conv runs GEMM or split-K plans only (no Winograd transforms over views)
+                if (viewIO && plan.algo == VKHIP_CONV_WINOGRAD) check(vkhip_conv_plan_make(&d, VKHIP_CONV_GEMM, -1, 0, &plan), "conv plan");
                 std::vector<uint8_t> host(plan.weight_bytes);
                 check(vkhip_conv_pack_weights(&d, &plan, w, b, host.data()), "conv weight pack");
                 blob = upload(host.data(), host.size());
@@ -164,7 +169,7 @@ namespace vknn {
                     return;
                 }
                 vkhip_conv_plan tmp;
-                const bool wino_ok = !dw && vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, -1, 0, &tmp) == VKHIP_OK && d.Cin >= 32 && d.Cout >= 32;
+                const bool wino_ok = !dw && !viewIO && vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, -1, 0, &tmp) == VKHIP_OK && d.Cin >= 32 && d.Cout >= 32;
                 if (wino == (int) Mode::On && wino_ok) {
                     check(vkhip_conv_plan_make(&d, VKHIP_CONV_WINOGRAD, -1, 0, &plan), "conv plan");
                     build(w, b);
@@ -175,7 +180,7 @@ namespace vknn {
                     build(w, b);
                     return;
                 }
-                const std::string key = keyOf(d, tuning * 4 + wino);
+                const std::string key = keyOf(d, tuning * 4 + wino) + (viewIO ? "_view" : "");
                 int32_t           cached = 0;
                 if (TuneCache::instance().get(key, cached)) {
                     // an entry that no longer makes a plan (e.g. written by another build) is re-tuned
@@ -328,6 +333,11 @@ namespace vknn {
                     check(vkhip_conv_forward_pooled(&d, &plan, env.dev(in), blob->ptr, res != kNoTensor ? env.dev(res) : nullptr, env.dev(out),
                                                     gapPart->ptr, s),
                           "conv + pool sums " + name);
+                    return;
+                }
+                if (viewIO) {
+                    check(vkhip_conv_forward_view(&d, &plan, env.dev(in), env.pstride(in), blob->ptr, env.dev(out), env.pstride(out), ws ? ws->ptr : nullptr, s),
+                          "conv " + name);
                     return;
                 }
                 check(forward(plan, env.dev(in), xscale != kNoTensor ? env.dev(xscale) : nullptr, blob->ptr,
@@ -579,6 +589,12 @@ namespace vknn {
                 bytes = n * 6;
             }
             void record(SegEnv &env, vkhip_stream_t s) override {
+                const int64_t pa = env.pstride(a), pb = env.pstride(b), py = env.pstride(out);
+                if (pa || pb || py) {
+                    const NCHW x = NCHW::from(env.graph->desc(out).shape);
+                    check(vkhip_add_view(env.dev(a), pa, env.dev(b), pb, env.dev(out), py, x.n, x.c, x.h * x.w, act, lo, hi, s), "add " + name);
+                    return;
+                }
                 check(vkhip_add(env.dev(a), env.dev(b), env.dev(out), n, act, lo, hi, s), "add " + name);
             }
         };
@@ -669,7 +685,9 @@ namespace vknn {
                 kind = "maxpool";
                 bytes = (int64_t) (nc4Bytes(env.graph->desc(in).shape) + nc4Bytes(env.graph->desc(out).shape));
             }
-            void record(SegEnv &env, vkhip_stream_t s) override { check(vkhip_maxpool(&d, env.dev(in), env.dev(out), s), "maxpool " + name); }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                check(vkhip_maxpool_view(&d, env.dev(in), env.pstride(in), env.dev(out), env.pstride(out), s), "maxpool " + name);
+            }
         };
 
         struct ConcatOp: HipOp {
@@ -736,7 +754,8 @@ namespace vknn {
                 bytes = (int64_t) (nc4Bytes(env.graph->desc(in).shape) + nc4Bytes(env.graph->desc(out).shape));
             }
             void record(SegEnv &env, vkhip_stream_t s) override {
-                check(vkhip_resize_nearest(env.dev(in), env.dev(out), x.n, x.c, x.h, x.w, y.h, y.w, s), "resize " + name);
+                check(vkhip_resize_nearest_view(env.dev(in), env.pstride(in), env.dev(out), env.pstride(out), x.n, x.c, x.h, x.w, y.h, y.w, s),
+                      "resize " + name);
             }
         };
 
@@ -752,7 +771,7 @@ namespace vknn {
             std::string into, what = "scale";
             void        prepare(const Node &, SegEnv &) override { kind = "folded"; }
             void        record(SegEnv &, vkhip_stream_t) override {}
-            std::string describe() const override { return what + " folded into " + into; }
+            std::string describe() const override { return what + (what.find(':') != std::string::npos ? " " : " folded into ") + into; }
         };
 
         // Stem + pool fusion: a MaxPool 3x3 stride 2 pad 1 whose input is the output of a conv of the
@@ -900,17 +919,9 @@ namespace vknn {
                 for (TensorId t: nd.outputs)
                     if (t != kNoTensor) produced.insert(t);
             }
-            // Device buffers: one NC4HW4 fp16 buffer per activation (aliases share their source's).
             for (int i: idx) {
                 const Node &nd = g.nodes[i];
-                if (isAliasOp(g, nd)) {
-                    alias_[nd.outputs[0]] = resolve(nd.inputs[0]);
-                    continue;
-                }
-                for (TensorId t: nd.inputs)
-                    if (t != kNoTensor && !g.isInitializer(t) && !produced.count(t) && !bufs_.count(t)) bufs_[t] = std::make_shared<DevBuf>(nc4Bytes(g.desc(t).shape));
-                for (TensorId t: nd.outputs)
-                    if (t != kNoTensor && !bufs_.count(t)) bufs_[t] = std::make_shared<DevBuf>(nc4Bytes(g.desc(t).shape));
+                if (isAliasOp(g, nd)) alias_[nd.outputs[0]] = resolve(nd.inputs[0]);
             }
             std::map<int, std::pair<TensorId, TensorId>> scaled;
             std::set<int>                                folded;
@@ -972,6 +983,26 @@ namespace vknn {
             std::map<int, std::shared_ptr<DevBuf>> gapParts; // folded GAP node -> partial sums
             std::map<int, int>      gapR;
             std::map<int, size_t>   opPos; // node -> index of its op
+            // In-place concat / split (planViews); VKNN_HIP_VIEWS=0 keeps their copies (A/B).
+            {
+                std::set<int> noWrite, noRead;
+                for (auto &kv: convPool) noWrite.insert(kv.first);
+                for (auto &kv: scaled) noRead.insert(kv.first);
+                for (int m: folded) noRead.insert(m), noWrite.insert(m);
+                for (auto &kv: gapConv) noWrite.insert(kv.second);
+                const char *views_env = std::getenv("VKNN_HIP_VIEWS");
+                if (!views_env || std::string(views_env) != "0") planViews(idx, noWrite, noRead);
+            }
+            // Device buffers: one NC4HW4 fp16 buffer per activation (aliases share their source's;
+            // a tensor placed in another one by planViews has none of its own).
+            for (int i: idx) {
+                const Node &nd = g.nodes[i];
+                if (isAliasOp(g, nd)) continue;
+                for (TensorId t: nd.inputs)
+                    if (t != kNoTensor && !g.isInitializer(t) && !produced.count(t) && !bufs_.count(t)) bufs_[t] = std::make_shared<DevBuf>(nc4Bytes(g.desc(t).shape));
+                for (TensorId t: nd.outputs)
+                    if (t != kNoTensor && !bufs_.count(t) && !place_.count(t)) bufs_[t] = std::make_shared<DevBuf>(nc4Bytes(g.desc(t).shape));
+            }
             std::vector<std::vector<TensorId>> ins, outs;
             for (int i: idx) {
                 const Node &nd = g.nodes[i];
@@ -991,7 +1022,13 @@ namespace vknn {
                         op      = std::move(f);
                     }
                 }
-                if (op) {
+                const bool inPlace = viewCats_.count(i) || viewSplits_.count(i);
+                if (inPlace) {
+                    auto f  = std::make_unique<FoldedMulOp>();
+                    f->what = nd.type == OpType::Concat ? "concat in place: its inputs are written into" : "split in place: its outputs are views of";
+                    f->into = g.desc(nd.type == OpType::Concat ? nd.outputs[0] : nd.inputs[0]).name;
+                    op      = std::move(f);
+                } else if (op) {
                 } else if (folded.count(i) || pools.count(i)) {
                     auto f  = std::make_unique<FoldedMulOp>();
                     f->into = foldedInto[i];
@@ -1017,6 +1054,11 @@ namespace vknn {
                 op->name = nd.name;
                 op->type = nd.type;
                 const bool gapFolded = gapParts.count(i) > 0;
+                if (nd.type == OpType::Conv && !inPlace && !gapFolded && !folded.count(i) && !pools.count(i)) {
+                    bool v = false;
+                    for (TensorId t: {nd.inputs[0], nd.outputs[0]}) v = v || pstride(t) > 0;
+                    static_cast<ConvOp *>(op.get())->viewIO = v;
+                }
                 if (!gapFolded) op->prepare(nd, env_);
                 else op->kind = "folded";
                 if (gapConv.size() && nd.type == OpType::Conv) convOps[i] = static_cast<ConvOp *>(op.get());
@@ -1033,6 +1075,17 @@ namespace vknn {
                 ops_.push_back(std::move(op));
                 // data the op's launches read and write (alias and folded ops launch nothing)
                 std::vector<TensorId> in, out;
+                if (inPlace) {
+                    // no launch, but the dependency chain runs through it (readers of the concat
+                    // output wait for the writers of its slices)
+                    for (TensorId t: nd.inputs)
+                        if (t != kNoTensor) in.push_back(resolve(t));
+                    for (TensorId t: nd.outputs)
+                        if (t != kNoTensor) out.push_back(resolve(t));
+                    ins.push_back(in);
+                    outs.push_back(out);
+                    continue;
+                }
                 if (gapFolded) {
                     // the pool's output stands for the sums the conv's launch writes
                     outs[opPos[gapConv[i]]].push_back(resolve(nd.outputs[0]));
@@ -1212,6 +1265,136 @@ namespace vknn {
             }
         }
 
+        // In-place channel concat and split (no counterpart in the reference, which copies: ops/concat.cpp,
+        // ops/split.cpp). NC4HW4 stores each image as consecutive 4-channel planes, so a channel slice
+        // that starts on a 4-channel boundary is a view: the same buffer at a plane offset, with the
+        // wider tensor's planes per image as its stride. A Concat whose inputs are all such slices
+        // is planned so every producer writes straight into its slice of the concat's buffer, and a
+        // Split so its outputs are views of its input; neither launches anything. Every op that
+        // writes or reads such a view must take plane strides (the conv GEMM and split-K kernels,
+        // add, max pool, resize); a concat or split whose tensors meet any other op keeps its copy.
+        void HipSegment::planViews(const std::vector<int> &idx, const std::set<int> &noWrite, const std::set<int> &noRead) {
+            const Graph &g = g_;
+            std::set<int> inSeg(idx.begin(), idx.end());
+            std::map<TensorId, int>              producer;
+            std::map<TensorId, std::vector<int>> readers;
+            for (size_t i = 0; i < g.nodes.size(); ++i) {
+                const Node &nd = g.nodes[i];
+                for (TensorId t: nd.inputs)
+                    if (t != kNoTensor) readers[t].push_back((int) i);
+                if (nd.fusedResidual != kNoTensor && std::find(nd.inputs.begin(), nd.inputs.end(), nd.fusedResidual) == nd.inputs.end())
+                    readers[nd.fusedResidual].push_back((int) i);
+                for (TensorId t: nd.outputs)
+                    if (t != kNoTensor) producer[t] = (int) i;
+            }
+            std::set<TensorId> gout(g.outputs.begin(), g.outputs.end());
+            auto is4d = [&](TensorId t) { return g.desc(t).shape.size() == 4; };
+            auto chan = [&](TensorId t) { return g.desc(t).shape[1]; };
+            auto axis1 = [&](const Node &nd) {
+                int64_t ax = nd.attr.geti("axis", 0);
+                return ax == 1 || ax == -3;
+            };
+            // candidates: channel concats / splits whose slices all start on a 4-channel boundary
+            std::set<int> cats, splits;
+            for (int i: idx) {
+                const Node &nd = g.nodes[i];
+                if (nd.outputs.empty() || nd.outputs[0] == kNoTensor || !is4d(nd.outputs[0])) continue;
+                if (nd.type == OpType::Concat && axis1(nd) && nd.inputs.size() >= 2) {
+                    bool ok = true;
+                    for (size_t k = 0; k + 1 < nd.inputs.size(); ++k) ok = ok && nd.inputs[k] != kNoTensor && chan(nd.inputs[k]) % 4 == 0;
+                    if (ok) cats.insert(i);
+                }
+                if (nd.type == OpType::Split && axis1(nd) && nd.inputs.size() >= 1 && is4d(nd.inputs[0])) {
+                    bool ok = true;
+                    for (size_t k = 0; k + 1 < nd.outputs.size(); ++k) ok = ok && (nd.outputs[k] == kNoTensor || chan(nd.outputs[k]) % 4 == 0);
+                    if (ok) splits.insert(i);
+                }
+            }
+            auto weightsCin = [&](const Node &nd) { return g.desc(nd.inputs[1]).shape.size() == 4 ? g.desc(nd.inputs[1]).shape[1] : 0; };
+            auto canWrite = [&](int p, const std::set<int> &cs) {
+                const Node &nd = g.nodes[p];
+                if (noWrite.count(p)) return false;
+                switch (nd.type) {
+                    case OpType::Conv: return nd.attr.geti("group", 1) == 1 && nd.fusedResidual == kNoTensor && weightsCin(nd) > 4;
+                    case OpType::Add: return nd.inputs.size() == 2 && g.desc(nd.inputs[0]).shape == g.desc(nd.inputs[1]).shape;
+                    case OpType::MaxPool: case OpType::Resize: return true;
+                    case OpType::Concat: return cs.count(p) > 0; // an in-place concat inside another one
+                    default: return false;
+                }
+            };
+            auto canRead = [&](int c, TensorId t, const std::set<int> &cs, const std::set<int> &ss) {
+                const Node &nd = g.nodes[c];
+                if (!inSeg.count(c) || noRead.count(c)) return false;
+                switch (nd.type) {
+                    case OpType::Conv:
+                        return nd.attr.geti("group", 1) == 1 && nd.inputs[0] == t && nd.fusedResidual != t && weightsCin(nd) > 4 &&
+                               std::count(nd.inputs.begin(), nd.inputs.end(), t) == 1;
+                    case OpType::Add: return nd.inputs.size() == 2 && g.desc(nd.inputs[0]).shape == g.desc(nd.inputs[1]).shape;
+                    case OpType::MaxPool: case OpType::Resize: return true;
+                    case OpType::Concat: return cs.count(c) > 0;
+                    case OpType::Split: return ss.count(c) > 0;
+                    default: return false;
+                }
+            };
+            for (int round = 0; round < 64; ++round) {
+                place_.clear();
+                std::set<int> badCat, badSplit;
+                for (int i: splits) {
+                    const Node &nd = g.nodes[i];
+                    int64_t     c0 = 0;
+                    for (TensorId t: nd.outputs) {
+                        if (t != kNoTensor) place_[t] = {nd.inputs[0], c0 / 4};
+                        c0 += t == kNoTensor ? 0 : chan(t);
+                    }
+                }
+                std::set<TensorId> fromCat; // tensors placed by a concat
+                for (int i: cats) {
+                    const Node &nd = g.nodes[i];
+                    int64_t     off = 0;
+                    for (TensorId t0: nd.inputs) {
+                        TensorId t = t0;
+                        int64_t  o = off;
+                        while (place_.count(t) && !fromCat.count(t)) { // climb from a split output to the split input
+                            o -= place_[t].off;
+                            t = place_[t].parent;
+                        }
+                        auto it = place_.find(t);
+                        const bool clash = (it != place_.end() && (it->second.parent != nd.outputs[0] || it->second.off != o)) || alias_.count(t);
+                        if (o < 0 || clash || !producer.count(t) || !inSeg.count(producer[t]) || gout.count(t)) {
+                            badCat.insert(i);
+                            break;
+                        }
+                        place_[t] = {nd.outputs[0], o};
+                        fromCat.insert(t);
+                        off += chan(t0) / 4;
+                    }
+                }
+                // every tensor that lives in another one: written by a view-capable op, read only by
+                // view-capable ops of this segment, not a graph output
+                for (auto &kv: place_) {
+                    const TensorId t = kv.first;
+                    int            owner = -1; // the concat or split that made it a view
+                    for (int i: cats)
+                        if (g.nodes[i].outputs[0] == kv.second.parent && fromCat.count(t)) owner = i;
+                    const bool splitOut = !fromCat.count(t);
+                    if (splitOut)
+                        for (int i: splits)
+                            if (std::find(g.nodes[i].outputs.begin(), g.nodes[i].outputs.end(), t) != g.nodes[i].outputs.end()) owner = i;
+                    bool ok = !gout.count(t) && !alias_.count(t);
+                    if (!splitOut) ok = ok && producer.count(t) && canWrite(producer[t], cats);
+                    for (int c: readers[t]) ok = ok && canRead(c, t, cats, splits);
+                    if (!ok && owner >= 0) (splitOut ? badSplit : badCat).insert(owner);
+                }
+                // a concat output that is itself placed must come from an in-place concat (checked
+                // above); a split input may be a view itself (nested offsets add up in dev())
+                if (badCat.empty() && badSplit.empty()) break;
+                for (int i: badCat) cats.erase(i);
+                for (int i: badSplit) splits.erase(i);
+            }
+            viewCats_   = cats;
+            viewSplits_ = splits;
+        }
+
         TensorId HipSegment::resolve(TensorId t) const {
             auto it = alias_.find(t);
             while (it != alias_.end()) {
@@ -1222,12 +1405,26 @@ namespace vknn {
         }
 
         void *HipSegment::dev(TensorId t) {
-            auto it = bufs_.find(resolve(t));
+            t       = resolve(t);
+            auto pl = place_.find(t);
+            if (pl != place_.end()) {
+                const Shape &sh = g_.desc(t).shape;
+                return static_cast<char *>(dev(pl->second.parent)) + pl->second.off * sh[2] * sh[3] * 8;
+            }
+            auto it = bufs_.find(t);
             if (it == bufs_.end()) throw Error(Status::RuntimeError, "no device buffer for tensor " + std::to_string(t));
             return it->second->ptr;
         }
 
-        void *SegEnv::dev(TensorId t) { return seg->dev(t); }
+        int64_t HipSegment::pstride(TensorId t) const {
+            t = resolve(t);
+            if (!place_.count(t)) return 0;
+            while (place_.count(t)) t = place_.at(t).parent;
+            return (g_.desc(t).shape[1] + 3) / 4;
+        }
+
+        void   *SegEnv::dev(TensorId t) { return seg->dev(t); }
+        int64_t SegEnv::pstride(TensorId t) { return seg->pstride(t); }
 
         void HipSegment::bindDeviceInput(TensorId t, const float *devNchw) {
             if (extIn_[t] != devNchw || extFmt_.count(t)) {

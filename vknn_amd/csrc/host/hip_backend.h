@@ -33,6 +33,9 @@ namespace vknn {
             bool          tunable = true;
             HipSegment   *seg     = nullptr;
             void         *dev(TensorId t);
+            // channel blocks per image of the buffer t lives in when t is a view into a wider
+            // tensor (a slice of an in-place channel concat or split), 0 when t is dense
+            int64_t       pstride(TensorId t);
         };
 
         // One HIP operator: prepare = classify + prepack/upload weights (+ autotune); record =
@@ -54,6 +57,7 @@ namespace vknn {
             ~HipSegment() override;
             void        run(ExecContext &ctx) override;
             void       *dev(TensorId t);
+            int64_t     pstride(TensorId t) const;
             // Read a boundary input straight from device memory (NCHW fp32) instead of host data.
             void        bindDeviceInput(TensorId t, const float *devNchw);
             // Same, from a declared layout (0 NCHW, 1 NHWC, 2 NC4HW4) and dtype (fp16 or fp32),
@@ -88,6 +92,15 @@ namespace vknn {
             std::vector<std::unique_ptr<HipOp>>            ops_;
             std::map<TensorId, std::shared_ptr<DevBuf>>    bufs_, staging_, outStaging_;
             std::map<TensorId, TensorId>                   alias_;
+            // In-place channel concat / split: tensor -> (the tensor it lives in, its first channel
+            // block there); only the outermost tensor of a chain owns a buffer.
+            struct Place {
+                TensorId parent;
+                int64_t  off;
+            };
+            std::map<TensorId, Place>                      place_;
+            void planViews(const std::vector<int> &idx, const std::set<int> &noWrite, const std::set<int> &noRead);
+            std::set<int>                                  viewCats_, viewSplits_; // concat / split nodes done in place
             std::map<TensorId, const float *>              extIn_;
             std::map<TensorId, std::pair<int, bool>>       extFmt_; // declared (layout, fp16) of a bound input
             struct DmaImport {

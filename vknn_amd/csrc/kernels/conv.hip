@@ -29,7 +29,7 @@ namespace vkhip {
 
     // Split-K reduce: y = act(sum_s part[s] + bias (+res)).
     __global__ void splitk_reduce_kernel(const float4v *part, const float *bias, const uint2 *res, uint2 *y, int ksplit,
-                                         int Coutb, int Cout, int P, int OHW, int act, float lo, float hi, int has_res) {
+                                         int Coutb, int Cout, int P, int OHW, int act, float lo, float hi, int has_res, int ypst) {
         long long idx   = (long long) blockIdx.x * blockDim.x + threadIdx.x;
         long long total = (long long) Coutb * P;
         if (idx >= total) return;
@@ -38,7 +38,7 @@ namespace vkhip {
         float4v v   = *reinterpret_cast<const float4v *>(bias + ocb * 4);
         for (int s = 0; s < ksplit; ++s) v += part[((long long) s * Coutb + ocb) * P + px];
         int       pn = px / OHW, pr = px - pn * OHW;
-        long long yi = ((long long) pn * Coutb + ocb) * OHW + pr;
+        long long yi = ((long long) pn * ypst + ocb) * OHW + pr; // (a residual conv is never a view: ypst == Coutb)
         if (has_res) v += h4_to_f4(u2_as_h4(res[yi]));
         v.x = apply_act(v.x, act, lo, hi);
         v.y = apply_act(v.y, act, lo, hi);
@@ -883,9 +883,21 @@ int vkhip_conv_maxpool_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *
 } // extern "C"
 
 // The forward pass of every conv algorithm; xs is the input scale of an in_scale plan (or null).
+// x_pstride / y_pstride: channel blocks per image of the buffers x and y point into (0: dense, i.e.
+// ceil(Cin/4) / ceil(Cout/4)); larger for views into a wider tensor (a channel slice of a concat).
 static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *xs, const void *blob,
-                             const void *res, void *y, void *workspace, vkhip_stream_t s, void *pool = nullptr) {
+                             const void *res, void *y, void *workspace, vkhip_stream_t s, void *pool = nullptr, int64_t x_pstride = 0,
+                             int64_t y_pstride = 0) {
     if (!d || !plan || !x || !blob || !y) return set_error(VKHIP_ERR_INVALID, "conv_forward: null argument");
+    const int64_t cinb = ceil_div(d->Cin, 4), coutb = ceil_div(d->Cout, 4);
+    const int64_t xps = x_pstride > 0 ? x_pstride : cinb, yps = y_pstride > 0 ? y_pstride : coutb;
+    const bool    dense = xps == cinb && yps == coutb;
+    if (xps < cinb || yps < coutb) return set_error(VKHIP_ERR_INVALID, "conv_forward: plane stride below the channel blocks");
+    if (!dense && (plan->algo == VKHIP_CONV_WINOGRAD || plan->algo == VKHIP_CONV_DEPTHWISE || d->has_res || d->in_scale ||
+                   (plan->tile >= 0 && plan->tile < kNumTiles && kTiles[plan->tile].kind == 4)))
+        return set_error(VKHIP_ERR_UNSUPPORTED, "conv_forward_view: views need a GEMM or split-K plan (not the stem tiles), no residual, no input scale");
+    if ((int64_t) d->N * std::max(xps * d->H * d->W, yps * d->OH * d->OW) * 8 >= (1LL << 31))
+        return set_error(VKHIP_ERR_INVALID, "conv_forward: view >= 2 GiB");
     if (d->has_res && !res) return set_error(VKHIP_ERR_INVALID, "conv_forward: has_res without a residual tensor");
     if (plan->workspace_bytes && !workspace) return set_error(VKHIP_ERR_INVALID, "conv_forward: plan needs a workspace");
     hipStream_t st = resolve_stream(s);
@@ -942,6 +954,8 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
     a.Coutb  = (int) g.Coutb;
     a.Cout   = d->Cout;
     a.P      = (int) g.P;
+    a.x_pstride = (int) g.Cinb;
+    a.y_pstride = (int) g.Coutb;
     a.Pv     = (int) g.Pv;
     a.OHWp   = (int) g.HWp;
     a.Kslots = (int) g.Kslots;
@@ -989,8 +1003,10 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
     a.x  = (const uint2 *) x;
     a.xs = (const uint2 *) xs;
     a.xs_bytes = (unsigned) ((int64_t) d->N * g.Cinb * 8);
-    a.x_bytes = (unsigned) ((int64_t) d->N * g.Cinb * d->H * d->W * 8);
-    a.y_bytes = (unsigned) ((int64_t) d->N * g.Coutb * d->OH * d->OW * 8);
+    a.x_bytes = (unsigned) (((int64_t) (d->N - 1) * xps + g.Cinb) * d->H * d->W * 8);
+    a.y_bytes = (unsigned) (((int64_t) (d->N - 1) * yps + g.Coutb) * d->OH * d->OW * 8);
+    a.x_pstride = (int) xps;
+    a.y_pstride = (int) yps;
     a.y  = (uint2 *) y;
     a.res = (const uint2 *) res;
     a.has_res = d->has_res;
@@ -1010,7 +1026,7 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
         int64_t total = g.Coutb * g.P;
         splitk_reduce_kernel<<<dim3((unsigned) ceil_div(total, 256)), 256, 0, st>>>(
             (const float4v *) workspace, a.bias, a.res, a.y, ks, (int) g.Coutb, d->Cout, (int) g.P, a.OHW, d->act, d->act_lo,
-            d->act_hi, d->has_res);
+            d->act_hi, d->has_res, (int) yps);
         return check_launch("splitk_reduce");
     }
     a.omode = OMODE_EPILOGUE;
@@ -1025,6 +1041,12 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
                        void *y, void *workspace, vkhip_stream_t s) {
     if (d && d->in_scale) return set_error(VKHIP_ERR_INVALID, "conv_forward: an in_scale plan runs through vkhip_conv_forward_scaled");
     return conv_forward_impl(d, plan, x, nullptr, blob, res, y, workspace, s);
+}
+
+int vkhip_conv_forward_view(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, int64_t x_pstride, const void *blob, void *y,
+                            int64_t y_pstride, void *workspace, vkhip_stream_t s) {
+    if (d && d->in_scale) return set_error(VKHIP_ERR_INVALID, "conv_forward_view: no input-scale plans");
+    return conv_forward_impl(d, plan, x, nullptr, blob, nullptr, y, workspace, s, nullptr, x_pstride, y_pstride);
 }
 
 int vkhip_conv_pool_parts(const vkhip_conv_desc *d, const vkhip_conv_plan *plan) {

@@ -53,6 +53,8 @@ namespace vkhip {
         unsigned      y_bytes;                         // bytes of one batch slice of y (< 2 GiB)
         const uint2  *xs;                              // input channel scale [N][Cinb] x 4 fp16 (in_scale)
         unsigned      xs_bytes;                        // bytes of xs
+        int           x_pstride, y_pstride;            // channel blocks per image of the buffers x / y point into
+                                                       // (Cinb / Coutb, or more for a view into a wider tensor)
     };
 
     enum { OMODE_EPILOGUE = 0, OMODE_RAW = 1, OMODE_PARTIAL = 2 };
@@ -153,7 +155,7 @@ namespace vkhip {
             piy[i]       = oy * a.SH - a.PT;
             pix[i]       = ox * a.SW - a.PL;
             // byte offset of (n, channel block 0, iy0, ix0); x slices are < 2 GiB
-            pbyte[i] = (n * a.Cinb * a.HW + piy[i] * a.W + pix[i]) * 8;
+            pbyte[i] = (n * a.x_pstride * a.HW + piy[i] * a.W + pix[i]) * 8;
         }
 
         const int ks_begin = split * a.steps_per_split;
@@ -389,7 +391,7 @@ namespace vkhip {
                     const int ocb = (m0 + wm0 + i * 32 + qq * 8 + lk * 4) >> 2;
                     const bool ok = pok & (ocb < a.Coutb);
                     if (a.omode == OMODE_PARTIAL) yoff[j][i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + px) * 16) : kInvalid;
-                    else yoff[j][i][qq] = ok ? (unsigned) (((pn * a.Coutb + ocb) * a.OHW + pr) * 8) : kInvalid;
+                    else yoff[j][i][qq] = ok ? (unsigned) (((pn * a.y_pstride + ocb) * a.OHW + pr) * 8) : kInvalid;
                 }
         }
         if (a.omode == OMODE_PARTIAL) {
@@ -550,7 +552,7 @@ namespace vkhip {
                             const bool ok  = pok & (ocb < a.Coutb);
                             if constexpr (MODE == 0)
                                 yoff[b][jj][i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + pn * a.OHW + pr) * 16) : kInvalid;
-                            else yoff[b][jj][i][qq] = ok ? (unsigned) (((pn * a.Coutb + ocb) * a.OHW + pr) * 8) : kInvalid;
+                            else yoff[b][jj][i][qq] = ok ? (unsigned) (((pn * a.y_pstride + ocb) * a.OHW + pr) * 8) : kInvalid;
                             if constexpr (MODE == 3) rv[b][jj][i][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[b][jj][i][qq], 0, 0);
                         }
                 }
@@ -680,7 +682,7 @@ namespace vkhip {
             const int ox = r - oy * a.OW;
             piy[j]       = oy * a.SH - a.PT;
             pix[j]       = ox * a.SW - a.PL;
-            pbase[j]     = (unsigned) ((n * a.Cinb * a.HW + piy[j] * a.W + pix[j]) * 8 + lead + 2 * g * hw8);
+            pbase[j]     = (unsigned) ((n * a.x_pstride * a.HW + piy[j] * a.W + pix[j]) * 8 + lead + 2 * g * hw8);
             tapok[j]     = 0;
             if constexpr (BMODE == BMODE_ALIGNED) {
                 for (int t = 0; t < a.Kslots / a.Cinb; ++t) {
@@ -910,13 +912,13 @@ namespace vkhip {
             if constexpr (PS == 8) {
                 const int p = n0 + pb * 128 + 2 * lane;
                 const int n = p / a.OHWp;
-                pbase[pb]   = p < a.Pv ? (unsigned) ((n * a.Cinb * a.HW + (p - n * a.OHWp)) * 8) : kInvalid;
+                pbase[pb]   = p < a.Pv ? (unsigned) ((n * a.x_pstride * a.HW + (p - n * a.OHWp)) * 8) : kInvalid;
             } else {
                 const int p  = n0 + pb * 64 + lane;
                 const int n  = p / a.OHW;
                 const int r  = p - n * a.OHW;
                 const int oy = r / a.OW;
-                pbase[pb]    = p < a.P ? (unsigned) ((n * a.Cinb * a.HW + (a.SH * oy) * a.W + a.SW * (r - oy * a.OW)) * 8) : kInvalid;
+                pbase[pb]    = p < a.P ? (unsigned) ((n * a.x_pstride * a.HW + (a.SH * oy) * a.W + a.SW * (r - oy * a.OW)) * 8) : kInvalid;
             }
         }
         // XS: images n_first .. n_first+7 of the scale table; lane l copies image n_first + l/8
@@ -1129,7 +1131,7 @@ namespace vkhip {
             const int n    = nf + vabs / (H + 2);
             const int iy   = vabs % (H + 2) - 1;
             const bool ok  = 2 * pc < W && iy >= 0 && iy < H && n < NI && vrow < nrows;
-            bsrc[i]        = ok ? (unsigned) (((n * a.Cinb) * HW + iy * W + 2 * pc) * 8) : kInvalid;
+            bsrc[i]        = ok ? (unsigned) (((n * a.x_pstride) * HW + iy * W + 2 * pc) * 8) : kInvalid;
         }
         const unsigned hw8 = (unsigned) HW * 8u;
         auto issue = [&](int ks, int buf) __attribute__((always_inline)) {

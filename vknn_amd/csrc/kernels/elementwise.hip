@@ -3,6 +3,7 @@
 // pool, the fused SE middle, max pool, channel concat/slice and nearest resize. All are coalesced
 // wave64 kernels over 8- or 16-byte vectors; none uses MFMA.
 #include "common.h"
+#include <algorithm>
 #include <cstring>
 
 namespace vkhip {
@@ -228,14 +229,17 @@ namespace vkhip {
 
     // Max pool over NC4HW4; out-of-image taps are skipped (reference maxpool.cpp semantics).
     template <typename I>
-    __global__ void maxpool_kernel(vkhip_pool_desc d, const uint2 *x, uint2 *y, I total) {
+    // xps / yps: channel blocks per image of the buffers x and y point into (a view of a wider
+    // tensor, e.g. a slice of a channel concat; equal to ceil(C/4) for a dense tensor)
+    __global__ void maxpool_kernel(vkhip_pool_desc d, const uint2 *x, uint2 *y, I total, int Cb, int xps, int yps) {
         I i = (I) blockIdx.x * blockDim.x + threadIdx.x;
         if (i >= total) return;
         int ox = (int) (i % (I) d.OW);
         I   t  = i / (I) d.OW;
         int oy = (int) (t % (I) d.OH);
         I   nc = t / (I) d.OH;
-        const uint2 *src = x + (int64_t) nc * d.H * d.W;
+        const I n = nc / Cb, cb = nc - n * Cb;
+        const uint2 *src = x + ((int64_t) n * xps + cb) * d.H * d.W;
         float4v m = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
         for (int ky = 0; ky < d.KH; ++ky) {
             int iy = oy * d.SH - d.PT + ky;
@@ -250,7 +254,7 @@ namespace vkhip {
                 m.w = fmaxf(m.w, v.w);
             }
         }
-        y[i] = h4_as_u2(f4_to_h4(m));
+        y[(((int64_t) n * yps + cb) * d.OH + oy) * d.OW + ox] = h4_as_u2(f4_to_h4(m));
     }
 
     // 3x3 stride-2 max pool with pad 1 on the left/top (the ResNet stem pool), even W. One thread
@@ -354,15 +358,32 @@ namespace vkhip {
         for (int64_t c = C; c < Cb * 4; ++c) y[((n * Cb + c / 4) * HW + p) * 4 + (c & 3)] = (half_t) 0.f;
     }
 
-    __global__ void resize_nearest_kernel(const uint2 *x, uint2 *y, int64_t H, int64_t W, int64_t OH, int64_t OW, int64_t total) {
+    __global__ void resize_nearest_kernel(const uint2 *x, uint2 *y, int64_t H, int64_t W, int64_t OH, int64_t OW, int64_t total, int64_t Cb,
+                                          int64_t xps, int64_t yps) {
         int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
         if (i >= total) return;
         int64_t ox = i % OW;
         int64_t t  = i / OW;
         int64_t oy = t % OH;
         int64_t nc = t / OH;
+        int64_t n = nc / Cb, cb = nc - n * Cb;
         int64_t iy = (oy * H) / OH, ix = (ox * W) / OW;
-        y[i]       = x[(nc * H + iy) * W + ix];
+        y[((n * yps + cb) * OH + oy) * OW + ox] = x[((n * xps + cb) * H + iy) * W + ix];
+    }
+
+    // y = act(a + b) over one image per blockIdx.y: `per` contiguous halves of each image, the
+    // images `aps` / `bps` / `yps` halves apart (views of wider tensors)
+    __global__ void add_view_kernel(const half_t *a, int64_t aps, const half_t *b, int64_t bps, half_t *y, int64_t yps, int64_t per, int act,
+                                    float lo, float hi) {
+        const int64_t n = blockIdx.y;
+        const int64_t i = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) * 4;
+        if (i >= per) return;
+        const half4 va = *reinterpret_cast<const half4 *>(a + n * aps + i);
+        const half4 vb = *reinterpret_cast<const half4 *>(b + n * bps + i);
+        half4       r;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r[k] = (half_t) apply_act((float) va[k] + (float) vb[k], act, lo, hi);
+        *reinterpret_cast<half4 *>(y + n * yps + i) = r;
     }
 
     static dim3 grid1(int64_t n, int bs = 256) { return dim3((unsigned) ceil_div(n, bs)); }
@@ -514,12 +535,24 @@ int vkhip_fused_se_pooled(const void *part, int32_t R, int64_t HW, const void *b
     return vkhip_fc(workspace, (const char *) blob + se_w2_offset(C, Cr), y, N, Cr, C, VKHIP_ACT_HARDSIGMOID, alpha, beta, s);
 }
 
-int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s) {
+static int maxpool_impl(const vkhip_pool_desc *d, const void *x, int64_t xps, void *y, int64_t yps, vkhip_stream_t s);
+
+int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s) { return maxpool_impl(d, x, 0, y, 0, s); }
+
+int vkhip_maxpool_view(const vkhip_pool_desc *d, const void *x, int64_t x_pstride, void *y, int64_t y_pstride, vkhip_stream_t s) {
+    return maxpool_impl(d, x, x_pstride, y, y_pstride, s);
+}
+
+static int maxpool_impl(const vkhip_pool_desc *d, const void *x, int64_t xps_, void *y, int64_t yps_, vkhip_stream_t s) {
     if (!d || !x || !y || d->N <= 0 || d->C <= 0 || d->OH <= 0 || d->OW <= 0 || d->KH <= 0 || d->KW <= 0 || d->SH <= 0 || d->SW <= 0)
         return set_error(VKHIP_ERR_INVALID, "maxpool: bad arguments");
+    const int Cb  = (int) ceil_div(d->C, 4);
+    const int xps = xps_ > 0 ? (int) xps_ : Cb, yps = yps_ > 0 ? (int) yps_ : Cb;
+    if (xps < Cb || yps < Cb) return set_error(VKHIP_ERR_INVALID, "maxpool: plane stride below the channel blocks");
+    const bool dense = xps == Cb && yps == Cb;
     // the stem pool shape: 3x3 stride 2, pad 1 left/top, even W (pixel pairs 16-byte aligned), and
     // the output width the padding implies (right pad 0 or 1)
-    if (d->KH == 3 && d->KW == 3 && d->SH == 2 && d->SW == 2 && d->PT == 1 && d->PL == 1 && d->W % 2 == 0 && d->OW == d->W / 2 &&
+    if (dense && d->KH == 3 && d->KW == 3 && d->SH == 2 && d->SW == 2 && d->PT == 1 && d->PL == 1 && d->W % 2 == 0 && d->OW == d->W / 2 &&
         d->OH <= (d->H + 1) / 2 + 1 && d->OH >= 1) {
         const int     OHq = (d->OH + 1) / 2, OWq = (d->OW + 1) / 2;
         const int64_t tq  = (int64_t) d->N * ceil_div(d->C, 4) * OHq * OWq;
@@ -532,10 +565,10 @@ int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream
         return check_launch("maxpool");
     }
     int64_t total = (int64_t) d->N * ceil_div(d->C, 4) * d->OH * d->OW;
-    if ((int64_t) d->N * ceil_div(d->C, 4) * d->H * d->W < INT32_MAX)
-        maxpool_kernel<int><<<grid1(total), 256, 0, resolve_stream(s)>>>(*d, (const uint2 *) x, (uint2 *) y, (int) total);
+    if ((int64_t) d->N * std::max(xps, yps) * std::max(d->H * d->W, d->OH * d->OW) < INT32_MAX)
+        maxpool_kernel<int><<<grid1(total), 256, 0, resolve_stream(s)>>>(*d, (const uint2 *) x, (uint2 *) y, (int) total, Cb, xps, yps);
     else
-        maxpool_kernel<int64_t><<<grid1(total), 256, 0, resolve_stream(s)>>>(*d, (const uint2 *) x, (uint2 *) y, total);
+        maxpool_kernel<int64_t><<<grid1(total), 256, 0, resolve_stream(s)>>>(*d, (const uint2 *) x, (uint2 *) y, total, Cb, xps, yps);
     return check_launch("maxpool");
 }
 
@@ -582,11 +615,30 @@ int vkhip_slice_channels(const void *x, void *y, int64_t N, int64_t Cx, int64_t 
     return check_launch("slice_tail");
 }
 
-int vkhip_resize_nearest(const void *x, void *y, int64_t N, int64_t C, int64_t H, int64_t W, int64_t OH, int64_t OW, vkhip_stream_t s) {
+int vkhip_resize_nearest_view(const void *x, int64_t x_pstride, void *y, int64_t y_pstride, int64_t N, int64_t C, int64_t H, int64_t W,
+                              int64_t OH, int64_t OW, vkhip_stream_t s) {
     if (!x || !y || N <= 0 || C <= 0 || H <= 0 || W <= 0 || OH <= 0 || OW <= 0) return set_error(VKHIP_ERR_INVALID, "resize: bad arguments");
-    int64_t total = N * ceil_div(C, 4) * OH * OW;
-    resize_nearest_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, H, W, OH, OW, total);
+    const int64_t Cb = ceil_div(C, 4), xps = x_pstride > 0 ? x_pstride : Cb, yps = y_pstride > 0 ? y_pstride : Cb;
+    if (xps < Cb || yps < Cb) return set_error(VKHIP_ERR_INVALID, "resize: plane stride below the channel blocks");
+    int64_t total = N * Cb * OH * OW;
+    resize_nearest_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, H, W, OH, OW, total, Cb, xps, yps);
     return check_launch("resize_nearest");
+}
+
+int vkhip_resize_nearest(const void *x, void *y, int64_t N, int64_t C, int64_t H, int64_t W, int64_t OH, int64_t OW, vkhip_stream_t s) {
+    return vkhip_resize_nearest_view(x, 0, y, 0, N, C, H, W, OH, OW, s);
+}
+
+int vkhip_add_view(const void *a, int64_t a_pstride, const void *b, int64_t b_pstride, void *y, int64_t y_pstride, int64_t N, int64_t C,
+                   int64_t HW, int32_t act, float lo, float hi, vkhip_stream_t s) {
+    if (!a || !b || !y || N <= 0 || C <= 0 || HW <= 0 || N > 65535) return set_error(VKHIP_ERR_INVALID, "add_view: bad arguments");
+    const int64_t Cb = ceil_div(C, 4), per = Cb * HW * 4;
+    const int64_t aps = (a_pstride > 0 ? a_pstride : Cb) * HW * 4, bps = (b_pstride > 0 ? b_pstride : Cb) * HW * 4,
+                  yps = (y_pstride > 0 ? y_pstride : Cb) * HW * 4;
+    if (aps < per || bps < per || yps < per) return set_error(VKHIP_ERR_INVALID, "add_view: plane stride below the channel blocks");
+    add_view_kernel<<<dim3((unsigned) ceil_div(per / 4, 256), (unsigned) N), 256, 0, resolve_stream(s)>>>(
+        (const half_t *) a, aps, (const half_t *) b, bps, (half_t *) y, yps, per, act, lo, hi);
+    return check_launch("add_view");
 }
 
 } // extern "C"
