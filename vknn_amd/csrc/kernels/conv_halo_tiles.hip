@@ -1,4 +1,4 @@
-// Tile instantiations of conv_halo_kernel (tiles 17-20, 26, 27: 3x3 with the input band staged once).
+// Tile instantiations of conv_halo_kernel (tiles 17-20, 26, 27, 32, 33: 3x3 with the input band staged once).
 #include "conv_kernels.h"
 
 namespace vkhip {
@@ -21,6 +21,8 @@ namespace vkhip {
             case 20: return pick_halo<2, 1, 1, 4, 1, 1, 1, 2, 3, 4, 5, 6, 8, 10, 12, 16>(nbi);
             case 26: return pick_halo<2, 1, 1, 4, 1, 2, 1, 2, 3, 4, 5, 6, 8>(nbi);
             case 27: return pick_halo<2, 2, 1, 4, 1, 1, 2, 4, 6, 8, 10, 12, 15>(nbi);
+            case 32: return pick_halo<1, 2, 1, 4, 1, 2, 1, 2, 3, 4, 5, 6, 8, 10, 12, 15>(nbi);
+            case 33: return pick_halo<1, 1, 1, 4, 1, 2, 1, 2, 3, 4, 5, 6, 8>(nbi);
         }
         return nullptr;
     }

@@ -1432,9 +1432,11 @@ namespace vkhip {
         {128, 128, 2, 2, 2, 2, 2},    // 29 tile 14 with a 3-stage ring
         {64, 256, 1, 4, 2, 2, 2},     // 30 tile 25 with a 3-stage ring
         {64, 128, 2, 2, 2, 1, 2},     // 31 tile 24 with a 4-stage ring
+        {32, 256, 1, 4, 3, 1, 2, 1},  // 32 halo for few output channels (2-stage ring)
+        {32, 128, 1, 4, 3, 1, 1, 1},  // 33 halo for few output channels, small bands (2-stage ring)
     };
-    constexpr int kNumTiles = 32;
-    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8, 15, 0, 0, 0, 0};
+    constexpr int kNumTiles = 34;
+    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8, 15, 0, 0, 0, 0, 15, 8};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
