@@ -121,7 +121,7 @@ def test_conv_auto(gpu, case):
 NUM_TILES = V.vkhip().vkhip_conv_tile_count()
 BD_TILES = [8, 9, 10]            # conv_bd_kernel tiles (A via LDS DMA, B gathered into registers)
 DMA_TILES = [11, 12, 13, 14, 15, 16, 24, 25, 28, 29, 30, 31]    # conv_dma_kernel tiles (A and B via LDS DMA; dense B only)
-HALO_TILES = [17, 18, 19, 20, 26, 27, 32, 33]      # conv_halo_kernel tiles (3x3 s1 p1: input band staged once for all taps)
+HALO_TILES = [17, 18, 19, 20, 26, 27, 32, 33, 34, 35]      # conv_halo_kernel tiles (3x3 s1 p1: input band staged once for all taps)
 STEM_TILES = [21, 22, 23]                 # conv_stem_kernel tiles (3x3/7x7 over at most 4 input channels)
 GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES + HALO_TILES + STEM_TILES]
 

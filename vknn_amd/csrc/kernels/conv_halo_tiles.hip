@@ -1,4 +1,4 @@
-// Tile instantiations of conv_halo_kernel (tiles 17-20, 26, 27, 32, 33: 3x3 with the input band staged once).
+// Tile instantiations of conv_halo_kernel (tiles 17-20, 26, 27, 32-35: 3x3 with the input band staged once).
 #include "conv_kernels.h"
 
 namespace vkhip {
@@ -23,6 +23,8 @@ namespace vkhip {
             case 27: return pick_halo<2, 2, 1, 4, 1, 1, 2, 4, 6, 8, 10, 12, 15>(nbi);
             case 32: return pick_halo<1, 2, 1, 4, 1, 2, 1, 2, 3, 4, 5, 6, 8, 10, 12, 15>(nbi);
             case 33: return pick_halo<1, 1, 1, 4, 1, 2, 1, 2, 3, 4, 5, 6, 8>(nbi);
+            case 34: return pick_halo<1, 2, 1, 4, 1, 1, 2, 4, 6, 8, 10, 12, 16>(nbi);
+            case 35: return pick_halo<1, 1, 1, 4, 1, 1, 2, 4, 6, 8, 10>(nbi);
         }
         return nullptr;
     }

@@ -1434,9 +1434,11 @@ namespace vkhip {
         {64, 128, 2, 2, 2, 1, 2},     // 31 tile 24 with a 4-stage ring
         {32, 256, 1, 4, 3, 1, 2, 1},  // 32 halo for few output channels (2-stage ring)
         {32, 128, 1, 4, 3, 1, 1, 1},  // 33 halo for few output channels, small bands (2-stage ring)
+        {32, 256, 1, 4, 3, 1, 2, 1},  // 34 tile 32 with one stage (single-stage reductions: more workgroups per CU)
+        {32, 128, 1, 4, 3, 1, 1, 1},  // 35 tile 33 with one stage
     };
-    constexpr int kNumTiles = 34;
-    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8, 15, 0, 0, 0, 0, 15, 8};
+    constexpr int kNumTiles = 36;
+    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8, 15, 0, 0, 0, 0, 15, 8, 16, 10};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
