@@ -116,6 +116,72 @@ CPU_CONFIGS = [("conv3x3_bn_relu", "config 0"), ("mnv2_block", "config 1"), ("re
                ("mobilenetv3_large", "config 3"), ("yolov8n", "config 4")]
 
 
+def winograd_stages(batch, launches=20):
+    """The three Winograd F(2x2,3x3) stages of ResNet-50's four 3x3 stride-1 conv shapes at this
+    batch, each timed on its own (vkhip_conv_forward_stages) with HIP events around `launches`
+    back-to-back launches. The transforms are HBM-bound: input transform reads x and writes the
+    16 V planes, output transform reads the 16 M planes (and the residual) and writes y, all fp16.
+    The GEMM stage does 16 batched Cout x Cin x tiles GEMMs."""
+    import vknn_amd as V
+    lib = V.vkhip()
+    rng = np.random.default_rng(11)
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    V.check(lib.vkhip_event_create(ctypes.byref(e0)))
+    V.check(lib.vkhip_event_create(ctypes.byref(e1)))
+    rows, tot = [], {"in": [0.0, 0], "out": [0.0, 0], "gemm": [0.0, 0]}
+    for C, H in ((64, 56), (128, 28), (256, 14), (512, 7)):
+        d = V.ConvDesc(N=batch, Cin=C, H=H, W=H, Cout=C, OH=H, OW=H, KH=3, KW=3, SH=1, SW=1, PT=1, PL=1, DH=1, DW=1,
+                       group=1, act=1, act_lo=0.0, act_hi=0.0, has_res=1)
+        plan = V.ConvPlan()
+        V.check(lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_WINOGRAD, -1, 0, ctypes.byref(plan)), "winograd plan")
+        w = (rng.standard_normal((C, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+        b = (rng.standard_normal(C) * 0.1).astype(np.float32)
+        blob = np.zeros(plan.weight_bytes, np.uint8)
+        V.check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(plan), w.ctypes.data, b.ctypes.data, blob.ctypes.data))
+        act_bytes = V.nc4_elems(batch, C, H, H) * 2
+        xb = V.DeviceBuffer.from_array(rng.standard_normal(act_bytes // 2).astype(np.float16))
+        rb = V.DeviceBuffer.from_array(rng.standard_normal(act_bytes // 2).astype(np.float16))
+        yb = V.DeviceBuffer(act_bytes)
+        wb = V.DeviceBuffer.from_array(blob)
+        ws = V.DeviceBuffer(plan.workspace_bytes)
+        nT = batch * ((H + 1) // 2) ** 2
+        planes = 16 * ((C + 3) // 4) * nT * 8  # the 16 V (or M) planes, fp16 x 4 channels
+        row = {"shape": f"{C}->{C} 3x3 at {H}x{H}, b{batch}", "tiles": nT}
+        for name, mask, nbytes, flops in (("in", 1, act_bytes + planes, 0), ("gemm", 2, 0, 2 * 16 * C * C * nT),
+                                          ("out", 4, planes + 2 * act_bytes, 0)):
+            args = (ctypes.byref(d), ctypes.byref(plan), xb.ptr, wb.ptr, rb.ptr, yb.ptr, ws.ptr)
+            for _ in range(3):
+                V.check(lib.vkhip_conv_forward_stages(*args, 7, None))
+            V.check(lib.vkhip_event_record(e0, None))
+            for _ in range(launches):
+                V.check(lib.vkhip_conv_forward_stages(*args, mask, None))
+            V.check(lib.vkhip_event_record(e1, None))
+            V.check(lib.vkhip_stream_sync(None))
+            ms = ctypes.c_float()
+            V.check(lib.vkhip_event_elapsed_ms(e0, e1, ctypes.byref(ms)))
+            us = ms.value * 1e3 / launches
+            row[name + "_us"] = round(us, 2)
+            if nbytes:
+                row[name + "_GBs"] = round(nbytes / us / 1e3, 1)
+                tot[name][0] += us; tot[name][1] += nbytes
+            else:
+                row["gemm_TFLOPs"] = round(flops / us / 1e6, 1)
+                tot[name][0] += us; tot[name][1] += flops
+        rows.append(row)
+        for buf in (xb, rb, yb, wb, ws):
+            buf.close()
+    lib.vkhip_event_destroy(e0)
+    lib.vkhip_event_destroy(e1)
+    tb = tot["in"][1] + tot["out"][1]
+    tu = tot["in"][0] + tot["out"][0]
+    return {"workload": f"ResNet-50 3x3 stride-1 shapes at b{batch}, forced winograd, {launches} launches per stage",
+            "transforms_achieved_GBs": round(tb / tu / 1e3, 1), "peak_GBs": PEAK_HBM_GBS,
+            "transforms_frac": round(tb / tu / 1e3 / PEAK_HBM_GBS, 4),
+            "input_frac": round(tot["in"][1] / tot["in"][0] / 1e3 / PEAK_HBM_GBS, 4),
+            "output_frac": round(tot["out"][1] / tot["out"][0] / 1e3 / PEAK_HBM_GBS, 4),
+            "gemm_TFLOPs": round(tot["gemm"][1] / tot["gemm"][0] / 1e6, 1), "shapes": rows}
+
+
 def _cpu_model():
     try:
         for ln in open("/proc/cpuinfo"):
@@ -339,6 +405,10 @@ def main():
                                    "frac_of_step_time": round(f_bytes / (f_ms * fscale * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                                    "execution": [ln for ln in fplan.splitlines() if "[dwpw]" in ln]}
         xd.close()
+
+    # ---- Winograd transforms (the tuner rarely picks Winograd on these shapes; forced here)
+    if not args.no_profile:
+        extra["winograd"] = winograd_stages(args.batch)
 
     # ---- every config at its two batch sizes (img/s and TFLOP/s of whole forward passes, the
     # default session options; the headline config is the line's value)

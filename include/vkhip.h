@@ -178,6 +178,15 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
 int vkhip_conv_forward_scaled(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *xs,
                               const void *blob, const void *res, void *y, void *workspace, vkhip_stream_t s);
 
+/* vkhip_conv_forward running only some stages of a Winograd plan, for timing each kernel on its
+ * own: `stages` is a mask, 1 = input transform (x -> V in the workspace), 2 = the 16 batched
+ * GEMMs (V -> M), 4 = output transform (M -> y, with bias, residual and activation); 7 runs the
+ * whole conv and is the only mask other plans accept. Stages read what earlier calls left in the
+ * workspace. No counterpart in the reference (its Winograd records the three dispatches together,
+ * src/backend/vulkan/ops/conv.cpp; for reports and tests only). */
+int vkhip_conv_forward_stages(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res,
+                              void *y, void *workspace, int stages, vkhip_stream_t s);
+
 /* vkhip_conv_forward without a workspace argument and without any allocation: the split-K
  * partials or Winograd V/M planes go to a fixed device-resident scratch array of
  * VKHIP_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends. No counterpart in the

@@ -437,6 +437,33 @@ def test_conv_winograd_residual(gpu, shape):
     assert_parity(got, oracle_conv(x, w, b, (1, 1), (1, 1, 1, 1), res=res, act=5), f"winograd+res {shape}")
 
 
+def test_conv_winograd_stages(gpu):
+    """The three Winograd stages run one call each (vkhip_conv_forward_stages, masks 1, 2, 4) leave
+    the same bits as the whole conv; a non-Winograd plan refuses a partial mask."""
+    N, C, H, W, Cout = 2, 64, 14, 14, 64
+    r = rng(77)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    res = round_half(r.standard_normal((N, Cout, H, W)))
+    whole, plan, _ = gpu_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=1, res=res, algo=V.CONV_WINOGRAD)
+    assert plan.algo == V.CONV_WINOGRAD
+    lib = V.vkhip()
+    d, yshape = conv_desc(x.shape, w.shape, (1, 1), (1, 1, 1, 1), act=1, has_res=1)
+    blob = np.zeros(plan.weight_bytes, np.uint8)
+    check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(plan), w.ctypes.data, b.ctypes.data, blob.ctypes.data), "pack")
+    dblob, dx, dres = DeviceBuffer.from_array(blob), to_device_nc4(x), to_device_nc4(res)
+    dy, ws = DeviceBuffer(V.nc4_elems(*yshape) * 2), DeviceBuffer(plan.workspace_bytes)
+    dy.zero()
+    for m in (1, 2, 4):
+        check(lib.vkhip_conv_forward_stages(ctypes.byref(d), ctypes.byref(plan), dx.ptr, dblob.ptr, dres.ptr, dy.ptr, ws.ptr, m, None), f"stage {m}")
+    check(lib.vkhip_stream_sync(None), "sync")
+    assert np.array_equal(from_device_nc4(dy, yshape), whole)
+    gplan = V.ConvPlan()
+    check(lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, -1, 0, ctypes.byref(gplan)), "gemm plan")
+    assert lib.vkhip_conv_forward_stages(ctypes.byref(d), ctypes.byref(gplan), dx.ptr, dblob.ptr, dres.ptr, dy.ptr, ws.ptr, 1, None) != 0
+
+
 def test_conv_dilation(gpu):
     r = rng(40)
     x = round_half(r.standard_normal((1, 16, 15, 15)))

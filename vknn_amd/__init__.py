@@ -93,6 +93,7 @@ VKHIP_API = {
     "vkhip_conv_pack_weights": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp]),
     "vkhip_conv_forward": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_forward_noalloc": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "vkhip_conv_forward_stages": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp]),
     "vkhip_conv_forward_scaled": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_pool_parts": (c_int, [P(ConvDesc), P(ConvPlan)]),
     "vkhip_conv_forward_view": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp]),

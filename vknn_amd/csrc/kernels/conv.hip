@@ -887,7 +887,7 @@ int vkhip_conv_maxpool_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *
 // ceil(Cin/4) / ceil(Cout/4)); larger for views into a wider tensor (a channel slice of a concat).
 static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *xs, const void *blob,
                              const void *res, void *y, void *workspace, vkhip_stream_t s, void *pool = nullptr, int64_t x_pstride = 0,
-                             int64_t y_pstride = 0) {
+                             int64_t y_pstride = 0, int stages = 7) {
     if (!d || !plan || !x || !blob || !y) return set_error(VKHIP_ERR_INVALID, "conv_forward: null argument");
     const int64_t cinb = ceil_div(d->Cin, 4), coutb = ceil_div(d->Cout, 4);
     const int64_t xps = x_pstride > 0 ? x_pstride : cinb, yps = y_pstride > 0 ? y_pstride : coutb;
@@ -976,9 +976,11 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
         uint2    *V   = (uint2 *) workspace;
         uint2    *M   = (uint2 *) ((char *) workspace + align256((size_t) 16 * g.Cinb * nT * 8));
         int64_t   nin = g.Cinb * nT;
-        wino_input_kernel<<<dim3((unsigned) ceil_div(nin, 256)), 256, 0, st>>>((const uint2 *) x, V, (int) g.Cinb, d->H, d->W, nTH, nTW, nT);
-        int rc = check_launch("wino_input");
-        if (rc) return rc;
+        int rc = 0;
+        if (stages & 1) {
+            wino_input_kernel<<<dim3((unsigned) ceil_div(nin, 256)), 256, 0, st>>>((const uint2 *) x, V, (int) g.Cinb, d->H, d->W, nTH, nTW, nT);
+            if ((rc = check_launch("wino_input"))) return rc;
+        }
         a.x = V;
         a.x_bytes = (unsigned) (g.Cinb * nT * 8);
         a.y_bytes = (unsigned) (g.Coutb * nT * 8);
@@ -991,8 +993,11 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
         a.w_bstride = (long long) g.Coutp * g.Kp;
         a.y_bstride = (long long) g.Coutb * nT;
         dim3 grid((unsigned) (g.m_tiles * g.n_tiles), 1, 16);
-        fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
-        if ((rc = check_launch("wino_gemm"))) return rc;
+        if (stages & 2) {
+            fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
+            if ((rc = check_launch("wino_gemm"))) return rc;
+        }
+        if (!(stages & 4)) return VKHIP_OK;
         int64_t nout = g.Coutb * nT;
         wino_output_kernel<<<dim3((unsigned) ceil_div(nout, 256)), 256, 0, st>>>(M, a.bias, d->has_res ? (const uint2 *) res : nullptr, (uint2 *) y,
                                                                                (int) g.Coutb, d->Cout, d->OH, d->OW,
@@ -1041,6 +1046,15 @@ int vkhip_conv_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, co
                        void *y, void *workspace, vkhip_stream_t s) {
     if (d && d->in_scale) return set_error(VKHIP_ERR_INVALID, "conv_forward: an in_scale plan runs through vkhip_conv_forward_scaled");
     return conv_forward_impl(d, plan, x, nullptr, blob, res, y, workspace, s);
+}
+
+int vkhip_conv_forward_stages(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res,
+                              void *y, void *workspace, int stages, vkhip_stream_t s) {
+    if (!plan || stages < 1 || stages > 7) return set_error(VKHIP_ERR_INVALID, "conv_forward_stages: stages is a mask of 1..7");
+    if (plan->algo != VKHIP_CONV_WINOGRAD && stages != 7)
+        return set_error(VKHIP_ERR_INVALID, "conv_forward_stages: only a Winograd plan runs part of its stages");
+    if (d && d->in_scale) return set_error(VKHIP_ERR_INVALID, "conv_forward_stages: no input-scale plans");
+    return conv_forward_impl(d, plan, x, nullptr, blob, res, y, workspace, s, nullptr, 0, 0, stages);
 }
 
 int vkhip_conv_forward_view(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, int64_t x_pstride, const void *blob, void *y,
