@@ -93,14 +93,17 @@ int vknn_session_create_onnx(const char *path, const char *options, vknn_session
  * "cache_file=<path>" (and cache_mode tune or full, the default full) merges the file's table
  * before compiling and writes it back afterwards when it changed. These calls reach the same
  * process-wide table directly; none needs a device.
- *   load: merge a file's entries (once per path), returns the number read (0 if absent/unknown)
- *   save: write the table (untouched when the bytes are unchanged); get: 0 found, 1 absent */
+ *   load: merge a file's entries (once per path), returns the number of tune entries read (0 if
+ *         absent/unknown); its prepacked weight blobs are kept too, as with CacheMode::Full
+ *   save: write the table and the weight blobs (untouched when the bytes are unchanged);
+ *   get: 0 found, 1 absent; weight_cache_stats: blobs held, and lookups that found / missed one */
 int vknn_tune_cache_load(const char *path);
 int vknn_tune_cache_save(const char *path);
 int vknn_tune_cache_put(const char *key, int32_t value);
 int vknn_tune_cache_get(const char *key, int32_t *value);
 int vknn_tune_cache_clear(void);
 int vknn_tune_cache_stats(int64_t *entries, int64_t *hits, int64_t *misses);
+int vknn_weight_cache_stats(int64_t *entries, int64_t *hits, int64_t *misses);
 /* The key namespace of this device ("hip-<arch>-<CUs>cu"); needs the device. */
 int vknn_tune_cache_gpu_tag(char *buf, int64_t cap);
 

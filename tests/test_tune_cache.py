@@ -5,6 +5,8 @@ on the same cache file takes every plan from the file instead of timing candidat
 import ctypes
 import struct
 
+import numpy as np
+
 import pytest
 
 import vknn_amd as V
@@ -47,6 +49,37 @@ def test_reads_reference_layout(lib, tmp_path):
     n, h, m = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
     lib.vknn_tune_cache_stats(ctypes.byref(n), ctypes.byref(h), ctypes.byref(m))
     assert (n.value, h.value, m.value) == (2, 2, 1)
+    lib.vknn_weight_cache_stats(ctypes.byref(n), None, None)
+    assert n.value == 1  # the prepacked blob is retained (CacheMode::Full)
+
+
+def test_weight_section_roundtrip(lib, tmp_path):
+    """Prepacked weight blobs survive a load and a rewrite byte for byte, next to the tune table
+    and a foreign pipeline section; keys come out sorted, as the reference's std::map writes them."""
+    src = container(b"PIPE", [(b"hip/w/conv_9#b", [0.5, -2.0]), (b"hip/w/conv_1#a", [1.0, 2.0, 3.0])], [(b"t", 7)])
+    f, g = tmp_path / "a.cache", tmp_path / "b.cache"
+    f.write_bytes(src)
+    assert lib.vknn_tune_cache_load(str(f).encode()) == 1
+    n = ctypes.c_int64()
+    lib.vknn_weight_cache_stats(ctypes.byref(n), None, None)
+    assert n.value == 2
+    assert lib.vknn_tune_cache_save(str(g).encode()) == 0
+    assert g.read_bytes() == container(b"PIPE", [(b"hip/w/conv_1#a", [1.0, 2.0, 3.0]), (b"hip/w/conv_9#b", [0.5, -2.0])], [(b"t", 7)])
+
+
+def test_truncated_weight_section_keeps_nothing_past_the_cut(lib, tmp_path):
+    """A weight blob cut short (section length fixed so the container parses) ends the section:
+    the complete blob before it is kept, the tune table after it is not reached."""
+    full = container(b"", [(b"w0", [1.0]), (b"w1", [2.0, 3.0])], [(b"t", 1)])
+    body = full[:-(4 + 1 + 4 + 4 + 4)]  # drop the tune table and the last float of w1
+    wl = len(body) - 16
+    body = body[:12] + struct.pack("<I", wl) + body[16:]
+    f = tmp_path / "w.cache"
+    f.write_bytes(body)
+    assert lib.vknn_tune_cache_load(str(f).encode()) == 0
+    n = ctypes.c_int64()
+    lib.vknn_weight_cache_stats(ctypes.byref(n), None, None)
+    assert n.value == 1 and get(lib, b"t") is None
 
 
 def test_save_roundtrip_and_unchanged_file_untouched(lib, tmp_path):
@@ -135,3 +168,37 @@ def test_warm_start_takes_plans_from_cache_file(lib, tmp_path):
     assert s2.describe() == plan1
     del s2
     assert f.read_bytes() == data  # unchanged table: file untouched
+
+
+@pytest.mark.gpu
+def test_warm_start_takes_prepacked_weights_from_cache_file(lib, tmp_path):
+    """CacheMode::Full (the default) with a cache file keeps every conv's prepacked blob in the
+    file's weight section. A warm session packs nothing: every blob comes from the file, and the
+    outputs are bit-identical. A model with other weights (another seed) finds no blob of its own."""
+    V.require_gpu()
+    f = tmp_path / "w.cache"
+    opts = f"cache_file={f}"
+    s1 = V.Session("resnet_tiny", 2, seed=3, options=opts)
+    x = np.random.default_rng(0).standard_normal(s1.in_shape).astype(np.float32)
+    y1 = s1.run(x)
+    convs = s1.count_ops("Conv")
+    del s1
+    n, h, m = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    lib.vknn_weight_cache_stats(ctypes.byref(n), None, None)
+    assert n.value >= convs > 0
+    lib.vknn_tune_cache_clear()
+    s2 = V.Session("resnet_tiny", 2, seed=3, options=opts)
+    lib.vknn_weight_cache_stats(ctypes.byref(n), ctypes.byref(h), ctypes.byref(m))
+    assert m.value == 0 and h.value == convs
+    np.testing.assert_array_equal(s2.run(x), y1)
+    del s2
+    lib.vknn_tune_cache_clear()
+    s3 = V.Session("resnet_tiny", 2, seed=4, options=opts)
+    lib.vknn_weight_cache_stats(ctypes.byref(n), ctypes.byref(h), ctypes.byref(m))
+    assert h.value == 0 and m.value == convs
+    del s3
+    lib.vknn_tune_cache_clear()
+    s4 = V.Session("resnet_tiny", 2, seed=3, options=opts + ";cache_mode=tune")
+    lib.vknn_weight_cache_stats(ctypes.byref(n), ctypes.byref(h), ctypes.byref(m))
+    assert h.value == 0 and m.value == 0  # Tune mode neither reads nor keeps blobs
+    np.testing.assert_array_equal(s4.run(x), y1)

@@ -158,6 +158,7 @@ VKNN_API = {
     "vknn_tune_cache_get": (c_int, [c_char_p, P(c_i32)]),
     "vknn_tune_cache_clear": (c_int, []),
     "vknn_tune_cache_stats": (c_int, [P(c_i64), P(c_i64), P(c_i64)]),
+    "vknn_weight_cache_stats": (c_int, [P(c_i64), P(c_i64), P(c_i64)]),
     "vknn_tune_cache_gpu_tag": (c_int, [c_char_p, c_i64]),
 }
 

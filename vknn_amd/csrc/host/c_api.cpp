@@ -422,7 +422,7 @@ int vknn_session_save_optimized(vknn_session s, const char *path) {
 
 int vknn_tune_cache_load(const char *path) {
     try {
-        return path ? hipbe::TuneCache::instance().load(path) : 0;
+        return path ? hipbe::TuneCache::instance().load(path, true) : 0;
     } catch (const std::exception &e) {
         fail(e.what());
         return 0;
@@ -474,6 +474,18 @@ int vknn_tune_cache_stats(int64_t *entries, int64_t *hits, int64_t *misses) {
         if (entries) *entries = (int64_t) c.size();
         if (hits) *hits = c.hits();
         if (misses) *misses = c.misses();
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
+}
+
+int vknn_weight_cache_stats(int64_t *entries, int64_t *hits, int64_t *misses) {
+    try {
+        auto &c = hipbe::TuneCache::instance();
+        if (entries) *entries = (int64_t) c.weightCount();
+        if (hits) *hits = c.weightHits();
+        if (misses) *misses = c.weightMisses();
         return 0;
     } catch (const std::exception &e) {
         return fail(e.what());

@@ -110,9 +110,11 @@ namespace vknn {
             // Set by the segment before prepare when the conv reads or writes a view (a slice of an
             // in-place concat or split): the plan is then a GEMM or split-K one (no Winograd).
             bool                    viewIO = false;
+            bool                    cacheWeights = false; // keep the prepacked blob in the cache file
 
             void prepare(const Node &node, SegEnv &env) override {
                 const Graph &g = *env.graph;
+                cacheWeights   = env.config->cachesWeights() && !env.config->cacheFile.empty();
                 in             = scaledIn != kNoTensor ? scaledIn : node.inputs[0];
                 out            = node.outputs[0];
                 res            = node.fusedResidual;
@@ -149,11 +151,38 @@ namespace vknn {
                 choosePlan(env, w, b);
             }
 
+            // Cache key of the prepacked blob: the node, its conv signature and plan, and a hash of
+            // the source weights and bias (a changed model or plan never takes a stale blob). The
+            // reference keys its blobs by model tag + node + role (vk_op_common.h uploadCached).
+            std::string weightKey(const float *w, const float *b) const {
+                uint64_t h = 1469598103934665603ull; // FNV-1a, 64 bit, over the fp32 bytes
+                auto mix = [&](const float *p, size_t n) {
+                    const uint8_t *c = reinterpret_cast<const uint8_t *>(p);
+                    for (size_t i = 0; i < n * 4; ++i) h = (h ^ c[i]) * 1099511628211ull;
+                };
+                mix(w, (size_t) d.Cout * (d.Cin / d.group) * d.KH * d.KW);
+                if (b) mix(b, (size_t) d.Cout);
+                char tail[96];
+                std::snprintf(tail, sizeof tail, "#p%d_%d_%d#%016llx", plan.algo, plan.tile, plan.ksplit, (unsigned long long) h);
+                return gpuTag() + "/w/" + name + keyOf(d, 0).substr(gpuTag().size()) + tail;
+            }
+
             void build(const float *w, const float *b) {
                 // a view conv runs GEMM or split-K plans only (no Winograd transforms over views)
                 if (viewIO && plan.algo == VKHIP_CONV_WINOGRAD) check(vkhip_conv_plan_make(&d, VKHIP_CONV_GEMM, -1, 0, &plan), "conv plan");
-                std::vector<uint8_t> host(plan.weight_bytes);
-                check(vkhip_conv_pack_weights(&d, &plan, w, b, host.data()), "conv weight pack");
+                // warm start: the prepacked blob from the cache file's weight section (CacheMode::Full
+                // with a cache file, reference uploadCached); packed and retained on a miss
+                std::vector<uint8_t> host;
+                std::string          wkey;
+                if (cacheWeights) {
+                    wkey = weightKey(w, b);
+                    if (!TuneCache::instance().getWeights(wkey, plan.weight_bytes, host)) host.clear();
+                }
+                if (host.empty()) {
+                    host.resize(plan.weight_bytes);
+                    check(vkhip_conv_pack_weights(&d, &plan, w, b, host.data()), "conv weight pack");
+                    if (cacheWeights) TuneCache::instance().putWeights(wkey, host);
+                }
                 blob = upload(host.data(), host.size());
                 ws   = plan.workspace_bytes ? std::make_shared<DevBuf>(plan.workspace_bytes) : nullptr;
             }
@@ -1669,7 +1698,7 @@ namespace vknn {
             // warm start: the tune table of the unified cache file (reference vk_backend.cpp:440-509)
             if (cfg.cachesTuning() && !cfg.cacheFile.empty()) {
                 cacheFile_ = cfg.cacheFile;
-                TuneCache::instance().load(cacheFile_);
+                TuneCache::instance().load(cacheFile_, cfg.cachesWeights());
             }
             auto s     = std::make_unique<HipSegment>(idx, g, cfg);
             s->backend = this;

@@ -18,7 +18,8 @@ namespace vknn {
             out.insert(out.end(), b, b + 4);
         }
 
-        bool TuneCache::parse(const std::vector<uint8_t> &bytes, std::map<std::string, int32_t> &tune, std::vector<char> *pipe) {
+        bool TuneCache::parse(const std::vector<uint8_t> &bytes, std::map<std::string, int32_t> &tune, std::vector<char> *pipe,
+                              std::map<std::string, std::vector<uint8_t>> *weights) {
             const uint8_t *p = bytes.data();
             const size_t   n = bytes.size();
             if (n < 8 || std::memcmp(p, "VKNNCAC1", 8) != 0) return false;
@@ -39,11 +40,13 @@ namespace vknn {
             auto rdIn = [&](uint32_t &v) { return off + 4 <= end && rd32(v); };
             uint32_t nw = 0;
             if (!rdIn(nw)) return true;
-            for (uint32_t i = 0; i < nw; ++i) { // prepacked weight blobs: skipped
+            for (uint32_t i = 0; i < nw; ++i) { // prepacked weight blobs: kept when asked for, else skipped
                 uint32_t kl = 0, nf = 0;
                 if (!rdIn(kl) || off + kl > end) return true;
+                std::string k((const char *) p + off, kl);
                 off += kl;
                 if (!rdIn(nf) || off + (size_t) nf * 4 > end) return true;
+                if (weights) (*weights)[k].assign(p + off, p + off + (size_t) nf * 4);
                 off += (size_t) nf * 4;
             }
             uint32_t nt = 0;
@@ -63,7 +66,15 @@ namespace vknn {
 
         std::vector<uint8_t> TuneCache::serialize() {
             std::vector<uint8_t> w;
-            wr32(w, 0); // no prepacked weights
+            wr32(w, (uint32_t) weights_.size());
+            for (auto &kv: weights_) { // blobs as whole floats (zero padded to 4 bytes)
+                wr32(w, (uint32_t) kv.first.size());
+                w.insert(w.end(), kv.first.begin(), kv.first.end());
+                const size_t nf = (kv.second.size() + 3) / 4;
+                wr32(w, (uint32_t) nf);
+                w.insert(w.end(), kv.second.begin(), kv.second.end());
+                w.insert(w.end(), nf * 4 - kv.second.size(), 0);
+            }
             wr32(w, (uint32_t) tune_.size());
             for (auto &kv: tune_) {
                 wr32(w, (uint32_t) kv.first.size());
@@ -78,20 +89,48 @@ namespace vknn {
             return out;
         }
 
-        int TuneCache::load(const std::string &path) {
+        int TuneCache::load(const std::string &path, bool keepWeights) {
             std::lock_guard<std::mutex> lk(mu_);
-            if (path.empty() || loaded_[path]) return 0;
-            loaded_[path] = true;
+            if (path.empty() || (loaded_[path] && (!keepWeights || wloaded_[path]))) return 0;
+            const bool first = !loaded_[path];
+            loaded_[path]    = true;
+            if (keepWeights) wloaded_[path] = true;
             std::ifstream f(path, std::ios::binary);
             if (!f) return 0;
             std::vector<uint8_t> bytes((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
-            fileBytes_[path] = bytes;
             std::map<std::string, int32_t> t;
             std::vector<char>              pipe;
-            if (!parse(bytes, t, &pipe)) return 0; // unrecognised -> regenerate
+            std::map<std::string, std::vector<uint8_t>> w;
+            if (!parse(bytes, t, &pipe, keepWeights ? &w : nullptr)) return 0; // unrecognised -> regenerate
+            for (auto &kv: w) weights_.insert(kv); // blobs packed in this process take precedence
+            if (!first) return 0;                 // a later load that only adds the weights
+            fileBytes_[path] = bytes;
             if (pipe_.empty()) pipe_ = pipe;
             for (auto &kv: t) tune_.insert(kv); // entries tuned in this process take precedence
             return (int) t.size();
+        }
+
+        bool TuneCache::getWeights(const std::string &key, size_t bytes, std::vector<uint8_t> &out) {
+            std::lock_guard<std::mutex> lk(mu_);
+            auto it = weights_.find(key);
+            // stored as whole floats: the blob is the first `bytes` of a (bytes + 3) / 4 float run
+            if (it == weights_.end() || (it->second.size() != bytes && it->second.size() != (bytes + 3) / 4 * 4)) {
+                ++wMisses_;
+                return false;
+            }
+            ++wHits_;
+            out.assign(it->second.begin(), it->second.begin() + bytes);
+            return true;
+        }
+
+        void TuneCache::putWeights(const std::string &key, const std::vector<uint8_t> &blob) {
+            std::lock_guard<std::mutex> lk(mu_);
+            weights_[key] = blob;
+        }
+
+        size_t TuneCache::weightCount() {
+            std::lock_guard<std::mutex> lk(mu_);
+            return weights_.size();
         }
 
         int TuneCache::save(const std::string &path) {
@@ -128,7 +167,10 @@ namespace vknn {
         void TuneCache::clear() {
             std::lock_guard<std::mutex> lk(mu_);
             tune_.clear();
+            weights_.clear();
             loaded_.clear();
+            wloaded_.clear();
+            wHits_ = wMisses_ = 0;
             fileBytes_.clear();
             pipe_.clear();
             hits_ = misses_ = 0;
