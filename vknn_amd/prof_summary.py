@@ -5,6 +5,9 @@ HBM traffic:   python -m vknn_amd.prof_summary traffic <fetch counter csv> <writ
                    --fetch-scale F --write-scale W
 Per layer:     python -m vknn_amd.prof_summary layers <run_kernel_trace.csv> <plan.txt> --steps K
                    [--fetch <csv> --write <csv> --fetch-scale F --write-scale W]
+Wave states:   python -m vknn_amd.prof_summary stalls <counter csv> [<counter csv> ...] --steps K
+                   (runs with SQ_WAVE_CYCLES in every --pmc pass, e.g. SQ_WAIT_ANY, SQ_WAIT_INST_ANY,
+                   SQ_ACTIVE_INST_VALU/_VMEM/_LDS, SQ_VALU_MFMA_BUSY_CYCLES)
 
 The timed region of bench.py is K forward passes, each starting with one NCHW->NC4HW4 pack
 dispatch; the last K pack dispatches therefore delimit the timed steps (session creation,
@@ -85,6 +88,57 @@ def counter_per_family(path, steps, counter):
         e[0] += 1
         e[1] += float(r["Counter_Value"]) * 1024.0
     return fam
+
+
+def cmd_stalls(a):
+    """Per kernel family over the timed steps: each SQ counter summed over its dispatches as a
+    fraction of SQ_WAVE_CYCLES from the same pass (the share of resident-wave time spent waiting on
+    a dependency counter, waiting to issue, or issuing each instruction type), and the MFMA busy
+    share, SQ_VALU_MFMA_BUSY_CYCLES over the dispatches' duration x clock x 4 SIMDs x CUs."""
+    cols, fams = [], OrderedDict()
+    for path in a.csv:
+        rows = list(csv.DictReader(open(path)))
+        names = sorted({r["Counter_Name"] for r in rows})
+        byid = OrderedDict()
+        for r in rows:
+            e = byid.setdefault(r["Dispatch_Id"], dict(r))
+            e[r["Counter_Name"]] = float(r["Counter_Value"])
+        timed = timed_rows(list(byid.values()), a.steps)
+        for r in timed:
+            f = fams.setdefault(family(r["Kernel_Name"]), {})
+            for n in names:
+                f.setdefault(n, [0.0, 0])
+                f[n][0] += r.get(n, 0.0)
+                f[n][1] += 1
+            dus = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            f.setdefault("#us", {})[path] = f.get("#us", {}).get(path, 0.0) + dus
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in names:
+                f["#mf_us"] = f.get("#mf_us", 0.0) + dus
+        cols += [n for n in names if n != "SQ_WAVE_CYCLES" and not n.startswith("GRBM_") and n not in cols]
+    print(f"# {a.title}\n")
+    if a.command:
+        print(f"Command: `{a.command}`\n")
+    print("Shares of SQ_WAVE_CYCLES (resident-wave time) per kernel family over the timed steps; "
+          f"mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (dispatch time x {a.clock_ghz} GHz x 4 x {a.cus} CUs).\n")
+    hdr = [c.replace("SQ_", "").lower() for c in cols if c != "SQ_VALU_MFMA_BUSY_CYCLES"]
+    mf = "SQ_VALU_MFMA_BUSY_CYCLES" in cols
+    print("| kernel | us/step | " + " | ".join(hdr) + (" | mfma_busy |" if mf else " |"))
+    print("|---|---:|" + "---:|" * (len(hdr) + (1 if mf else 0)))
+    def us(f):
+        return min(f["#us"].values()) / a.steps
+    for k, f in sorted(fams.items(), key=lambda kv: -us(kv[1])):
+        if us(f) < a.min_us:
+            continue
+        cells = []
+        for c in cols:
+            if c == "SQ_VALU_MFMA_BUSY_CYCLES":
+                continue
+            wc = f.get("SQ_WAVE_CYCLES", [0.0, 0])[0]
+            cells.append(f"{f[c][0] / wc:.3f}" if c in f and wc > 0 else "-")
+        if mf:
+            p = f.get("#mf_us")
+            cells.append(f"{f['SQ_VALU_MFMA_BUSY_CYCLES'][0] / (p * 1e3 * a.clock_ghz * 4 * a.cus):.3f}" if p and "SQ_VALU_MFMA_BUSY_CYCLES" in f else "-")
+        print(f"| `{k}` | {us(f):.1f} | " + " | ".join(cells) + " |")
 
 
 def cmd_trace(a):
@@ -252,12 +306,17 @@ def main():
     lay.add_argument("--write", default="")
     lay.add_argument("--fetch-scale", type=float, default=1.0)
     lay.add_argument("--write-scale", type=float, default=1.0)
-    for p in (t, c, lay):
+    st = sub.add_parser("stalls")
+    st.add_argument("csv", nargs="+")
+    st.add_argument("--cus", type=int, default=256)
+    st.add_argument("--min-us", type=float, default=2.0)
+    st.add_argument("--clock-ghz", type=float, default=2.4)
+    for p in (t, c, lay, st):
         p.add_argument("--steps", type=int, required=True)
         p.add_argument("--title", default="kernel time per forward pass")
         p.add_argument("--command", default="")
     a = ap.parse_args()
-    {"trace": cmd_trace, "traffic": cmd_traffic, "layers": cmd_layers}[a.cmd](a)
+    {"trace": cmd_trace, "traffic": cmd_traffic, "layers": cmd_layers, "stalls": cmd_stalls}[a.cmd](a)
 
 
 if __name__ == "__main__":
