@@ -234,6 +234,29 @@ int    vkhip_dwpw_pack_weights(const vkhip_dwpw_desc *d, const float *dw_w, cons
                                const float *pw_b, void *blob);
 int    vkhip_dwpw_forward(const vkhip_dwpw_desc *d, const void *x, const void *blob, const void *res, void *y, vkhip_stream_t s);
 
+/* ---------------------------------------------------------------- fused 3x3 + 1x1
+ * A bottleneck's 3x3 conv and the 1x1 conv that is the only reader of its output, as one kernel:
+ * t = conv.act(conv3x3(x) + b3) rounded to fp16 as the 3x3's own store would round it, then
+ * y = act(W1 t + b1 (+ res)). The reference runs them as two Conv nodes (ConvCpu,
+ * src/backend/cpu/ops/conv.cpp:9-92, each with its fused epilogue); the intermediate never reaches
+ * memory here. No reference counterpart as an entry point. conv: the 3x3 (pad 1, stride 1 or 2,
+ * even W, Cin a multiple of 16, Cout = the mid width 64 or 128, has_res = 0); Cout, act and
+ * has_res: the 1x1 (stride 1, no padding). */
+typedef struct vkhip_convpw_desc {
+    vkhip_conv_desc conv;
+    int32_t         Cout;
+    int32_t         act;
+    float           act_lo, act_hi;
+    int32_t         has_res;
+} vkhip_convpw_desc;
+/* VKHIP_ERR_UNSUPPORTED when no fused kernel fits the shapes; weight_bytes = the whole blob. */
+int vkhip_convpw_plan(const vkhip_convpw_desc *d, vkhip_conv_plan *plan);
+/* w3 [Cmid][Cin][3][3], w1 [Cout][Cmid] fp32 (rounded to fp16, RNE), biases fp32 or null. */
+int vkhip_convpw_pack_weights(const vkhip_convpw_desc *d, const vkhip_conv_plan *plan, const float *w3, const float *b3, const float *w1,
+                              const float *b1, void *blob);
+int vkhip_convpw_forward(const vkhip_convpw_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res, void *y,
+                         vkhip_stream_t s);
+
 /* ---------------------------------------------------------------- squeeze-excite + pooling
  * Global average pool: x [N,C,H,W] -> y [N,C,1,1] (both NC4HW4 fp16; fp32 accumulation). */
 int vkhip_global_avg_pool(const void *x, void *y, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s);

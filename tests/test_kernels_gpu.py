@@ -464,6 +464,66 @@ def test_conv_winograd_stages(gpu):
     assert lib.vkhip_conv_forward_stages(ctypes.byref(d), ctypes.byref(gplan), dx.ptr, dblob.ptr, dres.ptr, dy.ptr, ws.ptr, 1, None) != 0
 
 
+def gpu_convpw(x, w3, b3, stride, act3, w1, b1, act1, res=None):
+    """The fused 3x3 -> 1x1 kernel through the C ABI (vkhip_convpw_*)."""
+    lib = V.vkhip()
+    d3, mshape = conv_desc(x.shape, w3.shape, stride, (1, 1, 1, 1), act=act3)
+    d = V.ConvPwDesc(conv=d3, Cout=w1.shape[0], act=act1, act_lo=0.0, act_hi=6.0, has_res=int(res is not None))
+    plan = V.ConvPlan()
+    check(lib.vkhip_convpw_plan(ctypes.byref(d), ctypes.byref(plan)), "convpw plan")
+    blob = np.zeros(plan.weight_bytes, np.uint8)
+    w3 = np.ascontiguousarray(w3, np.float32)
+    w1 = np.ascontiguousarray(w1.reshape(w1.shape[0], -1), np.float32)
+    check(lib.vkhip_convpw_pack_weights(ctypes.byref(d), ctypes.byref(plan), w3.ctypes.data, b3.ctypes.data, w1.ctypes.data,
+                                        b1.ctypes.data, blob.ctypes.data), "convpw pack")
+    dblob, dx = DeviceBuffer.from_array(blob), to_device_nc4(x)
+    dres = to_device_nc4(res) if res is not None else None
+    yshape = (x.shape[0], w1.shape[0], mshape[2], mshape[3])
+    dy = DeviceBuffer(V.nc4_elems(*yshape) * 2)
+    dy.zero()
+    check(lib.vkhip_convpw_forward(ctypes.byref(d), ctypes.byref(plan), dx.ptr, dblob.ptr, dres.ptr if dres else None, dy.ptr, None), "convpw")
+    check(lib.vkhip_stream_sync(None), "sync")
+    return from_device_nc4(dy, yshape), dy, yshape
+
+
+@pytest.mark.parametrize("N,Cin,H,W,Cmid,Cout,S,act3,act1,res", [
+    (2, 64, 14, 14, 64, 256, 1, 1, 1, True),     # layer-1 bottleneck shape, small map
+    (1, 32, 9, 10, 64, 40, 1, 2, 2, False),      # ragged: odd H, Cout not a multiple of 32
+    (2, 256, 16, 16, 128, 512, 2, 1, 1, True),   # layer-2 first block: stride 2, 128 mid channels
+    (3, 128, 12, 8, 128, 100, 1, 5, 0, False),   # SiLU mid, no 1x1 activation, 3 images across workgroups
+])
+def test_convpw(gpu, N, Cin, H, W, Cmid, Cout, S, act3, act1, res):
+    """3x3 (+bias, act, fp16 rounding) then 1x1 (+bias, residual, act) in one kernel against the
+    oracle running the two convs with the intermediate rounded to fp16 between them."""
+    r = rng(N * 1000 + Cin + H + Cout)
+    x = round_half(r.standard_normal((N, Cin, H, W)))
+    w3 = (r.standard_normal((Cmid, Cin, 3, 3)) * np.sqrt(2.0 / (9 * Cin))).astype(np.float32)
+    b3 = (r.standard_normal(Cmid) * 0.1).astype(np.float32)
+    w1 = (r.standard_normal((Cout, Cmid, 1, 1)) * np.sqrt(2.0 / Cmid)).astype(np.float32)
+    b1 = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    OH, OW = (H - 1) // S + 1, (W - 1) // S + 1
+    rs = round_half(r.standard_normal((N, Cout, OH, OW))) if res else None
+    got, dy, yshape = gpu_convpw(x, w3, b3, (S, S), act3, w1, b1, act1, rs)
+    mid = round_half(oracle_conv(x, w3, b3, (S, S), (1, 1, 1, 1), act=act3))
+    ref = oracle_conv(mid, w1, b1, (1, 1), (0, 0, 0, 0), res=rs, act=act1, lo=0.0, hi=6.0)
+    assert_parity(got, ref, f"convpw N{N} C{Cin} {H}x{W} s{S} mid{Cmid} out{Cout}")
+    if Cout % 4:  # channel lanes past Cout stay +0
+        raw = raw_nc4(dy, yshape).reshape(N, -1, OH, OW, 4)
+        assert np.all(raw[:, -1, :, :, Cout % 4:] == 0)
+
+
+def test_convpw_rejects_unsupported(gpu):
+    """Mid widths other than 64/128, 1x1 or padded-wrong convs and a 3x3 with a residual have no
+    fused kernel: the plan call says so and launches nothing."""
+    lib = V.vkhip()
+    for shape, w, kw in [((1, 64, 8, 8), (96, 64, 3, 3), {}), ((1, 64, 8, 8), (64, 64, 1, 1), {}),
+                         ((1, 64, 8, 8), (64, 64, 3, 3), {"has_res": 1})]:
+        d3, _ = conv_desc(shape, w, (1, 1), (1, 1, 1, 1) if w[2] == 3 else (0, 0, 0, 0), **kw)
+        d = V.ConvPwDesc(conv=d3, Cout=256, act=1, act_lo=0.0, act_hi=0.0, has_res=0)
+        plan = V.ConvPlan()
+        assert lib.vkhip_convpw_plan(ctypes.byref(d), ctypes.byref(plan)) != 0
+
+
 def test_conv_dilation(gpu):
     r = rng(40)
     x = round_half(r.standard_normal((1, 16, 15, 15)))

@@ -43,6 +43,11 @@ class DwPwDesc(ctypes.Structure):
                 ("has_res", c_i32)]
 
 
+class ConvPwDesc(ctypes.Structure):
+    _fields_ = [("conv", ConvDesc), ("Cout", c_i32), ("act", c_i32), ("act_lo", c_f), ("act_hi", c_f),
+                ("has_res", c_i32)]
+
+
 class PoolDesc(ctypes.Structure):
     _fields_ = [(n, c_i32) for n in ("N", "C", "H", "W", "OH", "OW", "KH", "KW", "SH", "SW", "PT", "PL")]
 
@@ -93,6 +98,9 @@ VKHIP_API = {
     "vkhip_conv_pack_weights": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp]),
     "vkhip_conv_forward": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_forward_noalloc": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "vkhip_convpw_plan": (c_int, [P(ConvPwDesc), P(ConvPlan)]),
+    "vkhip_convpw_pack_weights": (c_int, [P(ConvPwDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "vkhip_convpw_forward": (c_int, [P(ConvPwDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_forward_stages": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp]),
     "vkhip_conv_forward_scaled": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_pool_parts": (c_int, [P(ConvDesc), P(ConvPlan)]),

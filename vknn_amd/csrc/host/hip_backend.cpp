@@ -15,6 +15,7 @@
 #include "vkhip.h"
 #include "vknn/profiler.h"
 #include <algorithm>
+#include <functional>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -803,6 +804,181 @@ namespace vknn {
             std::string describe() const override { return what + (what.find(':') != std::string::npos ? " " : " folded into ") + into; }
         };
 
+        // ------------------------------------------------------------ fused 3x3 + 1x1
+        // A 3x3 conv whose only reader is a 1x1 conv (a bottleneck's middle conv and its expansion)
+        // as one op at the 1x1's place in the order (its residual, e.g. a projection shortcut, may be
+        // computed between the two). Either the fused kernel (vkhip_convpw_forward: the 3x3 output
+        // stays in registers) or the two convs on their own tuned plans with the intermediate in
+        // HBM; prepare() plans both convs like standalone ones, times the fused kernel against them
+        // on rotating buffer sets larger than the last-level cache, and keeps the faster (the
+        // choice is kept in the tune table).
+        struct ConvPwOp: HipOp {
+            const Node             *n3 = nullptr; // the 3x3 node (this op is prepared with the 1x1 node)
+            ConvOp                  c3, c1;
+            vkhip_convpw_desc       pd {};
+            vkhip_conv_plan         plan {};
+            std::shared_ptr<DevBuf> blob;
+            bool                    split = true;
+
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g = *env.graph;
+                c3.name = n3->name;
+                c1.name = node.name;
+                c3.prepare(*n3, env);
+                c1.prepare(node, env);
+                kind  = "convpw";
+                flops = c3.flops + c1.flops;
+                bytes = c3.bytes + c1.bytes;
+                pd.conv = c3.d;
+                pd.Cout = c1.d.Cout; pd.act = c1.d.act; pd.act_lo = c1.d.act_lo; pd.act_hi = c1.d.act_hi; pd.has_res = c1.d.has_res;
+                if (!env.tunable || vkhip_convpw_plan(&pd, &plan) != VKHIP_OK) return;
+                std::vector<uint8_t> host(plan.weight_bytes);
+                std::vector<float>   w1(initF32(g, node.inputs[1]), initF32(g, node.inputs[1]) + (size_t) pd.Cout * pd.conv.Cout);
+                check(vkhip_convpw_pack_weights(&pd, &plan, initF32(g, n3->inputs[1]), initF32(g, biasOf(*n3)), w1.data(), initF32(g, biasOf(node)),
+                                                host.data()),
+                      "convpw pack");
+                std::string key = gpuTag() + "/convpw";
+                for (int v: {pd.conv.N, pd.conv.Cin, pd.conv.H, pd.conv.W, pd.conv.Cout, pd.conv.SH, pd.Cout, pd.has_res, c3.plan.tile, c1.plan.tile})
+                    key += "_" + std::to_string(v);
+                int32_t cached = 0;
+                if (TuneCache::instance().get(key, cached)) split = cached != 0;
+                else {
+                    blob  = upload(host.data(), host.size());
+                    split = timeSplit(g) <= timeFused();
+                    TuneCache::instance().put(key, split ? 1 : 0);
+                }
+                if (split) {
+                    blob.reset();
+                    return;
+                }
+                if (!blob) blob = upload(host.data(), host.size());
+                const vkhip_conv_desc &c = pd.conv;
+                bytes = (int64_t) (nc4Bytes({c.N, c.Cin, c.H, c.W}) + nc4Bytes({c.N, pd.Cout, c.OH, c.OW}) * (pd.has_res ? 2 : 1)) +
+                        (int64_t) c.Cout * (c.Cin * 9 + pd.Cout) * 2;
+            }
+
+            // Rotating buffer sets (input, intermediate, residual, output) whose total exceeds the
+            // 256 MB last-level cache, so both alternatives are timed from HBM as in a forward pass.
+            struct Set {
+                std::shared_ptr<DevBuf> x, m, r, y;
+            };
+            std::vector<Set> sets_;
+            void makeSets() {
+                if (!sets_.empty()) return;
+                const vkhip_conv_desc &c = pd.conv;
+                const size_t xb = nc4Bytes({c.N, c.Cin, c.H, c.W}), mb = nc4Bytes({c.N, c.Cout, c.OH, c.OW}), yb = nc4Bytes({c.N, pd.Cout, c.OH, c.OW});
+                const size_t one = xb + mb + yb * (pd.has_res ? 2 : 1);
+                const int    n   = (int) std::min<size_t>(6, std::max<size_t>(1, ((size_t) 640 << 20) / std::max<size_t>(one, 1) + 1));
+                for (int k = 0; k < n; ++k) {
+                    Set t;
+                    t.x = std::make_shared<DevBuf>(xb);
+                    t.m = std::make_shared<DevBuf>(mb);
+                    t.y = std::make_shared<DevBuf>(yb);
+                    check(vkhip_fill_zero(t.x->ptr, xb, nullptr), "convpw tune fill");
+                    if (pd.has_res) {
+                        t.r = std::make_shared<DevBuf>(yb);
+                        check(vkhip_fill_zero(t.r->ptr, yb, nullptr), "convpw tune fill");
+                    }
+                    sets_.push_back(t);
+                }
+            }
+            double timeRuns(const std::function<void(const Set &)> &run) {
+                makeSets();
+                vkhip_event_t e0, e1;
+                check(vkhip_event_create(&e0), "event");
+                check(vkhip_event_create(&e1), "event");
+                double best = 1e30;
+                size_t k    = 0;
+                for (int r = 0; r < 5; ++r) {
+                    vkhip_event_record(e0, nullptr);
+                    for (int i = 0; i < 6; ++i) run(sets_[k++ % sets_.size()]);
+                    vkhip_event_record(e1, nullptr);
+                    vkhip_event_sync(e1);
+                    float ms = 0;
+                    vkhip_event_elapsed_ms(e0, e1, &ms);
+                    if (r > 0) best = std::min(best, (double) ms); // the first round warms up
+                }
+                vkhip_event_destroy(e0);
+                vkhip_event_destroy(e1);
+                return best;
+            }
+            double timeFused() {
+                return timeRuns([&](const Set &t) {
+                    check(vkhip_convpw_forward(&pd, &plan, t.x->ptr, blob->ptr, t.r ? t.r->ptr : nullptr, t.y->ptr, nullptr), "convpw tune");
+                });
+            }
+            double timeSplit(const Graph &) {
+                return timeRuns([&](const Set &t) {
+                    check(c3.forward(c3.plan, t.x->ptr, nullptr, c3.blob->ptr, nullptr, t.m->ptr, c3.ws ? c3.ws->ptr : nullptr, nullptr), "convpw tune 3x3");
+                    check(c1.forward(c1.plan, t.m->ptr, nullptr, c1.blob->ptr, t.r ? t.r->ptr : nullptr, t.y->ptr, c1.ws ? c1.ws->ptr : nullptr, nullptr),
+                          "convpw tune 1x1");
+                });
+            }
+
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                if (split) {
+                    c3.record(env, s);
+                    c1.record(env, s);
+                    return;
+                }
+                check(vkhip_convpw_forward(&pd, &plan, env.dev(c3.in), blob->ptr, c1.res != kNoTensor ? env.dev(c1.res) : nullptr, env.dev(c1.out), s),
+                      "convpw " + name);
+            }
+            std::string describe() const override {
+                return split ? "split: " + c3.name + " (" + c3.describe() + ") then 1x1 " + c1.describe()
+                             : "fused 3x3 + 1x1 (" + c3.name + " in registers) kernel=conv_halo_pw_kernel";
+            }
+        };
+
+        // 3x3 + 1x1 pairs (ConvPwOp): a 3x3 conv of the segment whose output only a 1x1 stride-1
+        // conv of the segment reads, with shapes the fused kernel may take (vkhip_convpw_plan; the
+        // timing in ConvPwOp decides). Returns 1x1 node -> 3x3 node. `skip`: nodes already fused or
+        // folded into another op.
+        static void planPwPairs(const Graph &g, const std::vector<int> &idx, const std::set<int> &skip, std::map<int, int> &pw) {
+            std::set<int>           inSeg(idx.begin(), idx.end());
+            std::map<TensorId, int> readers, producer;
+            for (size_t i = 0; i < g.nodes.size(); ++i) {
+                const Node &nd = g.nodes[i];
+                for (TensorId t: nd.inputs)
+                    if (t != kNoTensor) ++readers[t];
+                if (nd.fusedResidual != kNoTensor) ++readers[nd.fusedResidual];
+                for (TensorId t: nd.outputs)
+                    if (t != kNoTensor) producer[t] = (int) i;
+            }
+            for (TensorId t: g.outputs) readers[t] += 1000;
+            auto convDesc = [&](const Node &c, vkhip_conv_desc &d) {
+                if (c.type != OpType::Conv || c.inputs.size() < 2 || !g.isInitializer(c.inputs[1]) || c.outputs.empty()) return false;
+                const Shape &ws = g.desc(c.inputs[1]).shape;
+                if (ws.size() != 4 || g.desc(c.inputs[0]).shape.size() != 4) return false;
+                NCHW x = NCHW::from(g.desc(c.inputs[0]).shape), y = NCHW::from(g.desc(c.outputs[0]).shape);
+                auto st = attrInts(c, "strides", {1, 1}), pad = attrInts(c, "pads", {0, 0, 0, 0}), dl = attrInts(c, "dilations", {1, 1});
+                if (pad[2] != pad[0] || pad[3] != pad[1]) return false;
+                d = vkhip_conv_desc {};
+                d.N = (int) x.n; d.Cin = (int) x.c; d.H = (int) x.h; d.W = (int) x.w; d.Cout = (int) ws[0]; d.OH = (int) y.h; d.OW = (int) y.w;
+                d.KH = (int) ws[2]; d.KW = (int) ws[3]; d.SH = (int) st[0]; d.SW = (int) st[1]; d.PT = (int) pad[0]; d.PL = (int) pad[1];
+                d.DH = (int) dl[0]; d.DW = (int) dl[1]; d.group = (int) c.attr.geti("group", 1); d.act = (int) c.fusedAct;
+                d.act_lo = c.actLo; d.act_hi = c.actHi; d.has_res = c.fusedResidual != kNoTensor;
+                return true;
+            };
+            for (int b: idx) {
+                const Node     &n1 = g.nodes[b];
+                vkhip_conv_desc d1, d3;
+                if (skip.count(b) || !convDesc(n1, d1) || d1.KH != 1 || d1.KW != 1 || d1.SH != 1 || d1.SW != 1 || d1.PT != 0 || d1.PL != 0 || d1.group != 1)
+                    continue;
+                const TensorId t  = n1.inputs[0];
+                auto           pit = producer.find(t);
+                if (pit == producer.end() || !inSeg.count(pit->second) || skip.count(pit->second) || readers[t] != 1) continue;
+                const Node &n3 = g.nodes[pit->second];
+                if (!convDesc(n3, d3) || d3.KH != 3 || d3.has_res || d3.Cout != d1.Cin || n1.fusedResidual == t) continue;
+                vkhip_convpw_desc pd {};
+                pd.conv = d3;
+                pd.Cout = d1.Cout; pd.act = d1.act; pd.act_lo = d1.act_lo; pd.act_hi = d1.act_hi; pd.has_res = d1.has_res;
+                vkhip_conv_plan plan;
+                if (vkhip_convpw_plan(&pd, &plan) != VKHIP_OK) continue;
+                pw[b] = pit->second;
+            }
+        }
+
         // Stem + pool fusion: a MaxPool 3x3 stride 2 pad 1 whose input is the output of a conv of the
         // same segment that nothing else reads, and that conv a first layer the fused kernel takes
         // (vkhip_conv_maxpool_supported on its stem plan). Returns conv node -> pool node.
@@ -1022,6 +1198,30 @@ namespace vknn {
                 const char *views_env = std::getenv("VKNN_HIP_VIEWS");
                 if (!views_env || std::string(views_env) != "0") planViews(idx, noWrite, noRead);
             }
+            // 3x3 + 1x1 pairs (ConvPwOp) among the convs no other fold or view touches;
+            // VKNN_HIP_FUSE_PW=0 keeps every conv on its own (A/B).
+            std::map<int, int> pwPairs; // 1x1 node -> 3x3 node
+            std::set<int>      pwFolded; // 3x3 nodes of the pairs
+            {
+                const char *pw_env = std::getenv("VKNN_HIP_FUSE_PW");
+                if (!pw_env || std::string(pw_env) != "0") {
+                    std::set<int> skip(folded.begin(), folded.end());
+                    for (auto &kv: scaled) skip.insert(kv.first);
+                    for (auto &kv: convPool) skip.insert(kv.first), skip.insert(kv.second);
+                    for (auto &kv: gapConv) skip.insert(kv.first), skip.insert(kv.second);
+                    std::map<int, int> cand;
+                    planPwPairs(g, idx, skip, cand);
+                    for (auto &kv: cand) {
+                        const Node &n1 = g.nodes[kv.first], &n3 = g.nodes[kv.second];
+                        bool view = false;
+                        for (TensorId t: {n3.inputs[0], n3.outputs[0], n1.outputs[0], n1.fusedResidual})
+                            if (t != kNoTensor && (place_.count(resolve(t)) || pstride(t) > 0)) view = true;
+                        if (view) continue;
+                        pwPairs[kv.first] = kv.second;
+                        pwFolded.insert(kv.second);
+                    }
+                }
+            }
             // Device buffers: one NC4HW4 fp16 buffer per activation (aliases share their source's;
             // a tensor placed in another one by planViews has none of its own).
             for (int i: idx) {
@@ -1063,6 +1263,16 @@ namespace vknn {
                     f->into = foldedInto[i];
                     if (pools.count(i)) f->what = "max pool";
                     op      = std::move(f);
+                } else if (pwFolded.count(i)) {
+                    auto f = std::make_unique<FoldedMulOp>();
+                    f->what = "3x3 conv: runs with the 1x1 conv that reads it,";
+                    for (auto &kv: pwPairs)
+                        if (kv.second == i) f->into = g.nodes[kv.first].name;
+                    op = std::move(f);
+                } else if (pwPairs.count(i)) {
+                    auto c = std::make_unique<ConvPwOp>();
+                    c->n3  = &g.nodes[pwPairs[i]];
+                    op     = std::move(c);
                 } else op = makeOp(g, nd);
                 if (!op) throw Error(Status::Unsupported, std::string("HIP backend has no kernel for ") + opTypeName(nd.type) + " (" + nd.name + ")");
                 auto sit = scaled.find(i);
@@ -1083,14 +1293,15 @@ namespace vknn {
                 op->name = nd.name;
                 op->type = nd.type;
                 const bool gapFolded = gapParts.count(i) > 0;
-                if (nd.type == OpType::Conv && !inPlace && !gapFolded && !folded.count(i) && !pools.count(i)) {
+                const bool pwOp = pwPairs.count(i) || pwFolded.count(i);
+                if (nd.type == OpType::Conv && !inPlace && !gapFolded && !folded.count(i) && !pools.count(i) && !pwOp) {
                     bool v = false;
                     for (TensorId t: {nd.inputs[0], nd.outputs[0]}) v = v || pstride(t) > 0;
                     static_cast<ConvOp *>(op.get())->viewIO = v;
                 }
                 if (!gapFolded) op->prepare(nd, env_);
                 else op->kind = "folded";
-                if (gapConv.size() && nd.type == OpType::Conv) convOps[i] = static_cast<ConvOp *>(op.get());
+                if (gapConv.size() && nd.type == OpType::Conv && !pwOp) convOps[i] = static_cast<ConvOp *>(op.get());
                 auto sg = seGap.find(i);
                 if (sg != seGap.end() && gapParts.count(sg->second)) {
                     auto       *se = static_cast<SeOp *>(op.get());
@@ -1122,7 +1333,16 @@ namespace vknn {
                     outs.push_back(out);
                     continue;
                 }
-                if (folded.count(i) || pools.count(i)) {
+                if (folded.count(i) || pools.count(i) || pwFolded.count(i)) {
+                    ins.push_back(in);
+                    outs.push_back(out);
+                    continue;
+                }
+                if (pwPairs.count(i)) {
+                    // the pair reads the 3x3's input (and the 1x1's residual) and writes the 1x1's output
+                    in.push_back(resolve(g.nodes[pwPairs[i]].inputs[0]));
+                    if (nd.fusedResidual != kNoTensor) in.push_back(resolve(nd.fusedResidual));
+                    out.push_back(resolve(nd.outputs[0]));
                     ins.push_back(in);
                     outs.push_back(out);
                     continue;

@@ -1101,3 +1101,159 @@ int vkhip_conv_forward_noalloc(const vkhip_conv_desc *d, const vkhip_conv_plan *
 }
 
 } // extern "C"
+
+// ---------------------------------------------------------------------- fused 3x3 + 1x1
+namespace vkhip {
+
+    // The fused kernel's tile for a mid width: its halo geometry (the 3x3 weights are packed like
+    // the halo tile with the same BM and KK, which fixes the A layout) and the 1x1 chunking.
+    struct PwTile {
+        int     halo_tile; // kTiles entry whose A layout the 3x3 weights use (BM = mid width, KK = 1)
+        TileCfg t;         // the fused workgroup: BM = mid width, WM = 1, WN = 4
+        int     MC;        // 32-row 1x1 fragments per chunk
+    };
+    static bool pw_tile(int cmid, PwTile &p) {
+        if (cmid == 64) p = {18, {64, 256, 1, 4, 3, 2, 2, 1}, 1};
+        else if (cmid == 128) p = {17, {128, 128, 1, 4, 3, 4, 1, 1}, 1};
+        else return false;
+        return true;
+    }
+    static constexpr int kPwMaxNBI64 = 15, kPwMaxNBI128 = 10;
+
+    // 1x1 parts of the blob, after the 3x3 plan's weight bytes: bias [nchunks * 32 * MC] fp32, then
+    // the weights [nchunks * MC fragments][2 * FM steps][64 lanes][8 halves]
+    struct PwLayout {
+        size_t  w3_bytes, off_b1, off_w1, bytes;
+        int64_t nchunks, frags, steps;
+    };
+    static PwLayout pw_layout(const vkhip_convpw_desc *d, const PwTile &pt, size_t w3_bytes) {
+        PwLayout L;
+        L.w3_bytes = w3_bytes;
+        L.nchunks  = ceil_div(d->Cout, 32 * pt.MC);
+        L.frags    = L.nchunks * pt.MC;
+        L.steps    = 2 * (d->conv.Cout / 32);
+        L.off_b1   = align256(w3_bytes);
+        L.off_w1   = L.off_b1 + align256((size_t) L.frags * 32 * 4);
+        L.bytes    = L.off_w1 + (size_t) L.frags * L.steps * 1024;
+        return L;
+    }
+
+    static int pw_check(const vkhip_convpw_desc *d, PwTile &pt, vkhip_conv_plan &p3) {
+        if (!d) return set_error(VKHIP_ERR_INVALID, "convpw: null descriptor");
+        const vkhip_conv_desc &c = d->conv;
+        if (!pw_tile(c.Cout, pt)) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw: mid width %d (64 or 128 only)", c.Cout);
+        if (c.has_res || c.in_scale || c.N <= 0 || d->Cout <= 0 || c.W % 2) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw: 3x3 with a residual, an input scale or odd width");
+        if (!halo_shape_ok(&c, pt.t)) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw: not a halo-tile 3x3 (pad 1, stride 1/2, Cin %% 16 == 0)");
+        const int nbi = halo_nbi(&c, pt.t);
+        if (nbi > (c.Cout == 64 ? kPwMaxNBI64 : kPwMaxNBI128) || !pw_tile_kernel(c.Cout, nbi))
+            return set_error(VKHIP_ERR_UNSUPPORTED, "convpw: input band too large for LDS");
+        const int64_t P = (int64_t) c.N * c.OH * c.OW;
+        if (P * ceil_div(std::max(c.Cin, d->Cout), 4) * 8 >= (1LL << 31) || (int64_t) c.N * ceil_div(c.Cin, 4) * c.H * c.W * 8 >= (1LL << 31))
+            return set_error(VKHIP_ERR_UNSUPPORTED, "convpw: tensor >= 2 GiB");
+        // the 3x3 part is packed like a GEMM plan of the halo tile with the same A layout (the band
+        // limit that tile's own kernels have does not apply: the fused kernel checked its own above)
+        const ConvGeom g = gemm_geom(&c, pt.halo_tile, false);
+        std::memset(&p3, 0, sizeof(p3));
+        p3.algo         = VKHIP_CONV_GEMM;
+        p3.tile         = pt.halo_tile;
+        p3.weight_bytes = align256((size_t) g.Coutp * 4) + (size_t) g.Coutp * g.Kp * 2;
+        return VKHIP_OK;
+    }
+
+} // namespace vkhip
+
+extern "C" {
+
+int vkhip_convpw_plan(const vkhip_convpw_desc *d, vkhip_conv_plan *plan) {
+    if (!plan) return set_error(VKHIP_ERR_INVALID, "convpw_plan: null plan");
+    PwTile          pt;
+    vkhip_conv_plan p3;
+    int rc = pw_check(d, pt, p3);
+    if (rc) return rc;
+    *plan              = p3;
+    plan->weight_bytes = pw_layout(d, pt, p3.weight_bytes).bytes;
+    plan->workspace_bytes = 0;
+    return VKHIP_OK;
+}
+
+int vkhip_convpw_pack_weights(const vkhip_convpw_desc *d, const vkhip_conv_plan *plan, const float *w3, const float *b3, const float *w1,
+                              const float *b1, void *blob) {
+    if (!plan || !w3 || !w1 || !blob) return set_error(VKHIP_ERR_INVALID, "convpw_pack: null argument");
+    PwTile          pt;
+    vkhip_conv_plan p3;
+    int rc = pw_check(d, pt, p3);
+    if (rc) return rc;
+    const PwLayout L = pw_layout(d, pt, p3.weight_bytes);
+    if (plan->weight_bytes != L.bytes) return set_error(VKHIP_ERR_INVALID, "convpw_pack: plan does not match the descriptor");
+    std::memset(blob, 0, L.bytes);
+    if ((rc = vkhip_conv_pack_weights(&d->conv, &p3, w3, b3, blob))) return rc;
+    float  *bias = (float *) ((char *) blob + L.off_b1);
+    half_t *wp   = (half_t *) ((char *) blob + L.off_w1);
+    const int Cmid = d->conv.Cout;
+    if (b1)
+        for (int m = 0; m < d->Cout; ++m) bias[m] = b1[m];
+    // fragment f, step s = 2i + h, lane l = g*32 + row%32, entry t: channel i*32 + (2h + t/4)*8 + 4g + t%4
+    for (int64_t f = 0; f < L.frags; ++f)
+        for (int64_t s = 0; s < L.steps; ++s)
+            for (int l = 0; l < 64; ++l)
+                for (int t = 0; t < 8; ++t) {
+                    const int64_t m = f * 32 + (l & 31);
+                    const int     i = (int) (s / 2), h = (int) (s % 2), g = l >> 5;
+                    const int     ch = i * 32 + (2 * h + t / 4) * 8 + 4 * g + t % 4;
+                    if (m < d->Cout) wp[((f * L.steps + s) * 64 + l) * 8 + t] = (half_t) w1[m * Cmid + ch];
+                }
+    return VKHIP_OK;
+}
+
+int vkhip_convpw_forward(const vkhip_convpw_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res, void *y,
+                         vkhip_stream_t s) {
+    if (!plan || !x || !blob || !y) return set_error(VKHIP_ERR_INVALID, "convpw_forward: null argument");
+    PwTile          pt;
+    vkhip_conv_plan p3;
+    int rc = pw_check(d, pt, p3);
+    if (rc) return rc;
+    const PwLayout L = pw_layout(d, pt, p3.weight_bytes);
+    if (plan->weight_bytes != L.bytes) return set_error(VKHIP_ERR_INVALID, "convpw_forward: plan does not match the descriptor");
+    if (d->has_res && !res) return set_error(VKHIP_ERR_INVALID, "convpw_forward: has_res without a residual tensor");
+    const vkhip_conv_desc &c = d->conv;
+    const int              nbi = halo_nbi(&c, pt.t);
+    PwKernelFn             fn  = pw_tile_kernel(c.Cout, nbi);
+    if (!fn) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw_forward: no kernel for band %d", nbi);
+    ConvGeom g = gemm_geom(&c, pt.halo_tile, false);
+    GemmArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.x = (const uint2 *) x;
+    a.w = (const half_t *) ((const char *) blob + align256((size_t) g.Coutp * 4));
+    a.bias = (const float *) blob;
+    a.Cinb = (int) g.Cinb; a.Coutb = (int) g.Coutb; a.Cout = c.Cout;
+    a.P = (int) g.P; a.Pv = (int) g.Pv; a.OHWp = (int) g.HWp;
+    a.Kslots = (int) g.Kslots; a.nsteps = (int) g.nsteps; a.steps_per_split = (int) g.nsteps;
+    a.act = c.act; a.lo = c.act_lo; a.hi = c.act_hi;
+    a.m_tiles = 1;
+    a.x_pstride = (int) g.Cinb; a.y_pstride = (int) g.Coutb;
+    a.x_bytes = (unsigned) ((int64_t) c.N * g.Cinb * c.H * c.W * 8);
+    a.H = c.H; a.W = c.W; a.HW = c.H * c.W; a.OW = c.OW; a.OHW = c.OH * c.OW;
+    a.KW = c.KW; a.SH = c.SH; a.SW = c.SW; a.PT = c.PT; a.PL = c.PL; a.DH = c.DH; a.DW = c.DW;
+    a.omode = OMODE_EPILOGUE;
+    PwArgs p;
+    std::memset(&p, 0, sizeof(p));
+    p.w       = (const half_t *) ((const char *) blob + L.off_w1);
+    p.nchunks = (int) L.nchunks;
+    GemmArgs &e = p.e;
+    const int64_t Coutb = ceil_div(d->Cout, 4), OHW = (int64_t) c.OH * c.OW;
+    e.bias = (const float *) ((const char *) blob + L.off_b1);
+    e.res = (const uint2 *) res; e.has_res = d->has_res;
+    e.y = (uint2 *) y;
+    e.Cout = d->Cout; e.Coutb = (int) Coutb;
+    e.P = (int) g.P; e.Pv = (int) g.P; e.OHW = (int) OHW; e.OHWp = (int) OHW; e.OW = c.OW;
+    e.y_pstride = (int) Coutb;
+    e.y_bytes = (unsigned) ((int64_t) c.N * Coutb * OHW * 8);
+    e.act = d->act; e.lo = d->act_lo; e.hi = d->act_hi;
+    e.omode = OMODE_EPILOGUE;
+    e.m_tiles = 1;
+    const unsigned grid = (unsigned) ceil_div(g.P, pt.t.BN);
+    fn<<<dim3(grid), 64 * pt.t.WN, 0, resolve_stream(s)>>>(a, p);
+    return check_launch("convpw");
+}
+
+} // extern "C"

@@ -1058,8 +1058,18 @@ namespace vkhip {
     //   pair that holds pixel W-1 also copies the next image row's first pixel into column W, the
     //   right pad; the B fragments of the right-hand taps are zeroed in registers for the output
     //   columns whose right neighbour is that pad.
-    template <int FM, int FN, int WM, int WN, int KK, int NS, int NBI, bool ODD = false>
-    __global__ __launch_bounds__(64 * WM * WN, 1) void conv_halo_kernel(GemmArgs a) {
+    // LDS bytes of a halo workgroup: NS ring stages plus the spare 1 KB that surplus A copies fill
+    template <int FM, int WM, int WN, int KK, int NS, int NBI>
+    __host__ __device__ constexpr int halo_lds_bytes() {
+        return NS * (9 * KK * FM * WM * 1024 + 32 + 4 * KK * NBI * 1024) + ((9 * KK * FM * WM) % (WM * WN) ? 1024 : 0);
+    }
+
+    // The halo kernel's main loop (everything before its epilogue): the workgroup (m_tile, n0)
+    // accumulates its BM x BN tile over K stages ks_begin .. ks_end of split `split` into acc,
+    // with the ring in `sm` (halo_lds_bytes).
+    template <int FM, int FN, int WM, int WN, int KK, int NS, int NBI, bool ODD>
+    __device__ __forceinline__ void halo_mainloop(const GemmArgs &a, unsigned char *sm, float16v (&acc)[FM][FN], int tid, int lane, int wave,
+                                                  int m_tile, int n0, int split) {
         constexpr int NW     = WM * WN;
         constexpr int BM     = 32 * FM * WM;
         constexpr int BN     = 32 * FN * WN;
@@ -1077,23 +1087,11 @@ namespace vkhip {
         constexpr int NAW = (NA + NW - 1) / NW;
         constexpr int SPARE = NA % NW ? 1024 : 0;
         static_assert(NS * STAGE + SPARE <= 160 * 1024, "LDS budget");
+        static_assert(NS * STAGE + SPARE == halo_lds_bytes<FM, WM, WN, KK, NS, NBI>(), "LDS size");
         static_assert(NB % NW == 0, "band copies per wave");
-        __shared__ __attribute__((aligned(16))) unsigned char sm[NS * STAGE + SPARE];
-
-        const int tid  = threadIdx.x;
-        const int lane = tid & 63;
-        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-        const int wmi  = wave / WN;
-        const int wni  = wave % WN;
-
-        const int lin    = xcd_remap(blockIdx.x, gridDim.x);
-        const int m_tile = lin % a.m_tiles;
-        const int n_tile = lin / a.m_tiles;
-        const int m0     = m_tile * BM;
-        const int n0     = n_tile * BN;
-        const int split  = blockIdx.y;
-        const int wm0    = wmi * 32 * FM;
-        const int wn0    = wni * 32 * FN;
+        const int wmi = wave / WN;
+        const int wni = wave % WN;
+        const int wn0 = wni * 32 * FN;
 
         const int W   = a.W, H = a.H, HW = a.HW, OW = a.OW, OHW = a.OHW, S = a.SH;
         const int RS  = (W + 3) & ~1; // band row stride in pixels: W data + 1 or 2 zero pads (even)
@@ -1174,7 +1172,6 @@ namespace vkhip {
 #pragma unroll
         for (int t = 0; t < 9; ++t) tapoff[t] = ((t / 3 - 1) * RS + (t % 3 - 1)) * 8;
 
-        float16v acc[FM][FN];
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1247,7 +1244,191 @@ namespace vkhip {
                 compute(rel % NS, ks + NS - 1 < ks_end ? ks + NS - 1 : -1, (rel + NS - 1) % NS);
             }
         }
-        gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, 0, lane);
+    }
+
+    template <int FM, int FN, int WM, int WN, int KK, int NS, int NBI, bool ODD = false>
+    __global__ __launch_bounds__(64 * WM * WN, 1) void conv_halo_kernel(GemmArgs a) {
+        constexpr int BM = 32 * FM * WM;
+        constexpr int BN = 32 * FN * WN;
+        __shared__ __attribute__((aligned(16))) unsigned char sm[halo_lds_bytes<FM, WM, WN, KK, NS, NBI>()];
+        const int tid    = threadIdx.x;
+        const int lane   = tid & 63;
+        const int wave   = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int lin    = xcd_remap(blockIdx.x, gridDim.x);
+        const int m_tile = lin % a.m_tiles;
+        const int n0     = (lin / a.m_tiles) * BN;
+        const int split  = blockIdx.y;
+        float16v  acc[FM][FN];
+        halo_mainloop<FM, FN, WM, WN, KK, NS, NBI, ODD>(a, sm, acc, tid, lane, wave, m_tile, n0, split);
+        gemm_epilogue<FM, FN>(a, acc, m_tile * BM + (wave / WN) * 32 * FM, n0 + (wave % WN) * 32 * FN, split, 0, lane);
+    }
+
+    // ------------------------------------------------------------------ fused 3x3 -> 1x1 kernel
+    // A 3x3 conv (the halo main loop above, with the workgroup's M tile covering all BM = Cmid of
+    // its output channels: one wave row, WM = 1) followed by a 1x1 conv over those Cmid channels
+    // (a bottleneck's 3x3 then its 1x1 expansion), without the Cmid-channel intermediate leaving
+    // the registers. After the 3x3 main loop each wave holds all Cmid channels of its 32*FN pixels
+    // as fp32 MFMA results: acc[i][j][8h + t] is channel i*32 + (2h + t/4)*8 + 4g + t%4 (g = lane /
+    // 32) of pixel column j. Bias, activation and the fp16 rounding the separate conv's store
+    // applies turn them in place into the B operand of the 1x1: the 8 values of (i, h) are exactly
+    // one 16-deep K step of lane group g, so the 1x1 weights are prepacked with their K order
+    // permuted to match ([32-row fragment][step s = 2i + h][lane][8 halves], lane = g*32 + row%32,
+    // entry t = channel i*32 + (2h + t/4)*8 + 4g + t%4). The 1x1 then runs in chunks of 32*MC
+    // output channels: the chunk's weight fragments are loaded straight from global memory (they
+    // stay in L2; every wave reads the same ones) one chunk ahead, so they are in flight before the
+    // previous chunk's epilogue stores, and each chunk ends in the shared epilogue (bias, residual,
+    // activation, fp16 store) with the 1x1's arguments.
+    struct PwArgs {
+        const half_t *w;       // prepacked 1x1 weights, nchunks * MC fragments of 2*FM KB
+        int           nchunks; // ceil(Cout / (32 * MC))
+        GemmArgs      e;       // the 1x1's epilogue: bias, res, y, Cout / Coutb, P, OHW, act, ...
+    };
+
+    template <int FM, int FN, int WN, int KK, int NS, int NBI, bool ODD, int MC>
+    __global__ __launch_bounds__(64 * WN, 2) void conv_halo_pw_kernel(GemmArgs a, PwArgs p) {
+        constexpr int BN = 32 * FN * WN;
+        constexpr int KS = 2 * FM; // 16-deep K steps of the 1x1
+        __shared__ __attribute__((aligned(16))) unsigned char sm[halo_lds_bytes<FM, 1, WN, KK, NS, NBI>()];
+        const int tid  = threadIdx.x;
+        const int lane = tid & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int n0   = xcd_remap(blockIdx.x, gridDim.x) * BN; // m_tiles == 1
+        const int wn0  = wave * 32 * FN;
+        float16v  acc[FM][FN];
+        halo_mainloop<FM, FN, 1, WN, KK, NS, NBI, ODD>(a, sm, acc, tid, lane, wave, 0, n0, 0);
+
+        // the 3x3's epilogue without its store: bias, activation, fp16 -> the 1x1's B fragments
+        const int g = lane >> 5;
+        half8     bm[FM][2][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float4v b0 = *reinterpret_cast<const float4v *>(a.bias + i * 32 + (2 * h) * 8 + g * 4);
+                const float4v b1 = *reinterpret_cast<const float4v *>(a.bias + i * 32 + (2 * h + 1) * 8 + g * 4);
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    float4v lo = {acc[i][j][8 * h + 0], acc[i][j][8 * h + 1], acc[i][j][8 * h + 2], acc[i][j][8 * h + 3]};
+                    float4v hi = {acc[i][j][8 * h + 4], acc[i][j][8 * h + 5], acc[i][j][8 * h + 6], acc[i][j][8 * h + 7]};
+                    lo += b0;
+                    hi += b1;
+                    if (a.act == VKHIP_ACT_RELU) { // the bottleneck case, without the activation switch
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            lo[e] = fmaxf(lo[e], 0.f);
+                            hi[e] = fmaxf(hi[e], 0.f);
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            lo[e] = apply_act(lo[e], a.act, a.lo, a.hi);
+                            hi[e] = apply_act(hi[e], a.act, a.lo, a.hi);
+                        }
+                    }
+                    const half4 l4 = f4_to_h4(lo), h4 = f4_to_h4(hi);
+                    bm[i][h][j] = half8 {l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+                }
+            }
+
+        // The 1x1 in chunks of 32*MC output channels, software-pipelined one chunk deep: the next
+        // chunk's weight fragments and residual values are loaded before this chunk's MFMAs and
+        // stores (the vector memory counter retires in order, so they never wait behind the stores).
+        const GemmArgs &e   = p.e;
+        const half8    *W2  = reinterpret_cast<const half8 *>(p.w);
+        constexpr unsigned kInvalid = 0x80000000u;
+        const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc((void *) e.y, (short) 0, (int) e.y_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc((void *) (e.has_res ? e.res : e.y), (short) 0, (int) e.y_bytes, 0x00020000);
+        // per fragment column: the output pixel's byte offset at channel block 0 (or invalid)
+        unsigned pbase[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int px = n0 + wn0 + 32 * j + (lane & 31);
+            const int pn = px / e.OHW, pr = px - pn * e.OHW;
+            pbase[j]     = px < e.P ? (unsigned) ((pn * e.y_pstride * e.OHW + pr) * 8) : kInvalid;
+        }
+        // output offset of (chunk c, fragment mi, column j, row group qq): block ocb = 8(c*MC + mi) + 2qq + g
+        auto yoff = [&](int c, int mi, int j, int qq) __attribute__((always_inline)) {
+            const int ocb = 8 * (c * MC + mi) + 2 * qq + g;
+            return pbase[j] != kInvalid && ocb < e.Coutb ? pbase[j] + (unsigned) (ocb * e.OHW * 8) : kInvalid;
+        };
+        half8   an[MC][KS];
+        u32x2   rn[MC][FN][4];
+        float4v bn[MC][4];
+        auto load = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+            for (int mi = 0; mi < MC; ++mi) {
+#pragma unroll
+                for (int s = 0; s < KS; ++s) an[mi][s] = W2[((long long) ((c * MC + mi) * KS + s)) * 64 + lane];
+#pragma unroll
+                for (int qq = 0; qq < 4; ++qq) bn[mi][qq] = *reinterpret_cast<const float4v *>(e.bias + 32 * (c * MC + mi) + 8 * qq + 4 * g);
+            }
+            if (e.has_res) {
+#pragma unroll
+                for (int mi = 0; mi < MC; ++mi)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+#pragma unroll
+                        for (int qq = 0; qq < 4; ++qq) rn[mi][j][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff(c, mi, j, qq), 0, 0);
+            }
+        };
+        load(0);
+        for (int c = 0; c < p.nchunks; ++c) {
+            half8   ac[MC][KS];
+            u32x2   rc[MC][FN][4];
+            float4v bc[MC][4];
+#pragma unroll
+            for (int mi = 0; mi < MC; ++mi) {
+#pragma unroll
+                for (int s = 0; s < KS; ++s) ac[mi][s] = an[mi][s];
+#pragma unroll
+                for (int qq = 0; qq < 4; ++qq) bc[mi][qq] = bn[mi][qq];
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) rc[mi][j][qq] = rn[mi][j][qq];
+            }
+            if (c + 1 < p.nchunks) load(c + 1);
+            float16v acc2[MC][FN];
+#pragma unroll
+            for (int mi = 0; mi < MC; ++mi)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc2[mi][j][r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+#pragma unroll
+                for (int mi = 0; mi < MC; ++mi)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) acc2[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ac[mi][s], bm[s / 2][s % 2][j], acc2[mi][j], 0, 0, 0);
+            // epilogue: bias, residual, activation (compile-time), zero past Cout, fp16 store
+            auto epi = [&](auto act_c) __attribute__((always_inline)) {
+                constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+                for (int mi = 0; mi < MC; ++mi)
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) {
+                        const int oc = 32 * (c * MC + mi) + 8 * qq + 4 * g;
+#pragma unroll
+                        for (int j = 0; j < FN; ++j) {
+                            float4v v = {acc2[mi][j][qq * 4 + 0], acc2[mi][j][qq * 4 + 1], acc2[mi][j][qq * 4 + 2], acc2[mi][j][qq * 4 + 3]};
+                            v += bc[mi][qq];
+                            if (e.has_res) v += h4_to_f4(__builtin_bit_cast(half4, rc[mi][j][qq]));
+#pragma unroll
+                            for (int t = 0; t < 4; ++t) v[t] = oc + t < e.Cout ? apply_act(v[t], ACT, e.lo, e.hi) : 0.f;
+                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff(c, mi, j, qq), 0, 0);
+                        }
+                    }
+            };
+            switch (e.act) {
+                case VKHIP_ACT_RELU: epi(std::integral_constant<int, VKHIP_ACT_RELU> {}); break;
+                case VKHIP_ACT_RELU6: epi(std::integral_constant<int, VKHIP_ACT_RELU6> {}); break;
+                case VKHIP_ACT_CLIP: epi(std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
+                case VKHIP_ACT_HARDSWISH: epi(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
+                case VKHIP_ACT_SILU: epi(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
+                default: epi(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
+            }
+        }
     }
 
     // ------------------------------------------------------------------ stem kernel (Cin <= 4)
@@ -1448,6 +1629,9 @@ namespace vkhip {
     GemmKernelFn bd_tile_kernel(int tile, int bmode);
     GemmKernelFn dma_tile_kernel(int tile, int bmode, int steps, bool xs);
     GemmKernelFn halo_tile_kernel(int tile, int nbi);
+    typedef void (*PwKernelFn)(GemmArgs, PwArgs);
+    // the fused 3x3 -> 1x1 kernel for a mid width (64 or 128) and band size, or null
+    PwKernelFn pw_tile_kernel(int cmid, int nbi);
     // stem conv + 3x3/s2 max pool (stem_pool.hip): FM = 2 (64 output channels), WM = 1, WN waves
     // over FN fragments each, so BN = 32 FN WN GEMM columns = up to BN / OW conv rows; LDS holds the
     // conv tile (16 channel blocks x BN columns) plus a spare KB. Two configurations: 0 = 8 waves x
