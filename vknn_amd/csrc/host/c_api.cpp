@@ -78,12 +78,17 @@ extern "C" {
 const char *vknn_last_error(void) { return g_err.c_str(); }
 
 int vknn_model_io(const char *model, int64_t batch, int64_t *in_shape4, int64_t *out_elems, int32_t *n_out, int32_t max_out) {
-    std::vector<int64_t> in, out;
-    if (!vknn_zoo::io_shapes(model, batch, in, out)) return fail(std::string("unknown model ") + model);
-    for (int i = 0; i < 4; ++i) in_shape4[i] = in[i];
-    *n_out = (int32_t) out.size();
-    for (int i = 0; i < (int) out.size() && i < max_out; ++i) out_elems[i] = out[i];
-    return 0;
+    try {
+        if (!model || !in_shape4 || !n_out || (max_out > 0 && !out_elems)) return fail("model_io: null argument");
+        std::vector<int64_t> in, out;
+        if (!vknn_zoo::io_shapes(model, batch, in, out)) return fail(std::string("unknown model ") + model);
+        for (int i = 0; i < 4; ++i) in_shape4[i] = in[i];
+        *n_out = (int32_t) out.size();
+        for (int i = 0; i < (int) out.size() && i < max_out; ++i) out_elems[i] = out[i];
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 double vknn_model_flops(const char *model) {
@@ -203,9 +208,13 @@ int vknn_session_bind_device_input_as(vknn_session s, const void *dev_x, int32_t
 }
 
 int vknn_session_run_device(vknn_session s) {
-    if (!s) return fail("run_device: null session");
-    Status st = s->sess->runSegments();
-    return st == Status::Ok ? 0 : fail(std::string("run failed: ") + statusStr(st) + ": " + s->sess->lastError());
+    try {
+        if (!s) return fail("run_device: null session");
+        Status st = s->sess->runSegments();
+        return st == Status::Ok ? 0 : fail(std::string("run failed: ") + statusStr(st) + ": " + s->sess->lastError());
+    } catch (const std::exception &e) {
+        return fail(e.what());
+    }
 }
 
 int vknn_session_sync(vknn_session s) {
