@@ -36,7 +36,8 @@ EDGE = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.996, 65520.0, -65520.0, 1e
 
 
 @pytest.mark.parametrize("shape", [(1, 1, 1, 1), (1, 3, 5, 7), (2, 5, 3, 3), (2, 6, 4, 9), (1, 7, 11, 2),
-                                   (3, 64, 14, 14), (1, 3, 224, 224), (2, 5, 2, 2), (3, 1, 8, 6)])
+                                   (3, 64, 14, 14), (1, 3, 224, 224), (2, 5, 2, 2), (3, 1, 8, 6), (4, 8, 1, 1),
+                                   (3, 10, 1, 1), (2, 1000, 1, 1)])
 def test_pack_bitexact(gpu, shape):
     x = rng(1).standard_normal(shape).astype(np.float32) * 300
     flat = x.ravel()

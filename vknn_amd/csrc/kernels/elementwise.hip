@@ -120,6 +120,36 @@ namespace vkhip {
         dst[i]    = (float) src[((n * Cb + c / 4) * HW + p) * 4 + (c & 3)];
     }
 
+    // The same for H*W a multiple of 4: thread = 4 consecutive pixels of one 4-channel block (32
+    // contiguous bytes in) -> 4 channel planes x 4 pixels (one 16-byte store per plane).
+    __global__ void unpack_quad_kernel(const uint4 *src, float4 *dst, int C, int Cb, int HW4, int total) {
+        const int i = blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return;
+        const int q = i % HW4, t = i / HW4, cb = t % Cb, n = t / Cb;
+        const uint4 a = src[2 * i], b = src[2 * i + 1]; // pixels 4q, 4q+1 | 4q+2, 4q+3, 4 channels each
+        const half4 px[4] = {u2_as_h4(uint2 {a.x, a.y}), u2_as_h4(uint2 {a.z, a.w}), u2_as_h4(uint2 {b.x, b.y}), u2_as_h4(uint2 {b.z, b.w})};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int c = cb * 4 + k;
+            if (c < C) dst[((long long) n * C + c) * HW4 + q] = float4 {(float) px[0][k], (float) px[1][k], (float) px[2][k], (float) px[3][k]};
+        }
+    }
+
+    // The same for H*W == 1 (a classifier's [N, C] output): NCHW is channel-contiguous, so one
+    // 4-channel block (8 bytes in) is 4 consecutive floats out.
+    __global__ void unpack_vec_kernel(const uint2 *src, float *dst, int C, int Cb, int total) {
+        const int i = blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return;
+        const int   cb = i % Cb, n = i / Cb;
+        const half4 v  = u2_as_h4(src[i]);
+        float      *d  = dst + (long long) n * C + cb * 4;
+        if ((C & 3) == 0) *reinterpret_cast<float4 *>(d) = float4 {(float) v[0], (float) v[1], (float) v[2], (float) v[3]};
+        else
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (cb * 4 + k < C) d[k] = (float) v[k];
+    }
+
     // An empty one-wave dispatch: a separator in profiler traces between the launches of
     // consecutive operators (the id argument is not read).
     __global__ void dispatch_marker_kernel(int) {}
@@ -415,8 +445,14 @@ int vkhip_pack_nchw_f32(const float *src, void *dst, int64_t N, int64_t C, int64
 
 int vkhip_unpack_nchw_f32(const void *src, float *dst, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s) {
     if (!src || !dst || N <= 0 || C <= 0 || H <= 0 || W <= 0) return set_error(VKHIP_ERR_INVALID, "unpack: bad arguments");
-    int64_t Cb = ceil_div(C, 4), total = N * C * H * W;
-    unpack_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>((const half_t *) src, dst, C, H * W, Cb, total);
+    int64_t Cb = ceil_div(C, 4), total = N * C * H * W, HW = H * W;
+    if (HW % 4 == 0 && N * Cb * HW < INT32_MAX && ((uintptr_t) dst & 15) == 0) {
+        const int64_t quads = N * Cb * (HW / 4);
+        unpack_quad_kernel<<<grid1(quads), 256, 0, resolve_stream(s)>>>((const uint4 *) src, (float4 *) dst, (int) C, (int) Cb, (int) (HW / 4), (int) quads);
+    } else if (HW == 1 && N * Cb < INT32_MAX && ((uintptr_t) dst & 15) == 0) {
+        unpack_vec_kernel<<<grid1(N * Cb), 256, 0, resolve_stream(s)>>>((const uint2 *) src, dst, (int) C, (int) Cb, (int) (N * Cb));
+    } else
+        unpack_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>((const half_t *) src, dst, C, HW, Cb, total);
     return check_launch("unpack");
 }
 
