@@ -62,8 +62,11 @@ def timed_rows(rows, steps):
     return rows[packs[-steps]:]
 
 
+MARKER = "dispatch_marker_kernel"  # the empty per-operator separators of VKNN_HIP_OP_MARKERS=1
+
+
 def summarise(path, steps):
-    timed = timed_rows(list(csv.DictReader(open(path))), steps)
+    timed = [r for r in timed_rows(list(csv.DictReader(open(path))), steps) if not family(r["Kernel_Name"]).startswith(MARKER)]
     span_ns = int(timed[-1]["End_Timestamp"]) - int(timed[0]["Start_Timestamp"])
     fam = OrderedDict()
     for r in timed:
@@ -84,6 +87,8 @@ def counter_per_family(path, steps, counter):
     fam = OrderedDict()
     for r in timed:
         f = family(r["Kernel_Name"])
+        if f.startswith(MARKER):
+            continue
         e = fam.setdefault(f, [0, 0.0])
         e[0] += 1
         e[1] += float(r["Counter_Value"]) * 1024.0
