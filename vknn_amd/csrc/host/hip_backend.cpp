@@ -25,6 +25,7 @@
 #include <map>
 #include <mutex>
 #include <set>
+#include <sstream>
 
 namespace vknn {
 
@@ -223,7 +224,16 @@ namespace vknn {
                 // Candidates: every GEMM tile, split-K for low-parallelism shapes, Winograd if eligible.
                 std::vector<std::array<int32_t, 3>> cands;
                 const int ntiles = dw ? 0 : vkhip_conv_tile_count();
-                for (int t = 0; t < ntiles; ++t) cands.push_back({VKHIP_CONV_GEMM, t, 0});
+                // VKNN_HIP_SKIP_TILES=a,b,...: tiles the tuner leaves out (A/B measurements)
+                std::set<int> skipTiles;
+                if (const char *st = std::getenv("VKNN_HIP_SKIP_TILES")) {
+                    std::stringstream ss(st);
+                    std::string       tok;
+                    while (std::getline(ss, tok, ','))
+                        if (!tok.empty()) skipTiles.insert(std::atoi(tok.c_str()));
+                }
+                for (int t = 0; t < ntiles; ++t)
+                    if (!skipTiles.count(t)) cands.push_back({VKHIP_CONV_GEMM, t, 0});
                 if (dw) // the depthwise kernel's rows per strip
                     for (int rt: {4, 7, 14}) cands.push_back({VKHIP_CONV_DEPTHWISE, rt, 0});
                 vkhip_conv_plan base;
