@@ -240,7 +240,7 @@ int    vkhip_dwpw_forward(const vkhip_dwpw_desc *d, const void *x, const void *b
  * y = act(W1 t + b1 (+ res)). The reference runs them as two Conv nodes (ConvCpu,
  * src/backend/cpu/ops/conv.cpp:9-92, each with its fused epilogue); the intermediate never reaches
  * memory here. No reference counterpart as an entry point. conv: the 3x3 (pad 1, stride 1 or 2,
- * even W, Cin a multiple of 16, Cout = the mid width 64 or 128, has_res = 0); Cout, act and
+ * even W, Cin a multiple of 16, Cout = the mid width 64, has_res = 0); Cout, act and
  * has_res: the 1x1 (stride 1, no padding). */
 typedef struct vkhip_convpw_desc {
     vkhip_conv_desc conv;
@@ -256,6 +256,22 @@ int vkhip_convpw_pack_weights(const vkhip_convpw_desc *d, const vkhip_conv_plan 
                               const float *b1, void *blob);
 int vkhip_convpw_forward(const vkhip_convpw_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res, void *y,
                          vkhip_stream_t s);
+/* The pair above chained with a second 1x1 that reads the pair's output (the next bottleneck's
+ * reduction): y2 = act3(W2 y + b2), accumulated chunk by chunk from the fp16 values the pair stores
+ * to y, so y is written once and not read back. 64 mid channels and Cout3 <= 64 only; y is still
+ * written in full (the next block's residual). No reference counterpart (three Conv nodes there). */
+typedef struct vkhip_convpw2_desc {
+    vkhip_convpw_desc pw;
+    int32_t           Cout3;
+    int32_t           act3;
+    float             act3_lo, act3_hi;
+} vkhip_convpw2_desc;
+int vkhip_convpw2_plan(const vkhip_convpw2_desc *d, vkhip_conv_plan *plan);
+/* w2 [Cout3][pw.Cout] fp32, b2 [Cout3] or null; the rest as vkhip_convpw_pack_weights. */
+int vkhip_convpw2_pack_weights(const vkhip_convpw2_desc *d, const vkhip_conv_plan *plan, const float *w3, const float *b3, const float *w1,
+                               const float *b1, const float *w2, const float *b2, void *blob);
+int vkhip_convpw2_forward(const vkhip_convpw2_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res, void *y,
+                          void *y2, vkhip_stream_t s);
 
 /* ---------------------------------------------------------------- squeeze-excite + pooling
  * Global average pool: x [N,C,H,W] -> y [N,C,1,1] (both NC4HW4 fp16; fp32 accumulation). */

@@ -490,8 +490,8 @@ def gpu_convpw(x, w3, b3, stride, act3, w1, b1, act1, res=None):
 @pytest.mark.parametrize("N,Cin,H,W,Cmid,Cout,S,act3,act1,res", [
     (2, 64, 14, 14, 64, 256, 1, 1, 1, True),     # layer-1 bottleneck shape, small map
     (1, 32, 9, 10, 64, 40, 1, 2, 2, False),      # ragged: odd H, Cout not a multiple of 32
-    (2, 256, 16, 16, 128, 512, 2, 1, 1, True),   # layer-2 first block: stride 2, 128 mid channels
-    (3, 128, 12, 8, 128, 100, 1, 5, 0, False),   # SiLU mid, no 1x1 activation, 3 images across workgroups
+    (2, 256, 16, 16, 64, 256, 2, 1, 1, True),    # stride 2
+    (3, 128, 12, 8, 64, 100, 1, 5, 0, False),    # SiLU mid, no 1x1 activation, 3 images across workgroups
 ])
 def test_convpw(gpu, N, Cin, H, W, Cmid, Cout, S, act3, act1, res):
     """3x3 (+bias, act, fp16 rounding) then 1x1 (+bias, residual, act) in one kernel against the
@@ -513,11 +513,59 @@ def test_convpw(gpu, N, Cin, H, W, Cmid, Cout, S, act3, act1, res):
         assert np.all(raw[:, -1, :, :, Cout % 4:] == 0)
 
 
+@pytest.mark.parametrize("N,Cin,H,W,Cout,Cout3,res", [
+    (2, 64, 14, 14, 256, 64, True),   # layer-1 bottleneck then the next block's reduction
+    (1, 32, 9, 10, 72, 40, False),    # ragged: Cout and Cout3 not multiples of 32, odd H
+    (3, 64, 8, 8, 128, 24, True),     # one chained fragment (Cout3 <= 32)
+])
+def test_convpw2_chain(gpu, N, Cin, H, W, Cout, Cout3, res):
+    """3x3 -> 1x1 (+residual) -> 1x1 in one kernel: y against the oracle and bit-equal to the pair
+    kernel; y2 against the oracle's 1x1 over y rounded to fp16 (what the chained 1x1 reads)."""
+    lib = V.vkhip()
+    r = rng(N * 100 + Cin + Cout + Cout3)
+    x = round_half(r.standard_normal((N, Cin, H, W)))
+    w3 = (r.standard_normal((64, Cin, 3, 3)) * np.sqrt(2.0 / (9 * Cin))).astype(np.float32)
+    b3 = (r.standard_normal(64) * 0.1).astype(np.float32)
+    w1 = (r.standard_normal((Cout, 64)) * np.sqrt(2.0 / 64)).astype(np.float32)
+    b1 = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    w2 = (r.standard_normal((Cout3, Cout)) * np.sqrt(2.0 / Cout)).astype(np.float32)
+    b2 = (r.standard_normal(Cout3) * 0.1).astype(np.float32)
+    rs = round_half(r.standard_normal((N, Cout, H, W))) if res else None
+    d3, _ = conv_desc(x.shape, w3.shape, (1, 1), (1, 1, 1, 1), act=1)
+    pw = V.ConvPwDesc(conv=d3, Cout=Cout, act=1, act_lo=0.0, act_hi=0.0, has_res=int(res))
+    d = V.ConvPw2Desc(pw=pw, Cout3=Cout3, act3=1, act3_lo=0.0, act3_hi=0.0)
+    plan = V.ConvPlan()
+    check(lib.vkhip_convpw2_plan(ctypes.byref(d), ctypes.byref(plan)), "convpw2 plan")
+    blob = np.zeros(plan.weight_bytes, np.uint8)
+    check(lib.vkhip_convpw2_pack_weights(ctypes.byref(d), ctypes.byref(plan), w3.ctypes.data, b3.ctypes.data, w1.ctypes.data,
+                                         b1.ctypes.data, w2.ctypes.data, b2.ctypes.data, blob.ctypes.data), "convpw2 pack")
+    dblob, dx = DeviceBuffer.from_array(blob), to_device_nc4(x)
+    dres = to_device_nc4(rs) if res else None
+    yshape, y2shape = (N, Cout, H, W), (N, Cout3, H, W)
+    dy, dy2 = DeviceBuffer(V.nc4_elems(*yshape) * 2), DeviceBuffer(V.nc4_elems(*y2shape) * 2)
+    dy.zero()
+    dy2.zero()
+    check(lib.vkhip_convpw2_forward(ctypes.byref(d), ctypes.byref(plan), dx.ptr, dblob.ptr, dres.ptr if dres else None, dy.ptr, dy2.ptr,
+                                    None), "convpw2")
+    check(lib.vkhip_stream_sync(None), "sync")
+    y, y2 = from_device_nc4(dy, yshape), from_device_nc4(dy2, y2shape)
+    pair, _, _ = gpu_convpw(x, w3, b3, (1, 1), 1, w1.reshape(Cout, 64, 1, 1), b1, 1, rs)
+    assert np.array_equal(y, pair)
+    mid = round_half(oracle_conv(x, w3, b3, (1, 1), (1, 1, 1, 1), act=1))
+    yref = oracle_conv(mid, w1.reshape(Cout, 64, 1, 1), b1, res=rs, act=1)
+    assert_parity(y, yref, f"convpw2 y N{N} {H}x{W} {Cout}")
+    y2ref = oracle_conv(round_half(yref), w2.reshape(Cout3, Cout, 1, 1), b2, act=1)
+    assert_parity(y2, y2ref, f"convpw2 y2 N{N} {H}x{W} {Cout}->{Cout3}")
+    if Cout3 % 4:
+        raw = raw_nc4(dy2, y2shape).reshape(N, -1, H, W, 4)
+        assert np.all(raw[:, -1, :, :, Cout3 % 4:] == 0)
+
+
 def test_convpw_rejects_unsupported(gpu):
-    """Mid widths other than 64/128, 1x1 or padded-wrong convs and a 3x3 with a residual have no
+    """Mid widths other than 64, 1x1 or padded-wrong convs and a 3x3 with a residual have no
     fused kernel: the plan call says so and launches nothing."""
     lib = V.vkhip()
-    for shape, w, kw in [((1, 64, 8, 8), (96, 64, 3, 3), {}), ((1, 64, 8, 8), (64, 64, 1, 1), {}),
+    for shape, w, kw in [((1, 64, 8, 8), (96, 64, 3, 3), {}), ((1, 64, 8, 8), (128, 64, 3, 3), {}), ((1, 64, 8, 8), (64, 64, 1, 1), {}),
                          ((1, 64, 8, 8), (64, 64, 3, 3), {"has_res": 1})]:
         d3, _ = conv_desc(shape, w, (1, 1), (1, 1, 1, 1) if w[2] == 3 else (0, 0, 0, 0), **kw)
         d = V.ConvPwDesc(conv=d3, Cout=256, act=1, act_lo=0.0, act_hi=0.0, has_res=0)

@@ -48,6 +48,10 @@ class ConvPwDesc(ctypes.Structure):
                 ("has_res", c_i32)]
 
 
+class ConvPw2Desc(ctypes.Structure):
+    _fields_ = [("pw", ConvPwDesc), ("Cout3", c_i32), ("act3", c_i32), ("act3_lo", c_f), ("act3_hi", c_f)]
+
+
 class PoolDesc(ctypes.Structure):
     _fields_ = [(n, c_i32) for n in ("N", "C", "H", "W", "OH", "OW", "KH", "KW", "SH", "SW", "PT", "PL")]
 
@@ -101,6 +105,9 @@ VKHIP_API = {
     "vkhip_convpw_plan": (c_int, [P(ConvPwDesc), P(ConvPlan)]),
     "vkhip_convpw_pack_weights": (c_int, [P(ConvPwDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_convpw_forward": (c_int, [P(ConvPwDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "vkhip_convpw2_plan": (c_int, [P(ConvPw2Desc), P(ConvPlan)]),
+    "vkhip_convpw2_pack_weights": (c_int, [P(ConvPw2Desc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    "vkhip_convpw2_forward": (c_int, [P(ConvPw2Desc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_forward_stages": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp]),
     "vkhip_conv_forward_scaled": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_pool_parts": (c_int, [P(ConvDesc), P(ConvPlan)]),

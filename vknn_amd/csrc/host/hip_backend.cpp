@@ -824,11 +824,14 @@ namespace vknn {
         // choice is kept in the tune table).
         struct ConvPwOp: HipOp {
             const Node             *n3 = nullptr; // the 3x3 node (this op is prepared with the 1x1 node)
-            ConvOp                  c3, c1;
+            const Node             *n4 = nullptr; // optional: a 1x1 reading the pair's output (the chain)
+            ConvOp                  c3, c1, c4;
             vkhip_convpw_desc       pd {};
-            vkhip_conv_plan         plan {};
-            std::shared_ptr<DevBuf> blob;
-            bool                    split = true;
+            vkhip_convpw2_desc      pd2 {};
+            vkhip_conv_plan         plan {}, plan2 {};
+            std::shared_ptr<DevBuf> blob, blob2;
+            // 0: fused pair (then c4 on its own), 1: split (c3, c1, c4), 2: the chained kernel
+            int                     mode = 1;
 
             void prepare(const Node &node, SegEnv &env) override {
                 const Graph &g = *env.graph;
@@ -836,54 +839,77 @@ namespace vknn {
                 c1.name = node.name;
                 c3.prepare(*n3, env);
                 c1.prepare(node, env);
+                if (n4) {
+                    c4.name = n4->name;
+                    c4.prepare(*n4, env);
+                }
                 kind  = "convpw";
-                flops = c3.flops + c1.flops;
-                bytes = c3.bytes + c1.bytes;
+                flops = c3.flops + c1.flops + (n4 ? c4.flops : 0);
+                bytes = c3.bytes + c1.bytes + (n4 ? c4.bytes : 0);
                 pd.conv = c3.d;
                 pd.Cout = c1.d.Cout; pd.act = c1.d.act; pd.act_lo = c1.d.act_lo; pd.act_hi = c1.d.act_hi; pd.has_res = c1.d.has_res;
                 if (!env.tunable || vkhip_convpw_plan(&pd, &plan) != VKHIP_OK) return;
-                std::vector<uint8_t> host(plan.weight_bytes);
-                std::vector<float>   w1(initF32(g, node.inputs[1]), initF32(g, node.inputs[1]) + (size_t) pd.Cout * pd.conv.Cout);
+                std::vector<float> w1(initF32(g, node.inputs[1]), initF32(g, node.inputs[1]) + (size_t) pd.Cout * pd.conv.Cout);
+                std::vector<uint8_t> host(plan.weight_bytes), host2;
                 check(vkhip_convpw_pack_weights(&pd, &plan, initF32(g, n3->inputs[1]), initF32(g, biasOf(*n3)), w1.data(), initF32(g, biasOf(node)),
                                                 host.data()),
                       "convpw pack");
-                std::string key = gpuTag() + "/convpw";
-                for (int v: {pd.conv.N, pd.conv.Cin, pd.conv.H, pd.conv.W, pd.conv.Cout, pd.conv.SH, pd.Cout, pd.has_res, c3.plan.tile, c1.plan.tile})
+                bool chain = false;
+                if (n4) {
+                    pd2.pw = pd;
+                    pd2.Cout3 = c4.d.Cout; pd2.act3 = c4.d.act; pd2.act3_lo = c4.d.act_lo; pd2.act3_hi = c4.d.act_hi;
+                    if (vkhip_convpw2_plan(&pd2, &plan2) == VKHIP_OK) {
+                        host2.resize(plan2.weight_bytes);
+                        check(vkhip_convpw2_pack_weights(&pd2, &plan2, initF32(g, n3->inputs[1]), initF32(g, biasOf(*n3)), w1.data(),
+                                                         initF32(g, biasOf(node)), initF32(g, n4->inputs[1]), initF32(g, biasOf(*n4)), host2.data()),
+                              "convpw2 pack");
+                        chain = true;
+                    }
+                }
+                std::string key = gpuTag() + (n4 ? "/convpw2" : "/convpw");
+                for (int v: {pd.conv.N, pd.conv.Cin, pd.conv.H, pd.conv.W, pd.conv.Cout, pd.conv.SH, pd.Cout, pd.has_res, c3.plan.tile, c1.plan.tile,
+                             n4 ? c4.d.Cout : 0, n4 ? c4.plan.tile : 0})
                     key += "_" + std::to_string(v);
                 int32_t cached = 0;
-                if (TuneCache::instance().get(key, cached)) split = cached != 0;
-                else {
-                    blob  = upload(host.data(), host.size());
-                    split = timeSplit(g) <= timeFused();
-                    TuneCache::instance().put(key, split ? 1 : 0);
+                if (!TuneCache::instance().get(key, cached) || (cached == 2 && !chain)) {
+                    blob = upload(host.data(), host.size());
+                    if (chain) blob2 = upload(host2.data(), host2.size());
+                    const double ts = timeRuns(1), tf = timeRuns(0), tc = chain ? timeRuns(2) : 1e30;
+                    cached = ts <= std::min(tf, tc) ? 1 : (tc < tf ? 2 : 0);
+                    TuneCache::instance().put(key, cached);
                 }
-                if (split) {
-                    blob.reset();
-                    return;
-                }
-                if (!blob) blob = upload(host.data(), host.size());
+                mode = cached;
+                if (mode != 0) blob.reset();
+                if (mode != 2) blob2.reset();
+                if (mode == 1) return;
+                if (mode == 0 && !blob) blob = upload(host.data(), host.size());
+                if (mode == 2 && !blob2) blob2 = upload(host2.data(), host2.size());
                 const vkhip_conv_desc &c = pd.conv;
                 bytes = (int64_t) (nc4Bytes({c.N, c.Cin, c.H, c.W}) + nc4Bytes({c.N, pd.Cout, c.OH, c.OW}) * (pd.has_res ? 2 : 1)) +
                         (int64_t) c.Cout * (c.Cin * 9 + pd.Cout) * 2;
+                if (n4) bytes += mode == 2 ? (int64_t) nc4Bytes({c.N, c4.d.Cout, c.OH, c.OW}) + (int64_t) c4.d.Cout * pd.Cout * 2 : c4.bytes;
             }
 
-            // Rotating buffer sets (input, intermediate, residual, output) whose total exceeds the
-            // 256 MB last-level cache, so both alternatives are timed from HBM as in a forward pass.
+            // Rotating buffer sets (input, intermediate, residual, output, chained output) whose total
+            // exceeds the 256 MB last-level cache, so every alternative is timed from HBM as in a
+            // forward pass.
             struct Set {
-                std::shared_ptr<DevBuf> x, m, r, y;
+                std::shared_ptr<DevBuf> x, m, r, y, y2;
             };
             std::vector<Set> sets_;
             void makeSets() {
                 if (!sets_.empty()) return;
                 const vkhip_conv_desc &c = pd.conv;
                 const size_t xb = nc4Bytes({c.N, c.Cin, c.H, c.W}), mb = nc4Bytes({c.N, c.Cout, c.OH, c.OW}), yb = nc4Bytes({c.N, pd.Cout, c.OH, c.OW});
-                const size_t one = xb + mb + yb * (pd.has_res ? 2 : 1);
+                const size_t y2b = n4 ? nc4Bytes({c.N, c4.d.Cout, c.OH, c.OW}) : 0;
+                const size_t one = xb + mb + yb * (pd.has_res ? 2 : 1) + y2b;
                 const int    n   = (int) std::min<size_t>(6, std::max<size_t>(1, ((size_t) 640 << 20) / std::max<size_t>(one, 1) + 1));
                 for (int k = 0; k < n; ++k) {
                     Set t;
                     t.x = std::make_shared<DevBuf>(xb);
                     t.m = std::make_shared<DevBuf>(mb);
                     t.y = std::make_shared<DevBuf>(yb);
+                    if (n4) t.y2 = std::make_shared<DevBuf>(y2b);
                     check(vkhip_fill_zero(t.x->ptr, xb, nullptr), "convpw tune fill");
                     if (pd.has_res) {
                         t.r = std::make_shared<DevBuf>(yb);
@@ -892,7 +918,19 @@ namespace vknn {
                     sets_.push_back(t);
                 }
             }
-            double timeRuns(const std::function<void(const Set &)> &run) {
+            void launch(int m, const void *x, const void *mid, const void *r, void *y, void *y2, vkhip_stream_t s) {
+                if (m == 2) {
+                    check(vkhip_convpw2_forward(&pd2, &plan2, x, blob2->ptr, r, y, y2, s), "convpw2 " + name);
+                    return;
+                }
+                if (m == 0) check(vkhip_convpw_forward(&pd, &plan, x, blob->ptr, r, y, s), "convpw " + name);
+                else {
+                    check(c3.forward(c3.plan, x, nullptr, c3.blob->ptr, nullptr, (void *) mid, c3.ws ? c3.ws->ptr : nullptr, s), "convpw 3x3 " + name);
+                    check(c1.forward(c1.plan, mid, nullptr, c1.blob->ptr, r, y, c1.ws ? c1.ws->ptr : nullptr, s), "convpw 1x1 " + name);
+                }
+                if (n4) check(c4.forward(c4.plan, y, nullptr, c4.blob->ptr, nullptr, y2, c4.ws ? c4.ws->ptr : nullptr, s), "convpw chained 1x1 " + name);
+            }
+            double timeRuns(int m) {
                 makeSets();
                 vkhip_event_t e0, e1;
                 check(vkhip_event_create(&e0), "event");
@@ -901,7 +939,10 @@ namespace vknn {
                 size_t k    = 0;
                 for (int r = 0; r < 5; ++r) {
                     vkhip_event_record(e0, nullptr);
-                    for (int i = 0; i < 6; ++i) run(sets_[k++ % sets_.size()]);
+                    for (int i = 0; i < 6; ++i) {
+                        const Set &t = sets_[k++ % sets_.size()];
+                        launch(m, t.x->ptr, t.m->ptr, t.r ? t.r->ptr : nullptr, t.y->ptr, t.y2 ? t.y2->ptr : nullptr, nullptr);
+                    }
                     vkhip_event_record(e1, nullptr);
                     vkhip_event_sync(e1);
                     float ms = 0;
@@ -912,31 +953,16 @@ namespace vknn {
                 vkhip_event_destroy(e1);
                 return best;
             }
-            double timeFused() {
-                return timeRuns([&](const Set &t) {
-                    check(vkhip_convpw_forward(&pd, &plan, t.x->ptr, blob->ptr, t.r ? t.r->ptr : nullptr, t.y->ptr, nullptr), "convpw tune");
-                });
-            }
-            double timeSplit(const Graph &) {
-                return timeRuns([&](const Set &t) {
-                    check(c3.forward(c3.plan, t.x->ptr, nullptr, c3.blob->ptr, nullptr, t.m->ptr, c3.ws ? c3.ws->ptr : nullptr, nullptr), "convpw tune 3x3");
-                    check(c1.forward(c1.plan, t.m->ptr, nullptr, c1.blob->ptr, t.r ? t.r->ptr : nullptr, t.y->ptr, c1.ws ? c1.ws->ptr : nullptr, nullptr),
-                          "convpw tune 1x1");
-                });
-            }
 
             void record(SegEnv &env, vkhip_stream_t s) override {
-                if (split) {
-                    c3.record(env, s);
-                    c1.record(env, s);
-                    return;
-                }
-                check(vkhip_convpw_forward(&pd, &plan, env.dev(c3.in), blob->ptr, c1.res != kNoTensor ? env.dev(c1.res) : nullptr, env.dev(c1.out), s),
-                      "convpw " + name);
+                launch(mode, env.dev(c3.in), env.dev(c3.out), c1.res != kNoTensor ? env.dev(c1.res) : nullptr, env.dev(c1.out),
+                       n4 ? env.dev(c4.out) : nullptr, s);
             }
             std::string describe() const override {
-                return split ? "split: " + c3.name + " (" + c3.describe() + ") then 1x1 " + c1.describe()
-                             : "fused 3x3 + 1x1 (" + c3.name + " in registers) kernel=conv_halo_pw_kernel";
+                const std::string chained = n4 ? " then 1x1 " + c4.name + " (" + c4.describe() + ")" : "";
+                if (mode == 1) return "split: " + c3.name + " (" + c3.describe() + ") then 1x1 " + c1.describe() + chained;
+                if (mode == 2) return "fused 3x3 + 1x1 + 1x1 (" + c3.name + " in registers, " + c4.name + " chained) kernel=conv_halo_pw_kernel";
+                return "fused 3x3 + 1x1 (" + c3.name + " in registers) kernel=conv_halo_pw_kernel" + chained;
             }
         };
 
@@ -1212,6 +1238,8 @@ namespace vknn {
             // VKNN_HIP_FUSE_PW=0 keeps every conv on its own (A/B).
             std::map<int, int> pwPairs; // 1x1 node -> 3x3 node
             std::set<int>      pwFolded; // 3x3 nodes of the pairs
+            std::map<int, int> pwChain;  // 1x1 node of a pair -> the 1x1 chained after it
+            std::set<int>      pwChained;
             {
                 const char *pw_env = std::getenv("VKNN_HIP_FUSE_PW");
                 if (!pw_env || std::string(pw_env) != "0") {
@@ -1229,6 +1257,28 @@ namespace vknn {
                         if (view) continue;
                         pwPairs[kv.first] = kv.second;
                         pwFolded.insert(kv.second);
+                    }
+                    // chains: a 1x1 stride-1 conv of at most 64 outputs, no residual, reading a pair's
+                    // output (the next bottleneck's reduction) runs inside the pair's op
+                    std::set<int> inSeg(idx.begin(), idx.end());
+                    for (auto &kv: pwPairs) {
+                        const TensorId t = g.nodes[kv.first].outputs[0];
+                        for (int r: idx) {
+                            const Node &nr = g.nodes[r];
+                            if (r == kv.first || skip.count(r) || pwPairs.count(r) || pwFolded.count(r) || pwChained.count(r)) continue;
+                            if (nr.type != OpType::Conv || nr.inputs.size() < 2 || nr.inputs[0] != t || nr.fusedResidual != kNoTensor ||
+                                !g.isInitializer(nr.inputs[1]) || nr.outputs.empty())
+                                continue;
+                            const Shape &ws = g.desc(nr.inputs[1]).shape;
+                            auto st = attrInts(nr, "strides", {1, 1}), pad = attrInts(nr, "pads", {0, 0, 0, 0});
+                            if (ws.size() != 4 || ws[2] != 1 || ws[3] != 1 || ws[0] > 64 || st[0] != 1 || st[1] != 1 || pad[0] || pad[1] || pad[2] ||
+                                pad[3] || nr.attr.geti("group", 1) != 1)
+                                continue;
+                            if (place_.count(resolve(nr.outputs[0])) || pstride(nr.outputs[0]) > 0) continue;
+                            pwChain[kv.first] = r;
+                            pwChained.insert(r);
+                            break;
+                        }
                     }
                 }
             }
@@ -1279,9 +1329,16 @@ namespace vknn {
                     for (auto &kv: pwPairs)
                         if (kv.second == i) f->into = g.nodes[kv.first].name;
                     op = std::move(f);
+                } else if (pwChained.count(i)) {
+                    auto f = std::make_unique<FoldedMulOp>();
+                    f->what = "1x1 conv: runs with the 3x3 + 1x1 pair whose output it reads,";
+                    for (auto &kv: pwChain)
+                        if (kv.second == i) f->into = g.nodes[kv.first].name;
+                    op = std::move(f);
                 } else if (pwPairs.count(i)) {
                     auto c = std::make_unique<ConvPwOp>();
                     c->n3  = &g.nodes[pwPairs[i]];
+                    if (pwChain.count(i)) c->n4 = &g.nodes[pwChain[i]];
                     op     = std::move(c);
                 } else op = makeOp(g, nd);
                 if (!op) throw Error(Status::Unsupported, std::string("HIP backend has no kernel for ") + opTypeName(nd.type) + " (" + nd.name + ")");
@@ -1303,7 +1360,7 @@ namespace vknn {
                 op->name = nd.name;
                 op->type = nd.type;
                 const bool gapFolded = gapParts.count(i) > 0;
-                const bool pwOp = pwPairs.count(i) || pwFolded.count(i);
+                const bool pwOp = pwPairs.count(i) || pwFolded.count(i) || pwChained.count(i);
                 if (nd.type == OpType::Conv && !inPlace && !gapFolded && !folded.count(i) && !pools.count(i) && !pwOp) {
                     bool v = false;
                     for (TensorId t: {nd.inputs[0], nd.outputs[0]}) v = v || pstride(t) > 0;
@@ -1343,7 +1400,7 @@ namespace vknn {
                     outs.push_back(out);
                     continue;
                 }
-                if (folded.count(i) || pools.count(i) || pwFolded.count(i)) {
+                if (folded.count(i) || pools.count(i) || pwFolded.count(i) || pwChained.count(i)) {
                     ins.push_back(in);
                     outs.push_back(out);
                     continue;
@@ -1353,6 +1410,7 @@ namespace vknn {
                     in.push_back(resolve(g.nodes[pwPairs[i]].inputs[0]));
                     if (nd.fusedResidual != kNoTensor) in.push_back(resolve(nd.fusedResidual));
                     out.push_back(resolve(nd.outputs[0]));
+                    if (pwChain.count(i)) out.push_back(resolve(g.nodes[pwChain[i]].outputs[0]));
                     ins.push_back(in);
                     outs.push_back(out);
                     continue;

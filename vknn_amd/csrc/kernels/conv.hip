@@ -1113,12 +1113,11 @@ namespace vkhip {
         int     MC;        // 32-row 1x1 fragments per chunk
     };
     static bool pw_tile(int cmid, PwTile &p) {
-        if (cmid == 64) p = {18, {64, 256, 1, 4, 3, 2, 2, 1}, 1};
-        else if (cmid == 128) p = {17, {128, 128, 1, 4, 3, 4, 1, 1}, 1};
-        else return false;
+        if (cmid != 64) return false;
+        p = {18, {64, 256, 1, 4, 3, 2, 2, 1}, 1};
         return true;
     }
-    static constexpr int kPwMaxNBI64 = 15, kPwMaxNBI128 = 10;
+    static constexpr int kPwMaxNBI64 = 15;
 
     // 1x1 parts of the blob, after the 3x3 plan's weight bytes: bias [nchunks * 32 * MC] fp32, then
     // the weights [nchunks * MC fragments][2 * FM steps][64 lanes][8 halves]
@@ -1141,12 +1140,17 @@ namespace vkhip {
     static int pw_check(const vkhip_convpw_desc *d, PwTile &pt, vkhip_conv_plan &p3) {
         if (!d) return set_error(VKHIP_ERR_INVALID, "convpw: null descriptor");
         const vkhip_conv_desc &c = d->conv;
-        if (!pw_tile(c.Cout, pt)) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw: mid width %d (64 or 128 only)", c.Cout);
+        if (!pw_tile(c.Cout, pt)) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw: mid width %d (64 only)", c.Cout);
         if (c.has_res || c.in_scale || c.N <= 0 || d->Cout <= 0 || c.W % 2) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw: 3x3 with a residual, an input scale or odd width");
         if (!halo_shape_ok(&c, pt.t)) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw: not a halo-tile 3x3 (pad 1, stride 1/2, Cin %% 16 == 0)");
         const int nbi = halo_nbi(&c, pt.t);
-        if (nbi > (c.Cout == 64 ? kPwMaxNBI64 : kPwMaxNBI128) || !pw_tile_kernel(c.Cout, nbi))
+        int       lds = 0;
+        if (nbi > kPwMaxNBI64 || !pw_tile_kernel(c.Cout, nbi, 0, &lds))
             return set_error(VKHIP_ERR_UNSUPPORTED, "convpw: input band too large for LDS");
+        // the 1x1 weights and bias are staged in the kernel's LDS ring
+        const int64_t nch = ceil_div(d->Cout, 32 * pt.MC);
+        if ((nch * pt.MC * 2 * (c.Cout / 32) + ceil_div(nch * pt.MC * 32 * 4, 1024)) * 1024 > lds)
+            return set_error(VKHIP_ERR_UNSUPPORTED, "convpw: 1x1 weights do not fit the kernel's LDS");
         const int64_t P = (int64_t) c.N * c.OH * c.OW;
         if (P * ceil_div(std::max(c.Cin, d->Cout), 4) * 8 >= (1LL << 31) || (int64_t) c.N * ceil_div(c.Cin, 4) * c.H * c.W * 8 >= (1LL << 31))
             return set_error(VKHIP_ERR_UNSUPPORTED, "convpw: tensor >= 2 GiB");
@@ -1158,6 +1162,90 @@ namespace vkhip {
         p3.tile         = pt.halo_tile;
         p3.weight_bytes = align256((size_t) g.Coutp * 4) + (size_t) g.Coutp * g.Kp * 2;
         return VKHIP_OK;
+    }
+
+    // The chained second 1x1 (vkhip_convpw2_*): after the pair's blob, its bias [32 * MR] fp32 and
+    // weights [MR fragments][2 * nchunks steps][64][8 halves].
+    struct PwChain {
+        PwLayout pair;
+        int      MR;
+        size_t   off_b2, off_w2, bytes;
+    };
+    static int pw_chain(const vkhip_convpw2_desc *d, const PwTile &pt, const vkhip_conv_plan &p3, PwChain &ch) {
+        if (d->pw.conv.Cout != 64 || pt.MC != 1 || d->Cout3 <= 0 || d->Cout3 > 64)
+            return set_error(VKHIP_ERR_UNSUPPORTED, "convpw2: the chained 1x1 needs 64 mid channels and at most 64 outputs");
+        ch.pair = pw_layout(&d->pw, pt, p3.weight_bytes);
+        ch.MR   = (int) ceil_div(d->Cout3, 32);
+        int lds = 0;
+        if (!pw_tile_kernel(64, halo_nbi(&d->pw.conv, pt.t), ch.MR, &lds)) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw2: no chained kernel for this band");
+        const int64_t kb = ch.pair.frags * ch.pair.steps + ceil_div(ch.pair.frags * 32 * 4, 1024) + ch.MR * 2 * ch.pair.nchunks + 1;
+        if (kb * 1024 > lds) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw2: weights do not fit the kernel's LDS");
+        ch.off_b2 = align256(ch.pair.bytes);
+        ch.off_w2 = ch.off_b2 + align256((size_t) ch.MR * 32 * 4);
+        ch.bytes  = ch.off_w2 + (size_t) ch.MR * 2 * ch.pair.nchunks * 1024;
+        return VKHIP_OK;
+    }
+
+    static int convpw_forward_impl(const vkhip_convpw_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res,
+                                   void *y, const vkhip_convpw2_desc *d2, void *y2, vkhip_stream_t s) {
+        if (!plan || !x || !blob || !y) return set_error(VKHIP_ERR_INVALID, "convpw_forward: null argument");
+        PwTile          pt;
+        vkhip_conv_plan p3;
+        int rc = pw_check(d, pt, p3);
+        if (rc) return rc;
+        const PwLayout L = pw_layout(d, pt, p3.weight_bytes);
+        PwChain        ch {};
+        if (d2 && (rc = pw_chain(d2, pt, p3, ch))) return rc;
+        if (plan->weight_bytes != (d2 ? ch.bytes : L.bytes)) return set_error(VKHIP_ERR_INVALID, "convpw_forward: plan does not match the descriptor");
+        if (d->has_res && !res) return set_error(VKHIP_ERR_INVALID, "convpw_forward: has_res without a residual tensor");
+        const vkhip_conv_desc &c = d->conv;
+        const int              nbi = halo_nbi(&c, pt.t);
+        PwKernelFn             fn  = pw_tile_kernel(c.Cout, nbi, d2 ? ch.MR : 0, nullptr);
+        if (!fn) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw_forward: no kernel for band %d", nbi);
+        ConvGeom g = gemm_geom(&c, pt.halo_tile, false);
+        GemmArgs a;
+        std::memset(&a, 0, sizeof(a));
+        a.x = (const uint2 *) x;
+        a.w = (const half_t *) ((const char *) blob + align256((size_t) g.Coutp * 4));
+        a.bias = (const float *) blob;
+        a.Cinb = (int) g.Cinb; a.Coutb = (int) g.Coutb; a.Cout = c.Cout;
+        a.P = (int) g.P; a.Pv = (int) g.Pv; a.OHWp = (int) g.HWp;
+        a.Kslots = (int) g.Kslots; a.nsteps = (int) g.nsteps; a.steps_per_split = (int) g.nsteps;
+        a.act = c.act; a.lo = c.act_lo; a.hi = c.act_hi;
+        a.m_tiles = 1;
+        a.x_pstride = (int) g.Cinb; a.y_pstride = (int) g.Coutb;
+        a.x_bytes = (unsigned) ((int64_t) c.N * g.Cinb * c.H * c.W * 8);
+        a.H = c.H; a.W = c.W; a.HW = c.H * c.W; a.OW = c.OW; a.OHW = c.OH * c.OW;
+        a.KW = c.KW; a.SH = c.SH; a.SW = c.SW; a.PT = c.PT; a.PL = c.PL; a.DH = c.DH; a.DW = c.DW;
+        a.omode = OMODE_EPILOGUE;
+        PwArgs p;
+        std::memset(&p, 0, sizeof(p));
+        p.w       = (const half_t *) ((const char *) blob + L.off_w1);
+        p.nchunks = (int) L.nchunks;
+        GemmArgs &e = p.e;
+        const int64_t Coutb = ceil_div(d->Cout, 4), OHW = (int64_t) c.OH * c.OW;
+        e.bias = (const float *) ((const char *) blob + L.off_b1);
+        e.res = (const uint2 *) res; e.has_res = d->has_res;
+        e.y = (uint2 *) y;
+        e.Cout = d->Cout; e.Coutb = (int) Coutb;
+        e.P = (int) g.P; e.Pv = (int) g.P; e.OHW = (int) OHW; e.OHWp = (int) OHW; e.OW = c.OW;
+        e.y_pstride = (int) Coutb;
+        e.y_bytes = (unsigned) ((int64_t) c.N * Coutb * OHW * 8);
+        e.act = d->act; e.lo = d->act_lo; e.hi = d->act_hi;
+        e.omode = OMODE_EPILOGUE;
+        e.m_tiles = 1;
+        if (d2) {
+            p.w3     = (const half_t *) ((const char *) blob + ch.off_w2);
+            p.bias3  = (const float *) ((const char *) blob + ch.off_b2);
+            p.y3     = (uint2 *) y2;
+            p.Cout3  = d2->Cout3;
+            p.Coutb3 = (int) ceil_div(d2->Cout3, 4);
+            p.act3   = d2->act3; p.lo3 = d2->act3_lo; p.hi3 = d2->act3_hi;
+            p.y3_bytes = (unsigned) ((int64_t) c.N * p.Coutb3 * OHW * 8);
+        }
+        const unsigned grid = (unsigned) ceil_div(g.P, pt.t.BN);
+        fn<<<dim3(grid), 64 * pt.t.WN, 0, resolve_stream(s)>>>(a, p);
+        return check_launch(d2 ? "convpw2" : "convpw");
     }
 
 } // namespace vkhip
@@ -1207,53 +1295,60 @@ int vkhip_convpw_pack_weights(const vkhip_convpw_desc *d, const vkhip_conv_plan 
 
 int vkhip_convpw_forward(const vkhip_convpw_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res, void *y,
                          vkhip_stream_t s) {
-    if (!plan || !x || !blob || !y) return set_error(VKHIP_ERR_INVALID, "convpw_forward: null argument");
+    return convpw_forward_impl(d, plan, x, blob, res, y, nullptr, nullptr, s);
+}
+
+int vkhip_convpw2_plan(const vkhip_convpw2_desc *d, vkhip_conv_plan *plan) {
+    if (!d || !plan) return set_error(VKHIP_ERR_INVALID, "convpw2_plan: null argument");
     PwTile          pt;
     vkhip_conv_plan p3;
-    int rc = pw_check(d, pt, p3);
+    int rc = pw_check(&d->pw, pt, p3);
     if (rc) return rc;
-    const PwLayout L = pw_layout(d, pt, p3.weight_bytes);
-    if (plan->weight_bytes != L.bytes) return set_error(VKHIP_ERR_INVALID, "convpw_forward: plan does not match the descriptor");
-    if (d->has_res && !res) return set_error(VKHIP_ERR_INVALID, "convpw_forward: has_res without a residual tensor");
-    const vkhip_conv_desc &c = d->conv;
-    const int              nbi = halo_nbi(&c, pt.t);
-    PwKernelFn             fn  = pw_tile_kernel(c.Cout, nbi);
-    if (!fn) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw_forward: no kernel for band %d", nbi);
-    ConvGeom g = gemm_geom(&c, pt.halo_tile, false);
-    GemmArgs a;
-    std::memset(&a, 0, sizeof(a));
-    a.x = (const uint2 *) x;
-    a.w = (const half_t *) ((const char *) blob + align256((size_t) g.Coutp * 4));
-    a.bias = (const float *) blob;
-    a.Cinb = (int) g.Cinb; a.Coutb = (int) g.Coutb; a.Cout = c.Cout;
-    a.P = (int) g.P; a.Pv = (int) g.Pv; a.OHWp = (int) g.HWp;
-    a.Kslots = (int) g.Kslots; a.nsteps = (int) g.nsteps; a.steps_per_split = (int) g.nsteps;
-    a.act = c.act; a.lo = c.act_lo; a.hi = c.act_hi;
-    a.m_tiles = 1;
-    a.x_pstride = (int) g.Cinb; a.y_pstride = (int) g.Coutb;
-    a.x_bytes = (unsigned) ((int64_t) c.N * g.Cinb * c.H * c.W * 8);
-    a.H = c.H; a.W = c.W; a.HW = c.H * c.W; a.OW = c.OW; a.OHW = c.OH * c.OW;
-    a.KW = c.KW; a.SH = c.SH; a.SW = c.SW; a.PT = c.PT; a.PL = c.PL; a.DH = c.DH; a.DW = c.DW;
-    a.omode = OMODE_EPILOGUE;
-    PwArgs p;
-    std::memset(&p, 0, sizeof(p));
-    p.w       = (const half_t *) ((const char *) blob + L.off_w1);
-    p.nchunks = (int) L.nchunks;
-    GemmArgs &e = p.e;
-    const int64_t Coutb = ceil_div(d->Cout, 4), OHW = (int64_t) c.OH * c.OW;
-    e.bias = (const float *) ((const char *) blob + L.off_b1);
-    e.res = (const uint2 *) res; e.has_res = d->has_res;
-    e.y = (uint2 *) y;
-    e.Cout = d->Cout; e.Coutb = (int) Coutb;
-    e.P = (int) g.P; e.Pv = (int) g.P; e.OHW = (int) OHW; e.OHWp = (int) OHW; e.OW = c.OW;
-    e.y_pstride = (int) Coutb;
-    e.y_bytes = (unsigned) ((int64_t) c.N * Coutb * OHW * 8);
-    e.act = d->act; e.lo = d->act_lo; e.hi = d->act_hi;
-    e.omode = OMODE_EPILOGUE;
-    e.m_tiles = 1;
-    const unsigned grid = (unsigned) ceil_div(g.P, pt.t.BN);
-    fn<<<dim3(grid), 64 * pt.t.WN, 0, resolve_stream(s)>>>(a, p);
-    return check_launch("convpw");
+    PwChain ch;
+    if ((rc = pw_chain(d, pt, p3, ch))) return rc;
+    *plan                 = p3;
+    plan->weight_bytes    = ch.bytes;
+    plan->workspace_bytes = 0;
+    return VKHIP_OK;
+}
+
+int vkhip_convpw2_pack_weights(const vkhip_convpw2_desc *d, const vkhip_conv_plan *plan, const float *w3, const float *b3, const float *w1,
+                               const float *b1, const float *w2, const float *b2, void *blob) {
+    if (!d || !plan || !w2 || !blob) return set_error(VKHIP_ERR_INVALID, "convpw2_pack: null argument");
+    PwTile          pt;
+    vkhip_conv_plan p3;
+    int rc = pw_check(&d->pw, pt, p3);
+    if (rc) return rc;
+    PwChain ch;
+    if ((rc = pw_chain(d, pt, p3, ch))) return rc;
+    if (plan->weight_bytes != ch.bytes) return set_error(VKHIP_ERR_INVALID, "convpw2_pack: plan does not match the descriptor");
+    vkhip_conv_plan pp = *plan;
+    pp.weight_bytes    = ch.pair.bytes;
+    if ((rc = vkhip_convpw_pack_weights(&d->pw, &pp, w3, b3, w1, b1, blob))) return rc;
+    std::memset((char *) blob + ch.pair.bytes, 0, ch.bytes - ch.pair.bytes);
+    float  *bias = (float *) ((char *) blob + ch.off_b2);
+    half_t *wp   = (half_t *) ((char *) blob + ch.off_w2);
+    const int K2 = d->pw.Cout; // the chained 1x1 reads the pair's output channels
+    if (b2)
+        for (int m = 0; m < d->Cout3; ++m) bias[m] = b2[m];
+    // fragment m, step s = 2c + h (chunk c of the pair's output), lane l = g*32 + row%32, entry t:
+    // channel c*32 + (2h + t/4)*8 + 4g + t%4 (the order the pair's stored chunk holds them in)
+    for (int m = 0; m < ch.MR; ++m)
+        for (int64_t st = 0; st < 2 * ch.pair.nchunks; ++st)
+            for (int l = 0; l < 64; ++l)
+                for (int t = 0; t < 8; ++t) {
+                    const int64_t row = m * 32 + (l & 31);
+                    const int     c = (int) (st / 2), h = (int) (st % 2), g = l >> 5;
+                    const int     k = c * 32 + (2 * h + t / 4) * 8 + 4 * g + t % 4;
+                    if (row < d->Cout3 && k < K2) wp[((m * 2 * ch.pair.nchunks + st) * 64 + l) * 8 + t] = (half_t) w2[row * K2 + k];
+                }
+    return VKHIP_OK;
+}
+
+int vkhip_convpw2_forward(const vkhip_convpw2_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob, const void *res, void *y,
+                          void *y2, vkhip_stream_t s) {
+    if (!d || !y2) return set_error(VKHIP_ERR_INVALID, "convpw2_forward: null argument");
+    return convpw_forward_impl(&d->pw, plan, x, blob, res, y, d, y2, s);
 }
 
 } // extern "C"

@@ -1282,10 +1282,20 @@ namespace vkhip {
         const half_t *w;       // prepacked 1x1 weights, nchunks * MC fragments of 2*FM KB
         int           nchunks; // ceil(Cout / (32 * MC))
         GemmArgs      e;       // the 1x1's epilogue: bias, res, y, Cout / Coutb, P, OHW, act, ...
+        // An optional second 1x1 (MR > 0) over the first one's output (the next bottleneck's
+        // reduction), accumulated chunk by chunk: w3 [MR fragments][2 * nchunks steps][64][8 halves]
+        // (K order permuted like w, chunk c being fragment c), its bias [32 * MR], output y3.
+        const half_t *w3;
+        const float  *bias3;
+        uint2        *y3;
+        int           Cout3, Coutb3, act3;
+        float         lo3, hi3;
+        unsigned      y3_bytes;
     };
 
-    template <int FM, int FN, int WN, int KK, int NS, int NBI, bool ODD, int MC>
+    template <int FM, int FN, int WN, int KK, int NS, int NBI, bool ODD, int MC, int MR = 0>
     __global__ __launch_bounds__(64 * WN, 2) void conv_halo_pw_kernel(GemmArgs a, PwArgs p) {
+        static_assert(MR == 0 || MC == 1, "the chained 1x1 takes 32-row chunks");
         constexpr int BN = 32 * FN * WN;
         constexpr int KS = 2 * FM; // 16-deep K steps of the 1x1
         __shared__ __attribute__((aligned(16))) unsigned char sm[halo_lds_bytes<FM, 1, WN, KK, NS, NBI>()];
@@ -1333,9 +1343,33 @@ namespace vkhip {
         // The 1x1 in chunks of 32*MC output channels, software-pipelined one chunk deep: the next
         // chunk's weight fragments and residual values are loaded before this chunk's MFMAs and
         // stores (the vector memory counter retires in order, so they never wait behind the stores).
-        const GemmArgs &e   = p.e;
-        const half8    *W2  = reinterpret_cast<const half8 *>(p.w);
+        const GemmArgs &e = p.e;
         constexpr unsigned kInvalid = 0x80000000u;
+        // The 1x1 weights and bias (and the chained 1x1's) are staged in the idle ring once per
+        // workgroup, 1 KB copy units dealt round-robin to the waves, while the mid epilogue runs;
+        // every wave then reads its fragments from LDS. Layout: W2 [chunk][step][lane] x 16 bytes,
+        // bias [nchunks * 32 * MC] fp32, W3 [fragment][step][lane] x 16 bytes, bias3 [32 * MR] fp32.
+        const int NW2 = p.nchunks * MC * KS;              // KB of W2
+        const int NB  = (p.nchunks * MC * 32 * 4 + 1023) / 1024;
+        const int NW3 = MR > 0 ? MR * 2 * p.nchunks : 0;
+        const int NB3 = MR > 0 ? 1 : 0;
+        const int OB = NW2 * 1024, OW3 = OB + NB * 1024, OB3 = OW3 + NW3 * 1024;
+        {
+            __syncthreads(); // every wave is done with the ring
+            const __amdgpu_buffer_rsrc_t r2 = __builtin_amdgcn_make_buffer_rsrc((void *) p.w, (short) 0, NW2 * 1024, 0x00020000);
+            const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void *) e.bias, (short) 0, p.nchunks * MC * 32 * 4, 0x00020000);
+            const __amdgpu_buffer_rsrc_t r3 = __builtin_amdgcn_make_buffer_rsrc((void *) (MR > 0 ? p.w3 : p.w), (short) 0, NW3 * 1024, 0x00020000);
+            const __amdgpu_buffer_rsrc_t rb3 = __builtin_amdgcn_make_buffer_rsrc((void *) (MR > 0 ? p.bias3 : e.bias), (short) 0, MR * 32 * 4, 0x00020000);
+            const int units = NW2 + NB + NW3 + NB3;
+            for (int u = wave; u < units; u += WN) {
+                __amdgpu_buffer_rsrc_t rs = r2;
+                int                    k  = u;
+                if (u >= NW2 + NB + NW3) rs = rb3, k = u - NW2 - NB - NW3;
+                else if (u >= NW2 + NB) rs = r3, k = u - NW2 - NB;
+                else if (u >= NW2) rs = rb, k = u - NW2;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *) (sm + u * 1024), 16, (unsigned) (k * 1024 + lane * 16), 0, 0, 0);
+            }
+        }
         const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc((void *) e.y, (short) 0, (int) e.y_bytes, 0x00020000);
         const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc((void *) (e.has_res ? e.res : e.y), (short) 0, (int) e.y_bytes, 0x00020000);
         // per fragment column: the output pixel's byte offset at channel block 0 (or invalid)
@@ -1351,17 +1385,8 @@ namespace vkhip {
             const int ocb = 8 * (c * MC + mi) + 2 * qq + g;
             return pbase[j] != kInvalid && ocb < e.Coutb ? pbase[j] + (unsigned) (ocb * e.OHW * 8) : kInvalid;
         };
-        half8   an[MC][KS];
-        u32x2   rn[MC][FN][4];
-        float4v bn[MC][4];
-        auto load = [&](int c) __attribute__((always_inline)) {
-#pragma unroll
-            for (int mi = 0; mi < MC; ++mi) {
-#pragma unroll
-                for (int s = 0; s < KS; ++s) an[mi][s] = W2[((long long) ((c * MC + mi) * KS + s)) * 64 + lane];
-#pragma unroll
-                for (int qq = 0; qq < 4; ++qq) bn[mi][qq] = *reinterpret_cast<const float4v *>(e.bias + 32 * (c * MC + mi) + 8 * qq + 4 * g);
-            }
+        u32x2 rn[MC][FN][4];
+        auto  load = [&](int c) __attribute__((always_inline)) { // the residual of chunk c
             if (e.has_res) {
 #pragma unroll
                 for (int mi = 0; mi < MC; ++mi)
@@ -1372,21 +1397,28 @@ namespace vkhip {
             }
         };
         load(0);
+        constexpr int MRX = MR > 0 ? MR : 1;
+        float16v      acc3[MRX][FN];
+        if constexpr (MR > 0) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc3[m][j][r] = 0.f;
+        }
+        // the staged weights have landed (the residual loads issued after them may stay in flight)
+        if (e.has_res) __builtin_amdgcn_s_waitcnt((MC * FN * 4) | (7 << 4) | (15 << 8));
+        else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+        __syncthreads();
         for (int c = 0; c < p.nchunks; ++c) {
-            half8   ac[MC][KS];
-            u32x2   rc[MC][FN][4];
-            float4v bc[MC][4];
+            u32x2 rc[MC][FN][4];
 #pragma unroll
-            for (int mi = 0; mi < MC; ++mi) {
-#pragma unroll
-                for (int s = 0; s < KS; ++s) ac[mi][s] = an[mi][s];
-#pragma unroll
-                for (int qq = 0; qq < 4; ++qq) bc[mi][qq] = bn[mi][qq];
+            for (int mi = 0; mi < MC; ++mi)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
 #pragma unroll
                     for (int qq = 0; qq < 4; ++qq) rc[mi][j][qq] = rn[mi][j][qq];
-            }
             if (c + 1 < p.nchunks) load(c + 1);
             float16v acc2[MC][FN];
 #pragma unroll
@@ -1398,25 +1430,31 @@ namespace vkhip {
 #pragma unroll
             for (int s = 0; s < KS; ++s)
 #pragma unroll
-                for (int mi = 0; mi < MC; ++mi)
+                for (int mi = 0; mi < MC; ++mi) {
+                    const half8 af = *reinterpret_cast<const half8 *>(sm + (((c * MC + mi) * KS + s) * 64 + lane) * 16);
 #pragma unroll
-                    for (int j = 0; j < FN; ++j) acc2[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ac[mi][s], bm[s / 2][s % 2][j], acc2[mi][j], 0, 0, 0);
+                    for (int j = 0; j < FN; ++j) acc2[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bm[s / 2][s % 2][j], acc2[mi][j], 0, 0, 0);
+                }
             // epilogue: bias, residual, activation (compile-time), zero past Cout, fp16 store
+            half4 o16[4][FN]; // the stored fp16 values: the chained 1x1's B operand
             auto epi = [&](auto act_c) __attribute__((always_inline)) {
                 constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
                 for (int mi = 0; mi < MC; ++mi)
 #pragma unroll
                     for (int qq = 0; qq < 4; ++qq) {
-                        const int oc = 32 * (c * MC + mi) + 8 * qq + 4 * g;
+                        const int     oc = 32 * (c * MC + mi) + 8 * qq + 4 * g;
+                        const float4v bv = *reinterpret_cast<const float4v *>(sm + OB + oc * 4);
 #pragma unroll
                         for (int j = 0; j < FN; ++j) {
                             float4v v = {acc2[mi][j][qq * 4 + 0], acc2[mi][j][qq * 4 + 1], acc2[mi][j][qq * 4 + 2], acc2[mi][j][qq * 4 + 3]};
-                            v += bc[mi][qq];
+                            v += bv;
                             if (e.has_res) v += h4_to_f4(__builtin_bit_cast(half4, rc[mi][j][qq]));
 #pragma unroll
                             for (int t = 0; t < 4; ++t) v[t] = oc + t < e.Cout ? apply_act(v[t], ACT, e.lo, e.hi) : 0.f;
-                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff(c, mi, j, qq), 0, 0);
+                            const half4 o = f4_to_h4(v);
+                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o), yrs, yoff(c, mi, j, qq), 0, 0);
+                            if constexpr (MR > 0) o16[qq][j] = o;
                         }
                     }
             };
@@ -1427,6 +1465,56 @@ namespace vkhip {
                 case VKHIP_ACT_HARDSWISH: epi(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
                 case VKHIP_ACT_SILU: epi(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
                 default: epi(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
+            }
+            // the chained 1x1: this chunk's 32 output channels are its K steps 2c, 2c + 1 (the
+            // stored values of row groups 2h, 2h + 1 form the B fragment of step 2c + h)
+            if constexpr (MR > 0) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+                        const half4 lo = o16[2 * h][j], hi = o16[2 * h + 1][j];
+                        const half8 b8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+                        for (int m = 0; m < MR; ++m) {
+                            const half8 wf = *reinterpret_cast<const half8 *>(sm + OW3 + ((m * 2 * p.nchunks + 2 * c + h) * 64 + lane) * 16);
+                            acc3[m][j]     = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, b8, acc3[m][j], 0, 0, 0);
+                        }
+                    }
+            }
+        }
+        if constexpr (MR > 0) {
+            // the chained 1x1's epilogue: bias, activation, fp16 store into y3
+            const __amdgpu_buffer_rsrc_t y3rs = __builtin_amdgcn_make_buffer_rsrc((void *) p.y3, (short) 0, (int) p.y3_bytes, 0x00020000);
+            auto epi3 = [&](auto act_c) __attribute__((always_inline)) {
+                constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+                for (int m = 0; m < MR; ++m)
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) {
+                        const int     oc = 32 * m + 8 * qq + 4 * g;
+                        const float4v bv = *reinterpret_cast<const float4v *>(sm + OB3 + oc * 4);
+#pragma unroll
+                        for (int j = 0; j < FN; ++j) {
+                            float4v v = {acc3[m][j][qq * 4 + 0], acc3[m][j][qq * 4 + 1], acc3[m][j][qq * 4 + 2], acc3[m][j][qq * 4 + 3]};
+                            v += bv;
+#pragma unroll
+                            for (int t = 0; t < 4; ++t) v[t] = oc + t < p.Cout3 ? apply_act(v[t], ACT, p.lo3, p.hi3) : 0.f;
+                            const int      px  = n0 + wn0 + 32 * j + (lane & 31);
+                            const int      pn  = px / e.OHW, pr = px - pn * e.OHW;
+                            const int      ocb = oc >> 2;
+                            const unsigned off = px < e.P && ocb < p.Coutb3 ? (unsigned) (((pn * p.Coutb3 + ocb) * e.OHW + pr) * 8) : kInvalid;
+                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), y3rs, off, 0, 0);
+                        }
+                    }
+            };
+            switch (p.act3) {
+                case VKHIP_ACT_RELU: epi3(std::integral_constant<int, VKHIP_ACT_RELU> {}); break;
+                case VKHIP_ACT_RELU6: epi3(std::integral_constant<int, VKHIP_ACT_RELU6> {}); break;
+                case VKHIP_ACT_CLIP: epi3(std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
+                case VKHIP_ACT_HARDSWISH: epi3(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
+                case VKHIP_ACT_SILU: epi3(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
+                default: epi3(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
             }
         }
     }
@@ -1631,7 +1719,7 @@ namespace vkhip {
     GemmKernelFn halo_tile_kernel(int tile, int nbi);
     typedef void (*PwKernelFn)(GemmArgs, PwArgs);
     // the fused 3x3 -> 1x1 kernel for a mid width (64 or 128) and band size, or null
-    PwKernelFn pw_tile_kernel(int cmid, int nbi);
+    PwKernelFn pw_tile_kernel(int cmid, int nbi, int mr, int *lds);
     // stem conv + 3x3/s2 max pool (stem_pool.hip): FM = 2 (64 output channels), WM = 1, WN waves
     // over FN fragments each, so BN = 32 FN WN GEMM columns = up to BN / OW conv rows; LDS holds the
     // conv tile (16 channel blocks x BN columns) plus a spare KB. Two configurations: 0 = 8 waves x
