@@ -945,6 +945,34 @@ def test_conv_input_scale_rejects_other_shapes(gpu):
         assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_AUTO, -1, 0, ctypes.byref(plan)) == 2
 
 
+@pytest.mark.parametrize("N,C,Cr,R,HW", [(20, 960, 240, 1, 49), (3, 72, 24, 4, 784), (33, 120, 32, 2, 784), (16, 672, 168, 1, 196)])
+def test_se_pooled_one_launch(gpu, N, C, Cr, R, HW):
+    """vkhip_fused_se_pooled (both FCs in one launch, 16 images per workgroup; ragged image
+    groups) against a float64 restatement: x = fp16(sum of the partials / HW),
+    h = fp16(relu(W1 x + b1)), y = clamp(alpha (W2 h + b2) + beta, 0, 1), weights rounded to fp16."""
+    lib = V.vkhip()
+    r = rng(500 + C + N)
+    Cb = (C + 3) // 4
+    part = (r.standard_normal((N, Cb, R, 4)) * HW * 0.3).astype(np.float32)
+    w1 = (r.standard_normal((Cr, C)) * 0.1).astype(np.float32)
+    b1 = (r.standard_normal(Cr) * 0.1).astype(np.float32)
+    w2 = (r.standard_normal((C, Cr)) * 0.2).astype(np.float32)
+    b2 = (r.standard_normal(C) * 0.1).astype(np.float32)
+    blob = np.zeros(lib.vkhip_se_weight_bytes(C, Cr), np.uint8)
+    check(lib.vkhip_se_pack_weights(C, Cr, w1.ctypes.data, b1.ctypes.data, w2.ctypes.data, b2.ctypes.data, blob.ctypes.data))
+    dblob, dpart = DeviceBuffer.from_array(blob), DeviceBuffer.from_array(part)
+    ws = DeviceBuffer(lib.vkhip_se_workspace_bytes(N, Cr))
+    out = DeviceBuffer(V.nc4_elems(N, C, 1, 1) * 2)
+    check(lib.vkhip_fused_se_pooled(dpart.ptr, R, HW, dblob.ptr, out.ptr, N, C, Cr, 1.0 / 6, 0.5, ws.ptr, None))
+    check(lib.vkhip_stream_sync(None))
+    got = from_device_nc4(out, (N, C, 1, 1)).reshape(N, C)
+    f16 = lambda a: np.asarray(a, np.float64).astype(np.float16).astype(np.float64)
+    x = f16(part.astype(np.float64).sum(2).reshape(N, Cb * 4)[:, :C].astype(np.float32) / np.float32(HW))
+    h = f16(np.maximum(x @ f16(w1).T + b1, 0.0))
+    ref = np.clip((h @ f16(w2).T + b2) / 6 + 0.5, 0.0, 1.0)
+    assert_parity(got, ref, f"se pooled N{N} C{C} Cr{Cr}")
+
+
 # ---------------------------------------------------------------- depthwise + squeeze-excite pool sums
 @pytest.mark.parametrize("shape,k,s,rt", [((3, 72, 28, 28), 3, 2, 7), ((2, 120, 28, 28), 5, 1, 4), ((4, 960, 7, 7), 5, 1, 7),
                                           ((2, 22, 14, 14), 3, 1, 14), ((5, 40, 56, 56), 5, 2, 4)])
