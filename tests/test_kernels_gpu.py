@@ -946,9 +946,9 @@ def test_conv_input_scale_rejects_other_shapes(gpu):
 
 
 @pytest.mark.parametrize("N,C,Cr,R,HW", [(20, 960, 240, 1, 49), (3, 72, 24, 4, 784), (33, 120, 32, 2, 784), (16, 672, 168, 1, 196)])
-def test_se_pooled_one_launch(gpu, N, C, Cr, R, HW):
-    """vkhip_fused_se_pooled (both FCs in one launch, 16 images per workgroup; ragged image
-    groups) against a float64 restatement: x = fp16(sum of the partials / HW),
+def test_se_pooled(gpu, N, C, Cr, R, HW):
+    """vkhip_fused_se_pooled (pooled partial sums -> FC1 -> FC2 -> hard-sigmoid; image counts
+    that are not a multiple of the kernels' image groups) against a float64 restatement: x = fp16(sum of the partials / HW),
     h = fp16(relu(W1 x + b1)), y = clamp(alpha (W2 h + b2) + beta, 0, 1), weights rounded to fp16."""
     lib = V.vkhip()
     r = rng(500 + C + N)
