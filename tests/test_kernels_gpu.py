@@ -607,11 +607,12 @@ def test_depthwise(gpu, k, s, C, act):
 @pytest.mark.parametrize("shape,k,s,act,res", [((3, 20, 28, 28), 3, 1, 4, True), ((2, 24, 56, 56), 5, 2, 1, False),
                                                ((4, 160, 7, 7), 5, 1, 2, True), ((1, 16, 112, 112), 3, 2, 3, False),
                                                ((2, 6, 14, 13), 3, 1, 5, True)])
-@pytest.mark.parametrize("rt", [4, 7, 14])
+@pytest.mark.parametrize("rt", [4, 7, 14, 204, 207, 404, 407])
 def test_depthwise_tiled_shapes(gpu, shape, k, s, act, res, rt):
     """Even/odd widths (16- and 8-byte row copies), several planes per workgroup, row tiles with
-    halos (4, 7 or 14 output rows per strip, the plan's tile), residual epilogue, ragged channel
-    count."""
+    halos (4, 7 or 14 output rows per strip, the plan's tile), 2 or 4 strips per workgroup with
+    the next strip's input prefetched (tile 2xx / 4xx; odd widths fall back to one strip),
+    residual epilogue, ragged channel count."""
     N, C, H, W = shape
     r = rng(70 + k + s + C)
     x = round_half(r.standard_normal(shape))
@@ -975,7 +976,8 @@ def test_se_pooled(gpu, N, C, Cr, R, HW):
 
 # ---------------------------------------------------------------- depthwise + squeeze-excite pool sums
 @pytest.mark.parametrize("shape,k,s,rt", [((3, 72, 28, 28), 3, 2, 7), ((2, 120, 28, 28), 5, 1, 4), ((4, 960, 7, 7), 5, 1, 7),
-                                          ((2, 22, 14, 14), 3, 1, 14), ((5, 40, 56, 56), 5, 2, 4)])
+                                          ((2, 22, 14, 14), 3, 1, 14), ((5, 40, 56, 56), 5, 2, 4),
+                                          ((3, 120, 28, 28), 5, 1, 207), ((4, 72, 56, 56), 3, 1, 404)])
 def test_depthwise_pool_sums(gpu, shape, k, s, rt):
     """vkhip_conv_forward_pooled writes exactly the depthwise output of vkhip_conv_forward and the
     per-(plane, row tile) sums of it; a squeeze-excite fed from those sums (vkhip_fused_se_pooled)
@@ -992,7 +994,7 @@ def test_depthwise_pool_sums(gpu, shape, k, s, rt):
     d, yshape = conv_desc(x.shape, w.shape, (s, s), (p, p, p, p), (1, 1), C, 4, 0.0, 0.0, 0)
     R = lib.vkhip_conv_pool_parts(ctypes.byref(d), ctypes.byref(plan))
     OH = yshape[2]
-    assert R == -(-OH // rt)
+    assert R == -(-OH // (rt % 100))
     blob = np.zeros(plan.weight_bytes, np.uint8)
     check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(plan), w.ctypes.data, b.ctypes.data, blob.ctypes.data))
     dblob = DeviceBuffer.from_array(blob)

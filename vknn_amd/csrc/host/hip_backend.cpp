@@ -235,7 +235,9 @@ namespace vknn {
                 for (int t = 0; t < ntiles; ++t)
                     if (!skipTiles.count(t)) cands.push_back({VKHIP_CONV_GEMM, t, 0});
                 if (dw) // the depthwise kernel's rows per strip
-                    for (int rt: {4, 7, 14}) cands.push_back({VKHIP_CONV_DEPTHWISE, rt, 0});
+                    for (int rt: {4, 7, 14, 204, 207, 404, 407}) // + 100 x strips per workgroup (VKNN_HIP_DW_PIPE=0: one strip only)
+                        if (rt < 100 || !(std::getenv("VKNN_HIP_DW_PIPE") && std::getenv("VKNN_HIP_DW_PIPE")[0] == '0'))
+                            cands.push_back({VKHIP_CONV_DEPTHWISE, rt, 0});
                 vkhip_conv_plan base;
                 check(vkhip_conv_plan_make(&d, VKHIP_CONV_AUTO, -1, 0, &base), "conv plan");
                 int64_t pixels = (int64_t) d.N * d.OH * d.OW;

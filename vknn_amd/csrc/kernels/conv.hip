@@ -257,6 +257,7 @@ namespace vkhip {
         int PP, IR, IWp, PLA; // planes per WG, LDS rows per plane, LDS row pitch (pixels), LDS column of ix=0
         int PS;               // LDS plane pitch (pixels): IR * IWp padded so consecutive planes start on different banks
         int row_tiles, plane_groups;
+        int RPW, rt_groups;   // row tiles per workgroup (> 1: software-pipelined strips), workgroups per plane group
         unsigned mHW, mW;     // ceil(2^32 / (H*W)), ceil(2^32 / W): n / d = umulhi(n, m) for n * d < 2^32 (0: divide)
     };
 
@@ -266,13 +267,11 @@ namespace vkhip {
         constexpr int IR = (RT - 1) * S + KH; // input rows of one strip
         uint2 *tile = reinterpret_cast<uint2 *>(dsm); // [PP][PS: IR x IWp + padding]
         const int tid = threadIdx.x;
-        const int rt  = blockIdx.x % t.row_tiles;
-        const int pg  = blockIdx.x / t.row_tiles;
+        const int rtg = blockIdx.x % t.rt_groups;
+        const int pg  = blockIdx.x / t.rt_groups;
         const int NCb = a.N * a.Cb;
         const int p0  = pg * t.PP;
         const int np  = min(t.PP, NCb - p0);
-        const int oy0 = rt * RT;
-        const int iy0 = oy0 * S - a.PT;
         const int IWp = t.IWp, PLA = t.PLA;
 
         // The thread's output column and plane; its weights and bias are loaded first so their
@@ -290,6 +289,9 @@ namespace vkhip {
         const float4v b0 = *reinterpret_cast<const float4v *>(a.bias + cb * 4);
 
         const int W = a.W, H = a.H;
+        // input strip of row tile rt -> LDS
+        auto load_tile = [&](const int rt) __attribute__((always_inline)) {
+        const int iy0 = rt * RT * S - a.PT;
         if (t.row_tiles == 1) {
             // One strip covers every output row, so the workgroup's planes are one contiguous range
             // of the input (np * H * W pixels from plane p0): zero the LDS tile, then copy the range
@@ -360,7 +362,11 @@ namespace vkhip {
                 }
             }
         }
-        __syncthreads();
+        };
+
+        // strip of row tile rt from LDS: RT outputs per thread, activation, store, pool partials
+        auto strip = [&](const int rt) __attribute__((always_inline)) {
+        const int oy0 = rt * RT;
 
         const bool live = pl < np;
         float4v acc[RT];
@@ -432,11 +438,62 @@ namespace vkhip {
                 a.pool[(long long) (p0 + tid) * t.row_tiles + rt] = sum;
             }
         }
+        };
+
+        const int rt_first = rtg * t.RPW;
+        const int rt_end   = min(rt_first + t.RPW, t.row_tiles);
+        if (t.RPW > 1) {
+            // Several strips per workgroup, software-pipelined: the global loads of strip k + 1 are
+            // issued into registers before strip k is computed from LDS, so their latency hides
+            // behind the FMAs. The host selects this only when one round of PF loads of 16 bytes
+            // per thread covers a strip (W even, np * IR <= PF * rows per round).
+            constexpr int PF   = 8;
+            const int     cols = IWp / 2, rpp = 256 / cols;
+            const int     col = tid % cols, r2 = tid / cols;
+            const int     ix  = 2 * col - PLA;
+            const bool    cok = ix >= 0 && ix < W && r2 < rpp;
+            const int     rows = np * IR;
+            u32x4         v[PF];
+            auto fetch = [&](const int rt) __attribute__((always_inline)) {
+                const int iy0 = rt * RT * S - a.PT;
+#pragma unroll
+                for (int u = 0; u < PF; ++u) {
+                    const int  row = r2 + u * rpp;
+                    const int  pl = row / IR, r = row - pl * IR;
+                    const int  iy = iy0 + r;
+                    const bool ok = row < rows && cok && (unsigned) iy < (unsigned) H;
+                    v[u] = u32x4 {0u, 0u, 0u, 0u};
+                    if (ok) v[u] = *reinterpret_cast<const u32x4 *>(a.x + ((long long) (p0 + pl) * H + iy) * W + ix);
+                }
+            };
+            fetch(rt_first);
+            for (int rt = rt_first; rt < rt_end; ++rt) {
+                if (rt > rt_first) __syncthreads(); // the previous strip's LDS reads are done
+                if (r2 < rpp) {
+#pragma unroll
+                    for (int u = 0; u < PF; ++u) {
+                        const int row = r2 + u * rpp;
+                        const int pl = row / IR, r = row - pl * IR;
+                        if (row < rows) *reinterpret_cast<u32x4 *>(tile + pl * t.PS + r * IWp + 2 * col) = v[u];
+                    }
+                }
+                __syncthreads();
+                if (rt + 1 < rt_end) fetch(rt + 1);
+                strip(rt);
+            }
+        } else {
+            for (int rt = rt_first; rt < rt_end; ++rt) {
+                if (rt > rt_first) __syncthreads();
+                load_tile(rt);
+                __syncthreads();
+                strip(rt);
+            }
+        }
     }
 
     // Tile geometry for dwconv_lds_kernel: as many planes as fill 256 threads with one output
     // column each; RT output rows per strip.
-    static bool dw_tile(const vkhip_conv_desc *d, int64_t NCb, int RT, DwTile &t) {
+    static bool dw_tile(const vkhip_conv_desc *d, int64_t NCb, int RT, int RPW, DwTile &t) {
         const int S = d->SH;
         if (d->OW > 256) return false;
         t.PLA = (d->PL + 1) & ~1;
@@ -459,6 +516,10 @@ namespace vkhip {
         t.mW  = d->W > 1 && HW * (uint64_t) d->W < (1ULL << 32) ? (unsigned) (((1ULL << 32) + d->W - 1) / d->W) : 0u;
         t.row_tiles    = (int) ceil_div(d->OH, RT);
         t.plane_groups = (int) ceil_div(NCb, t.PP);
+        // pipelined strips: W even (16-byte loads) and one round of 8 loads per thread per strip
+        t.RPW = std::max(1, std::min(RPW, t.row_tiles));
+        if (t.RPW > 1 && (d->W % 2 != 0 || t.PP * t.IR > 8 * (256 / (t.IWp / 2)))) t.RPW = 1;
+        t.rt_groups = (int) ceil_div(t.row_tiles, t.RPW);
         return true;
     }
 
@@ -699,8 +760,9 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
             return set_error(VKHIP_ERR_UNSUPPORTED, "grouped conv with group=%d (Cin=%d Cout=%d) is not depthwise", d->group, d->Cin, d->Cout);
         if (algo != VKHIP_CONV_AUTO && algo != VKHIP_CONV_DEPTHWISE)
             return set_error(VKHIP_ERR_INVALID, "depthwise conv only runs the depthwise algorithm");
-        if (tile > 0 && tile != 4 && tile != 7 && tile != 14)
-            return set_error(VKHIP_ERR_INVALID, "depthwise tile %d: the rows per strip are 4, 7 or 14 (0 or -1: by shape)", tile);
+        // tile = rows per strip (4, 7 or 14) + 100 x strips per workgroup (2 or 4: pipelined strips)
+        if (tile > 0 && ((tile % 100 != 4 && tile % 100 != 7 && tile % 100 != 14) || (tile / 100 != 0 && tile / 100 != 2 && tile / 100 != 4)))
+            return set_error(VKHIP_ERR_INVALID, "depthwise tile %d: rows per strip 4, 7 or 14, plus 100 x 2 or 4 strips per workgroup (0 or -1: by shape)", tile);
         int64_t Cb         = ceil_div(d->Cin, 4);
         plan->algo         = VKHIP_CONV_DEPTHWISE;
         plan->tile         = tile > 0 ? tile : 0;
@@ -916,10 +978,11 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
         a.pool = (float4v *) pool;
         bool unit = d->DH == 1 && d->DW == 1 && d->SH == d->SW;
         DwTile t;
-        const int RT = plan->tile > 0 ? plan->tile : (d->OH % 7 == 0 ? 7 : 4);
-        if (unit && d->KH == d->KW && (d->KH == 3 || d->KH == 5) && (d->SH == 1 || d->SH == 2) && dw_tile(d, (int64_t) d->N * Cb, RT, t)) {
+        const int RT = plan->tile > 0 ? plan->tile % 100 : (d->OH % 7 == 0 ? 7 : 4);
+        if (unit && d->KH == d->KW && (d->KH == 3 || d->KH == 5) && (d->SH == 1 || d->SH == 2) &&
+            dw_tile(d, (int64_t) d->N * Cb, RT, std::max(1, plan->tile / 100), t)) {
             const size_t sm = std::max<size_t>((size_t) t.PP * t.PS * 8, pool ? 256 * 16 : 0); // the pool reduction reuses the tile
-            dim3 g2((unsigned) ((int64_t) t.row_tiles * t.plane_groups));
+            dim3 g2((unsigned) ((int64_t) t.rt_groups * t.plane_groups));
 #define VKHIP_DW_LAUNCH(K, S_)                                                                                 \
     (RT == 14 ? dwconv_lds_kernel<K, K, S_, 14><<<g2, 256, sm, st>>>(a, t) : RT == 7 ? dwconv_lds_kernel<K, K, S_, 7><<<g2, 256, sm, st>>>(a, t) : dwconv_lds_kernel<K, K, S_, 4><<<g2, 256, sm, st>>>(a, t))
             if (d->KH == 3 && d->SH == 1) VKHIP_DW_LAUNCH(3, 1);
@@ -1066,9 +1129,10 @@ int vkhip_conv_forward_view(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
 int vkhip_conv_pool_parts(const vkhip_conv_desc *d, const vkhip_conv_plan *plan) {
     if (!d || !plan || plan->algo != VKHIP_CONV_DEPTHWISE || d->in_scale) return 0;
     const bool unit = d->DH == 1 && d->DW == 1 && d->SH == d->SW;
-    const int  RT   = plan->tile > 0 ? plan->tile : (d->OH % 7 == 0 ? 7 : 4);
+    const int  RT   = plan->tile > 0 ? plan->tile % 100 : (d->OH % 7 == 0 ? 7 : 4);
     DwTile     t;
-    if (!(unit && d->KH == d->KW && (d->KH == 3 || d->KH == 5) && (d->SH == 1 || d->SH == 2) && dw_tile(d, (int64_t) d->N * ceil_div(d->Cin, 4), RT, t)))
+    if (!(unit && d->KH == d->KW && (d->KH == 3 || d->KH == 5) && (d->SH == 1 || d->SH == 2) &&
+          dw_tile(d, (int64_t) d->N * ceil_div(d->Cin, 4), RT, std::max(1, plan->tile / 100), t)))
         return 0;
     return t.row_tiles;
 }
