@@ -261,7 +261,7 @@ namespace vkhip {
         unsigned mHW, mW;     // ceil(2^32 / (H*W)), ceil(2^32 / W): n / d = umulhi(n, m) for n * d < 2^32 (0: divide)
     };
 
-    template <int KH, int KW, int S, int RT>
+    template <int KH, int KW, int S, int RT, bool PIPE>
     __global__ __launch_bounds__(256) void dwconv_lds_kernel(DwArgs a, DwTile t) {
         extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
         constexpr int IR = (RT - 1) * S + KH; // input rows of one strip
@@ -440,9 +440,9 @@ namespace vkhip {
         }
         };
 
-        const int rt_first = rtg * t.RPW;
-        const int rt_end   = min(rt_first + t.RPW, t.row_tiles);
-        if (t.RPW > 1) {
+        if constexpr (PIPE) {
+            const int rt_first = rtg * t.RPW;
+            const int rt_end   = min(rt_first + t.RPW, t.row_tiles);
             // Several strips per workgroup, software-pipelined: the global loads of strip k + 1 are
             // issued into registers before strip k is computed from LDS, so their latency hides
             // behind the FMAs. The host selects this only when one round of PF loads of 16 bytes
@@ -482,12 +482,10 @@ namespace vkhip {
                 strip(rt);
             }
         } else {
-            for (int rt = rt_first; rt < rt_end; ++rt) {
-                if (rt > rt_first) __syncthreads();
-                load_tile(rt);
-                __syncthreads();
-                strip(rt);
-            }
+            // one strip per workgroup (the host launches this variant only with RPW == 1)
+            load_tile(rtg);
+            __syncthreads();
+            strip(rtg);
         }
     }
 
@@ -984,7 +982,12 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
             const size_t sm = std::max<size_t>((size_t) t.PP * t.PS * 8, pool ? 256 * 16 : 0); // the pool reduction reuses the tile
             dim3 g2((unsigned) ((int64_t) t.rt_groups * t.plane_groups));
 #define VKHIP_DW_LAUNCH(K, S_)                                                                                 \
-    (RT == 14 ? dwconv_lds_kernel<K, K, S_, 14><<<g2, 256, sm, st>>>(a, t) : RT == 7 ? dwconv_lds_kernel<K, K, S_, 7><<<g2, 256, sm, st>>>(a, t) : dwconv_lds_kernel<K, K, S_, 4><<<g2, 256, sm, st>>>(a, t))
+    (t.RPW > 1 ? (RT == 14 ? dwconv_lds_kernel<K, K, S_, 14, true><<<g2, 256, sm, st>>>(a, t)                                      \
+                          : RT == 7 ? dwconv_lds_kernel<K, K, S_, 7, true><<<g2, 256, sm, st>>>(a, t)                                \
+                                    : dwconv_lds_kernel<K, K, S_, 4, true><<<g2, 256, sm, st>>>(a, t))                               \
+               : (RT == 14 ? dwconv_lds_kernel<K, K, S_, 14, false><<<g2, 256, sm, st>>>(a, t)                                     \
+                           : RT == 7 ? dwconv_lds_kernel<K, K, S_, 7, false><<<g2, 256, sm, st>>>(a, t)                              \
+                                     : dwconv_lds_kernel<K, K, S_, 4, false><<<g2, 256, sm, st>>>(a, t)))
             if (d->KH == 3 && d->SH == 1) VKHIP_DW_LAUNCH(3, 1);
             else if (d->KH == 3) VKHIP_DW_LAUNCH(3, 2);
             else if (d->SH == 1) VKHIP_DW_LAUNCH(5, 1);
