@@ -139,3 +139,22 @@ def test_model_flops_match_survey_arithmetic():
     f = V.vknn().vknn_model_flops(b"resnet50")
     assert abs(f - 8.17e9) / 8.17e9 < 0.01
     assert abs(V.vknn().vknn_model_flops(b"conv3x3_bn_relu") - 231.2e6) / 231.2e6 < 0.001
+
+
+def test_noalloc_refuses_plan_for_another_shape():
+    """The allocation-free conv sizes its fixed scratch from the descriptor: a split-K plan made for
+    a larger batch (a bigger workspace than this descriptor needs) or an edited workspace size is
+    refused before any device call, so no kernel can write past the scratch array."""
+    from tests.gpu_helpers import conv_desc
+    lib = V.vkhip()
+    big, _ = conv_desc((8, 256, 14, 14), (256, 256, 1, 1))
+    small, _ = conv_desc((1, 256, 14, 14), (256, 256, 1, 1))
+    plan = V.ConvPlan()
+    V.check(lib.vkhip_conv_plan_make(ctypes.byref(big), V.CONV_SPLITK, -1, 4, ctypes.byref(plan)), "plan")
+    assert plan.workspace_bytes > 0
+    rc = lib.vkhip_conv_forward_noalloc(ctypes.byref(small), ctypes.byref(plan), None, None, None, None, None)
+    assert rc == 1 and b"differ" in lib.vkhip_last_error()
+    V.check(lib.vkhip_conv_plan_make(ctypes.byref(small), V.CONV_SPLITK, -1, 4, ctypes.byref(plan)), "plan")
+    plan.workspace_bytes -= 256
+    rc = lib.vkhip_conv_forward_noalloc(ctypes.byref(small), ctypes.byref(plan), None, None, None, None, None)
+    assert rc == 1 and b"differ" in lib.vkhip_last_error()

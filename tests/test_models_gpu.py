@@ -129,8 +129,9 @@ def check_batch_items(model, batch, items, seed, opts=""):
         check_outputs(g, ref, per_item, f"{model} b{batch}[{opts}] item {k}")
 
 
-def test_config1_mnv2_block_b32(gpu):
-    check_batch_items("mnv2_block", 32, (0, 31), 7)
+@pytest.mark.parametrize("opts", ["", "fuse_dwpw=1"])
+def test_config1_mnv2_block_b32(gpu, opts):
+    check_batch_items("mnv2_block", 32, (0, 31), 7, opts)
 
 
 def test_config2_resnet50_b64_items(gpu):
@@ -160,8 +161,9 @@ def test_se_scale_folded_into_projection(gpu, opts, monkeypatch):
     check_outputs(got, plain.run(x), sess.out_elems, f"config3 b2 folded vs unfolded[{opts}]")
 
 
-def test_config3_mobilenetv3_large_b128_items(gpu):
-    check_batch_items("mobilenetv3_large", 128, (0, 127), 7, "fuse_se=1;fuse_dwpw=1")
+@pytest.mark.parametrize("opts", ["", "fuse_se=1;fuse_dwpw=1"])
+def test_config3_mobilenetv3_large_b128_items(gpu, opts):
+    check_batch_items("mobilenetv3_large", 128, (0, 127), 7, opts)
 
 
 def test_config4_yolov8n(gpu):

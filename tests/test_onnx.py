@@ -164,6 +164,14 @@ def test_malformed_files_are_rejected(tmp_path):
     ext = W.tensor("w", w, store="external", external=("small.bin", 8, w.nbytes))
     cases["external_out_of_range"] = W.model(W.graph([W.node("Conv", ["x", "w"], ["y"], name="c")], [W.value_info("x", [1, 4, 5, 5])],
                                                      [W.value_info("y")], [ext]))
+    # an offset near INT64_MAX: offset + length would wrap negative if the check added them
+    ext = W.tensor("w", w, store="external", external=("small.bin", 9223372036854775807, w.nbytes))
+    cases["external_offset_overflow"] = W.model(W.graph([W.node("Conv", ["x", "w"], ["y"], name="c")], [W.value_info("x", [1, 4, 5, 5])],
+                                                        [W.value_info("y")], [ext]))
+    # dims whose product wraps to 2 elements (3 x 6148914691236517206 = 2 mod 2^64), with 8 raw bytes
+    huge = W.f_packed_varints(1, [3, 6148914691236517206]) + W.f_varint(2, W.FLOAT) + W.f_bytes(8, "w") + W.f_bytes(9, b"\0" * 8)
+    cases["dims_overflow"] = W.model(W.graph([W.node("Conv", ["x", "w"], ["y"], name="c")], [W.value_info("x", [1, 4, 5, 5])],
+                                             [W.value_info("y")], [huge]))
     for name, blob in cases.items():
         p = tmp_path / f"{name}.onnx"
         p.write_bytes(blob)

@@ -202,3 +202,17 @@ def test_warm_start_takes_prepacked_weights_from_cache_file(lib, tmp_path):
     lib.vknn_weight_cache_stats(ctypes.byref(n), ctypes.byref(h), ctypes.byref(m))
     assert h.value == 0 and m.value == 0  # Tune mode neither reads nor keeps blobs
     np.testing.assert_array_equal(s4.run(x), y1)
+    del s4
+    # blobs written under another pack-format version (the key's #f<version># field) are not taken
+    import re
+    data = f.read_bytes()
+    vers = set(re.findall(rb"#f(\d+)#", data))
+    assert len(vers) == 1, vers
+    ver = vers.pop()
+    other = str((int(ver) + 1) % (10 ** len(ver))).zfill(len(ver)).encode()
+    f.write_bytes(data.replace(b"#f" + ver + b"#", b"#f" + other + b"#"))
+    lib.vknn_tune_cache_clear()
+    s5 = V.Session("resnet_tiny", 2, seed=3, options=opts)
+    lib.vknn_weight_cache_stats(ctypes.byref(n), ctypes.byref(h), ctypes.byref(m))
+    assert h.value == 0 and m.value == convs
+    np.testing.assert_array_equal(s5.run(x), y1)

@@ -153,8 +153,9 @@ namespace vknn {
                 choosePlan(env, w, b);
             }
 
-            // Cache key of the prepacked blob: the node, its conv signature and plan, and a hash of
-            // the source weights and bias (a changed model or plan never takes a stale blob). The
+            // Cache key of the prepacked blob: the node, its conv signature and plan, the blob layout
+            // version (VKHIP_PACK_FORMAT) and a hash of the source weights and bias (a changed model,
+            // plan or packer never takes a stale blob). The
             // reference keys its blobs by model tag + node + role (vk_op_common.h uploadCached).
             std::string weightKey(const float *w, const float *b) const {
                 uint64_t h = 1469598103934665603ull; // FNV-1a, 64 bit, over the fp32 bytes
@@ -165,7 +166,8 @@ namespace vknn {
                 mix(w, (size_t) d.Cout * (d.Cin / d.group) * d.KH * d.KW);
                 if (b) mix(b, (size_t) d.Cout);
                 char tail[96];
-                std::snprintf(tail, sizeof tail, "#p%d_%d_%d#%016llx", plan.algo, plan.tile, plan.ksplit, (unsigned long long) h);
+                std::snprintf(tail, sizeof tail, "#p%d_%d_%d#f%d#%016llx", plan.algo, plan.tile, plan.ksplit, VKHIP_PACK_FORMAT,
+                              (unsigned long long) h);
                 return gpuTag() + "/w/" + name + keyOf(d, 0).substr(gpuTag().size()) + tail;
             }
 

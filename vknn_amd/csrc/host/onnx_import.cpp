@@ -153,6 +153,9 @@ namespace vknn {
                 int64_t n = 1;
                 for (int64_t d: dims) {
                     if (d < 0) malformed("tensor '" + name + "' has a negative dimension");
+                    // no product may wrap: a wrapped count would pass the byte checks below while
+                    // the shape still claims the huge size
+                    if (d && n > (int64_t(1) << 40) / d) malformed("tensor '" + name + "' has more than 2^40 elements");
                     n *= d;
                 }
                 return n;
@@ -242,7 +245,7 @@ namespace vknn {
             if (t.raw) {
                 const size_t eb = elemBytes(t.dtype);
                 if (!eb) malformed("tensor '" + t.name + "' has unsupported element type " + std::to_string(t.dtype));
-                if (t.rawN < (size_t) n * eb) malformed("tensor '" + t.name + "' holds fewer bytes than its dims need");
+                if ((size_t) n > t.rawN / eb) malformed("tensor '" + t.name + "' holds fewer bytes than its dims need");
                 for (int64_t i = 0; i < n; ++i) v[i] = (float) rawValue(t.raw, t.dtype, i);
                 return v;
             }
@@ -265,7 +268,7 @@ namespace vknn {
         std::vector<int64_t> int64Values(const TensorMsg &t, int64_t n) {
             std::vector<int64_t> v((size_t) n);
             if (t.raw) {
-                if (t.rawN < (size_t) n * 8) malformed("tensor '" + t.name + "' holds fewer bytes than its dims need");
+                if ((size_t) n > t.rawN / 8) malformed("tensor '" + t.name + "' holds fewer bytes than its dims need");
                 std::memcpy(v.data(), t.raw, (size_t) n * 8);
             } else {
                 if ((int64_t) t.int64s.size() < n) malformed("tensor '" + t.name + "' holds fewer values than its dims need");
@@ -518,7 +521,8 @@ namespace vknn {
                 }
                 const std::vector<uint8_t> &file = it->second;
                 const int64_t len = t.length >= 0 ? t.length : (int64_t) file.size() - t.offset;
-                if (t.offset < 0 || len < 0 || t.offset + len > (int64_t) file.size())
+                // checked without adding: offset and length come from the file and may be near INT64_MAX
+                if (t.offset < 0 || len < 0 || t.offset > (int64_t) file.size() || len > (int64_t) file.size() - t.offset)
                     malformed("external slice of tensor '" + t.name + "' lies outside " + path);
                 t.raw  = file.data() + t.offset;
                 t.rawN = (size_t) len;

@@ -1155,6 +1155,14 @@ int vkhip_conv_forward_scaled(const vkhip_conv_desc *d, const vkhip_conv_plan *p
 int vkhip_conv_forward_noalloc(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob,
                                const void *res, void *y, vkhip_stream_t s) {
     if (!d || !plan) return set_error(VKHIP_ERR_INVALID, "conv_forward_noalloc: null argument");
+    // The scratch is a fixed array next to other module globals: size it from the descriptor, not
+    // from the caller's plan, so a plan made for another shape cannot make a kernel write past it.
+    vkhip_conv_plan fresh;
+    if (vkhip_conv_plan_make(d, plan->algo, plan->tile, plan->ksplit, &fresh) != VKHIP_OK)
+        return set_error(VKHIP_ERR_INVALID, "conv_forward_noalloc: the plan does not fit the descriptor");
+    if (fresh.workspace_bytes != plan->workspace_bytes || fresh.weight_bytes != plan->weight_bytes)
+        return set_error(VKHIP_ERR_INVALID, "conv_forward_noalloc: the plan's sizes (workspace %zu, weights %zu) differ from the "
+                         "descriptor's (%zu, %zu)", plan->workspace_bytes, plan->weight_bytes, fresh.workspace_bytes, fresh.weight_bytes);
     if (plan->workspace_bytes > VKHIP_NOALLOC_SCRATCH_BYTES)
         return set_error(VKHIP_ERR_INVALID, "conv_forward_noalloc: the plan needs %zu bytes of workspace, more than the %zu-byte scratch",
                          plan->workspace_bytes, (size_t) VKHIP_NOALLOC_SCRATCH_BYTES);
