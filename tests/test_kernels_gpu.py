@@ -121,7 +121,8 @@ def test_conv_auto(gpu, case):
 
 NUM_TILES = V.vkhip().vkhip_conv_tile_count()
 BD_TILES = [8, 9, 10]            # conv_bd_kernel tiles (A via LDS DMA, B gathered into registers)
-DMA_TILES = [11, 12, 13, 14, 15, 16, 24, 25, 28, 29, 30, 31]    # conv_dma_kernel tiles (A and B via LDS DMA; dense B only)
+PERS_TILES = [36, 37, 38, 39, 40, 41, 42]  # conv_dma_persist_kernel tiles (conv_dma_kernel's tiles, one workgroup walks many)
+DMA_TILES = [11, 12, 13, 14, 15, 16, 24, 25, 28, 29, 30, 31] + PERS_TILES  # dense-B tiles (A and B via LDS DMA)
 HALO_TILES = [17, 18, 19, 20, 26, 27, 32, 33, 34, 35]      # conv_halo_kernel tiles (3x3 s1 p1: input band staged once for all taps)
 STEM_TILES = [21, 22, 23]                 # conv_stem_kernel tiles (3x3/7x7 over at most 4 input channels)
 GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES + HALO_TILES + STEM_TILES]
@@ -179,7 +180,37 @@ def test_conv_dma_1x1(gpu, tile, shape):
     assert_parity(got, oracle_conv(x, w, b, res=res, act=1), f"dma 1x1 tile {tile} {shape}")
 
 
-@pytest.mark.parametrize("tile", [14, 15, 24, 25])
+@pytest.mark.parametrize("tile", PERS_TILES)
+@pytest.mark.parametrize("shape", [(32, 64, 28, 28, 512), (17, 200, 7, 7, 256), (9, 96, 15, 15, 200)])
+def test_conv_dma_persist_many_tiles(gpu, tile, shape):
+    """Persistent tiles on shapes with more tiles than resident workgroups (every workgroup walks
+    several tiles and its ring crosses tile boundaries), K tails, odd images, ragged channels,
+    residual + ReLU6 epilogue; then the same shape without a residual."""
+    N, C, H, W, Cout = shape
+    r = rng(700 + tile + C)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, 1, 1)) * 0.1).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    res = round_half(r.standard_normal((N, Cout, H, W)))
+    got, plan, _ = gpu_conv(x, w, b, act=2, res=res, algo=V.CONV_GEMM, tile=tile)
+    assert plan.tile == tile
+    assert_parity(got, oracle_conv(x, w, b, res=res, act=2), f"persistent 1x1 tile {tile} {shape}")
+    got, plan, _ = gpu_conv(x, w, b, act=1, algo=V.CONV_GEMM, tile=tile)
+    assert_parity(got, oracle_conv(x, w, b, act=1), f"persistent 1x1 no residual tile {tile} {shape}")
+
+
+def test_conv_persist_tiles_refuse_other_algorithms(gpu):
+    """Persistent tiles run plain GEMM plans only: split-K and Winograd plans are refused."""
+    lib = V.vkhip()
+    plan = V.ConvPlan()
+    d, _ = conv_desc((2, 64, 8, 8), (64, 64, 1, 1))
+    d3, _ = conv_desc((2, 64, 8, 8), (64, 64, 3, 3), pads=(1, 1, 1, 1))
+    for t in PERS_TILES:
+        assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_SPLITK, t, 2, ctypes.byref(plan)) != 0
+        assert lib.vkhip_conv_plan_make(ctypes.byref(d3), V.CONV_WINOGRAD, t, 0, ctypes.byref(plan)) != 0
+
+
+@pytest.mark.parametrize("tile", [14, 15, 24, 25, 36, 38, 40, 41])
 @pytest.mark.parametrize("shape", [(2, 64, 14, 14, 128), (3, 72, 9, 11, 70), (1, 256, 28, 28, 512)])
 def test_conv_dma_1x1_stride2(gpu, tile, shape):
     """Stride-2 1x1 (ResNet downsample) on the dense-B kernel: one pixel per copy lane with its

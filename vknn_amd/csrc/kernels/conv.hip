@@ -696,6 +696,33 @@ namespace vkhip {
 
     static size_t align256(size_t v) { return (v + 255) & ~(size_t) 255; }
 
+    // Grid of a persistent kernel: the workgroups the device holds at once (occupancy of this
+    // kernel x CUs), a multiple of 8 (its tile order deals tiles to the 8 XCDs), and no more than
+    // the tiles need.
+    static unsigned persist_grid(GemmKernelFn fn, int threads, int64_t ntiles) {
+        static std::mutex                   mu;
+        static std::vector<std::pair<const void *, int>> occ;
+        static int                          cus = 0;
+        int                                 n   = 0;
+        {
+            std::lock_guard<std::mutex> lock(mu);
+            if (!cus) {
+                int dev = 0;
+                if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                    cus <= 0)
+                    cus = 256;
+            }
+            for (auto &e: occ)
+                if (e.first == (const void *) fn) n = e.second;
+            if (!n) {
+                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void *) fn, threads, 0) != hipSuccess || n <= 0) n = 1;
+                occ.emplace_back((const void *) fn, n);
+            }
+        }
+        int64_t g = std::max<int64_t>(8, ((int64_t) cus * n) / 8 * 8);
+        return (unsigned) std::min<int64_t>(g, round_up(ntiles, 8));
+    }
+
     // Scratch of the allocation-free forward entry point: one copy per GPU (a __device__ array
     // lives in every device's memory at its own address). Host code never passes the array's name
     // to a kernel: it is only a host-side handle, so the per-device address comes from
@@ -733,6 +760,7 @@ int vkhip_conv_tile_count(void) { return kNumTiles; }
 const char *vkhip_conv_plan_kernel(const vkhip_conv_plan *plan) {
     static const char *kinds[] = {"conv_gemm_kernel", "conv_bd_kernel", "conv_dma_kernel", "conv_halo_kernel", "conv_stem_kernel"};
     if (!plan) return "?";
+    if (plan->algo == VKHIP_CONV_GEMM && plan->tile >= 0 && plan->tile < kNumTiles && kTiles[plan->tile].PERS) return "conv_dma_persist_kernel";
     if (plan->algo == VKHIP_CONV_DEPTHWISE) return "dwconv_lds_kernel";
     if (plan->tile < 0 || plan->tile >= kNumTiles) return "?";
     if (plan->algo == VKHIP_CONV_WINOGRAD) return "wino_input_kernel+conv_gemm_kernel+wino_output_kernel";
@@ -802,6 +830,8 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d has no stride-2 variant (LDS)", tile);
     if (kTiles[tile].kind == 2 && !dma_eligible(d, wino))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a dense B operand (1x1 stride 1 with an even pixel count, or Winograd)", tile);
+    if (kTiles[tile].PERS && (algo != VKHIP_CONV_GEMM || d->in_scale))
+        return set_error(VKHIP_ERR_UNSUPPORTED, "persistent tile %d runs plain GEMM plans only (no split-K, Winograd or input scale)", tile);
     ConvGeom g = gemm_geom(d, tile, wino);
     plan->algo = algo;
     plan->tile = tile;
@@ -1100,7 +1130,14 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
             d->act_hi, d->has_res, (int) yps);
         return check_launch("splitk_reduce");
     }
-    a.omode = OMODE_EPILOGUE;
+    a.omode   = OMODE_EPILOGUE;
+    a.n_tiles = (int) g.n_tiles;
+    if (t.PERS) {
+        const int threads = 64 * (t.WM * t.WN + kProducers);
+        dim3      grid(persist_grid(fn, threads, g.m_tiles * g.n_tiles), 1, 1);
+        fn<<<grid, threads, 0, st>>>(a);
+        return check_launch("conv_gemm_persist");
+    }
     dim3 grid((unsigned) (g.m_tiles * g.n_tiles), 1, 1);
     fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
     return check_launch("conv_gemm");

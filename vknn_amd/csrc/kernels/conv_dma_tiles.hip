@@ -1,4 +1,5 @@
-// Tile instantiations of conv_dma_kernel (tiles 11-16, 24, 25, 28-31: dense B operands via LDS DMA).
+// Tile instantiations of conv_dma_kernel (tiles 11-16, 24, 25, 28-31: dense B operands via LDS DMA) and of its
+// persistent variant conv_dma_persist_kernel (tiles 36-42).
 #include "conv_kernels.h"
 
 namespace vkhip {
@@ -21,6 +22,17 @@ namespace vkhip {
             else return nullptr;
         }
         return pick_dma_ps<FM, FN, NS, WM, WN, 8>(steps);
+    }
+
+    // persistent variants (the ring spans tiles, so it is never cut to the step count)
+    template <int FM, int FN, int NS, int WM, int WN>
+    static GemmKernelFn pick_pers(int bmode) {
+        constexpr int lds16 = NS * ((32 * FM * WM + 2 * 32 * FN * WN) * kBK * 2 + 1024) + 1024; // ring + bias slices + spare
+        if (bmode == 2) {
+            if constexpr (lds16 <= 160 * 1024) return conv_dma_persist_kernel<FM, FN, NS, WM, WN, 16>;
+            else return nullptr;
+        }
+        return conv_dma_persist_kernel<FM, FN, NS, WM, WN, 8>;
     }
 
     // the smallest band-size instantiation (NBIS ascending) that holds nbi chunks per slot
@@ -50,6 +62,13 @@ namespace vkhip {
             case 29: return pick_dma<2, 2, 3, 2, 2>(steps, bmode);
             case 30: return pick_dma<2, 2, 3, 1, 4>(steps, bmode);
             case 31: return pick_dma<1, 2, 4, 2, 2>(steps, bmode);
+            case 36: return pick_pers<2, 2, 2, 2, 2>(bmode);
+            case 37: return pick_pers<2, 2, 3, 2, 2>(bmode);
+            case 38: return pick_pers<1, 2, 2, 2, 2>(bmode);
+            case 39: return pick_pers<1, 2, 4, 2, 2>(bmode);
+            case 40: return pick_pers<2, 2, 2, 1, 4>(bmode);
+            case 41: return pick_pers<2, 2, 2, 4, 2>(bmode);
+            case 42: return pick_pers<2, 2, 4, 2, 2>(bmode);
         }
         return nullptr;
     }

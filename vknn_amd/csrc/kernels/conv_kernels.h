@@ -48,6 +48,7 @@ namespace vkhip {
         int           act;
         float         lo, hi;
         int           has_res, omode, m_tiles;
+        int           n_tiles;                         // column tiles (persistent kernels walk m_tiles x n_tiles)
         long long     x_bstride, w_bstride, y_bstride; // batch (blockIdx.z) strides: uint2 / half / uint2
         unsigned      x_bytes;                         // bytes of one batch slice of x (< 2 GiB)
         unsigned      y_bytes;                         // bytes of one batch slice of y (< 2 GiB)
@@ -1037,6 +1038,259 @@ namespace vkhip {
         gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, bz, lane);
     }
 
+    // ------------------------------------------------------------------ persistent LDS-DMA GEMM kernel
+    // conv_dma_kernel's operands, stage layout and 16-K step, with the copies and the math split
+    // over two groups of waves, run by one workgroup per CU that walks a strided list of tiles.
+    // Why: in conv_dma_kernel every wave both copies its share of each K stage and stores its
+    // epilogue, and the vector-memory counter retires in issue order, so a wave that waits for its
+    // next copies also waits for every store it issued before them; and all workgroups of a launch
+    // start together, so the whole GPU loads, then stores, in lockstep. Measured on 1x1 layers with
+    // a residual, the load phase and the epilogue phase add up instead of overlapping. Here:
+    //   * NP = 4 producer waves only copy: each issues its quarter of every K stage's A and B
+    //     chunks (buffer-load-to-LDS) into an NS-stage ring, NS-1 stages ahead, across tile
+    //     boundaries, and waits only for its own copies; with the stage's copies it also copies
+    //     the tile's bias slice into the stage that holds the tile's last K step;
+    //   * the WM x WN consumer waves only compute and store: at the first K stage of a tile they
+    //     load its residual into registers (hidden behind the tile's MFMAs), run the 16-K steps
+    //     from LDS, then apply bias (from LDS), residual and activation and store. Their counter
+    //     holds only residual loads and stores, so the epilogue of tile t never waits for copies
+    //     and the producers keep streaming tile t+1 meanwhile.
+    // One s_barrier per K stage pairs the two groups: before it the producers wait for stage s's
+    // copies and the consumers finish stage s-1; after it the consumers read stage s and the
+    // producers refill stage s-1's buffer.
+    // Tile order: at step it, XCD x runs tiles (it*8 + x)*per + 0..per-1 (per = gridDim.x / 8;
+    // workgroup ids are dealt to the XCDs round-robin), so the tiles an XCD runs at once are
+    // consecutive and share their B columns (tile % m_tiles is the M tile) in its L2.
+    // GEMM epilogue mode only (no split-K partials, no Winograd positions).
+    constexpr int kProducers = 4;
+    template <int FM, int FN, int NS, int WM, int WN, int PS = 8>
+    __global__ __launch_bounds__(64 * (WM * WN + kProducers), 1) void conv_dma_persist_kernel(GemmArgs a) {
+        constexpr int NC     = WM * WN;       // consumer waves
+        constexpr int NP     = kProducers;
+        constexpr int BM     = 32 * FM * WM;
+        constexpr int BN     = 32 * FN * WN;
+        constexpr int MF     = BM / 32;
+        constexpr int ASTAGE = BM * kBK * 2;
+        constexpr int BSTAGE = BN * kBK * 2 * PS / 8;
+        constexpr int NA     = ASTAGE / (NP * 1024);  // A chunks per producer per stage
+        constexpr int NB     = BSTAGE / (NP * 1024);  // B chunks per producer per stage
+        static_assert(NS >= 2 && NA >= 1 && NB >= 1 && ASTAGE % (NP * 1024) == 0 && BSTAGE % (NP * 1024) == 0, "stage split");
+        static_assert(BM * 4 <= 1024, "bias slice fits one 1 KB copy");
+        constexpr int BPB    = BN * PS / 1024;
+        constexpr int STAGE  = ASTAGE + BSTAGE + 1024; // + the bias slice
+        constexpr int NPP    = NA + NB + 1;            // copies per producer per stage (one bias copy each; 3 of them idle)
+        static_assert((NS - 1) * NPP <= 63, "copies in flight fit the counter");
+        __shared__ __attribute__((aligned(16))) unsigned char sm[NS * STAGE + 1024]; // + a spare block for idle bias copies
+
+        const int tid  = threadIdx.x;
+        const int lane = tid & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+        const int ntiles = a.m_tiles * a.n_tiles;
+        const int per    = gridDim.x >> 3;
+        const int first  = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+        const int ntw    = first < ntiles ? (ntiles - first + 8 * per - 1) / (8 * per) : 0; // tiles of this workgroup
+        const int nst    = a.nsteps;
+        const int S      = ntw * nst;                                                          // K stages of this workgroup
+        if (S == 0) return;
+        auto tile_of = [&](int it) { return first + it * 8 * per; };
+        constexpr unsigned kInvalid = 0x80000000u;
+
+        if (wave >= NC) {
+            // ---------------- producer
+            const int pw = wave - NC;
+            const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) a.x_bytes, 0x00020000);
+            const __amdgpu_buffer_rsrc_t wrs =
+                __builtin_amdgcn_make_buffer_rsrc((void *) a.w, (short) 0, a.m_tiles * nst * ASTAGE, 0x00020000);
+            const __amdgpu_buffer_rsrc_t brs =
+                __builtin_amdgcn_make_buffer_rsrc((void *) a.bias, (short) 0, a.m_tiles * BM * 4, 0x00020000);
+            const int hw8 = a.HW * 8;
+            int       i_it = 0, i_ks = 0, m_tile = 0;
+            unsigned  pbase[BPB];
+            auto set_issue_tile = [&](int it) __attribute__((always_inline)) {
+                const int t  = tile_of(it);
+                m_tile       = t % a.m_tiles;
+                const int n0 = (t / a.m_tiles) * BN;
+#pragma unroll
+                for (int pb = 0; pb < BPB; ++pb) {
+                    if constexpr (PS == 8) {
+                        const int p = n0 + pb * 128 + 2 * lane;
+                        const int n = p / a.OHWp;
+                        pbase[pb]   = p < a.Pv ? (unsigned) ((n * a.x_pstride * a.HW + (p - n * a.OHWp)) * 8) : kInvalid;
+                    } else {
+                        const int p  = n0 + pb * 64 + lane;
+                        const int n  = p / a.OHW;
+                        const int r  = p - n * a.OHW;
+                        const int oy = r / a.OW;
+                        pbase[pb]    = p < a.P ? (unsigned) ((n * a.x_pstride * a.HW + (a.SH * oy) * a.W + a.SW * (r - oy * a.OW)) * 8) : kInvalid;
+                    }
+                }
+            };
+            auto issue = [&](int buf) __attribute__((always_inline)) {
+                unsigned char *dst = sm + buf * STAGE;
+                const unsigned wofs = (unsigned) ((m_tile * nst + i_ks) * ASTAGE);
+#pragma unroll
+                for (int r = 0; r < NA; ++r) {
+                    const int chunk = (r * NP + pw) * 1024;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (__attribute__((address_space(3))) void *) (dst + chunk), 16,
+                                                             (unsigned) (chunk + lane * 16) + wofs, 0, 0, 0);
+                }
+#pragma unroll
+                for (int r = 0; r < NB; ++r) {
+                    const int c    = r * NP + pw;
+                    const int slot = i_ks * 16 + c / BPB; // wave-uniform
+                    const unsigned vo = slot < a.Kslots ? pbase[c % BPB] : kInvalid;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void *) (dst + ASTAGE + c * 1024), 16, vo,
+                                                             (unsigned) (slot * hw8), 0, 0);
+                }
+                // producer 0 copies the tile's bias into the stage of its last K step; the others
+                // copy nothing into the spare block, so every producer's copy count stays NPP
+                const bool bias_here = pw == 0 && i_ks == nst - 1;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (__attribute__((address_space(3))) void *) (bias_here ? dst + ASTAGE + BSTAGE : sm + NS * STAGE),
+                                                         16, bias_here && lane * 16 < BM * 4 ? (unsigned) (m_tile * BM * 4 + lane * 16) : kInvalid, 0, 0, 0);
+                if (++i_ks == nst) {
+                    i_ks = 0;
+                    if (++i_it < ntw) set_issue_tile(i_it);
+                }
+            };
+            set_issue_tile(0);
+#pragma unroll
+            for (int d = 0; d < NS - 1; ++d)
+                if (d < S) issue(d);
+            constexpr int kAhead = (NS - 2) * NPP;
+            int buf = 0;
+            for (int s = 0; s < S; ++s) {
+                if (s + NS - 2 < S) __builtin_amdgcn_s_waitcnt((kAhead & 15) | (7 << 4) | (15 << 8) | ((kAhead >> 4) << 14));
+                else __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+                __asm__ volatile("s_barrier" ::: "memory");
+                const int nb = buf == 0 ? NS - 1 : buf - 1; // (s + NS - 1) % NS
+                if (s + NS - 1 < S) issue(nb);
+                buf = buf + 1 == NS ? 0 : buf + 1;
+            }
+            return;
+        }
+
+        // ---------------- consumer
+        const int wmi  = wave / WN;
+        const int wni  = wave % WN;
+        const int wm0  = wmi * 32 * FM;
+        const int wn0  = wni * 32 * FN;
+        const int lrow = lane & 31;
+        const int lk   = lane >> 5;
+        const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc((void *) a.y, (short) 0, (int) a.y_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rrs =
+            __builtin_amdgcn_make_buffer_rsrc((void *) (a.has_res ? a.res : a.y), (short) 0, a.has_res ? (int) a.y_bytes : 0, 0x00020000);
+
+        float16v acc[FM][FN];
+        u32x2    rv[FN][FM][4];
+        // byte offset of output (j, i, qq) of this lane in y (and the residual), or kInvalid
+        auto out_offset = [&](int t, int j, int i, int qq) __attribute__((always_inline)) {
+            const int  px  = (t / a.m_tiles) * BN + wn0 + j * 32 + lrow;
+            const int  pn  = px / a.OHWp;
+            const int  pr  = px - pn * a.OHWp;
+            const int  ocb = ((t % a.m_tiles) * BM + wm0 + i * 32 + qq * 8 + lk * 4) >> 2;
+            return (px < a.Pv) & (pr < a.OHW) & (ocb < a.Coutb) ? (unsigned) (((pn * a.y_pstride + ocb) * a.OHW + pr) * 8) : kInvalid;
+        };
+        auto prefetch_residual = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int qq = 0; qq < 4; ++qq) rv[j][i][qq] = a.has_res ? __builtin_amdgcn_raw_buffer_load_b64(rrs, out_offset(t, j, i, qq), 0, 0)
+                                                                            : u32x2 {0u, 0u};
+        };
+        auto store_tile = [&](int t, const unsigned char *bias_lds, auto act_c) __attribute__((always_inline)) {
+            constexpr int ACT = decltype(act_c)::value;
+            const int     mw0 = (t % a.m_tiles) * BM + wm0;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int qq = 0; qq < 4; ++qq) {
+                    const float4v bv = *reinterpret_cast<const float4v *>(bias_lds + (wm0 + i * 32 + qq * 8 + lk * 4) * 4);
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+                        const int oc = mw0 + i * 32 + qq * 8 + lk * 4;
+                        float4v   v  = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
+                        v += bv;
+                        v += h4_to_f4(__builtin_bit_cast(half4, rv[j][i][qq]));
+                        v.x = apply_act(v.x, ACT, a.lo, a.hi);
+                        v.y = apply_act(v.y, ACT, a.lo, a.hi);
+                        v.z = apply_act(v.z, ACT, a.lo, a.hi);
+                        v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                        if (oc + 0 >= a.Cout) v.x = 0.f;
+                        if (oc + 1 >= a.Cout) v.y = 0.f;
+                        if (oc + 2 >= a.Cout) v.z = 0.f;
+                        if (oc + 3 >= a.Cout) v.w = 0.f;
+                        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, out_offset(t, j, i, qq), 0, 0);
+                    }
+                }
+        };
+        auto epilogue = [&](int t, const unsigned char *bias_lds) __attribute__((always_inline)) {
+            using std::integral_constant;
+            switch (a.act) {
+                case VKHIP_ACT_RELU: store_tile(t, bias_lds, integral_constant<int, VKHIP_ACT_RELU> {}); break;
+                case VKHIP_ACT_RELU6: store_tile(t, bias_lds, integral_constant<int, VKHIP_ACT_RELU6> {}); break;
+                case VKHIP_ACT_CLIP: store_tile(t, bias_lds, integral_constant<int, VKHIP_ACT_CLIP> {}); break;
+                case VKHIP_ACT_HARDSWISH: store_tile(t, bias_lds, integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
+                case VKHIP_ACT_SILU: store_tile(t, bias_lds, integral_constant<int, VKHIP_ACT_SILU> {}); break;
+                default: store_tile(t, bias_lds, integral_constant<int, VKHIP_ACT_NONE> {}); break;
+            }
+        };
+
+        const int g = lane >> 5;
+        auto compute = [&](int buf) __attribute__((always_inline)) {
+            const unsigned char *Ab = sm + buf * STAGE + ((wmi * FM) * 64 + lane) * 16;
+            const unsigned char *Bb = sm + buf * STAGE + ASTAGE + (2 * g * BN + wn0 + (lane & 31)) * PS;
+            half8 fa[2][FM], fb[2][FN];
+            auto rd = [&](int kk, int d) __attribute__((always_inline)) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const u32x2 lo = *reinterpret_cast<const u32x2 *>(Bb + (kk * 4 * BN + 32 * j) * PS);
+                    const u32x2 hi = *reinterpret_cast<const u32x2 *>(Bb + ((kk * 4 + 1) * BN + 32 * j) * PS);
+                    fb[d][j] = __builtin_bit_cast(half8, u32x4_make(lo.x, lo.y, hi.x, hi.y));
+                }
+#pragma unroll
+                for (int i = 0; i < FM; ++i) fa[d][i] = *reinterpret_cast<const half8 *>(Ab + (kk * MF + i) * 1024);
+            };
+            rd(0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                if (kk < 3) rd(kk + 1, (kk + 1) & 1);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk & 1][i], fb[kk & 1][j], acc[i][j], 0, 0, 0);
+                if (kk < 3) StepSchedule<0, FM * FN, FM + 2 * FN, 4 * FN>::apply();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+
+        int buf = 0;
+        for (int it = 0; it < ntw; ++it) {
+            const int t = tile_of(it);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+            int last = buf;
+            for (int ks = 0; ks < nst; ++ks) {
+                __asm__ volatile("s_barrier" ::: "memory");
+                if (ks == 0) prefetch_residual(t);
+                compute(buf);
+                last = buf;
+                buf  = buf + 1 == NS ? 0 : buf + 1;
+            }
+            // the bias slice rides in the tile's last stage, which no copy overwrites before the
+            // next barrier
+            epilogue(t, sm + last * STAGE + ASTAGE + BSTAGE);
+        }
+    }
+
     // ------------------------------------------------------------------ 3x3 halo-tile GEMM kernel
     // Direct 3x3 pad-1 convolution, stride 1 or 2 (Cin a multiple of 16*KK, even input width W),
     // that reads each input pixel once per workgroup instead of once per tap: the workgroup's BN
@@ -1665,8 +1919,10 @@ namespace vkhip {
     // kind 3: conv_halo_kernel (3x3 pad-1, stride 1 or 2: input band staged once in LDS for all 9
     //         taps), KK 16-channel K steps per LDS stage.
     // kind 4: conv_stem_kernel (3x3 or 7x7, stride 1 or 2, pad K/2, at most 4 input channels).
+    // PERS (kind 2 only): the persistent variant (conv_dma_persist_kernel), gridDim = resident
+    // workgroups, each walking a strided list of tiles.
     struct TileCfg {
-        int BM, BN, WM, WN, kind, FM, FN, KK;
+        int BM, BN, WM, WN, kind, FM, FN, KK, PERS;
     };
     static const TileCfg kTiles[] = {
         {128, 128, 2, 2, 0, 0, 0}, // 0
@@ -1705,9 +1961,17 @@ namespace vkhip {
         {32, 128, 1, 4, 3, 1, 1, 1},  // 33 halo for few output channels, small bands (2-stage ring)
         {32, 256, 1, 4, 3, 1, 2, 1},  // 34 tile 32 with one stage (single-stage reductions: more workgroups per CU)
         {32, 128, 1, 4, 3, 1, 1, 1},  // 35 tile 33 with one stage
+        {128, 128, 2, 2, 2, 2, 2, 0, 1}, // 36 persistent tile 14 (2-stage ring)
+        {128, 128, 2, 2, 2, 2, 2, 0, 1}, // 37 persistent tile 14, 3-stage ring
+        {64, 128, 2, 2, 2, 1, 2, 0, 1},  // 38 persistent tile 24 (2-stage ring)
+        {64, 128, 2, 2, 2, 1, 2, 0, 1},  // 39 persistent tile 24, 4-stage ring
+        {64, 256, 1, 4, 2, 2, 2, 0, 1},  // 40 persistent tile 25 (2-stage ring)
+        {256, 128, 4, 2, 2, 2, 2, 0, 1}, // 41 persistent tile 15 (8 waves, 2-stage ring)
+        {128, 128, 2, 2, 2, 2, 2, 0, 1}, // 42 persistent tile 14, 4-stage ring
     };
-    constexpr int kNumTiles = 36;
-    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8, 15, 0, 0, 0, 0, 15, 8, 16, 10};
+    constexpr int kNumTiles = 43;
+    constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8, 15, 0, 0, 0, 0, 15, 8, 16, 10,
+                                            0, 0, 0, 0, 0, 0, 0};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
