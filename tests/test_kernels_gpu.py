@@ -125,7 +125,8 @@ PERS_TILES = [36, 37, 38, 39, 40, 41, 42]  # conv_dma_persist_kernel tiles (conv
 DMA_TILES = [11, 12, 13, 14, 15, 16, 24, 25, 28, 29, 30, 31] + PERS_TILES  # dense-B tiles (A and B via LDS DMA)
 HALO_TILES = [17, 18, 19, 20, 26, 27, 32, 33, 34, 35]      # conv_halo_kernel tiles (3x3 s1 p1: input band staged once for all taps)
 STEM_TILES = [21, 22, 23]                 # conv_stem_kernel tiles (3x3/7x7 over at most 4 input channels)
-GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES + HALO_TILES + STEM_TILES]
+THIN_TILES = [43, 44, 45]                 # conv_thin_kernel tiles (<= 32 input, 16/32/64 output channels)
+GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES + HALO_TILES + STEM_TILES + THIN_TILES]
 
 
 @pytest.mark.parametrize("tile", GATHER_TILES)
@@ -178,6 +179,54 @@ def test_conv_dma_1x1(gpu, tile, shape):
     got, plan, _ = gpu_conv(x, w, b, act=1, res=res, algo=V.CONV_GEMM, tile=tile)
     assert plan.tile == tile
     assert_parity(got, oracle_conv(x, w, b, res=res, act=1), f"dma 1x1 tile {tile} {shape}")
+
+
+@pytest.mark.parametrize("shape", [(2, 16, 20, 24, 16, 3, 1), (2, 16, 20, 24, 32, 3, 2), (1, 3, 32, 34, 16, 3, 2), (2, 32, 18, 18, 32, 3, 1),
+                                   (2, 32, 16, 16, 64, 1, 1), (3, 24, 10, 14, 24, 3, 1), (2, 16, 30, 150, 16, 3, 1), (2, 5, 16, 16, 40, 3, 2),
+                                   (1, 8, 9, 130, 12, 3, 2), (2, 12, 7, 6, 64, 3, 1), (1, 32, 12, 12, 20, 3, 2)])
+@pytest.mark.parametrize("act", [1, 5])
+def test_conv_thin(gpu, shape, act):
+    """Thin-channel kernel (16x16x32 MFMA, weights in registers, double-buffered input bands):
+    every tile that takes the shape, against the oracle. Ragged channel counts (Cin 3, 5, 12, 24:
+    zero slots of the rounded reduction), column blocks cut by the image edge, bands above and
+    below the image, stride 2, 1x1, ReLU and SiLU epilogues."""
+    N, C, H, W, Cout, K, S = shape
+    r = rng(900 + C + H + Cout + K * S)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, K, K)) * np.sqrt(2.0 / (K * K * C))).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    p = K // 2
+    ref = oracle_conv(x, w, b, (S, S), (p, p, p, p), act=act)
+    ran = 0
+    lib = V.vkhip()
+    for tile in THIN_TILES:
+        d, _ = conv_desc(x.shape, w.shape, (S, S), (p, p, p, p), act=act)
+        if lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, tile, 0, ctypes.byref(V.ConvPlan())) != 0:
+            assert Cout > {43: 16, 44: 32, 45: 64}[tile] or (C > 16 and tile == 45), (tile, shape)  # not instantiated: weights over budget
+            continue
+        got, plan, _ = gpu_conv(x, w, b, (S, S), (p, p, p, p), act=act, algo=V.CONV_GEMM, tile=tile)
+        assert plan.tile == tile
+        assert_parity(got, ref, f"thin tile {tile} {shape} act {act}")
+        ran += 1
+    assert ran > 0
+
+
+def test_conv_thin_refuses_other_shapes(gpu):
+    """Thin tiles refuse residuals, odd input widths, 5x5, dilation, grouped convs, too many
+    channels and split-K / Winograd plans."""
+    lib = V.vkhip()
+    plan = V.ConvPlan()
+    bad = [dict(x=(1, 16, 8, 8), w=(16, 16, 3, 3), pads=(1, 1, 1, 1), has_res=1), dict(x=(1, 16, 8, 9), w=(16, 16, 3, 3), pads=(1, 1, 1, 1)),
+           dict(x=(1, 16, 8, 8), w=(16, 16, 5, 5), pads=(2, 2, 2, 2)), dict(x=(1, 16, 8, 8), w=(16, 16, 3, 3), pads=(2, 2, 2, 2), dil=(2, 2)),
+           dict(x=(1, 40, 8, 8), w=(16, 40, 3, 3), pads=(1, 1, 1, 1)), dict(x=(1, 16, 8, 8), w=(80, 16, 3, 3), pads=(1, 1, 1, 1))]
+    for c in bad:
+        d, _ = conv_desc(c["x"], c["w"], pads=c["pads"], dil=c.get("dil", (1, 1)), has_res=c.get("has_res", 0))
+        for t in THIN_TILES:
+            assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, t, 0, ctypes.byref(plan)) != 0, (c, t)
+    d, _ = conv_desc((1, 16, 8, 8), (16, 16, 3, 3), pads=(1, 1, 1, 1))
+    assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, 43, 0, ctypes.byref(plan)) == 0
+    assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_SPLITK, 43, 2, ctypes.byref(plan)) != 0
+    assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_WINOGRAD, 43, 0, ctypes.byref(plan)) != 0
 
 
 @pytest.mark.parametrize("tile", PERS_TILES)

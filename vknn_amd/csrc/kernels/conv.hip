@@ -604,6 +604,18 @@ namespace vkhip {
         return (int) ceil_div(rows * (RS / 2), 64);
     }
 
+    // conv_thin_kernel: 3x3 pad 1 (stride 1 or 2) or 1x1 pad 0 stride 1, dilation 1, Cin <= 32, Cout
+    // within the tile's BM, even input width (the band copies whole pixel pairs), no residual or
+    // input scale, and an instantiated kernel (its weights fit the register budget)
+    static bool thin_shape_ok(const vkhip_conv_desc *d, const TileCfg &t, int algo) {
+        const int K = d->KH, S = d->SH;
+        if (algo != VKHIP_CONV_GEMM || d->group != 1 || d->has_res || d->in_scale || d->Cin > 32 || d->Cout > t.BM) return false;
+        if (d->KW != K || d->SW != S || d->DH != 1 || d->DW != 1 || d->W % 2) return false;
+        if (!((K == 3 && d->PT == 1 && d->PL == 1 && (S == 1 || S == 2)) || (K == 1 && d->PT == 0 && d->PL == 0 && S == 1))) return false;
+        if (d->OH != (d->H + 2 * d->PT - K) / S + 1 || d->OW != (d->W + 2 * d->PL - K) / S + 1) return false;
+        return thin_kernel_for((int) ceil_div(d->Cin, 4), t.FM, K, S) != nullptr;
+    }
+
     static bool wino_eligible(const vkhip_conv_desc *d) {
         return d->group == 1 && d->KH == 3 && d->KW == 3 && d->SH == 1 && d->SW == 1 && d->PT == 1 && d->PL == 1 &&
                d->DH == 1 && d->DW == 1 && d->OH == d->H && d->OW == d->W;
@@ -637,6 +649,10 @@ namespace vkhip {
             g.nsteps = 1;
             g.bmode  = d->KH;
         }
+        if (t.kind == 5) { // (tap, channel) over the rounded slot count, 32-deep MFMA steps
+            g.nsteps = ceil_div((int64_t) d->KH * d->KW * thin_cinb(g.Cinb) * 4, 32);
+            g.Kp     = g.nsteps * 32;
+        }
         if (t.kind == 3) { // 9 taps x Cin, stages of 16*KK channels (all 9 taps each)
             g.Kp     = 9 * (int64_t) d->Cin;
             g.nsteps = d->Cin / (16 * t.KK);
@@ -659,6 +675,12 @@ namespace vkhip {
         const int     BM   = t.BM;
         const int64_t base = ((oc / BM) * g.nsteps + k / kBK) * (int64_t) (BM * kBK);
         if (t.kind == 0) return base + (oc % BM) * kBK + k % kBK; // kinds 1 and 2: fragment order
+        if (t.kind == 5) {
+            // [m_frag][step][lane][8 halves], lane = (kt%32)/8 * 16 + oc%16, kt = tap*4*cinb' + c
+            const int64_t tap = (k / 4) / g.Cinb, c = ((k / 4) % g.Cinb) * 4 + k % 4;
+            const int64_t kt  = tap * thin_cinb(g.Cinb) * 4 + c;
+            return (((oc / 16) * g.nsteps + kt / 32) * 64 + ((kt % 32) / 8) * 16 + oc % 16) * 8 + kt % 8;
+        }
         if (t.kind == 4) {
             // [m_tile][step][m_frag][lane][8 halves]; Cinb = 1, so k = tap*4 + c and step = tap/4
             const int64_t tap = k / 4, kr = (tap % 4) * 4 + k % 4, r = oc % BM;
@@ -758,7 +780,7 @@ extern "C" {
 int vkhip_conv_tile_count(void) { return kNumTiles; }
 
 const char *vkhip_conv_plan_kernel(const vkhip_conv_plan *plan) {
-    static const char *kinds[] = {"conv_gemm_kernel", "conv_bd_kernel", "conv_dma_kernel", "conv_halo_kernel", "conv_stem_kernel"};
+    static const char *kinds[] = {"conv_gemm_kernel", "conv_bd_kernel", "conv_dma_kernel", "conv_halo_kernel", "conv_stem_kernel", "conv_thin_kernel"};
     if (!plan) return "?";
     if (plan->algo == VKHIP_CONV_GEMM && plan->tile >= 0 && plan->tile < kNumTiles && kTiles[plan->tile].PERS) return "conv_dma_persist_kernel";
     if (plan->algo == VKHIP_CONV_DEPTHWISE) return "dwconv_lds_kernel";
@@ -830,6 +852,9 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d has no stride-2 variant (LDS)", tile);
     if (kTiles[tile].kind == 2 && !dma_eligible(d, wino))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a dense B operand (1x1 stride 1 with an even pixel count, or Winograd)", tile);
+    if (kTiles[tile].kind == 5 && !thin_shape_ok(d, kTiles[tile], algo))
+        return set_error(VKHIP_ERR_UNSUPPORTED, "thin tile %d needs a plain GEMM plan of a 3x3 pad-1 or 1x1 conv, stride 1 or 2 (1x1: stride 1), "
+                         "Cin <= 32, Cout <= %d, even input width, no residual", tile, kTiles[tile].BM);
     if (kTiles[tile].PERS && (algo != VKHIP_CONV_GEMM || d->in_scale))
         return set_error(VKHIP_ERR_UNSUPPORTED, "persistent tile %d runs plain GEMM plans only (no split-K, Winograd or input scale)", tile);
     ConvGeom g = gemm_geom(d, tile, wino);
@@ -1064,7 +1089,7 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
     const int split_steps = plan->algo == VKHIP_CONV_SPLITK ? (int) ceil_div(g.nsteps, plan->ksplit) : (int) g.nsteps;
     GemmKernelFn fn = gemm_kernel_for(plan->tile, g.bmode, split_steps,
                                       t.kind == 3 ? halo_nbi(d, t) * (d->W % 2 ? -1 : 1) : (t.kind == 4 ? stem_nbi(d, t) : 0), d->in_scale != 0);
-    if (!fn) return set_error(VKHIP_ERR_INVALID, "conv_forward: no kernel for tile %d", plan->tile);
+    if (!fn && t.kind != 5) return set_error(VKHIP_ERR_INVALID, "conv_forward: no kernel for tile %d", plan->tile);
 
     if (wino) {
         const int nTH = (int) ceil_div(d->OH, 2), nTW = (int) ceil_div(d->OW, 2);
@@ -1132,6 +1157,17 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
     }
     a.omode   = OMODE_EPILOGUE;
     a.n_tiles = (int) g.n_tiles;
+    if (t.kind == 5) {
+        GemmKernelFn tf = thin_kernel_for((int) g.Cinb, t.FM, d->KH, d->SH);
+        if (!tf) return set_error(VKHIP_ERR_INVALID, "conv_forward: no thin kernel for this shape");
+        const int64_t items = (int64_t) d->N * ceil_div(d->OH, 4) * ceil_div(d->OW, 64);
+        // as many workgroups as the device holds at once: the items are short, so concurrency,
+        // not the per-workgroup pipeline, hides most of the load latency (measured: one or two
+        // workgroups per CU run 1.2-2x slower than full occupancy)
+        dim3 grid((unsigned) std::min<int64_t>(persist_grid(tf, 256, items), items), 1, 1);
+        tf<<<grid, 256, 0, st>>>(a);
+        return check_launch("conv_thin");
+    }
     if (t.PERS) {
         const int threads = 64 * (t.WM * t.WN + kProducers);
         dim3      grid(persist_grid(fn, threads, g.m_tiles * g.n_tiles), 1, 1);

@@ -1919,6 +1919,8 @@ namespace vkhip {
     // kind 3: conv_halo_kernel (3x3 pad-1, stride 1 or 2: input band staged once in LDS for all 9
     //         taps), KK 16-channel K steps per LDS stage.
     // kind 4: conv_stem_kernel (3x3 or 7x7, stride 1 or 2, pad K/2, at most 4 input channels).
+    // kind 5: conv_thin_kernel (3x3 pad 1 or 1x1, stride 1 or 2, at most 32 input channels and BM
+    //         output channels, FM = BM / 16 fragments; weights in registers).
     // PERS (kind 2 only): the persistent variant (conv_dma_persist_kernel), gridDim = resident
     // workgroups, each walking a strided list of tiles.
     struct TileCfg {
@@ -1968,16 +1970,23 @@ namespace vkhip {
         {64, 256, 1, 4, 2, 2, 2, 0, 1},  // 40 persistent tile 25 (2-stage ring)
         {256, 128, 4, 2, 2, 2, 2, 0, 1}, // 41 persistent tile 15 (8 waves, 2-stage ring)
         {128, 128, 2, 2, 2, 2, 2, 0, 1}, // 42 persistent tile 14, 4-stage ring
+        {16, 256, 1, 4, 5, 1, 0, 0},     // 43 thin conv, 16 output channels (conv_thin_kernel)
+        {32, 256, 1, 4, 5, 2, 0, 0},     // 44 thin conv, 32 output channels
+        {64, 256, 1, 4, 5, 4, 0, 0},     // 45 thin conv, 64 output channels
     };
-    constexpr int kNumTiles = 43;
+    constexpr int kNumTiles = 46;
     constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8, 15, 0, 0, 0, 0, 15, 8, 16, 10,
-                                            0, 0, 0, 0, 0, 0, 0};
+                                            0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
     // Kernel selectors, one per tile family (each defined in its own translation unit so the
     // template instantiations compile in parallel). bmode / steps / nbi as in gemm_kernel_for.
     GemmKernelFn gemm_tile_kernel(int tile, int bmode);
+    // conv_thin_kernel for cinb input slots (rounded up to 1, 2, 4 or 8), mt 16-channel output
+    // fragments, a k x k kernel and stride s (nullptr if not instantiated)
+    GemmKernelFn thin_kernel_for(int cinb, int mt, int k, int s);
+    inline int thin_cinb(int64_t cinb) { return cinb <= 1 ? 1 : cinb <= 2 ? 2 : cinb <= 4 ? 4 : 8; }
     GemmKernelFn bd_tile_kernel(int tile, int bmode);
     GemmKernelFn dma_tile_kernel(int tile, int bmode, int steps, bool xs);
     GemmKernelFn halo_tile_kernel(int tile, int nbi);

@@ -1,0 +1,208 @@
+// Thin-channel direct convolution for gfx950: 3x3 (pad 1) or 1x1 (pad 0) convs, stride 1 or 2,
+// over at most 32 input and 64 output channels (the first layers of YOLOv8n and the MobileNet
+// stems: 3->16, 16->32, 16->16, 32->32 at 160x160 and above). The implicit-GEMM tiles waste most
+// of a 32-row MFMA tile and a whole LDS stage per workgroup on such layers, and the tiles are too
+// short to overlap one workgroup's load latency with another's stores, so they run at ~0.1-0.25
+// of HBM. Here:
+//   * MFMA v_mfma_f32_16x16x32_f16 (M = 16 output channels, N = 16 output pixels of one row,
+//     K = 32 values of (tap, channel)), so a 16-channel conv wastes nothing; the whole reduction
+//     of one output channel block is at most 20 fragments held in registers (the weights are
+//     loaded once per workgroup);
+//   * one persistent workgroup per CU slot walks work items of 4 output rows x 64 columns; the
+//     input band of the next item (rows (4-1)*S + K, 64*S + 4 columns, every channel slot) is
+//     copied global->LDS by buffer-load-to-LDS while the current item computes from the other
+//     half of a double buffer, and the current item's stores are issued after those copies, so
+//     the next wait never waits for them;
+//   * the accumulator layout of the 16x16 MFMA (lane l: pixel l%16, channels 4(l/16)..+3) is one
+//     NC4HW4 slot of one pixel, so every store is one 8-byte write of 4 channels.
+// Reference semantics: ConvCpu (src/backend/cpu/ops/conv.cpp:9-92) — bias, activation, fp16 store.
+#include "conv_kernels.h"
+
+namespace vkhip {
+
+    namespace thin {
+        constexpr int OR  = 4;  // output rows per work item (one per wave)
+        constexpr int OCW = 64; // output columns per work item (4 pixel tiles of 16)
+        template <int K, int S>
+        struct Band {
+            static constexpr int PAD  = K / 2;
+            static constexpr int COFF = K == 3 ? 2 : 0;                   // band column of input column ox0*S (even start)
+            static constexpr int ROWS = (OR - 1) * S + K;
+            static constexpr int COLS = ((OCW - 1) * S + K + (K == 3 ? 1 : 0) + 1) & ~1; // even: whole pixel pairs
+            static constexpr int PPR  = COLS / 2;                           // pixel pairs per band row
+        };
+    } // namespace thin
+
+    template <int CINB, int MT, int K, int S>
+    __global__ __launch_bounds__(256, 2) void conv_thin_kernel(GemmArgs a) {
+        using B = thin::Band<K, S>;
+        constexpr int OR = thin::OR, OCW = thin::OCW;
+        constexpr int CIN4   = CINB * 4;
+        constexpr int NSTEPS = (K * K * CIN4 + 31) / 32;   // 32-deep MFMA steps
+        constexpr int TP     = CINB * B::ROWS * B::PPR;    // pixel pairs of one band
+        constexpr int NI     = (TP + 63) / 64;             // 1 KB copies of one band
+        constexpr int NBW    = (NI + 3) / 4;               // copies per wave (the surplus ones copy zeros)
+        constexpr int BAND   = NBW * 4 * 1024;             // LDS bytes of one band buffer
+        static_assert(2 * BAND <= 160 * 1024, "band double buffer fits LDS");
+        static_assert(MT * NSTEPS <= 20, "weights fit the register budget");
+        __shared__ __attribute__((aligned(16))) unsigned char sm[2 * BAND];
+
+        const int lane = threadIdx.x & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int OH = a.OHW / a.OW, OW = a.OW, H = a.H, W = a.W;
+        const int N      = a.P / a.OHW;
+        const int rblk   = (OH + OR - 1) / OR, cblk = (OW + OCW - 1) / OCW;
+        const int items  = N * rblk * cblk;
+        constexpr unsigned kInvalid = 0x80000000u;
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) a.x_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc((void *) a.y, (short) 0, (int) a.y_bytes, 0x00020000);
+
+        // weights: fragment (m, j) of lane l holds rows m*16 + l%16, reduction values 32j + 8(l/16) .. +7
+        half8 wf[MT][NSTEPS];
+        {
+            const half8 *wp = reinterpret_cast<const half8 *>(a.w);
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int j = 0; j < NSTEPS; ++j) wf[m][j] = wp[(m * NSTEPS + j) * 64 + lane];
+        }
+        // per (step, half): the LDS pixel offset of this lane's 4-channel slot relative to the
+        // output pixel's band position, or -1 for a zero pad of the reduction (tap >= K*K)
+        int boff[NSTEPS][2];
+#pragma unroll
+        for (int j = 0; j < NSTEPS; ++j)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int k   = 32 * j + 8 * (lane >> 4) + 4 * q;
+                const int tap = k / CIN4, slot = (k % CIN4) / 4;
+                boff[j][q]    = tap < K * K ? (slot * B::ROWS + tap / K) * B::COLS + tap % K - B::PAD + B::COFF : -1;
+            }
+
+        auto item_pos = [&](int it, int &n, int &oy0, int &ox0) __attribute__((always_inline)) {
+            const int cb = it % cblk, rest = it / cblk;
+            ox0 = cb * OCW;
+            oy0 = (rest % rblk) * OR;
+            n   = rest / rblk;
+        };
+        auto issue_band = [&](int it, int buf) __attribute__((always_inline)) {
+            int n, oy0, ox0;
+            item_pos(it, n, oy0, ox0);
+            const int iy0 = oy0 * S - B::PAD, ix0 = ox0 * S - B::COFF;
+            unsigned char *dst = sm + buf * BAND;
+#pragma unroll
+            for (int r = 0; r < NBW; ++r) {
+                const int i   = r * 4 + wave;
+                const int p   = i * 64 + lane;
+                const int pc  = p % B::PPR, rs = p / B::PPR;
+                const int row = rs % B::ROWS, slot = rs / B::ROWS;
+                const int iy  = iy0 + row, ix = ix0 + 2 * pc;
+                const bool ok = p < TP && slot < a.Cinb && iy >= 0 && iy < H && ix >= 0 && ix < W;
+                const unsigned off = ok ? (unsigned) ((((n * a.x_pstride + slot) * H + iy) * W + ix) * 8) : kInvalid;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void *) (dst + i * 1024), 16, off, 0, 0, 0);
+            }
+        };
+
+        auto finish = [&](int it, int buf, auto act_c) __attribute__((always_inline)) {
+            constexpr int ACT = decltype(act_c)::value;
+            int n, oy0, ox0;
+            item_pos(it, n, oy0, ox0);
+            const unsigned char *band = sm + buf * BAND;
+            const int oy  = oy0 + wave;
+            const int g   = lane >> 4;
+#pragma unroll
+            for (int t = 0; t < OCW / 16; ++t) {
+                const int ox   = ox0 + t * 16 + (lane & 15);
+                const int base = wave * S * B::COLS + (t * 16 + (lane & 15)) * S;
+                float4v   acc[MT];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) acc[m] = float4v {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < NSTEPS; ++j) {
+                    u32x2 v[2];
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        v[q] = boff[j][q] >= 0 ? *reinterpret_cast<const u32x2 *>(band + (base + boff[j][q]) * 8) : u32x2 {0u, 0u};
+                    }
+                    const half8 bf = __builtin_bit_cast(half8, u32x4_make(v[0].x, v[0].y, v[1].x, v[1].y));
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[m][j], bf, acc[m], 0, 0, 0);
+                }
+                const bool pok = oy < OH && ox < OW;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const int ocb = m * 4 + g;
+                    const int oc  = ocb * 4;
+                    float4v   v   = acc[m] + *reinterpret_cast<const float4v *>(a.bias + oc);
+                    v.x = apply_act(v.x, ACT, a.lo, a.hi);
+                    v.y = apply_act(v.y, ACT, a.lo, a.hi);
+                    v.z = apply_act(v.z, ACT, a.lo, a.hi);
+                    v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                    if (oc + 0 >= a.Cout) v.x = 0.f;
+                    if (oc + 1 >= a.Cout) v.y = 0.f;
+                    if (oc + 2 >= a.Cout) v.z = 0.f;
+                    if (oc + 3 >= a.Cout) v.w = 0.f;
+                    const unsigned off = pok && ocb < a.Coutb ? (unsigned) ((((n * a.y_pstride + ocb) * OH + oy) * OW + ox) * 8) : kInvalid;
+                    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, off, 0, 0);
+                }
+            }
+        };
+        auto compute_store = [&](int it, int buf) __attribute__((always_inline)) {
+            using std::integral_constant;
+            switch (a.act) {
+                case VKHIP_ACT_RELU: finish(it, buf, integral_constant<int, VKHIP_ACT_RELU> {}); break;
+                case VKHIP_ACT_RELU6: finish(it, buf, integral_constant<int, VKHIP_ACT_RELU6> {}); break;
+                case VKHIP_ACT_CLIP: finish(it, buf, integral_constant<int, VKHIP_ACT_CLIP> {}); break;
+                case VKHIP_ACT_HARDSWISH: finish(it, buf, integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
+                case VKHIP_ACT_SILU: finish(it, buf, integral_constant<int, VKHIP_ACT_SILU> {}); break;
+                default: finish(it, buf, integral_constant<int, VKHIP_ACT_NONE> {}); break;
+            }
+        };
+
+        // stores per wave per item: every (pixel tile, fragment) store is issued, out-of-range ones
+        // with an offset the buffer drops, so the count is fixed
+        constexpr int kStores = (OCW / 16) * MT;
+        static_assert(kStores <= 63, "stores fit the counter");
+        int it = blockIdx.x, buf = 0;
+        if (it < items) issue_band(it, 0);
+        for (bool first = true; it < items; it += gridDim.x, first = false) {
+            // this item's band was issued before the previous item's stores: wait until at most those
+            // stores remain outstanding (the counter retires in issue order)
+            if (first) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+            else __builtin_amdgcn_s_waitcnt((kStores & 15) | (7 << 4) | (15 << 8) | ((kStores >> 4) << 14));
+            __asm__ volatile("s_barrier" ::: "memory"); // all copies of the band landed; the other buffer is free
+            const int nxt = it + gridDim.x;
+            if (nxt < items) issue_band(nxt, buf ^ 1);
+            compute_store(it, buf);
+            buf ^= 1;
+        }
+    }
+
+    template <int CB, int MT_>
+    static GemmKernelFn thin_pick_ks(int k, int s) {
+        if constexpr (MT_ * ((9 * CB * 4 + 31) / 32) <= 20) {
+            if (k == 3 && s == 1) return conv_thin_kernel<CB, MT_, 3, 1>;
+            if (k == 3 && s == 2) return conv_thin_kernel<CB, MT_, 3, 2>;
+        }
+        if (k == 1 && s == 1) return conv_thin_kernel<CB, MT_, 1, 1>;
+        return nullptr;
+    }
+    template <int CB>
+    static GemmKernelFn thin_pick_mt(int mt, int k, int s) {
+        if (mt == 1) return thin_pick_ks<CB, 1>(k, s);
+        if (mt == 2) return thin_pick_ks<CB, 2>(k, s);
+        if (mt == 4) return thin_pick_ks<CB, 4>(k, s);
+        return nullptr;
+    }
+    // kernel for a thin plan: cinb input slots (rounded up to 1, 2, 4 or 8), mt 16-channel output
+    // fragments (1, 2 or 4)
+    GemmKernelFn thin_kernel_for(int cinb, int mt, int k, int s) {
+        switch (thin_cinb(cinb)) {
+            case 1: return thin_pick_mt<1>(mt, k, s);
+            case 2: return thin_pick_mt<2>(mt, k, s);
+            case 4: return thin_pick_mt<4>(mt, k, s);
+            case 8: return thin_pick_mt<8>(mt, k, s);
+        }
+        return nullptr;
+    }
+
+} // namespace vkhip
