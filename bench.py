@@ -59,6 +59,7 @@ def time_steps(sess, steps, warmup):
 
 
 def profile_ops(model, batch, x_dev, options="", reps=3, launches=5):
+    # (options carry the plan file, so the profiled session runs the timed session's plans)
     """Per-op device times: HIP events on the segment stream around `launches` back-to-back
     launches of each op (their average; one launch per event pair would add the event overhead,
     several microseconds, to every short kernel)."""
@@ -94,22 +95,84 @@ def plan_info(plan):
     return out
 
 
-def profiled_layer_traffic(model, batch, family):
-    """Mean measured HBM bytes per launch of one kernel family, from the committed per-layer
-    rocprofv3 summary of this workload (profiles/<model>_b<batch>_layers.md), or None."""
-    path = os.path.join(ROOT, "profiles", f"{model}_b{batch}_layers.md")
+PLANS = os.path.join(ROOT, "profiles", "bench_plans.vkc")
+
+
+def layer_rows(stem):
+    """Rows of a committed per-layer rocprofv3 summary (profiles/<stem>_layers.md, written by
+    `python -m vknn_amd.prof_summary layers`): op, kind, plan, kernels, us, GFLOP, alg. MB, HBM MB."""
+    path = os.path.join(ROOT, "profiles", f"{stem}_layers.md")
     if not os.path.exists(path):
-        return None
-    kernel, tile = family.split(" tile=") if " tile=" in family else (family, None)
-    vals = []
+        return []
+    rows = []
     for ln in open(path):
         c = [x.strip() for x in ln.split("|")]
         if len(c) < 16 or not c[1].isdigit():
             continue
-        plan, kern = c[4], c[5]
-        if kernel in kern and (tile is None or f"tile={tile} " in plan + " "):
-            vals.append(float(c[13]) * 1e6)
-    return round(sum(vals) / len(vals)) if vals else None
+        try:
+            rows.append({"op": c[2], "kind": c[3], "plan": c[4], "kernels": c[5], "us": float(c[6]), "gflop": float(c[7]),
+                         "alg_mb": float(c[8]), "hbm_mb": float(c[13])})
+        except ValueError:
+            continue
+    return rows
+
+
+def profiled_traffic(stem, names):
+    """Measured HBM bytes per launch (FETCH_SIZE x2 + WRITE_SIZE x1) over the same operators as
+    `names`, from the committed per-layer summary of this workload; None when it does not list
+    every one of them (then it was taken on another plan)."""
+    rows = {r["op"]: r for r in layer_rows(stem)}
+    if not names or any(n not in rows for n in names):
+        return None
+    hbm = sum(rows[n]["hbm_mb"] for n in names) * 1e6
+    alg = sum(rows[n]["alg_mb"] for n in names) * 1e6
+    us = sum(rows[n]["us"] for n in names)
+    return {"traffic": round(hbm / len(names)), "profile_algorithmic_bytes_per_launch": round(alg / len(names)),
+            "profile_launch_us": round(us / len(names), 3), "traffic_over_algorithmic": round(hbm / max(alg, 1), 3)}
+
+
+def profiled_kind(stem, kind):
+    """In-graph figures of one operator kind from the committed per-layer summary: the kernels'
+    device time inside the profiled forward passes (no repeated launches), their algorithmic and
+    measured HBM bytes."""
+    rows = [r for r in layer_rows(stem) if r["kind"] == kind and r["us"] > 0]
+    if not rows:
+        return None
+    us = sum(r["us"] for r in rows)
+    alg = sum(r["alg_mb"] for r in rows) * 1e6
+    hbm = sum(r["hbm_mb"] for r in rows) * 1e6
+    return {"source": f"profiles/{stem}_layers.md", "ops": len(rows), "device_us_per_step": round(us, 2),
+            "achieved_GBs": round(alg / us / 1e3, 1), "frac": round(alg / us / 1e3 / PEAK_HBM_GBS, 4),
+            "hbm_over_algorithmic": round(hbm / max(alg, 1), 3)}
+
+
+PROFILED = [("conv3x3_bn_relu_b1", "config 0"), ("mnv2_block_b32", "config 1"), ("mnv2_block_b128", "config 1, fuse_dwpw=1"),
+            ("resnet50_b1", "config 2"), ("resnet50_b64", "config 2"), ("mobilenetv3_large_b128", "config 3"), ("yolov8n_b16", "config 4")]
+
+
+def profiled_roofline(stem):
+    """Every operator of one profiled forward pass against its own roofline, from the committed
+    per-layer summary: attainable time = sum over operators of max(FLOPs / MFMA peak, algorithmic
+    bytes / HBM peak) over the measured kernel time, plus the MFMA- and HBM-bound operators' own
+    fractions."""
+    rows = [r for r in layer_rows(stem) if r["us"] > 0]
+    if not rows:
+        return None
+    us = sum(r["us"] for r in rows)
+    att = sum(max(r["gflop"] * 1e3 / PEAK_FP16_TFLOPS, r["alg_mb"] / PEAK_HBM_GBS * 1e3) for r in rows)
+    mf = [r for r in rows if r["alg_mb"] > 0 and r["gflop"] * 1e3 / r["alg_mb"] > RIDGE]
+    hb = [r for r in rows if r not in mf]
+    out = {"source": f"profiles/{stem}_layers.md", "kernel_us_per_step": round(us, 1), "attainable_us": round(att, 1),
+           "frac": round(att / us, 4)}
+    if mf:
+        mu = sum(r["us"] for r in mf)
+        out["mfma_bound_ops"] = {"n": len(mf), "TFLOPs": round(sum(r["gflop"] for r in mf) / mu * 1e3, 1),
+                                 "frac": round(sum(r["gflop"] for r in mf) / mu * 1e3 / PEAK_FP16_TFLOPS, 4)}
+    if hb:
+        hu = sum(r["us"] for r in hb)
+        out["hbm_bound_ops"] = {"n": len(hb), "GBs": round(sum(r["alg_mb"] for r in hb) / hu * 1e3, 1),
+                                "frac": round(sum(r["alg_mb"] for r in hb) / hu * 1e3 / PEAK_HBM_GBS, 4)}
+    return out
 
 
 CPU_CONFIGS = [("conv3x3_bn_relu", "config 0"), ("mnv2_block", "config 1"), ("resnet50", "config 2"),
@@ -239,10 +302,19 @@ def main():
     ap.add_argument("--dw-batch", type=int, default=128, help="batch of the MobileNetV3-Large depthwise measurement (0 = skip)")
     ap.add_argument("--plan-out", default="", help="write the timed session's plan (one line per op with its flops and "
                                                    "bytes) to this file, for vknn_amd.prof_summary layers")
+    ap.add_argument("--plans", default=PLANS if os.path.exists(PLANS) else "",
+                    help="tune-table file every session of this run reads its plans from (and writes new ones to): the "
+                         "committed profiles/bench_plans.vkc by default, so the bench line and the committed rocprofv3 "
+                         "summaries run the same plans; 'none' tunes every session afresh")
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="MELEMS",
                     help="only run the flat fp32->fp16 convert over MELEMS million elements 5 times (known HBM "
                          "traffic: 6 bytes per element), to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    plan_opts = f"cache_mode=tune;cache_file={args.plans}" if args.plans and args.plans != "none" else ""
+
+    def opts(*extra):
+        return ";".join(o for o in (args.options, plan_opts) + extra if o)
+
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (--gpus {args.gpus} refused). "
               "The conv path shards by batch with no exchange; run one process per GPU.", file=sys.stderr)
@@ -263,7 +335,7 @@ def main():
 
     # ---- batch-B throughput (the headline)
     t = time.perf_counter()
-    sess = V.Session(args.model, args.batch, seed=7, options=args.options)
+    sess = V.Session(args.model, args.batch, seed=7, options=opts())
     log(f"session create (plan + autotune) {time.perf_counter() - t:.1f}s")
     x = np.random.default_rng(0).standard_normal(sess.in_shape).astype(np.float32)
     x_dev = V.DeviceBuffer.from_array(x)
@@ -279,7 +351,7 @@ def main():
     # ---- batch-1 latency (skipped with --b1-steps 0, e.g. under a profiler)
     b1_ms = None
     if args.b1_steps > 0:
-        s1 = V.Session(args.model, 1, seed=7, options=args.options)
+        s1 = V.Session(args.model, 1, seed=7, options=opts())
         x1 = V.DeviceBuffer.from_array(x[:1])
         s1.bind_device_input(x1.ptr)
         wall1, _ = time_steps(s1, args.b1_steps, 10)
@@ -291,7 +363,7 @@ def main():
     extra = {}
     roof = None
     if not args.no_profile:
-        ops, plan = profile_ops(args.model, args.batch, x_dev, args.options)
+        ops, plan = profile_ops(args.model, args.batch, x_dev, opts())
         # Per-op times come from back-to-back replays of each op (warmer caches, no gaps); scale
         # them so they add up to the measured graph step, i.e. every op's share of the real pass.
         scale = ms_step / sum(o["gpu_ms"] for o in ops)
@@ -323,10 +395,13 @@ def main():
             ach, peak, unit = d["bytes"] / d["n"] / launch_s / 1e9, PEAK_HBM_GBS, "GB/s"
         else:
             ach, peak, unit = d["flops"] / d["n"] / launch_s / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s"
+        tr = profiled_traffic(f"{args.model}_b{args.batch}", d["names"])
         roof = {"bound": "hbm" if hbm else "mfma", "achieved": round(ach, 2), "peak": peak, "unit": unit,
                 "frac": round(ach / peak, 4),
-                "traffic": profiled_layer_traffic(args.model, args.batch, dom),
-                "traffic_unit": "HBM bytes per launch (FETCH_SIZE x2 + WRITE_SIZE x1, profiles/<model>_b<batch>_layers.md), null if not profiled",
+                "traffic": tr["traffic"] if tr else None,
+                "traffic_unit": "HBM bytes per launch (FETCH_SIZE x2 + WRITE_SIZE x1) over the same operators, from "
+                                "profiles/<model>_b<batch>_layers.md (taken on the same plan file); null if that summary lacks any of them",
+                "traffic_detail": tr,
                 "kernel": f"{dom}: {d['n']} launches per step ({', '.join(d['names'])})",
                 "launch_us": round(launch_s * 1e6, 3),
                 "algorithmic_bytes_per_launch": round(d["bytes"] / d["n"]), "flops_per_launch": round(d["flops"] / d["n"]),
@@ -358,8 +433,8 @@ def main():
     if not args.no_profile and args.dw_batch > 0:
         xs, _ = V.model_io("mobilenetv3_large", args.dw_batch)
         xd = V.DeviceBuffer.from_array(np.random.default_rng(1).standard_normal(xs).astype(np.float32))
-        dops, dplan = profile_ops("mobilenetv3_large", args.dw_batch, xd, "")
-        ds = V.Session("mobilenetv3_large", args.dw_batch, seed=7)
+        dops, dplan = profile_ops("mobilenetv3_large", args.dw_batch, xd, plan_opts)
+        ds = V.Session("mobilenetv3_large", args.dw_batch, seed=7, options=plan_opts)
         ds.bind_device_input(xd.ptr)
         dwall, _ = time_steps(ds, 10, 3)
         ds.close()
@@ -381,15 +456,16 @@ def main():
                                   "frac": round(b_bytes / (b_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                                   "launch_ms": round(b_ms, 4), "bytes_per_step": b_bytes,
                                   "replay_to_step_scale": round(dscale, 4),
-                                  "frac_of_step_time": round(b_bytes / (b_ms * dscale * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+                                  "frac_of_step_time": round(b_bytes / (b_ms * dscale * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                                  "in_graph": profiled_kind(f"mobilenetv3_large_b{args.dw_batch}", "dwconv")}
         xd.close()
 
     # ---- fused dw+pw (config 1: the MobileNetV2 block with the dw+pw fusion pass) at batch 128
     if not args.no_profile and args.dw_batch > 0:
         xs, _ = V.model_io("mnv2_block", args.dw_batch)
         xd = V.DeviceBuffer.from_array(np.random.default_rng(2).standard_normal(xs).astype(np.float32))
-        fops, fplan = profile_ops("mnv2_block", args.dw_batch, xd, "fuse_dwpw=1")
-        fs = V.Session("mnv2_block", args.dw_batch, seed=7, options="fuse_dwpw=1")
+        fops, fplan = profile_ops("mnv2_block", args.dw_batch, xd, ";".join(o for o in ("fuse_dwpw=1", plan_opts) if o))
+        fs = V.Session("mnv2_block", args.dw_batch, seed=7, options=";".join(o for o in ("fuse_dwpw=1", plan_opts) if o))
         fs.bind_device_input(xd.ptr)
         fwall, _ = time_steps(fs, 10, 3)
         fs.close()
@@ -403,7 +479,8 @@ def main():
                                    "frac": round(f_bytes / (f_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                                    "launch_ms": round(f_ms, 4), "bytes_per_step": f_bytes, "replay_to_step_scale": round(fscale, 4),
                                    "frac_of_step_time": round(f_bytes / (f_ms * fscale * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                                   "execution": [ln for ln in fplan.splitlines() if "[dwpw]" in ln]}
+                                   "execution": [ln for ln in fplan.splitlines() if "[dwpw]" in ln],
+                                   "in_graph": profiled_kind(f"mnv2_block_b{args.dw_batch}", "dwpw")}
         xd.close()
 
     # ---- Winograd transforms (the tuner rarely picks Winograd on these shapes; forced here)
@@ -414,23 +491,26 @@ def main():
     # default session options; the headline config is the line's value)
     if not args.no_configs:
         per = {}
-        for name, batches, opts in (("conv3x3_bn_relu", (1,), ""), ("mnv2_block", (1, 32), ""), ("mnv2_block", (32,), "fuse_dwpw=1"),
+        for name, batches, copts in (("conv3x3_bn_relu", (1,), ""), ("mnv2_block", (1, 32), ""), ("mnv2_block", (32,), "fuse_dwpw=1"),
                                      ("mobilenetv3_large", (1, 128), ""), ("mobilenetv3_large", (128,), "fuse_se=1"),
                                      ("yolov8n", (1, 16), "")):
             fl = V.vknn().vknn_model_flops(name.encode())
             for b in batches:
-                cs = V.Session(name, b, seed=7, options=opts)
+                cs = V.Session(name, b, seed=7, options=";".join(o for o in (copts, plan_opts) if o))
                 cx = V.DeviceBuffer.from_array(np.random.default_rng(3).standard_normal(cs.in_shape).astype(np.float32))
                 cs.bind_device_input(cx.ptr)
                 n = 50 if b == 1 else 20
                 cw, _ = time_steps(cs, n, 5)
                 cs.close()
                 cx.close()
-                key = name + (f" ({opts})" if opts else "")
+                key = name + (f" ({copts})" if copts else "")
                 per.setdefault(key, {})[f"b{b}"] = {"ms_per_step": round(cw / n * 1e3, 4), "img_per_s": round(b * n / cw, 1),
                                                       "tflops": round(fl * b * n / cw / 1e12, 2)}
                 log(f"{key} b{b}: {cw / n * 1e3:.3f} ms/step")
         extra["per_config"] = per
+
+    pr = {f"{stem} ({label})": profiled_roofline(stem) for stem, label in PROFILED}
+    extra["profiled_rooflines"] = {k: v for k, v in pr.items() if v}
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.model)
 
@@ -450,6 +530,7 @@ def main():
         "config": {"workload": f"{args.model} v1.5 forward, config 2" if args.model == "resnet50" else args.model,
                    "batch": args.batch, "input": "x".join(map(str, sess.in_shape[1:])),
                    "layout": "NC4HW4 fp16", "options": args.options or "default",
+                   "plans": os.path.relpath(args.plans, ROOT) if plan_opts else "tuned in this run",
                    "tflops_per_step": round(flops_img * args.batch / 1e12, 4)},
         "b1_ms_per_img": round(b1_ms, 4) if b1_ms else None,
         "b1_img_per_s": round(1000.0 / b1_ms, 1) if b1_ms else None,

@@ -30,7 +30,7 @@ import csv
 import re
 from collections import OrderedDict
 
-CONV_PREFIX = ("conv_gemm", "conv_bd", "conv_dma", "conv_halo", "conv_stem", "splitk_reduce", "wino_", "dwconv", "dwpw", "fc_kernel")
+CONV_PREFIX = ("conv_gemm", "conv_bd", "conv_dma", "conv_halo", "conv_stem", "conv_thin", "splitk_reduce", "wino_", "dwconv", "dwpw", "fc_kernel")
 
 
 def family(name):
@@ -63,6 +63,22 @@ def timed_rows(rows, steps):
 
 
 MARKER = "dispatch_marker_kernel"  # the empty per-operator separators of VKNN_HIP_OP_MARKERS=1
+
+
+def busy_and_gaps(timed):
+    """Device time covered by at least one kernel (overlapping dispatches of two streams counted
+    once) and the idle gaps between consecutive covered intervals, in ns."""
+    iv = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in timed)
+    busy, gaps, cur_s, cur_e = 0, [], iv[0][0], iv[0][1]
+    for s0, e0 in iv[1:]:
+        if s0 > cur_e:
+            busy += cur_e - cur_s
+            gaps.append(s0 - cur_e)
+            cur_s, cur_e = s0, e0
+        else:
+            cur_e = max(cur_e, e0)
+    busy += cur_e - cur_s
+    return busy, gaps
 
 
 def summarise(path, steps):
@@ -119,12 +135,13 @@ def cmd_stalls(a):
             f.setdefault("#us", {})[path] = f.get("#us", {}).get(path, 0.0) + dus
             if "SQ_VALU_MFMA_BUSY_CYCLES" in names:
                 f["#mf_us"] = f.get("#mf_us", 0.0) + dus
-        cols += [n for n in names if n != "SQ_WAVE_CYCLES" and not n.startswith("GRBM_") and n not in cols]
+        cols += [n for n in names if n not in ("SQ_WAVE_CYCLES", "SQ_WAVES") and not n.startswith("GRBM_") and n not in cols]
     print(f"# {a.title}\n")
     if a.command:
         print(f"Command: `{a.command}`\n")
     print("Shares of SQ_WAVE_CYCLES (resident-wave time) per kernel family over the timed steps; "
-          f"mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (dispatch time x {a.clock_ghz} GHz x 4 x {a.cus} CUs).\n")
+          f"mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (dispatch time x {a.clock_ghz} GHz x 4 x {a.cus} CUs); "
+          "insts_valu = SQ_INSTS_VALU per wave (SQ_WAVES of the same pass).\n")
     hdr = [c.replace("SQ_", "").lower() for c in cols if c != "SQ_VALU_MFMA_BUSY_CYCLES"]
     mf = "SQ_VALU_MFMA_BUSY_CYCLES" in cols
     print("| kernel | us/step | " + " | ".join(hdr) + (" | mfma_busy |" if mf else " |"))
@@ -139,6 +156,10 @@ def cmd_stalls(a):
             if c == "SQ_VALU_MFMA_BUSY_CYCLES":
                 continue
             wc = f.get("SQ_WAVE_CYCLES", [0.0, 0])[0]
+            if c == "SQ_INSTS_VALU":
+                nw = f.get("SQ_WAVES", [0.0, 0])[0]
+                cells.append(f"{f[c][0] / nw:.0f}" if c in f and nw > 0 else "-")
+                continue
             cells.append(f"{f[c][0] / wc:.3f}" if c in f and wc > 0 else "-")
         if mf:
             p = f.get("#mf_us")
@@ -155,6 +176,13 @@ def cmd_trace(a):
     if a.command:
         print(f"Command: `{a.command}`\n")
     print(f"Timed steps: {a.steps}; dispatches in them: {n}; first-to-last dispatch span {span_ns / a.steps / 1e3:.1f} us/step\n")
+    timed = [r for r in timed_rows(list(csv.DictReader(open(a.trace))), a.steps) if not family(r["Kernel_Name"]).startswith(MARKER)]
+    busy, gaps = busy_and_gaps(timed)
+    if gaps:
+        gs = sorted(gaps)
+        print(f"Device busy (at least one kernel running) {busy / a.steps / 1e3:.1f} us/step = {100 * busy / span_ns:.1f}% of the span; "
+              f"{len(gaps) / a.steps:.1f} idle gaps per step between dispatches, {sum(gaps) / a.steps / 1e3:.1f} us/step in total, "
+              f"median {gs[len(gs) // 2] / 1e3:.2f} us, 90th percentile {gs[int(len(gs) * 0.9)] / 1e3:.2f} us\n")
     print("| kernel | dispatches/step | mean us | us/step | share |")
     print("|---|---:|---:|---:|---:|")
     for k, (c, d) in sorted(fam.items(), key=lambda kv: -kv[1][1]):
