@@ -708,6 +708,36 @@ def test_depthwise_tiled_shapes(gpu, shape, k, s, act, res, rt):
     assert_parity(got, ref, f"dw {shape} k{k} s{s} rows/strip {rt}")
 
 
+@pytest.mark.parametrize("shape,k,s,act,res,rt", [((128, 960, 7, 7), 5, 1, 4, False, 907), ((128, 480, 14, 14), 3, 1, 1, True, 914),
+                                                  ((32, 88, 8, 8), 3, 2, 2, False, 904), ((9, 22, 7, 7), 3, 1, 5, True, 907),
+                                                  ((128, 200, 14, 14), 5, 1, 4, False, 914)])
+def test_depthwise_persistent_groups(gpu, shape, k, s, act, res, rt):
+    """Persistent plane groups (tile 9xx): more groups than resident workgroups (each walks
+    several, its channel blocks fixed by the grid size), the tile halo kept across groups, a last
+    group with fewer planes, ragged channels, residual."""
+    N, C, H, W = shape
+    r = rng(310 + k + s + C)
+    x = round_half(r.standard_normal(shape))
+    w = (r.standard_normal((C, 1, k, k)) * 0.3).astype(np.float32)
+    b = (r.standard_normal(C) * 0.1).astype(np.float32)
+    p = k // 2
+    OH, OW = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    rr = round_half(r.standard_normal((N, C, OH, OW))) if res else None
+    got, plan, _ = gpu_conv(x, w, b, (s, s), (p, p, p, p), group=C, act=act, res=rr, algo=V.CONV_DEPTHWISE, tile=rt)
+    assert plan.tile == rt
+    ref = oracle_conv(x, w, b, (s, s), (p, p, p, p), group=C, res=rr, act=act)
+    assert_parity(got, ref, f"dw persistent {shape} k{k} s{s} tile {rt}")
+
+
+def test_depthwise_persistent_refuses_large_groups(gpu):
+    """Tile 9xx needs one strip per plane and at most 4096 input pixels per plane group."""
+    lib = V.vkhip()
+    plan = V.ConvPlan()
+    for xs, k, s, rt in [((2, 64, 28, 28), 3, 1, 907), ((2, 64, 14, 14), 3, 1, 907), ((2, 64, 56, 56), 3, 1, 914)]:
+        d, _ = conv_desc(xs, (xs[1], 1, k, k), (s, s), (k // 2,) * 4, group=xs[1])
+        assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_DEPTHWISE, rt, 0, ctypes.byref(plan)) != 0, (xs, k, s, rt)
+
+
 def test_depthwise_dilated_generic(gpu):
     r = rng(55)
     x = round_half(r.standard_normal((1, 12, 16, 16)))
@@ -1057,7 +1087,8 @@ def test_se_pooled(gpu, N, C, Cr, R, HW):
 # ---------------------------------------------------------------- depthwise + squeeze-excite pool sums
 @pytest.mark.parametrize("shape,k,s,rt", [((3, 72, 28, 28), 3, 2, 7), ((2, 120, 28, 28), 5, 1, 4), ((4, 960, 7, 7), 5, 1, 7),
                                           ((2, 22, 14, 14), 3, 1, 14), ((5, 40, 56, 56), 5, 2, 4),
-                                          ((3, 120, 28, 28), 5, 1, 207), ((4, 72, 56, 56), 3, 1, 404)])
+                                          ((3, 120, 28, 28), 5, 1, 207), ((4, 72, 56, 56), 3, 1, 404), ((128, 960, 7, 7), 5, 1, 907),
+                                          ((96, 120, 14, 14), 3, 1, 914)])
 def test_depthwise_pool_sums(gpu, shape, k, s, rt):
     """vkhip_conv_forward_pooled writes exactly the depthwise output of vkhip_conv_forward and the
     per-(plane, row tile) sums of it; a squeeze-excite fed from those sums (vkhip_fused_se_pooled)

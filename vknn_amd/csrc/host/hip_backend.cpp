@@ -237,7 +237,8 @@ namespace vknn {
                 for (int t = 0; t < ntiles; ++t)
                     if (!skipTiles.count(t)) cands.push_back({VKHIP_CONV_GEMM, t, 0});
                 if (dw) // the depthwise kernel's rows per strip
-                    for (int rt: {4, 7, 14, 204, 207, 404, 407}) // + 100 x strips per workgroup (VKNN_HIP_DW_PIPE=0: one strip only)
+                    // + 100 x strips per workgroup, 900: persistent plane groups (VKNN_HIP_DW_PIPE=0: one strip only)
+                    for (int rt: {4, 7, 14, 204, 207, 404, 407, 907, 914})
                         if (rt < 100 || !(std::getenv("VKNN_HIP_DW_PIPE") && std::getenv("VKNN_HIP_DW_PIPE")[0] == '0'))
                             cands.push_back({VKHIP_CONV_DEPTHWISE, rt, 0});
                 vkhip_conv_plan base;

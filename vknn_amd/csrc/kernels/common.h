@@ -7,7 +7,22 @@
 
 namespace vkhip {
 
+    // Cache policy (buffer instruction aux bits) of the streaming accesses of the conv epilogues:
+    // the residual, read once, and the output, written once per layer. NT (non-temporal, bit 1) on
+    // the residual load keeps it from evicting the operand tiles that the other workgroups of the
+    // launch re-read from L2. The output stays cached: the next layer reads it, and with NT stores
+    // it would miss the last-level cache (measured: NT on both costs ResNet-50 b64 4%).
+#ifndef VKHIP_STREAM_LOAD
+#define VKHIP_STREAM_LOAD 2
+#endif
+#ifndef VKHIP_STREAM_STORE
+#define VKHIP_STREAM_STORE 0
+#endif
+    constexpr int kStreamLoad  = VKHIP_STREAM_LOAD;
+    constexpr int kStreamStore = VKHIP_STREAM_STORE;
+
     typedef _Float16 half_t;
+    typedef _Float16 half2v __attribute__((ext_vector_type(2)));
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
     typedef _Float16 half8 __attribute__((ext_vector_type(8)));
     typedef float    float4v __attribute__((ext_vector_type(4)));

@@ -17,6 +17,7 @@
 // (shaders/conv1x1_reduce_fp16.comp) for partial sums + bias + residual + activation.
 #include "conv_kernels.h"
 #include <mutex>
+#include <numeric>
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -261,17 +262,23 @@ namespace vkhip {
         unsigned mHW, mW;     // ceil(2^32 / (H*W)), ceil(2^32 / W): n / d = umulhi(n, m) for n * d < 2^32 (0: divide)
     };
 
-    template <int KH, int KW, int S, int RT, bool PIPE>
+    // MODE 0: one strip per workgroup. MODE 1: RPW consecutive strips of the same planes per
+    // workgroup, the next strip's input prefetched into registers. MODE 2 (one strip covers the
+    // plane): a persistent workgroup walks plane groups pg, pg + gridDim.x, ...; the next group's
+    // input (one contiguous range) is loaded into registers while the current group computes, and
+    // the host sizes the grid so that gridDim.x * PP is a multiple of Cb: every thread keeps the
+    // same channel block, so its weights are loaded once.
+    template <int KH, int KW, int S, int RT, int MODE>
     __global__ __launch_bounds__(256) void dwconv_lds_kernel(DwArgs a, DwTile t) {
         extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
         constexpr int IR = (RT - 1) * S + KH; // input rows of one strip
         uint2 *tile = reinterpret_cast<uint2 *>(dsm); // [PP][PS: IR x IWp + padding]
         const int tid = threadIdx.x;
-        const int rtg = blockIdx.x % t.rt_groups;
-        const int pg  = blockIdx.x / t.rt_groups;
+        const int rtg = MODE == 2 ? 0 : blockIdx.x % t.rt_groups;
+        int       pg  = MODE == 2 ? blockIdx.x : blockIdx.x / t.rt_groups;
         const int NCb = a.N * a.Cb;
-        const int p0  = pg * t.PP;
-        const int np  = min(t.PP, NCb - p0);
+        int       p0  = pg * t.PP;
+        int       np  = min(t.PP, NCb - p0);
         const int IWp = t.IWp, PLA = t.PLA;
 
         // The thread's output column and plane; its weights and bias are loaded first so their
@@ -279,14 +286,26 @@ namespace vkhip {
         const int OW = a.OW;
         const int ox = tid % OW;
         const int pl = tid / OW;
-        const int p  = p0 + min(pl, np - 1);
-        const int cb = p % a.Cb;
+        int       p  = p0 + min(pl, np - 1);
+        const int cb = MODE == 2 ? (p0 + min(pl, t.PP - 1)) % a.Cb : p % a.Cb;
         // weights stored and held as fp16 (the storage precision of every GPU weight on this path):
         // half the registers of fp32, and v_fma_mix takes fp16 x fp16 products into the fp32 sums
         half4 w[KH * KW];
 #pragma unroll
         for (int k = 0; k < KH * KW; ++k) w[k] = a.w[(long long) cb * KH * KW + k];
         const float4v b0 = *reinterpret_cast<const float4v *>(a.bias + cb * 4);
+        // the same weights as channel-wise column pairs for v_dot2_f32_f16 (see strip)
+        half2v wp2[KH][KW / 2 > 0 ? KW / 2 : 1][4];
+#pragma unroll
+        for (int ky = 0; ky < KH; ++ky)
+#pragma unroll
+            for (int q = 0; q < KW / 2; ++q) {
+                const half4 w0 = w[ky * KW + 2 * q], w1 = w[ky * KW + 2 * q + 1];
+                wp2[ky][q][0] = half2v {w0.x, w1.x};
+                wp2[ky][q][1] = half2v {w0.y, w1.y};
+                wp2[ky][q][2] = half2v {w0.z, w1.z};
+                wp2[ky][q][3] = half2v {w0.w, w1.w};
+            }
 
         const int W = a.W, H = a.H;
         // input strip of row tile rt -> LDS
@@ -368,27 +387,46 @@ namespace vkhip {
         auto strip = [&](const int rt) __attribute__((always_inline)) {
         const int oy0 = rt * RT;
 
-        const bool live = pl < np;
+        const bool live = pl < np && (MODE != 2 || pl < t.PP);
         float4v acc[RT];
 #pragma unroll
         for (int r = 0; r < RT; ++r) acc[r] = b0;
         const uint2 *src = tile + min(pl, np - 1) * t.PS + ox * S + (PLA - a.PL);
+        // Taps in column pairs (kx, kx+1) go through v_dot2_f32_f16: one instruction adds both
+        // fp16 x fp16 products of one channel into its fp32 sum, half the FMAs of the strip. A
+        // pair's two taps of one channel are packed once per input row and reused by every output
+        // row whose window covers the row; an odd last column stays a mixed-precision FMA.
 #pragma unroll
         for (int ir = 0; ir < IR; ++ir) {
             half4 tap[KW];
 #pragma unroll
             for (int kx = 0; kx < KW; ++kx) tap[kx] = u2_as_h4(src[ir * IWp + kx]);
+            half2v tp[KW / 2][4];
+#pragma unroll
+            for (int q = 0; q < KW / 2; ++q) {
+                tp[q][0] = half2v {tap[2 * q].x, tap[2 * q + 1].x};
+                tp[q][1] = half2v {tap[2 * q].y, tap[2 * q + 1].y};
+                tp[q][2] = half2v {tap[2 * q].z, tap[2 * q + 1].z};
+                tp[q][3] = half2v {tap[2 * q].w, tap[2 * q + 1].w};
+            }
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
                 const int ky = ir - r * S;
                 if (ky < 0 || ky >= KH) continue;
 #pragma unroll
-                for (int kx = 0; kx < KW; ++kx) {
-                    const half4 wv = w[ky * KW + kx];
-                    acc[r].x = __builtin_fmaf((float) tap[kx].x, (float) wv.x, acc[r].x);
-                    acc[r].y = __builtin_fmaf((float) tap[kx].y, (float) wv.y, acc[r].y);
-                    acc[r].z = __builtin_fmaf((float) tap[kx].z, (float) wv.z, acc[r].z);
-                    acc[r].w = __builtin_fmaf((float) tap[kx].w, (float) wv.w, acc[r].w);
+                for (int q = 0; q < KW / 2; ++q) {
+                    acc[r].x = __builtin_amdgcn_fdot2(tp[q][0], wp2[ky][q][0], acc[r].x, false);
+                    acc[r].y = __builtin_amdgcn_fdot2(tp[q][1], wp2[ky][q][1], acc[r].y, false);
+                    acc[r].z = __builtin_amdgcn_fdot2(tp[q][2], wp2[ky][q][2], acc[r].z, false);
+                    acc[r].w = __builtin_amdgcn_fdot2(tp[q][3], wp2[ky][q][3], acc[r].w, false);
+                }
+                if constexpr (KW % 2) {
+                    const half4 wv = w[ky * KW + KW - 1];
+                    const half4 tv = tap[KW - 1];
+                    acc[r].x = __builtin_fmaf((float) tv.x, (float) wv.x, acc[r].x);
+                    acc[r].y = __builtin_fmaf((float) tv.y, (float) wv.y, acc[r].y);
+                    acc[r].z = __builtin_fmaf((float) tv.z, (float) wv.z, acc[r].z);
+                    acc[r].w = __builtin_fmaf((float) tv.w, (float) wv.w, acc[r].w);
                 }
             }
         }
@@ -429,7 +467,8 @@ namespace vkhip {
             // output back: sum of the fp16 values just stored, per plane of this row tile (columns
             // in order, then the host-visible partials per row tile in order: deterministic)
             __syncthreads(); // every wave is done with the input tile
-            float4v *red = reinterpret_cast<float4v *>(dsm);
+            // MODE 2 keeps the tile's zero halo across groups: its reduction area follows the tile
+            float4v *red = reinterpret_cast<float4v *>(dsm + (MODE == 2 ? ((t.PP * t.PS * 8 + 15) & ~15) : 0));
             red[tid] = psum;
             __syncthreads();
             if (tid < np) {
@@ -440,7 +479,44 @@ namespace vkhip {
         }
         };
 
-        if constexpr (PIPE) {
+        if constexpr (MODE == 2) {
+            // persistent plane groups (row_tiles == 1): the halo of the tile is zeroed once and
+            // only the data positions are rewritten per group
+            constexpr int UP  = 16; // pixels per thread of one group's input (host: PP * H * W <= 4096)
+            const int     HW  = H * W;
+            for (int i = tid; i < t.PP * t.PS; i += 256) tile[i] = uint2 {0u, 0u};
+            uint2 v[UP];
+            auto fetch = [&](const int g) __attribute__((always_inline)) {
+                const int    q0   = g * t.PP;
+                const int    tot  = min(t.PP, NCb - q0) * HW;
+                const uint2 *base = a.x + (long long) q0 * HW;
+#pragma unroll
+                for (int u = 0; u < UP; ++u) {
+                    const int e = tid + u * 256;
+                    v[u]        = e < tot ? base[e] : uint2 {0u, 0u};
+                }
+            };
+            if (pg < t.plane_groups) fetch(pg);
+            for (bool first = true; pg < t.plane_groups; pg += gridDim.x, first = false) {
+                p0 = pg * t.PP;
+                np = min(t.PP, NCb - p0);
+                p  = p0 + min(pl, np - 1);
+                __syncthreads(); // the previous group's strip is done with the tile (first: the halo is zero)
+                const int tot = np * HW;
+#pragma unroll
+                for (int u = 0; u < UP; ++u) {
+                    const int e = tid + u * 256;
+                    if (e >= tot) break;
+                    const int pq = t.mHW ? (int) __umulhi((unsigned) e, t.mHW) : e / HW, pix = e - pq * HW;
+                    const int iy = t.mW ? (int) __umulhi((unsigned) pix, t.mW) : pix / W, ix = pix - iy * W;
+                    tile[pq * t.PS + (iy + a.PT) * IWp + ix + PLA] = v[u];
+                }
+                __syncthreads();
+                if (pg + (int) gridDim.x < t.plane_groups) fetch(pg + gridDim.x);
+                strip(0);
+                (void) first;
+            }
+        } else if constexpr (MODE == 1) {
             const int rt_first = rtg * t.RPW;
             const int rt_end   = min(rt_first + t.RPW, t.row_tiles);
             // Several strips per workgroup, software-pipelined: the global loads of strip k + 1 are
@@ -519,6 +595,37 @@ namespace vkhip {
         if (t.RPW > 1 && (d->W % 2 != 0 || t.PP * t.IR > 8 * (256 / (t.IWp / 2)))) t.RPW = 1;
         t.rt_groups = (int) ceil_div(t.row_tiles, t.RPW);
         return true;
+    }
+
+    // Persistent plane groups (depthwise tiles 9xx): one strip covers the plane and one group's
+    // input fits 16 pixels per thread.
+    static bool dw_persist_ok(const vkhip_conv_desc *d, const DwTile &t) {
+        return t.row_tiles == 1 && (int64_t) t.PP * d->H * d->W <= 16 * 256;
+    }
+    // Grid of the persistent depthwise kernel: every workgroup walks groups g, g + G, ... and keeps
+    // its threads' channel blocks only if G * PP is a multiple of Cb, so G is a multiple of
+    // q = Cb / gcd(PP, Cb), as many as the device holds at once (at least q); or one workgroup per
+    // group when that many fit at once anyway.
+    static unsigned dw_persist_grid(const vkhip_conv_desc *d, const DwTile &t, size_t sm) {
+        static std::mutex mu;
+        static int        cus = 0;
+        {
+            std::lock_guard<std::mutex> lock(mu);
+            if (!cus) {
+                int dev = 0;
+                if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+                    cus = 256;
+            }
+        }
+        // resident workgroups of 256 threads: 3 per CU by registers for the 3x3 kernels with up to 7
+        // rows per strip (<= 168 VGPRs), 2 for the others (<= 232), fewer if the LDS holds fewer
+        const int     by_regs = d->KH == 3 && t.IR <= 9 + 6 ? 3 : 2;
+        const int64_t per_cu  = std::max<int64_t>(1, std::min<int64_t>(by_regs, (160 * 1024) / std::max<size_t>(sm, 1)));
+        const int64_t res    = per_cu * cus;
+        if (t.plane_groups <= res) return (unsigned) t.plane_groups;
+        const int64_t Cb = ceil_div(d->Cin, 4);
+        const int64_t q  = Cb / std::gcd((int64_t) t.PP, Cb);
+        return (unsigned) std::max<int64_t>(q, res / q * q);
     }
 
     // ------------------------------------------------------------------ host side: plans
@@ -809,8 +916,16 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
         if (algo != VKHIP_CONV_AUTO && algo != VKHIP_CONV_DEPTHWISE)
             return set_error(VKHIP_ERR_INVALID, "depthwise conv only runs the depthwise algorithm");
         // tile = rows per strip (4, 7 or 14) + 100 x strips per workgroup (2 or 4: pipelined strips)
-        if (tile > 0 && ((tile % 100 != 4 && tile % 100 != 7 && tile % 100 != 14) || (tile / 100 != 0 && tile / 100 != 2 && tile / 100 != 4)))
-            return set_error(VKHIP_ERR_INVALID, "depthwise tile %d: rows per strip 4, 7 or 14, plus 100 x 2 or 4 strips per workgroup (0 or -1: by shape)", tile);
+        if (tile > 0 && ((tile % 100 != 4 && tile % 100 != 7 && tile % 100 != 14) || (tile / 100 != 0 && tile / 100 != 2 && tile / 100 != 4 && tile / 100 != 9)))
+            return set_error(VKHIP_ERR_INVALID, "depthwise tile %d: rows per strip 4, 7 or 14, plus 100 x 2 or 4 strips per workgroup, or 900 "
+                             "(persistent plane groups) (0 or -1: by shape)", tile);
+        if (tile >= 900) {
+            DwTile t;
+            const bool unit = d->DH == 1 && d->DW == 1 && d->SH == d->SW && d->KH == d->KW && (d->KH == 3 || d->KH == 5) && (d->SH == 1 || d->SH == 2);
+            if (!unit || !dw_tile(d, (int64_t) d->N * ceil_div(d->Cin, 4), tile % 100, 1, t) || !dw_persist_ok(d, t))
+                return set_error(VKHIP_ERR_UNSUPPORTED, "depthwise tile %d: persistent plane groups need one strip per plane and at most 4096 "
+                                 "input pixels per group", tile);
+        }
         int64_t Cb         = ceil_div(d->Cin, 4);
         plan->algo         = VKHIP_CONV_DEPTHWISE;
         plan->tile         = tile > 0 ? tile : 0;
@@ -1034,15 +1149,25 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
         const int RT = plan->tile > 0 ? plan->tile % 100 : (d->OH % 7 == 0 ? 7 : 4);
         if (unit && d->KH == d->KW && (d->KH == 3 || d->KH == 5) && (d->SH == 1 || d->SH == 2) &&
             dw_tile(d, (int64_t) d->N * Cb, RT, std::max(1, plan->tile / 100), t)) {
-            const size_t sm = std::max<size_t>((size_t) t.PP * t.PS * 8, pool ? 256 * 16 : 0); // the pool reduction reuses the tile
+            const bool   pers = plan->tile >= 900;
+            const size_t tile_bytes = (size_t) t.PP * t.PS * 8;
+            // the pool reduction reuses the tile, or (persistent groups: the halo must survive) follows it
+            const size_t sm = pers ? ((tile_bytes + 15) & ~(size_t) 15) + (pool ? 256 * 16 : 0) : std::max<size_t>(tile_bytes, pool ? 256 * 16 : 0);
             dim3 g2((unsigned) ((int64_t) t.rt_groups * t.plane_groups));
+            if (pers) {
+                if (!dw_persist_ok(d, t)) return set_error(VKHIP_ERR_INVALID, "conv_forward: depthwise tile %d does not fit this shape", plan->tile);
+                g2 = dim3(dw_persist_grid(d, t, sm));
+            }
 #define VKHIP_DW_LAUNCH(K, S_)                                                                                 \
-    (t.RPW > 1 ? (RT == 14 ? dwconv_lds_kernel<K, K, S_, 14, true><<<g2, 256, sm, st>>>(a, t)                                      \
-                          : RT == 7 ? dwconv_lds_kernel<K, K, S_, 7, true><<<g2, 256, sm, st>>>(a, t)                                \
-                                    : dwconv_lds_kernel<K, K, S_, 4, true><<<g2, 256, sm, st>>>(a, t))                               \
-               : (RT == 14 ? dwconv_lds_kernel<K, K, S_, 14, false><<<g2, 256, sm, st>>>(a, t)                                     \
-                           : RT == 7 ? dwconv_lds_kernel<K, K, S_, 7, false><<<g2, 256, sm, st>>>(a, t)                              \
-                                     : dwconv_lds_kernel<K, K, S_, 4, false><<<g2, 256, sm, st>>>(a, t)))
+    (pers ? (RT == 14 ? dwconv_lds_kernel<K, K, S_, 14, 2><<<g2, 256, sm, st>>>(a, t)                                          \
+                      : RT == 7 ? dwconv_lds_kernel<K, K, S_, 7, 2><<<g2, 256, sm, st>>>(a, t)                                  \
+                                : dwconv_lds_kernel<K, K, S_, 4, 2><<<g2, 256, sm, st>>>(a, t))                                 \
+     : t.RPW > 1 ? (RT == 14 ? dwconv_lds_kernel<K, K, S_, 14, 1><<<g2, 256, sm, st>>>(a, t)                                    \
+                             : RT == 7 ? dwconv_lds_kernel<K, K, S_, 7, 1><<<g2, 256, sm, st>>>(a, t)                           \
+                                       : dwconv_lds_kernel<K, K, S_, 4, 1><<<g2, 256, sm, st>>>(a, t))                          \
+                 : (RT == 14 ? dwconv_lds_kernel<K, K, S_, 14, 0><<<g2, 256, sm, st>>>(a, t)                                    \
+                             : RT == 7 ? dwconv_lds_kernel<K, K, S_, 7, 0><<<g2, 256, sm, st>>>(a, t)                           \
+                                       : dwconv_lds_kernel<K, K, S_, 4, 0><<<g2, 256, sm, st>>>(a, t)))
             if (d->KH == 3 && d->SH == 1) VKHIP_DW_LAUNCH(3, 1);
             else if (d->KH == 3) VKHIP_DW_LAUNCH(3, 2);
             else if (d->SH == 1) VKHIP_DW_LAUNCH(5, 1);

@@ -426,7 +426,7 @@ namespace vkhip {
 #pragma unroll
                     for (int i = 0; i < FM; ++i)
 #pragma unroll
-                        for (int qq = 0; qq < 4; ++qq) rv[j][i][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[j][i][qq], 0, 0);
+                        for (int qq = 0; qq < 4; ++qq) rv[j][i][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[j][i][qq], 0, kStreamLoad);
             } else {
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
@@ -455,7 +455,7 @@ namespace vkhip {
                             if (oc + 1 >= a.Cout) v.y = 0.f;
                             if (oc + 2 >= a.Cout) v.z = 0.f;
                             if (oc + 3 >= a.Cout) v.w = 0.f;
-                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff[j][i][qq], 0, 0);
+                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff[j][i][qq], 0, kStreamStore);
                         }
             };
             switch (epi ? a.act : 0) {
@@ -554,7 +554,7 @@ namespace vkhip {
                             if constexpr (MODE == 0)
                                 yoff[b][jj][i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + pn * a.OHW + pr) * 16) : kInvalid;
                             else yoff[b][jj][i][qq] = ok ? (unsigned) (((pn * a.y_pstride + ocb) * a.OHW + pr) * 8) : kInvalid;
-                            if constexpr (MODE == 3) rv[b][jj][i][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[b][jj][i][qq], 0, 0);
+                            if constexpr (MODE == 3) rv[b][jj][i][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[b][jj][i][qq], 0, kStreamLoad);
                         }
                 }
             };
@@ -573,7 +573,7 @@ namespace vkhip {
                             const int oc = mw0 + i * 32 + qq * 8 + lk * 4;
                             float4v   v  = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
                             if constexpr (MODE == 0) {
-                                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yrs, yoff[b][jj][i][qq], 0, 0);
+                                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yrs, yoff[b][jj][i][qq], 0, kStreamStore);
                                 continue;
                             }
                             if constexpr (MODE >= 2) v += bv[i][qq];
@@ -586,7 +586,7 @@ namespace vkhip {
                             if (oc + 1 >= a.Cout) v.y = 0.f;
                             if (oc + 2 >= a.Cout) v.z = 0.f;
                             if (oc + 3 >= a.Cout) v.w = 0.f;
-                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff[b][jj][i][qq], 0, 0);
+                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, yoff[b][jj][i][qq], 0, kStreamStore);
                         }
             }
         };
@@ -1197,7 +1197,7 @@ namespace vkhip {
 #pragma unroll
                 for (int i = 0; i < FM; ++i)
 #pragma unroll
-                    for (int qq = 0; qq < 4; ++qq) rv[j][i][qq] = a.has_res ? __builtin_amdgcn_raw_buffer_load_b64(rrs, out_offset(t, j, i, qq), 0, 0)
+                    for (int qq = 0; qq < 4; ++qq) rv[j][i][qq] = a.has_res ? __builtin_amdgcn_raw_buffer_load_b64(rrs, out_offset(t, j, i, qq), 0, kStreamLoad)
                                                                             : u32x2 {0u, 0u};
         };
         auto store_tile = [&](int t, const unsigned char *bias_lds, auto act_c) __attribute__((always_inline)) {
@@ -1222,7 +1222,7 @@ namespace vkhip {
                         if (oc + 1 >= a.Cout) v.y = 0.f;
                         if (oc + 2 >= a.Cout) v.z = 0.f;
                         if (oc + 3 >= a.Cout) v.w = 0.f;
-                        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, out_offset(t, j, i, qq), 0, 0);
+                        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, out_offset(t, j, i, qq), 0, kStreamStore);
                     }
                 }
         };
@@ -1647,7 +1647,7 @@ namespace vkhip {
 #pragma unroll
                     for (int j = 0; j < FN; ++j)
 #pragma unroll
-                        for (int qq = 0; qq < 4; ++qq) rn[mi][j][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff(c, mi, j, qq), 0, 0);
+                        for (int qq = 0; qq < 4; ++qq) rn[mi][j][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff(c, mi, j, qq), 0, kStreamLoad);
             }
         };
         load(0);
@@ -1707,7 +1707,7 @@ namespace vkhip {
 #pragma unroll
                             for (int t = 0; t < 4; ++t) v[t] = oc + t < e.Cout ? apply_act(v[t], ACT, e.lo, e.hi) : 0.f;
                             const half4 o = f4_to_h4(v);
-                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o), yrs, yoff(c, mi, j, qq), 0, 0);
+                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o), yrs, yoff(c, mi, j, qq), 0, kStreamStore);
                             if constexpr (MR > 0) o16[qq][j] = o;
                         }
                     }
@@ -1758,7 +1758,7 @@ namespace vkhip {
                             const int      pn  = px / e.OHW, pr = px - pn * e.OHW;
                             const int      ocb = oc >> 2;
                             const unsigned off = px < e.P && ocb < p.Coutb3 ? (unsigned) (((pn * p.Coutb3 + ocb) * e.OHW + pr) * 8) : kInvalid;
-                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), y3rs, off, 0, 0);
+                            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), y3rs, off, 0, kStreamStore);
                         }
                     }
             };

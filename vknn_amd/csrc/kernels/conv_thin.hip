@@ -142,7 +142,7 @@ namespace vkhip {
                     if (oc + 2 >= a.Cout) v.z = 0.f;
                     if (oc + 3 >= a.Cout) v.w = 0.f;
                     const unsigned off = pok && ocb < a.Coutb ? (unsigned) ((((n * a.y_pstride + ocb) * OH + oy) * OW + ox) * 8) : kInvalid;
-                    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, off, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(v)), yrs, off, 0, kStreamStore);
                 }
             }
         };
