@@ -122,11 +122,12 @@ def test_conv_auto(gpu, case):
 NUM_TILES = V.vkhip().vkhip_conv_tile_count()
 BD_TILES = [8, 9, 10]            # conv_bd_kernel tiles (A via LDS DMA, B gathered into registers)
 PERS_TILES = [36, 37, 38, 39, 40, 41, 42]  # conv_dma_persist_kernel tiles (conv_dma_kernel's tiles, one workgroup walks many)
+LE_TILES = [46, 47, 48, 49]                # conv_dma_kernel with the LDS-staged epilogue (even pixel count per image)
 DMA_TILES = [11, 12, 13, 14, 15, 16, 24, 25, 28, 29, 30, 31] + PERS_TILES  # dense-B tiles (A and B via LDS DMA)
 HALO_TILES = [17, 18, 19, 20, 26, 27, 32, 33, 34, 35]      # conv_halo_kernel tiles (3x3 s1 p1: input band staged once for all taps)
 STEM_TILES = [21, 22, 23]                 # conv_stem_kernel tiles (3x3/7x7 over at most 4 input channels)
 THIN_TILES = [43, 44, 45]                 # conv_thin_kernel tiles (<= 32 input, 16/32/64 output channels)
-GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES + HALO_TILES + STEM_TILES + THIN_TILES]
+GATHER_TILES = [t for t in range(NUM_TILES) if t not in DMA_TILES + HALO_TILES + STEM_TILES + THIN_TILES + LE_TILES]
 
 
 @pytest.mark.parametrize("tile", GATHER_TILES)
@@ -246,6 +247,34 @@ def test_conv_dma_persist_many_tiles(gpu, tile, shape):
     assert_parity(got, oracle_conv(x, w, b, res=res, act=2), f"persistent 1x1 tile {tile} {shape}")
     got, plan, _ = gpu_conv(x, w, b, act=1, algo=V.CONV_GEMM, tile=tile)
     assert_parity(got, oracle_conv(x, w, b, act=1), f"persistent 1x1 no residual tile {tile} {shape}")
+
+
+@pytest.mark.parametrize("tile", LE_TILES)
+@pytest.mark.parametrize("shape,stride,act", [((3, 72, 6, 10, 70), 1, 1), ((2, 256, 14, 14, 300), 1, 4), ((1, 24, 8, 8, 8), 1, 2),
+                                              ((5, 64, 6, 9, 40), 1, 5), ((1, 256, 28, 28, 512), 2, 1), ((2, 48, 12, 12, 130), 2, 0)])
+def test_conv_dma_lds_epilogue(gpu, tile, shape, stride, act):
+    """LDS-staged epilogue (residual copied into LDS as kilobyte rows, outputs finished in place,
+    16-byte row stores): pixel tiles crossing images and the end of the batch, ragged channels,
+    stride 2, every activation family, with and without a residual."""
+    N, C, H, W, Cout = shape
+    r = rng(470 + tile + C + H)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, 1, 1)) * 0.1).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    OH, OW = (H - 1) // stride + 1, (W - 1) // stride + 1
+    res = round_half(r.standard_normal((N, Cout, OH, OW)))
+    for rr in (res, None):
+        got, plan, _ = gpu_conv(x, w, b, (stride, stride), act=act, res=rr, algo=V.CONV_GEMM, tile=tile)
+        assert plan.tile == tile
+        assert_parity(got, oracle_conv(x, w, b, (stride, stride), res=rr, act=act), f"lds epilogue tile {tile} {shape} s{stride}")
+
+
+def test_conv_dma_lds_epilogue_refuses_odd_images(gpu):
+    lib = V.vkhip()
+    plan = V.ConvPlan()
+    d, _ = conv_desc((2, 64, 7, 7), (64, 64, 1, 1))
+    for t in LE_TILES:
+        assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, t, 0, ctypes.byref(plan)) != 0
 
 
 def test_conv_persist_tiles_refuse_other_algorithms(gpu):

@@ -970,6 +970,8 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
     if (kTiles[tile].kind == 5 && !thin_shape_ok(d, kTiles[tile], algo))
         return set_error(VKHIP_ERR_UNSUPPORTED, "thin tile %d needs a plain GEMM plan of a 3x3 pad-1 or 1x1 conv, stride 1 or 2 (1x1: stride 1), "
                          "Cin <= 32, Cout <= %d, even input width, no residual", tile, kTiles[tile].BM);
+    if (kTiles[tile].LE && (algo != VKHIP_CONV_GEMM || d->in_scale || ((int64_t) d->OH * d->OW) % 2))
+        return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d (LDS-staged epilogue) runs plain GEMM plans of an even pixel count per image only", tile);
     if (kTiles[tile].PERS && (algo != VKHIP_CONV_GEMM || d->in_scale))
         return set_error(VKHIP_ERR_UNSUPPORTED, "persistent tile %d runs plain GEMM plans only (no split-K, Winograd or input scale)", tile);
     ConvGeom g = gemm_geom(d, tile, wino);

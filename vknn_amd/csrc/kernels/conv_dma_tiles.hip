@@ -1,4 +1,4 @@
-// Tile instantiations of conv_dma_kernel (tiles 11-16, 24, 25, 28-31: dense B operands via LDS DMA) and of its
+// Tile instantiations of conv_dma_kernel (tiles 11-16, 24, 25, 28-31, and 46-49 with the LDS-staged epilogue: dense B operands via LDS DMA) and of its
 // persistent variant conv_dma_persist_kernel (tiles 36-42).
 #include "conv_kernels.h"
 
@@ -22,6 +22,26 @@ namespace vkhip {
             else return nullptr;
         }
         return pick_dma_ps<FM, FN, NS, WM, WN, 8>(steps);
+    }
+
+    // LDS-staged epilogue variants (the ring cut to the step count like pick_dma_ps, but never
+    // below what the epilogue's BM / 4 rows of 1040 bytes need)
+    template <int FM, int FN, int NS, int WM, int WN, int PS = 8>
+    static GemmKernelFn pick_le_ps(int steps) {
+        constexpr int STG = (32 * FM * WM + 32 * FN * WN * PS / 8) * kBK * 2;
+        if constexpr (NS > 1 && (NS - 1) * STG >= (32 * FM * WM / 4) * 1040) {
+            if (steps < NS) return pick_le_ps<FM, FN, NS - 1, WM, WN, PS>(steps);
+        }
+        return conv_dma_kernel<FM, FN, NS, WM, WN, PS, false, true>;
+    }
+    template <int FM, int FN, int NS, int WM, int WN>
+    static GemmKernelFn pick_le(int steps, int bmode) {
+        constexpr int lds16 = NS * (32 * FM * WM + 2 * 32 * FN * WN) * kBK * 2;
+        if (bmode == 2) {
+            if constexpr (lds16 <= 160 * 1024) return pick_le_ps<FM, FN, NS, WM, WN, 16>(steps);
+            else return nullptr;
+        }
+        return pick_le_ps<FM, FN, NS, WM, WN, 8>(steps);
     }
 
     // persistent variants (the ring spans tiles, so it is never cut to the step count)
@@ -69,6 +89,10 @@ namespace vkhip {
             case 40: return pick_pers<2, 2, 2, 1, 4>(bmode);
             case 41: return pick_pers<2, 2, 2, 4, 2>(bmode);
             case 42: return pick_pers<2, 2, 4, 2, 2>(bmode);
+            case 46: return pick_le<2, 2, 2, 2, 2>(steps, bmode);
+            case 47: return pick_le<1, 2, 2, 2, 2>(steps, bmode);
+            case 48: return pick_le<2, 2, 3, 2, 2>(steps, bmode);
+            case 49: return pick_le<1, 2, 4, 2, 2>(steps, bmode);
         }
         return nullptr;
     }

@@ -840,6 +840,86 @@ namespace vkhip {
         gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, bz, lane);
     }
 
+    // ------------------------------------------------------------------ LDS-staged epilogue
+    // Epilogue of a BM x 128 tile through LDS, for dense NC4HW4 outputs with an even pixel count
+    // per image: the residual tile reaches LDS by buffer-load-to-LDS, one 1 KB row (128 pixels of
+    // one channel block) per copy; each lane finishes its accumulators in place there (bias,
+    // residual, activation, fp16); then whole rows leave as 16-byte stores. Against the register
+    // epilogue (one 8-byte load and one 8-byte store per lane per 4-channel fragment quarter) it
+    // issues half the vector-memory instructions, each moving a contiguous kilobyte. `sm` must hold
+    // BM / 4 rows of 1040 bytes; the caller has finished reading it.
+    template <int FM, int FN, int BM, int BN, int NW>
+    __device__ __forceinline__ void gemm_epilogue_lds(const GemmArgs &a, float16v (&acc)[FM][FN], unsigned char *sm, int m0, int n0, int wm0,
+                                                      int wn0, int wave, int lane) {
+        static_assert(BN == 128, "one copy per channel-block row");
+        constexpr int      RS = BN * 8 + 16; // row stride, padded so the two half-waves of an 8-byte access use other banks
+        constexpr int      ROWS = BM / 4;
+        constexpr unsigned kInvalid = 0x80000000u;
+        const int          lrow = lane & 31, lk = lane >> 5;
+        const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc((void *) a.y, (short) 0, (int) a.y_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rrs =
+            __builtin_amdgcn_make_buffer_rsrc((void *) (a.has_res ? a.res : a.y), (short) 0, a.has_res ? (int) a.y_bytes : 0, 0x00020000);
+        // this lane's pixel pair of every row
+        const int  px  = n0 + 2 * lane;
+        const int  pn  = px / a.OHWp;
+        const int  pr  = px - pn * a.OHWp;
+        const bool pok = px < a.Pv && pr < a.OHW;
+        auto goff = [&](int r) __attribute__((always_inline)) {
+            const int ocb = (m0 >> 2) + r;
+            return pok && ocb < a.Coutb ? (unsigned) (((pn * a.y_pstride + ocb) * a.OHW + pr) * 8) : kInvalid;
+        };
+        __syncthreads(); // every wave is done with the ring
+        if (a.has_res) {
+#pragma unroll
+            for (int r = wave; r < ROWS; r += NW) {
+#if defined(__HIP_DEVICE_COMPILE__) // `sm` is a generic pointer here: the host pass rejects its cast to the LDS space
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rrs, (__attribute__((address_space(3))) void *) (sm + r * RS), 16, goff(r), 0, 0, kStreamLoad);
+#endif
+            }
+            __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+        }
+        __syncthreads();
+        auto finish = [&](auto act_c) __attribute__((always_inline)) {
+            constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int qq = 0; qq < 4; ++qq) {
+                    const int     rl = (wm0 + i * 32 + qq * 8 + lk * 4) >> 2;
+                    const int     oc = m0 + rl * 4;
+                    const float4v bv = *reinterpret_cast<const float4v *>(a.bias + oc);
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+                        u32x2  *e = reinterpret_cast<u32x2 *>(sm + rl * RS + (wn0 + j * 32 + lrow) * 8);
+                        float4v v = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
+                        v += bv;
+                        if (a.has_res) v += h4_to_f4(__builtin_bit_cast(half4, *e));
+                        v.x = apply_act(v.x, ACT, a.lo, a.hi);
+                        v.y = apply_act(v.y, ACT, a.lo, a.hi);
+                        v.z = apply_act(v.z, ACT, a.lo, a.hi);
+                        v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                        if (oc + 0 >= a.Cout) v.x = 0.f;
+                        if (oc + 1 >= a.Cout) v.y = 0.f;
+                        if (oc + 2 >= a.Cout) v.z = 0.f;
+                        if (oc + 3 >= a.Cout) v.w = 0.f;
+                        *e = __builtin_bit_cast(u32x2, f4_to_h4(v));
+                    }
+                }
+        };
+        switch (a.act) {
+            case VKHIP_ACT_RELU: finish(std::integral_constant<int, VKHIP_ACT_RELU> {}); break;
+            case VKHIP_ACT_RELU6: finish(std::integral_constant<int, VKHIP_ACT_RELU6> {}); break;
+            case VKHIP_ACT_CLIP: finish(std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
+            case VKHIP_ACT_HARDSWISH: finish(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
+            case VKHIP_ACT_SILU: finish(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
+            default: finish(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = wave; r < ROWS; r += NW)
+            __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4 *>(sm + r * RS + lane * 16), yrs, goff(r), 0, kStreamStore);
+    }
+
     // ------------------------------------------------------------------ LDS-DMA GEMM kernel
     // Third main loop, for dense B operands: 1x1 stride-1 convs over images with an even pixel
     // count, and the Winograd position GEMMs. Both operands reach LDS through the buffer unit
@@ -861,7 +941,9 @@ namespace vkhip {
     // up to 8 consecutive images (lane l: image l/8, halves (l%8)*8..+7) into 1 KB after the B
     // stage, and every B fragment is multiplied by the scales of its column's image before the
     // MFMA (fp16 products, rounded like the separate Mul's fp16 store).
-    template <int FM, int FN, int NS, int WM, int WN, int PS = 8, bool XS = false>
+    // LE: the LDS-staged epilogue (gemm_epilogue_lds; GEMM epilogue mode, BN = 128, even pixel
+    // count per image).
+    template <int FM, int FN, int NS, int WM, int WN, int PS = 8, bool XS = false, bool LE = false>
     __global__ __launch_bounds__(64 * WM * WN, 1) void conv_dma_kernel(GemmArgs a) {
         constexpr int NW     = WM * WN; // waves
         constexpr int BM     = 32 * FM * WM;
@@ -1035,7 +1117,12 @@ namespace vkhip {
                 compute(rel % NS, ks + NS - 1 < ks_end ? ks + NS - 1 : -1, (rel + NS - 1) % NS);
             }
         }
-        gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, bz, lane);
+        static_assert(!LE || NS * STAGE >= (BM / 4) * 1040, "the LDS-staged epilogue fits the ring");
+        if constexpr (LE) {
+            unsigned char *smg = sm;
+            gemm_epilogue_lds<FM, FN, BM, BN, NW>(a, acc, smg, m0, n0, wm0, wn0, wave, lane);
+        }
+        else gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, bz, lane);
     }
 
     // ------------------------------------------------------------------ persistent LDS-DMA GEMM kernel
@@ -1189,7 +1276,7 @@ namespace vkhip {
             const int  pn  = px / a.OHWp;
             const int  pr  = px - pn * a.OHWp;
             const int  ocb = ((t % a.m_tiles) * BM + wm0 + i * 32 + qq * 8 + lk * 4) >> 2;
-            return (px < a.Pv) & (pr < a.OHW) & (ocb < a.Coutb) ? (unsigned) (((pn * a.y_pstride + ocb) * a.OHW + pr) * 8) : kInvalid;
+            return ((px < a.Pv) & (pr < a.OHW) & (ocb < a.Coutb)) ? (unsigned) (((pn * a.y_pstride + ocb) * a.OHW + pr) * 8) : kInvalid;
         };
         auto prefetch_residual = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
@@ -1923,8 +2010,9 @@ namespace vkhip {
     //         output channels, FM = BM / 16 fragments; weights in registers).
     // PERS (kind 2 only): the persistent variant (conv_dma_persist_kernel), gridDim = resident
     // workgroups, each walking a strided list of tiles.
+    // LE (kind 2 only): the LDS-staged epilogue (gemm_epilogue_lds).
     struct TileCfg {
-        int BM, BN, WM, WN, kind, FM, FN, KK, PERS;
+        int BM, BN, WM, WN, kind, FM, FN, KK, PERS, LE;
     };
     static const TileCfg kTiles[] = {
         {128, 128, 2, 2, 0, 0, 0}, // 0
@@ -1973,10 +2061,14 @@ namespace vkhip {
         {16, 256, 1, 4, 5, 1, 0, 0},     // 43 thin conv, 16 output channels (conv_thin_kernel)
         {32, 256, 1, 4, 5, 2, 0, 0},     // 44 thin conv, 32 output channels
         {64, 256, 1, 4, 5, 4, 0, 0},     // 45 thin conv, 64 output channels
+        {128, 128, 2, 2, 2, 2, 2, 0, 0, 1}, // 46 tile 14 with the LDS-staged epilogue
+        {64, 128, 2, 2, 2, 1, 2, 0, 0, 1},  // 47 tile 24 with the LDS-staged epilogue
+        {128, 128, 2, 2, 2, 2, 2, 0, 0, 1}, // 48 tile 29 (3-stage ring) with the LDS-staged epilogue
+        {64, 128, 2, 2, 2, 1, 2, 0, 0, 1},  // 49 tile 31 (4-stage ring) with the LDS-staged epilogue
     };
-    constexpr int kNumTiles = 46;
+    constexpr int kNumTiles = 50;
     constexpr int kHaloMaxNBI[kNumTiles] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 4, 15, 10, 16, 48, 48, 48, 0, 0, 8, 15, 0, 0, 0, 0, 15, 8, 16, 10,
-                                            0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+                                            0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
     typedef void (*GemmKernelFn)(GemmArgs);
 
