@@ -140,12 +140,19 @@ typedef struct vkhip_conv_desc {
 /* Algorithms. GEMM is the implicit-GEMM MFMA kernel (any KHxKW/stride/pad/dilation, group 1);
  * SPLITK splits its reduction over `ksplit` workgroups and reduces fp32 partials in a second pass;
  * WINOGRAD is F(2x2,3x3) (3x3 s1 p1 d1 only): input transform, 16 batched MFMA GEMMs, output
- * transform; DEPTHWISE is the bandwidth kernel for group == C. */
+ * transform; DEPTHWISE is the bandwidth kernel for group == C. SPLITK_LAST is SPLITK without the
+ * second pass: the workgroup that finishes a tile's partials last sums them (in split order, so
+ * the result does not depend on arrival order) and runs the epilogue. Its workspace holds the
+ * partials, then at align256(ksplit * 16 * ceil(Cout/4) * N*OH*OW) one int arrival counter per
+ * output tile: they must be zero before a workspace's first SPLITK_LAST call, and every call
+ * leaves them zero (so calls that share a workspace must not overlap in time). The reference's
+ * split-K (src/backend/vulkan/ops/conv.cpp:51-65,440-447) always runs a reduce dispatch. */
 #define VKHIP_CONV_AUTO 0
 #define VKHIP_CONV_GEMM 1
 #define VKHIP_CONV_SPLITK 2
 #define VKHIP_CONV_WINOGRAD 3
 #define VKHIP_CONV_DEPTHWISE 4
+#define VKHIP_CONV_SPLITK_LAST 5
 
 typedef struct vkhip_conv_plan {
     int32_t algo;            /* one of VKHIP_CONV_* (never AUTO once planned) */
@@ -201,6 +208,9 @@ int vkhip_conv_forward_stages(const vkhip_conv_desc *d, const vkhip_conv_plan *p
  * scratch, which keeps the last call's contents: calls that overlap in time on one GPU (two
  * streams, or two host threads) race and must be serialised by the caller. */
 #define VKHIP_NOALLOC_SCRATCH_BYTES ((size_t) 64 << 20)
+/* SPLITK_LAST plans keep their arrival counters in a separate device array of this many ints per
+ * GPU (zero at load, left zero by every call); plans with more output tiles are rejected. */
+#define VKHIP_NOALLOC_MAX_TILES 16384
 /* Depthwise conv that also leaves, for a following global average pool, the sum of its stored fp16
  * outputs per (plane, row tile): pool is [N*ceil(C/4)][R] x 4 fp32, R = vkhip_conv_pool_parts
  * (0: the plan's kernel cannot; then use vkhip_conv_forward and vkhip_global_avg_pool). y is

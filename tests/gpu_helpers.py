@@ -64,6 +64,8 @@ def gpu_conv(x, w, b=None, stride=(1, 1), pads=(0, 0, 0, 0), dil=(1, 1), group=1
     dy = DeviceBuffer(V.nc4_elems(*yshape) * 2)
     dy.zero()
     ws = DeviceBuffer(plan.workspace_bytes) if plan.workspace_bytes else None
+    if ws:
+        ws.zero()  # SPLITK_LAST keeps arrival counters in it that start at zero
     check(lib.vkhip_conv_forward(ctypes.byref(d), ctypes.byref(plan), dx.ptr, dblob.ptr,
                                  dres.ptr if dres else None, dy.ptr, ws.ptr if ws else None, None), "conv_forward")
     check(lib.vkhip_stream_sync(None), "sync")

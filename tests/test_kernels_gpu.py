@@ -520,6 +520,73 @@ def test_conv_splitk(gpu, ksplit):
     assert_parity(got, oracle_conv(x, w, b, res=res, act=1), f"splitk {ksplit}")
 
 
+# (tile, ksplit, x shape, Cout, kernel size, residual): gather (3, 6, 1), B-direct (8, 10), LDS-DMA
+# (14, 16) and halo (17, 18, 20, 26) tiles, up to 16 splits and tiles with several workgroups
+SPLITK_LAST_CASES = [(3, 2, (1, 512, 7, 7), 128, 1, True), (3, 16, (1, 1024, 7, 7), 256, 1, True), (6, 4, (1, 256, 7, 7), 32, 3, False),
+                     (1, 3, (2, 256, 14, 14), 64, 1, True), (8, 6, (1, 256, 7, 7), 128, 3, False), (10, 4, (1, 256, 7, 7), 128, 3, False),
+                     (14, 4, (2, 512, 14, 14), 256, 1, True), (16, 2, (2, 512, 14, 14), 128, 1, False),
+                     (17, 4, (2, 256, 14, 14), 128, 3, False), (18, 4, (2, 256, 14, 14), 128, 3, False),
+                     (20, 8, (1, 512, 7, 7), 512, 3, False), (26, 2, (4, 512, 7, 7), 512, 3, True)]
+
+
+@pytest.mark.parametrize("case", SPLITK_LAST_CASES, ids=lambda c: f"t{c[0]}k{c[1]}")
+def test_conv_splitk_last(gpu, case):
+    """Split-K with the reduction in the conv kernel (the last workgroup of each tile sums the
+    partials in split order): oracle parity, the same bits on a second call over the same workspace
+    (the sum does not depend on which workgroup arrives last), and every arrival counter back at
+    zero after each call."""
+    tile, ks, xs, Cout, k, has_res = case
+    lib = V.vkhip()
+    r = rng(700 + tile * 17 + ks)
+    x = round_half(r.standard_normal(xs))
+    w = (r.standard_normal((Cout, xs[1], k, k)) * (0.6 / np.sqrt(xs[1] * k * k))).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    pad = k // 2
+    d, yshape = conv_desc(x.shape, w.shape, (1, 1), (pad,) * 4, act=1, has_res=int(has_res))
+    res = round_half(r.standard_normal(yshape)) if has_res else None
+    plan = V.ConvPlan()
+    check(lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_SPLITK_LAST, tile, ks, ctypes.byref(plan)), "plan")
+    assert plan.algo == V.CONV_SPLITK_LAST and plan.tile == tile and plan.ksplit == ks
+    blob = np.zeros(plan.weight_bytes, np.uint8)
+    check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(plan), w.ctypes.data, b.ctypes.data, blob.ctypes.data), "pack")
+    dblob, dx = DeviceBuffer.from_array(blob), to_device_nc4(x)
+    dres = to_device_nc4(res) if has_res else None
+    ws = DeviceBuffer(plan.workspace_bytes)
+    ws.zero()
+    coutb, P = (Cout + 3) // 4, xs[0] * xs[2] * xs[3]
+    cnt_off = -(-(ks * coutb * P * 16) // 256) * 256
+    ntiles = (plan.workspace_bytes - cnt_off) // 4
+    assert ntiles >= 1
+    outs = []
+    for call in range(2):
+        dy = DeviceBuffer(V.nc4_elems(*yshape) * 2)
+        dy.zero()
+        check(lib.vkhip_conv_forward(ctypes.byref(d), ctypes.byref(plan), dx.ptr, dblob.ptr, dres.ptr if dres else None, dy.ptr,
+                                     ws.ptr, None), "conv_forward")
+        check(lib.vkhip_stream_sync(None), "sync")
+        cnt = ws.download(np.int32, plan.workspace_bytes // 4)[cnt_off // 4:]
+        assert not cnt.any(), f"call {call}: {np.count_nonzero(cnt)} of {ntiles} arrival counters left nonzero"
+        outs.append(raw_nc4(dy, yshape))
+        if call == 0:
+            ref = oracle_conv(x, w, b, (1, 1), (pad,) * 4, res=res, act=1)
+            assert_parity(from_device_nc4(dy, yshape), ref, f"split-K in-kernel reduction tile {tile} ksplit {ks}")
+    assert np.array_equal(outs[0], outs[1]), "a second call gave other bits"
+
+
+def test_conv_splitk_last_refuses_other_tiles(gpu):
+    """Stem, thin, persistent and LDS-staged-epilogue tiles have no in-kernel split-K reduction."""
+    lib = V.vkhip()
+    plan = V.ConvPlan()
+    d, _ = conv_desc((2, 64, 14, 14), (64, 64, 1, 1))
+    for t in (36, 37, 46):
+        assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_SPLITK_LAST, t, 2, ctypes.byref(plan)) != 0
+    d, _ = conv_desc((1, 3, 32, 32), (16, 3, 3, 3), (1, 1), (1, 1, 1, 1))
+    for t in (21, 43):
+        assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_SPLITK_LAST, t, 2, ctypes.byref(plan)) != 0
+    d, _ = conv_desc((1, 64, 8, 8), (64, 64, 1, 1))
+    assert lib.vkhip_conv_plan_make(ctypes.byref(d), 6, 3, 2, ctypes.byref(plan)) != 0
+
+
 @pytest.mark.parametrize("shape", [(1, 64, 56, 56, 64), (2, 32, 13, 15, 40), (1, 256, 14, 14, 256), (2, 512, 7, 7, 512)])
 def test_conv_winograd(gpu, shape):
     N, C, H, W, Cout = shape

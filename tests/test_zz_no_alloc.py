@@ -1,7 +1,8 @@
 """vkhip_conv_forward_noalloc (the allocation-free variant of vkhip_conv_forward) against
 vkhip_conv_forward with a caller-allocated workspace, through the C ABI: identical plans run the
 same kernels, so the outputs must agree bit for bit. Two calls in a row on each plan family, the
-second on a smaller input, so the shared scratch is reused with stale contents from the first."""
+second on a smaller input, so the shared scratch is reused with stale contents from the first
+(split-K with the in-kernel reduction keeps its arrival counters apart from the scratch)."""
 import ctypes
 
 import numpy as np
@@ -35,6 +36,7 @@ def _run_both(lib, x, w, b, algo, ksplit=0, pads=(0, 0, 0, 0), res=None):
     y_ref.zero()
     y_new.zero()
     ws = DeviceBuffer(plan.workspace_bytes)
+    ws.zero()  # SPLITK_LAST keeps arrival counters in it that start at zero
     check(lib.vkhip_conv_forward(ctypes.byref(d), ctypes.byref(plan), dx.ptr, dblob.ptr, dres.ptr if dres else None, y_ref.ptr,
                                  ws.ptr, None), "conv_forward")
     check(lib.vkhip_conv_forward_noalloc(ctypes.byref(d), ctypes.byref(plan), dx.ptr, dblob.ptr, dres.ptr if dres else None,
@@ -45,16 +47,17 @@ def _run_both(lib, x, w, b, algo, ksplit=0, pads=(0, 0, 0, 0), res=None):
     return a, n, plan
 
 
+@pytest.mark.parametrize("algo", [V.CONV_SPLITK, V.CONV_SPLITK_LAST])
 @pytest.mark.parametrize("shapes", [[(4, 512, 7, 7, 256), (2, 256, 7, 7, 128)], [(1, 2048, 7, 7, 512), (1, 1024, 5, 5, 96)]])
-def test_noalloc_splitk_matches_workspace_path(lib, shapes):
+def test_noalloc_splitk_matches_workspace_path(lib, shapes, algo):
     for i, (N, C, H, W, Co) in enumerate(shapes):
         r = np.random.default_rng(300 + i + C)
         x = round_half(r.standard_normal((N, C, H, W)))
         w = (r.standard_normal((Co, C, 1, 1)) * 0.05).astype(np.float32)
         b = (r.standard_normal(Co) * 0.1).astype(np.float32)
         res = round_half(r.standard_normal((N, Co, H, W)))
-        a, n, plan = _run_both(lib, x, w, b, V.CONV_SPLITK, ksplit=4, res=res)
-        print(f"split-K call {i} {(N, C, H, W, Co)} ksplit={plan.ksplit} workspace={plan.workspace_bytes}", flush=True)
+        a, n, plan = _run_both(lib, x, w, b, algo, ksplit=4, res=res)
+        print(f"split-K (algo {algo}) call {i} {(N, C, H, W, Co)} ksplit={plan.ksplit} workspace={plan.workspace_bytes}", flush=True)
         assert np.array_equal(a, n), f"call {i}: {np.count_nonzero(a != n)} of {a.size} fp16 values differ"
 
 

@@ -24,7 +24,7 @@ c_int, c_i32, c_i64, c_u64, c_f, c_vp, c_sz, c_char_p = (
 c_dbl = ctypes.c_double
 
 ACT = {"none": 0, "relu": 1, "relu6": 2, "clip": 3, "hardswish": 4, "silu": 5}
-CONV_AUTO, CONV_GEMM, CONV_SPLITK, CONV_WINOGRAD, CONV_DEPTHWISE = 0, 1, 2, 3, 4
+CONV_AUTO, CONV_GEMM, CONV_SPLITK, CONV_WINOGRAD, CONV_DEPTHWISE, CONV_SPLITK_LAST = 0, 1, 2, 3, 4, 5
 
 
 class ConvDesc(ctypes.Structure):

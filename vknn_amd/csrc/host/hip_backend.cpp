@@ -49,6 +49,15 @@ namespace vknn {
             if (ptr) vkhip_free(ptr);
         }
 
+        // A conv workspace, zeroed: split-K plans that reduce in the kernel (VKHIP_CONV_SPLITK_LAST)
+        // keep arrival counters in it that must start at zero (each call leaves them zero).
+        std::shared_ptr<DevBuf> workspace(size_t bytes) {
+            if (!bytes) return nullptr;
+            auto b = std::make_shared<DevBuf>(bytes);
+            check(vkhip_fill_zero(b->ptr, bytes, nullptr), "workspace fill");
+            return b;
+        }
+
         std::shared_ptr<DevBuf> upload(const void *host, size_t bytes) {
             auto b = std::make_shared<DevBuf>(bytes);
             check(vkhip_memcpy_h2d(b->ptr, host, bytes, nullptr), "weight upload");
@@ -188,7 +197,7 @@ namespace vknn {
                     if (cacheWeights) TuneCache::instance().putWeights(wkey, host);
                 }
                 blob = upload(host.data(), host.size());
-                ws   = plan.workspace_bytes ? std::make_shared<DevBuf>(plan.workspace_bytes) : nullptr;
+                ws   = workspace(plan.workspace_bytes);
             }
 
             void choosePlan(SegEnv &env, const float *w, const float *b) {
@@ -249,14 +258,15 @@ namespace vknn {
                 const int64_t kdepth = (int64_t) d.KH * d.KW * ((d.Cin + 3) / 4) * 4;
                 if (!dw && (pixels <= 4096 || base.algo == VKHIP_CONV_SPLITK || (pixels * (int64_t) d.Cout <= (int64_t) 512 * 128 * 256 && kdepth >= 512))) {
                     for (int t: {3, 6, 1, 8, 10, 14, 16, 17, 18, 20, 26})
-                        for (int ks: {2, 3, 4, 8, 16}) cands.push_back({VKHIP_CONV_SPLITK, t, ks});
+                        for (int ks: {2, 3, 4, 8, 16})
+                            for (int alg: {VKHIP_CONV_SPLITK, VKHIP_CONV_SPLITK_LAST}) cands.push_back({alg, t, ks});
                 }
                 if (tuning != (int) Mode::Thorough) {
                     // Fast: the heuristic pick, the tiles that win somewhere on the config shapes, and
                     // the split-K set.
                     std::vector<std::array<int32_t, 3>> keep;
                     for (auto &c: cands)
-                        if (c[0] == VKHIP_CONV_SPLITK || c[0] == VKHIP_CONV_DEPTHWISE || c[1] == base.tile || c[1] == 0 || c[1] == 1 || c[1] == 3 || c[1] == 5 ||
+                        if (c[0] == VKHIP_CONV_SPLITK || c[0] == VKHIP_CONV_SPLITK_LAST || c[0] == VKHIP_CONV_DEPTHWISE || c[1] == base.tile || c[1] == 0 || c[1] == 1 || c[1] == 3 || c[1] == 5 ||
                             c[1] == 7 || c[1] >= 8)
                             keep.push_back(c);
                     cands = keep;
@@ -338,7 +348,7 @@ namespace vknn {
                 std::vector<uint8_t> host(p.weight_bytes);
                 if (vkhip_conv_pack_weights(&d, &p, w, b, host.data())) return 1e30;
                 auto   bl  = upload(host.data(), host.size());
-                auto   wsb = p.workspace_bytes ? std::make_shared<DevBuf>(p.workspace_bytes) : nullptr;
+                auto   wsb = workspace(p.workspace_bytes);
                 size_t k   = 0;
                 auto   run = [&]() {
                     const TuneSet &t = sets[k++ % sets.size()];
@@ -391,7 +401,7 @@ namespace vknn {
             }
 
             std::string describe() const override {
-                static const char *algos[] = {"auto", "gemm", "splitk", "winograd", "depthwise"};
+                static const char *algos[] = {"auto", "gemm", "splitk", "winograd", "depthwise", "splitk_last"};
                 return std::string(algos[plan.algo]) + " tile=" + std::to_string(plan.tile) + " ksplit=" + std::to_string(plan.ksplit) +
                        (d.in_scale ? " +input scale" : "") + (poolOut != kNoTensor ? " +max pool" : "") + (gapPart ? " +pool sums" : "") + " kernel=" +
                        (poolOut != kNoTensor ? std::string("stem_pool_kernel") : std::string(vkhip_conv_plan_kernel(&plan)));

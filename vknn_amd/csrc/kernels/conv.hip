@@ -857,24 +857,31 @@ namespace vkhip {
     // to a kernel: it is only a host-side handle, so the per-device address comes from
     // hipGetSymbolAddress, taken once per device with that device current.
     static __device__ __align__(256) unsigned char scratch[VKHIP_NOALLOC_SCRATCH_BYTES];
+    // Arrival counters of its in-kernel split-K reductions (VKHIP_CONV_SPLITK_LAST), apart from the
+    // scratch that other calls overwrite: zero when the module loads, and every call leaves them zero.
+    static __device__ __align__(256) int scratch_counters[VKHIP_NOALLOC_MAX_TILES];
     constexpr int kMaxDevices = 64;
 
-    static int scratch_ptr(void **out) {
+    static int scratch_ptr(void **out, int **counters) {
         static std::mutex mu;
         static void      *ptrs[kMaxDevices] = {};
+        static void      *cptrs[kMaxDevices] = {};
         int               dev             = 0;
         if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
             return set_error(VKHIP_ERR_RUNTIME, "conv_forward_noalloc: no current device");
         std::lock_guard<std::mutex> lock(mu);
         if (!ptrs[dev]) {
-            void      *p  = nullptr;
+            void      *p = nullptr, *c = nullptr;
             hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-            if (rc != hipSuccess || !p)
+            if (rc == hipSuccess) rc = hipGetSymbolAddress(&c, HIP_SYMBOL(scratch_counters));
+            if (rc != hipSuccess || !p || !c)
                 return set_error(VKHIP_ERR_RUNTIME, "conv_forward_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
                                  hipGetErrorString(rc));
-            ptrs[dev] = p;
+            ptrs[dev]  = p;
+            cptrs[dev] = c;
         }
-        *out = ptrs[dev];
+        *out      = ptrs[dev];
+        *counters = (int *) cptrs[dev];
         return VKHIP_OK;
     }
 
@@ -950,14 +957,18 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
     }
     if (algo == VKHIP_CONV_WINOGRAD && !wino_eligible(d))
         return set_error(VKHIP_ERR_INVALID, "Winograd F(2,3) needs 3x3 stride 1 pad 1 dilation 1");
+    if (algo < VKHIP_CONV_AUTO || algo > VKHIP_CONV_SPLITK_LAST) return set_error(VKHIP_ERR_INVALID, "unknown conv algorithm %d", algo);
     if (algo == VKHIP_CONV_AUTO) {
         ConvGeom g   = gemm_geom(d, 3, false);
         int64_t  wgs = g.m_tiles * g.n_tiles;
         algo         = (wgs < 256 && g.nsteps >= 16) ? VKHIP_CONV_SPLITK : VKHIP_CONV_GEMM;
     }
-    const bool wino = algo == VKHIP_CONV_WINOGRAD;
-    if (tile < 0) tile = (algo == VKHIP_CONV_SPLITK) ? (ceil_div(d->Cout, 4) * 4 <= 32 ? 6 : 3) : default_tile(d, wino);
+    const bool wino  = algo == VKHIP_CONV_WINOGRAD;
+    const bool split = algo == VKHIP_CONV_SPLITK || algo == VKHIP_CONV_SPLITK_LAST;
+    if (tile < 0) tile = split ? (ceil_div(d->Cout, 4) * 4 <= 32 ? 6 : 3) : default_tile(d, wino);
     if (tile >= kNumTiles) return set_error(VKHIP_ERR_INVALID, "tile index %d out of range", tile);
+    if (algo == VKHIP_CONV_SPLITK_LAST && (kTiles[tile].kind > 3 || kTiles[tile].PERS || kTiles[tile].LE))
+        return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d has no in-kernel split-K reduction (gather, B-direct, LDS-DMA and halo tiles only)", tile);
     if (kTiles[tile].kind == 3 && (wino || !halo_shape_ok(d, kTiles[tile]) || halo_nbi(d, kTiles[tile]) > kHaloMaxNBI[tile]))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a 3x3 stride-1/2 pad-1 conv with Cin %% %d == 0 and a band that fits LDS", tile,
                          16 * kTiles[tile].KK);
@@ -979,7 +990,7 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
     plan->tile = tile;
     size_t wb  = (size_t) g.Coutp * g.Kp * 2;
     plan->weight_bytes = align256((size_t) g.Coutp * 4) + wb * (wino ? 16 : 1);
-    if (algo == VKHIP_CONV_SPLITK) {
+    if (split) {
         int64_t wgs = g.m_tiles * g.n_tiles;
         if (ksplit <= 0) {
             ksplit = (int) std::min<int64_t>({(int64_t) 16, std::max<int64_t>(2, ceil_div(512, wgs)), g.nsteps});
@@ -989,6 +1000,8 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
         while (ksplit > 1 && (int64_t) ksplit * g.Coutb * g.P * 16 >= (1LL << 31)) --ksplit;
         plan->ksplit          = ksplit;
         plan->workspace_bytes = (size_t) ksplit * g.Coutb * g.P * 16;
+        // SPLITK_LAST: one arrival counter per output tile after the partials
+        if (algo == VKHIP_CONV_SPLITK_LAST) plan->workspace_bytes = align256(plan->workspace_bytes) + (size_t) wgs * 4;
     } else if (wino) {
         int64_t nT            = g.P;
         plan->workspace_bytes = align256((size_t) 16 * g.Cinb * nT * 8) + (size_t) 16 * g.Coutb * nT * 8;
@@ -1119,7 +1132,7 @@ int vkhip_conv_maxpool_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *
 // ceil(Cin/4) / ceil(Cout/4)); larger for views into a wider tensor (a channel slice of a concat).
 static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *xs, const void *blob,
                              const void *res, void *y, void *workspace, vkhip_stream_t s, void *pool = nullptr, int64_t x_pstride = 0,
-                             int64_t y_pstride = 0, int stages = 7) {
+                             int64_t y_pstride = 0, int stages = 7, int *counters = nullptr) {
     if (!d || !plan || !x || !blob || !y) return set_error(VKHIP_ERR_INVALID, "conv_forward: null argument");
     const int64_t cinb = ceil_div(d->Cin, 4), coutb = ceil_div(d->Cout, 4);
     const int64_t xps = x_pstride > 0 ? x_pstride : cinb, yps = y_pstride > 0 ? y_pstride : coutb;
@@ -1213,7 +1226,8 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
     a.lo     = d->act_lo;
     a.hi     = d->act_hi;
     a.m_tiles = (int) g.m_tiles;
-    const int split_steps = plan->algo == VKHIP_CONV_SPLITK ? (int) ceil_div(g.nsteps, plan->ksplit) : (int) g.nsteps;
+    const bool split       = plan->algo == VKHIP_CONV_SPLITK || plan->algo == VKHIP_CONV_SPLITK_LAST;
+    const int  split_steps = split ? (int) ceil_div(g.nsteps, plan->ksplit) : (int) g.nsteps;
     GemmKernelFn fn = gemm_kernel_for(plan->tile, g.bmode, split_steps,
                                       t.kind == 3 ? halo_nbi(d, t) * (d->W % 2 ? -1 : 1) : (t.kind == 4 ? stem_nbi(d, t) : 0), d->in_scale != 0);
     if (!fn && t.kind != 5) return set_error(VKHIP_ERR_INVALID, "conv_forward: no kernel for tile %d", plan->tile);
@@ -1266,16 +1280,20 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
     a.H  = d->H; a.W = d->W; a.HW = d->H * d->W;
     a.OW = d->OW; a.OHW = d->OH * d->OW;
     a.KW = d->KW; a.SH = d->SH; a.SW = d->SW; a.PT = d->PT; a.PL = d->PL; a.DH = d->DH; a.DW = d->DW;
-    if (plan->algo == VKHIP_CONV_SPLITK) {
+    if (split) {
         int ks = plan->ksplit;
         a.steps_per_split = (int) ceil_div(g.nsteps, ks);
         ks = (int) ceil_div(g.nsteps, a.steps_per_split);
         a.omode = OMODE_PARTIAL;
         a.part  = (float4v *) workspace;
+        if (plan->algo == VKHIP_CONV_SPLITK_LAST) {
+            // the last workgroup of each tile sums the partials: counters after them, zero between calls
+            a.cnt = counters ? counters : (int *) ((char *) workspace + align256((size_t) plan->ksplit * g.Coutb * g.P * 16));
+        }
         dim3 grid((unsigned) (g.m_tiles * g.n_tiles), (unsigned) ks, 1);
         fn<<<grid, 64 * t.WM * t.WN, 0, st>>>(a);
         int rc = check_launch("conv_gemm_splitk");
-        if (rc) return rc;
+        if (rc || plan->algo == VKHIP_CONV_SPLITK_LAST) return rc;
         int64_t total = g.Coutb * g.P;
         splitk_reduce_kernel<<<dim3((unsigned) ceil_div(total, 256)), 256, 0, st>>>(
             (const float4v *) workspace, a.bias, a.res, a.y, ks, (int) g.Coutb, d->Cout, (int) g.P, a.OHW, d->act, d->act_lo,
@@ -1366,13 +1384,21 @@ int vkhip_conv_forward_noalloc(const vkhip_conv_desc *d, const vkhip_conv_plan *
     if (plan->workspace_bytes > VKHIP_NOALLOC_SCRATCH_BYTES)
         return set_error(VKHIP_ERR_INVALID, "conv_forward_noalloc: the plan needs %zu bytes of workspace, more than the %zu-byte scratch",
                          plan->workspace_bytes, (size_t) VKHIP_NOALLOC_SCRATCH_BYTES);
-    void *ws = nullptr;
+    if (plan->algo == VKHIP_CONV_SPLITK_LAST) {
+        const ConvGeom g = gemm_geom(d, plan->tile, false);
+        if (g.m_tiles * g.n_tiles > VKHIP_NOALLOC_MAX_TILES)
+            return set_error(VKHIP_ERR_INVALID, "conv_forward_noalloc: the plan has %lld output tiles, more than the %d arrival counters",
+                             (long long) (g.m_tiles * g.n_tiles), VKHIP_NOALLOC_MAX_TILES);
+    }
+    void *ws  = nullptr;
+    int  *cnt = nullptr;
     if (plan->workspace_bytes) {
         int rc = vkhip_init();
         if (rc) return rc;
-        if ((rc = scratch_ptr(&ws))) return rc;
+        if ((rc = scratch_ptr(&ws, &cnt))) return rc;
     }
-    return vkhip_conv_forward(d, plan, x, blob, res, y, ws, s);
+    if (d->in_scale) return set_error(VKHIP_ERR_INVALID, "conv_forward: an in_scale plan runs through vkhip_conv_forward_scaled");
+    return conv_forward_impl(d, plan, x, nullptr, blob, res, y, ws, s, nullptr, 0, 0, 7, cnt);
 }
 
 } // extern "C"

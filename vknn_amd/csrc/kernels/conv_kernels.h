@@ -56,6 +56,8 @@ namespace vkhip {
         unsigned      xs_bytes;                        // bytes of xs
         int           x_pstride, y_pstride;            // channel blocks per image of the buffers x / y point into
                                                        // (Cinb / Coutb, or more for a view into a wider tensor)
+        int          *cnt;                             // split-K: per-tile arrival counters when the last
+                                                       // workgroup of a tile sums the partials (else null)
     };
 
     enum { OMODE_EPILOGUE = 0, OMODE_RAW = 1, OMODE_PARTIAL = 2 };
@@ -102,6 +104,86 @@ namespace vkhip {
             }
         }
     };
+
+    // ------------------------------------------------------------------ in-kernel split-K reduction
+    // The split-K workgroups of one output tile (blockIdx.x, splits blockIdx.y) store their fp32
+    // partial tiles agent-coherent (MODE 4: written through to the device coherence point, so no
+    // cache write-back is needed before counting in), wait for those stores, and count in on the
+    // tile's counter; the workgroup that arrives last resets the counter (each launch leaves every
+    // counter at zero) and returns true. `flag`: a word of the kernel's LDS that no wave reads or
+    // writes any more (the broadcast of the outcome).
+    constexpr int kCoherent = 16; // buffer cache policy: sc1 (agent scope)
+
+    __device__ __forceinline__ bool splitk_last_arrival(const GemmArgs &a, volatile int *flag) {
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); // vmcnt(0): this wave's partial stores are complete
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int      *c    = a.cnt + blockIdx.x;
+            const int old  = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int last = old == (int) gridDim.y - 1;
+            if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *flag = last;
+        }
+        __syncthreads();
+        return *flag != 0;
+    }
+
+    // acc := the sum of the tile's partials over splits 0, 1, ..., in that order (this workgroup's
+    // own split from its registers, the others read agent-coherent), so the result does not depend
+    // on which workgroup arrived last.
+    template <int FM, int FN>
+    __device__ __forceinline__ void splitk_gather(const GemmArgs &a, float16v (&acc)[FM][FN], int mw0, int nw0, int split, int lane) {
+        constexpr unsigned kInvalid = 0x80000000u;
+        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc((void *) a.part, (short) 0, 0x7FFFFFFF, 0x00020000);
+        const int      lrow = lane & 31, lk = lane >> 5;
+        const unsigned sstride = (unsigned) a.Coutb * (unsigned) a.P * 16u;
+        unsigned       off[FN][FM][4];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int  px  = nw0 + j * 32 + lrow;
+            const int  pn  = px / a.OHWp;
+            const int  pr  = px - pn * a.OHWp;
+            const bool pok = (px < a.Pv) & (pr < a.OHW);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int qq = 0; qq < 4; ++qq) {
+                    const int ocb = (mw0 + i * 32 + qq * 8 + lk * 4) >> 2;
+                    off[j][i][qq] = pok & (ocb < a.Coutb) ? (unsigned) ((ocb * a.P + pn * a.OHW + pr) * 16) : kInvalid;
+                }
+        }
+        float16v sum[FM][FN];
+        const int ks = (int) gridDim.y;
+        for (int s = 0; s < ks; ++s) {
+            float16v p[FM][FN];
+            if (s == split) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) p[i][j] = acc[i][j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+#pragma unroll
+                        for (int qq = 0; qq < 4; ++qq) {
+                            const unsigned o = off[j][i][qq] == kInvalid ? kInvalid : off[j][i][qq] + (unsigned) s * sstride;
+                            const float4v  v = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(prs, o, 0, kCoherent));
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) p[i][j][qq * 4 + r] = v[r];
+                        }
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) sum[i][j] = s == 0 ? p[i][j] : sum[i][j] + p[i][j];
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = sum[i][j];
+    }
 
     template <int BM, int BN, int WM, int WN, int BMODE_>
     __global__ __launch_bounds__(kThreads) void conv_gemm_kernel(GemmArgs a) {
@@ -379,37 +461,53 @@ namespace vkhip {
         // pixels outside the tensor get an out-of-range offset, so their loads read zero and their
         // stores are dropped by the buffer unit.
         unsigned yoff[FN][FM][4];
+        auto offsets = [&](bool partial) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int  px = n0 + wn0 + j * 32 + lrow;
-            const bool pok = px < a.P;
-            const int  pn  = px / a.OHW;
-            const int  pr  = px - pn * a.OHW;
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int qq = 0; qq < 4; ++qq) {
-                    const int ocb = (m0 + wm0 + i * 32 + qq * 8 + lk * 4) >> 2;
-                    const bool ok = pok & (ocb < a.Coutb);
-                    if (a.omode == OMODE_PARTIAL) yoff[j][i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + px) * 16) : kInvalid;
-                    else yoff[j][i][qq] = ok ? (unsigned) (((pn * a.y_pstride + ocb) * a.OHW + pr) * 8) : kInvalid;
-                }
-        }
-        if (a.omode == OMODE_PARTIAL) {
-            const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc((void *) a.part, (short) 0, 0x7FFFFFFF, 0x00020000);
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
+            for (int j = 0; j < FN; ++j) {
+                const int  px  = n0 + wn0 + j * 32 + lrow;
+                const bool pok = px < a.P;
+                const int  pn  = px / a.OHW;
+                const int  pr  = px - pn * a.OHW;
 #pragma unroll
                 for (int i = 0; i < FM; ++i)
 #pragma unroll
                     for (int qq = 0; qq < 4; ++qq) {
-                        float4v v = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
-                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs, yoff[j][i][qq], 0, 0);
+                        const int  ocb = (m0 + wm0 + i * 32 + qq * 8 + lk * 4) >> 2;
+                        const bool ok  = pok & (ocb < a.Coutb);
+                        if (partial) yoff[j][i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + px) * 16) : kInvalid;
+                        else yoff[j][i][qq] = ok ? (unsigned) (((pn * a.y_pstride + ocb) * a.OHW + pr) * 8) : kInvalid;
                     }
-        } else {
+            }
+        };
+        offsets(a.omode == OMODE_PARTIAL);
+        bool epi = a.omode == OMODE_EPILOGUE;
+        if (a.omode == OMODE_PARTIAL) {
+            const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc((void *) a.part, (short) 0, 0x7FFFFFFF, 0x00020000);
+            auto store = [&](auto aux_c) __attribute__((always_inline)) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+#pragma unroll
+                        for (int qq = 0; qq < 4; ++qq) {
+                            float4v v = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs, yoff[j][i][qq], 0, decltype(aux_c)::value);
+                        }
+            };
+            if (!a.cnt) {
+                store(std::integral_constant<int, 0> {});
+                return;
+            }
+            store(std::integral_constant<int, kCoherent> {});
+            if (!splitk_last_arrival(a, reinterpret_cast<volatile int *>(&Bs[0][0]))) return;
+            // the workgroup that arrived last finishes the tile from the summed partials
+            splitk_gather<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, lane);
+            offsets(false);
+            epi = true;
+        }
+        {
             uint2 *Y = a.y + bz * a.y_bstride;
             const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc((void *) Y, (short) 0, (int) a.y_bytes, 0x00020000);
-            const bool  epi = a.omode == OMODE_EPILOGUE;
             float4v     bia[FM][4];
             u32x2       rv[FN][FM][4];
 #pragma unroll
@@ -508,7 +606,7 @@ namespace vkhip {
 
     template <int FM, int FN>
     __device__ __forceinline__ void gemm_epilogue(const GemmArgs &a, float16v (&acc)[FM][FN], int mw0, int nw0, int split, int bz,
-                                                  int lane) {
+                                                  int lane, volatile int *flag = nullptr) {
         constexpr unsigned kInvalid = 0x80000000u;
         const int  lrow = lane & 31;
         const int  lk   = lane >> 5;
@@ -519,18 +617,20 @@ namespace vkhip {
         // goes out before the stores it could queue behind: the vector memory counter retires in
         // order, so waiting for a load issued after a store also waits for that store.
         // MODE (compile time, so the element loop has no branches): 0 split-K partials (fp32, raw),
-        // 1 raw fp16 (Winograd M), 2 bias + act, 3 bias + residual + act.
+        // 1 raw fp16 (Winograd M), 2 bias + act, 3 bias + residual + act, 4 split-K partials stored
+        // agent-coherent (write-through, for the in-kernel reduction).
         constexpr int JG = FM * FN <= 8 ? FN : 1; // fragment columns per group
         constexpr int NG = FN / JG;
         auto finish = [&](auto mode_c, auto act_c) __attribute__((always_inline)) {
             constexpr int MODE = decltype(mode_c)::value;
             constexpr int ACT  = decltype(act_c)::value;
-            const __amdgpu_buffer_rsrc_t yrs = MODE == 0 ? __builtin_amdgcn_make_buffer_rsrc((void *) a.part, (short) 0, 0x7FFFFFFF, 0x00020000)
-                                                         : __builtin_amdgcn_make_buffer_rsrc((void *) Y, (short) 0, (int) a.y_bytes, 0x00020000);
+            constexpr bool PARTIAL = MODE == 0 || MODE == 4;
+            const __amdgpu_buffer_rsrc_t yrs = PARTIAL ? __builtin_amdgcn_make_buffer_rsrc((void *) a.part, (short) 0, 0x7FFFFFFF, 0x00020000)
+                                                       : __builtin_amdgcn_make_buffer_rsrc((void *) Y, (short) 0, (int) a.y_bytes, 0x00020000);
             const __amdgpu_buffer_rsrc_t rrs =
                 __builtin_amdgcn_make_buffer_rsrc((void *) (MODE == 3 ? a.res + bz * a.y_bstride : Y), (short) 0, (int) a.y_bytes, 0x00020000);
             float4v bv[FM][4];
-            if constexpr (MODE >= 2) {
+            if constexpr (MODE == 2 || MODE == 3) {
 #pragma unroll
                 for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -551,7 +651,7 @@ namespace vkhip {
                         for (int qq = 0; qq < 4; ++qq) {
                             const int  ocb = (mw0 + i * 32 + qq * 8 + lk * 4) >> 2;
                             const bool ok  = pok & (ocb < a.Coutb);
-                            if constexpr (MODE == 0)
+                            if constexpr (PARTIAL)
                                 yoff[b][jj][i][qq] = ok ? (unsigned) (((split * a.Coutb + ocb) * a.P + pn * a.OHW + pr) * 16) : kInvalid;
                             else yoff[b][jj][i][qq] = ok ? (unsigned) (((pn * a.y_pstride + ocb) * a.OHW + pr) * 8) : kInvalid;
                             if constexpr (MODE == 3) rv[b][jj][i][qq] = __builtin_amdgcn_raw_buffer_load_b64(rrs, yoff[b][jj][i][qq], 0, kStreamLoad);
@@ -572,11 +672,12 @@ namespace vkhip {
                             const int j  = j0 + jj;
                             const int oc = mw0 + i * 32 + qq * 8 + lk * 4;
                             float4v   v  = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
-                            if constexpr (MODE == 0) {
-                                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yrs, yoff[b][jj][i][qq], 0, kStreamStore);
+                            if constexpr (PARTIAL) {
+                                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yrs, yoff[b][jj][i][qq], 0,
+                                                                       MODE == 4 ? kCoherent : kStreamStore);
                                 continue;
                             }
-                            if constexpr (MODE >= 2) v += bv[i][qq];
+                            if constexpr (MODE == 2 || MODE == 3) v += bv[i][qq];
                             if constexpr (MODE == 3) v += h4_to_f4(__builtin_bit_cast(half4, rv[b][jj][i][qq]));
                             v.x = apply_act(v.x, ACT, a.lo, a.hi);
                             v.y = apply_act(v.y, ACT, a.lo, a.hi);
@@ -591,8 +692,13 @@ namespace vkhip {
             }
         };
         using I = std::integral_constant<int, 0>;
-        if (a.omode == OMODE_PARTIAL) return finish(I {}, I {});
-        if (a.omode == OMODE_RAW) return finish(std::integral_constant<int, 1> {}, I {});
+        if (a.omode == OMODE_PARTIAL) {
+            if (!a.cnt) return finish(I {}, I {});
+            finish(std::integral_constant<int, 4> {}, I {});
+            if (!splitk_last_arrival(a, flag)) return;
+            splitk_gather<FM, FN>(a, acc, mw0, nw0, split, lane);
+            // the workgroup that arrived last finishes the tile from the summed partials
+        } else if (a.omode == OMODE_RAW) return finish(std::integral_constant<int, 1> {}, I {});
         auto with_act = [&](auto mode_c) __attribute__((always_inline)) {
             switch (a.act) {
                 case VKHIP_ACT_RELU: finish(mode_c, std::integral_constant<int, VKHIP_ACT_RELU> {}); break;
@@ -837,7 +943,7 @@ namespace vkhip {
             });
         }
 
-        gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, bz, lane);
+        gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, bz, lane, reinterpret_cast<volatile int *>(&As[0][0]));
     }
 
     // ------------------------------------------------------------------ LDS-staged epilogue
@@ -1122,7 +1228,7 @@ namespace vkhip {
             unsigned char *smg = sm;
             gemm_epilogue_lds<FM, FN, BM, BN, NW>(a, acc, smg, m0, n0, wm0, wn0, wave, lane);
         }
-        else gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, bz, lane);
+        else gemm_epilogue<FM, FN>(a, acc, m0 + wm0, n0 + wn0, split, bz, lane, reinterpret_cast<volatile int *>(sm));
     }
 
     // ------------------------------------------------------------------ persistent LDS-DMA GEMM kernel
@@ -1601,7 +1707,8 @@ namespace vkhip {
         const int split  = blockIdx.y;
         float16v  acc[FM][FN];
         halo_mainloop<FM, FN, WM, WN, KK, NS, NBI, ODD>(a, sm, acc, tid, lane, wave, m_tile, n0, split);
-        gemm_epilogue<FM, FN>(a, acc, m_tile * BM + (wave / WN) * 32 * FM, n0 + (wave % WN) * 32 * FN, split, 0, lane);
+        gemm_epilogue<FM, FN>(a, acc, m_tile * BM + (wave / WN) * 32 * FM, n0 + (wave % WN) * 32 * FN, split, 0, lane,
+                              reinterpret_cast<volatile int *>(sm));
     }
 
     // ------------------------------------------------------------------ fused 3x3 -> 1x1 kernel
