@@ -1180,6 +1180,53 @@ def test_se_pooled(gpu, N, C, Cr, R, HW):
     assert_parity(got, ref, f"se pooled N{N} C{C} Cr{Cr}")
 
 
+@pytest.mark.parametrize("pooled", [False, True])
+@pytest.mark.parametrize("N,C,Cr", [(128, 960, 240), (128, 72, 24), (128, 120, 32), (128, 480, 120), (128, 672, 168), (1, 960, 240),
+                                    (37, 240, 64), (200, 96, 24)])
+def test_se_matches_two_fc_launches(gpu, N, C, Cr, pooled):
+    """vkhip_fused_se / vkhip_fused_se_pooled against vkhip_fc (or vkhip_fc_pooled) for FC1 and
+    vkhip_fc for FC2 on the same blob (the SE blob is the two fc blobs, W2's at the next 256-byte
+    boundary): the same bits, on two calls in a row over one workspace."""
+    lib = V.vkhip()
+    r = rng(900 + C + N + pooled)
+    Cb, R, HW = (C + 3) // 4, 2, 49
+    w1 = (r.standard_normal((Cr, C)) * 0.1).astype(np.float32)
+    b1 = (r.standard_normal(Cr) * 0.1).astype(np.float32)
+    w2 = (r.standard_normal((C, Cr)) * 0.2).astype(np.float32)
+    b2 = (r.standard_normal(C) * 0.1).astype(np.float32)
+    blob = np.zeros(lib.vkhip_se_weight_bytes(C, Cr), np.uint8)
+    check(lib.vkhip_se_pack_weights(C, Cr, w1.ctypes.data, b1.ctypes.data, w2.ctypes.data, b2.ctypes.data, blob.ctypes.data))
+    w1_bytes = lib.vkhip_fc_weight_bytes(C, Cr)
+    w2_off = (w1_bytes + 255) // 256 * 256
+    dblob = DeviceBuffer.from_array(blob)
+    if pooled:
+        src = DeviceBuffer.from_array((r.standard_normal((N, Cb, R, 4)) * HW * 0.3).astype(np.float32))
+    else:
+        src = to_device_nc4(round_half(r.standard_normal((N, C, 1, 1))))
+    nbytes = V.nc4_elems(N, C, 1, 1) * 2
+    ws_bytes = lib.vkhip_se_workspace_bytes(N, Cr)
+    ws = DeviceBuffer(ws_bytes)
+    ws.zero()
+    hid, ref = DeviceBuffer(V.nc4_elems(N, Cr, 1, 1) * 2), DeviceBuffer(nbytes)
+    if pooled:
+        check(lib.vkhip_fc_pooled(src.ptr, R, HW, dblob.ptr, hid.ptr, N, C, Cr, 1, 0.0, 0.0, None))
+    else:
+        check(lib.vkhip_fc(src.ptr, dblob.ptr, hid.ptr, N, C, Cr, 1, 0.0, 0.0, None))
+    check(lib.vkhip_fc(hid.ptr, dblob.ptr + w2_off, ref.ptr, N, Cr, C, 6, 1.0 / 6, 0.5, None))
+    want = None
+    for call in range(2):
+        out = DeviceBuffer(nbytes)
+        out.zero()
+        if pooled:
+            check(lib.vkhip_fused_se_pooled(src.ptr, R, HW, dblob.ptr, out.ptr, N, C, Cr, 1.0 / 6, 0.5, ws.ptr, None))
+        else:
+            check(lib.vkhip_fused_se(src.ptr, dblob.ptr, out.ptr, N, C, Cr, 1.0 / 6, 0.5, ws.ptr, None))
+        check(lib.vkhip_stream_sync(None))
+        want = ref.download(np.uint16, nbytes // 2) if want is None else want
+        got = out.download(np.uint16, nbytes // 2)
+        assert np.array_equal(got, want), f"call {call}: {np.count_nonzero(got != want)} of {got.size} fp16 values differ"
+
+
 # ---------------------------------------------------------------- depthwise + squeeze-excite pool sums
 @pytest.mark.parametrize("shape,k,s,rt", [((3, 72, 28, 28), 3, 2, 7), ((2, 120, 28, 28), 5, 1, 4), ((4, 960, 7, 7), 5, 1, 7),
                                           ((2, 22, 14, 14), 3, 1, 14), ((5, 40, 56, 56), 5, 2, 4),

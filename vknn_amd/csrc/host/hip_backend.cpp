@@ -522,7 +522,7 @@ namespace vknn {
                                             initF32(g, node.inputs[4]), host.data()),
                       "se pack");
                 blob  = upload(host.data(), host.size());
-                ws    = std::make_shared<DevBuf>(vkhip_se_workspace_bytes(N, Cr));
+                ws    = workspace(vkhip_se_workspace_bytes(N, Cr));
                 kind  = "se";
                 flops = 4.0 * N * C * Cr;
                 bytes = (int64_t) (host.size() + (size_t) N * ((C + 3) / 4 * 4) * 2 * 2);

@@ -806,26 +806,35 @@ namespace vkhip {
     // PART: x is not given; each 4-channel block of it is the global average pool of a depthwise
     // output, fp16(sum of R fp32 partial sums [N][Kb][R] / HW) (what the pool kernel computes and
     // stores), formed while loading.
-    template <int NF, bool X16, bool PART = false>
-    __global__ __launch_bounds__(512) void fc_kernel(const uint2 *x, const half_t *w, const float *b, uint2 *y, int N, int Kb,
-                                                     int Kp, int M, int Mb, int act, float lo, float hi, const float4v *part = nullptr,
-                                                     int R = 0, float hw = 1.f) {
+    struct FcArgs {
+        const uint2   *x;
+        const half_t  *w;
+        const float   *b;
+        uint2         *y;
+        int            N, Kb, Kp, M, Mb, act;
+        float          lo, hi;
+        const float4v *part;
+        int            R;
+        float          hw;
+    };
+
+    template <int NF, bool X16, bool PART>
+    __device__ __forceinline__ void fc_tile(const FcArgs &f_, int m0, int n0, float4v (*red)[NF][64]) {
         constexpr int U = 8;
-        __shared__ float4v red[8][NF][64];
+        const FcArgs &A = f_;
         const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
         const int r = lane & 15, q = lane >> 4;
-        const int m0 = blockIdx.x * 16, n0 = blockIdx.y * (16 * NF);
-        const half_t *wrow = w + (size_t) (m0 + r) * Kp + 8 * q;
+        const half_t *wrow = A.w + (size_t) (m0 + r) * A.Kp + 8 * q;
         const uint2  *xrow[NF];
         bool          nok[NF];
         for (int f = 0; f < NF; ++f) {
             const int n = n0 + f * 16 + r;
-            nok[f]      = n < N;
-            xrow[f]     = x + (size_t) (nok[f] ? n : 0) * Kb + 2 * q;
+            nok[f]      = n < A.N;
+            xrow[f]     = A.x + (size_t) (nok[f] ? n : 0) * A.Kb + 2 * q;
         }
         float4v acc[NF];
         for (int f = 0; f < NF; ++f) acc[f] = float4v {0.f, 0.f, 0.f, 0.f};
-        const int chunks = Kp >> 5;
+        const int chunks = A.Kp >> 5;
         for (int c0 = wave; c0 < chunks; c0 += 8 * U) {
             half8 a[U], bv[U][NF];
 #pragma unroll
@@ -840,23 +849,23 @@ namespace vkhip {
                     if (PART) {
                         const int n = n0 + f * 16 + r;
                         auto pooled = [&](int k) __attribute__((always_inline)) {
-                            const float4v *q = part + ((long long) n * Kb + k) * R;
+                            const float4v *q = A.part + ((long long) n * A.Kb + k) * A.R;
                             float4v        s4 = {0.f, 0.f, 0.f, 0.f};
-                            for (int i = 0; i < R; ++i) s4 += q[i];
-                            return f4_to_h4(s4 / hw);
+                            for (int i = 0; i < A.R; ++i) s4 += q[i];
+                            return f4_to_h4(s4 / A.hw);
                         };
-                        if (c < chunks && nok[f] && kb < Kb) lo4 = pooled(kb);
-                        if (c < chunks && nok[f] && kb + 1 < Kb) hi4 = pooled(kb + 1);
+                        if (c < chunks && nok[f] && kb < A.Kb) lo4 = pooled(kb);
+                        if (c < chunks && nok[f] && kb + 1 < A.Kb) hi4 = pooled(kb + 1);
                     } else if (c < chunks && nok[f]) {
                         if (X16) {
-                            if (kb < Kb) {
+                            if (kb < A.Kb) {
                                 const uint4 v = *(const uint4 *) (xrow[f] + c * 8);
                                 lo4 = u2_as_h4(uint2 {v.x, v.y});
                                 hi4 = u2_as_h4(uint2 {v.z, v.w});
                             }
                         } else {
-                            if (kb < Kb) lo4 = u2_as_h4(xrow[f][c * 8]);
-                            if (kb + 1 < Kb) hi4 = u2_as_h4(xrow[f][c * 8 + 1]);
+                            if (kb < A.Kb) lo4 = u2_as_h4(xrow[f][c * 8]);
+                            if (kb + 1 < A.Kb) hi4 = u2_as_h4(xrow[f][c * 8 + 1]);
                         }
                     }
                     bv[u][f] = half8 {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
@@ -875,19 +884,27 @@ namespace vkhip {
         }
         for (int f = 0; f < NF; ++f) red[wave][f][lane] = acc[f];
         __syncthreads();
-        if (threadIdx.x >= NF * 64) return;
-        const int f = threadIdx.x >> 6;
-        float4v   v = red[0][f][lane];
-        for (int k = 1; k < 8; ++k) v += red[k][f][lane];
-        const int n  = n0 + f * 16 + r;
-        const int mb = (m0 >> 2) + q; // output channel block: rows m0+4q .. +3
-        if (n >= N || mb >= Mb) return;
-        float4v o;
-        for (int j = 0; j < 4; ++j) {
-            const int m = mb * 4 + j;
-            o[j]        = m < M ? apply_act(v[j] + b[m], act, lo, hi) : 0.f;
+        if (threadIdx.x < NF * 64) {
+            const int f = threadIdx.x >> 6;
+            float4v   v = red[0][f][lane];
+            for (int k = 1; k < 8; ++k) v += red[k][f][lane];
+            const int n  = n0 + f * 16 + r;
+            const int mb = (m0 >> 2) + q; // output channel block: rows m0+4q .. +3
+            if (n < A.N && mb < A.Mb) {
+                float4v o;
+                for (int j = 0; j < 4; ++j) {
+                    const int m = mb * 4 + j;
+                    o[j]        = m < A.M ? apply_act(v[j] + A.b[m], A.act, A.lo, A.hi) : 0.f;
+                }
+                A.y[(size_t) n * A.Mb + mb] = h4_as_u2(f4_to_h4(o));
+            }
         }
-        y[(size_t) n * Mb + mb] = h4_as_u2(f4_to_h4(o));
+    }
+
+    template <int NF, bool X16, bool PART = false>
+    __global__ __launch_bounds__(512) void fc_kernel(FcArgs f) {
+        __shared__ float4v red[8][NF][64];
+        fc_tile<NF, X16, PART>(f, blockIdx.x * 16, blockIdx.y * (16 * NF), red);
     }
 
 } // namespace vkhip
@@ -1028,6 +1045,29 @@ int vkhip_fc_pack_weights(int64_t K, int64_t M, const float *w, int32_t transB, 
     return VKHIP_OK;
 }
 
+static FcArgs fc_args(const void *x, const float4v *part, int R, int HW, const void *blob, void *y, int64_t N, int64_t K, int64_t M, int32_t act,
+                      float lo, float hi) {
+    int64_t Kp, Mp;
+    fc_geom(K, M, Kp, Mp);
+    FcArgs f;
+    f.x    = (const uint2 *) x;
+    f.w    = (const half_t *) blob;
+    f.b    = (const float *) ((const char *) blob + Mp * Kp * 2);
+    f.y    = (uint2 *) y;
+    f.N    = (int) N;
+    f.Kb   = (int) (round_up(K, 4) / 4);
+    f.Kp   = (int) Kp;
+    f.M    = (int) M;
+    f.Mb   = (int) (round_up(M, 4) / 4);
+    f.act  = act;
+    f.lo   = lo;
+    f.hi   = hi;
+    f.part = part;
+    f.R    = R;
+    f.hw   = (float) HW;
+    return f;
+}
+
 // fc launcher: x as fp16 rows, or (part != null) as the pooled partial sums described at fc_kernel
 static int fc_launch(const void *x, const float4v *part, int R, int HW, const void *blob, void *y, int64_t N, int64_t K, int64_t M, int32_t act,
                      float lo, float hi, vkhip_stream_t s) {
@@ -1035,25 +1075,21 @@ static int fc_launch(const void *x, const float4v *part, int R, int HW, const vo
     if (N * round_up(K, 4) >= (1LL << 31) || N * round_up(M, 4) >= (1LL << 31)) return set_error(VKHIP_ERR_UNSUPPORTED, "fc: tensor too large");
     int64_t Kp, Mp;
     fc_geom(K, M, Kp, Mp);
-    const half_t *wp = (const half_t *) blob;
-    const float  *bp = (const float *) ((const char *) blob + Mp * Kp * 2);
-    const int Kb = (int) (round_up(K, 4) / 4), Mb = (int) (round_up(M, 4) / 4);
+    const int Kb = (int) (round_up(K, 4) / 4);
     // n tiles of 16 while the grid is small (more workgroups pulling weights), else 32
     const bool nf1 = (Mp / 16) * ceil_div(N, 16) <= 512;
     dim3       grid((unsigned) (Mp / 16), (unsigned) ceil_div(N, nf1 ? 16 : 32));
     hipStream_t st = resolve_stream(s);
-    const uint2 *xx = (const uint2 *) x;
-    uint2       *yy = (uint2 *) y;
-    const float  hw = (float) HW;
+    const FcArgs f = fc_args(x, part, R, HW, blob, y, N, K, M, act, lo, hi);
     if (part) {
-        if (nf1) fc_kernel<1, false, true><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi, part, R, hw);
-        else fc_kernel<2, false, true><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi, part, R, hw);
+        if (nf1) fc_kernel<1, false, true><<<grid, 512, 0, st>>>(f);
+        else fc_kernel<2, false, true><<<grid, 512, 0, st>>>(f);
     } else if (nf1) {
-        if (Kb % 2 == 0) fc_kernel<1, true><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi);
-        else fc_kernel<1, false><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi);
+        if (Kb % 2 == 0) fc_kernel<1, true><<<grid, 512, 0, st>>>(f);
+        else fc_kernel<1, false><<<grid, 512, 0, st>>>(f);
     } else {
-        if (Kb % 2 == 0) fc_kernel<2, true><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi);
-        else fc_kernel<2, false><<<grid, 512, 0, st>>>(xx, wp, bp, yy, (int) N, Kb, (int) Kp, (int) M, Mb, act, lo, hi);
+        if (Kb % 2 == 0) fc_kernel<2, true><<<grid, 512, 0, st>>>(f);
+        else fc_kernel<2, false><<<grid, 512, 0, st>>>(f);
     }
     return check_launch("fc");
 }
@@ -1067,6 +1103,45 @@ int vkhip_fc_pooled(const void *part, int32_t R, int64_t HW, const void *blob, v
                     float hi, vkhip_stream_t s) {
     if (!part || R <= 0 || HW <= 0 || HW >= (1LL << 24)) return set_error(VKHIP_ERR_INVALID, "fc_pooled: bad arguments");
     return fc_launch(nullptr, (const float4v *) part, R, (int) HW, blob, y, N, K, M, act, lo, hi, s);
+}
+
+// ---------------------------------------------------------------- squeeze-excite middle
+// The blob is the fc blob of W1 (K = C, M = Cr) at offset 0 and that of W2 (K = Cr, M = C) at a
+// 256-byte aligned offset. The workspace holds the fp16 hidden layer [N][ceil(Cr/4)] x 4.
+static size_t se_w2_offset(int64_t C, int64_t Cr) { return (vkhip_fc_weight_bytes(C, Cr) + 255) & ~(size_t) 255; }
+
+size_t vkhip_se_weight_bytes(int64_t C, int64_t Cr) { return C > 0 && Cr > 0 ? se_w2_offset(C, Cr) + vkhip_fc_weight_bytes(Cr, C) : 0; }
+
+size_t vkhip_se_workspace_bytes(int64_t N, int64_t Cr) { return N > 0 && Cr > 0 ? (size_t) (N * round_up(Cr, 4) * 2) : 0; }
+
+int vkhip_se_pack_weights(int64_t C, int64_t Cr, const float *w1, const float *b1, const float *w2, const float *b2, void *blob) {
+    if (!w1 || !w2 || !blob || C <= 0 || Cr <= 0) return set_error(VKHIP_ERR_INVALID, "se_pack: bad arguments");
+    std::memset(blob, 0, vkhip_se_weight_bytes(C, Cr));
+    int rc = vkhip_fc_pack_weights(C, Cr, w1, 1, b1, 1.f, 1.f, blob);
+    if (rc) return rc;
+    return vkhip_fc_pack_weights(Cr, C, w2, 1, b2, 1.f, 1.f, (char *) blob + se_w2_offset(C, Cr));
+}
+
+// x (avg, fp16 rows) or part (the pooled partial sums): FC1 + ReLU into the workspace, then FC2 +
+// hard-sigmoid into y, as two fc launches.
+static int se_launch(const void *avg, const float4v *part, int R, int64_t HW, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr,
+                     float alpha, float beta, void *workspace, vkhip_stream_t s) {
+    int rc = fc_launch(avg, part, R, (int) HW, blob, workspace, N, C, Cr, VKHIP_ACT_RELU, 0.f, 0.f, s);
+    if (rc) return rc;
+    return fc_launch(workspace, nullptr, 0, 1, (const char *) blob + se_w2_offset(C, Cr), y, N, Cr, C, VKHIP_ACT_HARDSIGMOID, alpha, beta, s);
+}
+
+int vkhip_fused_se(const void *avg, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr, float alpha, float beta, void *workspace,
+                   vkhip_stream_t s) {
+    if (!avg || !blob || !y || !workspace || N <= 0 || C <= 0 || Cr <= 0) return set_error(VKHIP_ERR_INVALID, "fused_se: bad arguments");
+    return se_launch(avg, nullptr, 0, 1, blob, y, N, C, Cr, alpha, beta, workspace, s);
+}
+
+int vkhip_fused_se_pooled(const void *part, int32_t R, int64_t HW, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr, float alpha,
+                          float beta, void *workspace, vkhip_stream_t s) {
+    if (!part || R <= 0 || HW <= 0 || HW >= (1LL << 24) || !blob || !y || !workspace || N <= 0 || C <= 0 || Cr <= 0)
+        return set_error(VKHIP_ERR_INVALID, "fused_se_pooled: bad arguments");
+    return se_launch(nullptr, (const float4v *) part, R, HW, blob, y, N, C, Cr, alpha, beta, workspace, s);
 }
 
 } // extern "C"

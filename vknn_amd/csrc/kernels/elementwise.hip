@@ -539,38 +539,6 @@ int vkhip_global_avg_pool(const void *x, void *y, int64_t N, int64_t C, int64_t 
     return check_launch("global_avg_pool");
 }
 
-// Fused SE middle as two batched skinny GEMMs (vkhip_fc): the blob is the fc blob of W1 (K = C,
-// M = Cr) at offset 0 and that of W2 (K = Cr, M = C) at a 256-byte aligned offset.
-static size_t se_w2_offset(int64_t C, int64_t Cr) { return (vkhip_fc_weight_bytes(C, Cr) + 255) & ~(size_t) 255; }
-
-size_t vkhip_se_weight_bytes(int64_t C, int64_t Cr) { return C > 0 && Cr > 0 ? se_w2_offset(C, Cr) + vkhip_fc_weight_bytes(Cr, C) : 0; }
-
-size_t vkhip_se_workspace_bytes(int64_t N, int64_t Cr) { return N > 0 && Cr > 0 ? (size_t) (N * round_up(Cr, 4) * 2) : 0; }
-
-int vkhip_se_pack_weights(int64_t C, int64_t Cr, const float *w1, const float *b1, const float *w2, const float *b2, void *blob) {
-    if (!w1 || !w2 || !blob || C <= 0 || Cr <= 0) return set_error(VKHIP_ERR_INVALID, "se_pack: bad arguments");
-    std::memset(blob, 0, vkhip_se_weight_bytes(C, Cr));
-    int rc = vkhip_fc_pack_weights(C, Cr, w1, 1, b1, 1.f, 1.f, blob);
-    if (rc) return rc;
-    return vkhip_fc_pack_weights(Cr, C, w2, 1, b2, 1.f, 1.f, (char *) blob + se_w2_offset(C, Cr));
-}
-
-int vkhip_fused_se(const void *avg, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr, float alpha, float beta, void *workspace,
-                   vkhip_stream_t s) {
-    if (!avg || !blob || !y || !workspace || N <= 0 || C <= 0 || Cr <= 0) return set_error(VKHIP_ERR_INVALID, "fused_se: bad arguments");
-    int rc = vkhip_fc(avg, blob, workspace, N, C, Cr, VKHIP_ACT_RELU, 0.f, 0.f, s);
-    if (rc) return rc;
-    return vkhip_fc(workspace, (const char *) blob + se_w2_offset(C, Cr), y, N, Cr, C, VKHIP_ACT_HARDSIGMOID, alpha, beta, s);
-}
-
-int vkhip_fused_se_pooled(const void *part, int32_t R, int64_t HW, const void *blob, void *y, int64_t N, int64_t C, int64_t Cr, float alpha,
-                          float beta, void *workspace, vkhip_stream_t s) {
-    if (!part || !blob || !y || !workspace || N <= 0 || C <= 0 || Cr <= 0) return set_error(VKHIP_ERR_INVALID, "fused_se_pooled: bad arguments");
-    int rc = vkhip_fc_pooled(part, R, HW, blob, workspace, N, C, Cr, VKHIP_ACT_RELU, 0.f, 0.f, s);
-    if (rc) return rc;
-    return vkhip_fc(workspace, (const char *) blob + se_w2_offset(C, Cr), y, N, Cr, C, VKHIP_ACT_HARDSIGMOID, alpha, beta, s);
-}
-
 static int maxpool_impl(const vkhip_pool_desc *d, const void *x, int64_t xps, void *y, int64_t yps, vkhip_stream_t s);
 
 int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s) { return maxpool_impl(d, x, 0, y, 0, s); }
