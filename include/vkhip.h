@@ -64,6 +64,10 @@ int vkhip_memcpy_d2h(void *dst, const void *src, size_t bytes, vkhip_stream_t s)
 int vkhip_memcpy_d2d(void *dst, const void *src, size_t bytes, vkhip_stream_t s);
 /* Zero `bytes` with a fill kernel (safe inside a captured graph, unlike a memset node). */
 int vkhip_fill_zero(void *p, size_t bytes, vkhip_stream_t s);
+/* Hold stream s for about `us` microseconds (0 .. 100000) with a one-wave kernel that sleeps and
+ * exits: the host can enqueue a timed sequence behind it, so the kernels then run back to back.
+ * For measurements (the plan refinement); no counterpart in the reference. */
+int vkhip_gpu_sleep(int32_t us, vkhip_stream_t s);
 
 int vkhip_stream_create(vkhip_stream_t *s);
 int vkhip_stream_destroy(vkhip_stream_t s);

@@ -38,6 +38,8 @@ def make_input(shape, seed, uniform=False):
     ("mnv3_tiny", 2, "fuse_se=1;fuse_dwpw=1"),
     ("yolo_tiny", 2, ""),
     ("resnet_tiny", 2, "tuning=off;graphs=0"),
+    ("resnet_tiny", 3, "refine=0"),
+    ("yolo_tiny", 2, "refine=0"),
 ])
 def test_tiny_models(gpu, model, batch, opts):
     sess = V.Session(model, batch, seed=11, options=opts)

@@ -77,6 +77,7 @@ VKHIP_API = {
     "vkhip_memcpy_d2h": (c_int, [c_vp, c_vp, c_sz, c_vp]),
     "vkhip_memcpy_d2d": (c_int, [c_vp, c_vp, c_sz, c_vp]),
     "vkhip_fill_zero": (c_int, [c_vp, c_sz, c_vp]),
+    "vkhip_gpu_sleep": (c_int, [c_i32, c_vp]),
     "vkhip_stream_create": (c_int, [P(c_vp)]),
     "vkhip_stream_destroy": (c_int, [c_vp]),
     "vkhip_stream_sync": (c_int, [c_vp]),

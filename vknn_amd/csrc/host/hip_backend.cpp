@@ -122,6 +122,16 @@ namespace vknn {
             // in-place concat or split): the plan is then a GEMM or split-K one (no Winograd).
             bool                    viewIO = false;
             bool                    cacheWeights = false; // keep the prepacked blob in the cache file
+            // The tuner's near-ties for the in-graph refinement (HipSegment::refinePlans), each with
+            // its packed blob and workspace; [0] is the tuner's pick. Empty unless this op was tuned.
+            struct Cand {
+                vkhip_conv_plan         p {};
+                std::shared_ptr<DevBuf> blob, ws;
+                std::vector<uint8_t>    host; // kept for the cache file's weight section
+                std::string             wkey;
+            };
+            std::vector<Cand> nearTies;
+            std::string       tuneKey;
 
             void prepare(const Node &node, SegEnv &env) override {
                 const Graph &g = *env.graph;
@@ -166,7 +176,8 @@ namespace vknn {
             // version (VKHIP_PACK_FORMAT) and a hash of the source weights and bias (a changed model,
             // plan or packer never takes a stale blob). The
             // reference keys its blobs by model tag + node + role (vk_op_common.h uploadCached).
-            std::string weightKey(const float *w, const float *b) const {
+            std::string weightKey(const float *w, const float *b) const { return weightKey(w, b, plan); }
+            std::string weightKey(const float *w, const float *b, const vkhip_conv_plan &pl) const {
                 uint64_t h = 1469598103934665603ull; // FNV-1a, 64 bit, over the fp32 bytes
                 auto mix = [&](const float *p, size_t n) {
                     const uint8_t *c = reinterpret_cast<const uint8_t *>(p);
@@ -175,7 +186,7 @@ namespace vknn {
                 mix(w, (size_t) d.Cout * (d.Cin / d.group) * d.KH * d.KW);
                 if (b) mix(b, (size_t) d.Cout);
                 char tail[96];
-                std::snprintf(tail, sizeof tail, "#p%d_%d_%d#f%d#%016llx", plan.algo, plan.tile, plan.ksplit, VKHIP_PACK_FORMAT,
+                std::snprintf(tail, sizeof tail, "#p%d_%d_%d#f%d#%016llx", pl.algo, pl.tile, pl.ksplit, VKHIP_PACK_FORMAT,
                               (unsigned long long) h);
                 return gpuTag() + "/w/" + name + keyOf(d, 0).substr(gpuTag().size()) + tail;
             }
@@ -223,6 +234,7 @@ namespace vknn {
                     return;
                 }
                 const std::string key = keyOf(d, tuning * 4 + wino) + (viewIO ? "_view" : "");
+                tuneKey               = key;
                 int32_t           cached = 0;
                 if (TuneCache::instance().get(key, cached)) {
                     // an entry that no longer makes a plan (e.g. written by another build) is re-tuned
@@ -337,6 +349,44 @@ namespace vknn {
                 TuneCache::instance().put(key, encodePick(pick));
                 check(vkhip_conv_plan_make(&d, pick[0], pick[1], pick[2], &plan), "conv plan");
                 build(w, b);
+                if (cfg.hipRefinePlans && !viewIO) {
+                    // near-ties (within 12% of the pick on the isolated shape), at most three
+                    std::vector<std::array<int32_t, 3>> alts;
+                    for (auto &t: timed)
+                        if (t.second != pick && t.first <= best * 1.12 && alts.size() < 3) alts.push_back(t.second);
+                    if (!alts.empty()) {
+                        nearTies.push_back({plan, blob, ws, {}, {}});
+                        for (auto &c: alts) {
+                            Cand k;
+                            if (vkhip_conv_plan_make(&d, c[0], c[1], c[2], &k.p)) continue;
+                            k.host.resize(k.p.weight_bytes);
+                            if (vkhip_conv_pack_weights(&d, &k.p, w, b, k.host.data())) continue;
+                            k.blob = upload(k.host.data(), k.host.size());
+                            k.ws   = workspace(k.p.workspace_bytes);
+                            if (cacheWeights) k.wkey = weightKey(w, b, k.p);
+                            else k.host.clear();
+                            nearTies.push_back(std::move(k));
+                        }
+                        if (nearTies.size() < 2) nearTies.clear();
+                    }
+                }
+            }
+
+            std::string planKey() const override { return tuneKey; }
+            int  candidates() const override { return gapPart || poolOut != kNoTensor ? 0 : (int) nearTies.size(); }
+            void useCandidate(int j) override {
+                plan = nearTies[j].p;
+                blob = nearTies[j].blob;
+                ws   = nearTies[j].ws;
+            }
+            void commitCandidate(int j) override {
+                if (nearTies.empty()) return;
+                useCandidate(j);
+                if (j > 0) {
+                    TuneCache::instance().put(tuneKey, encodePick({plan.algo, plan.tile, plan.ksplit}));
+                    if (cacheWeights && !nearTies[j].host.empty()) TuneCache::instance().putWeights(nearTies[j].wkey, nearTies[j].host);
+                }
+                nearTies.clear();
             }
 
             struct TuneSet {
@@ -1450,6 +1500,64 @@ namespace vknn {
             }
             check(vkhip_stream_sync(nullptr), "prepare sync");
             if (cfg.hipBranches) planStreams(ins, outs);
+            if (cfg.hipRefinePlans && !markers_) refinePlans();
+        }
+
+        // In-graph plan refinement. The autotuner times each conv alone on rotating cold buffers;
+        // inside the forward pass its input was just written by the op before it and partly sits in
+        // the last-level cache, which can reorder near-ties. Every op with near-tie candidates is
+        // timed here in the segment's own op order (one in-order stream, events around each op,
+        // the whole pass queued behind a short device sleep so the kernels run back to back), each
+        // pass switching all such ops to their j-th candidate at once (ops are timed independently
+        // of each other's choice). Three passes per candidate; an op keeps an alternative only if
+        // its best time beats the tuner's pick by more than 2%.
+        void HipSegment::refinePlans() {
+            // a pick is changed only for a tune-table key no other op of the segment uses (another op
+            // with the same key took the tuner's pick from the table and keeps it)
+            std::map<std::string, int> keyUses;
+            for (auto &op: ops_)
+                if (!op->planKey().empty()) ++keyUses[op->planKey()];
+            std::vector<int> ks;
+            int              nc = 0;
+            for (size_t k = 0; k < ops_.size(); ++k)
+                if (ops_[k]->candidates() > 1 && keyUses[ops_[k]->planKey()] == 1) {
+                    ks.push_back((int) k);
+                    nc = std::max(nc, ops_[k]->candidates());
+                } else ops_[k]->commitCandidate(0); // keeps its pick, frees the alternatives
+            if (ks.empty()) return;
+            for (TensorId t: boundaryInputs)
+                if (!extIn_.count(t) && !staging_.count(t)) {
+                    staging_[t] = std::make_shared<DevBuf>((size_t) numElements(g_.desc(t).shape) * 4);
+                    check(vkhip_fill_zero(staging_[t]->ptr, staging_[t]->bytes, stream_), "refine fill");
+                }
+            for (TensorId t: boundaryOutputs)
+                if (!outStaging_.count(t)) outStaging_[t] = std::make_shared<DevBuf>((size_t) numElements(g_.desc(t).shape) * 4);
+            while (events_.size() < 2 * ops_.size()) {
+                vkhip_event_t e;
+                check(vkhip_event_create(&e), "event");
+                events_.push_back(e);
+            }
+            std::vector<std::vector<double>> us(ks.size(), std::vector<double>(nc, 1e30));
+            for (int rep = 0; rep < 4; ++rep)
+                for (int j = 0; j < nc; ++j) {
+                    for (int k: ks) ops_[k]->useCandidate(std::min(j, ops_[k]->candidates() - 1));
+                    check(vkhip_gpu_sleep(3000, stream_), "refine sleep");
+                    recordAll(true);
+                    check(vkhip_stream_sync(stream_), "refine sync");
+                    if (rep == 0) continue; // the first pass of each candidate warms it up
+                    for (size_t i = 0; i < ks.size(); ++i) {
+                        if (j >= ops_[ks[i]]->candidates()) continue;
+                        float ms = 0;
+                        check(vkhip_event_elapsed_ms(events_[2 * ks[i]], events_[2 * ks[i] + 1], &ms), "event time");
+                        us[i][j] = std::min(us[i][j], (double) ms * 1e3);
+                    }
+                }
+            for (size_t i = 0; i < ks.size(); ++i) {
+                int best = 0;
+                for (int j = 1; j < ops_[ks[i]]->candidates(); ++j)
+                    if (us[i][j] < us[i][0] * 0.98 && us[i][j] < us[i][best]) best = j;
+                ops_[ks[i]]->commitCandidate(best);
+            }
         }
 
         // Two-stream list schedule over the recorded op order. Every activation has its own buffer

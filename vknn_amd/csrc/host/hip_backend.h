@@ -45,6 +45,12 @@ namespace vknn {
             virtual void        prepare(const Node &, SegEnv &) = 0;
             virtual void        record(SegEnv &, vkhip_stream_t) = 0;
             virtual std::string describe() const { return ""; }
+            // In-graph plan refinement: alternative plans of the op (0 or 1: nothing to refine),
+            // switching to one of them, and keeping one (which also records it as the op's pick).
+            virtual int  candidates() const { return 0; }
+            virtual void useCandidate(int) {}
+            virtual void commitCandidate(int) {}
+            virtual std::string planKey() const { return {}; } // tune-table key of the op's plan ("" if none)
             std::string         name, kind;
             OpType              type  = OpType::Unknown;
             double              flops = 0;
@@ -75,6 +81,7 @@ namespace vknn {
           private:
             TensorId resolve(TensorId t) const;
             void     planStreams(const std::vector<std::vector<TensorId>> &ins, const std::vector<std::vector<TensorId>> &outs);
+            void     refinePlans();
             void     recordAll(bool timed);
             void     launch(bool profile);
             void     dropGraph();

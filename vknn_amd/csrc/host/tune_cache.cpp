@@ -101,7 +101,9 @@ namespace vknn {
             std::map<std::string, int32_t> t;
             std::vector<char>              pipe;
             std::map<std::string, std::vector<uint8_t>> w;
-            if (!parse(bytes, t, &pipe, keepWeights ? &w : nullptr)) return 0; // unrecognised -> regenerate
+            // the weight section is carried along even when this session does not use it (tune-only
+            // mode), so that writing the table back never drops another session's blobs
+            if (!parse(bytes, t, &pipe, &w)) return 0; // unrecognised -> regenerate
             for (auto &kv: w) weights_.insert(kv); // blobs packed in this process take precedence
             if (!first) return 0;                 // a later load that only adds the weights
             fileBytes_[path] = bytes;

@@ -47,6 +47,12 @@ namespace vkhip {
         for (size_t k = n16 * 16 + i; k < bytes; k += st) p[k] = 0;
     }
 
+    // Holds the stream for about `iters` x 3.4 us (s_sleep 127 = 127 x 64 clocks at ~2.4 GHz),
+    // then exits: a bounded wait, never a spin on memory.
+    __global__ void sleep_kernel(int iters) {
+        for (int i = 0; i < iters; ++i) __builtin_amdgcn_s_sleep(127);
+    }
+
 } // namespace vkhip
 
 using namespace vkhip;
@@ -203,6 +209,12 @@ int vkhip_fill_zero(void *p, size_t bytes, vkhip_stream_t s) {
     if (blocks > 4096) blocks = 4096;
     fill_zero_kernel<<<dim3((unsigned) blocks), dim3(256), 0, resolve_stream(s)>>>((uint8_t *) p, bytes);
     return check_launch("fill_zero");
+}
+
+int vkhip_gpu_sleep(int32_t us, vkhip_stream_t s) {
+    if (us < 0 || us > 100000) return set_error(VKHIP_ERR_INVALID, "vkhip_gpu_sleep: 0 .. 100000 us");
+    sleep_kernel<<<dim3(1), dim3(64), 0, resolve_stream(s)>>>((us + 2) / 3);
+    return check_launch("gpu_sleep");
 }
 
 int vkhip_stream_create(vkhip_stream_t *s) {

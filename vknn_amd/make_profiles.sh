@@ -54,7 +54,7 @@ prof() {
         # wave states: two counter passes on the same plans (SQ_WAVE_CYCLES in both as the denominator)
         timeout -s KILL 300 rocprofv3 --pmc SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_VMEM SQ_ACTIVE_INST_LDS SQ_ACTIVE_INST_SCA \
             --output-format csv -d "$T/${stem}_sa" -o run -- python3 "$R/bench.py" $C --options "$O" > /dev/null 2>&1
-        timeout -s KILL 300 rocprofv3 --pmc SQ_WAVE_CYCLES SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_LDS_BANK_CONFLICT SQ_VMEM_TA_ADDR_FIFO_FULL SQ_INSTS_VALU \
+        timeout -s KILL 300 rocprofv3 --pmc SQ_WAVE_CYCLES SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_LDS_BANK_CONFLICT SQ_VMEM_TA_ADDR_FIFO_FULL SQ_INSTS_VALU SQ_WAVES \
             --output-format csv -d "$T/${stem}_sb" -o run -- python3 "$R/bench.py" $C --options "$O" > /dev/null 2>&1
         PYTHONPATH="$R" python3 -m vknn_amd.prof_summary stalls "$T/${stem}_sa/run_counter_collection.csv" "$T/${stem}_sb/run_counter_collection.csv" --steps 10 \
             --title "$title: wave states and MFMA busy per kernel family on MI355X" \
