@@ -68,11 +68,6 @@ namespace vknn {
         // (e.g. a residual block's projection shortcut) on a second stream, joined back by events,
         // so independent branches of a segment overlap. false keeps one in-order stream.
         bool hipBranches = true;
-        // HIP backend: after a segment's ops are planned, time the autotuner's near-tie plans of
-        // each conv (within 12% of its pick on the isolated shape) inside the segment's own
-        // sequence, where its input was just written by the op before it, and keep the fastest
-        // there (the cache file then holds that pick). false keeps the isolated pick.
-        bool hipRefinePlans = true;
         // HIP backend, profiling only: launches per op between its two timing events (the op's
         // time is their average; amortizes the event overhead on short kernels).
         int profileReps = 1;

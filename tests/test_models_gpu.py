@@ -38,10 +38,13 @@ def make_input(shape, seed, uniform=False):
     ("mnv3_tiny", 2, "fuse_se=1;fuse_dwpw=1"),
     ("yolo_tiny", 2, ""),
     ("resnet_tiny", 2, "tuning=off;graphs=0"),
-    ("resnet_tiny", 3, "refine=0"),
-    ("yolo_tiny", 2, "refine=0"),
+    ("resnet_tiny", 3, "VKNN_HIP_REFINE=0"),
+    ("yolo_tiny", 2, "VKNN_HIP_REFINE=0"),
 ])
-def test_tiny_models(gpu, model, batch, opts):
+def test_tiny_models(gpu, monkeypatch, model, batch, opts):
+    if opts.startswith("VKNN_"):  # an environment switch of the backend, not a session option
+        monkeypatch.setenv(*opts.split("="))
+        opts = ""
     sess = V.Session(model, batch, seed=11, options=opts)
     x = make_input(sess.in_shape, 5)
     got = sess.run(x)

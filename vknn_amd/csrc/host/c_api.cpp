@@ -44,7 +44,6 @@ namespace {
                 else if (k == "tuning") cfg.setHint(Hint::Tuning, tuningFromStr(v));
                 else if (k == "graphs") cfg.hipGraphs = v != "0";
                 else if (k == "branches") cfg.hipBranches = v != "0";
-                else if (k == "refine") cfg.hipRefinePlans = v != "0";
                 else if (k == "profile") cfg.profile = v != "0";
                 else if (k == "profile_reps") cfg.profileReps = std::max(1, std::atoi(v.c_str()));
                 else if (k == "fuse_dwpw") cfg.fuseDwPw = v != "0";

@@ -98,6 +98,12 @@ namespace vknn {
         static int32_t encodePick(const std::array<int32_t, 3> &p) { return (p[0] & 0xff) | (((p[1] + 1) & 0xff) << 8) | ((p[2] & 0xff) << 16); }
         static std::array<int32_t, 3> decodePick(int32_t v) { return {v & 0xff, ((v >> 8) & 0xff) - 1, (v >> 16) & 0xff}; }
 
+        // In-graph plan refinement (HipSegment::refinePlans) is on unless VKNN_HIP_REFINE=0.
+        static bool refineEnabled() {
+            const char *e = std::getenv("VKNN_HIP_REFINE");
+            return !(e && e[0] == '0');
+        }
+
         // ------------------------------------------------------------ conv
         struct ConvOp: HipOp {
             vkhip_conv_desc         d {};
@@ -349,7 +355,7 @@ namespace vknn {
                 TuneCache::instance().put(key, encodePick(pick));
                 check(vkhip_conv_plan_make(&d, pick[0], pick[1], pick[2], &plan), "conv plan");
                 build(w, b);
-                if (cfg.hipRefinePlans && !viewIO) {
+                if (refineEnabled() && !viewIO) {
                     // near-ties (within 12% of the pick on the isolated shape), at most three
                     std::vector<std::array<int32_t, 3>> alts;
                     for (auto &t: timed)
@@ -1500,7 +1506,7 @@ namespace vknn {
             }
             check(vkhip_stream_sync(nullptr), "prepare sync");
             if (cfg.hipBranches) planStreams(ins, outs);
-            if (cfg.hipRefinePlans && !markers_) refinePlans();
+            if (refineEnabled() && !markers_) refinePlans();
         }
 
         // In-graph plan refinement. The autotuner times each conv alone on rotating cold buffers;
