@@ -184,13 +184,15 @@ def test_conv_dma_1x1(gpu, tile, shape):
 
 @pytest.mark.parametrize("shape", [(2, 16, 20, 24, 16, 3, 1), (2, 16, 20, 24, 32, 3, 2), (1, 3, 32, 34, 16, 3, 2), (2, 32, 18, 18, 32, 3, 1),
                                    (2, 32, 16, 16, 64, 1, 1), (3, 24, 10, 14, 24, 3, 1), (2, 16, 30, 150, 16, 3, 1), (2, 5, 16, 16, 40, 3, 2),
-                                   (1, 8, 9, 130, 12, 3, 2), (2, 12, 7, 6, 64, 3, 1), (1, 32, 12, 12, 20, 3, 2)])
+                                   (1, 8, 9, 130, 12, 3, 2), (2, 12, 7, 6, 64, 3, 1), (1, 32, 12, 12, 20, 3, 2),
+                                   (2, 3, 224, 224, 64, 7, 2), (1, 3, 30, 34, 40, 7, 2), (3, 4, 18, 20, 16, 7, 2), (1, 1, 9, 136, 64, 7, 2)])
 @pytest.mark.parametrize("act", [1, 5])
 def test_conv_thin(gpu, shape, act):
     """Thin-channel kernel (16x16x32 MFMA, weights in registers, double-buffered input bands):
     every tile that takes the shape, against the oracle. Ragged channel counts (Cin 3, 5, 12, 24:
     zero slots of the rounded reduction), column blocks cut by the image edge, bands above and
-    below the image, stride 2, 1x1, ReLU and SiLU epilogues."""
+    below the image, stride 2, 1x1, the 7x7 stride-2 stem over 1-4 channels, ReLU and SiLU
+    epilogues."""
     N, C, H, W, Cout, K, S = shape
     r = rng(900 + C + H + Cout + K * S)
     x = round_half(r.standard_normal((N, C, H, W)))

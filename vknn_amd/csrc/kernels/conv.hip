@@ -711,14 +711,17 @@ namespace vkhip {
         return (int) ceil_div(rows * (RS / 2), 64);
     }
 
-    // conv_thin_kernel: 3x3 pad 1 (stride 1 or 2) or 1x1 pad 0 stride 1, dilation 1, Cin <= 32, Cout
+    // conv_thin_kernel: 3x3 pad 1 (stride 1 or 2), 1x1 pad 0 stride 1 or 7x7 pad 3 stride 2 over at most
+    // 4 channels; dilation 1, Cin <= 32, Cout
     // within the tile's BM, even input width (the band copies whole pixel pairs), no residual or
     // input scale, and an instantiated kernel (its weights fit the register budget)
     static bool thin_shape_ok(const vkhip_conv_desc *d, const TileCfg &t, int algo) {
         const int K = d->KH, S = d->SH;
         if (algo != VKHIP_CONV_GEMM || d->group != 1 || d->has_res || d->in_scale || d->Cin > 32 || d->Cout > t.BM) return false;
         if (d->KW != K || d->SW != S || d->DH != 1 || d->DW != 1 || d->W % 2) return false;
-        if (!((K == 3 && d->PT == 1 && d->PL == 1 && (S == 1 || S == 2)) || (K == 1 && d->PT == 0 && d->PL == 0 && S == 1))) return false;
+        if (!((K == 3 && d->PT == 1 && d->PL == 1 && (S == 1 || S == 2)) || (K == 1 && d->PT == 0 && d->PL == 0 && S == 1) ||
+              (K == 7 && d->PT == 3 && d->PL == 3 && S == 2 && d->Cin <= 4)))
+            return false;
         if (d->OH != (d->H + 2 * d->PT - K) / S + 1 || d->OW != (d->W + 2 * d->PL - K) / S + 1) return false;
         return thin_kernel_for((int) ceil_div(d->Cin, 4), t.FM, K, S) != nullptr;
     }

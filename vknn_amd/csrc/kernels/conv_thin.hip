@@ -1,12 +1,13 @@
 // Thin-channel direct convolution for gfx950: 3x3 (pad 1) or 1x1 (pad 0) convs, stride 1 or 2,
 // over at most 32 input and 64 output channels (the first layers of YOLOv8n and the MobileNet
-// stems: 3->16, 16->32, 16->16, 32->32 at 160x160 and above). The implicit-GEMM tiles waste most
+// stems: 3->16, 16->32, 16->16, 32->32 at 160x160 and above), and 7x7 pad-3 convs over at most 4
+// input channels (the ResNet stem, 3->64 at stride 2). The implicit-GEMM tiles waste most
 // of a 32-row MFMA tile and a whole LDS stage per workgroup on such layers, and the tiles are too
 // short to overlap one workgroup's load latency with another's stores, so they run at ~0.1-0.25
 // of HBM. Here:
 //   * MFMA v_mfma_f32_16x16x32_f16 (M = 16 output channels, N = 16 output pixels of one row,
 //     K = 32 values of (tap, channel)), so a 16-channel conv wastes nothing; the whole reduction
-//     of one output channel block is at most 20 fragments held in registers (the weights are
+//     of the output channel blocks is at most 28 fragments held in registers (the weights are
 //     loaded once per workgroup);
 //   * one persistent workgroup per CU slot walks work items of 4 output rows x 64 columns; the
 //     input band of the next item (rows (4-1)*S + K, 64*S + 4 columns, every channel slot) is
@@ -26,9 +27,9 @@ namespace vkhip {
         template <int K, int S>
         struct Band {
             static constexpr int PAD  = K / 2;
-            static constexpr int COFF = K == 3 ? 2 : 0;                   // band column of input column ox0*S (even start)
+            static constexpr int COFF = (PAD + 1) & ~1;                     // band column of input column ox0*S (even start, >= PAD)
             static constexpr int ROWS = (OR - 1) * S + K;
-            static constexpr int COLS = ((OCW - 1) * S + K + (K == 3 ? 1 : 0) + 1) & ~1; // even: whole pixel pairs
+            static constexpr int COLS = ((OCW - 1) * S + K + (COFF - PAD) + 1) & ~1; // even: whole pixel pairs
             static constexpr int PPR  = COLS / 2;                           // pixel pairs per band row
         };
     } // namespace thin
@@ -44,7 +45,7 @@ namespace vkhip {
         constexpr int NBW    = (NI + 3) / 4;               // copies per wave (the surplus ones copy zeros)
         constexpr int BAND   = NBW * 4 * 1024;             // LDS bytes of one band buffer
         static_assert(2 * BAND <= 160 * 1024, "band double buffer fits LDS");
-        static_assert(MT * NSTEPS <= 20, "weights fit the register budget");
+        static_assert(MT * NSTEPS <= 28, "weights fit the register budget");
         __shared__ __attribute__((aligned(16))) unsigned char sm[2 * BAND];
 
         const int lane = threadIdx.x & 63;
@@ -182,6 +183,9 @@ namespace vkhip {
         if constexpr (MT_ * ((9 * CB * 4 + 31) / 32) <= 20) {
             if (k == 3 && s == 1) return conv_thin_kernel<CB, MT_, 3, 1>;
             if (k == 3 && s == 2) return conv_thin_kernel<CB, MT_, 3, 2>;
+        }
+        if constexpr (CB == 1) {
+            if (k == 7 && s == 2) return conv_thin_kernel<CB, MT_, 7, 2>;
         }
         if (k == 1 && s == 1) return conv_thin_kernel<CB, MT_, 1, 1>;
         return nullptr;
