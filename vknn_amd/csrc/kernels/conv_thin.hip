@@ -10,10 +10,10 @@
 //     of the output channel blocks is at most 28 fragments held in registers (the weights are
 //     loaded once per workgroup);
 //   * one persistent workgroup per CU slot walks work items of 4 output rows x 64 columns; the
-//     input band of the next item (rows (4-1)*S + K, 64*S + 4 columns, every channel slot) is
-//     copied global->LDS by buffer-load-to-LDS while the current item computes from the other
-//     half of a double buffer, and the current item's stores are issued after those copies, so
-//     the next wait never waits for them;
+//     input bands of the next NBUF-1 items (rows (4-1)*S + K, 64*S + K + 1 columns, every channel
+//     slot) are copied global->LDS by buffer-load-to-LDS while the current item computes from
+//     another buffer of an NBUF-deep ring, and the current item's stores are issued after those
+//     copies, so a wait for a band never waits for the stores issued after it;
 //   * the accumulator layout of the 16x16 MFMA (lane l: pixel l%16, channels 4(l/16)..+3) is one
 //     NC4HW4 slot of one pixel, so every store is one 8-byte write of 4 channels.
 // Reference semantics: ConvCpu (src/backend/cpu/ops/conv.cpp:9-92) — bias, activation, fp16 store.
@@ -34,7 +34,14 @@ namespace vkhip {
         };
     } // namespace thin
 
-    template <int CINB, int MT, int K, int S>
+    // LDS bytes of one band buffer of the thin kernel
+    template <int CINB, int K, int S>
+    constexpr int thin_band_bytes() {
+        using B = thin::Band<K, S>;
+        return ((CINB * B::ROWS * B::PPR + 63) / 64 + 3) / 4 * 4 * 1024;
+    }
+
+    template <int CINB, int MT, int K, int S, int NBUF>
     __global__ __launch_bounds__(256, 2) void conv_thin_kernel(GemmArgs a) {
         using B = thin::Band<K, S>;
         constexpr int OR = thin::OR, OCW = thin::OCW;
@@ -44,9 +51,10 @@ namespace vkhip {
         constexpr int NI     = (TP + 63) / 64;             // 1 KB copies of one band
         constexpr int NBW    = (NI + 3) / 4;               // copies per wave (the surplus ones copy zeros)
         constexpr int BAND   = NBW * 4 * 1024;             // LDS bytes of one band buffer
-        static_assert(2 * BAND <= 160 * 1024, "band double buffer fits LDS");
+        static_assert(BAND == thin_band_bytes<CINB, K, S>() && (NBUF == 2 || NBUF == 3), "band ring");
+        static_assert(NBUF * BAND <= 160 * 1024, "band ring fits LDS");
         static_assert(MT * NSTEPS <= 28, "weights fit the register budget");
-        __shared__ __attribute__((aligned(16))) unsigned char sm[2 * BAND];
+        __shared__ __attribute__((aligned(16))) unsigned char sm[NBUF * BAND];
 
         const int lane = threadIdx.x & 63;
         const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -162,32 +170,62 @@ namespace vkhip {
         // stores per wave per item: every (pixel tile, fragment) store is issued, out-of-range ones
         // with an offset the buffer drops, so the count is fixed
         constexpr int kStores = (OCW / 16) * MT;
-        static_assert(kStores <= 63, "stores fit the counter");
+        static_assert((NBUF - 1) * kStores + NBW <= 63, "stores and copies in flight fit the counter");
+        // vmcnt(n) with n a compile-time constant (the counter retires in issue order)
+        auto wait_for = [](auto n_c) __attribute__((always_inline)) {
+            constexpr int n = decltype(n_c)::value;
+            __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
+        };
+        using std::integral_constant;
+        const int G = gridDim.x;
         int it = blockIdx.x, buf = 0;
-        if (it < items) issue_band(it, 0);
-        for (bool first = true; it < items; it += gridDim.x, first = false) {
-            // this item's band was issued before the previous item's stores: wait until at most those
-            // stores remain outstanding (the counter retires in issue order)
-            if (first) __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
-            else __builtin_amdgcn_s_waitcnt((kStores & 15) | (7 << 4) | (15 << 8) | ((kStores >> 4) << 14));
-            __asm__ volatile("s_barrier" ::: "memory"); // all copies of the band landed; the other buffer is free
-            const int nxt = it + gridDim.x;
-            if (nxt < items) issue_band(nxt, buf ^ 1);
+#pragma unroll
+        for (int d = 0; d < NBUF - 1; ++d)
+            if (it + d * G < items) issue_band(it + d * G, d);
+        for (int k = 0; it < items; it += G, ++k) {
+            // Wait for this item's band. Issued after it, and allowed to stay in flight: the stores
+            // of the (at most NBUF - 1) items computed since, and the band of the next item when
+            // NBUF = 3 and that item exists.
+            const bool more = NBUF == 3 && it + G < items;
+            if constexpr (NBUF == 2) {
+                if (k == 0) wait_for(integral_constant<int, 0> {});
+                else wait_for(integral_constant<int, kStores> {});
+            } else {
+                if (k == 0) {
+                    if (more) wait_for(integral_constant<int, NBW> {});
+                    else wait_for(integral_constant<int, 0> {});
+                } else if (k == 1) {
+                    if (more) wait_for(integral_constant<int, NBW + kStores> {});
+                    else wait_for(integral_constant<int, kStores> {});
+                } else {
+                    if (more) wait_for(integral_constant<int, NBW + 2 * kStores> {});
+                    else wait_for(integral_constant<int, 2 * kStores> {});
+                }
+            }
+            __asm__ volatile("s_barrier" ::: "memory"); // all copies of the band landed; the oldest buffer is free
+            const int nxt = it + (NBUF - 1) * G;
+            if (nxt < items) issue_band(nxt, buf == 0 ? NBUF - 1 : buf - 1);
             compute_store(it, buf);
-            buf ^= 1;
+            buf = buf + 1 == NBUF ? 0 : buf + 1;
         }
+    }
+
+    // ring depth: three bands (two items ahead) when they leave room for two workgroups per CU
+    template <int CB, int K, int S>
+    constexpr int thin_nbuf() {
+        return 3 * thin_band_bytes<CB, K, S>() <= 80 * 1024 ? 3 : 2;
     }
 
     template <int CB, int MT_>
     static GemmKernelFn thin_pick_ks(int k, int s) {
         if constexpr (MT_ * ((9 * CB * 4 + 31) / 32) <= 20) {
-            if (k == 3 && s == 1) return conv_thin_kernel<CB, MT_, 3, 1>;
-            if (k == 3 && s == 2) return conv_thin_kernel<CB, MT_, 3, 2>;
+            if (k == 3 && s == 1) return conv_thin_kernel<CB, MT_, 3, 1, thin_nbuf<CB, 3, 1>()>;
+            if (k == 3 && s == 2) return conv_thin_kernel<CB, MT_, 3, 2, thin_nbuf<CB, 3, 2>()>;
         }
         if constexpr (CB == 1) {
-            if (k == 7 && s == 2) return conv_thin_kernel<CB, MT_, 7, 2>;
+            if (k == 7 && s == 2) return conv_thin_kernel<CB, MT_, 7, 2, thin_nbuf<CB, 7, 2>()>;
         }
-        if (k == 1 && s == 1) return conv_thin_kernel<CB, MT_, 1, 1>;
+        if (k == 1 && s == 1) return conv_thin_kernel<CB, MT_, 1, 1, thin_nbuf<CB, 1, 1>()>;
         return nullptr;
     }
     template <int CB>
