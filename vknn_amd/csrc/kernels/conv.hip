@@ -434,6 +434,9 @@ namespace vkhip {
         const long long yb    = ((long long) p * a.OH + oy0) * OW + ox;
         const int       c     = cb * 4;
         float4v         psum  = {0.f, 0.f, 0.f, 0.f}; // this column's share of the plane sum (pool)
+        // uniform conditions, tested once: a channel count that is not a multiple of 4 (padding
+        // channels of the last block are stored as zeros) and the pool sums
+        const bool ragged = (a.C & 3) != 0, pooled = a.pool != nullptr;
         auto finish = [&](auto act_c) __attribute__((always_inline)) {
             constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
@@ -445,13 +448,22 @@ namespace vkhip {
                 v.y = apply_act(v.y, ACT, a.lo, a.hi);
                 v.z = apply_act(v.z, ACT, a.lo, a.hi);
                 v.w = apply_act(v.w, ACT, a.lo, a.hi);
-                if (c + 0 >= a.C) v.x = 0.f;
-                if (c + 1 >= a.C) v.y = 0.f;
-                if (c + 2 >= a.C) v.z = 0.f;
-                if (c + 3 >= a.C) v.w = 0.f;
+                if (ragged) {
+                    if (c + 0 >= a.C) v.x = 0.f;
+                    if (c + 1 >= a.C) v.y = 0.f;
+                    if (c + 2 >= a.C) v.z = 0.f;
+                    if (c + 3 >= a.C) v.w = 0.f;
+                }
                 const half4 h = f4_to_h4(v);
                 a.y[yb + (long long) r * OW] = h4_as_u2(h);
-                psum += h4_to_f4(h);
+                if (pooled) {
+                    // fp16 value x 1 + fp32 sum: one mixed-precision fma per channel, the same
+                    // single rounding as converting and adding
+                    psum.x = __builtin_fmaf((float) h.x, 1.f, psum.x);
+                    psum.y = __builtin_fmaf((float) h.y, 1.f, psum.y);
+                    psum.z = __builtin_fmaf((float) h.z, 1.f, psum.z);
+                    psum.w = __builtin_fmaf((float) h.w, 1.f, psum.w);
+                }
             }
         };
         switch (a.act) {
