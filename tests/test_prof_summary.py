@@ -32,6 +32,7 @@ def _rows(steps):
             for j, name in enumerate(kern):
                 add(name, [4000, 1000, 2500, 500][k] if j == 0 else 300)
         add("unpack_kernel", 200)
+        add("unpack_quad_kernel", 160)  # a second boundary unpack after the last operator (not conv_2's or flat_3's)
     return rows
 
 
@@ -65,6 +66,8 @@ def test_layers_join(tmp_path):
     # measured bytes: one dispatch 1000 KiB x2 + 500 KiB x1; conv_2 has two dispatches
     assert float(c0[13]) == pytest.approx(2.56) and float(c2[13]) == pytest.approx(5.12)
     assert f3[13] == "0.00"
+    # the boundary conversions (500 + 200 + 160 ns per step) are reported apart from the operators
+    assert "7.8 us of operator kernels, and 0.9 us of the segment's boundary conversions" in out
 
 
 def test_layers_rejects_unmarked_trace(tmp_path):

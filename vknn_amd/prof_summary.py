@@ -216,7 +216,8 @@ def cmd_traffic(a):
 
 PEAK_TFLOPS, PEAK_GBS = 2500.0, 8000.0
 RIDGE = PEAK_TFLOPS * 1e12 / (PEAK_GBS * 1e9)
-BOUNDARY = ("pack_kernel", "pack4_kernel", "unpack_kernel", "boundary_convert")
+# the segment's boundary conversions (fp32 NCHW <-> NC4HW4 fp16), which belong to no operator
+BOUNDARY = ("pack_kernel", "pack4_kernel", "unpack", "boundary_convert")
 
 
 def read_plan(path):
@@ -228,8 +229,9 @@ def read_plan(path):
     return ops
 
 
-def marker_groups(rows, steps, n_ops):
-    """Per timed step, the dispatch rows of each operator (cut at the markers)."""
+def marker_groups(rows, steps, n_ops, boundary=None):
+    """Per timed step, the dispatch rows of each operator (cut at the markers); the boundary
+    conversions of each step go to `boundary` (a list) if given."""
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     starts = [i for i, r in enumerate(rows) if family(r["Kernel_Name"]).startswith(("pack_kernel", "pack4_kernel"))]
     if len(starts) < steps:
@@ -242,7 +244,10 @@ def marker_groups(rows, steps, n_ops):
             f = family(r["Kernel_Name"])
             if f.startswith("dispatch_marker"):
                 groups.append([])
-            elif groups and not f.startswith(BOUNDARY):
+            elif f.startswith(BOUNDARY):
+                if boundary is not None:
+                    boundary.append(r)
+            elif groups:
                 groups[-1].append(r)
         if len(groups) != n_ops:
             raise SystemExit(f"step {s_i}: {len(groups)} marker groups for {n_ops} plan lines (run with VKNN_HIP_OP_MARKERS=1)")
@@ -262,7 +267,8 @@ def counters_by_dispatch(path, counter):
 
 def cmd_layers(a):
     ops = read_plan(a.plan)
-    steps = marker_groups(list(csv.DictReader(open(a.trace))), a.steps, len(ops))
+    bnd = []
+    steps = marker_groups(list(csv.DictReader(open(a.trace))), a.steps, len(ops), bnd)
     measured = None
     if a.fetch and a.write:
         fv, frows = counters_by_dispatch(a.fetch, "FETCH_SIZE")
@@ -313,7 +319,9 @@ def cmd_layers(a):
             line += f" {(rd + wr) / 1e6:.2f} | " + (f"{(rd + wr) / op['bytes']:.2f} |" if op["bytes"] else "- |")
         print(line)
     mf, hb = tot["mfma"], tot["hbm"]
-    print(f"\nPer step: {all_us:.1f} us of operator kernels.")
+    bnd_us = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in bnd) / a.steps / 1e3
+    print(f"\nPer step: {all_us:.1f} us of operator kernels, and {bnd_us:.1f} us of the segment's boundary conversions "
+          f"(input pack, output unpack; in no operator row).")
     if mf[1]:
         print(f"MFMA-bound operators: {mf[0] / 1e9:.1f} GFLOP in {mf[1]:.1f} us = {mf[0] / (mf[1] * 1e-6) / 1e12:.1f} TFLOP/s, "
               f"{mf[0] / (mf[1] * 1e-6) / 1e12 / PEAK_TFLOPS:.3f} of peak.")
