@@ -361,7 +361,9 @@ int vkhip_concat_channels(const void *const *xs, const int64_t *cs, int32_t coun
                           vkhip_stream_t s);
 /* Channel slice [c0, c0+C) of x (Cx channels) into y (C channels). */
 int vkhip_slice_channels(const void *x, void *y, int64_t N, int64_t Cx, int64_t c0, int64_t C, int64_t HW, vkhip_stream_t s);
-/* Nearest-neighbour resize (ONNX asymmetric/floor): y[oy,ox] = x[floor(oy*H/OH), floor(ox*W/OW)]. */
+/* Nearest-neighbour resize: y[oy,ox] = x[floor(oy*H/OH), floor(ox*W/OW)]. For integer upscale
+ * factors this is the reference's nearest (round_prefer_floor, src/backend/cpu/ops/resize.cpp:30-87)
+ * under half_pixel and pytorch_half_pixel coordinates, and under asymmetric ones up to 2x. */
 int vkhip_resize_nearest(const void *x, void *y, int64_t N, int64_t C, int64_t H, int64_t W, int64_t OH, int64_t OW,
                          vkhip_stream_t s);
 /* vkhip_resize_nearest over views (plane strides per image; 0 = dense). */

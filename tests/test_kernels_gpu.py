@@ -1015,6 +1015,30 @@ def test_fc(gpu, N, K, M, act):
         assert not raw[:, M:].any()
 
 
+@pytest.mark.parametrize("shape", [(2, 13, 5, 7, 10, 14), (1, 8, 4, 6, 12, 6), (3, 4, 6, 5, 6, 15), (16, 256, 20, 20, 40, 40),
+                                   (1, 4, 3, 300, 6, 600), (2, 6, 5, 5, 7, 9), (2, 64, 1, 1, 3, 2)])
+def test_resize_nearest_factors(gpu, shape):
+    """Nearest resize: integer factors (2x2 with odd and even widths, 3x1, 1x3, the detector-neck
+    2x at 20x20, a 1x1 image) on the division-free kernel, a width above 256 and a non-integer
+    factor on the generic one. Integer factors: bit-equal to the oracle's nearest under half_pixel
+    coordinates (and under asymmetric ones at 2x); every shape: bit-equal to floor indexing."""
+    lib, o = V.vkhip(), oracle()
+    N, C, H, W, OH, OW = shape
+    x = round_half(rng(120 + H + W).standard_normal((N, C, H, W)))
+    dx = to_device_nc4(x)
+    dy = DeviceBuffer(V.nc4_elems(N, C, OH, OW) * 2)
+    check(lib.vkhip_resize_nearest(dx.ptr, dy.ptr, N, C, H, W, OH, OW, None))
+    got = from_device_nc4(dy, (N, C, OH, OW))
+    iy, ix = (np.arange(OH) * H) // OH, (np.arange(OW) * W) // OW
+    assert np.array_equal(got, x[:, :, iy][:, :, :, ix])
+    if OH % H == 0 and OW % W == 0:
+        modes = [0] + ([2] if max(OH // H, OW // W) <= 2 else [])
+        for mode in modes:
+            want = np.zeros((N, C, OH, OW), np.float32)
+            o.oracle_resize_nearest(np.ascontiguousarray(x).ctypes.data, want.ctypes.data, N * C, H, W, OH, OW, mode)
+            assert np.array_equal(got, want), mode
+
+
 def test_concat_slice_resize(gpu):
     lib = V.vkhip()
     o = oracle()

@@ -853,14 +853,28 @@ namespace vknn {
             }
         };
 
+        // The resize kernel reads x[floor(d / s)] for an integer upscale s. The reference's nearest
+        // rule (round_prefer_floor of the source coordinate, cpu/ops/resize.cpp:30-87) gives the same
+        // index under half_pixel and pytorch_half_pixel coordinates ((d + 0.5) / s - 0.5 stays within
+        // 0.5 - 0.5/s of floor(d / s)), under asymmetric ones only up to s = 2 (d / s = k + 2/3 rounds
+        // up at s = 3), and under align_corners only for s = 1.
+        static bool resizeFloorExact(const Node &nd, int64_t h, int64_t w, int64_t oh, int64_t ow) {
+            if (nd.attr.gets("mode", "nearest") != "nearest" || h <= 0 || w <= 0 || oh % h || ow % w) return false;
+            const std::string c = nd.attr.gets("coordinate_transformation_mode", "half_pixel");
+            const int64_t     s = std::max(oh / h, ow / w);
+            if (c == "half_pixel" || c == "pytorch_half_pixel") return true;
+            if (c == "asymmetric") return s <= 2;
+            return s == 1;
+        }
+
         struct ResizeOp: HipOp {
             TensorId in, out;
             NCHW     x, y;
             void prepare(const Node &node, SegEnv &env) override {
                 in = node.inputs[0]; out = node.outputs[0];
                 x = NCHW::from(env.graph->desc(in).shape); y = NCHW::from(env.graph->desc(out).shape);
-                if (node.attr.gets("mode", "nearest") != "nearest") throw Error(Status::Unsupported, "Resize: only nearest");
-                if (y.n != x.n || y.c != x.c || y.h % x.h || y.w % x.w) throw Error(Status::Unsupported, "Resize: only integer spatial upscales");
+                if (!resizeFloorExact(node, x.h, x.w, y.h, y.w))
+                    throw Error(Status::Unsupported, "Resize: only nearest integer upscales whose source index is floor(d / factor)");
                 kind = "resize";
                 bytes = (int64_t) (nc4Bytes(env.graph->desc(in).shape) + nc4Bytes(env.graph->desc(out).shape));
             }
@@ -2104,8 +2118,7 @@ namespace vknn {
                 case OpType::Split: return g.desc(nd.inputs[0]).shape.size() == 4 && (nd.attr.geti("axis", 0) == 1 || nd.attr.geti("axis", 0) == -3);
                 case OpType::Resize: {
                     const Shape &i = g.desc(nd.inputs[0]).shape, &o = g.desc(nd.outputs[0]).shape;
-                    return nd.attr.gets("mode", "nearest") == "nearest" && i.size() == 4 && o.size() == 4 && i[0] == o[0] && i[1] == o[1] &&
-                           o[2] % i[2] == 0 && o[3] % i[3] == 0;
+                    return i.size() == 4 && o.size() == 4 && i[0] == o[0] && i[1] == o[1] && resizeFloorExact(nd, i[2], i[3], o[2], o[3]);
                 }
                 default: return true;
             }

@@ -401,6 +401,31 @@ namespace vkhip {
         y[((n * yps + cb) * OH + oy) * OW + ox] = x[((n * xps + cb) * H + iy) * W + ix];
     }
 
+    // Nearest upsampling by integer factors (OH = SH * H, OW = SW * W: the 2x upsample of a detector
+    // neck): a block covers R = 256 / W input rows (at least one) of one plane (blockIdx.y), each
+    // thread one input pixel, which it reads once and writes SH x SW times (the SW copies of a row
+    // as one store when SW is 2 and the rows are 16-byte aligned). No per-element division: the
+    // generic kernel above spends most of its time in 64-bit index divisions.
+    template <int SW2>
+    __global__ __launch_bounds__(256) void resize_int_kernel(const uint2 *x, uint2 *y, int H, int W, int SH, int SW, int R, int Cb,
+                                                              int64_t xps, int64_t yps) {
+        const int p  = blockIdx.y;
+        const int n  = p / Cb, cb = p - n * Cb;
+        const int r  = threadIdx.x / W, ix = threadIdx.x - r * W;
+        const int iy = blockIdx.x * R + r;
+        if (r >= R || iy >= H) return;
+        const uint2 v   = x[((int64_t) n * xps + cb) * H * W + (int64_t) iy * W + ix];
+        const int   OW  = W * SW;
+        uint2      *row = y + ((int64_t) n * yps + cb) * H * SH * OW + (int64_t) iy * SH * OW;
+        for (int k = 0; k < SH; ++k) {
+            if constexpr (SW2) {
+                *reinterpret_cast<uint4 *>(row + (int64_t) k * OW + 2 * ix) = uint4 {v.x, v.y, v.x, v.y};
+            } else {
+                for (int c = 0; c < SW; ++c) row[(int64_t) k * OW + ix * SW + c] = v;
+            }
+        }
+    }
+
     // y = act(a + b) over one image per blockIdx.y: `per` contiguous halves of each image, the
     // images `aps` / `bps` / `yps` halves apart (views of wider tensors)
     __global__ void add_view_kernel(const half_t *a, int64_t aps, const half_t *b, int64_t bps, half_t *y, int64_t yps, int64_t per, int act,
@@ -624,6 +649,17 @@ int vkhip_resize_nearest_view(const void *x, int64_t x_pstride, void *y, int64_t
     if (!x || !y || N <= 0 || C <= 0 || H <= 0 || W <= 0 || OH <= 0 || OW <= 0) return set_error(VKHIP_ERR_INVALID, "resize: bad arguments");
     const int64_t Cb = ceil_div(C, 4), xps = x_pstride > 0 ? x_pstride : Cb, yps = y_pstride > 0 ? y_pstride : Cb;
     if (xps < Cb || yps < Cb) return set_error(VKHIP_ERR_INVALID, "resize: plane stride below the channel blocks");
+    if (OH % H == 0 && OW % W == 0 && W <= 256 && N * Cb <= 65535 && N * yps * OH * OW < (1LL << 40)) {
+        // integer factors: one input pixel per thread, no index divisions
+        const int R  = (int) std::max<int64_t>(1, 256 / W);
+        const int SH = (int) (OH / H), SW = (int) (OW / W);
+        dim3      grid((unsigned) ceil_div(H, R), (unsigned) (N * Cb));
+        // the 2-wide store needs 16-byte aligned output rows and planes (OW and OH * OW even)
+        if (SW == 2 && OW % 2 == 0 && ((uintptr_t) y & 15) == 0)
+            resize_int_kernel<1><<<grid, 256, 0, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, (int) H, (int) W, SH, SW, R, (int) Cb, xps, yps);
+        else resize_int_kernel<0><<<grid, 256, 0, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, (int) H, (int) W, SH, SW, R, (int) Cb, xps, yps);
+        return check_launch("resize_int");
+    }
     int64_t total = N * Cb * OH * OW;
     resize_nearest_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, H, W, OH, OW, total, Cb, xps, yps);
     return check_launch("resize_nearest");
