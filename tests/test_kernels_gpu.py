@@ -970,6 +970,32 @@ def test_maxpool(gpu):
         assert np.array_equal(got, ref), f"maxpool k{k}"  # max of fp16 values is exact
 
 
+@pytest.mark.parametrize("shape,k", [((16, 128, 20, 20), 5), ((2, 9, 17, 23), 3), ((1, 6, 1, 30), 5), ((3, 4, 40, 56), 5), ((1, 8, 10, 62), 3),
+                                     ((1, 4, 8, 70), 5), ((2, 12, 3, 3), 5)])
+def test_maxpool_same(gpu, shape, k):
+    """"Same" max pools (KxK, stride 1, pad K/2; the SPPF pools) on the LDS plane kernel: exact
+    against the oracle, widths above 64 columns, windows larger than the image; then written into
+    a channel slice of a wider tensor through vkhip_maxpool_view (the in-place concat of SPPF)."""
+    lib = V.vkhip()
+    N, C, H, W = shape
+    x = round_half(rng(95 + H + W + k).standard_normal(shape) * 3)
+    p = k // 2
+    d = V.PoolDesc(N=N, C=C, H=H, W=W, OH=H, OW=W, KH=k, KW=k, SH=1, SW=1, PT=p, PL=p)
+    dx = to_device_nc4(x)
+    dy = DeviceBuffer(V.nc4_elems(N, C, H, W) * 2)
+    check(lib.vkhip_maxpool(ctypes.byref(d), dx.ptr, dy.ptr, None))
+    ref = np.zeros((N, C, H, W), np.float32)
+    oracle().oracle_maxpool(x.ctypes.data, ref.ctypes.data, N, C, H, W, k, k, 1, 1, p, p, H, W)
+    assert np.array_equal(from_device_nc4(dy, (N, C, H, W)), ref)
+    if C % 4 == 0:
+        Ct = 2 * C
+        dw = DeviceBuffer(V.nc4_elems(N, Ct, H, W) * 2)
+        dw.zero()
+        check(lib.vkhip_maxpool_view(ctypes.byref(d), dx.ptr, 0, dw.ptr + (C // 4) * H * W * 8, Ct // 4, None))
+        wide = from_device_nc4(dw, (N, Ct, H, W))
+        assert np.array_equal(wide[:, C:], ref) and not wide[:, :C].any()
+
+
 @pytest.mark.parametrize("shape,pb", [((2, 9, 18, 18), 1), ((1, 8, 16, 20), 1), ((3, 5, 15, 20), 0), ((2, 4, 15, 12), 1),
                                       ((1, 64, 112, 112), 1), ((2, 7, 2, 2), 1), ((1, 4, 1, 6), 1)])
 def test_maxpool_3x3_s2_pairs(gpu, shape, pb):

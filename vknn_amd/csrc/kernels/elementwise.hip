@@ -401,6 +401,52 @@ namespace vkhip {
         y[((n * yps + cb) * OH + oy) * OW + ox] = x[((n * xps + cb) * H + iy) * W + ix];
     }
 
+    // Max pool with a KxK window, stride 1 and pad K/2 (output size = input size: the SPPF pools
+    // of a detector neck) over small planes: one workgroup per 4-channel plane copies the plane into
+    // LDS with a -inf halo, takes the maxima of K-wide row windows into a second LDS image, then of
+    // K-high column windows of that (2K instead of K*K maxima per output), on packed fp16 pairs
+    // (the max of fp16 values is exact in any width). Threads are (column, row group): 64 x 4.
+    __device__ __forceinline__ uint2 max_u2(uint2 a, uint2 b) {
+        const half2v x0 = __builtin_elementwise_max(__builtin_bit_cast(half2v, a.x), __builtin_bit_cast(half2v, b.x));
+        const half2v x1 = __builtin_elementwise_max(__builtin_bit_cast(half2v, a.y), __builtin_bit_cast(half2v, b.y));
+        return uint2 {__builtin_bit_cast(unsigned, x0), __builtin_bit_cast(unsigned, x1)};
+    }
+    template <int K>
+    __global__ __launch_bounds__(256) void maxpool_same_kernel(const uint2 *x, uint2 *y, int H, int W, int Cb, int xps, int yps) {
+        extern __shared__ uint2 pool_sm[];
+        constexpr int P  = K / 2;
+        const int     RW = W + K - 1, RH = H + K - 1;
+        uint2        *tin = pool_sm, *trow = pool_sm + RH * RW; // [RH][RW] input with halo; [RH][W] row maxima
+        const int     p = blockIdx.x, n = p / Cb, cb = p - n * Cb;
+        const int     tx = threadIdx.x, ty = threadIdx.y;
+        const uint2  *src = x + ((int64_t) n * xps + cb) * H * W;
+        const uint2   ninf = {0xFC00FC00u, 0xFC00FC00u};
+        for (int r = ty; r < RH; r += 4) {
+            const int iy = r - P;
+            for (int c = tx; c < RW; c += 64) {
+                const int ix = c - P;
+                tin[r * RW + c] = (iy >= 0 && iy < H && ix >= 0 && ix < W) ? src[iy * W + ix] : ninf;
+            }
+        }
+        __syncthreads();
+        for (int r = ty; r < RH; r += 4)
+            for (int c = tx; c < W; c += 64) {
+                uint2 m = tin[r * RW + c];
+#pragma unroll
+                for (int k = 1; k < K; ++k) m = max_u2(m, tin[r * RW + c + k]);
+                trow[r * W + c] = m;
+            }
+        __syncthreads();
+        uint2 *dst = y + ((int64_t) n * yps + cb) * H * W;
+        for (int r = ty; r < H; r += 4)
+            for (int c = tx; c < W; c += 64) {
+                uint2 m = trow[r * W + c];
+#pragma unroll
+                for (int k = 1; k < K; ++k) m = max_u2(m, trow[(r + k) * W + c]);
+                dst[r * W + c] = m;
+            }
+    }
+
     // Nearest upsampling by integer factors (OH = SH * H, OW = SW * W: the 2x upsample of a detector
     // neck): a block covers R = 256 / W input rows (at least one) of one plane (blockIdx.y), each
     // thread one input pixel, which it reads once and writes SH x SW times (the SW copies of a row
@@ -592,6 +638,18 @@ static int maxpool_impl(const vkhip_pool_desc *d, const void *x, int64_t xps_, v
         else
             maxpool3s2_kernel<int64_t><<<grid1(tq), 256, 0, resolve_stream(s)>>>((const uint4 *) x, y2, (uint2 *) y, d->H, d->W / 2, d->OH, d->OW, OHq, OWq, tq);
         return check_launch("maxpool");
+    }
+    // "same" pools (KxK, stride 1, pad K/2, K = 3 or 5) over planes that fit LDS twice
+    const int K = d->KH;
+    if (K == d->KW && (K == 3 || K == 5) && d->SH == 1 && d->SW == 1 && d->PT == K / 2 && d->PL == K / 2 && d->OH == d->H &&
+        d->OW == d->W && (int64_t) d->N * Cb <= INT32_MAX && (int64_t) d->N * std::max(xps, yps) * d->H * d->W < INT32_MAX) {
+        const size_t sm = (size_t) (d->H + K - 1) * (2 * d->W + K - 1) * 8;
+        if (sm <= 64 * 1024) {
+            const dim3 grid((unsigned) (d->N * Cb)), block(64, 4);
+            if (K == 3) maxpool_same_kernel<3><<<grid, block, sm, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, (int) d->H, (int) d->W, Cb, xps, yps);
+            else maxpool_same_kernel<5><<<grid, block, sm, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, (int) d->H, (int) d->W, Cb, xps, yps);
+            return check_launch("maxpool_same");
+        }
     }
     int64_t total = (int64_t) d->N * ceil_div(d->C, 4) * d->OH * d->OW;
     if ((int64_t) d->N * std::max(xps, yps) * std::max(d->H * d->W, d->OH * d->OW) < INT32_MAX)
