@@ -40,6 +40,7 @@ def make_input(shape, seed, uniform=False):
     ("resnet_tiny", 2, "tuning=off;graphs=0"),
     ("resnet_tiny", 3, "VKNN_HIP_REFINE=0"),
     ("yolo_tiny", 2, "VKNN_HIP_REFINE=0"),
+    ("mnv3_tiny", 2, "VKNN_HIP_FOLD_ACT=0"),
 ])
 def test_tiny_models(gpu, monkeypatch, model, batch, opts):
     if opts.startswith("VKNN_"):  # an environment switch of the backend, not a session option

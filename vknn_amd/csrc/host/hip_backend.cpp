@@ -119,6 +119,12 @@ namespace vknn {
             // its own output never exists in memory.
             TensorId                poolOut = kNoTensor;
             vkhip_pool_desc         pd {};
+            // Set by the segment before prepare when the hard-sigmoid that is this conv's only reader
+            // is folded into its epilogue (the squeeze-excite gate after the second FC): the conv
+            // writes `actOut` with activation `foldAct` (lo, hi) instead of its own output.
+            TensorId                actOut = kNoTensor;
+            int                     foldAct = 0;
+            float                   foldLo = 0.f, foldHi = 0.f;
             // Set by the segment after prepare when the global average pool of a squeeze-excite
             // that reads this depthwise conv's output is folded into it: the conv also writes the
             // per-(plane, row tile) sums of its output into `gapPart` (gapR partials per plane).
@@ -143,7 +149,7 @@ namespace vknn {
                 const Graph &g = *env.graph;
                 cacheWeights   = env.config->cachesWeights() && !env.config->cacheFile.empty();
                 in             = scaledIn != kNoTensor ? scaledIn : node.inputs[0];
-                out            = node.outputs[0];
+                out            = actOut != kNoTensor ? actOut : node.outputs[0];
                 res            = node.fusedResidual;
                 NCHW         x  = NCHW::from(g.desc(in).shape);
                 NCHW         y  = NCHW::from(g.desc(out).shape);
@@ -157,6 +163,7 @@ namespace vknn {
                 d.PT = (int) pad[0]; d.PL = (int) pad[1]; d.DH = (int) dil[0]; d.DW = (int) dil[1];
                 d.group = (int) node.attr.geti("group", 1);
                 d.act = (int) node.fusedAct; d.act_lo = node.actLo; d.act_hi = node.actHi;
+                if (actOut != kNoTensor) d.act = foldAct, d.act_lo = foldLo, d.act_hi = foldHi;
                 d.has_res = res != kNoTensor;
                 d.in_scale = xscale != kNoTensor;
                 kind  = d.group > 1 ? "dwconv" : "conv";
@@ -1153,6 +1160,40 @@ namespace vknn {
         // input scale, so h*s is never written (the reference runs the Mul as its own Binary op,
         // ops/binary.cpp:32-43; the product is rounded to fp16 exactly as that op's store does).
         // Returns conv node -> (h, s) and the set of folded Mul nodes.
+        // Activation folds: a HardSigmoid unary whose input is the output of a 1x1 stride-1 dense conv
+        // of this segment with no activation of its own, read by nothing else, runs in that conv's
+        // epilogue (the squeeze-excite gate after its second FC when the SE is not fused): the conv
+        // writes the unary's output with VKHIP_ACT_HARDSIGMOID (lo = alpha, hi = beta, computed on
+        // the fp32 sum, where the separate unary reads the conv's fp16 output).
+        static void planActFolds(const Graph &g, const std::vector<int> &idx, const std::set<int> &skip, std::map<int, int> &convOf) {
+            std::set<int>           inSeg(idx.begin(), idx.end());
+            std::map<TensorId, int> readers, producer;
+            for (size_t i = 0; i < g.nodes.size(); ++i) {
+                const Node &nd = g.nodes[i];
+                for (TensorId t: nd.inputs)
+                    if (t != kNoTensor) ++readers[t];
+                if (nd.fusedResidual != kNoTensor) ++readers[nd.fusedResidual];
+                for (TensorId t: nd.outputs)
+                    if (t != kNoTensor) producer[t] = (int) i;
+            }
+            for (TensorId t: g.outputs) readers[t] += 1000; // a graph output is never folded away
+            for (int u: idx) {
+                const Node &un = g.nodes[u];
+                if (un.type != OpType::Unary || (UnaryType) un.subOp != UnaryType::HardSigmoid || un.inputs.empty() || un.outputs.empty()) continue;
+                const TensorId t = un.inputs[0];
+                auto           pit = producer.find(t);
+                if (pit == producer.end() || !inSeg.count(pit->second) || skip.count(pit->second) || readers[t] != 1) continue;
+                const Node &c = g.nodes[pit->second];
+                if (c.type != OpType::Conv || c.fusedAct != ActType::None || c.inputs.size() < 2 || !g.isInitializer(c.inputs[1])) continue;
+                const Shape &w = g.desc(c.inputs[1]).shape;
+                auto st = attrInts(c, "strides", {1, 1}), pad = attrInts(c, "pads", {0, 0, 0, 0});
+                if (w.size() != 4 || w[2] != 1 || w[3] != 1 || c.attr.geti("group", 1) != 1 || st[0] != 1 || st[1] != 1 || pad[0] || pad[1] ||
+                    pad[2] || pad[3])
+                    continue;
+                convOf[u] = pit->second;
+            }
+        }
+
         static void planScaleFolds(const Graph &g, const std::vector<int> &idx, std::map<int, std::pair<TensorId, TensorId>> &conv,
                                    std::set<int> &muls) {
             std::set<int>           inSeg(idx.begin(), idx.end());
@@ -1367,6 +1408,31 @@ namespace vknn {
                     }
                 }
             }
+            // Hard-sigmoid folds into the producing conv (planActFolds); VKNN_HIP_FOLD_ACT=0 keeps the
+            // unary launches (A/B).
+            std::map<int, int> actFold; // HardSigmoid node -> conv node
+            std::map<int, int> actConv; // conv node -> HardSigmoid node
+            {
+                const char *act_env = std::getenv("VKNN_HIP_FOLD_ACT");
+                if (!act_env || std::string(act_env) != "0") {
+                    std::set<int> skip(folded.begin(), folded.end());
+                    for (auto &kv: scaled) skip.insert(kv.first);
+                    for (auto &kv: convPool) skip.insert(kv.first), skip.insert(kv.second);
+                    for (auto &kv: gapConv) skip.insert(kv.second);
+                    for (auto &kv: pwPairs) skip.insert(kv.first);
+                    skip.insert(pwFolded.begin(), pwFolded.end());
+                    skip.insert(pwChained.begin(), pwChained.end());
+                    planActFolds(g, idx, skip, actFold);
+                    for (auto it = actFold.begin(); it != actFold.end();) {
+                        // a conv that writes or reads a view keeps its own output
+                        const Node &c = g.nodes[it->second];
+                        if (pstride(c.inputs[0]) > 0 || pstride(g.nodes[it->first].outputs[0]) > 0 || place_.count(resolve(c.outputs[0])))
+                            it = actFold.erase(it);
+                        else ++it;
+                    }
+                    for (auto &kv: actFold) actConv[kv.second] = kv.first;
+                }
+            }
             // Device buffers: one NC4HW4 fp16 buffer per activation (aliases share their source's;
             // a tensor placed in another one by planViews has none of its own).
             for (int i: idx) {
@@ -1408,6 +1474,11 @@ namespace vknn {
                     f->into = foldedInto[i];
                     if (pools.count(i)) f->what = "max pool";
                     op      = std::move(f);
+                } else if (actFold.count(i)) {
+                    auto f  = std::make_unique<FoldedMulOp>();
+                    f->what = "hard-sigmoid";
+                    f->into = g.nodes[actFold[i]].name;
+                    op      = std::move(f);
                 } else if (pwFolded.count(i)) {
                     auto f = std::make_unique<FoldedMulOp>();
                     f->what = "3x3 conv: runs with the 1x1 conv that reads it,";
@@ -1432,6 +1503,15 @@ namespace vknn {
                     auto *c     = static_cast<ConvOp *>(op.get());
                     c->scaledIn = sit->second.first;
                     c->xscale   = sit->second.second;
+                }
+                auto ait = actConv.find(i);
+                if (ait != actConv.end()) {
+                    auto       *c  = static_cast<ConvOp *>(op.get());
+                    const Node &un = g.nodes[ait->second];
+                    c->actOut      = un.outputs[0];
+                    c->foldAct     = VKHIP_ACT_HARDSIGMOID;
+                    c->foldLo      = un.actLo;
+                    c->foldHi      = un.actHi;
                 }
                 auto pit = convPool.find(i);
                 if (pit != convPool.end()) {
@@ -1485,7 +1565,7 @@ namespace vknn {
                     outs.push_back(out);
                     continue;
                 }
-                if (folded.count(i) || pools.count(i) || pwFolded.count(i) || pwChained.count(i)) {
+                if (folded.count(i) || pools.count(i) || pwFolded.count(i) || pwChained.count(i) || actFold.count(i)) {
                     ins.push_back(in);
                     outs.push_back(out);
                     continue;
@@ -1511,6 +1591,7 @@ namespace vknn {
                     }
                     if (nd.fusedResidual != kNoTensor) in.push_back(resolve(nd.fusedResidual));
                     if (pit != convPool.end()) out.push_back(resolve(g.nodes[pit->second].outputs[0]));
+                    else if (ait != actConv.end()) out.push_back(resolve(g.nodes[ait->second].outputs[0]));
                     else
                         for (TensorId t: nd.outputs)
                             if (t != kNoTensor) out.push_back(resolve(t));

@@ -562,6 +562,7 @@ namespace vkhip {
                 case VKHIP_ACT_CLIP: finish(std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
                 case VKHIP_ACT_HARDSWISH: finish(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
                 case VKHIP_ACT_SILU: finish(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
+                case VKHIP_ACT_HARDSIGMOID: finish(std::integral_constant<int, VKHIP_ACT_HARDSIGMOID> {}); break;
                 default: finish(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
             }
         }
@@ -706,6 +707,7 @@ namespace vkhip {
                 case VKHIP_ACT_CLIP: finish(mode_c, std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
                 case VKHIP_ACT_HARDSWISH: finish(mode_c, std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
                 case VKHIP_ACT_SILU: finish(mode_c, std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
+                case VKHIP_ACT_HARDSIGMOID: finish(mode_c, std::integral_constant<int, VKHIP_ACT_HARDSIGMOID> {}); break;
                 default: finish(mode_c, std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
             }
         };
@@ -1018,6 +1020,7 @@ namespace vkhip {
             case VKHIP_ACT_CLIP: finish(std::integral_constant<int, VKHIP_ACT_CLIP> {}); break;
             case VKHIP_ACT_HARDSWISH: finish(std::integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
             case VKHIP_ACT_SILU: finish(std::integral_constant<int, VKHIP_ACT_SILU> {}); break;
+            case VKHIP_ACT_HARDSIGMOID: finish(std::integral_constant<int, VKHIP_ACT_HARDSIGMOID> {}); break;
             default: finish(std::integral_constant<int, VKHIP_ACT_NONE> {}); break;
         }
         __syncthreads();
@@ -1427,6 +1430,7 @@ namespace vkhip {
                 case VKHIP_ACT_CLIP: store_tile(t, bias_lds, integral_constant<int, VKHIP_ACT_CLIP> {}); break;
                 case VKHIP_ACT_HARDSWISH: store_tile(t, bias_lds, integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
                 case VKHIP_ACT_SILU: store_tile(t, bias_lds, integral_constant<int, VKHIP_ACT_SILU> {}); break;
+                case VKHIP_ACT_HARDSIGMOID: store_tile(t, bias_lds, integral_constant<int, VKHIP_ACT_HARDSIGMOID> {}); break;
                 default: store_tile(t, bias_lds, integral_constant<int, VKHIP_ACT_NONE> {}); break;
             }
         };

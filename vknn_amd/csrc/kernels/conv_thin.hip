@@ -163,6 +163,7 @@ namespace vkhip {
                 case VKHIP_ACT_CLIP: finish(it, buf, integral_constant<int, VKHIP_ACT_CLIP> {}); break;
                 case VKHIP_ACT_HARDSWISH: finish(it, buf, integral_constant<int, VKHIP_ACT_HARDSWISH> {}); break;
                 case VKHIP_ACT_SILU: finish(it, buf, integral_constant<int, VKHIP_ACT_SILU> {}); break;
+                case VKHIP_ACT_HARDSIGMOID: finish(it, buf, integral_constant<int, VKHIP_ACT_HARDSIGMOID> {}); break;
                 default: finish(it, buf, integral_constant<int, VKHIP_ACT_NONE> {}); break;
             }
         };
