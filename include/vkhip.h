@@ -136,7 +136,11 @@ typedef struct vkhip_conv_desc {
     int32_t group;
     int32_t act;
     float   act_lo, act_hi;
-    int32_t has_res; /* residual tensor of the output's shape is added before the activation */
+    int32_t has_res; /* 1: a residual tensor of the output's shape is added before the activation
+                      * (the reference's fused residual, FuseResidualAdd); 2: after it, y = act(conv
+                      * + bias) + res (a standalone Add after an activated conv, e.g. the YOLOv8
+                      * bottleneck shortcut; GEMM / split-K plans, not Winograd, depthwise or the
+                      * stem tiles) */
     int32_t in_scale; /* 1: the input is first multiplied by a per-(image, input channel) scale
                        * (vkhip_conv_forward_scaled; dense 1x1 stride-1 pad-0 convs only) */
 } vkhip_conv_desc;
@@ -232,6 +236,14 @@ int vkhip_conv_forward_pooled(const vkhip_conv_desc *d, const vkhip_conv_plan *p
  * the reference, whose Concat and Split copy (ops/concat.cpp, ops/split.cpp). */
 int vkhip_conv_forward_view(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, int64_t x_pstride, const void *blob,
                             void *y, int64_t y_pstride, void *workspace, vkhip_stream_t s);
+
+/* vkhip_conv_forward_view for a conv with a residual (has_res 1 or 2): `res` is read with y's
+ * layout, i.e. `y_pstride` channel blocks per image (a slice of the same concat as y, as in a
+ * YOLOv8 C2f block, or a dense tensor when y is dense). The reference has no view entry points:
+ * its Add (src/backend/cpu/ops/add.cpp) after the conv and its in-place concat are what this
+ * call replaces. */
+int vkhip_conv_forward_view_res(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, int64_t x_pstride, const void *blob,
+                                const void *res, void *y, int64_t y_pstride, void *workspace, vkhip_stream_t s);
 
 int vkhip_conv_forward_noalloc(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob,
                                const void *res, void *y, vkhip_stream_t s);

@@ -48,9 +48,10 @@ def conv_desc(x_shape, w_shape, stride=(1, 1), pads=(0, 0, 0, 0), dil=(1, 1), gr
 
 
 def gpu_conv(x, w, b=None, stride=(1, 1), pads=(0, 0, 0, 0), dil=(1, 1), group=1, act=0, lo=0.0, hi=0.0, res=None,
-             algo=V.CONV_AUTO, tile=-1, ksplit=0):
+             algo=V.CONV_AUTO, tile=-1, ksplit=0, res_post=False):
+    """res_post: the residual is added after the activation (has_res 2) instead of before it."""
     lib = V.vkhip()
-    d, yshape = conv_desc(x.shape, w.shape, stride, pads, dil, group, act, lo, hi, int(res is not None))
+    d, yshape = conv_desc(x.shape, w.shape, stride, pads, dil, group, act, lo, hi, (2 if res_post else 1) if res is not None else 0)
     plan = V.ConvPlan()
     check(lib.vkhip_conv_plan_make(ctypes.byref(d), algo, tile, ksplit, ctypes.byref(plan)), "plan")
     blob = np.zeros(plan.weight_bytes, np.uint8)

@@ -215,11 +215,11 @@ def test_conv_thin(gpu, shape, act):
 
 
 def test_conv_thin_refuses_other_shapes(gpu):
-    """Thin tiles refuse residuals, odd input widths, 5x5, dilation, grouped convs, too many
+    """Thin tiles refuse residuals except on 3x3 stride 1, odd input widths, 5x5, dilation, grouped convs, too many
     channels and split-K / Winograd plans."""
     lib = V.vkhip()
     plan = V.ConvPlan()
-    bad = [dict(x=(1, 16, 8, 8), w=(16, 16, 3, 3), pads=(1, 1, 1, 1), has_res=1), dict(x=(1, 16, 8, 9), w=(16, 16, 3, 3), pads=(1, 1, 1, 1)),
+    bad = [dict(x=(1, 16, 8, 8), w=(16, 16, 1, 1), pads=(0, 0, 0, 0), has_res=1), dict(x=(1, 16, 8, 9), w=(16, 16, 3, 3), pads=(1, 1, 1, 1)),
            dict(x=(1, 16, 8, 8), w=(16, 16, 5, 5), pads=(2, 2, 2, 2)), dict(x=(1, 16, 8, 8), w=(16, 16, 3, 3), pads=(2, 2, 2, 2), dil=(2, 2)),
            dict(x=(1, 40, 8, 8), w=(16, 40, 3, 3), pads=(1, 1, 1, 1)), dict(x=(1, 16, 8, 8), w=(80, 16, 3, 3), pads=(1, 1, 1, 1))]
     for c in bad:
@@ -230,6 +230,92 @@ def test_conv_thin_refuses_other_shapes(gpu):
     assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, 43, 0, ctypes.byref(plan)) == 0
     assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_SPLITK, 43, 2, ctypes.byref(plan)) != 0
     assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_WINOGRAD, 43, 0, ctypes.byref(plan)) != 0
+
+
+# (algo, tile, ksplit, kernel size): one or two tiles of every kernel family that takes a residual
+RES_POST_CASES = [(V.CONV_GEMM, t, 0, 3) for t in (0, 3, 8, 10, 26, 33, 43, 44, 45)] + \
+                 [(V.CONV_GEMM, t, 0, 1) for t in (14, 24, 38, 47)] + \
+                 [(V.CONV_SPLITK, 3, 2, 3), (V.CONV_SPLITK_LAST, 26, 2, 3)]
+
+
+@pytest.mark.parametrize("has_res", [1, 2])
+@pytest.mark.parametrize("case", RES_POST_CASES)
+def test_conv_residual_after_activation(gpu, case, has_res):
+    """has_res 2: y = act(conv + bias) + res (a conv followed by a standalone Add, the YOLOv8
+    bottleneck shortcut), against the oracle conv then the oracle's fp16 add; has_res 1 (residual
+    before the activation) on the same tiles, which covers the thin kernel's residual path. Ragged
+    output channels, column blocks cut by the image edge."""
+    algo, tile, ks, k = case
+    r = rng(1300 + tile * 3 + k + has_res)
+    N, C, H, W, Cout = (2, 32, 11, 36, 40) if k == 3 else (3, 64, 10, 12, 70)
+    if tile in THIN_TILES:
+        Cout = {43: 16, 44: 28, 45: 60}[tile]
+        C = 16 if tile == 45 else C  # 64 outputs over 32 inputs exceed the weight register budget
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w = (r.standard_normal((Cout, C, k, k)) * np.sqrt(2.0 / (k * k * C))).astype(np.float32)
+    b = (r.standard_normal(Cout) * 0.1).astype(np.float32)
+    p = k // 2
+    res = round_half(r.standard_normal((N, Cout, H, W)))
+    d, _ = conv_desc(x.shape, w.shape, (1, 1), (p,) * 4, act=5, has_res=has_res)
+    plan = V.ConvPlan()
+    check(V.vkhip().vkhip_conv_plan_make(ctypes.byref(d), algo, tile, ks, ctypes.byref(plan)), f"plan {case}")
+    if has_res == 2:
+        ref = round_half(oracle_conv(x, w, b, (1, 1), (p,) * 4, act=5)) + res
+        got, plan, _ = gpu_conv(x, w, b, (1, 1), (p,) * 4, act=5, res=res, algo=algo, tile=tile, ksplit=ks, res_post=True)
+    else:
+        ref = oracle_conv(x, w, b, (1, 1), (p,) * 4, res=res, act=5)
+        got, plan, _ = gpu_conv(x, w, b, (1, 1), (p,) * 4, act=5, res=res, algo=algo, tile=tile, ksplit=ks)
+    assert plan.algo == algo and plan.tile == tile
+    assert_parity(got, ref, f"residual mode {has_res} algo {algo} tile {tile}")
+
+
+def test_conv_residual_after_activation_refusals(gpu):
+    """Winograd, depthwise and stem plans have no residual-after-activation epilogue; has_res
+    outside 0..2 is an error."""
+    lib = V.vkhip()
+    plan = V.ConvPlan()
+    d, _ = conv_desc((1, 64, 14, 14), (64, 64, 3, 3), pads=(1, 1, 1, 1), act=5, has_res=2)
+    assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_WINOGRAD, -1, 0, ctypes.byref(plan)) != 0
+    d, _ = conv_desc((1, 16, 14, 14), (16, 1, 3, 3), pads=(1, 1, 1, 1), group=16, act=5, has_res=2)
+    assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_DEPTHWISE, -1, 0, ctypes.byref(plan)) != 0
+    d, _ = conv_desc((1, 3, 32, 32), (16, 3, 3, 3), pads=(1, 1, 1, 1), act=5, has_res=2)
+    for t in STEM_TILES:
+        assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, t, 0, ctypes.byref(plan)) != 0
+    d, _ = conv_desc((1, 16, 8, 8), (16, 16, 3, 3), pads=(1, 1, 1, 1), has_res=3)
+    assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, 43, 0, ctypes.byref(plan)) != 0
+
+
+@pytest.mark.parametrize("tile", [43, 33, 3])
+def test_conv_view_residual(gpu, tile):
+    """vkhip_conv_forward_view_res as in a YOLOv8 C2f block: the residual is one channel slice of a
+    wide tensor and the output another slice of the same tensor (both at its plane stride), the
+    input a third slice; y = SiLU(conv(x)) + res. The other slices stay untouched."""
+    lib = V.vkhip()
+    r = rng(1400 + tile)
+    N, H, W, C = 2, 12, 40, 16
+    wide = round_half(r.standard_normal((N, 4 * C, H, W)))  # slices: [x | res | y | spare]
+    x, res = wide[:, 0:C], wide[:, C:2 * C]
+    w = (r.standard_normal((C, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+    b = (r.standard_normal(C) * 0.1).astype(np.float32)
+    d, _ = conv_desc(x.shape, w.shape, (1, 1), (1, 1, 1, 1), act=5, has_res=2)
+    plan = V.ConvPlan()
+    check(lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, tile, 0, ctypes.byref(plan)), "plan")
+    blob = np.zeros(plan.weight_bytes, np.uint8)
+    check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(plan), w.ctypes.data, b.ctypes.data, blob.ctypes.data), "pack")
+    dblob, dwide = DeviceBuffer.from_array(blob), to_device_nc4(wide)
+    ws = DeviceBuffer(plan.workspace_bytes) if plan.workspace_bytes else None
+    plane = H * W * 8  # bytes of one 4-channel plane
+    cb, ps = C // 4, 4 * C // 4
+    check(lib.vkhip_conv_forward_view_res(ctypes.byref(d), ctypes.byref(plan), dwide.ptr, ps, dblob.ptr, dwide.ptr + cb * plane,
+                                          dwide.ptr + 2 * cb * plane, ps, ws.ptr if ws else None, None), "forward_view_res")
+    check(lib.vkhip_stream_sync(None), "sync")
+    out = from_device_nc4(dwide, wide.shape)
+    ref = round_half(oracle_conv(x, w, b, (1, 1), (1, 1, 1, 1), act=5)) + res
+    assert_parity(out[:, 2 * C:3 * C], ref, f"view residual tile {tile}")
+    for sl in (slice(0, C), slice(C, 2 * C), slice(3 * C, 4 * C)):
+        assert np.array_equal(out[:, sl], wide[:, sl])
+    # the plain view entry refuses a residual descriptor
+    assert lib.vkhip_conv_forward_view(ctypes.byref(d), ctypes.byref(plan), dwide.ptr, ps, dblob.ptr, dwide.ptr, ps, None, None) != 0
 
 
 @pytest.mark.parametrize("tile", PERS_TILES)

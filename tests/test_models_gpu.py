@@ -41,6 +41,7 @@ def make_input(shape, seed, uniform=False):
     ("resnet_tiny", 3, "VKNN_HIP_REFINE=0"),
     ("yolo_tiny", 2, "VKNN_HIP_REFINE=0"),
     ("mnv3_tiny", 2, "VKNN_HIP_FOLD_ACT=0"),
+    ("yolo_tiny", 2, "VKNN_HIP_FOLD_ADD=0"),
 ])
 def test_tiny_models(gpu, monkeypatch, model, batch, opts):
     if opts.startswith("VKNN_"):  # an environment switch of the backend, not a session option
@@ -165,6 +166,22 @@ def test_se_scale_folded_into_projection(gpu, opts, monkeypatch):
     plain = V.Session("mobilenetv3_large", 2, seed=7, options=opts)
     assert "+input scale" not in plain.describe()
     check_outputs(got, plain.run(x), sess.out_elems, f"config3 b2 folded vs unfolded[{opts}]")
+
+
+def test_bottleneck_add_folded_into_conv(gpu, monkeypatch):
+    """The six YOLOv8n bottleneck shortcuts (an Add after an activated 3x3 conv, writing a slice of
+    the C2f concat) run inside that conv's epilogue as a residual after the activation: no add
+    launch, the same result as the oracle and as the unfolded session."""
+    sess = V.Session("yolov8n", 1, seed=7)
+    plan = sess.describe()
+    assert plan.count("add (a residual after the activation) folded into") == 6, plan
+    x = make_input(sess.in_shape, 6)
+    got = sess.run(x)
+    check_outputs(got, oracle_model_run("yolov8n", 1, 7, x), sess.out_elems, "config4 b1 add folded")
+    monkeypatch.setenv("VKNN_HIP_FOLD_ADD", "0")
+    plain = V.Session("yolov8n", 1, seed=7)
+    assert "residual after the activation" not in plain.describe()
+    check_outputs(got, plain.run(x), sess.out_elems, "config4 b1 add folded vs unfolded")
 
 
 @pytest.mark.parametrize("opts", ["", "fuse_se=1;fuse_dwpw=1"])

@@ -113,6 +113,7 @@ VKHIP_API = {
     "vkhip_conv_forward_scaled": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     "vkhip_conv_pool_parts": (c_int, [P(ConvDesc), P(ConvPlan)]),
     "vkhip_conv_forward_view": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp]),
+    "vkhip_conv_forward_view_res": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp]),
     "vkhip_add_view": (c_int, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64, c_i32, c_f, c_f, c_vp]),
     "vkhip_maxpool_view": (c_int, [P(PoolDesc), c_vp, c_i64, c_vp, c_i64, c_vp]),
     "vkhip_resize_nearest_view": (c_int, [c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp]),

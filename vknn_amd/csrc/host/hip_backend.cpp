@@ -125,6 +125,11 @@ namespace vknn {
             TensorId                actOut = kNoTensor;
             int                     foldAct = 0;
             float                   foldLo = 0.f, foldHi = 0.f;
+            // Set by the segment before prepare when the Add that is this conv's only reader (the
+            // conv already applies its own activation) is folded into its epilogue: the conv writes
+            // the Add's output `addOut` = act(conv + bias) + `postRes` (a residual after the
+            // activation, has_res 2).
+            TensorId                addOut = kNoTensor, postRes = kNoTensor;
             // Set by the segment after prepare when the global average pool of a squeeze-excite
             // that reads this depthwise conv's output is folded into it: the conv also writes the
             // per-(plane, row tile) sums of its output into `gapPart` (gapR partials per plane).
@@ -149,8 +154,8 @@ namespace vknn {
                 const Graph &g = *env.graph;
                 cacheWeights   = env.config->cachesWeights() && !env.config->cacheFile.empty();
                 in             = scaledIn != kNoTensor ? scaledIn : node.inputs[0];
-                out            = actOut != kNoTensor ? actOut : node.outputs[0];
-                res            = node.fusedResidual;
+                out            = actOut != kNoTensor ? actOut : addOut != kNoTensor ? addOut : node.outputs[0];
+                res            = postRes != kNoTensor ? postRes : node.fusedResidual;
                 NCHW         x  = NCHW::from(g.desc(in).shape);
                 NCHW         y  = NCHW::from(g.desc(out).shape);
                 const Shape &ws_ = g.desc(node.inputs[1]).shape;
@@ -164,7 +169,7 @@ namespace vknn {
                 d.group = (int) node.attr.geti("group", 1);
                 d.act = (int) node.fusedAct; d.act_lo = node.actLo; d.act_hi = node.actHi;
                 if (actOut != kNoTensor) d.act = foldAct, d.act_lo = foldLo, d.act_hi = foldHi;
-                d.has_res = res != kNoTensor;
+                d.has_res = postRes != kNoTensor ? 2 : res != kNoTensor ? 1 : 0;
                 d.in_scale = xscale != kNoTensor;
                 kind  = d.group > 1 ? "dwconv" : "conv";
                 flops = 2.0 * d.N * d.Cout * (double) (d.Cin / d.group) * d.KH * d.KW * d.OH * d.OW;
@@ -454,8 +459,14 @@ namespace vknn {
                     return;
                 }
                 if (viewIO) {
-                    check(vkhip_conv_forward_view(&d, &plan, env.dev(in), env.pstride(in), blob->ptr, env.dev(out), env.pstride(out), ws ? ws->ptr : nullptr, s),
-                          "conv " + name);
+                    if (res != kNoTensor)
+                        check(vkhip_conv_forward_view_res(&d, &plan, env.dev(in), env.pstride(in), blob->ptr, env.dev(res), env.dev(out), env.pstride(out),
+                                                          ws ? ws->ptr : nullptr, s),
+                              "conv " + name);
+                    else
+                        check(vkhip_conv_forward_view(&d, &plan, env.dev(in), env.pstride(in), blob->ptr, env.dev(out), env.pstride(out),
+                                                      ws ? ws->ptr : nullptr, s),
+                              "conv " + name);
                     return;
                 }
                 check(forward(plan, env.dev(in), xscale != kNoTensor ? env.dev(xscale) : nullptr, blob->ptr,
@@ -1194,6 +1205,47 @@ namespace vknn {
             }
         }
 
+        // Adds that fold into the conv producing one operand as a residual after its activation
+        // (y = act(conv + bias) + r, the YOLOv8 bottleneck shortcut): an Add without activation of
+        // two same-shape tensors, one written by a dense conv of this segment that nothing else
+        // reads; the other operand r is produced before that conv in the segment order (or comes
+        // from outside the segment), so it exists when the conv runs. Views are checked by the
+        // caller. convOf: Add node -> conv node.
+        static void planResFolds(const Graph &g, const std::vector<int> &idx, const std::set<int> &skip, std::map<int, std::pair<int, TensorId>> &convOf) {
+            std::map<int, int>      pos;
+            for (size_t k = 0; k < idx.size(); ++k) pos[idx[k]] = (int) k;
+            std::map<TensorId, int> readers, producer;
+            for (size_t i = 0; i < g.nodes.size(); ++i) {
+                const Node &nd = g.nodes[i];
+                for (TensorId t: nd.inputs)
+                    if (t != kNoTensor) ++readers[t];
+                if (nd.fusedResidual != kNoTensor) ++readers[nd.fusedResidual];
+                for (TensorId t: nd.outputs)
+                    if (t != kNoTensor) producer[t] = (int) i;
+            }
+            for (TensorId t: g.outputs) readers[t] += 1000; // a graph output is never folded away
+            std::set<int> taken;
+            for (int u: idx) {
+                const Node &ad = g.nodes[u];
+                if (ad.type != OpType::Add || ad.inputs.size() != 2 || ad.outputs.empty() || ad.fusedAct != ActType::None || skip.count(u)) continue;
+                if (ad.inputs[0] == ad.inputs[1] || g.desc(ad.inputs[0]).shape != g.desc(ad.inputs[1]).shape || g.desc(ad.inputs[0]).shape.size() != 4) continue;
+                for (int e = 0; e < 2; ++e) {
+                    const TensorId t = ad.inputs[e], r = ad.inputs[1 - e];
+                    auto           pit = producer.find(t);
+                    if (pit == producer.end() || !pos.count(pit->second) || skip.count(pit->second) || taken.count(pit->second) || readers[t] != 1) continue;
+                    const Node &c = g.nodes[pit->second];
+                    if (c.type != OpType::Conv || c.fusedResidual != kNoTensor || c.attr.geti("group", 1) != 1 || c.inputs.size() < 2 ||
+                        !g.isInitializer(c.inputs[1]) || g.desc(c.inputs[1]).shape.size() != 4 || r == c.inputs[0])
+                        continue;
+                    auto rp = producer.find(r);
+                    if (rp != producer.end() && pos.count(rp->second) && pos[rp->second] >= pos[pit->second]) continue;
+                    convOf[u] = {pit->second, r};
+                    taken.insert(pit->second);
+                    break;
+                }
+            }
+        }
+
         static void planScaleFolds(const Graph &g, const std::vector<int> &idx, std::map<int, std::pair<TensorId, TensorId>> &conv,
                                    std::set<int> &muls) {
             std::set<int>           inSeg(idx.begin(), idx.end());
@@ -1433,6 +1485,35 @@ namespace vknn {
                     for (auto &kv: actFold) actConv[kv.second] = kv.first;
                 }
             }
+            // Adds after an activated conv fold into its epilogue (planResFolds); VKNN_HIP_FOLD_ADD=0
+            // keeps the add launches (A/B).
+            std::map<int, std::pair<int, TensorId>> addFold; // Add node -> (conv node, residual)
+            std::map<int, int>                      addConv; // conv node -> Add node
+            {
+                const char *add_env = std::getenv("VKNN_HIP_FOLD_ADD");
+                if (!add_env || std::string(add_env) != "0") {
+                    std::set<int> skip(folded.begin(), folded.end());
+                    for (auto &kv: scaled) skip.insert(kv.first);
+                    for (auto &kv: convPool) skip.insert(kv.first), skip.insert(kv.second);
+                    for (auto &kv: gapConv) skip.insert(kv.second);
+                    for (auto &kv: pwPairs) skip.insert(kv.first);
+                    skip.insert(pwFolded.begin(), pwFolded.end());
+                    skip.insert(pwChained.begin(), pwChained.end());
+                    for (auto &kv: actConv) skip.insert(kv.first);
+                    for (int i: idx)
+                        if (viewCats_.count(i) || viewSplits_.count(i)) skip.insert(i);
+                    planResFolds(g, idx, skip, addFold);
+                    // the residual is read at the output's plane stride: both dense, or both slices
+                    // of tensors with the same channel blocks per image
+                    auto eff = [&](TensorId t) { return pstride(t) > 0 ? pstride(t) : (g.desc(t).shape[1] + 3) / 4; };
+                    for (auto it = addFold.begin(); it != addFold.end();) {
+                        const TensorId o = g.nodes[it->first].outputs[0], r = it->second.second;
+                        if (eff(o) != eff(r) || (pstride(o) > 0) != (pstride(r) > 0)) it = addFold.erase(it);
+                        else ++it;
+                    }
+                    for (auto &kv: addFold) addConv[kv.second.first] = kv.first;
+                }
+            }
             // Device buffers: one NC4HW4 fp16 buffer per activation (aliases share their source's;
             // a tensor placed in another one by planViews has none of its own).
             for (int i: idx) {
@@ -1479,6 +1560,11 @@ namespace vknn {
                     f->what = "hard-sigmoid";
                     f->into = g.nodes[actFold[i]].name;
                     op      = std::move(f);
+                } else if (addFold.count(i)) {
+                    auto f  = std::make_unique<FoldedMulOp>();
+                    f->what = "add (a residual after the activation)";
+                    f->into = g.nodes[addFold[i].first].name;
+                    op      = std::move(f);
                 } else if (pwFolded.count(i)) {
                     auto f = std::make_unique<FoldedMulOp>();
                     f->what = "3x3 conv: runs with the 1x1 conv that reads it,";
@@ -1513,6 +1599,12 @@ namespace vknn {
                     c->foldLo      = un.actLo;
                     c->foldHi      = un.actHi;
                 }
+                auto dit = addConv.find(i);
+                if (dit != addConv.end()) {
+                    auto *c    = static_cast<ConvOp *>(op.get());
+                    c->addOut  = g.nodes[dit->second].outputs[0];
+                    c->postRes = addFold[dit->second].second;
+                }
                 auto pit = convPool.find(i);
                 if (pit != convPool.end()) {
                     auto       *c  = static_cast<ConvOp *>(op.get());
@@ -1529,6 +1621,7 @@ namespace vknn {
                 if (nd.type == OpType::Conv && !inPlace && !gapFolded && !folded.count(i) && !pools.count(i) && !pwOp) {
                     bool v = false;
                     for (TensorId t: {nd.inputs[0], nd.outputs[0]}) v = v || pstride(t) > 0;
+                    if (dit != addConv.end()) v = v || pstride(g.nodes[dit->second].outputs[0]) > 0;
                     static_cast<ConvOp *>(op.get())->viewIO = v;
                 }
                 if (!gapFolded) op->prepare(nd, env_);
@@ -1565,7 +1658,7 @@ namespace vknn {
                     outs.push_back(out);
                     continue;
                 }
-                if (folded.count(i) || pools.count(i) || pwFolded.count(i) || pwChained.count(i) || actFold.count(i)) {
+                if (folded.count(i) || pools.count(i) || pwFolded.count(i) || pwChained.count(i) || actFold.count(i) || addFold.count(i)) {
                     ins.push_back(in);
                     outs.push_back(out);
                     continue;
@@ -1590,8 +1683,10 @@ namespace vknn {
                         if (t != kNoTensor && !g.isInitializer(t)) in.push_back(resolve(t));
                     }
                     if (nd.fusedResidual != kNoTensor) in.push_back(resolve(nd.fusedResidual));
+                    if (dit != addConv.end()) in.push_back(resolve(addFold[dit->second].second));
                     if (pit != convPool.end()) out.push_back(resolve(g.nodes[pit->second].outputs[0]));
                     else if (ait != actConv.end()) out.push_back(resolve(g.nodes[ait->second].outputs[0]));
+                    else if (dit != addConv.end()) out.push_back(resolve(g.nodes[dit->second].outputs[0]));
                     else
                         for (TensorId t: nd.outputs)
                             if (t != kNoTensor) out.push_back(resolve(t));

@@ -39,12 +39,15 @@ namespace vkhip {
         float4v v   = *reinterpret_cast<const float4v *>(bias + ocb * 4);
         for (int s = 0; s < ksplit; ++s) v += part[((long long) s * Coutb + ocb) * P + px];
         int       pn = px / OHW, pr = px - pn * OHW;
-        long long yi = ((long long) pn * ypst + ocb) * OHW + pr; // (a residual conv is never a view: ypst == Coutb)
-        if (has_res) v += h4_to_f4(u2_as_h4(res[yi]));
+        long long yi = ((long long) pn * ypst + ocb) * OHW + pr; // the residual shares y's plane stride
+        float4v   r  = {0.f, 0.f, 0.f, 0.f};
+        if (has_res) r = h4_to_f4(u2_as_h4(res[yi]));
+        if (has_res != 2) v += r;
         v.x = apply_act(v.x, act, lo, hi);
         v.y = apply_act(v.y, act, lo, hi);
         v.z = apply_act(v.z, act, lo, hi);
         v.w = apply_act(v.w, act, lo, hi);
+        if (has_res == 2) v += r;
         int oc = ocb * 4;
         if (oc + 0 >= Cout) v.x = 0.f;
         if (oc + 1 >= Cout) v.y = 0.f;
@@ -725,17 +728,17 @@ namespace vkhip {
 
     // conv_thin_kernel: 3x3 pad 1 (stride 1 or 2), 1x1 pad 0 stride 1 or 7x7 pad 3 stride 2 over at most
     // 4 channels; dilation 1, Cin <= 32, Cout
-    // within the tile's BM, even input width (the band copies whole pixel pairs), no residual or
-    // input scale, and an instantiated kernel (its weights fit the register budget)
+    // within the tile's BM, even input width (the band copies whole pixel pairs), no input scale, a
+    // residual only on 3x3 stride 1, and an instantiated kernel (its weights fit the register budget)
     static bool thin_shape_ok(const vkhip_conv_desc *d, const TileCfg &t, int algo) {
         const int K = d->KH, S = d->SH;
-        if (algo != VKHIP_CONV_GEMM || d->group != 1 || d->has_res || d->in_scale || d->Cin > 32 || d->Cout > t.BM) return false;
+        if (algo != VKHIP_CONV_GEMM || d->group != 1 || d->in_scale || d->Cin > 32 || d->Cout > t.BM) return false;
         if (d->KW != K || d->SW != S || d->DH != 1 || d->DW != 1 || d->W % 2) return false;
         if (!((K == 3 && d->PT == 1 && d->PL == 1 && (S == 1 || S == 2)) || (K == 1 && d->PT == 0 && d->PL == 0 && S == 1) ||
               (K == 7 && d->PT == 3 && d->PL == 3 && S == 2 && d->Cin <= 4)))
             return false;
         if (d->OH != (d->H + 2 * d->PT - K) / S + 1 || d->OW != (d->W + 2 * d->PL - K) / S + 1) return false;
-        return thin_kernel_for((int) ceil_div(d->Cin, 4), t.FM, K, S) != nullptr;
+        return thin_kernel_for((int) ceil_div(d->Cin, 4), t.FM, K, S, d->has_res != 0) != nullptr;
     }
 
     static bool wino_eligible(const vkhip_conv_desc *d) {
@@ -930,8 +933,10 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
         (int64_t) d->N * ceil_div(d->Cout, 4) * d->OH * d->OW * 8 >= (1LL << 31) ||
         (int64_t) 16 * d->N * ceil_div(std::max(d->Cin, d->Cout), 4) * ceil_div(d->OH, 2) * ceil_div(d->OW, 2) * 8 >= (1LL << 31))
         return set_error(VKHIP_ERR_INVALID, "conv_plan_make: input tensor >= 2 GiB (split the batch)");
+    if (d->has_res < 0 || d->has_res > 2) return set_error(VKHIP_ERR_INVALID, "conv_plan_make: has_res is 0, 1 or 2");
     std::memset(plan, 0, sizeof(*plan));
     const bool dw = is_depthwise(d);
+    if (dw && d->has_res == 2) return set_error(VKHIP_ERR_UNSUPPORTED, "depthwise conv: no residual after the activation");
     if (dw) {
         if (d->group != d->Cin || d->group != d->Cout)
             return set_error(VKHIP_ERR_UNSUPPORTED, "grouped conv with group=%d (Cin=%d Cout=%d) is not depthwise", d->group, d->Cin, d->Cout);
@@ -984,6 +989,9 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
     if (tile >= kNumTiles) return set_error(VKHIP_ERR_INVALID, "tile index %d out of range", tile);
     if (algo == VKHIP_CONV_SPLITK_LAST && (kTiles[tile].kind > 3 || kTiles[tile].PERS || kTiles[tile].LE))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d has no in-kernel split-K reduction (gather, B-direct, LDS-DMA and halo tiles only)", tile);
+    if (d->has_res == 2 && (wino || kTiles[tile].kind == 4))
+        return set_error(VKHIP_ERR_UNSUPPORTED, "a residual after the activation runs on GEMM / split-K plans of the gather, B-direct, LDS-DMA, "
+                         "halo and thin tiles only");
     if (kTiles[tile].kind == 3 && (wino || !halo_shape_ok(d, kTiles[tile]) || halo_nbi(d, kTiles[tile]) > kHaloMaxNBI[tile]))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a 3x3 stride-1/2 pad-1 conv with Cin %% %d == 0 and a band that fits LDS", tile,
                          16 * kTiles[tile].KK);
@@ -995,7 +1003,7 @@ int vkhip_conv_plan_make(const vkhip_conv_desc *d, int32_t algo, int32_t tile, i
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d needs a dense B operand (1x1 stride 1 with an even pixel count, or Winograd)", tile);
     if (kTiles[tile].kind == 5 && !thin_shape_ok(d, kTiles[tile], algo))
         return set_error(VKHIP_ERR_UNSUPPORTED, "thin tile %d needs a plain GEMM plan of a 3x3 pad-1 or 1x1 conv, stride 1 or 2 (1x1: stride 1), "
-                         "Cin <= 32, Cout <= %d, even input width, no residual", tile, kTiles[tile].BM);
+                         "Cin <= 32, Cout <= %d, even input width, a residual only on 3x3 stride 1", tile, kTiles[tile].BM);
     if (kTiles[tile].LE && (algo != VKHIP_CONV_GEMM || d->in_scale || ((int64_t) d->OH * d->OW) % 2))
         return set_error(VKHIP_ERR_UNSUPPORTED, "tile %d (LDS-staged epilogue) runs plain GEMM plans of an even pixel count per image only", tile);
     if (kTiles[tile].PERS && (algo != VKHIP_CONV_GEMM || d->in_scale))
@@ -1153,9 +1161,13 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
     const int64_t xps = x_pstride > 0 ? x_pstride : cinb, yps = y_pstride > 0 ? y_pstride : coutb;
     const bool    dense = xps == cinb && yps == coutb;
     if (xps < cinb || yps < coutb) return set_error(VKHIP_ERR_INVALID, "conv_forward: plane stride below the channel blocks");
-    if (!dense && (plan->algo == VKHIP_CONV_WINOGRAD || plan->algo == VKHIP_CONV_DEPTHWISE || d->has_res || d->in_scale ||
+    if (!dense && (plan->algo == VKHIP_CONV_WINOGRAD || plan->algo == VKHIP_CONV_DEPTHWISE || d->in_scale ||
                    (plan->tile >= 0 && plan->tile < kNumTiles && kTiles[plan->tile].kind == 4)))
-        return set_error(VKHIP_ERR_UNSUPPORTED, "conv_forward_view: views need a GEMM or split-K plan (not the stem tiles), no residual, no input scale");
+        return set_error(VKHIP_ERR_UNSUPPORTED, "conv_forward_view: views need a GEMM or split-K plan (not the stem tiles), no input scale");
+    if (d->has_res < 0 || d->has_res > 2) return set_error(VKHIP_ERR_INVALID, "conv_forward: has_res is 0, 1 or 2");
+    if (d->has_res == 2 && (plan->algo == VKHIP_CONV_WINOGRAD || plan->algo == VKHIP_CONV_DEPTHWISE ||
+                            (plan->tile >= 0 && plan->tile < kNumTiles && kTiles[plan->tile].kind == 4)))
+        return set_error(VKHIP_ERR_UNSUPPORTED, "conv_forward: a residual after the activation needs a GEMM or split-K plan (not the stem tiles)");
     if ((int64_t) d->N * std::max(xps * d->H * d->W, yps * d->OH * d->OW) * 8 >= (1LL << 31))
         return set_error(VKHIP_ERR_INVALID, "conv_forward: view >= 2 GiB");
     if (d->has_res && !res) return set_error(VKHIP_ERR_INVALID, "conv_forward: has_res without a residual tensor");
@@ -1318,7 +1330,7 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
     a.omode   = OMODE_EPILOGUE;
     a.n_tiles = (int) g.n_tiles;
     if (t.kind == 5) {
-        GemmKernelFn tf = thin_kernel_for((int) g.Cinb, t.FM, d->KH, d->SH);
+        GemmKernelFn tf = thin_kernel_for((int) g.Cinb, t.FM, d->KH, d->SH, d->has_res != 0);
         if (!tf) return set_error(VKHIP_ERR_INVALID, "conv_forward: no thin kernel for this shape");
         const int64_t items = (int64_t) d->N * ceil_div(d->OH, 4) * ceil_div(d->OW, 64);
         // as many workgroups as the device holds at once: the items are short, so concurrency,
@@ -1359,7 +1371,14 @@ int vkhip_conv_forward_stages(const vkhip_conv_desc *d, const vkhip_conv_plan *p
 int vkhip_conv_forward_view(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, int64_t x_pstride, const void *blob, void *y,
                             int64_t y_pstride, void *workspace, vkhip_stream_t s) {
     if (d && d->in_scale) return set_error(VKHIP_ERR_INVALID, "conv_forward_view: no input-scale plans");
+    if (d && d->has_res) return set_error(VKHIP_ERR_INVALID, "conv_forward_view: a residual conv runs vkhip_conv_forward_view_res");
     return conv_forward_impl(d, plan, x, nullptr, blob, nullptr, y, workspace, s, nullptr, x_pstride, y_pstride);
+}
+
+int vkhip_conv_forward_view_res(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, int64_t x_pstride, const void *blob,
+                                const void *res, void *y, int64_t y_pstride, void *workspace, vkhip_stream_t s) {
+    if (d && d->in_scale) return set_error(VKHIP_ERR_INVALID, "conv_forward_view_res: no input-scale plans");
+    return conv_forward_impl(d, plan, x, nullptr, blob, res, y, workspace, s, nullptr, x_pstride, y_pstride);
 }
 
 int vkhip_conv_pool_parts(const vkhip_conv_desc *d, const vkhip_conv_plan *plan) {
@@ -1514,6 +1533,7 @@ namespace vkhip {
         if (d2 && (rc = pw_chain(d2, pt, p3, ch))) return rc;
         if (plan->weight_bytes != (d2 ? ch.bytes : L.bytes)) return set_error(VKHIP_ERR_INVALID, "convpw_forward: plan does not match the descriptor");
         if (d->has_res && !res) return set_error(VKHIP_ERR_INVALID, "convpw_forward: has_res without a residual tensor");
+        if (d->has_res > 1) return set_error(VKHIP_ERR_UNSUPPORTED, "convpw_forward: the residual is added before the activation only");
         const vkhip_conv_desc &c = d->conv;
         const int              nbi = halo_nbi(&c, pt.t);
         PwKernelFn             fn  = pw_tile_kernel(c.Cout, nbi, d2 ? ch.MR : 0, nullptr);

@@ -47,7 +47,7 @@ namespace vkhip {
                                 // column per image when the dense-B kernel needs an even count
         int           act;
         float         lo, hi;
-        int           has_res, omode, m_tiles;
+        int           has_res, omode, m_tiles;         // has_res: 1 residual added before the activation, 2 after it
         int           n_tiles;                         // column tiles (persistent kernels walk m_tiles x n_tiles)
         long long     x_bstride, w_bstride, y_bstride; // batch (blockIdx.z) strides: uint2 / half / uint2
         unsigned      x_bytes;                         // bytes of one batch slice of x (< 2 GiB)
@@ -544,11 +544,13 @@ namespace vkhip {
                             const int oc = m0 + wm0 + i * 32 + qq * 8 + lk * 4;
                             float4v   v  = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
                             v += bia[i][qq];
-                            v += h4_to_f4(__builtin_bit_cast(half4, rv[j][i][qq]));
+                            const float4v r = h4_to_f4(__builtin_bit_cast(half4, rv[j][i][qq]));
+                            if (a.has_res != 2) v += r;
                             v.x = apply_act(v.x, ACT, a.lo, a.hi);
                             v.y = apply_act(v.y, ACT, a.lo, a.hi);
                             v.z = apply_act(v.z, ACT, a.lo, a.hi);
                             v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                            if (a.has_res == 2) v += r;
                             if (oc + 0 >= a.Cout) v.x = 0.f;
                             if (oc + 1 >= a.Cout) v.y = 0.f;
                             if (oc + 2 >= a.Cout) v.z = 0.f;
@@ -679,11 +681,14 @@ namespace vkhip {
                                 continue;
                             }
                             if constexpr (MODE == 2 || MODE == 3) v += bv[i][qq];
-                            if constexpr (MODE == 3) v += h4_to_f4(__builtin_bit_cast(half4, rv[b][jj][i][qq]));
+                            float4v r = {0.f, 0.f, 0.f, 0.f};
+                            if constexpr (MODE == 3) r = h4_to_f4(__builtin_bit_cast(half4, rv[b][jj][i][qq]));
+                            if (MODE == 3 && a.has_res != 2) v += r;
                             v.x = apply_act(v.x, ACT, a.lo, a.hi);
                             v.y = apply_act(v.y, ACT, a.lo, a.hi);
                             v.z = apply_act(v.z, ACT, a.lo, a.hi);
                             v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                            if (MODE == 3 && a.has_res == 2) v += r;
                             if (oc + 0 >= a.Cout) v.x = 0.f;
                             if (oc + 1 >= a.Cout) v.y = 0.f;
                             if (oc + 2 >= a.Cout) v.z = 0.f;
@@ -1001,11 +1006,14 @@ namespace vkhip {
                         u32x2  *e = reinterpret_cast<u32x2 *>(sm + rl * RS + (wn0 + j * 32 + lrow) * 8);
                         float4v v = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
                         v += bv;
-                        if (a.has_res) v += h4_to_f4(__builtin_bit_cast(half4, *e));
+                        float4v r = {0.f, 0.f, 0.f, 0.f};
+                        if (a.has_res) r = h4_to_f4(__builtin_bit_cast(half4, *e));
+                        if (a.has_res != 2) v += r;
                         v.x = apply_act(v.x, ACT, a.lo, a.hi);
                         v.y = apply_act(v.y, ACT, a.lo, a.hi);
                         v.z = apply_act(v.z, ACT, a.lo, a.hi);
                         v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                        if (a.has_res == 2) v += r;
                         if (oc + 0 >= a.Cout) v.x = 0.f;
                         if (oc + 1 >= a.Cout) v.y = 0.f;
                         if (oc + 2 >= a.Cout) v.z = 0.f;
@@ -1409,11 +1417,13 @@ namespace vkhip {
                         const int oc = mw0 + i * 32 + qq * 8 + lk * 4;
                         float4v   v  = {acc[i][j][qq * 4 + 0], acc[i][j][qq * 4 + 1], acc[i][j][qq * 4 + 2], acc[i][j][qq * 4 + 3]};
                         v += bv;
-                        v += h4_to_f4(__builtin_bit_cast(half4, rv[j][i][qq]));
+                        const float4v r = h4_to_f4(__builtin_bit_cast(half4, rv[j][i][qq]));
+                        if (a.has_res != 2) v += r;
                         v.x = apply_act(v.x, ACT, a.lo, a.hi);
                         v.y = apply_act(v.y, ACT, a.lo, a.hi);
                         v.z = apply_act(v.z, ACT, a.lo, a.hi);
                         v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                        if (a.has_res == 2) v += r;
                         if (oc + 0 >= a.Cout) v.x = 0.f;
                         if (oc + 1 >= a.Cout) v.y = 0.f;
                         if (oc + 2 >= a.Cout) v.z = 0.f;
@@ -2188,7 +2198,7 @@ namespace vkhip {
     GemmKernelFn gemm_tile_kernel(int tile, int bmode);
     // conv_thin_kernel for cinb input slots (rounded up to 1, 2, 4 or 8), mt 16-channel output
     // fragments, a k x k kernel and stride s (nullptr if not instantiated)
-    GemmKernelFn thin_kernel_for(int cinb, int mt, int k, int s);
+    GemmKernelFn thin_kernel_for(int cinb, int mt, int k, int s, bool res);
     inline int thin_cinb(int64_t cinb) { return cinb <= 1 ? 1 : cinb <= 2 ? 2 : cinb <= 4 ? 4 : 8; }
     GemmKernelFn bd_tile_kernel(int tile, int bmode);
     GemmKernelFn dma_tile_kernel(int tile, int bmode, int steps, bool xs);

@@ -15,7 +15,11 @@
 //     another buffer of an NBUF-deep ring, and the current item's stores are issued after those
 //     copies, so a wait for a band never waits for the stores issued after it;
 //   * the accumulator layout of the 16x16 MFMA (lane l: pixel l%16, channels 4(l/16)..+3) is one
-//     NC4HW4 slot of one pixel, so every store is one 8-byte write of 4 channels.
+//     NC4HW4 slot of one pixel, so every store is one 8-byte write of 4 channels;
+//   * RES (3x3 stride 1 only): a residual of the output's shape and plane stride is copied into the
+//     same ring buffer as the item's input band (one 4 x 64 tile per output channel slot), so it
+//     arrives under the band's wait, and is added before (has_res 1) or after (has_res 2) the
+//     activation.
 // Reference semantics: ConvCpu (src/backend/cpu/ops/conv.cpp:9-92) — bias, activation, fp16 store.
 #include "conv_kernels.h"
 
@@ -34,14 +38,19 @@ namespace vkhip {
         };
     } // namespace thin
 
-    // LDS bytes of one band buffer of the thin kernel
+    // LDS bytes of one band buffer of the thin kernel (input band only)
     template <int CINB, int K, int S>
     constexpr int thin_band_bytes() {
         using B = thin::Band<K, S>;
         return ((CINB * B::ROWS * B::PPR + 63) / 64 + 3) / 4 * 4 * 1024;
     }
+    // 1 KB copies per wave of one item's residual tile (MT*4 slots x 4 rows x 64 pixels, 8 bytes each)
+    template <int MT, bool RES>
+    constexpr int thin_res_copies() {
+        return RES ? MT * 2 : 0;
+    }
 
-    template <int CINB, int MT, int K, int S, int NBUF>
+    template <int CINB, int MT, int K, int S, int NBUF, bool RES>
     __global__ __launch_bounds__(256, 2) void conv_thin_kernel(GemmArgs a) {
         using B = thin::Band<K, S>;
         constexpr int OR = thin::OR, OCW = thin::OCW;
@@ -50,8 +59,11 @@ namespace vkhip {
         constexpr int TP     = CINB * B::ROWS * B::PPR;    // pixel pairs of one band
         constexpr int NI     = (TP + 63) / 64;             // 1 KB copies of one band
         constexpr int NBW    = (NI + 3) / 4;               // copies per wave (the surplus ones copy zeros)
-        constexpr int BAND   = NBW * 4 * 1024;             // LDS bytes of one band buffer
-        static_assert(BAND == thin_band_bytes<CINB, K, S>() && (NBUF == 2 || NBUF == 3), "band ring");
+        constexpr int NRW    = thin_res_copies<MT, RES>(); // residual copies per wave
+        constexpr int RBASE  = NBW * 4 * 1024;             // residual tile's offset in a ring buffer
+        constexpr int BAND   = (NBW + NRW) * 4 * 1024;     // LDS bytes of one ring buffer
+        static_assert(RBASE == thin_band_bytes<CINB, K, S>() && (NBUF == 2 || NBUF == 3), "band ring");
+        static_assert(!RES || (K == 3 && S == 1), "residual: 3x3 stride 1 only");
         static_assert(NBUF * BAND <= 160 * 1024, "band ring fits LDS");
         static_assert(MT * NSTEPS <= 28, "weights fit the register budget");
         __shared__ __attribute__((aligned(16))) unsigned char sm[NBUF * BAND];
@@ -65,6 +77,7 @@ namespace vkhip {
         constexpr unsigned kInvalid = 0x80000000u;
         const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) a.x_bytes, 0x00020000);
         const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc((void *) a.y, (short) 0, (int) a.y_bytes, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc((void *) (RES ? a.res : a.y), (short) 0, RES ? (int) a.y_bytes : 0, 0x00020000);
 
         // weights: fragment (m, j) of lane l holds rows m*16 + l%16, reduction values 32j + 8(l/16) .. +7
         half8 wf[MT][NSTEPS];
@@ -109,6 +122,18 @@ namespace vkhip {
                 const unsigned off = ok ? (unsigned) ((((n * a.x_pstride + slot) * H + iy) * W + ix) * 8) : kInvalid;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void *) (dst + i * 1024), 16, off, 0, 0, 0);
             }
+            // residual tile: [slot][row][64 pixels], two pixels per lane and copy
+#pragma unroll
+            for (int r = 0; r < NRW; ++r) {
+                const int i    = r * 4 + wave;
+                const int p    = i * 64 + lane;
+                const int pc   = p % (OCW / 2), rs = p / (OCW / 2);
+                const int row  = rs % OR, slot = rs / OR;
+                const int oy   = oy0 + row, ox = ox0 + 2 * pc;
+                const bool ok  = slot < a.Coutb && oy < a.OHW / a.OW && ox < a.OW;
+                const unsigned off = ok ? (unsigned) ((((n * a.y_pstride + slot) * (a.OHW / a.OW) + oy) * a.OW + ox) * 8) : kInvalid;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rrs, (__attribute__((address_space(3))) void *) (dst + RBASE + i * 1024), 16, off, 0, 0, 0);
+            }
         };
 
         auto finish = [&](int it, int buf, auto act_c) __attribute__((always_inline)) {
@@ -142,10 +167,16 @@ namespace vkhip {
                     const int ocb = m * 4 + g;
                     const int oc  = ocb * 4;
                     float4v   v   = acc[m] + *reinterpret_cast<const float4v *>(a.bias + oc);
+                    float4v   r   = {0.f, 0.f, 0.f, 0.f};
+                    if constexpr (RES) {
+                        r = h4_to_f4(__builtin_bit_cast(half4, *reinterpret_cast<const u32x2 *>(band + RBASE + ((ocb * OR + wave) * OCW + t * 16 + (lane & 15)) * 8)));
+                        if (a.has_res != 2) v += r;
+                    }
                     v.x = apply_act(v.x, ACT, a.lo, a.hi);
                     v.y = apply_act(v.y, ACT, a.lo, a.hi);
                     v.z = apply_act(v.z, ACT, a.lo, a.hi);
                     v.w = apply_act(v.w, ACT, a.lo, a.hi);
+                    if (RES && a.has_res == 2) v += r;
                     if (oc + 0 >= a.Cout) v.x = 0.f;
                     if (oc + 1 >= a.Cout) v.y = 0.f;
                     if (oc + 2 >= a.Cout) v.z = 0.f;
@@ -171,7 +202,8 @@ namespace vkhip {
         // stores per wave per item: every (pixel tile, fragment) store is issued, out-of-range ones
         // with an offset the buffer drops, so the count is fixed
         constexpr int kStores = (OCW / 16) * MT;
-        static_assert((NBUF - 1) * kStores + NBW <= 63, "stores and copies in flight fit the counter");
+        constexpr int kCopies = NBW + NRW; // copies per wave per item
+        static_assert((NBUF - 1) * kStores + kCopies <= 63, "stores and copies in flight fit the counter");
         // vmcnt(n) with n a compile-time constant (the counter retires in issue order)
         auto wait_for = [](auto n_c) __attribute__((always_inline)) {
             constexpr int n = decltype(n_c)::value;
@@ -193,13 +225,13 @@ namespace vkhip {
                 else wait_for(integral_constant<int, kStores> {});
             } else {
                 if (k == 0) {
-                    if (more) wait_for(integral_constant<int, NBW> {});
+                    if (more) wait_for(integral_constant<int, kCopies> {});
                     else wait_for(integral_constant<int, 0> {});
                 } else if (k == 1) {
-                    if (more) wait_for(integral_constant<int, NBW + kStores> {});
+                    if (more) wait_for(integral_constant<int, kCopies + kStores> {});
                     else wait_for(integral_constant<int, kStores> {});
                 } else {
-                    if (more) wait_for(integral_constant<int, NBW + 2 * kStores> {});
+                    if (more) wait_for(integral_constant<int, kCopies + 2 * kStores> {});
                     else wait_for(integral_constant<int, 2 * kStores> {});
                 }
             }
@@ -211,39 +243,43 @@ namespace vkhip {
         }
     }
 
-    // ring depth: three bands (two items ahead) when they leave room for two workgroups per CU
-    template <int CB, int K, int S>
+    // ring depth: three buffers (two items ahead) when they leave room for two workgroups per CU
+    template <int CB, int K, int S, int MT, bool RES>
     constexpr int thin_nbuf() {
-        return 3 * thin_band_bytes<CB, K, S>() <= 80 * 1024 ? 3 : 2;
+        return 3 * (thin_band_bytes<CB, K, S>() + thin_res_copies<MT, RES>() * 4 * 1024) <= 80 * 1024 ? 3 : 2;
     }
 
     template <int CB, int MT_>
-    static GemmKernelFn thin_pick_ks(int k, int s) {
+    static GemmKernelFn thin_pick_ks(int k, int s, bool res) {
         if constexpr (MT_ * ((9 * CB * 4 + 31) / 32) <= 20) {
-            if (k == 3 && s == 1) return conv_thin_kernel<CB, MT_, 3, 1, thin_nbuf<CB, 3, 1>()>;
-            if (k == 3 && s == 2) return conv_thin_kernel<CB, MT_, 3, 2, thin_nbuf<CB, 3, 2>()>;
+            if (k == 3 && s == 1)
+                return res ? conv_thin_kernel<CB, MT_, 3, 1, thin_nbuf<CB, 3, 1, MT_, true>(), true>
+                           : conv_thin_kernel<CB, MT_, 3, 1, thin_nbuf<CB, 3, 1, MT_, false>(), false>;
+            if (res) return nullptr;
+            if (k == 3 && s == 2) return conv_thin_kernel<CB, MT_, 3, 2, thin_nbuf<CB, 3, 2, MT_, false>(), false>;
         }
+        if (res) return nullptr;
         if constexpr (CB == 1) {
-            if (k == 7 && s == 2) return conv_thin_kernel<CB, MT_, 7, 2, thin_nbuf<CB, 7, 2>()>;
+            if (k == 7 && s == 2) return conv_thin_kernel<CB, MT_, 7, 2, thin_nbuf<CB, 7, 2, MT_, false>(), false>;
         }
-        if (k == 1 && s == 1) return conv_thin_kernel<CB, MT_, 1, 1, thin_nbuf<CB, 1, 1>()>;
+        if (k == 1 && s == 1) return conv_thin_kernel<CB, MT_, 1, 1, thin_nbuf<CB, 1, 1, MT_, false>(), false>;
         return nullptr;
     }
     template <int CB>
-    static GemmKernelFn thin_pick_mt(int mt, int k, int s) {
-        if (mt == 1) return thin_pick_ks<CB, 1>(k, s);
-        if (mt == 2) return thin_pick_ks<CB, 2>(k, s);
-        if (mt == 4) return thin_pick_ks<CB, 4>(k, s);
+    static GemmKernelFn thin_pick_mt(int mt, int k, int s, bool res) {
+        if (mt == 1) return thin_pick_ks<CB, 1>(k, s, res);
+        if (mt == 2) return thin_pick_ks<CB, 2>(k, s, res);
+        if (mt == 4) return thin_pick_ks<CB, 4>(k, s, res);
         return nullptr;
     }
     // kernel for a thin plan: cinb input slots (rounded up to 1, 2, 4 or 8), mt 16-channel output
-    // fragments (1, 2 or 4)
-    GemmKernelFn thin_kernel_for(int cinb, int mt, int k, int s) {
+    // fragments (1, 2 or 4), with a residual (3x3 stride 1 only) or without
+    GemmKernelFn thin_kernel_for(int cinb, int mt, int k, int s, bool res) {
         switch (thin_cinb(cinb)) {
-            case 1: return thin_pick_mt<1>(mt, k, s);
-            case 2: return thin_pick_mt<2>(mt, k, s);
-            case 4: return thin_pick_mt<4>(mt, k, s);
-            case 8: return thin_pick_mt<8>(mt, k, s);
+            case 1: return thin_pick_mt<1>(mt, k, s, res);
+            case 2: return thin_pick_mt<2>(mt, k, s, res);
+            case 4: return thin_pick_mt<4>(mt, k, s, res);
+            case 8: return thin_pick_mt<8>(mt, k, s, res);
         }
         return nullptr;
     }

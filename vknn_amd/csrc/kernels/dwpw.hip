@@ -954,6 +954,7 @@ int vkhip_dwpw_forward(const vkhip_dwpw_desc *d, const void *x, const void *blob
     if (!d || !x || !blob || !y) return set_error(VKHIP_ERR_INVALID, "dwpw_forward: null argument");
     if (!vkhip_dwpw_supported(d)) return set_error(VKHIP_ERR_UNSUPPORTED, "dwpw_forward: unsupported descriptor");
     if (d->has_res && !res) return set_error(VKHIP_ERR_INVALID, "dwpw_forward: has_res without residual");
+    if (d->has_res > 1) return set_error(VKHIP_ERR_UNSUPPORTED, "dwpw_forward: the residual is added before the activation only");
     DwPwGeom g = dwpw_geom(d);
     const vkhip_conv_desc &c = d->dw;
     DwPwArgs a;
