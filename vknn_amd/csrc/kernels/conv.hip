@@ -1337,6 +1337,12 @@ static int conv_forward_impl(const vkhip_conv_desc *d, const vkhip_conv_plan *pl
         // not the per-workgroup pipeline, hides most of the load latency (measured: one or two
         // workgroups per CU run 1.2-2x slower than full occupancy)
         dim3 grid((unsigned) std::min<int64_t>(persist_grid(tf, 256, items), items), 1, 1);
+        // XCD-contiguous item ranges on 3x3 stride 1, where vertically adjacent items share a third
+        // of their input rows (16x16 3x3 at 160x160, b16: 12.3 -> 11.4 us); the strided walk
+        // elsewhere (stride 2 and 1x1 bands barely overlap, and there it measured 1-3% faster).
+        // VKHIP_THIN_ORDER=0: the strided walk everywhere (A/B).
+        static const bool xcd_order = !(std::getenv("VKHIP_THIN_ORDER") && std::getenv("VKHIP_THIN_ORDER")[0] == '0');
+        a.item_order = xcd_order && d->KH == 3 && d->SH == 1;
         tf<<<grid, 256, 0, st>>>(a);
         return check_launch("conv_thin");
     }

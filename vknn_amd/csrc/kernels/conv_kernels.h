@@ -58,6 +58,7 @@ namespace vkhip {
                                                        // (Cinb / Coutb, or more for a view into a wider tensor)
         int          *cnt;                             // split-K: per-tile arrival counters when the last
                                                        // workgroup of a tile sums the partials (else null)
+        int           item_order;                      // conv_thin_kernel: 1 XCD-contiguous item ranges, 0 strided
     };
 
     enum { OMODE_EPILOGUE = 0, OMODE_RAW = 1, OMODE_PARTIAL = 2 };

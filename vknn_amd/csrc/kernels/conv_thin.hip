@@ -210,16 +210,29 @@ namespace vkhip {
             __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
         };
         using std::integral_constant;
+        // Item order. Workgroup b runs on XCD b % 8 (ids are dealt to the 8 XCDs round-robin).
+        // a.item_order 1: the items are cut into 8 contiguous ranges, one per XCD, which that XCD's
+        // workgroups walk in order, so items a workgroup's XCD runs at the same time are neighbours
+        // and the input rows two vertically adjacent items share are read from that XCD's L2 once;
+        // 0: one strided walk over all items.
         const int G = gridDim.x;
-        int it = blockIdx.x, buf = 0;
+        const int xcd = blockIdx.x & 7, lb = blockIdx.x >> 3;
+        // XCD x holds gx workgroups, px of them on the XCDs before it; its range is its share
+        const int gx  = a.item_order ? (G >> 3) + ((G & 7) > xcd ? 1 : 0) : G;
+        const int px  = xcd * (G >> 3) + min(xcd, G & 7);
+        const int i0  = a.item_order ? (int) ((long long) items * px / G) + lb : blockIdx.x;
+        const int i1  = a.item_order ? (int) ((long long) items * (px + gx) / G) : items;
+        auto item_at = [&](int k) __attribute__((always_inline)) { return i0 + k * gx < i1 ? i0 + k * gx : -1; };
+        int buf = 0;
 #pragma unroll
         for (int d = 0; d < NBUF - 1; ++d)
-            if (it + d * G < items) issue_band(it + d * G, d);
-        for (int k = 0; it < items; it += G, ++k) {
+            if (item_at(d) >= 0) issue_band(item_at(d), d);
+        for (int k = 0; item_at(k) >= 0; ++k) {
+            const int it = item_at(k);
             // Wait for this item's band. Issued after it, and allowed to stay in flight: the stores
             // of the (at most NBUF - 1) items computed since, and the band of the next item when
             // NBUF = 3 and that item exists.
-            const bool more = NBUF == 3 && it + G < items;
+            const bool more = NBUF == 3 && item_at(k + 1) >= 0;
             if constexpr (NBUF == 2) {
                 if (k == 0) wait_for(integral_constant<int, 0> {});
                 else wait_for(integral_constant<int, kStores> {});
@@ -236,8 +249,8 @@ namespace vkhip {
                 }
             }
             __asm__ volatile("s_barrier" ::: "memory"); // all copies of the band landed; the oldest buffer is free
-            const int nxt = it + (NBUF - 1) * G;
-            if (nxt < items) issue_band(nxt, buf == 0 ? NBUF - 1 : buf - 1);
+            const int nxt = item_at(k + NBUF - 1);
+            if (nxt >= 0) issue_band(nxt, buf == 0 ? NBUF - 1 : buf - 1);
             compute_store(it, buf);
             buf = buf + 1 == NBUF ? 0 : buf + 1;
         }
