@@ -150,7 +150,7 @@ namespace vkhip {
 #pragma unroll
                 for (int qq = 0; qq < 4; ++qq) {
                     const int ocb = (mw0 + i * 32 + qq * 8 + lk * 4) >> 2;
-                    off[j][i][qq] = pok & (ocb < a.Coutb) ? (unsigned) ((ocb * a.P + pn * a.OHW + pr) * 16) : kInvalid;
+                    off[j][i][qq] = (pok & (ocb < a.Coutb)) ? (unsigned) ((ocb * a.P + pn * a.OHW + pr) * 16) : kInvalid;
                 }
         }
         float16v sum[FM][FN];
