@@ -42,6 +42,8 @@ def make_input(shape, seed, uniform=False):
     ("yolo_tiny", 2, "VKNN_HIP_REFINE=0"),
     ("mnv3_tiny", 2, "VKNN_HIP_FOLD_ACT=0"),
     ("yolo_tiny", 2, "VKNN_HIP_FOLD_ADD=0"),
+    ("mnv3_tiny", 2, "VKNN_HIP_AUTO_SE=0"),
+    ("mnv3_tiny", 2, "hip_auto_se=0"),
 ])
 def test_tiny_models(gpu, monkeypatch, model, batch, opts):
     if opts.startswith("VKNN_"):  # an environment switch of the backend, not a session option
@@ -166,6 +168,21 @@ def test_se_scale_folded_into_projection(gpu, opts, monkeypatch):
     plain = V.Session("mobilenetv3_large", 2, seed=7, options=opts)
     assert "+input scale" not in plain.describe()
     check_outputs(got, plain.run(x), sess.out_elems, f"config3 b2 folded vs unfolded[{opts}]")
+
+
+def test_squeeze_excite_fused_by_default(gpu, monkeypatch):
+    """Default options: the HIP backend still fuses every MobileNetV3 squeeze-excite (its pool then
+    folds into the depthwise conv), and the result matches the oracle's unfused graph and the
+    session without the automatic fusion."""
+    sess = V.Session("mobilenetv3_large", 2, seed=7)
+    plan = sess.describe()
+    assert plan.count("pool folded into the depthwise conv") == 8, plan
+    x = make_input(sess.in_shape, 8)
+    got = sess.run(x)
+    check_outputs(got, oracle_model_run("mobilenetv3_large", 2, 7, x), sess.out_elems, "config3 b2 auto SE")
+    plain = V.Session("mobilenetv3_large", 2, seed=7, options="hip_auto_se=0")
+    assert "pool folded into the depthwise conv" not in plain.describe()
+    check_outputs(got, plain.run(x), sess.out_elems, "config3 b2 auto SE vs unfused")
 
 
 def test_bottleneck_add_folded_into_conv(gpu, monkeypatch):

@@ -7,8 +7,10 @@
 #include "vknn/runtime.h"
 #include "vknn/session.h"
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <set>
+#include <string>
 
 namespace vknn {
 
@@ -22,6 +24,8 @@ namespace vknn {
         PassOptions opt;
         opt.fuseDwPw          = cfg.fuseDwPw;
         opt.fuseSqueezeExcite = cfg.fuseSqueezeExcite;
+        const char *auto_se   = std::getenv("VKNN_HIP_AUTO_SE");
+        if (cfg.backend == BackendKind::Hip && cfg.hipAutoSE && !(auto_se && std::string(auto_se) == "0")) opt.fuseSqueezeExcite = true;
         return create(std::move(g), cfg, opt);
     }
 
