@@ -83,6 +83,22 @@ namespace vknn {
 
         size_t nc4Bytes(const Shape &s) { return (size_t) formatElems(TensorFormat::NC4HW4, NCHW::from(s)) * 2; }
 
+        // The descriptor of a dense conv node as it runs on its own (no residual, no folds).
+        static vkhip_conv_desc convDescOf(const Graph &g, const Node &node) {
+            vkhip_conv_desc d {};
+            NCHW         x  = NCHW::from(g.desc(node.inputs[0]).shape);
+            NCHW         y  = NCHW::from(g.desc(node.outputs[0]).shape);
+            const Shape &ws = g.desc(node.inputs[1]).shape;
+            auto st = attrInts(node, "strides", {1, 1}), pad = attrInts(node, "pads", {0, 0, 0, 0}), dil = attrInts(node, "dilations", {1, 1});
+            d.N = (int) x.n; d.Cin = (int) x.c; d.H = (int) x.h; d.W = (int) x.w;
+            d.Cout = (int) ws[0]; d.OH = (int) y.h; d.OW = (int) y.w;
+            d.KH = (int) ws[2]; d.KW = (int) ws[3]; d.SH = (int) st[0]; d.SW = (int) st[1];
+            d.PT = (int) pad[0]; d.PL = (int) pad[1]; d.DH = (int) dil[0]; d.DW = (int) dil[1];
+            d.group = (int) node.attr.geti("group", 1);
+            d.act = (int) node.fusedAct; d.act_lo = node.actLo; d.act_hi = node.actHi;
+            return d;
+        }
+
         // ------------------------------------------------------------ conv autotune cache
         // Keyed by the conv geometry under the per-GPU tag; the chosen (algo, tile, ksplit) lives in
         // the process-wide TuneCache, which Config::cacheFile persists across processes (the
@@ -917,6 +933,39 @@ namespace vknn {
             std::string describe() const override { return what + (what.find(':') != std::string::npos ? " " : " folded into ") + into; }
         };
 
+        // ------------------------------------------------------------ two stride-2 stem convs
+        // A 3x3 stride-2 conv over at most 4 channels and the 3x3 stride-2 conv that is its only
+        // reader (the YOLOv8n stem, 3 -> 16 -> 32) as one op at the second conv's place: one
+        // launch of vkhip_conv3x3s2_pair_forward, the intermediate never in HBM. The weights are
+        // the thin tiles' blobs; no plan search (one kernel).
+        struct Stem2Op: HipOp {
+            const Node             *na = nullptr; // the first conv (this op is prepared with the second)
+            vkhip_conv_desc         d1 {}, d2 {};
+            vkhip_conv_plan         p1 {}, p2 {};
+            std::shared_ptr<DevBuf> blob1, blob2;
+            TensorId                in = kNoTensor, out = kNoTensor;
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g = *env.graph;
+                d1 = convDescOf(g, *na);
+                d2 = convDescOf(g, node);
+                in = na->inputs[0];
+                out = node.outputs[0];
+                check(vkhip_conv3x3s2_pair_plan(&d1, &d2, &p1, &p2), "stem pair plan " + name);
+                std::vector<uint8_t> h1(p1.weight_bytes), h2(p2.weight_bytes);
+                check(vkhip_conv_pack_weights(&d1, &p1, initF32(g, na->inputs[1]), initF32(g, biasOf(*na)), h1.data()), "stem pair pack");
+                check(vkhip_conv_pack_weights(&d2, &p2, initF32(g, node.inputs[1]), initF32(g, biasOf(node)), h2.data()), "stem pair pack");
+                blob1 = upload(h1.data(), h1.size());
+                blob2 = upload(h2.data(), h2.size());
+                kind  = "conv";
+                flops = 2.0 * d1.N * d1.Cout * d1.Cin * 9 * d1.OH * d1.OW + 2.0 * d2.N * d2.Cout * d2.Cin * 9 * d2.OH * d2.OW;
+                bytes = (int64_t) (nc4Bytes(g.desc(in).shape) + nc4Bytes(g.desc(out).shape)) + (int64_t) (d1.Cout * d1.Cin + d2.Cout * d2.Cin) * 9 * 2;
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                check(vkhip_conv3x3s2_pair_forward(&d1, &d2, env.dev(in), blob1->ptr, blob2->ptr, env.dev(out), env.pstride(out), s), "stem pair " + name);
+            }
+            std::string describe() const override { return "fused with " + na->name + " kernel=conv_stem2_kernel"; }
+        };
+
         // ------------------------------------------------------------ fused 3x3 + 1x1
         // A 3x3 conv whose only reader is a 1x1 conv (a bottleneck's middle conv and its expansion)
         // as one op at the 1x1's place in the order (its residual, e.g. a projection shortcut, may be
@@ -1514,6 +1563,55 @@ namespace vknn {
                     for (auto &kv: addFold) addConv[kv.second.first] = kv.first;
                 }
             }
+            // Two stride-2 stem convs as one op (Stem2Op): the second conv -> the first, which is
+            // folded. VKNN_HIP_FUSE_STEM2=0 keeps the two launches (A/B).
+            std::map<int, int> stem2Of; // second conv node -> first conv node
+            std::set<int>      stem2Folded;
+            {
+                const char *st2_env = std::getenv("VKNN_HIP_FUSE_STEM2");
+                if (!st2_env || std::string(st2_env) != "0") {
+                    std::set<int> skip(folded.begin(), folded.end());
+                    for (auto &kv: scaled) skip.insert(kv.first);
+                    for (auto &kv: convPool) skip.insert(kv.first), skip.insert(kv.second);
+                    for (auto &kv: gapConv) skip.insert(kv.second);
+                    for (auto &kv: pwPairs) skip.insert(kv.first);
+                    skip.insert(pwFolded.begin(), pwFolded.end());
+                    skip.insert(pwChained.begin(), pwChained.end());
+                    for (auto &kv: actConv) skip.insert(kv.first);
+                    for (auto &kv: addConv) skip.insert(kv.first);
+                    std::map<TensorId, int> readers, producer;
+                    for (size_t i = 0; i < g.nodes.size(); ++i) {
+                        for (TensorId t: g.nodes[i].inputs)
+                            if (t != kNoTensor) ++readers[t];
+                        if (g.nodes[i].fusedResidual != kNoTensor) ++readers[g.nodes[i].fusedResidual];
+                        for (TensorId t: g.nodes[i].outputs)
+                            if (t != kNoTensor) producer[t] = (int) i;
+                    }
+                    for (TensorId t: g.outputs) readers[t] += 1000;
+                    std::set<int> inSeg(idx.begin(), idx.end());
+                    auto dense = [&](const Node &c) {
+                        return c.type == OpType::Conv && c.inputs.size() >= 2 && g.isInitializer(c.inputs[1]) && c.fusedResidual == kNoTensor &&
+                               g.desc(c.inputs[1]).shape.size() == 4 && !c.outputs.empty();
+                    };
+                    for (int b: idx) {
+                        const Node &nb = g.nodes[b];
+                        if (skip.count(b) || !dense(nb)) continue;
+                        const TensorId t = nb.inputs[0];
+                        auto           pa = producer.find(t);
+                        if (pa == producer.end() || !inSeg.count(pa->second) || skip.count(pa->second) || stem2Folded.count(pa->second) ||
+                            stem2Of.count(pa->second) || readers[t] != 1)
+                            continue;
+                        const Node &na = g.nodes[pa->second];
+                        if (!dense(na) || place_.count(resolve(t)) || pstride(t) > 0 || pstride(na.inputs[0]) > 0 || place_.count(resolve(na.inputs[0])))
+                            continue;
+                        vkhip_conv_desc d1 = convDescOf(g, na), d2 = convDescOf(g, nb);
+                        vkhip_conv_plan q1, q2;
+                        if (vkhip_conv3x3s2_pair_plan(&d1, &d2, &q1, &q2) != VKHIP_OK) continue;
+                        stem2Of[b] = pa->second;
+                        stem2Folded.insert(pa->second);
+                    }
+                }
+            }
             // Device buffers: one NC4HW4 fp16 buffer per activation (aliases share their source's;
             // a tensor placed in another one by planViews has none of its own).
             for (int i: idx) {
@@ -1560,6 +1658,16 @@ namespace vknn {
                     f->what = "hard-sigmoid";
                     f->into = g.nodes[actFold[i]].name;
                     op      = std::move(f);
+                } else if (stem2Folded.count(i)) {
+                    auto f = std::make_unique<FoldedMulOp>();
+                    f->what = "3x3 stride-2 conv: runs with the stride-2 conv that reads it,";
+                    for (auto &kv: stem2Of)
+                        if (kv.second == i) f->into = g.nodes[kv.first].name;
+                    op = std::move(f);
+                } else if (stem2Of.count(i)) {
+                    auto c = std::make_unique<Stem2Op>();
+                    c->na  = &g.nodes[stem2Of[i]];
+                    op     = std::move(c);
                 } else if (addFold.count(i)) {
                     auto f  = std::make_unique<FoldedMulOp>();
                     f->what = "add (a residual after the activation)";
@@ -1617,7 +1725,7 @@ namespace vknn {
                 op->name = nd.name;
                 op->type = nd.type;
                 const bool gapFolded = gapParts.count(i) > 0;
-                const bool pwOp = pwPairs.count(i) || pwFolded.count(i) || pwChained.count(i);
+                const bool pwOp = pwPairs.count(i) || pwFolded.count(i) || pwChained.count(i) || stem2Of.count(i) || stem2Folded.count(i);
                 if (nd.type == OpType::Conv && !inPlace && !gapFolded && !folded.count(i) && !pools.count(i) && !pwOp) {
                     bool v = false;
                     for (TensorId t: {nd.inputs[0], nd.outputs[0]}) v = v || pstride(t) > 0;
@@ -1658,7 +1766,16 @@ namespace vknn {
                     outs.push_back(out);
                     continue;
                 }
-                if (folded.count(i) || pools.count(i) || pwFolded.count(i) || pwChained.count(i) || actFold.count(i) || addFold.count(i)) {
+                if (folded.count(i) || pools.count(i) || pwFolded.count(i) || pwChained.count(i) || actFold.count(i) || addFold.count(i) ||
+                    stem2Folded.count(i)) {
+                    ins.push_back(in);
+                    outs.push_back(out);
+                    continue;
+                }
+                if (stem2Of.count(i)) {
+                    // the pair reads the first conv's input and writes the second's output
+                    in.push_back(resolve(g.nodes[stem2Of[i]].inputs[0]));
+                    out.push_back(resolve(nd.outputs[0]));
                     ins.push_back(in);
                     outs.push_back(out);
                     continue;
