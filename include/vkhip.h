@@ -358,6 +358,13 @@ typedef struct vkhip_pool_desc {
 int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s);
 /* vkhip_maxpool over views (plane strides per image; 0 = dense). */
 int vkhip_maxpool_view(const vkhip_pool_desc *d, const void *x, int64_t x_pstride, void *y, int64_t y_pstride, vkhip_stream_t s);
+/* `count` (1-4) same-size max pools in a chain, one launch: ys[0] = pool(x), ys[k] = pool(ys[k-1])
+ * for a KxK (K = 3 or 5) stride-1 pad-K/2 pool whose plane fits LDS (the SPPF block of a detector
+ * neck); every output may be a view (y_pstrides[k]; 0 = dense). Bit-identical to `count`
+ * vkhip_maxpool_view calls. No reference counterpart: the reference runs its MaxPool
+ * (src/backend/cpu/ops/maxpool.cpp) once per node. */
+int vkhip_maxpool_chain(const vkhip_pool_desc *d, const void *x, int64_t x_pstride, void *const *ys, const int64_t *y_pstrides, int32_t count,
+                        vkhip_stream_t s);
 /* A first-layer conv (at most 4 input channels, 3x3 or 7x7, stride 1 or 2, pad K/2, <= 64 output
  * channels, no residual) followed by a 3x3 stride-2 pad-1 max pool over its output, in one
  * kernel: y = maxpool(act(conv(x) + bias)), bit-identical to vkhip_conv_forward then

@@ -1155,6 +1155,36 @@ def test_maxpool_same(gpu, shape, k):
         assert np.array_equal(wide[:, C:], ref) and not wide[:, :C].any()
 
 
+@pytest.mark.parametrize("count,k", [(3, 5), (2, 3), (4, 5), (1, 5)])
+def test_maxpool_chain(gpu, count, k):
+    """vkhip_maxpool_chain (the SPPF pools in one launch): every output bit-identical to the oracle
+    pool applied 1..count times, the outputs written into channel slices of one wide tensor (the
+    in-place concat) with the input in another; the other slices untouched."""
+    lib = V.vkhip()
+    N, C, H, W = 2, 8, 20, 20
+    x = round_half(rng(97 + count + k).standard_normal((N, C, H, W)) * 3)
+    p = k // 2
+    d = V.PoolDesc(N=N, C=C, H=H, W=W, OH=H, OW=W, KH=k, KW=k, SH=1, SW=1, PT=p, PL=p)
+    Ct = C * (count + 1)
+    wide = np.zeros((N, Ct, H, W), np.float32)
+    wide[:, :C] = x
+    dw = to_device_nc4(wide)
+    plane = H * W * 8
+    ys = (ctypes.c_void_p * 4)(*[dw.ptr + (c + 1) * (C // 4) * plane for c in range(count)] + [None] * (4 - count))
+    ps = (ctypes.c_int64 * 4)(*([Ct // 4] * 4))
+    check(lib.vkhip_maxpool_chain(ctypes.byref(d), dw.ptr, Ct // 4, ys, ps, count, None), "maxpool chain")
+    got = from_device_nc4(dw, wide.shape)
+    assert np.array_equal(got[:, :C], x)
+    cur = x
+    for c in range(count):
+        ref = np.zeros_like(cur)
+        oracle().oracle_maxpool(np.ascontiguousarray(cur).ctypes.data, ref.ctypes.data, N, C, H, W, k, k, 1, 1, p, p, H, W)
+        assert np.array_equal(got[:, (c + 1) * C:(c + 2) * C], ref), c
+        cur = ref
+    bad = (ctypes.c_void_p * 4)(dw.ptr, None, None, None)
+    assert lib.vkhip_maxpool_chain(ctypes.byref(d), dw.ptr, 0, bad, ps, 5, None) != 0
+
+
 @pytest.mark.parametrize("shape,pb", [((2, 9, 18, 18), 1), ((1, 8, 16, 20), 1), ((3, 5, 15, 20), 0), ((2, 4, 15, 12), 1),
                                       ((1, 64, 112, 112), 1), ((2, 7, 2, 2), 1), ((1, 4, 1, 6), 1)])
 def test_maxpool_3x3_s2_pairs(gpu, shape, pb):

@@ -828,11 +828,23 @@ namespace vknn {
                 d.N = (int) x.n; d.C = (int) x.c; d.H = (int) x.h; d.W = (int) x.w; d.OH = (int) y.h; d.OW = (int) y.w;
                 d.KH = (int) k[0]; d.KW = (int) k[1]; d.SH = (int) st[0]; d.SW = (int) st[1]; d.PT = (int) p[0]; d.PL = (int) p[1];
                 kind = "maxpool";
-                bytes = (int64_t) (nc4Bytes(env.graph->desc(in).shape) + nc4Bytes(env.graph->desc(out).shape));
+                bytes = (int64_t) (nc4Bytes(env.graph->desc(in).shape) + nc4Bytes(env.graph->desc(out).shape) * (1 + chain.size()));
             }
+            // Set by the segment before prepare: the same-size pools that follow this one in a
+            // chain (each the only pool reading the previous output, the SPPF block); their outputs
+            // come from this op's single launch (vkhip_maxpool_chain).
+            std::vector<TensorId> chain;
             void record(SegEnv &env, vkhip_stream_t s) override {
-                check(vkhip_maxpool_view(&d, env.dev(in), env.pstride(in), env.dev(out), env.pstride(out), s), "maxpool " + name);
+                if (chain.empty()) {
+                    check(vkhip_maxpool_view(&d, env.dev(in), env.pstride(in), env.dev(out), env.pstride(out), s), "maxpool " + name);
+                    return;
+                }
+                void   *ys[4] = {env.dev(out)};
+                int64_t ps[4] = {env.pstride(out)};
+                for (size_t k = 0; k < chain.size(); ++k) ys[k + 1] = env.dev(chain[k]), ps[k + 1] = env.pstride(chain[k]);
+                check(vkhip_maxpool_chain(&d, env.dev(in), env.pstride(in), ys, ps, (int32_t) (1 + chain.size()), s), "maxpool chain " + name);
             }
+            std::string describe() const override { return chain.empty() ? "" : "+" + std::to_string(chain.size()) + " chained pools in one launch"; }
         };
 
         struct ConcatOp: HipOp {
@@ -1563,6 +1575,49 @@ namespace vknn {
                     for (auto &kv: addFold) addConv[kv.second.first] = kv.first;
                 }
             }
+            // Chains of same-size max pools (the SPPF block: each pool the only pool reading the
+            // previous one's output) as one launch at the first pool's place. VKNN_HIP_POOL_CHAIN=0
+            // keeps one launch per pool (A/B).
+            std::map<int, std::vector<int>> poolChain; // first pool -> the pools it also computes
+            std::set<int>                   poolChained;
+            {
+                const char *pc_env = std::getenv("VKNN_HIP_POOL_CHAIN");
+                if (!pc_env || std::string(pc_env) != "0") {
+                    std::set<int> inSeg(idx.begin(), idx.end());
+                    std::map<TensorId, std::vector<int>> readers;
+                    for (int i: idx)
+                        for (TensorId t: g.nodes[i].inputs)
+                            if (t != kNoTensor) readers[t].push_back(i);
+                    auto samePool = [&](const Node &m) {
+                        if (m.type != OpType::MaxPool || m.inputs.empty() || m.outputs.empty() || pools.count(&m - &g.nodes[0])) return false;
+                        auto k = attrInts(m, "kernel_shape", {1, 1}), st = attrInts(m, "strides", {1, 1}), p = attrInts(m, "pads", {0, 0, 0, 0});
+                        auto dl = attrInts(m, "dilations", {1, 1});
+                        if (m.attr.geti("ceil_mode", 0) || dl[0] != 1 || dl[1] != 1 || k[0] != k[1] || (k[0] != 3 && k[0] != 5) || st[0] != 1 || st[1] != 1 ||
+                            p[0] != k[0] / 2 || p[1] != k[0] / 2 || p[2] != k[0] / 2 || p[3] != k[0] / 2)
+                            return false;
+                        const Shape &xs = g.desc(m.inputs[0]).shape;
+                        return xs.size() == 4 && xs == g.desc(m.outputs[0]).shape && (size_t) (xs[2] + k[0] - 1) * (2 * xs[3] + k[0] - 1) * 8 <= 64 * 1024;
+                    };
+                    for (int i: idx) {
+                        if (poolChained.count(i) || !samePool(g.nodes[i])) continue;
+                        std::vector<int> ch;
+                        int              cur = i;
+                        while (ch.size() < 3) {
+                            int nxt = -1;
+                            for (int r: readers[g.nodes[cur].outputs[0]])
+                                if (nxt < 0 && inSeg.count(r) && !poolChained.count(r) && r != i && samePool(g.nodes[r]) &&
+                                    attrInts(g.nodes[r], "kernel_shape", {1, 1}) == attrInts(g.nodes[i], "kernel_shape", {1, 1}))
+                                    nxt = r;
+                            if (nxt < 0) break;
+                            ch.push_back(nxt);
+                            cur = nxt;
+                        }
+                        if (ch.empty()) continue;
+                        poolChain[i] = ch;
+                        poolChained.insert(ch.begin(), ch.end());
+                    }
+                }
+            }
             // Two stride-2 stem convs as one op (Stem2Op): the second conv -> the first, which is
             // folded. VKNN_HIP_FUSE_STEM2=0 keeps the two launches (A/B).
             std::map<int, int> stem2Of; // second conv node -> first conv node
@@ -1658,6 +1713,13 @@ namespace vknn {
                     f->what = "hard-sigmoid";
                     f->into = g.nodes[actFold[i]].name;
                     op      = std::move(f);
+                } else if (poolChained.count(i)) {
+                    auto f  = std::make_unique<FoldedMulOp>();
+                    f->what = "max pool: computed in the launch of the chain's first pool,";
+                    for (auto &kv: poolChain)
+                        for (int m: kv.second)
+                            if (m == i) f->into = g.nodes[kv.first].name;
+                    op = std::move(f);
                 } else if (stem2Folded.count(i)) {
                     auto f = std::make_unique<FoldedMulOp>();
                     f->what = "3x3 stride-2 conv: runs with the stride-2 conv that reads it,";
@@ -1706,6 +1768,11 @@ namespace vknn {
                     c->foldAct     = VKHIP_ACT_HARDSIGMOID;
                     c->foldLo      = un.actLo;
                     c->foldHi      = un.actHi;
+                }
+                auto pcit = poolChain.find(i);
+                if (pcit != poolChain.end()) {
+                    auto *m = static_cast<MaxPoolOp *>(op.get());
+                    for (int c: pcit->second) m->chain.push_back(g.nodes[c].outputs[0]);
                 }
                 auto dit = addConv.find(i);
                 if (dit != addConv.end()) {
@@ -1767,7 +1834,7 @@ namespace vknn {
                     continue;
                 }
                 if (folded.count(i) || pools.count(i) || pwFolded.count(i) || pwChained.count(i) || actFold.count(i) || addFold.count(i) ||
-                    stem2Folded.count(i)) {
+                    stem2Folded.count(i) || poolChained.count(i)) {
                     ins.push_back(in);
                     outs.push_back(out);
                     continue;
@@ -1801,6 +1868,8 @@ namespace vknn {
                     }
                     if (nd.fusedResidual != kNoTensor) in.push_back(resolve(nd.fusedResidual));
                     if (dit != addConv.end()) in.push_back(resolve(addFold[dit->second].second));
+                    if (pcit != poolChain.end())
+                        for (int c: pcit->second) out.push_back(resolve(g.nodes[c].outputs[0]));
                     if (pit != convPool.end()) out.push_back(resolve(g.nodes[pit->second].outputs[0]));
                     else if (ait != actConv.end()) out.push_back(resolve(g.nodes[ait->second].outputs[0]));
                     else if (dit != addConv.end()) out.push_back(resolve(g.nodes[dit->second].outputs[0]));

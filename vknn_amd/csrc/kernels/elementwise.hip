@@ -411,8 +411,16 @@ namespace vkhip {
         const half2v x1 = __builtin_elementwise_max(__builtin_bit_cast(half2v, a.y), __builtin_bit_cast(half2v, b.y));
         return uint2 {__builtin_bit_cast(unsigned, x0), __builtin_bit_cast(unsigned, x1)};
     }
+    // Up to 4 such pools in a chain (y1 = pool(x), y2 = pool(y1), ...: the SPPF block), one launch:
+    // each pooled plane goes to its output and back into the LDS image's interior (the -inf halo
+    // stays), so every pool pads with -inf exactly like a separate launch.
+    struct PoolChain {
+        uint2 *y[4];
+        int    yps[4];
+        int    count;
+    };
     template <int K>
-    __global__ __launch_bounds__(256) void maxpool_same_kernel(const uint2 *x, uint2 *y, int H, int W, int Cb, int xps, int yps) {
+    __global__ __launch_bounds__(256) void maxpool_same_kernel(const uint2 *x, PoolChain out, int H, int W, int Cb, int xps) {
         extern __shared__ uint2 pool_sm[];
         constexpr int P  = K / 2;
         const int     RW = W + K - 1, RH = H + K - 1;
@@ -428,23 +436,26 @@ namespace vkhip {
                 tin[r * RW + c] = (iy >= 0 && iy < H && ix >= 0 && ix < W) ? src[iy * W + ix] : ninf;
             }
         }
-        __syncthreads();
-        for (int r = ty; r < RH; r += 4)
-            for (int c = tx; c < W; c += 64) {
-                uint2 m = tin[r * RW + c];
+        for (int k = 0; k < out.count; ++k) {
+            __syncthreads();
+            for (int r = ty; r < RH; r += 4)
+                for (int c = tx; c < W; c += 64) {
+                    uint2 m = tin[r * RW + c];
 #pragma unroll
-                for (int k = 1; k < K; ++k) m = max_u2(m, tin[r * RW + c + k]);
-                trow[r * W + c] = m;
-            }
-        __syncthreads();
-        uint2 *dst = y + ((int64_t) n * yps + cb) * H * W;
-        for (int r = ty; r < H; r += 4)
-            for (int c = tx; c < W; c += 64) {
-                uint2 m = trow[r * W + c];
+                    for (int q = 1; q < K; ++q) m = max_u2(m, tin[r * RW + c + q]);
+                    trow[r * W + c] = m;
+                }
+            __syncthreads();
+            uint2 *dst = out.y[k] + ((int64_t) n * out.yps[k] + cb) * H * W;
+            for (int r = ty; r < H; r += 4)
+                for (int c = tx; c < W; c += 64) {
+                    uint2 m = trow[r * W + c];
 #pragma unroll
-                for (int k = 1; k < K; ++k) m = max_u2(m, trow[(r + k) * W + c]);
-                dst[r * W + c] = m;
-            }
+                    for (int q = 1; q < K; ++q) m = max_u2(m, trow[(r + q) * W + c]);
+                    dst[r * W + c] = m;
+                    tin[(r + P) * RW + c + P] = m; // the next pool's input (rows read only by the row pass)
+                }
+        }
     }
 
     // Nearest upsampling by integer factors (OH = SH * H, OW = SW * W: the 2x upsample of a detector
@@ -614,6 +625,34 @@ static int maxpool_impl(const vkhip_pool_desc *d, const void *x, int64_t xps, vo
 
 int vkhip_maxpool(const vkhip_pool_desc *d, const void *x, void *y, vkhip_stream_t s) { return maxpool_impl(d, x, 0, y, 0, s); }
 
+int vkhip_maxpool_chain(const vkhip_pool_desc *d, const void *x, int64_t x_pstride, void *const *ys, const int64_t *y_pstrides, int32_t count,
+                        vkhip_stream_t s) {
+    if (!d || !x || !ys || !y_pstrides || count < 1 || count > 4) return set_error(VKHIP_ERR_INVALID, "maxpool_chain: bad arguments");
+    const int K = d->KH, Cb = (int) ceil_div(d->C, 4);
+    if (!(K == d->KW && (K == 3 || K == 5) && d->SH == 1 && d->SW == 1 && d->PT == K / 2 && d->PL == K / 2 && d->OH == d->H && d->OW == d->W &&
+          d->N > 0 && d->C > 0 && d->H > 0 && d->W > 0))
+        return set_error(VKHIP_ERR_UNSUPPORTED, "maxpool_chain: KxK (K = 3 or 5) stride-1 pad-K/2 pools only");
+    const size_t sm = (size_t) (d->H + K - 1) * (2 * d->W + K - 1) * 8;
+    if (sm > 64 * 1024) return set_error(VKHIP_ERR_UNSUPPORTED, "maxpool_chain: plane too large for LDS");
+    const int64_t xps = x_pstride > 0 ? x_pstride : Cb;
+    int64_t       big = xps;
+    PoolChain     out {};
+    for (int k = 0; k < count; ++k) {
+        if (!ys[k]) return set_error(VKHIP_ERR_INVALID, "maxpool_chain: null output");
+        const int64_t yps = y_pstrides[k] > 0 ? y_pstrides[k] : Cb;
+        if (yps < Cb) return set_error(VKHIP_ERR_INVALID, "maxpool_chain: plane stride below the channel blocks");
+        out.y[k] = (uint2 *) ys[k]; out.yps[k] = (int) yps;
+        big = std::max(big, yps);
+    }
+    out.count = count;
+    if (xps < Cb || (int64_t) d->N * Cb > INT32_MAX || (int64_t) d->N * big * d->H * d->W >= INT32_MAX)
+        return set_error(VKHIP_ERR_INVALID, "maxpool_chain: tensor too large or plane stride below the channel blocks");
+    const dim3 grid((unsigned) (d->N * Cb)), block(64, 4);
+    if (K == 3) maxpool_same_kernel<3><<<grid, block, sm, resolve_stream(s)>>>((const uint2 *) x, out, (int) d->H, (int) d->W, Cb, (int) xps);
+    else maxpool_same_kernel<5><<<grid, block, sm, resolve_stream(s)>>>((const uint2 *) x, out, (int) d->H, (int) d->W, Cb, (int) xps);
+    return check_launch("maxpool_chain");
+}
+
 int vkhip_maxpool_view(const vkhip_pool_desc *d, const void *x, int64_t x_pstride, void *y, int64_t y_pstride, vkhip_stream_t s) {
     return maxpool_impl(d, x, x_pstride, y, y_pstride, s);
 }
@@ -646,8 +685,10 @@ static int maxpool_impl(const vkhip_pool_desc *d, const void *x, int64_t xps_, v
         const size_t sm = (size_t) (d->H + K - 1) * (2 * d->W + K - 1) * 8;
         if (sm <= 64 * 1024) {
             const dim3 grid((unsigned) (d->N * Cb)), block(64, 4);
-            if (K == 3) maxpool_same_kernel<3><<<grid, block, sm, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, (int) d->H, (int) d->W, Cb, xps, yps);
-            else maxpool_same_kernel<5><<<grid, block, sm, resolve_stream(s)>>>((const uint2 *) x, (uint2 *) y, (int) d->H, (int) d->W, Cb, xps, yps);
+            PoolChain  out {};
+            out.y[0] = (uint2 *) y; out.yps[0] = yps; out.count = 1;
+            if (K == 3) maxpool_same_kernel<3><<<grid, block, sm, resolve_stream(s)>>>((const uint2 *) x, out, (int) d->H, (int) d->W, Cb, xps);
+            else maxpool_same_kernel<5><<<grid, block, sm, resolve_stream(s)>>>((const uint2 *) x, out, (int) d->H, (int) d->W, Cb, xps);
             return check_launch("maxpool_same");
         }
     }
