@@ -44,6 +44,8 @@ def make_input(shape, seed, uniform=False):
     ("yolo_tiny", 2, "VKNN_HIP_FOLD_ADD=0"),
     ("mnv3_tiny", 2, "VKNN_HIP_AUTO_SE=0"),
     ("mnv3_tiny", 2, "hip_auto_se=0"),
+    ("mnv2_tiny", 2, "hip_auto_dwpw=0"),
+    ("mnv3_tiny", 2, "hip_auto_se=0;hip_auto_dwpw=0"),
 ])
 def test_tiny_models(gpu, monkeypatch, model, batch, opts):
     if opts.startswith("VKNN_"):  # an environment switch of the backend, not a session option

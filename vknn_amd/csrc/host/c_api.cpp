@@ -49,6 +49,7 @@ namespace {
                 else if (k == "fuse_dwpw") cfg.fuseDwPw = v != "0";
                 else if (k == "fuse_se") cfg.fuseSqueezeExcite = v != "0";
                 else if (k == "hip_auto_se") cfg.hipAutoSE = v != "0";
+                else if (k == "hip_auto_dwpw") cfg.hipAutoDwPw = v != "0";
                 else if (k == "cache_file") cfg.cacheFile = v;
                 else if (k == "passes") passes = v != "0";
                 else if (k == "cpu_fallback") cfg.allowCpuFallback = v != "0";

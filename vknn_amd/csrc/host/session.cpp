@@ -26,6 +26,8 @@ namespace vknn {
         opt.fuseSqueezeExcite = cfg.fuseSqueezeExcite;
         const char *auto_se   = std::getenv("VKNN_HIP_AUTO_SE");
         if (cfg.backend == BackendKind::Hip && cfg.hipAutoSE && !(auto_se && std::string(auto_se) == "0")) opt.fuseSqueezeExcite = true;
+        const char *auto_dwpw = std::getenv("VKNN_HIP_AUTO_DWPW");
+        if (cfg.backend == BackendKind::Hip && cfg.hipAutoDwPw && !(auto_dwpw && std::string(auto_dwpw) == "0")) opt.fuseDwPw = true;
         return create(std::move(g), cfg, opt);
     }
 
