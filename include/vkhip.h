@@ -106,6 +106,11 @@ int vkhip_graph_destroy(vkhip_graph_t g);
  * (vk_backend.cpp:576-611) bit for bit. Unpack is exact. */
 int vkhip_pack_nchw_f32(const float *src, void *dst, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s);
 int vkhip_unpack_nchw_f32(const void *src, float *dst, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s);
+/* vkhip_unpack_nchw_f32 over `count` tensors (shapes: N, C, H, W per tensor), the ones whose H*W is
+ * a multiple of 4 (and whose destination is 16-byte aligned) in one launch per 8: a segment's
+ * several outputs (a detector's heads) leave in one dispatch. Same bits as one call per tensor.
+ * No reference counterpart: the reference downloads each output on its own (vk_backend.cpp). */
+int vkhip_unpack_nchw_f32_multi(const void *const *srcs, float *const *dsts, const int64_t *shapes, int32_t count, vkhip_stream_t s);
 /* Profiling aid, no counterpart in the reference: enqueue one empty single-wave dispatch
  * (dispatch_marker_kernel) so that a kernel trace can be cut into the launches of each operator.
  * The vknn session records one before every operator when VKNN_HIP_OP_MARKERS=1. */

@@ -68,6 +68,25 @@ def test_pack_exhaustive_rounding_boundaries(gpu):
     assert bad.size == 0, [(hex(bits[i]), hex(got[i]), hex(want[i])) for i in bad[:8]]
 
 
+def test_unpack_multi(gpu):
+    """Several tensors unpacked by one vkhip_unpack_nchw_f32_multi call: the same bits as one
+    vkhip_unpack_nchw_f32 per tensor, for quad-path tensors (grouped, more than 8 of them) and for
+    one whose H*W is not a multiple of 4 (handled on its own)."""
+    lib = V.vkhip()
+    r = rng(1900)
+    shapes = [(2, 144, 8, 8), (2, 144, 4, 4), (2, 144, 2, 2), (1, 7, 6, 6), (3, 5, 3, 3)] + [(1, 12, 4, 4)] * 6
+    xs = [round_half(r.standard_normal(sh)) for sh in shapes]
+    dxs = [to_device_nc4(x) for x in xs]
+    outs = [DeviceBuffer(int(np.prod(sh)) * 4) for sh in shapes]
+    srcs = (ctypes.c_void_p * len(shapes))(*[d.ptr for d in dxs])
+    dsts = (ctypes.c_void_p * len(shapes))(*[o.ptr for o in outs])
+    sh = (ctypes.c_int64 * (4 * len(shapes)))(*[v for s_ in shapes for v in s_])
+    check(lib.vkhip_unpack_nchw_f32_multi(srcs, dsts, sh, len(shapes), None), "unpack multi")
+    check(lib.vkhip_stream_sync(None), "sync")
+    for x, sh_, o in zip(xs, shapes, outs):
+        assert np.array_equal(o.download(np.float32, int(np.prod(sh_))).reshape(sh_), x)
+
+
 def test_flat_pack_unpack(gpu):
     x = rng(2).standard_normal(1003).astype(np.float32) * 1000
     src = DeviceBuffer.from_array(x)

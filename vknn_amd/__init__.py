@@ -94,6 +94,7 @@ VKHIP_API = {
     "vkhip_graph_destroy": (c_int, [c_vp]),
     "vkhip_pack_nchw_f32": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "vkhip_unpack_nchw_f32": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp]),
+    "vkhip_unpack_nchw_f32_multi": (c_int, [P(c_vp), P(c_vp), P(c_i64), c_i32, c_vp]),
     "vkhip_convert_layout": (c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32, c_vp]),
     "vkhip_boundary_convert": (c_int, [c_vp, c_i32, c_i32, c_vp, c_i32, c_i32, c_i64, c_i64, c_i64, c_i64, c_vp]),
     "vkhip_pack_flat_f32": (c_int, [c_vp, c_vp, c_i64, c_vp]),

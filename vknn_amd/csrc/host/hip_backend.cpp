@@ -2306,6 +2306,10 @@ namespace vknn {
                 check(vkhip_event_record(joinEvent_, side_), "event");
                 check(vkhip_stream_wait_event(stream_, joinEvent_), "stream wait");
             }
+            // host-bound outputs leave through one multi-tensor unpack (one launch for up to 8)
+            std::vector<const void *> usrc;
+            std::vector<float *>      udst;
+            std::vector<int64_t>      ushape;
             for (TensorId t: boundaryOutputs) {
                 NCHW y  = NCHW::from(g_.desc(t).shape);
                 auto xo = extOut_.find(t);
@@ -2313,8 +2317,14 @@ namespace vknn {
                     check(vkhip_boundary_convert(dev(t), 2, 1, xo->second.first, xo->second.second.first, xo->second.second.second ? 1 : 0, y.n,
                                                  y.c, y.h, y.w, stream_),
                           "boundary convert (dma-buf output)");
-                else check(vkhip_unpack_nchw_f32(dev(t), (float *) outStaging_[t]->ptr, y.n, y.c, y.h, y.w, stream_), "unpack");
+                else {
+                    usrc.push_back(dev(t));
+                    udst.push_back((float *) outStaging_[t]->ptr);
+                    for (int64_t v: {y.n, y.c, y.h, y.w}) ushape.push_back(v);
+                }
             }
+            if (!usrc.empty())
+                check(vkhip_unpack_nchw_f32_multi(usrc.data(), udst.data(), ushape.data(), (int32_t) usrc.size(), stream_), "unpack");
         }
 
         void HipSegment::launch(bool profile) {

@@ -135,6 +135,31 @@ namespace vkhip {
         }
     }
 
+    // unpack_quad_kernel over up to 8 tensors in one launch (a detector's several outputs): thread
+    // i belongs to the tensor whose quad range [start[k], start[k+1]) holds it.
+    struct UnpackSet {
+        const uint4 *src[8];
+        float4      *dst[8];
+        int          C[8], Cb[8], HW4[8];
+        int          start[9];
+        int          count;
+    };
+    __global__ void unpack_quad_multi_kernel(UnpackSet u) {
+        const int i = blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= u.start[u.count]) return;
+        int k = 0;
+        while (k + 1 < u.count && i >= u.start[k + 1]) ++k;
+        const int j = i - u.start[k], HW4 = u.HW4[k], Cb = u.Cb[k], C = u.C[k];
+        const int q = j % HW4, t = j / HW4, cb = t % Cb, n = t / Cb;
+        const uint4 a = u.src[k][2 * j], b = u.src[k][2 * j + 1];
+        const half4 px[4] = {u2_as_h4(uint2 {a.x, a.y}), u2_as_h4(uint2 {a.z, a.w}), u2_as_h4(uint2 {b.x, b.y}), u2_as_h4(uint2 {b.z, b.w})};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int c = cb * 4 + r;
+            if (c < C) u.dst[k][((long long) n * C + c) * HW4 + q] = float4 {(float) px[0][r], (float) px[1][r], (float) px[2][r], (float) px[3][r]};
+        }
+    }
+
     // The same for H*W == 1 (a classifier's [N, C] output): NCHW is channel-contiguous, so one
     // 4-channel block (8 bytes in) is 4 consecutive floats out.
     __global__ void unpack_vec_kernel(const uint2 *src, float *dst, int C, int Cb, int total) {
@@ -536,6 +561,41 @@ int vkhip_unpack_nchw_f32(const void *src, float *dst, int64_t N, int64_t C, int
     } else
         unpack_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>((const half_t *) src, dst, C, HW, Cb, total);
     return check_launch("unpack");
+}
+
+int vkhip_unpack_nchw_f32_multi(const void *const *srcs, float *const *dsts, const int64_t *shapes, int32_t count, vkhip_stream_t s) {
+    if (!srcs || !dsts || !shapes || count < 0) return set_error(VKHIP_ERR_INVALID, "unpack_multi: bad arguments");
+    // groups of up to 8 tensors that take the quad kernel share a launch; the others go one by one
+    UnpackSet u {};
+    int64_t   total = 0;
+    auto flush = [&]() {
+        if (!u.count) return VKHIP_OK;
+        u.start[u.count] = (int) total;
+        unpack_quad_multi_kernel<<<grid1(total), 256, 0, resolve_stream(s)>>>(u);
+        u = UnpackSet {};
+        total = 0;
+        return check_launch("unpack_multi");
+    };
+    for (int32_t k = 0; k < count; ++k) {
+        const int64_t N = shapes[4 * k], C = shapes[4 * k + 1], H = shapes[4 * k + 2], W = shapes[4 * k + 3];
+        if (!srcs[k] || !dsts[k] || N <= 0 || C <= 0 || H <= 0 || W <= 0) return set_error(VKHIP_ERR_INVALID, "unpack_multi: bad arguments");
+        const int64_t Cb = ceil_div(C, 4), HW = H * W, quads = N * Cb * (HW / 4);
+        if (HW % 4 || ((uintptr_t) dsts[k] & 15) || N * Cb * HW >= INT32_MAX || total + quads >= INT32_MAX) {
+            int rc = vkhip_unpack_nchw_f32(srcs[k], dsts[k], N, C, H, W, s);
+            if (rc) return rc;
+            continue;
+        }
+        u.src[u.count] = (const uint4 *) srcs[k];
+        u.dst[u.count] = (float4 *) dsts[k];
+        u.C[u.count] = (int) C; u.Cb[u.count] = (int) Cb; u.HW4[u.count] = (int) (HW / 4);
+        u.start[u.count] = (int) total;
+        total += quads;
+        if (++u.count == 8) {
+            int rc = flush();
+            if (rc) return rc;
+        }
+    }
+    return flush();
 }
 
 static int64_t layout_elems(int fmt, int64_t N, int64_t C, int64_t H, int64_t W) {
