@@ -185,10 +185,10 @@ int vkhip_conv_tile_count(void);
  * kernels joined by '+'), as a profiler shows it; for reports, no reference counterpart. */
 const char *vkhip_conv_plan_kernel(const vkhip_conv_plan *plan);
 /* Version of the prepacked blob layouts vkhip_conv_pack_weights (and the fused-op packers) write:
- * raised whenever any layout changes. Caches of packed blobs keep it in their keys, so a blob packed
+ * raised whenever any layout or the weight rounding changes. Caches of packed blobs keep it in their keys, so a blob packed
  * by another build is never taken (no counterpart in the reference, whose blobs are keyed by node
  * and role only, vk_op_common.h). */
-#define VKHIP_PACK_FORMAT 4
+#define VKHIP_PACK_FORMAT 5
 /* Host-side prepack: fp32 OIHW weights [Cout][Cin/group][KH][KW] and optional fp32 bias[Cout]
  * into the blob the plan's kernel reads (bias stays fp32; weights become fp16, RNE). */
 int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const float *w, const float *bias, void *blob);

@@ -5,6 +5,7 @@ import os
 import re
 import subprocess
 
+import numpy as np
 import pytest
 
 import vknn_amd as V
@@ -139,6 +140,27 @@ def test_model_flops_match_survey_arithmetic():
     f = V.vknn().vknn_model_flops(b"resnet50")
     assert abs(f - 8.17e9) / 8.17e9 < 0.01
     assert abs(V.vknn().vknn_model_flops(b"conv3x3_bn_relu") - 231.2e6) / 231.2e6 < 0.001
+
+
+def test_weights_pack_with_the_reference_codec_rounding():
+    """Packed conv weights carry the reference GPU path's fp16 weights: its codec rounds half away
+    from zero (include/vknn/dtype.h:121-157), where a plain fp16 cast rounds ties to even. Ties
+    placed in the weights of a 1x1 conv (GEMM and depthwise packers, host code, no GPU needed)
+    come out as the away-from-zero neighbour, the non-tie as the nearest value."""
+    lib = V.vkhip()
+    ties = np.array([1 + 2.0 ** -11, -(1 + 2.0 ** -11), 2 + 2.0 ** -10, 0.1], np.float32)
+    away = np.array([1 + 2.0 ** -10, -(1 + 2.0 ** -10), 2 + 2.0 ** -9, np.float16(0.1)], np.float32)
+    assert (np.float16(ties[:3]).astype(np.float32) != away[:3]).all()  # a plain cast would differ
+    C = len(ties)
+    for group in (1, C):
+        w = np.ascontiguousarray((np.diag(ties) if group == 1 else ties.reshape(C, 1))[:, :, None, None], np.float32)
+        d = V.ConvDesc(N=1, Cin=C, H=4, W=4, Cout=C, OH=4, OW=4, KH=1, KW=1, SH=1, SW=1, PT=0, PL=0, DH=1, DW=1, group=group)
+        plan = V.ConvPlan()
+        assert lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_DEPTHWISE if group > 1 else V.CONV_GEMM, -1, 0, ctypes.byref(plan)) == 0
+        blob = np.zeros(plan.weight_bytes, np.uint8)
+        assert lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(plan), w.ctypes.data, None, blob.ctypes.data) == 0
+        halves = blob.view(np.float16).astype(np.float32)
+        assert sorted(halves[halves != 0]) == sorted(away), group
 
 
 def test_noalloc_refuses_plan_for_another_shape():

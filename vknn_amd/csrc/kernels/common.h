@@ -42,6 +42,27 @@ namespace vkhip {
         return (r == 0.f || q2 != q2) ? q : q2;
     }
 
+    // fp32 -> fp16 bits with the reference codec's rounding (include/vknn/dtype.h:121-157): half away
+    // from zero on the dropped mantissa bits (a carry may ripple into the exponent), subnormals
+    // likewise, overflow to infinity, NaN kept quiet. The reference's GPU path converts conv weights
+    // this way (src/backend/vulkan/ops/conv.cpp:364-437), so every weight blob packed here does too
+    // (ref_half), and the input pack uses it for the reference host codec's bit-exact NC4HW4 image.
+    __host__ __device__ inline uint16_t ref_half_bits(float v) {
+        const uint32_t bits = __builtin_bit_cast(uint32_t, v);
+        const uint32_t sign = (bits >> 16) & 0x8000u;
+        const uint32_t fexp = (bits >> 23) & 0xFFu;
+        const uint32_t man  = bits & 0x7FFFFFu;
+        if (fexp == 0xFFu) return (uint16_t) (sign | 0x7C00u | (man ? 0x200u : 0u));
+        const int e = (int) fexp - 112;
+        if (e >= 31) return (uint16_t) (sign | 0x7C00u);
+        if (e > 0) return (uint16_t) ((sign | ((uint32_t) e << 10) | (man >> 13)) + ((man >> 12) & 1u));
+        if (e < -10) return (uint16_t) sign;
+        const uint32_t full = man | 0x800000u;
+        const uint32_t sh   = (uint32_t) (14 - e);
+        return (uint16_t) (sign | ((full >> sh) + ((full >> (sh - 1)) & 1u)));
+    }
+    __host__ __device__ inline half_t ref_half(float v) { return __builtin_bit_cast(half_t, ref_half_bits(v)); }
+
     // Fused activation (codes = vknn ActType). The formulas follow the reference's applyAct
     // (src/backend/cpu/cpu_backend.cpp:33-72): HardSwish = v*clamp(v+3,0,6)/6, SiLU = v/(1+e^-v).
     __device__ __forceinline__ float apply_act(float v, int act, float lo, float hi) {

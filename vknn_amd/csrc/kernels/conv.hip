@@ -1043,7 +1043,7 @@ int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
             if (bias) b[c] = bias[c];
             for (int ky = 0; ky < d->KH; ++ky)
                 for (int kx = 0; kx < d->KW; ++kx)
-                    wp[(((int64_t) (c / 4) * d->KH + ky) * d->KW + kx) * 4 + c % 4] = (half_t) w[((int64_t) c * d->KH + ky) * d->KW + kx];
+                    wp[(((int64_t) (c / 4) * d->KH + ky) * d->KW + kx) * 4 + c % 4] = ref_half(w[((int64_t) c * d->KH + ky) * d->KW + kx]);
         }
         return VKHIP_OK;
     }
@@ -1059,7 +1059,7 @@ int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
                 for (int ky = 0; ky < d->KH; ++ky)
                     for (int kx = 0; kx < d->KW; ++kx) {
                         int64_t slot = ((int64_t) ky * d->KW + kx) * g.Cinb + ic / 4;
-                        wp[tiled_index(g, kTiles[plan->tile], oc, slot * 4 + ic % 4)] = (half_t) w[(((int64_t) oc * d->Cin + ic) * d->KH + ky) * d->KW + kx];
+                        wp[tiled_index(g, kTiles[plan->tile], oc, slot * 4 + ic % 4)] = ref_half(w[(((int64_t) oc * d->Cin + ic) * d->KH + ky) * d->KW + kx]);
                     }
         return VKHIP_OK;
     }
@@ -1075,7 +1075,7 @@ int vkhip_conv_pack_weights(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
             for (int i = 0; i < 4; ++i)
                 for (int j = 0; j < 4; ++j) {
                     float u = Gg[i][0] * G[j][0] + Gg[i][1] * G[j][1] + Gg[i][2] * G[j][2];
-                    wp[(i * 4 + j) * plane + tiled_index(g, kTiles[plan->tile], oc, ic)] = (half_t) u;
+                    wp[(i * 4 + j) * plane + tiled_index(g, kTiles[plan->tile], oc, ic)] = ref_half(u);
                 }
         }
     return VKHIP_OK;
@@ -1630,7 +1630,7 @@ int vkhip_convpw_pack_weights(const vkhip_convpw_desc *d, const vkhip_conv_plan 
                     const int64_t m = f * 32 + (l & 31);
                     const int     i = (int) (s / 2), h = (int) (s % 2), g = l >> 5;
                     const int     ch = i * 32 + (2 * h + t / 4) * 8 + 4 * g + t % 4;
-                    if (m < d->Cout) wp[((f * L.steps + s) * 64 + l) * 8 + t] = (half_t) w1[m * Cmid + ch];
+                    if (m < d->Cout) wp[((f * L.steps + s) * 64 + l) * 8 + t] = ref_half(w1[m * Cmid + ch]);
                 }
     return VKHIP_OK;
 }
@@ -1682,7 +1682,7 @@ int vkhip_convpw2_pack_weights(const vkhip_convpw2_desc *d, const vkhip_conv_pla
                     const int64_t row = m * 32 + (l & 31);
                     const int     c = (int) (st / 2), h = (int) (st % 2), g = l >> 5;
                     const int     k = c * 32 + (2 * h + t / 4) * 8 + 4 * g + t % 4;
-                    if (row < d->Cout3 && k < K2) wp[((m * 2 * ch.pair.nchunks + st) * 64 + l) * 8 + t] = (half_t) w2[row * K2 + k];
+                    if (row < d->Cout3 && k < K2) wp[((m * 2 * ch.pair.nchunks + st) * 64 + l) * 8 + t] = ref_half(w2[row * K2 + k]);
                 }
     return VKHIP_OK;
 }

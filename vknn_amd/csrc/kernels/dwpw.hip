@@ -940,12 +940,12 @@ int vkhip_dwpw_pack_weights(const vkhip_dwpw_desc *d, const float *dw_w, const f
             for (int kx = 0; kx < KW; ++kx) {
                 const int64_t i = (((int64_t) (c / 4) * KH + ky) * KW + kx) * 4 + c % 4;
                 dww[i] = dw_w[((int64_t) c * KH + ky) * KW + kx];
-                dwh[i] = (half_t) dww[i];
+                dwh[i] = ref_half(dww[i]);
             }
     }
     for (int oc = 0; oc < d->Cout; ++oc) {
         if (pw_b) pwb[oc] = pw_b[oc];
-        for (int e = 0; e < E; ++e) pww[(int64_t) oc * g.Kp + e] = (half_t) pw_w[(int64_t) oc * E + e];
+        for (int e = 0; e < E; ++e) pww[(int64_t) oc * g.Kp + e] = ref_half(pw_w[(int64_t) oc * E + e]);
     }
     return VKHIP_OK;
 }
@@ -1040,7 +1040,7 @@ int vkhip_fc_pack_weights(int64_t K, int64_t M, const float *w, int32_t transB, 
     // Gemm B is [K][M] unless transB ([M][K]); alpha scales it and beta the bias, in fp32 before
     // the fp16 conversion (reference cpu/ops/gemm.cpp applies them to the fp32 product).
     for (int64_t m = 0; m < M; ++m) {
-        for (int64_t k = 0; k < K; ++k) wp[m * Kp + k] = (half_t) (alpha * (transB ? w[m * K + k] : w[k * M + m]));
+        for (int64_t k = 0; k < K; ++k) wp[m * Kp + k] = ref_half(alpha * (transB ? w[m * K + k] : w[k * M + m]));
         bp[m] = b ? beta * b[m] : 0.f;
     }
     return VKHIP_OK;

@@ -8,22 +8,8 @@
 
 namespace vkhip {
 
-    // fp32 -> fp16 with the reference host codec's integer rounding (include/vknn/dtype.h:121-157):
-    // half-away-from-zero on the dropped bits, carries may ripple into the exponent.
-    __device__ __forceinline__ uint16_t ref_float_to_half(float v) {
-        uint32_t bits = __float_as_uint(v);
-        uint32_t sign = (bits >> 16) & 0x8000u;
-        uint32_t fexp = (bits >> 23) & 0xFFu;
-        uint32_t man  = bits & 0x7FFFFFu;
-        if (fexp == 0xFFu) return (uint16_t) (sign | 0x7C00u | (man ? 0x200u : 0u));
-        int e = (int) fexp - 112;
-        if (e >= 31) return (uint16_t) (sign | 0x7C00u);
-        if (e > 0) return (uint16_t) ((sign | ((uint32_t) e << 10) | (man >> 13)) + ((man >> 12) & 1u));
-        if (e < -10) return (uint16_t) sign;
-        uint32_t full = man | 0x800000u;
-        uint32_t sh   = (uint32_t) (14 - e);
-        return (uint16_t) (sign | ((full >> sh) + ((full >> (sh - 1)) & 1u)));
-    }
+    // fp32 -> fp16 with the reference host codec's integer rounding (ref_half_bits)
+    __device__ __forceinline__ uint16_t ref_float_to_half(float v) { return ref_half_bits(v); }
 
     // NCHW fp32 -> NC4HW4 fp16; thread = one (n, cb, pixel) 4-lane vector.
     // I = 32-bit indices when the tensor allows them (64-bit division costs ~10x a 32-bit one)
