@@ -250,6 +250,19 @@ int vkhip_conv_forward_view(const vkhip_conv_desc *d, const vkhip_conv_plan *pla
 int vkhip_conv_forward_view_res(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, int64_t x_pstride, const void *blob,
                                 const void *res, void *y, int64_t y_pstride, void *workspace, vkhip_stream_t s);
 
+/* ---------------------------------------------------------------- two 3x3 convs in one kernel
+ * y = act2(conv2(act1(conv1(x)) rounded to fp16)) (+ x when c2->has_res == 2: the residual is the
+ * pair's input, added after act2), for two dense 3x3 stride-1 pad-1 convs with 9-32 channels in,
+ * between and out (all equal) and an even width: the YOLOv8 bottleneck (cv1, cv2 and its
+ * shortcut) and the C2f head pairs. The intermediate tensor stays in LDS. Weights: each conv's
+ * blob packed by vkhip_conv_pack_weights with the plan vkhip_conv3x3_pair_plan returns for it
+ * (c2's plan is made with has_res 0). x and y may be views (plane strides as in
+ * vkhip_conv_forward_view; 0 = dense). No reference counterpart: the reference runs the two
+ * ConvCpu calls (src/backend/cpu/ops/conv.cpp:9-92) and its Add (src/backend/cpu/ops/add.cpp). */
+int vkhip_conv3x3_pair_plan(const vkhip_conv_desc *c1, const vkhip_conv_desc *c2, vkhip_conv_plan *p1, vkhip_conv_plan *p2);
+int vkhip_conv3x3_pair_forward(const vkhip_conv_desc *c1, const vkhip_conv_desc *c2, const void *x, int64_t x_pstride, const void *blob1,
+                               const void *blob2, void *y, int64_t y_pstride, vkhip_stream_t s);
+
 /* ---------------------------------------------------------------- two stride-2 stem convs in one kernel
  * y = act2(conv2(act1(conv1(x)) rounded to fp16)) for two dense 3x3 stride-2 pad-1 convs, the first
  * over at most 4 input channels to 9-16 channels, the second to at most 32 (the YOLOv8n stem,

@@ -337,6 +337,100 @@ def test_conv_view_residual(gpu, tile):
     assert lib.vkhip_conv_forward_view(ctypes.byref(d), ctypes.byref(plan), dwide.ptr, ps, dblob.ptr, dwide.ptr, ps, None, None) != 0
 
 
+def gpu_conv_pair(x, w1, b1, w2, b2, act, res, wide=None):
+    """vkhip_conv3x3_pair_forward on x (or, with wide = (Cw, in_off, out_off), on a channel slice of a
+    wider tensor holding x at channel in_off, the output written at channel out_off)."""
+    lib = V.vkhip()
+    N, C, H, W = x.shape
+    d1, _ = conv_desc(x.shape, w1.shape, (1, 1), (1, 1, 1, 1), act=act)
+    d2, yshape = conv_desc(x.shape, w2.shape, (1, 1), (1, 1, 1, 1), act=act, has_res=2 if res else 0)
+    p1, p2 = V.ConvPlan(), V.ConvPlan()
+    check(lib.vkhip_conv3x3_pair_plan(ctypes.byref(d1), ctypes.byref(d2), ctypes.byref(p1), ctypes.byref(p2)), "pair plan")
+    blobs = []
+    for d, p, w, b in ((d1, p1, w1, b1), (d2, p2, w2, b2)):
+        blob = np.zeros(p.weight_bytes, np.uint8)
+        check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(p), w.ctypes.data, b.ctypes.data, blob.ctypes.data), "pack")
+        blobs.append(DeviceBuffer.from_array(blob))
+    if wide is None:
+        dx = to_device_nc4(x)
+        dy = DeviceBuffer(V.nc4_elems(*yshape) * 2)
+        dy.zero()
+        check(lib.vkhip_conv3x3_pair_forward(ctypes.byref(d1), ctypes.byref(d2), dx.ptr, 0, blobs[0].ptr, blobs[1].ptr, dy.ptr, 0, None), "pair")
+        return from_device_nc4(dy, yshape)
+    Cw, cin, cout = wide
+    r = rng(77)
+    full = round_half(r.standard_normal((N, Cw, H, W)))
+    full[:, cin:cin + C] = x
+    dw = to_device_nc4(full)
+    plane = H * W * 8
+    check(lib.vkhip_conv3x3_pair_forward(ctypes.byref(d1), ctypes.byref(d2), dw.ptr + cin // 4 * plane, Cw // 4, blobs[0].ptr, blobs[1].ptr,
+                                         dw.ptr + cout // 4 * plane, Cw // 4, None), "pair view")
+    out = from_device_nc4(dw, full.shape)
+    keep = [c for c in range(Cw) if not cout <= c < cout + C]
+    assert np.array_equal(out[:, keep], full[:, keep])  # nothing outside the output slice changes
+    return out[:, cout:cout + C]
+
+
+def oracle_pair(x, w1, b1, w2, b2, act, res):
+    t = round_half(oracle_conv(x, w1, b1, (1, 1), (1, 1, 1, 1), act=act))
+    y = oracle_conv(t, w2, b2, (1, 1), (1, 1, 1, 1), act=act)
+    return round_half(y) + x if res else y
+
+
+PAIR_CASES = [(2, 16, 20, 36, 5, True), (3, 32, 13, 70, 5, True), (2, 24, 9, 18, 1, False), (1, 12, 5, 130, 5, True),
+              (2, 32, 33, 66, 0, False), (1, 16, 4, 64, 2, True)]
+
+
+@pytest.mark.parametrize("case", PAIR_CASES)
+def test_conv3x3_pair(gpu, case):
+    """Two 3x3 convs in one kernel (the intermediate kept in LDS, rounded to fp16 like the separate
+    conv's store), with and without the bottleneck shortcut, against the oracle's two convs (+ its
+    add): 16 and 32 channels and ragged counts (12, 24: zero slots), item rows and columns cut by
+    the image edge, several column blocks, ReLU / ReLU6 / SiLU / no activation."""
+    N, C, H, W, act, res = case
+    r = rng(1500 + C + H + W)
+    x = round_half(r.standard_normal((N, C, H, W)))
+    w1 = (r.standard_normal((C, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+    w2 = (r.standard_normal((C, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+    b1 = (r.standard_normal(C) * 0.1).astype(np.float32)
+    b2 = (r.standard_normal(C) * 0.1).astype(np.float32)
+    got = gpu_conv_pair(x, w1, b1, w2, b2, act, res)
+    assert_parity(got, oracle_pair(x, w1, b1, w2, b2, act, res), f"pair {case}")
+
+
+@pytest.mark.parametrize("C", [16, 32])
+def test_conv3x3_pair_views(gpu, C):
+    """The pair reading a channel slice of a wide tensor and writing another slice of the same
+    tensor (the C2f split half in, the concat slice out), other slices untouched."""
+    r = rng(1600 + C)
+    x = round_half(r.standard_normal((2, C, 10, 40)))
+    w1 = (r.standard_normal((C, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+    w2 = (r.standard_normal((C, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+    b1 = (r.standard_normal(C) * 0.1).astype(np.float32)
+    b2 = (r.standard_normal(C) * 0.1).astype(np.float32)
+    got = gpu_conv_pair(x, w1, b1, w2, b2, 5, True, wide=(4 * C, C, 2 * C))
+    assert_parity(got, oracle_pair(x, w1, b1, w2, b2, 5, True), f"pair views C={C}")
+
+
+def test_conv3x3_pair_refusals(gpu):
+    """Channel counts outside 9-32 or unequal, odd widths, stride 2, 1x1, a residual before the
+    activation are refused."""
+    lib = V.vkhip()
+    p1, p2 = V.ConvPlan(), V.ConvPlan()
+    def ok(x, c1w, c2w, st=(1, 1), pads=(1, 1, 1, 1), res=0):
+        d1, ys = conv_desc(x, c1w, st, pads, act=5)
+        d2, _ = conv_desc(ys, c2w, (1, 1), (1, 1, 1, 1), act=5, has_res=res)
+        return lib.vkhip_conv3x3_pair_plan(ctypes.byref(d1), ctypes.byref(d2), ctypes.byref(p1), ctypes.byref(p2)) == 0
+    assert ok((1, 16, 8, 8), (16, 16, 3, 3), (16, 16, 3, 3), res=2)
+    assert not ok((1, 40, 8, 8), (40, 40, 3, 3), (40, 40, 3, 3))
+    assert not ok((1, 8, 8, 8), (8, 8, 3, 3), (8, 8, 3, 3))
+    assert not ok((1, 16, 8, 8), (32, 16, 3, 3), (32, 32, 3, 3))
+    assert not ok((1, 16, 8, 9), (16, 16, 3, 3), (16, 16, 3, 3))
+    assert not ok((1, 16, 8, 8), (16, 16, 3, 3), (16, 16, 3, 3), st=(2, 2))
+    assert not ok((1, 16, 8, 8), (16, 16, 1, 1), (16, 16, 3, 3), pads=(0, 0, 0, 0))
+    assert not ok((1, 16, 8, 8), (16, 16, 3, 3), (16, 16, 3, 3), res=1)
+
+
 def gpu_stem2(x, w1, b1, act1, w2, b2, act2, y_wide=None):
     """vkhip_conv3x3s2_pair_forward; with y_wide = (Cw, off) the output goes to channel `off` of a
     wider zero-filled tensor, which is returned whole."""

@@ -115,6 +115,8 @@ VKHIP_API = {
     "vkhip_conv_pool_parts": (c_int, [P(ConvDesc), P(ConvPlan)]),
     "vkhip_conv_forward_view": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_vp]),
     "vkhip_conv_forward_view_res": (c_int, [P(ConvDesc), P(ConvPlan), c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp]),
+    "vkhip_conv3x3_pair_plan": (c_int, [P(ConvDesc), P(ConvDesc), P(ConvPlan), P(ConvPlan)]),
+    "vkhip_conv3x3_pair_forward": (c_int, [P(ConvDesc), P(ConvDesc), c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp]),
     "vkhip_conv3x3s2_pair_plan": (c_int, [P(ConvDesc), P(ConvDesc), P(ConvPlan), P(ConvPlan)]),
     "vkhip_conv3x3s2_pair_forward": (c_int, [P(ConvDesc), P(ConvDesc), c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),
     "vkhip_add_view": (c_int, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64, c_i32, c_f, c_f, c_vp]),

@@ -978,6 +978,46 @@ namespace vknn {
             std::string describe() const override { return "fused with " + na->name + " kernel=conv_stem2_kernel"; }
         };
 
+        // ------------------------------------------------------------ two 3x3 stride-1 convs
+        // A 3x3 conv over 9-16 channels and the 3x3 conv that is its only reader, with the Add of
+        // the first conv's input after the second's activation when there is one (the YOLOv8
+        // bottleneck), as one op at the second conv's place: vkhip_conv3x3_pair_forward, the
+        // intermediate in LDS, the shortcut taken from the input band.
+        struct PairOp: HipOp {
+            const Node             *na = nullptr; // the first conv (this op is prepared with the second)
+            TensorId                addOut = kNoTensor; // the folded Add's output, when there is one
+            vkhip_conv_desc         d1 {}, d2 {};
+            vkhip_conv_plan         p1 {}, p2 {};
+            std::shared_ptr<DevBuf> blob1, blob2;
+            TensorId                in = kNoTensor, out = kNoTensor;
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g = *env.graph;
+                d1 = convDescOf(g, *na);
+                d2 = convDescOf(g, node);
+                if (addOut != kNoTensor) d2.has_res = 2;
+                in  = na->inputs[0];
+                out = addOut != kNoTensor ? addOut : node.outputs[0];
+                check(vkhip_conv3x3_pair_plan(&d1, &d2, &p1, &p2), "conv pair plan " + name);
+                vkhip_conv_desc e2 = d2;
+                e2.has_res = 0;
+                std::vector<uint8_t> h1(p1.weight_bytes), h2(p2.weight_bytes);
+                check(vkhip_conv_pack_weights(&d1, &p1, initF32(g, na->inputs[1]), initF32(g, biasOf(*na)), h1.data()), "conv pair pack");
+                check(vkhip_conv_pack_weights(&e2, &p2, initF32(g, node.inputs[1]), initF32(g, biasOf(node)), h2.data()), "conv pair pack");
+                blob1 = upload(h1.data(), h1.size());
+                blob2 = upload(h2.data(), h2.size());
+                kind  = "conv";
+                flops = 2.0 * 9 * d1.N * d1.OH * d1.OW * ((double) d1.Cout * d1.Cin + (double) d2.Cout * d2.Cin);
+                bytes = (int64_t) (nc4Bytes(g.desc(in).shape) + nc4Bytes(g.desc(out).shape)) + (int64_t) (d1.Cout * d1.Cin + d2.Cout * d2.Cin) * 9 * 2;
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                check(vkhip_conv3x3_pair_forward(&d1, &d2, env.dev(in), env.pstride(in), blob1->ptr, blob2->ptr, env.dev(out), env.pstride(out), s),
+                      "conv pair " + name);
+            }
+            std::string describe() const override {
+                return "fused with " + na->name + (addOut != kNoTensor ? " (+ its input after the activation)" : "") + " kernel=conv_pair_kernel";
+            }
+        };
+
         // ------------------------------------------------------------ fused 3x3 + 1x1
         // A 3x3 conv whose only reader is a 1x1 conv (a bottleneck's middle conv and its expansion)
         // as one op at the 1x1's place in the order (its residual, e.g. a projection shortcut, may be
@@ -1667,6 +1707,63 @@ namespace vknn {
                     }
                 }
             }
+            // Two 3x3 stride-1 convs over 9-16 channels (+ the Add of the first one's input) as one
+            // op (PairOp): second conv -> first; VKNN_HIP_FUSE_PAIR=0 keeps them apart (A/B). At 32
+            // channels the halo tiles the tuner picks for the two convs are as fast as the pair.
+            std::map<int, int> pairOf; // second conv -> first conv
+            std::set<int>      pairFolded;
+            {
+                const char *pr_env = std::getenv("VKNN_HIP_FUSE_PAIR");
+                if (!pr_env || std::string(pr_env) != "0") {
+                    std::set<int> skip(folded.begin(), folded.end());
+                    for (auto &kv: scaled) skip.insert(kv.first);
+                    for (auto &kv: convPool) skip.insert(kv.first), skip.insert(kv.second);
+                    for (auto &kv: gapConv) skip.insert(kv.second);
+                    for (auto &kv: pwPairs) skip.insert(kv.first);
+                    skip.insert(pwFolded.begin(), pwFolded.end());
+                    skip.insert(pwChained.begin(), pwChained.end());
+                    for (auto &kv: actConv) skip.insert(kv.first);
+                    skip.insert(stem2Folded.begin(), stem2Folded.end());
+                    for (auto &kv: stem2Of) skip.insert(kv.first);
+                    std::map<TensorId, int> readers, producer;
+                    for (size_t i = 0; i < g.nodes.size(); ++i) {
+                        for (TensorId t: g.nodes[i].inputs)
+                            if (t != kNoTensor) ++readers[t];
+                        if (g.nodes[i].fusedResidual != kNoTensor) ++readers[g.nodes[i].fusedResidual];
+                        for (TensorId t: g.nodes[i].outputs)
+                            if (t != kNoTensor) producer[t] = (int) i;
+                    }
+                    for (TensorId t: g.outputs) readers[t] += 1000;
+                    std::set<int> inSeg(idx.begin(), idx.end());
+                    for (int b: idx) {
+                        const Node &nb = g.nodes[b];
+                        if (skip.count(b) || nb.type != OpType::Conv || nb.inputs.size() < 2 || !g.isInitializer(nb.inputs[1]) ||
+                            nb.fusedResidual != kNoTensor || g.desc(nb.inputs[1]).shape.size() != 4)
+                            continue;
+                        const TensorId t = nb.inputs[0];
+                        auto           pa = producer.find(t);
+                        if (pa == producer.end() || !inSeg.count(pa->second) || skip.count(pa->second) || pairFolded.count(pa->second) ||
+                            pairOf.count(pa->second) || readers[t] != 1 || addConv.count(pa->second))
+                            continue;
+                        const Node &na = g.nodes[pa->second];
+                        if (na.type != OpType::Conv || na.inputs.size() < 2 || !g.isInitializer(na.inputs[1]) || na.fusedResidual != kNoTensor ||
+                            g.desc(na.inputs[1]).shape.size() != 4 || place_.count(resolve(t)) || pstride(t) > 0)
+                            continue;
+                        vkhip_conv_desc d1 = convDescOf(g, na), d2 = convDescOf(g, nb);
+                        if (d1.Cin > 16) continue;
+                        // a folded Add: only the one whose residual is the pair's input
+                        auto ad = addConv.find(b);
+                        if (ad != addConv.end()) {
+                            if (addFold[ad->second].second != na.inputs[0]) continue;
+                            d2.has_res = 2;
+                        }
+                        vkhip_conv_plan q1, q2;
+                        if (vkhip_conv3x3_pair_plan(&d1, &d2, &q1, &q2) != VKHIP_OK) continue;
+                        pairOf[b] = pa->second;
+                        pairFolded.insert(pa->second);
+                    }
+                }
+            }
             // Device buffers: one NC4HW4 fp16 buffer per activation (aliases share their source's;
             // a tensor placed in another one by planViews has none of its own).
             for (int i: idx) {
@@ -1713,6 +1810,18 @@ namespace vknn {
                     f->what = "hard-sigmoid";
                     f->into = g.nodes[actFold[i]].name;
                     op      = std::move(f);
+                } else if (pairFolded.count(i)) {
+                    auto f = std::make_unique<FoldedMulOp>();
+                    f->what = "3x3 conv: runs with the 3x3 conv that reads it,";
+                    for (auto &kv: pairOf)
+                        if (kv.second == i) f->into = g.nodes[kv.first].name;
+                    op = std::move(f);
+                } else if (pairOf.count(i)) {
+                    auto c = std::make_unique<PairOp>();
+                    c->na  = &g.nodes[pairOf[i]];
+                    auto ad = addConv.find(i);
+                    if (ad != addConv.end()) c->addOut = g.nodes[ad->second].outputs[0];
+                    op = std::move(c);
                 } else if (poolChained.count(i)) {
                     auto f  = std::make_unique<FoldedMulOp>();
                     f->what = "max pool: computed in the launch of the chain's first pool,";
@@ -1774,7 +1883,7 @@ namespace vknn {
                     auto *m = static_cast<MaxPoolOp *>(op.get());
                     for (int c: pcit->second) m->chain.push_back(g.nodes[c].outputs[0]);
                 }
-                auto dit = addConv.find(i);
+                auto dit = pairOf.count(i) ? addConv.end() : addConv.find(i); // a pair op takes its Add itself
                 if (dit != addConv.end()) {
                     auto *c    = static_cast<ConvOp *>(op.get());
                     c->addOut  = g.nodes[dit->second].outputs[0];
@@ -1792,7 +1901,8 @@ namespace vknn {
                 op->name = nd.name;
                 op->type = nd.type;
                 const bool gapFolded = gapParts.count(i) > 0;
-                const bool pwOp = pwPairs.count(i) || pwFolded.count(i) || pwChained.count(i) || stem2Of.count(i) || stem2Folded.count(i);
+                const bool pwOp = pwPairs.count(i) || pwFolded.count(i) || pwChained.count(i) || stem2Of.count(i) || stem2Folded.count(i) ||
+                                  pairOf.count(i) || pairFolded.count(i);
                 if (nd.type == OpType::Conv && !inPlace && !gapFolded && !folded.count(i) && !pools.count(i) && !pwOp) {
                     bool v = false;
                     for (TensorId t: {nd.inputs[0], nd.outputs[0]}) v = v || pstride(t) > 0;
@@ -1834,7 +1944,16 @@ namespace vknn {
                     continue;
                 }
                 if (folded.count(i) || pools.count(i) || pwFolded.count(i) || pwChained.count(i) || actFold.count(i) || addFold.count(i) ||
-                    stem2Folded.count(i) || poolChained.count(i)) {
+                    stem2Folded.count(i) || poolChained.count(i) || pairFolded.count(i)) {
+                    ins.push_back(in);
+                    outs.push_back(out);
+                    continue;
+                }
+                if (pairOf.count(i)) {
+                    // the pair reads the first conv's input and writes the second's output (or the Add's)
+                    in.push_back(resolve(g.nodes[pairOf[i]].inputs[0]));
+                    auto ad = addConv.find(i);
+                    out.push_back(resolve(ad != addConv.end() ? g.nodes[ad->second].outputs[0] : nd.outputs[0]));
                     ins.push_back(in);
                     outs.push_back(out);
                     continue;
