@@ -266,13 +266,17 @@ int vkhip_conv3x3_pair_forward(const vkhip_conv_desc *c1, const vkhip_conv_desc 
 /* ---------------------------------------------------------------- two stride-2 stem convs in one kernel
  * y = act2(conv2(act1(conv1(x)) rounded to fp16)) for two dense 3x3 stride-2 pad-1 convs, the first
  * over at most 4 input channels to 9-16 channels, the second to at most 32 (the YOLOv8n stem,
- * 3 -> 16 -> 32), with an even input width; the intermediate tensor stays in LDS. x is a dense
- * NC4HW4 tensor; y may be a view (`y_pstride` channel blocks per image; 0 = dense). Weights: each
- * conv's blob packed by vkhip_conv_pack_weights with the plan vkhip_conv3x3s2_pair_plan returns.
- * No reference counterpart: the reference runs two ConvCpu calls (src/backend/cpu/ops/conv.cpp:9-92). */
-int vkhip_conv3x3s2_pair_plan(const vkhip_conv_desc *c1, const vkhip_conv_desc *c2, vkhip_conv_plan *p1, vkhip_conv_plan *p2);
-int vkhip_conv3x3s2_pair_forward(const vkhip_conv_desc *c1, const vkhip_conv_desc *c2, const void *x, const void *blob1, const void *blob2, void *y,
-                                 int64_t y_pstride, vkhip_stream_t s);
+ * 3 -> 16 -> 32), with an even input width; the intermediate tensor stays in LDS. With c3 (else
+ * NULL): a dense 1x1 conv over the second conv's output (at most 32 out, the next layer when it is
+ * the second conv's only reader) runs in the same kernel, y is its output and the second conv's
+ * output stays in LDS too. x is a dense NC4HW4 tensor; y may be a view (`y_pstride` channel blocks
+ * per image; 0 = dense). Weights: each conv's blob packed by vkhip_conv_pack_weights with the plan
+ * vkhip_conv3x3s2_pair_plan returns for it. No reference counterpart: the reference runs the
+ * ConvCpu calls one by one (src/backend/cpu/ops/conv.cpp:9-92). */
+int vkhip_conv3x3s2_pair_plan(const vkhip_conv_desc *c1, const vkhip_conv_desc *c2, const vkhip_conv_desc *c3, vkhip_conv_plan *p1,
+                              vkhip_conv_plan *p2, vkhip_conv_plan *p3);
+int vkhip_conv3x3s2_pair_forward(const vkhip_conv_desc *c1, const vkhip_conv_desc *c2, const vkhip_conv_desc *c3, const void *x, const void *blob1,
+                                 const void *blob2, const void *blob3, void *y, int64_t y_pstride, vkhip_stream_t s);
 
 int vkhip_conv_forward_noalloc(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob,
                                const void *res, void *y, vkhip_stream_t s);

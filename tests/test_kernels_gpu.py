@@ -431,27 +431,29 @@ def test_conv3x3_pair_refusals(gpu):
     assert not ok((1, 16, 8, 8), (16, 16, 3, 3), (16, 16, 3, 3), res=1)
 
 
-def gpu_stem2(x, w1, b1, act1, w2, b2, act2, y_wide=None):
+def gpu_stem2(x, w1, b1, act1, w2, b2, act2, y_wide=None, tail=None):
     """vkhip_conv3x3s2_pair_forward; with y_wide = (Cw, off) the output goes to channel `off` of a
-    wider zero-filled tensor, which is returned whole."""
+    wider zero-filled tensor, which is returned whole; tail = (w3, b3, act3) adds the 1x1 tail."""
     lib = V.vkhip()
     d1, ys1 = conv_desc(x.shape, w1.shape, (2, 2), (1, 1, 1, 1), act=act1)
     d2, ys2 = conv_desc(ys1, w2.shape, (2, 2), (1, 1, 1, 1), act=act2)
-    p1, p2 = V.ConvPlan(), V.ConvPlan()
-    check(lib.vkhip_conv3x3s2_pair_plan(ctypes.byref(d1), ctypes.byref(d2), ctypes.byref(p1), ctypes.byref(p2)), "stem2 plan")
+    d3, ys3 = conv_desc(ys2, tail[0].shape, act=tail[2]) if tail else (None, ys2)
+    p1, p2, p3 = V.ConvPlan(), V.ConvPlan(), V.ConvPlan()
+    r3 = ctypes.byref(d3) if tail else None
+    check(lib.vkhip_conv3x3s2_pair_plan(ctypes.byref(d1), ctypes.byref(d2), r3, ctypes.byref(p1), ctypes.byref(p2), ctypes.byref(p3)), "stem2 plan")
     blobs = []
-    for d, p, w, b in ((d1, p1, w1, b1), (d2, p2, w2, b2)):
+    for d, p, w, b in ((d1, p1, w1, b1), (d2, p2, w2, b2)) + (((d3, p3, tail[0], tail[1]),) if tail else ()):
         blob = np.zeros(p.weight_bytes, np.uint8)
         check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(p), w.ctypes.data, b.ctypes.data, blob.ctypes.data), "pack")
         blobs.append(DeviceBuffer.from_array(blob))
     dx = to_device_nc4(x)
-    N, C2, H2, W2 = ys2
-    shape = ys2 if y_wide is None else (N, y_wide[0], H2, W2)
+    N, C2, H2, W2 = ys3
+    shape = ys3 if y_wide is None else (N, y_wide[0], H2, W2)
     dy = DeviceBuffer(V.nc4_elems(*shape) * 2)
     dy.zero()
     off = 0 if y_wide is None else y_wide[1] // 4 * H2 * W2 * 8
-    check(lib.vkhip_conv3x3s2_pair_forward(ctypes.byref(d1), ctypes.byref(d2), dx.ptr, blobs[0].ptr, blobs[1].ptr, dy.ptr + off,
-                                           0 if y_wide is None else y_wide[0] // 4, None), "stem2")
+    check(lib.vkhip_conv3x3s2_pair_forward(ctypes.byref(d1), ctypes.byref(d2), r3, dx.ptr, blobs[0].ptr, blobs[1].ptr,
+                                           blobs[2].ptr if tail else None, dy.ptr + off, 0 if y_wide is None else y_wide[0] // 4, None), "stem2")
     check(lib.vkhip_stream_sync(None), "sync")
     return from_device_nc4(dy, shape)
 
@@ -460,12 +462,14 @@ STEM2_CASES = [(2, 3, 64, 96, 16, 32, 5), (1, 3, 50, 130, 16, 32, 5), (3, 4, 22,
                (1, 3, 9, 8, 10, 7, 2), (2, 3, 640, 640, 16, 32, 5)]
 
 
+@pytest.mark.parametrize("tail", [None, 32, 20])
 @pytest.mark.parametrize("case", STEM2_CASES)
-def test_conv3x3s2_pair(gpu, case):
+def test_conv3x3s2_pair(gpu, case, tail):
     """The two stride-2 stem convs in one kernel (the intermediate in LDS, rounded to fp16 like
-    the separate conv's store) against the oracle's two convs: the YOLOv8n stem at full size,
-    odd intermediate and output sizes, items cut by the image edge, ragged channel counts (1, 4
-    in; 10, 12 between; 7, 24 out), SiLU / ReLU / ReLU6 / hard-swish."""
+    the separate conv's store) against the oracle's two convs, and with the 1x1 tail conv over
+    the second conv's output (its output in LDS too; 32 or 20 channels out): the YOLOv8n stem at
+    full size, odd intermediate and output sizes, items cut by the image edge, ragged channel
+    counts (1, 4 in; 10, 12 between; 7, 24 out), SiLU / ReLU / ReLU6 / hard-swish."""
     N, C, H, W, C1, C2, act = case
     r = rng(1700 + C + H + W + C1 + C2)
     x = round_half(r.standard_normal((N, C, H, W)))
@@ -473,35 +477,49 @@ def test_conv3x3s2_pair(gpu, case):
     w2 = (r.standard_normal((C2, C1, 3, 3)) * np.sqrt(2.0 / (9 * C1))).astype(np.float32)
     b1 = (r.standard_normal(C1) * 0.1).astype(np.float32)
     b2 = (r.standard_normal(C2) * 0.1).astype(np.float32)
-    got = gpu_stem2(x, w1, b1, act, w2, b2, act)
     t = round_half(oracle_conv(x, w1, b1, (2, 2), (1, 1, 1, 1), act=act))
-    assert_parity(got, oracle_conv(t, w2, b2, (2, 2), (1, 1, 1, 1), act=act), f"stem2 {case}")
+    ref = oracle_conv(t, w2, b2, (2, 2), (1, 1, 1, 1), act=act)
+    if tail:
+        w3 = (r.standard_normal((tail, C2, 1, 1)) * np.sqrt(2.0 / C2)).astype(np.float32)
+        b3 = (r.standard_normal(tail) * 0.1).astype(np.float32)
+        got = gpu_stem2(x, w1, b1, act, w2, b2, act, tail=(w3, b3, act))
+        ref = oracle_conv(round_half(ref), w3, b3, act=act)
+    else:
+        got = gpu_stem2(x, w1, b1, act, w2, b2, act)
+    assert_parity(got, ref, f"stem2 {case} tail {tail}")
 
 
 def test_conv3x3s2_pair_view_and_refusals(gpu):
-    """The output written into a channel slice of a wider tensor (other slices stay zero); shapes
-    outside the kernel's range are refused."""
+    """The output written into a channel slice of a wider tensor (other slices stay zero), with and
+    without the tail; shapes outside the kernel's range are refused."""
     r = rng(1800)
     x = round_half(r.standard_normal((2, 3, 40, 64)))
     w1 = (r.standard_normal((16, 3, 3, 3)) * 0.3).astype(np.float32)
     w2 = (r.standard_normal((32, 16, 3, 3)) * 0.1).astype(np.float32)
-    b1, b2 = np.zeros(16, np.float32), np.zeros(32, np.float32)
-    got = gpu_stem2(x, w1, b1, 5, w2, b2, 5, y_wide=(64, 16))
+    w3 = (r.standard_normal((32, 32, 1, 1)) * 0.2).astype(np.float32)
+    b1, b2, b3 = np.zeros(16, np.float32), np.zeros(32, np.float32), np.zeros(32, np.float32)
     t = round_half(oracle_conv(x, w1, b1, (2, 2), (1, 1, 1, 1), act=5))
-    assert_parity(got[:, 16:48], oracle_conv(t, w2, b2, (2, 2), (1, 1, 1, 1), act=5), "stem2 view")
-    assert not got[:, :16].any() and not got[:, 48:].any()
+    ref = oracle_conv(t, w2, b2, (2, 2), (1, 1, 1, 1), act=5)
+    for tail, want in ((None, ref), ((w3, b3, 5), oracle_conv(round_half(ref), w3, b3, act=5))):
+        got = gpu_stem2(x, w1, b1, 5, w2, b2, 5, y_wide=(64, 16), tail=tail)
+        assert_parity(got[:, 16:48], want, f"stem2 view tail {tail is not None}")
+        assert not got[:, :16].any() and not got[:, 48:].any()
     lib = V.vkhip()
-    p1, p2 = V.ConvPlan(), V.ConvPlan()
-    def ok(xs, c1, c2, s1=2, s2=2):
+    p1, p2, p3 = V.ConvPlan(), V.ConvPlan(), V.ConvPlan()
+    def ok(xs, c1, c2, s1=2, s2=2, c3=None, k3=1):
         d1, ys = conv_desc(xs, (c1, xs[1], 3, 3), (s1, s1), (1, 1, 1, 1))
-        d2, _ = conv_desc(ys, (c2, c1, 3, 3), (s2, s2), (1, 1, 1, 1))
-        return lib.vkhip_conv3x3s2_pair_plan(ctypes.byref(d1), ctypes.byref(d2), ctypes.byref(p1), ctypes.byref(p2)) == 0
-    assert ok((1, 3, 32, 32), 16, 32)
+        d2, ys2 = conv_desc(ys, (c2, c1, 3, 3), (s2, s2), (1, 1, 1, 1))
+        d3 = conv_desc(ys2, (c3, c2, k3, k3), pads=(k3 // 2,) * 4)[0] if c3 else None
+        return lib.vkhip_conv3x3s2_pair_plan(ctypes.byref(d1), ctypes.byref(d2), ctypes.byref(d3) if d3 else None, ctypes.byref(p1),
+                                             ctypes.byref(p2), ctypes.byref(p3)) == 0
+    assert ok((1, 3, 32, 32), 16, 32) and ok((1, 3, 32, 32), 16, 32, c3=32)
     assert not ok((1, 8, 32, 32), 16, 32)      # more than 4 input channels
     assert not ok((1, 3, 32, 32), 32, 32)      # more than 16 between
     assert not ok((1, 3, 32, 32), 16, 64)      # more than 32 out
     assert not ok((1, 3, 32, 33), 16, 32)      # odd input width
     assert not ok((1, 3, 32, 32), 16, 32, s2=1)
+    assert not ok((1, 3, 32, 32), 16, 32, c3=64)       # tail wider than 32
+    assert not ok((1, 3, 32, 32), 16, 32, c3=32, k3=3)  # tail not 1x1
 
 
 @pytest.mark.parametrize("tile", PERS_TILES)

@@ -188,13 +188,14 @@ def test_squeeze_excite_fused_by_default(gpu, monkeypatch):
 
 
 def test_stem_convs_and_pool_chain_fused(gpu, monkeypatch):
-    """YOLOv8n's two stride-2 stem convs (3 -> 16 -> 32) run as one kernel with the 16-channel
-    intermediate in LDS, the three SPPF pools as one launch, and the 16-channel bottleneck's two
+    """YOLOv8n's two stride-2 stem convs (3 -> 16 -> 32) and the 1x1 after them run as one kernel
+    with both intermediates in LDS, the three SPPF pools as one launch, and the 16-channel bottleneck's two
     3x3 convs and shortcut as one kernel; the result matches the oracle and the session with none
     of them."""
     sess = V.Session("yolov8n", 1, seed=7)
     plan = sess.describe()
     assert plan.count("runs with the stride-2 conv that reads it") == 1 and "conv_stem2_kernel" in plan, plan
+    assert plan.count("runs as the tail of the stride-2 pair") == 1, plan
     assert plan.count("+2 chained pools in one launch") == 1 and plan.count("computed in the launch of the chain's first pool") == 2, plan
     assert plan.count("kernel=conv_pair_kernel") == 1 and plan.count("runs with the 3x3 conv that reads it") == 1, plan
     x = make_input(sess.in_shape, 7)

@@ -952,30 +952,40 @@ namespace vknn {
         // the thin tiles' blobs; no plan search (one kernel).
         struct Stem2Op: HipOp {
             const Node             *na = nullptr; // the first conv (this op is prepared with the second)
-            vkhip_conv_desc         d1 {}, d2 {};
-            vkhip_conv_plan         p1 {}, p2 {};
-            std::shared_ptr<DevBuf> blob1, blob2;
+            const Node             *nc = nullptr; // optional 1x1 tail: the second conv's only reader
+            vkhip_conv_desc         d1 {}, d2 {}, d3 {};
+            vkhip_conv_plan         p1 {}, p2 {}, p3 {};
+            std::shared_ptr<DevBuf> blob1, blob2, blob3;
             TensorId                in = kNoTensor, out = kNoTensor;
             void prepare(const Node &node, SegEnv &env) override {
                 const Graph &g = *env.graph;
                 d1 = convDescOf(g, *na);
                 d2 = convDescOf(g, node);
+                if (nc) d3 = convDescOf(g, *nc);
                 in = na->inputs[0];
-                out = node.outputs[0];
-                check(vkhip_conv3x3s2_pair_plan(&d1, &d2, &p1, &p2), "stem pair plan " + name);
-                std::vector<uint8_t> h1(p1.weight_bytes), h2(p2.weight_bytes);
+                out = nc ? nc->outputs[0] : node.outputs[0];
+                check(vkhip_conv3x3s2_pair_plan(&d1, &d2, nc ? &d3 : nullptr, &p1, &p2, &p3), "stem pair plan " + name);
+                std::vector<uint8_t> h1(p1.weight_bytes), h2(p2.weight_bytes), h3(nc ? p3.weight_bytes : 0);
                 check(vkhip_conv_pack_weights(&d1, &p1, initF32(g, na->inputs[1]), initF32(g, biasOf(*na)), h1.data()), "stem pair pack");
                 check(vkhip_conv_pack_weights(&d2, &p2, initF32(g, node.inputs[1]), initF32(g, biasOf(node)), h2.data()), "stem pair pack");
+                if (nc) check(vkhip_conv_pack_weights(&d3, &p3, initF32(g, nc->inputs[1]), initF32(g, biasOf(*nc)), h3.data()), "stem pair pack");
                 blob1 = upload(h1.data(), h1.size());
                 blob2 = upload(h2.data(), h2.size());
+                if (nc) blob3 = upload(h3.data(), h3.size());
                 kind  = "conv";
-                flops = 2.0 * d1.N * d1.Cout * d1.Cin * 9 * d1.OH * d1.OW + 2.0 * d2.N * d2.Cout * d2.Cin * 9 * d2.OH * d2.OW;
-                bytes = (int64_t) (nc4Bytes(g.desc(in).shape) + nc4Bytes(g.desc(out).shape)) + (int64_t) (d1.Cout * d1.Cin + d2.Cout * d2.Cin) * 9 * 2;
+                flops = 2.0 * d1.N * d1.Cout * d1.Cin * 9 * d1.OH * d1.OW + 2.0 * d2.N * d2.Cout * d2.Cin * 9 * d2.OH * d2.OW +
+                        (nc ? 2.0 * d3.N * d3.Cout * d3.Cin * d3.OH * d3.OW : 0.0);
+                bytes = (int64_t) (nc4Bytes(g.desc(in).shape) + nc4Bytes(g.desc(out).shape)) +
+                        (int64_t) (d1.Cout * d1.Cin + d2.Cout * d2.Cin) * 9 * 2 + (nc ? (int64_t) d3.Cout * d3.Cin * 2 : 0);
             }
             void record(SegEnv &env, vkhip_stream_t s) override {
-                check(vkhip_conv3x3s2_pair_forward(&d1, &d2, env.dev(in), blob1->ptr, blob2->ptr, env.dev(out), env.pstride(out), s), "stem pair " + name);
+                check(vkhip_conv3x3s2_pair_forward(&d1, &d2, nc ? &d3 : nullptr, env.dev(in), blob1->ptr, blob2->ptr, nc ? blob3->ptr : nullptr,
+                                                   env.dev(out), env.pstride(out), s),
+                      "stem pair " + name);
             }
-            std::string describe() const override { return "fused with " + na->name + " kernel=conv_stem2_kernel"; }
+            std::string describe() const override {
+                return "fused with " + na->name + (nc ? " and the 1x1 " + nc->name + " after it" : std::string()) + " kernel=conv_stem2_kernel";
+            }
         };
 
         // ------------------------------------------------------------ two 3x3 stride-1 convs
@@ -1660,8 +1670,9 @@ namespace vknn {
             }
             // Two stride-2 stem convs as one op (Stem2Op): the second conv -> the first, which is
             // folded. VKNN_HIP_FUSE_STEM2=0 keeps the two launches (A/B).
-            std::map<int, int> stem2Of; // second conv node -> first conv node
-            std::set<int>      stem2Folded;
+            std::map<int, int> stem2Of;   // second conv node -> first conv node
+            std::map<int, int> stem2Tail; // second conv node -> its 1x1 tail conv
+            std::set<int>      stem2Folded; // first convs and tails
             {
                 const char *st2_env = std::getenv("VKNN_HIP_FUSE_STEM2");
                 if (!st2_env || std::string(st2_env) != "0") {
@@ -1700,10 +1711,22 @@ namespace vknn {
                         if (!dense(na) || place_.count(resolve(t)) || pstride(t) > 0 || pstride(na.inputs[0]) > 0 || place_.count(resolve(na.inputs[0])))
                             continue;
                         vkhip_conv_desc d1 = convDescOf(g, na), d2 = convDescOf(g, nb);
-                        vkhip_conv_plan q1, q2;
-                        if (vkhip_conv3x3s2_pair_plan(&d1, &d2, &q1, &q2) != VKHIP_OK) continue;
+                        vkhip_conv_plan q1, q2, q3;
+                        if (vkhip_conv3x3s2_pair_plan(&d1, &d2, nullptr, &q1, &q2, &q3) != VKHIP_OK) continue;
                         stem2Of[b] = pa->second;
                         stem2Folded.insert(pa->second);
+                        // the 1x1 conv that is the second conv's only reader runs as the kernel's tail
+                        const TensorId t2 = nb.outputs[0];
+                        if (readers[t2] != 1 || place_.count(resolve(t2)) || pstride(t2) > 0) continue;
+                        for (int c: idx) {
+                            const Node &ncn = g.nodes[c];
+                            if (skip.count(c) || !dense(ncn) || ncn.inputs[0] != t2) continue;
+                            vkhip_conv_desc d3 = convDescOf(g, ncn);
+                            if (vkhip_conv3x3s2_pair_plan(&d1, &d2, &d3, &q1, &q2, &q3) != VKHIP_OK) break;
+                            stem2Tail[b] = c;
+                            stem2Folded.insert(c);
+                            break;
+                        }
                     }
                 }
             }
@@ -1834,11 +1857,14 @@ namespace vknn {
                     f->what = "3x3 stride-2 conv: runs with the stride-2 conv that reads it,";
                     for (auto &kv: stem2Of)
                         if (kv.second == i) f->into = g.nodes[kv.first].name;
+                    for (auto &kv: stem2Tail)
+                        if (kv.second == i) f->what = "1x1 conv: runs as the tail of the stride-2 pair,", f->into = g.nodes[kv.first].name;
                     op = std::move(f);
                 } else if (stem2Of.count(i)) {
                     auto c = std::make_unique<Stem2Op>();
                     c->na  = &g.nodes[stem2Of[i]];
-                    op     = std::move(c);
+                    if (stem2Tail.count(i)) c->nc = &g.nodes[stem2Tail[i]];
+                    op = std::move(c);
                 } else if (addFold.count(i)) {
                     auto f  = std::make_unique<FoldedMulOp>();
                     f->what = "add (a residual after the activation)";
@@ -1959,9 +1985,9 @@ namespace vknn {
                     continue;
                 }
                 if (stem2Of.count(i)) {
-                    // the pair reads the first conv's input and writes the second's output
+                    // the pair reads the first conv's input and writes the second's output (or its tail's)
                     in.push_back(resolve(g.nodes[stem2Of[i]].inputs[0]));
-                    out.push_back(resolve(nd.outputs[0]));
+                    out.push_back(resolve(stem2Tail.count(i) ? g.nodes[stem2Tail[i]].outputs[0] : nd.outputs[0]));
                     ins.push_back(in);
                     outs.push_back(out);
                     continue;
