@@ -70,14 +70,32 @@ namespace vkhip {
         int th = tr / nTW, tw = tr - (tr / nTW) * nTW;
         const uint2 *src = x + ((long long) n * Cinb + cb) * H * W;
         float4v d[4][4];
+        // each tile row as two 16-byte loads of pixel pairs (8-byte aligned); pairs that cross the
+        // image's left or right edge fall back to single pixels with the outside one zero
+        const int c0 = 2 * tw - 1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            int iy = 2 * th - 1 + i;
+            const int iy = 2 * th - 1 + i;
+            if (iy < 0 || iy >= H) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                int ix = 2 * tw - 1 + j;
-                bool ok = iy >= 0 && iy < H && ix >= 0 && ix < W;
-                d[i][j] = ok ? h4_to_f4(u2_as_h4(src[iy * W + ix])) : float4v {0.f, 0.f, 0.f, 0.f};
+                for (int j = 0; j < 4; ++j) d[i][j] = float4v {0.f, 0.f, 0.f, 0.f};
+                continue;
+            }
+            const uint2 *row = src + (long long) iy * W;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int c = c0 + 2 * h;
+                uint2     p0 = {0u, 0u}, p1 = {0u, 0u};
+                if (c >= 0 && c + 1 < W) {
+                    const u32x4 q = *reinterpret_cast<const u32x4_a8 *>(row + c);
+                    p0 = uint2 {q.x, q.y};
+                    p1 = uint2 {q.z, q.w};
+                } else {
+                    if (c >= 0 && c < W) p0 = row[c];
+                    if (c + 1 >= 0 && c + 1 < W) p1 = row[c + 1];
+                }
+                d[i][2 * h]     = h4_to_f4(u2_as_h4(p0));
+                d[i][2 * h + 1] = h4_to_f4(u2_as_h4(p1));
             }
         }
         float4v tm[4][4];
