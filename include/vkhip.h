@@ -278,6 +278,21 @@ int vkhip_conv3x3s2_pair_plan(const vkhip_conv_desc *c1, const vkhip_conv_desc *
 int vkhip_conv3x3s2_pair_forward(const vkhip_conv_desc *c1, const vkhip_conv_desc *c2, const vkhip_conv_desc *c3, const void *x, const void *blob1,
                                  const void *blob2, const void *blob3, void *y, int64_t y_pstride, vkhip_stream_t s);
 
+/* ---------------------------------------------------------------- a stem and its first block in one kernel
+ * y = actp(Wp * rnd(actd(dw3x3(s))) + bp [+ s]) with s = rnd(acta(conv3x3s2(x))): a dense 3x3
+ * stride-2 pad-1 conv over at most 4 input channels to 9-16 channels (cs), a 3x3 stride-1 pad-1
+ * depthwise conv over them (cd) and a dense 1x1 projection to at most 16 channels (cp; has_res 1:
+ * the residual is the stem's output, Cout equal to the stem's). The MobileNetV3 stem and first
+ * inverted-residual block (3 -> 16 -> dw 16 -> 16 + x); both 16-channel tensors stay in LDS. x is
+ * a dense NC4HW4 tensor with an even width; y may be a view (`y_pstride` channel blocks per image;
+ * 0 = dense). Weights: each conv's blob packed by vkhip_conv_pack_weights with the plan
+ * vkhip_stem_dwpw_plan returns for it. No reference counterpart: the reference runs ConvCpu
+ * (src/backend/cpu/ops/conv.cpp:9-92) and then FusedDwPw (src/backend/cpu/ops/fused_dwpw.cpp:10-87). */
+int vkhip_stem_dwpw_plan(const vkhip_conv_desc *cs, const vkhip_conv_desc *cd, const vkhip_conv_desc *cp, vkhip_conv_plan *ps,
+                         vkhip_conv_plan *pd, vkhip_conv_plan *pp);
+int vkhip_stem_dwpw_forward(const vkhip_conv_desc *cs, const vkhip_conv_desc *cd, const vkhip_conv_desc *cp, const void *x, const void *blob_s,
+                            const void *blob_d, const void *blob_p, void *y, int64_t y_pstride, vkhip_stream_t s);
+
 int vkhip_conv_forward_noalloc(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const void *x, const void *blob,
                                const void *res, void *y, vkhip_stream_t s);
 

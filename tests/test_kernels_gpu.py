@@ -522,6 +522,96 @@ def test_conv3x3s2_pair_view_and_refusals(gpu):
     assert not ok((1, 3, 32, 32), 16, 32, c3=32, k3=3)  # tail not 1x1
 
 
+def gpu_stem_dwpw(x, ws, bs, acts, wd, bd, actd, wp, bp, actp, res=True, y_wide=None):
+    """vkhip_stem_dwpw_forward; with y_wide = (Cw, off) the output goes to channel `off` of a
+    wider zero-filled tensor, which is returned whole."""
+    lib = V.vkhip()
+    C1 = ws.shape[0]
+    ds, ys1 = conv_desc(x.shape, ws.shape, (2, 2), (1, 1, 1, 1), act=acts)
+    dd, _ = conv_desc(ys1, wd.shape, (1, 1), (1, 1, 1, 1), group=C1, act=actd, lo=0.0, hi=6.0)
+    dp, ys = conv_desc(ys1, wp.shape, act=actp, has_res=1 if res else 0)
+    ps, pd, pp = V.ConvPlan(), V.ConvPlan(), V.ConvPlan()
+    check(lib.vkhip_stem_dwpw_plan(ctypes.byref(ds), ctypes.byref(dd), ctypes.byref(dp), ctypes.byref(ps), ctypes.byref(pd),
+                                   ctypes.byref(pp)), "stem_dwpw plan")
+    blobs = []
+    for d, p, w, b in ((ds, ps, ws, bs), (dd, pd, wd, bd), (dp, pp, wp, bp)):
+        blob = np.zeros(p.weight_bytes, np.uint8)
+        check(lib.vkhip_conv_pack_weights(ctypes.byref(d), ctypes.byref(p), w.ctypes.data, b.ctypes.data, blob.ctypes.data), "pack")
+        blobs.append(DeviceBuffer.from_array(blob))
+    dx = to_device_nc4(x)
+    N, C2, H2, W2 = ys
+    shape = ys if y_wide is None else (N, y_wide[0], H2, W2)
+    dy = DeviceBuffer(V.nc4_elems(*shape) * 2)
+    dy.zero()
+    off = 0 if y_wide is None else y_wide[1] // 4 * H2 * W2 * 8
+    check(lib.vkhip_stem_dwpw_forward(ctypes.byref(ds), ctypes.byref(dd), ctypes.byref(dp), dx.ptr, blobs[0].ptr, blobs[1].ptr,
+                                      blobs[2].ptr, dy.ptr + off, 0 if y_wide is None else y_wide[0] // 4, None), "stem_dwpw")
+    check(lib.vkhip_stream_sync(None), "sync")
+    return from_device_nc4(dy, shape)
+
+
+def stem_dwpw_case(r, N, C, H, W, C1, C2):
+    x = round_half(r.standard_normal((N, C, H, W)))
+    ws = (r.standard_normal((C1, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float32)
+    wd = (r.standard_normal((C1, 1, 3, 3)) * np.sqrt(2.0 / 9)).astype(np.float32)
+    wp = (r.standard_normal((C2, C1, 1, 1)) * np.sqrt(1.0 / C1)).astype(np.float32)
+    bs, bd, bp = ((r.standard_normal(c) * 0.1).astype(np.float32) for c in (C1, C1, C2))
+    return x, ws, bs, wd, bd, wp, bp
+
+
+def oracle_stem_dwpw(x, ws, bs, acts, wd, bd, actd, wp, bp, actp, res=True):
+    t = round_half(oracle_conv(x, ws, bs, (2, 2), (1, 1, 1, 1), act=acts))
+    return oracle_dwpw(t, wd, bd, wp.reshape(wp.shape[0], -1), bp, dw_act=actd, res=t if res else None, act=actp)
+
+
+# N, C, H, W, stem channels, out channels, (stem act, dw act, projection act), residual
+STEM_DWPW_CASES = [(2, 3, 224, 224, 16, 16, (4, 1, 0), True), (1, 3, 98, 130, 16, 16, (4, 1, 0), True),
+                   (3, 4, 22, 18, 12, 12, (1, 2, 5), True), (2, 1, 30, 262, 16, 8, (5, 0, 1), False),
+                   (1, 3, 10, 8, 10, 7, (2, 1, 0), False), (1, 2, 6, 4, 9, 9, (4, 4, 4), True)]
+
+
+@pytest.mark.parametrize("case", STEM_DWPW_CASES)
+def test_stem_dwpw(gpu, case):
+    """The MobileNetV3 stem and first block in one kernel (stem output and depthwise output in LDS,
+    each rounded to fp16 like the separate kernels' stores) against the oracle's conv and fused
+    depthwise + projection, with the stem's output as the residual: MobileNetV3-Large's first block
+    at full size, odd stem outputs, items cut by the image edge, 1-4 input channels, 9-16 between,
+    7-16 out, with and without the residual, and the activation combinations the planner can meet."""
+    N, C, H, W, C1, C2, (acts, actd, actp), res = case
+    r = rng(1900 + C + H + W + C1 + C2)
+    x, ws, bs, wd, bd, wp, bp = stem_dwpw_case(r, N, C, H, W, C1, C2)
+    got = gpu_stem_dwpw(x, ws, bs, acts, wd, bd, actd, wp, bp, actp, res=res)
+    assert_parity(got, oracle_stem_dwpw(x, ws, bs, acts, wd, bd, actd, wp, bp, actp, res=res), f"stem_dwpw {case}")
+
+
+def test_stem_dwpw_view_and_refusals(gpu):
+    """The output written into a channel slice of a wider tensor (other slices stay zero); shapes
+    outside the kernel's range are refused."""
+    r = rng(1950)
+    x, ws, bs, wd, bd, wp, bp = stem_dwpw_case(r, 2, 3, 40, 64, 16, 16)
+    got = gpu_stem_dwpw(x, ws, bs, 4, wd, bd, 1, wp, bp, 0, y_wide=(48, 16))
+    assert_parity(got[:, 16:32], oracle_stem_dwpw(x, ws, bs, 4, wd, bd, 1, wp, bp, 0), "stem_dwpw view")
+    assert not got[:, :16].any() and not got[:, 32:].any()
+    lib = V.vkhip()
+    ps, pd, pp = V.ConvPlan(), V.ConvPlan(), V.ConvPlan()
+    def ok(xs, c1, c2, sd=1, kp=1, res=1, cd=None):
+        ds, ys = conv_desc(xs, (c1, xs[1], 3, 3), (2, 2), (1, 1, 1, 1))
+        cd = cd or c1
+        dd = conv_desc(ys, (cd, 1, 3, 3), (sd, sd), (1, 1, 1, 1), group=cd)[0]
+        dp = conv_desc(ys, (c2, c1, kp, kp), pads=(kp // 2,) * 4, has_res=res)[0]
+        return lib.vkhip_stem_dwpw_plan(ctypes.byref(ds), ctypes.byref(dd), ctypes.byref(dp), ctypes.byref(ps), ctypes.byref(pd),
+                                        ctypes.byref(pp)) == 0
+    assert ok((1, 3, 32, 32), 16, 16) and ok((1, 3, 32, 32), 16, 8, res=0)
+    assert not ok((1, 8, 32, 32), 16, 16)           # more than 4 input channels
+    assert not ok((1, 3, 32, 32), 32, 32)           # more than 16 between
+    assert not ok((1, 3, 32, 32), 16, 32, res=0)    # more than 16 out
+    assert not ok((1, 3, 32, 33), 16, 16)           # odd input width
+    assert not ok((1, 3, 32, 32), 16, 16, sd=2)     # strided depthwise conv
+    assert not ok((1, 3, 32, 32), 16, 16, kp=3)     # projection not 1x1
+    assert not ok((1, 3, 32, 32), 16, 8)            # residual with a channel count other than the stem's
+    assert not ok((1, 3, 32, 32), 16, 16, res=2)    # residual after the activation
+
+
 @pytest.mark.parametrize("tile", PERS_TILES)
 @pytest.mark.parametrize("shape", [(32, 64, 28, 28, 512), (17, 200, 7, 7, 256), (9, 96, 15, 15, 200)])
 def test_conv_dma_persist_many_tiles(gpu, tile, shape):

@@ -209,6 +209,22 @@ def test_stem_convs_and_pool_chain_fused(gpu, monkeypatch):
     check_outputs(got, plain.run(x), sess.out_elems, "config4 b1 stem fused vs two launches")
 
 
+def test_stem_and_first_block_fused(gpu, monkeypatch):
+    """MobileNetV3's stem conv (3 -> 16, hard-swish) and its first block (depthwise 3x3 + ReLU, 1x1
+    16 -> 16 + the stem's output) run as one kernel with both 16-channel tensors in LDS; the result
+    matches the oracle and the session with the two ops apart."""
+    sess = V.Session("mobilenetv3_large", 2, seed=7)
+    plan = sess.describe()
+    assert plan.count("kernel=conv_stem_dwpw_kernel") == 1 and plan.count("runs with the depthwise block that reads it") == 1, plan
+    x = make_input(sess.in_shape, 9)
+    got = sess.run(x)
+    check_outputs(got, oracle_model_run("mobilenetv3_large", 2, 7, x), sess.out_elems, "config3 b2 stem block fused")
+    monkeypatch.setenv("VKNN_HIP_FUSE_STEM_BLOCK", "0")
+    plain = V.Session("mobilenetv3_large", 2, seed=7)
+    assert "conv_stem_dwpw_kernel" not in plain.describe()
+    check_outputs(got, plain.run(x), sess.out_elems, "config3 b2 stem block fused vs apart")
+
+
 def test_bottleneck_add_folded_into_conv(gpu, monkeypatch):
     """The six YOLOv8n bottleneck shortcuts (an Add after an activated 3x3 conv, writing a slice of
     the C2f concat) run inside that conv's epilogue as a residual after the activation: no add

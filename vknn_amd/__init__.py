@@ -119,6 +119,8 @@ VKHIP_API = {
     "vkhip_conv3x3_pair_forward": (c_int, [P(ConvDesc), P(ConvDesc), c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp]),
     "vkhip_conv3x3s2_pair_plan": (c_int, [P(ConvDesc), P(ConvDesc), P(ConvDesc), P(ConvPlan), P(ConvPlan), P(ConvPlan)]),
     "vkhip_conv3x3s2_pair_forward": (c_int, [P(ConvDesc), P(ConvDesc), P(ConvDesc), c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),
+    "vkhip_stem_dwpw_plan": (c_int, [P(ConvDesc), P(ConvDesc), P(ConvDesc), P(ConvPlan), P(ConvPlan), P(ConvPlan)]),
+    "vkhip_stem_dwpw_forward": (c_int, [P(ConvDesc), P(ConvDesc), P(ConvDesc), c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),
     "vkhip_add_view": (c_int, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_i64, c_i64, c_i64, c_i32, c_f, c_f, c_vp]),
     "vkhip_maxpool_view": (c_int, [P(PoolDesc), c_vp, c_i64, c_vp, c_i64, c_vp]),
     "vkhip_maxpool_chain": (c_int, [P(PoolDesc), c_vp, c_i64, P(c_vp), P(c_i64), c_i32, c_vp]),

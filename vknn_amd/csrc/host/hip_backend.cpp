@@ -988,6 +988,60 @@ namespace vknn {
             }
         };
 
+        // ------------------------------------------------------------ stem + first depthwise block
+        // A 3x3 stride-2 stem conv over at most 4 channels and the FusedDwPw block that is its only
+        // reader (residual: the stem's output), the MobileNetV3 stem and first block, as one op at
+        // the block's place: vkhip_stem_dwpw_forward, both 16-channel tensors in LDS.
+        struct StemDwPwOp: HipOp {
+            const Node             *na = nullptr; // the stem conv (this op is prepared with the block)
+            vkhip_conv_desc         ds {}, dd {}, dp {};
+            vkhip_conv_plan         ps {}, pd {}, pp {};
+            std::shared_ptr<DevBuf> blobs, blobd, blobp;
+            TensorId                in = kNoTensor, out = kNoTensor;
+            // the block's three descriptors from the stem's and the FusedDwPw node's
+            static bool descs(const Graph &g, const Node &stem, const Node &blk, vkhip_conv_desc &s, vkhip_conv_desc &d, vkhip_conv_desc &p) {
+                s = convDescOf(g, stem);
+                NCHW x = NCHW::from(g.desc(blk.inputs[0]).shape), y = NCHW::from(g.desc(blk.outputs[0]).shape);
+                const Shape &dws = g.desc(blk.inputs[1]).shape, &pws = g.desc(blk.inputs[3]).shape;
+                if (dws.size() != 4 || pws.size() < 2 || pws[0] != y.c) return false;
+                auto st = attrInts(blk, "strides", {1, 1}), pad = attrInts(blk, "pads", {0, 0, 0, 0}), dil = attrInts(blk, "dilations", {1, 1});
+                d = vkhip_conv_desc {};
+                d.N = (int) x.n; d.Cin = d.Cout = d.group = (int) x.c; d.H = (int) x.h; d.W = (int) x.w; d.OH = (int) y.h; d.OW = (int) y.w;
+                d.KH = (int) dws[2]; d.KW = (int) dws[3]; d.SH = (int) st[0]; d.SW = (int) st[1]; d.PT = (int) pad[0]; d.PL = (int) pad[1];
+                d.DH = (int) dil[0]; d.DW = (int) dil[1]; d.act = blk.subOp; d.act_lo = 0; d.act_hi = 6;
+                if (pad.size() != 4 || pad[2] != pad[0] || pad[3] != pad[1]) return false;
+                p = vkhip_conv_desc {};
+                p.N = (int) y.n; p.Cin = (int) x.c; p.H = p.OH = (int) y.h; p.W = p.OW = (int) y.w; p.Cout = (int) y.c;
+                p.KH = p.KW = p.SH = p.SW = p.DH = p.DW = p.group = 1;
+                p.act = (int) blk.fusedAct; p.act_lo = blk.actLo; p.act_hi = blk.actHi; p.has_res = blk.fusedResidual != kNoTensor;
+                return true;
+            }
+            void prepare(const Node &node, SegEnv &env) override {
+                const Graph &g = *env.graph;
+                if (!descs(g, *na, node, ds, dd, dp)) throw Error(Status::Unsupported, "stem + block shapes: " + name);
+                in  = na->inputs[0];
+                out = node.outputs[0];
+                check(vkhip_stem_dwpw_plan(&ds, &dd, &dp, &ps, &pd, &pp), "stem block plan " + name);
+                vkhip_conv_desc ep = dp;
+                ep.has_res = 0;
+                std::vector<uint8_t> hs(ps.weight_bytes), hd(pd.weight_bytes), hp(pp.weight_bytes);
+                check(vkhip_conv_pack_weights(&ds, &ps, initF32(g, na->inputs[1]), initF32(g, biasOf(*na)), hs.data()), "stem block pack");
+                check(vkhip_conv_pack_weights(&dd, &pd, initF32(g, node.inputs[1]), initF32(g, node.inputs[2]), hd.data()), "stem block pack");
+                check(vkhip_conv_pack_weights(&ep, &pp, initF32(g, node.inputs[3]), initF32(g, node.inputs[4]), hp.data()), "stem block pack");
+                blobs = upload(hs.data(), hs.size());
+                blobd = upload(hd.data(), hd.size());
+                blobp = upload(hp.data(), hp.size());
+                kind  = "conv";
+                flops = 2.0 * ds.N * ds.OH * ds.OW * ((double) ds.Cout * ds.Cin * 9 + (double) dd.Cin * 9 + (double) dp.Cout * dp.Cin);
+                bytes = (int64_t) (nc4Bytes(g.desc(in).shape) + nc4Bytes(g.desc(out).shape));
+            }
+            void record(SegEnv &env, vkhip_stream_t s) override {
+                check(vkhip_stem_dwpw_forward(&ds, &dd, &dp, env.dev(in), blobs->ptr, blobd->ptr, blobp->ptr, env.dev(out), env.pstride(out), s),
+                      "stem block " + name);
+            }
+            std::string describe() const override { return "fused with " + na->name + " kernel=conv_stem_dwpw_kernel"; }
+        };
+
         // ------------------------------------------------------------ two 3x3 stride-1 convs
         // A 3x3 conv over 9-16 channels and the 3x3 conv that is its only reader, with the Add of
         // the first conv's input after the second's activation when there is one (the YOLOv8
@@ -1787,6 +1841,63 @@ namespace vknn {
                     }
                 }
             }
+            // A stem conv and the FusedDwPw block that reads it (StemDwPwOp): block -> stem, which
+            // is folded. VKNN_HIP_FUSE_STEM_BLOCK=0 keeps the two ops (A/B).
+            std::map<int, int> sdOf;
+            std::set<int>      sdFolded;
+            {
+                const char *sd_env = std::getenv("VKNN_HIP_FUSE_STEM_BLOCK");
+                if (!sd_env || std::string(sd_env) != "0") {
+                    std::set<int> skip(folded.begin(), folded.end());
+                    for (auto &kv: scaled) skip.insert(kv.first);
+                    for (auto &kv: convPool) skip.insert(kv.first), skip.insert(kv.second);
+                    for (auto &kv: gapConv) skip.insert(kv.second);
+                    for (auto &kv: pwPairs) skip.insert(kv.first);
+                    skip.insert(pwFolded.begin(), pwFolded.end());
+                    skip.insert(pwChained.begin(), pwChained.end());
+                    for (auto &kv: actConv) skip.insert(kv.first);
+                    for (auto &kv: addConv) skip.insert(kv.first);
+                    skip.insert(stem2Folded.begin(), stem2Folded.end());
+                    for (auto &kv: stem2Of) skip.insert(kv.first);
+                    skip.insert(pairFolded.begin(), pairFolded.end());
+                    for (auto &kv: pairOf) skip.insert(kv.first);
+                    std::map<TensorId, int> readers, producer;
+                    for (size_t i = 0; i < g.nodes.size(); ++i) {
+                        for (TensorId t: g.nodes[i].inputs)
+                            if (t != kNoTensor) ++readers[t];
+                        if (g.nodes[i].fusedResidual != kNoTensor) ++readers[g.nodes[i].fusedResidual];
+                        for (TensorId t: g.nodes[i].outputs)
+                            if (t != kNoTensor) producer[t] = (int) i;
+                    }
+                    for (TensorId t: g.outputs) readers[t] += 1000;
+                    std::set<int> inSeg(idx.begin(), idx.end());
+                    for (int b: idx) {
+                        const Node &nb = g.nodes[b];
+                        if (skip.count(b) || nb.type != OpType::FusedDwPw || nb.inputs.size() < 5 || nb.outputs.empty()) continue;
+                        bool inits = true; // weights given, biases given or absent
+                        for (int k = 1; k < 5; ++k) inits = inits && (nb.inputs[k] != kNoTensor ? g.isInitializer(nb.inputs[k]) : (k & 1) == 0);
+                        const TensorId t = nb.inputs[0];
+                        auto           pa = producer.find(t);
+                        const bool     res = nb.fusedResidual != kNoTensor;
+                        // the block is the stem output's only reader (it lists the residual as an input too)
+                        int own = res ? 1 : 0;
+                        for (TensorId u: nb.inputs) own += u == t;
+                        if (!inits || (res && nb.fusedResidual != t) || pa == producer.end() || !inSeg.count(pa->second) || skip.count(pa->second) ||
+                            readers[t] != own)
+                            continue;
+                        const Node &na = g.nodes[pa->second];
+                        if (na.type != OpType::Conv || na.inputs.size() < 2 || !g.isInitializer(na.inputs[1]) || na.fusedResidual != kNoTensor ||
+                            g.desc(na.inputs[1]).shape.size() != 4 || place_.count(resolve(t)) || pstride(t) > 0 || pstride(na.inputs[0]) > 0 ||
+                            place_.count(resolve(na.inputs[0])))
+                            continue;
+                        vkhip_conv_desc ds, dd, dp;
+                        vkhip_conv_plan q1, q2, q3;
+                        if (!StemDwPwOp::descs(g, na, nb, ds, dd, dp) || vkhip_stem_dwpw_plan(&ds, &dd, &dp, &q1, &q2, &q3) != VKHIP_OK) continue;
+                        sdOf[b] = pa->second;
+                        sdFolded.insert(pa->second);
+                    }
+                }
+            }
             // Device buffers: one NC4HW4 fp16 buffer per activation (aliases share their source's;
             // a tensor placed in another one by planViews has none of its own).
             for (int i: idx) {
@@ -1852,6 +1963,16 @@ namespace vknn {
                         for (int m: kv.second)
                             if (m == i) f->into = g.nodes[kv.first].name;
                     op = std::move(f);
+                } else if (sdFolded.count(i)) {
+                    auto f  = std::make_unique<FoldedMulOp>();
+                    f->what = "stem conv: runs with the depthwise block that reads it,";
+                    for (auto &kv: sdOf)
+                        if (kv.second == i) f->into = g.nodes[kv.first].name;
+                    op = std::move(f);
+                } else if (sdOf.count(i)) {
+                    auto c = std::make_unique<StemDwPwOp>();
+                    c->na  = &g.nodes[sdOf[i]];
+                    op     = std::move(c);
                 } else if (stem2Folded.count(i)) {
                     auto f = std::make_unique<FoldedMulOp>();
                     f->what = "3x3 stride-2 conv: runs with the stride-2 conv that reads it,";
@@ -1928,7 +2049,7 @@ namespace vknn {
                 op->type = nd.type;
                 const bool gapFolded = gapParts.count(i) > 0;
                 const bool pwOp = pwPairs.count(i) || pwFolded.count(i) || pwChained.count(i) || stem2Of.count(i) || stem2Folded.count(i) ||
-                                  pairOf.count(i) || pairFolded.count(i);
+                                  pairOf.count(i) || pairFolded.count(i) || sdOf.count(i) || sdFolded.count(i);
                 if (nd.type == OpType::Conv && !inPlace && !gapFolded && !folded.count(i) && !pools.count(i) && !pwOp) {
                     bool v = false;
                     for (TensorId t: {nd.inputs[0], nd.outputs[0]}) v = v || pstride(t) > 0;
@@ -1970,7 +2091,7 @@ namespace vknn {
                     continue;
                 }
                 if (folded.count(i) || pools.count(i) || pwFolded.count(i) || pwChained.count(i) || actFold.count(i) || addFold.count(i) ||
-                    stem2Folded.count(i) || poolChained.count(i) || pairFolded.count(i)) {
+                    stem2Folded.count(i) || poolChained.count(i) || pairFolded.count(i) || sdFolded.count(i)) {
                     ins.push_back(in);
                     outs.push_back(out);
                     continue;
@@ -1980,6 +2101,14 @@ namespace vknn {
                     in.push_back(resolve(g.nodes[pairOf[i]].inputs[0]));
                     auto ad = addConv.find(i);
                     out.push_back(resolve(ad != addConv.end() ? g.nodes[ad->second].outputs[0] : nd.outputs[0]));
+                    ins.push_back(in);
+                    outs.push_back(out);
+                    continue;
+                }
+                if (sdOf.count(i)) {
+                    // the op reads the stem's input and writes the block's output
+                    in.push_back(resolve(g.nodes[sdOf[i]].inputs[0]));
+                    out.push_back(resolve(nd.outputs[0]));
                     ins.push_back(in);
                     outs.push_back(out);
                     continue;
