@@ -1,17 +1,21 @@
 // A MobileNetV3 stem and its first block in one kernel: a 3x3 stride-2 conv over at most 4 input
 // channels to 9-16 channels, a 3x3 stride-1 depthwise conv over those channels, and the 1x1
 // projection back to at most 16 channels with the stem's output as the residual (MobileNetV3-Large:
-// 3 -> 16 hard-swish at 224x224, dw 3x3 ReLU, 16 -> 16 + x). Run as three launches (stem, dw,
-// 1x1), the 16-channel tensors at 112x112 go through HBM five times; here they stay in LDS:
-//   * one persistent workgroup per CU slot walks items of 2 output rows x 64 columns
-//     (XCD-contiguous item ranges);
-//   * the stem's input band (9 rows x 162 columns of the input's 4-channel slot) arrives in LDS by
-//     buffer-load-to-LDS; the stem computes the 4 x 80 pixels the depthwise window needs
-//     (16x16x32 MFMA, weights in registers) into LDS as fp16, zero outside the image (the
-//     depthwise conv's padding), rounded like the separate conv's store;
-//   * the depthwise conv (VALU, fp32 sums of fp16 taps) writes its 2 x 64 tile to LDS as fp16;
-//   * the projection (one 32-deep MFMA step per 16 pixels) adds bias, the stem's pixel from LDS as
-//     the residual, and its activation, and stores 8-byte NC4HW4 slots.
+// 3 -> 16 hard-swish at 224x224, dw 3x3 ReLU, 16 -> 16 + x). Run as separate launches, the
+// 16-channel tensors at 112x112 go through HBM several times; here they stay in LDS:
+//   * one persistent workgroup per CU slot walks items of 4 output rows x up to 64 columns (the
+//     width split evenly), XCD-contiguous item ranges;
+//   * the stem's input band (13 rows of the input's 4-channel slot) arrives in LDS by
+//     buffer-load-to-LDS, double-buffered: the next item's copies run under this item's work;
+//   * the stem computes the 6-row tile the depthwise window needs (16x16x32 MFMA, weights in
+//     registers) into LDS as fp16, zero outside the image (the depthwise conv's padding), rounded
+//     like the separate conv's store;
+//   * the depthwise conv runs on MFMA too, as a 3x3 conv over 16 channels whose weight matrix is
+//     zero off the diagonal (built in registers from the depthwise blob); its tile goes to LDS as fp16;
+//   * the projection (one 32-deep MFMA step per 16 pixels) adds the stem's pixel from LDS as the
+//     residual and its activation, and stores 8-byte NC4HW4 slots.
+// The kernel is bound by instruction issue, not HBM: biases seed the accumulators, phases are
+// branch-free and take two 16-pixel units per pass so LDS reads and MFMAs overlap.
 // Reference semantics: ConvCpu (src/backend/cpu/ops/conv.cpp:9-92) for the stem, FusedDwPw
 // (src/backend/cpu/ops/fused_dwpw.cpp:10-87) for the block.
 #include "conv_kernels.h"
@@ -30,6 +34,7 @@ namespace vkhip {
         const float  *ba, *bd, *bp;
         const uint2  *wd; // depthwise weights [slot][tap] x 4 channels fp16
         int           N, H, W;  // input
+        int           ocw;      // output columns per item
         int           OH, OW;   // stem / block output
         int           cbm, cbo; // channel slots: stem output, projection output
         int           y_pstride;
@@ -39,41 +44,61 @@ namespace vkhip {
     };
 
     namespace sdp {
-        constexpr int OR   = 2;          // output rows per item
-        constexpr int OCW  = 64;         // output columns per item
-        constexpr int IR   = OR + 2;     // stem rows the depthwise window needs
-        constexpr int IT   = 5;          // 16-pixel column tiles of the stem tile (66 of 80 used)
-        constexpr int ICW  = IT * 16;
-        constexpr int BR   = 2 * IR + 1; // input band rows
-        constexpr int BC   = 2 * ICW + 2; // input band columns (even: whole pixel pairs)
-        constexpr int BPPR = BC / 2;
-        constexpr int CB   = 4;          // channel slots of the block (9-16 channels)
+        constexpr int OR   = 4;           // output rows per item
+        constexpr int MAXW = 64;          // output columns per item, at most (a.ocw: the image width split evenly)
+        constexpr int IR   = OR + 2;      // stem rows the depthwise window needs
+        constexpr int MSW  = MAXW + 2;    // stem columns, at most
+        constexpr int BR   = 2 * IR + 1;  // input band rows
+        constexpr int MBPR = MSW + 1;     // band pixel pairs per row, at most (2 * MSW + 2 columns)
+        constexpr int CB   = 4;           // channel slots of the block (9-16 channels)
     } // namespace sdp
 
+    // Hard-swish as v * relu6(v + 3) times the fp32 reciprocal of 6 (within one fp32 ulp of the
+    // quotient, well inside the fp16 rounding that follows; 4 instructions instead of a divide).
     template <int ACT>
     __device__ __forceinline__ float sdp_act(float v, int act, float lo, float hi) {
+        if constexpr (ACT == VKHIP_ACT_HARDSWISH) return v * fminf(fmaxf(v + 3.f, 0.f), 6.f) * (1.f / 6.f);
         return apply_act(v, ACT >= 0 ? ACT : act, lo, hi);
     }
 
+    // v / d for 0 <= v < 2^12 and 1 <= d <= 128, with r = 1/d in fp32: v/d is at least 1/(2d)
+    // away from the next integer (v + 1/2 over d), far more than the product's rounding error.
+    __device__ __forceinline__ int fdiv(int v, float r) { return (int) (((float) v + 0.5f) * r); }
+
+    // A workgroup barrier over LDS writes only: the next item's band copies stay in flight
+    // (__syncthreads would wait for them too).
+    __device__ __forceinline__ void sdp_lds_barrier() {
+        __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0); vmcnt, expcnt untouched
+        __asm__ volatile("s_barrier" ::: "memory");
+    }
+
+    // Items of OR output rows x a.ocw columns; all tiles are indexed by flat pixel number, so the
+    // 16-pixel MFMA columns and the depthwise lanes run across row ends without padding columns.
+    // The band is double-buffered: the next item's copies are issued before this item's stem.
     template <int ACTA, int ACTD, int ACTP>
     __global__ __launch_bounds__(256, 2) void conv_stem_dwpw_kernel(StemDwPwArgs a) {
         using namespace sdp;
-        constexpr int NSA   = 2; // stem: 9 taps x 4 channels in 2 32-deep steps
-        constexpr int TP    = BR * BPPR;
-        constexpr int NI    = (TP + 63) / 64;
-        constexpr int NBW   = (NI + 3) / 4;
-        constexpr int BAND  = NBW * 4 * 1024;
-        constexpr int STEM  = CB * IR * ICW * 8;
-        constexpr int DWT   = CB * OR * OCW * 8;
-        static_assert(CB * OR * OCW == 2 * 256, "the depthwise loop: two pixels per thread");
-        __shared__ __attribute__((aligned(16))) unsigned char sm[BAND + STEM + DWT];
-        unsigned char *band = sm;
-        unsigned char *stem = sm + BAND;
-        unsigned char *dwt  = sm + BAND + STEM;
+        constexpr int NSA  = 2; // stem: 9 taps x 4 channels in 2 32-deep steps
+        constexpr int NI   = (BR * MBPR + 63) / 64;
+        constexpr int NBW  = (NI + 3) / 4;
+        constexpr int BAND = NI * 1024;
+        constexpr int STEM = CB * IR * MSW * 8;
+        constexpr int DWT  = CB * OR * MAXW * 8;
+        constexpr int DWTO = STEM;       // the depthwise tile's offset from the stem tile
+        constexpr int DUMPO = STEM + DWT; // 64 lanes x 8 bytes for the writes of lanes past a tile
+        static_assert(2 * BAND + STEM + DWT + 512 <= 160 * 1024 / 3, "three workgroups per CU");
+        __shared__ __attribute__((aligned(16))) unsigned char sm[2 * BAND + STEM + DWT + 512];
+        unsigned char *stem = sm + 2 * BAND;
+        unsigned char *dwt  = sm + 2 * BAND + STEM;
 
         const int lane = threadIdx.x & 63;
         const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-        const int rblk = (a.OH + OR - 1) / OR, cblk = (a.OW + OCW - 1) / OCW;
+        const int ocw  = a.ocw, sw = ocw + 2, bc = 2 * sw + 2, bppr = sw + 1;
+        const int tp   = BR * bppr;         // band pixel pairs
+        const int sp   = IR * sw;           // stem tile pixels per slot
+        const int op   = OR * ocw;          // output pixels per slot
+        const float rsw = 1.f / (float) sw, rocw = 1.f / (float) ocw, rbppr = 1.f / (float) bppr;
+        const int rblk = (a.OH + OR - 1) / OR, cblk = (a.OW + ocw - 1) / ocw;
         const int items = a.N * rblk * cblk;
         constexpr unsigned kInvalid = 0x80000000u;
         const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *) a.x, (short) 0, (int) a.x_bytes, 0x00020000);
@@ -88,25 +113,52 @@ namespace vkhip {
         }
         const int g = lane >> 4, px = lane & 15;
         // stem B operand: k = tap*4 + c; the lane's two 4-channel halves are taps 8j + 2g + q
-        int aoff[NSA][2];
+        int  aoff[NSA][2];
+        bool aval[NSA][2];
 #pragma unroll
         for (int j = 0; j < NSA; ++j)
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const int tap = 8 * j + 2 * g + q;
-                aoff[j][q]    = tap < 9 ? (tap / 3) * BC + tap % 3 : -1;
+                aval[j][q]    = tap < 9;
+                aoff[j][q]    = tap < 9 ? (tap / 3) * bc + tap % 3 : 0;
             }
         // projection B operand: k = slot*4 + c over the depthwise tile's 4 slots (k >= 16: zero)
-        const int poff[2] = {2 * g < CB ? (2 * g) * OR * OCW : -1, 2 * g + 1 < CB ? (2 * g + 1) * OR * OCW : -1};
-        // depthwise: wave w computes slot w, its lanes consecutive pixels (conflict-free LDS rows)
-        const int dslot = wave;
-        float4v   dww[9];
+        const bool pval[2] = {2 * g < CB, 2 * g + 1 < CB};
+        const int  poff[2] = {pval[0] ? (2 * g) * op : 0, pval[1] ? (2 * g + 1) * op : 0};
+        // depthwise on MFMA: a 3x3 conv over 16 channels whose weights are zero off the diagonal,
+        // k = tap*16 + channel in 5 32-deep steps. The lane's A fragment (row l%16, k = 32j + 8(l/16)
+        // + e) holds the one tap weight of channel l%16 when that channel is among its 8 k.
+        constexpr int NSD = 5;
+        half8 wfd[NSD];
         {
-            const uint2 *w = a.wd + dslot * 9;
+            const int     m  = lane & 15;
+            const half_t *wd = reinterpret_cast<const half_t *>(a.wd);
 #pragma unroll
-            for (int t = 0; t < 9; ++t) dww[t] = dslot < a.cbm ? h4_to_f4(u2_as_h4(w[t])) : float4v {0.f, 0.f, 0.f, 0.f}; // the blob holds cbm slots
+            for (int j = 0; j < NSD; ++j) {
+                const int k0 = 32 * j + 8 * g, tap = k0 / 16, c0 = k0 % 16;
+                half8     f  = {};
+                const bool hit = tap < 9 && m >= c0 && m < c0 + 8 && m / 4 < a.cbm;
+                const half_t w = hit ? wd[((m / 4) * 9 + tap) * 4 + m % 4] : (half_t) 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) f[e] = c0 + e == m ? w : (half_t) 0.f;
+                wfd[j] = f;
+            }
         }
-        const float4v dwb = *reinterpret_cast<const float4v *>(a.bd + dslot * 4);
+        // the lane's B halves: taps 2j + g/2, slots 2(g%2) + q of the stem tile
+        int  doff[NSD][2];
+        bool dval[NSD][2];
+#pragma unroll
+        for (int j = 0; j < NSD; ++j)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int tap = 2 * j + (g >> 1);
+                dval[j][q]    = tap < 9;
+                doff[j][q]    = tap < 9 ? (2 * (g & 1) + q) * sp + (tap / 3) * sw + tap % 3 : 0;
+            }
+        const float4v bsd = *reinterpret_cast<const float4v *>(a.bd + g * 4);
+        const float4v bsa = *reinterpret_cast<const float4v *>(a.ba + g * 4);
+        const float4v bsp = *reinterpret_cast<const float4v *>(a.bp + g * 4);
 
         // items: XCD-contiguous ranges (workgroup b runs on XCD b % 8)
         const int G = gridDim.x;
@@ -115,84 +167,136 @@ namespace vkhip {
         const int pxc = xcd * (G >> 3) + min(xcd, G & 7);
         const int i0  = (int) ((long long) items * pxc / G) + lb;
         const int i1  = (int) ((long long) items * (pxc + gx) / G);
-        for (int it = i0; it < i1; it += gx) {
+        // band row r, column c of item it <-> input (2 oy0 - 3 + r, 2 ox0 - 4 + c)
+        auto copy_band = [&](int it, unsigned char *band) __attribute__((always_inline)) {
             const int cb = it % cblk, rest = it / cblk;
-            const int ox0 = cb * OCW, oy0 = (rest % rblk) * OR, n = rest / rblk;
-            // band row r, column c <-> input (2 oy0 - 3 + r, 2 ox0 - 4 + c)
+            const int ox0 = cb * ocw, oy0 = (rest % rblk) * OR, n = rest / rblk;
             const int iy0 = 2 * oy0 - 3, ix0 = 2 * ox0 - 4;
 #pragma unroll
             for (int r = 0; r < NBW; ++r) {
                 const int i   = r * 4 + wave;
+                if (i >= NI) break; // wave-uniform
                 const int p   = i * 64 + lane;
-                const int pc  = p % BPPR, row = p / BPPR;
+                const int row = fdiv(p, rbppr), pc = p - row * bppr;
                 const int iy  = iy0 + row, ix = ix0 + 2 * pc;
-                const bool ok = p < TP && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
+                const bool ok = p < tp && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
                 const unsigned off = ok ? (unsigned) (((n * a.H + iy) * a.W + ix) * 8) : kInvalid;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xrs, (__attribute__((address_space(3))) void *) (band + i * 1024), 16, off, 0, 0, 0);
             }
+        };
+        if (i0 < i1) copy_band(i0, sm);
+        int buf = 0;
+        for (int it = i0; it < i1; it += gx, buf ^= 1) {
+            const int cb = it % cblk, rest = it / cblk;
+            const int ox0 = cb * ocw, oy0 = (rest % rblk) * OR, n = rest / rblk;
+            unsigned char *band = sm + buf * BAND;
             __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); // this wave's copies (and last item's stores) done
-            __asm__ volatile("s_barrier" ::: "memory");        // every wave's copies landed
-            // stem: tile pixel (r, c) <-> stem output (oy0 - 1 + r, ox0 - 1 + c), window at band row 2r, column 2c + 1
-            for (int u = wave; u < IR * IT; u += 4) {
-                const int r = u / IT, c = (u % IT) * 16 + px;
-                float4v   acc = {0.f, 0.f, 0.f, 0.f};
-                const int base = 2 * r * BC + 2 * c + 1;
+            __asm__ volatile("s_barrier" ::: "memory");        // every wave's copies landed; the other band is free
+            if (it + gx < i1) copy_band(it + gx, sm + (buf ^ 1) * BAND);
+            // Each phase takes two 16-pixel units per wave and pass, branch-free (reads of absent taps
+            // are masked after the read; lanes past the tile write to the dump slot), so the two
+            // units' LDS reads and MFMAs overlap.
+            // stem: tile pixel q = r * sw + c <-> stem output (oy0 - 1 + r, ox0 - 1 + c), window at band row 2r, column 2c + 1
+            auto stem_unit = [&](int u, float4v &acc, int &q, int &r, int &c) __attribute__((always_inline)) {
+                q = u * 16 + px;
+                r = fdiv(q, rsw);
+                c = q - r * sw;
+                const int base = 2 * r * bc + 2 * c + 1;
+                acc = bsa; // the bias seeds the accumulator
 #pragma unroll
                 for (int j = 0; j < NSA; ++j) {
                     u32x2 v[2];
 #pragma unroll
-                    for (int q = 0; q < 2; ++q) v[q] = aoff[j][q] >= 0 ? *reinterpret_cast<const u32x2 *>(band + (base + aoff[j][q]) * 8) : u32x2 {0u, 0u};
+                    for (int q2 = 0; q2 < 2; ++q2) {
+                        const u32x2 t = *reinterpret_cast<const u32x2 *>(band + (base + aoff[j][q2]) * 8);
+                        v[q2]         = aval[j][q2] ? t : u32x2 {0u, 0u};
+                    }
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wfa[j], __builtin_bit_cast(half8, u32x4_make(v[0].x, v[0].y, v[1].x, v[1].y)), acc, 0, 0, 0);
                 }
+            };
+            auto stem_store = [&](float4v acc, int q, int r, int c) __attribute__((always_inline)) {
                 const int  iy = oy0 - 1 + r, ix = ox0 - 1 + c;
-                const bool in = iy >= 0 && iy < a.OH && ix >= 0 && ix < a.OW && g < a.cbm;
-                float4v    v  = acc + *reinterpret_cast<const float4v *>(a.ba + g * 4);
+                const bool in = ((unsigned) iy < (unsigned) a.OH) & ((unsigned) ix < (unsigned) a.OW) & (g < a.cbm); // no branches
+                float4v    v  = acc;
                 v.x = sdp_act<ACTA>(v.x, a.acta, a.loa, a.hia);
                 v.y = sdp_act<ACTA>(v.y, a.acta, a.loa, a.hia);
                 v.z = sdp_act<ACTA>(v.z, a.acta, a.loa, a.hia);
                 v.w = sdp_act<ACTA>(v.w, a.acta, a.loa, a.hia);
-                *reinterpret_cast<u32x2 *>(stem + ((g * IR + r) * ICW + c) * 8) = in ? __builtin_bit_cast(u32x2, f4_to_h4(v)) : u32x2 {0u, 0u};
+                const int w = q < sp ? (g * sp + q) * 8 : DUMPO + lane * 8;
+                *reinterpret_cast<u32x2 *>(stem + w) = in ? __builtin_bit_cast(u32x2, f4_to_h4(v)) : u32x2 {0u, 0u};
+            };
+            for (int u = wave; u * 16 < sp; u += 8) {
+                float4v acc0, acc1;
+                int     q0, r0, c0, q1, r1, c1;
+                stem_unit(u, acc0, q0, r0, c0);
+                stem_unit(u + 4, acc1, q1, r1, c1);
+                stem_store(acc0, q0, r0, c0);
+                stem_store(acc1, q1, r1, c1);
             }
-            __syncthreads(); // the stem tile is complete
-            // depthwise: output (oy0 + orow, ox0 + c) of slot dslot, window at stem row orow, column c
+            sdp_lds_barrier(); // the stem tile is complete
+            // depthwise: output pixel p = orow * ocw + c, window at stem row orow, column c
+            auto dw_unit = [&](int u, float4v &acc, int &p) __attribute__((always_inline)) {
+                p = u * 16 + px;
+                const int orow = fdiv(p, rocw), c = p - orow * ocw;
+                const int base = orow * sw + c;
+                acc = bsd;
 #pragma unroll
-            for (int k = 0; k < CB * OR * OCW / 256; ++k) {
-                const int pix = lane + k * 64; // 0 .. OR*OCW-1
-                const int orow = pix / OCW, c = pix % OCW;
-                const unsigned char *s = stem + ((dslot * IR + orow) * ICW + c) * 8;
-                float4v acc = dwb;
+                for (int j = 0; j < NSD; ++j) {
+                    u32x2 v[2];
 #pragma unroll
-                for (int t = 0; t < 9; ++t) acc += dww[t] * h4_to_f4(__builtin_bit_cast(half4, *reinterpret_cast<const u32x2 *>(s + ((t / 3) * ICW + t % 3) * 8)));
-                acc.x = sdp_act<ACTD>(acc.x, a.actd, a.lod, a.hid);
-                acc.y = sdp_act<ACTD>(acc.y, a.actd, a.lod, a.hid);
-                acc.z = sdp_act<ACTD>(acc.z, a.actd, a.lod, a.hid);
-                acc.w = sdp_act<ACTD>(acc.w, a.actd, a.lod, a.hid);
-                *reinterpret_cast<u32x2 *>(dwt + ((dslot * OR + orow) * OCW + c) * 8) = dslot < a.cbm ? __builtin_bit_cast(u32x2, f4_to_h4(acc)) : u32x2 {0u, 0u};
+                    for (int q2 = 0; q2 < 2; ++q2) {
+                        const u32x2 t = *reinterpret_cast<const u32x2 *>(stem + (base + doff[j][q2]) * 8);
+                        v[q2]         = dval[j][q2] ? t : u32x2 {0u, 0u};
+                    }
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wfd[j], __builtin_bit_cast(half8, u32x4_make(v[0].x, v[0].y, v[1].x, v[1].y)), acc, 0, 0, 0);
+                }
+            };
+            auto dw_store = [&](float4v acc, int p) __attribute__((always_inline)) {
+                float4v v = acc;
+                v.x = sdp_act<ACTD>(v.x, a.actd, a.lod, a.hid);
+                v.y = sdp_act<ACTD>(v.y, a.actd, a.lod, a.hid);
+                v.z = sdp_act<ACTD>(v.z, a.actd, a.lod, a.hid);
+                v.w = sdp_act<ACTD>(v.w, a.actd, a.lod, a.hid);
+                const int w = p < op ? DWTO + (g * op + p) * 8 : DUMPO + lane * 8;
+                *reinterpret_cast<u32x2 *>(stem + w) = g < a.cbm ? __builtin_bit_cast(u32x2, f4_to_h4(v)) : u32x2 {0u, 0u};
+            };
+            for (int u = wave; u * 16 < op; u += 8) {
+                float4v acc0, acc1;
+                int     p0, p1;
+                dw_unit(u, acc0, p0);
+                dw_unit(u + 4, acc1, p1);
+                dw_store(acc0, p0);
+                dw_store(acc1, p1);
             }
-            __syncthreads(); // the depthwise tile is complete
-            // projection: output (oy0 + orow, ox0 + c) from the depthwise tile's pixel, residual from the stem tile
-#pragma unroll 1
-            for (int u = wave; u < OR * (OCW / 16); u += 4) {
-                const int orow = u / (OCW / 16), c = (u % (OCW / 16)) * 16 + px;
+            sdp_lds_barrier(); // the depthwise tile is complete
+            // projection: output pixel p from the depthwise tile, residual from the stem tile
+            auto pw_unit = [&](int u) __attribute__((always_inline)) {
+                const int p = u * 16 + px, orow = fdiv(p, rocw), c = p - orow * ocw;
                 u32x2     v[2];
 #pragma unroll
-                for (int q = 0; q < 2; ++q) v[q] = poff[q] >= 0 ? *reinterpret_cast<const u32x2 *>(dwt + (poff[q] + orow * OCW + c) * 8) : u32x2 {0u, 0u};
-                float4v acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wfp, __builtin_bit_cast(half8, u32x4_make(v[0].x, v[0].y, v[1].x, v[1].y)),
-                                                                     float4v {0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                for (int q2 = 0; q2 < 2; ++q2) {
+                    const u32x2 t = *reinterpret_cast<const u32x2 *>(dwt + (poff[q2] + p) * 8);
+                    v[q2]         = pval[q2] ? t : u32x2 {0u, 0u};
+                }
+                const u32x2 rv  = *reinterpret_cast<const u32x2 *>(stem + (g * sp + (orow + 1) * sw + c + 1) * 8);
+                float4v     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wfp, __builtin_bit_cast(half8, u32x4_make(v[0].x, v[0].y, v[1].x, v[1].y)), bsp, 0, 0, 0);
                 const int  oy = oy0 + orow, ox = ox0 + c;
-                const bool pok = oy < a.OH && ox < a.OW;
-                float4v    o   = acc + *reinterpret_cast<const float4v *>(a.bp + g * 4);
-                if (a.res) o += h4_to_f4(__builtin_bit_cast(half4, *reinterpret_cast<const u32x2 *>(stem + ((g * IR + orow + 1) * ICW + c + 1) * 8)));
+                const bool pok = (p < op) & (oy < a.OH) & (ox < a.OW) & (g < a.cbo);
+                float4v    o   = acc;
+                if (a.res) o += h4_to_f4(__builtin_bit_cast(half4, rv));
                 o.x = sdp_act<ACTP>(o.x, a.actp, a.lop, a.hip);
                 o.y = sdp_act<ACTP>(o.y, a.actp, a.lop, a.hip);
                 o.z = sdp_act<ACTP>(o.z, a.actp, a.lop, a.hip);
                 o.w = sdp_act<ACTP>(o.w, a.actp, a.lop, a.hip);
-                const unsigned off = pok && g < a.cbo ? (unsigned) ((((n * a.y_pstride + g) * a.OH + oy) * a.OW + ox) * 8) : kInvalid;
+                const unsigned off = pok ? (unsigned) ((((n * a.y_pstride + g) * a.OH + oy) * a.OW + ox) * 8) : kInvalid;
                 __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f4_to_h4(o)), yrs, off, 0, kStreamStore);
+            };
+            for (int u = wave; u * 16 < op; u += 8) {
+                pw_unit(u);
+                pw_unit(u + 4);
             }
-            // no barrier here: the next item's band copies overwrite only the band (last read before
-            // the stem tile's barrier), and its stem and depthwise writes follow barriers that every
-            // wave reaches after its projection
+            // no barrier here: the next item's stem and depthwise writes follow barriers that every
+            // wave reaches after its projection, and its band was filled while this item ran
         }
     }
 
@@ -271,7 +375,9 @@ int vkhip_stem_dwpw_forward(const vkhip_conv_desc *cs, const vkhip_conv_desc *cd
     a.actp = cp->act; a.lop = cp->act_lo; a.hip = cp->act_hi;
     a.res  = cp->has_res;
     StemDwPwKernelFn fn = stem_dwpw_pick(cs->act, cd->act, cp->act);
-    const int64_t items = (int64_t) cs->N * ceil_div(cs->OH, sdp::OR) * ceil_div(cs->OW, sdp::OCW);
+    const int cblk = (int) ceil_div(cs->OW, sdp::MAXW);
+    a.ocw = (int) ceil_div(cs->OW, cblk);
+    const int64_t items = (int64_t) cs->N * ceil_div(cs->OH, sdp::OR) * cblk;
     static std::mutex                                mu;
     static std::vector<std::pair<const void *, int>> occ;
     int per_cu = 0, cus = 256;
