@@ -132,19 +132,30 @@ namespace vkhip {
         auto mma = [&](const unsigned char *src, const auto &off, const auto &wf, int base, auto &acc) __attribute__((always_inline)) {
             constexpr int NS = sizeof(off) / sizeof(off[0]);
             constexpr int MT = sizeof(acc) / sizeof(acc[0]);
-#pragma unroll
-            for (int m = 0; m < MT; ++m) acc[m] = float4v {0.f, 0.f, 0.f, 0.f};
+            // acc holds the biases on entry; absent taps (off < 0) read the window origin and are
+            // masked after the read (no branches)
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
                 u32x2 v[2];
 #pragma unroll
-                for (int q = 0; q < 2; ++q) v[q] = off[j][q] >= 0 ? *reinterpret_cast<const u32x2 *>(src + (base + off[j][q]) * 8) : u32x2 {0u, 0u};
+                for (int q = 0; q < 2; ++q) {
+                    const int   o = off[j][q] < 0 ? 0 : off[j][q];
+                    const u32x2 t = *reinterpret_cast<const u32x2 *>(src + (base + o) * 8);
+                    v[q]          = off[j][q] >= 0 ? t : u32x2 {0u, 0u};
+                }
                 const half8 bf = __builtin_bit_cast(half8, u32x4_make(v[0].x, v[0].y, v[1].x, v[1].y));
 #pragma unroll
                 for (int m = 0; m < MT; ++m) acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[m][j], bf, acc[m], 0, 0, 0);
             }
         };
         const int g = lane >> 4, px = lane & 15;
+        // the lane's biases (rows 4g..4g+3 of each 16-channel fragment), which seed the accumulators
+        float4v bsa[1], bsb[MTB], bsc[MTC ? MTC : 1];
+        bsa[0] = *reinterpret_cast<const float4v *>(a.ba + g * 4);
+#pragma unroll
+        for (int m = 0; m < MTB; ++m) bsb[m] = *reinterpret_cast<const float4v *>(a.bb + (m * 4 + g) * 4);
+#pragma unroll
+        for (int m = 0; m < (MTC ? MTC : 1); ++m) bsc[m] = MTC ? *reinterpret_cast<const float4v *>(a.bc + (m * 4 + g) * 4) : float4v {};
 
         // items: XCD-contiguous ranges (workgroup b runs on XCD b % 8)
         const int G = gridDim.x;
@@ -172,18 +183,24 @@ namespace vkhip {
             __asm__ volatile("s_barrier" ::: "memory");        // every wave's copies landed
             // first conv: intermediate pixel (r, c) <-> first-conv output (2 oy0 - 1 + r, 2 ox0 - 1 + c),
             // its window at band row 2r, column 2c + 1
-            for (int u = wave; u < IR * IT; u += 4) {
+            // two units per pass, so their LDS reads and MFMAs overlap
+            auto first_unit = [&](int u) __attribute__((always_inline)) {
                 const int r = u / IT, c = (u % IT) * 16 + px;
-                float4v   acc[1];
+                float4v   acc[1] = {bsa[0]};
                 mma(band, aoff, wfa, 2 * r * BC + 2 * c + 1, acc);
                 const int  iy = 2 * oy0 - 1 + r, ix = 2 * ox0 - 1 + c;
-                const bool in = iy >= 0 && iy < a.HA && ix >= 0 && ix < a.WA && g < a.cbm;
-                float4v    v  = acc[0] + *reinterpret_cast<const float4v *>(a.ba + g * 4);
+                const bool in = ((unsigned) iy < (unsigned) a.HA) & ((unsigned) ix < (unsigned) a.WA) & (g < a.cbm);
+                float4v    v  = acc[0];
                 v.x = stem2_act<ACTA>(v.x, a.acta, a.loa, a.hia);
                 v.y = stem2_act<ACTA>(v.y, a.acta, a.loa, a.hia);
                 v.z = stem2_act<ACTA>(v.z, a.acta, a.loa, a.hia);
                 v.w = stem2_act<ACTA>(v.w, a.acta, a.loa, a.hia);
                 *reinterpret_cast<u32x2 *>(inter + ((g * IR + r) * ICW + c) * 8) = in ? __builtin_bit_cast(u32x2, f4_to_h4(v)) : u32x2 {0u, 0u};
+            };
+            // (past the end, the second unit repeats the last one: the same values to the same place)
+            for (int u = wave; u < IR * IT; u += 8) {
+                first_unit(u);
+                first_unit(min(u + 4, IR * IT - 1));
             }
             __syncthreads(); // the intermediate tile is complete
             // second conv: output (oy0 + orow, ox0 + c), window at intermediate row 2 orow, column 2c
@@ -191,13 +208,15 @@ namespace vkhip {
             for (int u = wave; u < OR * (OCW / 16); u += 4) {
                 const int orow = u / (OCW / 16), c = (u % (OCW / 16)) * 16 + px;
                 float4v   acc[MTB];
+#pragma unroll
+                for (int m = 0; m < MTB; ++m) acc[m] = bsb[m];
                 mma(inter, boff, wfb, 2 * orow * ICW + 2 * c, acc);
                 const int  oy = oy0 + orow, ox = ox0 + c;
                 const bool pok = oy < a.HB && ox < a.WB;
 #pragma unroll
                 for (int m = 0; m < MTB; ++m) {
                     const int ocb = m * 4 + g;
-                    float4v   v   = acc[m] + *reinterpret_cast<const float4v *>(a.bb + ocb * 4);
+                    float4v   v   = acc[m];
                     v.x = stem2_act<ACTB>(v.x, a.actb, a.lob, a.hib);
                     v.y = stem2_act<ACTB>(v.y, a.actb, a.lob, a.hib);
                     v.z = stem2_act<ACTB>(v.z, a.actb, a.lob, a.hib);
@@ -219,13 +238,15 @@ namespace vkhip {
                 for (int u = wave; u < OR * (OCW / 16); u += 4) {
                     const int orow = u / (OCW / 16), c = (u % (OCW / 16)) * 16 + px;
                     float4v   acc[MTC];
+#pragma unroll
+                    for (int m = 0; m < MTC; ++m) acc[m] = bsc[m];
                     mma(ctile, coff, wfc, orow * OCW + c, acc);
                     const int  oy = oy0 + orow, ox = ox0 + c;
                     const bool pok = oy < a.HB && ox < a.WB;
 #pragma unroll
                     for (int m = 0; m < MTC; ++m) {
                         const int ocb = m * 4 + g;
-                        float4v   v   = acc[m] + *reinterpret_cast<const float4v *>(a.bc + ocb * 4);
+                        float4v   v   = acc[m];
                         v.x = stem2_act<ACTB>(v.x, a.actc, a.loc, a.hic);
                         v.y = stem2_act<ACTB>(v.y, a.actc, a.loc, a.hic);
                         v.z = stem2_act<ACTB>(v.z, a.actc, a.loc, a.hic);
