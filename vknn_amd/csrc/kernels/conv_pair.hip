@@ -138,19 +138,30 @@ namespace vkhip {
         };
         auto mma = [&](const unsigned char *src, const int (&off)[NSTEPS][2], const half8 (&wf)[MT][NSTEPS], int base, float4v (&acc)[MT])
             __attribute__((always_inline)) {
-#pragma unroll
-            for (int m = 0; m < MT; ++m) acc[m] = float4v {0.f, 0.f, 0.f, 0.f};
+            // acc holds the biases on entry; absent taps (off < 0) read the window origin and are
+            // masked after the read (no branches)
 #pragma unroll
             for (int j = 0; j < NSTEPS; ++j) {
                 u32x2 v[2];
 #pragma unroll
-                for (int q = 0; q < 2; ++q) v[q] = off[j][q] >= 0 ? *reinterpret_cast<const u32x2 *>(src + (base + off[j][q]) * 8) : u32x2 {0u, 0u};
+                for (int q = 0; q < 2; ++q) {
+                    const int   o = off[j][q] < 0 ? 0 : off[j][q];
+                    const u32x2 t = *reinterpret_cast<const u32x2 *>(src + (base + o) * 8);
+                    v[q]          = off[j][q] >= 0 ? t : u32x2 {0u, 0u};
+                }
                 const half8 bf = __builtin_bit_cast(half8, u32x4_make(v[0].x, v[0].y, v[1].x, v[1].y));
 #pragma unroll
                 for (int m = 0; m < MT; ++m) acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[m][j], bf, acc[m], 0, 0, 0);
             }
         };
         const int g = lane >> 4, px = lane & 15;
+        // the lane's biases (rows 4g..4g+3 of each 16-channel fragment), which seed the accumulators
+        float4v bs1[MT], bs2[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            bs1[m] = *reinterpret_cast<const float4v *>(a.b1 + (m * 4 + g) * 4);
+            bs2[m] = *reinterpret_cast<const float4v *>(a.b2 + (m * 4 + g) * 4);
+        }
 
         // items: XCD-contiguous ranges (workgroup b runs on XCD b % 8)
         const int G = gridDim.x;
@@ -167,24 +178,36 @@ namespace vkhip {
             __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
             __asm__ volatile("s_barrier" ::: "memory");
             // first conv over the 6 x 80 intermediate tile: (row, column tile) units dealt to the waves
-            for (int u = wave; u < IR * IT; u += 4) {
+            // two units per pass, so their LDS reads and MFMAs overlap (past the end, the second
+            // unit repeats the last one: the same values to the same place)
+            auto first_unit = [&](int u) __attribute__((always_inline)) {
                 const int r = u / IT, t = u % IT;
                 const int c = t * 16 + px;                       // intermediate column
                 float4v   acc[MT];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) acc[m] = bs1[m];
                 mma(band, boff, wf1, r * BC + c, acc);
                 const int  iy = oy0 - 1 + r, ix = ox0 - 1 + c;
-                const bool in = iy >= 0 && iy < H && ix >= 0 && ix < W;
+                const bool in = ((unsigned) iy < (unsigned) H) & ((unsigned) ix < (unsigned) W);
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
                     const int ocb = m * 4 + g;
-                    float4v   v   = acc[m] + *reinterpret_cast<const float4v *>(a.b1 + ocb * 4);
+                    float4v   v   = acc[m];
                     v.x = pair_act<ACT1>(v.x, a.act1, a.lo1, a.hi1);
                     v.y = pair_act<ACT1>(v.y, a.act1, a.lo1, a.hi1);
                     v.z = pair_act<ACT1>(v.z, a.act1, a.lo1, a.hi1);
                     v.w = pair_act<ACT1>(v.w, a.act1, a.lo1, a.hi1);
                     // outside the image: the second conv's zero padding; channel slots past Cb: zero
-                    const u32x2 h = in && ocb < a.Cb ? __builtin_bit_cast(u32x2, f4_to_h4(v)) : u32x2 {0u, 0u};
+                    const u32x2 h = in & (ocb < a.Cb) ? __builtin_bit_cast(u32x2, f4_to_h4(v)) : u32x2 {0u, 0u};
                     *reinterpret_cast<u32x2 *>(inter + ((ocb * IR + r) * ICW + c) * 8) = h;
+                }
+            };
+            if constexpr (CB == 8) {
+                for (int u = wave; u < IR * IT; u += 4) first_unit(u);
+            } else {
+                for (int u = wave; u < IR * IT; u += 8) {
+                    first_unit(u);
+                    first_unit(min(u + 4, IR * IT - 1));
                 }
             }
             __syncthreads(); // the intermediate tile is complete
@@ -194,13 +217,15 @@ namespace vkhip {
             for (int t = 0; t < OCW / 16; ++t) {
                 const int c = t * 16 + px; // output column within the item
                 float4v   acc[MT];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) acc[m] = bs2[m];
                 mma(inter, ioff, wf2, wave * ICW + c, acc);
                 const int  ox  = ox0 + c;
-                const bool pok = oy < H && ox < W;
+                const bool pok = (oy < H) & (ox < W);
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
                     const int ocb = m * 4 + g;
-                    float4v   v   = acc[m] + *reinterpret_cast<const float4v *>(a.b2 + ocb * 4);
+                    float4v   v   = acc[m];
                     v.x = pair_act<ACT2>(v.x, a.act2, a.lo2, a.hi2);
                     v.y = pair_act<ACT2>(v.y, a.act2, a.lo2, a.hi2);
                     v.z = pair_act<ACT2>(v.z, a.act2, a.lo2, a.hi2);
