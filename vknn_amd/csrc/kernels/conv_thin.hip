@@ -88,6 +88,11 @@ namespace vkhip {
 #pragma unroll
                 for (int j = 0; j < NSTEPS; ++j) wf[m][j] = wp[(m * NSTEPS + j) * 64 + lane];
         }
+        // the lane's biases (rows 4(l/16)..+3 of each fragment), which seed the accumulators; held
+        // in registers, since a load in the tile loop could not move above the buffer stores
+        float4v bsv[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) bsv[m] = *reinterpret_cast<const float4v *>(a.bias + (m * 4 + (lane >> 4)) * 4);
         // per (step, half): the LDS pixel offset of this lane's 4-channel slot relative to the
         // output pixel's band position, or -1 for a zero pad of the reduction (tap >= K*K)
         int boff[NSTEPS][2];
@@ -149,13 +154,17 @@ namespace vkhip {
                 const int base = wave * S * B::COLS + (t * 16 + (lane & 15)) * S;
                 float4v   acc[MT];
 #pragma unroll
-                for (int m = 0; m < MT; ++m) acc[m] = float4v {0.f, 0.f, 0.f, 0.f};
+                for (int m = 0; m < MT; ++m) acc[m] = bsv[m];
 #pragma unroll
                 for (int j = 0; j < NSTEPS; ++j) {
                     u32x2 v[2];
 #pragma unroll
                     for (int q = 0; q < 2; ++q) {
-                        v[q] = boff[j][q] >= 0 ? *reinterpret_cast<const u32x2 *>(band + (base + boff[j][q]) * 8) : u32x2 {0u, 0u};
+                        // a zero pad of the reduction reads the window origin and is masked after
+                        // the read (no branch)
+                        const int   o = boff[j][q] < 0 ? 0 : boff[j][q];
+                        const u32x2 t = *reinterpret_cast<const u32x2 *>(band + (base + o) * 8);
+                        v[q]          = boff[j][q] >= 0 ? t : u32x2 {0u, 0u};
                     }
                     const half8 bf = __builtin_bit_cast(half8, u32x4_make(v[0].x, v[0].y, v[1].x, v[1].y));
 #pragma unroll
@@ -166,7 +175,7 @@ namespace vkhip {
                 for (int m = 0; m < MT; ++m) {
                     const int ocb = m * 4 + g;
                     const int oc  = ocb * 4;
-                    float4v   v   = acc[m] + *reinterpret_cast<const float4v *>(a.bias + oc);
+                    float4v   v   = acc[m];
                     float4v   r   = {0.f, 0.f, 0.f, 0.f};
                     if constexpr (RES) {
                         r = h4_to_f4(__builtin_bit_cast(half4, *reinterpret_cast<const u32x2 *>(band + RBASE + ((ocb * OR + wave) * OCW + t * 16 + (lane & 15)) * 8)));
