@@ -780,13 +780,20 @@ def test_conv_stem(gpu, tile, case):
     assert_parity(got, ref, f"stem tile {tile} {case}")
 
 
-@pytest.mark.parametrize("tile", [21, 22])
-@pytest.mark.parametrize("case", [(2, 3, 224, 224, 64, 7, 2, 1), (1, 3, 33, 40, 64, 7, 2, 0), (3, 4, 30, 46, 48, 3, 2, 2),
-                                  (2, 1, 17, 18, 20, 7, 1, 1), (1, 3, 9, 250, 64, 7, 2, 1)])
+STEM_POOL_CASES = [(2, 3, 224, 224, 64, 7, 2, 1), (1, 3, 33, 40, 64, 7, 2, 0), (3, 4, 30, 46, 48, 3, 2, 2), (2, 1, 17, 18, 20, 7, 1, 1),
+                   (1, 3, 9, 250, 64, 7, 2, 1)]
+# the thin-tile kernel: 7x7 stride 2 over an even width only
+THIN_POOL_CASES = [(2, 3, 224, 224, 64, 7, 2, 1), (1, 3, 33, 40, 64, 7, 2, 0), (1, 3, 9, 250, 64, 7, 2, 1), (3, 4, 30, 46, 48, 7, 2, 2),
+                   (2, 1, 17, 18, 20, 7, 2, 1), (1, 2, 6, 4, 9, 7, 2, 0)]
+
+
+@pytest.mark.parametrize("tile,case", [(t, c) for t in (21, 22) for c in STEM_POOL_CASES] + [(45, c) for c in THIN_POOL_CASES])
 def test_conv_maxpool_fused(gpu, tile, case):
     """Stem conv + 3x3/s2/p1 max pool in one kernel: bit-identical to the conv kernel followed by
     the max-pool kernel (odd heights, ragged output channels, stride 1 and 2, wide rows with one
-    pooled row per workgroup), and the pool of the oracle conv within the fp16 tolerance."""
+    pooled row per workgroup; on the stem tiles 21/22 and on the thin tile 45, whose kernel splits
+    the pooled width into items of at most 28 columns: 28, 20, 21, 12, 5 and 1 here), and the pool
+    of the oracle conv within the fp16 tolerance."""
     lib = V.vkhip()
     N, C, H, W, Cout, K, S, act = case
     r = rng(170 + tile + H + K)
@@ -834,6 +841,14 @@ def test_conv_maxpool_rejects_other_shapes(gpu):
     wide, _ = conv_desc((1, 3, 32, 32), (96, 3, 7, 7), (2, 2), (3, 3, 3, 3))
     assert lib.vkhip_conv_plan_make(ctypes.byref(wide), V.CONV_GEMM, 21, 0, ctypes.byref(plan)) != 0 or \
         lib.vkhip_conv_maxpool_supported(ctypes.byref(wide), ctypes.byref(plan), ctypes.byref(ok)) == 0
+    # the thin tile: 7x7 stride 2 pad 3 over an even width only
+    check(lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, 45, 0, ctypes.byref(plan)))
+    assert lib.vkhip_conv_maxpool_supported(ctypes.byref(d), ctypes.byref(plan), ctypes.byref(ok)) == 1
+    for shape, wshape, st, pads in [((1, 3, 32, 31), (64, 3, 7, 7), 2, 3), ((1, 3, 32, 32), (64, 3, 3, 3), 2, 1), ((1, 3, 32, 32), (64, 3, 7, 7), 1, 3)]:
+        o, (_, _, oh, ow) = conv_desc(shape, wshape, (st, st), (pads,) * 4)
+        op = V.PoolDesc(N=1, C=64, H=oh, W=ow, OH=(oh - 1) // 2 + 1, OW=(ow - 1) // 2 + 1, KH=3, KW=3, SH=2, SW=2, PT=1, PL=1)
+        assert lib.vkhip_conv_plan_make(ctypes.byref(o), V.CONV_GEMM, 45, 0, ctypes.byref(plan)) != 0 or \
+            lib.vkhip_conv_maxpool_supported(ctypes.byref(o), ctypes.byref(plan), ctypes.byref(op)) == 0, (shape, wshape, st)
     check(lib.vkhip_conv_plan_make(ctypes.byref(d), V.CONV_GEMM, 0, 0, ctypes.byref(plan)))
     assert lib.vkhip_conv_maxpool_supported(ctypes.byref(d), ctypes.byref(plan), ctypes.byref(ok)) == 0
 

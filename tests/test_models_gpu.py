@@ -278,15 +278,21 @@ def test_side_stream_branches_match_single_stream(gpu, model, batch, opts, graph
         np.testing.assert_array_equal(s2.run(x), s1.run(x))
 
 
-@pytest.mark.parametrize("model,batch", [("resnet_tiny", 3), ("resnet50", 2)])
-def test_stem_maxpool_fused(gpu, model, batch, monkeypatch):
-    """With VKNN_HIP_FUSE_POOL=1 the ResNet stem conv and its 3x3/s2 max pool run as one kernel
-    (the pool node folded into the conv): outputs within the tolerance of the session that runs
-    them apart (default), and of the oracle."""
-    monkeypatch.setenv("VKNN_HIP_FUSE_POOL", "1")
+@pytest.mark.parametrize("model,batch,env", [("resnet_tiny", 3, "1"), ("resnet50", 2, "1"), ("resnet50", 3, None)])
+def test_stem_maxpool_fused(gpu, model, batch, env, monkeypatch):
+    """By default the ResNet-50 stem conv (7x7/s2) and its 3x3/s2 max pool run as one thin-tile
+    kernel (the pool node folded into the conv); VKNN_HIP_FUSE_POOL=1 also allows the stem tiles
+    (resnet_tiny's 3x3 stem). Outputs within the tolerance of the session that runs them apart
+    (VKNN_HIP_FUSE_POOL=0), and of the oracle."""
+    if env:
+        monkeypatch.setenv("VKNN_HIP_FUSE_POOL", env)
+    else:
+        monkeypatch.delenv("VKNN_HIP_FUSE_POOL", raising=False)
     sess = V.Session(model, batch, seed=7)
     plan = sess.describe()
     assert plan.count("+max pool") == 1 and plan.count("max pool folded into") == 1, plan
+    if model == "resnet50":
+        assert "kernel=conv_thin_pool_kernel" in plan, plan
     x = make_input(sess.in_shape, 6)
     got = sess.run(x)
     monkeypatch.setenv("VKNN_HIP_FUSE_POOL", "0")

@@ -69,6 +69,15 @@ namespace vknn {
             return v.empty() ? d : v;
         }
 
+        // Plans a stem conv + max pool may take: thin tile 45 (conv_thin_pool_kernel, the 7x7 stride-2
+        // stem); VKNN_HIP_FUSE_POOL=1 adds the 64-row stem tiles (stem_pool_kernel, slower than the
+        // two launches on the ResNet-50 stem: kept for other stems).
+        static std::vector<int> poolTiles() {
+            const char *e = std::getenv("VKNN_HIP_FUSE_POOL");
+            if (e && std::string(e) == "1") return {45, 21, 22};
+            return {45};
+        }
+
         static const float *initF32(const Graph &g, TensorId id) {
             if (id == kNoTensor) return nullptr;
             auto it = g.initializers.find(id);
@@ -194,9 +203,9 @@ namespace vknn {
                 const float *w = initF32(g, node.inputs[1]);
                 const float *b = initF32(g, biasOf(node));
                 if (poolOut != kNoTensor) {
-                    // the fused stem + pool kernel runs the 64-row stem tiles
+                    // the fused stem + pool kernel: the thin tile, or (opt-in) the 64-row stem tiles
                     bool ok = false;
-                    for (int t: {21, 22})
+                    for (int t: poolTiles())
                         if (!ok && vkhip_conv_plan_make(&d, VKHIP_CONV_GEMM, t, 0, &plan) == VKHIP_OK && vkhip_conv_maxpool_supported(&d, &plan, &pd)) ok = true;
                     if (!ok) throw Error(Status::RuntimeError, "conv + max pool fusion planned for an unsupported shape: " + name);
                     bytes = (int64_t) (nc4Bytes(g.desc(in).shape) + nc4Bytes(g.desc(poolOut).shape)) + (int64_t) d.Cout * d.Cin * d.KH * d.KW * 2;
@@ -494,7 +503,7 @@ namespace vknn {
                 static const char *algos[] = {"auto", "gemm", "splitk", "winograd", "depthwise", "splitk_last"};
                 return std::string(algos[plan.algo]) + " tile=" + std::to_string(plan.tile) + " ksplit=" + std::to_string(plan.ksplit) +
                        (d.in_scale ? " +input scale" : "") + (poolOut != kNoTensor ? " +max pool" : "") + (gapPart ? " +pool sums" : "") + " kernel=" +
-                       (poolOut != kNoTensor ? std::string("stem_pool_kernel") : std::string(vkhip_conv_plan_kernel(&plan)));
+                       (poolOut != kNoTensor ? std::string(plan.tile == 45 ? "conv_thin_pool_kernel" : "stem_pool_kernel") : std::string(vkhip_conv_plan_kernel(&plan)));
             }
         };
 
@@ -1325,7 +1334,7 @@ namespace vknn {
                 pd.KH = pd.KW = 3; pd.SH = pd.SW = 2; pd.PT = pd.PL = 1;
                 vkhip_conv_plan plan;
                 bool            ok = false;
-                for (int tile: {21, 22})
+                for (int tile: poolTiles())
                     if (!ok && vkhip_conv_plan_make(&d, VKHIP_CONV_GEMM, tile, 0, &plan) == VKHIP_OK && vkhip_conv_maxpool_supported(&d, &plan, &pd)) ok = true;
                 if (ok) convPool[pit->second] = i;
             }
@@ -1516,14 +1525,12 @@ namespace vknn {
             for (auto &kv: scaled)
                 for (int m: folded)
                     if (g.nodes[m].outputs[0] == g.nodes[kv.first].inputs[0]) foldedInto[m] = g.nodes[kv.first].name;
-            // VKNN_HIP_FUSE_POOL=1 runs a stem conv and its max pool as one kernel. Off by default:
-            // on the ResNet-50 stem the fused kernel (70 us at b64) only matches the two kernels it
-            // replaces (49 + 25 us), because it recomputes the shared conv rows at the stem's low
-            // MFMA rate and holds one workgroup per CU.
+            // A stem conv and its max pool as one kernel (poolTiles); VKNN_HIP_FUSE_POOL=0 keeps the
+            // two launches (A/B).
             std::map<int, int> convPool;
             std::set<int>      pools;
             const char        *pool_env = std::getenv("VKNN_HIP_FUSE_POOL");
-            if (pool_env && std::string(pool_env) == "1") planPoolFolds(g, idx, convPool);
+            if (!pool_env || std::string(pool_env) != "0") planPoolFolds(g, idx, convPool);
             for (auto &kv: convPool) {
                 pools.insert(kv.second);
                 foldedInto[kv.second] = g.nodes[kv.first].name;

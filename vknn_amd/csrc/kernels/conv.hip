@@ -1135,12 +1135,13 @@ extern "C" {
 
 int vkhip_conv_maxpool_supported(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const vkhip_pool_desc *p) {
     int PR, NBI, cfg;
-    return stem_pool_geom(d, plan, p, PR, NBI, cfg) ? 1 : 0;
+    return thin_pool_ok(d, plan, p) || stem_pool_geom(d, plan, p, PR, NBI, cfg) ? 1 : 0;
 }
 
 int vkhip_conv_maxpool_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const vkhip_pool_desc *p, const void *x, const void *blob,
                                void *y, vkhip_stream_t s) {
     if (!d || !plan || !p || !x || !blob || !y) return set_error(VKHIP_ERR_INVALID, "conv_maxpool: null argument");
+    if (thin_pool_ok(d, plan, p)) return thin_pool_launch(d, p, x, blob, y, s);
     int PR = 0, NBI = 0, cfg = 0;
     if (!stem_pool_geom(d, plan, p, PR, NBI, cfg)) return set_error(VKHIP_ERR_UNSUPPORTED, "conv_maxpool: shape or plan not supported");
     StemPoolFn fn = stem_pool_kernel_for(d->KH, cfg);

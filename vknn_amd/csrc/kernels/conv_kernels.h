@@ -2200,6 +2200,9 @@ namespace vkhip {
     // conv_thin_kernel for cinb input slots (rounded up to 1, 2, 4 or 8), mt 16-channel output
     // fragments, a k x k kernel and stride s (nullptr if not instantiated)
     GemmKernelFn thin_kernel_for(int cinb, int mt, int k, int s, bool res);
+    // the 7x7 stride-2 stem on thin tile 45 with its 3x3 stride-2 max pool in one kernel (conv_thin_pool.hip)
+    bool thin_pool_ok(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const vkhip_pool_desc *p);
+    int  thin_pool_launch(const vkhip_conv_desc *d, const vkhip_pool_desc *p, const void *x, const void *blob, void *y, vkhip_stream_t s);
     inline int thin_cinb(int64_t cinb) { return cinb <= 1 ? 1 : cinb <= 2 ? 2 : cinb <= 4 ? 4 : 8; }
     GemmKernelFn bd_tile_kernel(int tile, int bmode);
     GemmKernelFn dma_tile_kernel(int tile, int bmode, int steps, bool xs);
