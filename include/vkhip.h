@@ -406,8 +406,9 @@ int vkhip_maxpool_chain(const vkhip_pool_desc *d, const void *x, int64_t x_pstri
  * channels, no residual) followed by a 3x3 stride-2 pad-1 max pool over its output, in one
  * kernel: y = maxpool(act(conv(x) + bias)), bit-identical to vkhip_conv_forward then
  * vkhip_maxpool, without the conv output in memory. The plan must be a stem-kernel plan with
- * 64-row tiles (vkhip_conv_plan_make with tile 21 or 22) and its packed blob. No counterpart in the
- * reference, which runs the two as separate ops (ops/conv.cpp, ops/pool.cpp). */
+ * 64-row tiles (vkhip_conv_plan_make with tile 21 or 22), or the 64-output thin plan (tile 45) for a
+ * 7x7 stride-2 pad-3 conv over an even input width (the ResNet stem), and its packed blob. No
+ * counterpart in the reference, which runs the two as separate ops (ops/conv.cpp, ops/pool.cpp). */
 int vkhip_conv_maxpool_supported(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const vkhip_pool_desc *p);
 int vkhip_conv_maxpool_forward(const vkhip_conv_desc *d, const vkhip_conv_plan *plan, const vkhip_pool_desc *p, const void *x, const void *blob,
                                void *y, vkhip_stream_t s);
