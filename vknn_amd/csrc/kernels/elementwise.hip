@@ -4,6 +4,7 @@
 // wave64 kernels over 8- or 16-byte vectors; none uses MFMA.
 #include "common.h"
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 
 namespace vkhip {
@@ -56,6 +57,33 @@ namespace vkhip {
         // padding lanes of a partial channel block hold +0 (ref_float_to_half(0) == 0)
         dst[2 * i]     = make_uint4(w[0][0], w[0][1], w[1][0], w[1][1]);
         dst[2 * i + 1] = make_uint4(w[2][0], w[2][1], w[3][0], w[3][1]);
+    }
+
+    // The same conversion, two consecutive pixels per thread (HW % 2 == 0): one 8-byte load per
+    // channel plane and one 16-byte store, so each store instruction of a wave covers 1 KB of
+    // contiguous output.
+    template <typename I>
+    __global__ void pack2_kernel(const float2 *src, uint4 *dst, I C, I HW2, I Cb, I total) {
+        I i = (I) blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= total) return;
+        I p  = i % HW2;
+        I t  = i / HW2;
+        I cb = t % Cb;
+        I n  = t / Cb;
+        float v[4][2]; // [channel lane][pixel]
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            I c = cb * 4 + l;
+            float2 f = c < C ? src[(n * C + c) * HW2 + p] : make_float2(0.f, 0.f);
+            v[l][0] = f.x; v[l][1] = f.y;
+        }
+        uint32_t w[2][2]; // [pixel][channel pair]
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            w[k][0] = (uint32_t) ref_float_to_half(v[0][k]) | ((uint32_t) ref_float_to_half(v[1][k]) << 16);
+            w[k][1] = (uint32_t) ref_float_to_half(v[2][k]) | ((uint32_t) ref_float_to_half(v[3][k]) << 16);
+        }
+        dst[i] = make_uint4(w[0][0], w[0][1], w[1][0], w[1][1]);
     }
 
     // Element offset of logical (n, c, h, w) in layout fmt (0 NCHW, 1 NHWC, 2 NC4HW4).
@@ -520,6 +548,14 @@ extern "C" {
 int vkhip_pack_nchw_f32(const float *src, void *dst, int64_t N, int64_t C, int64_t H, int64_t W, vkhip_stream_t s) {
     if (!src || !dst || N <= 0 || C <= 0 || H <= 0 || W <= 0) return set_error(VKHIP_ERR_INVALID, "pack: bad arguments");
     int64_t Cb = ceil_div(C, 4), total = N * Cb * H * W;
+    // two pixels per thread (one contiguous 16-byte store each) when planes hold an even pixel
+    // count; VKHIP_PACK2=0 keeps the four-pixel kernel below (A/B)
+    static const bool pack2 = [] { const char *e = std::getenv("VKHIP_PACK2"); return !e || e[0] != '0'; }();
+    if (pack2 && (H * W) % 2 == 0 && ((uintptr_t) src & 7) == 0 && ((uintptr_t) dst & 15) == 0 && N * Cb * 4 * H * W < INT32_MAX) {
+        const int64_t t2 = total / 2;
+        pack2_kernel<int><<<grid1(t2), 256, 0, resolve_stream(s)>>>((const float2 *) src, (uint4 *) dst, (int) C, (int) (H * W / 2), (int) Cb, (int) t2);
+        return check_launch("pack");
+    }
     // four pixels per thread when every plane starts 16-byte aligned
     if ((H * W) % 4 == 0 && ((uintptr_t) src & 15) == 0 && ((uintptr_t) dst & 15) == 0) {
         const int64_t t4 = total / 4;
