@@ -56,7 +56,7 @@ def family(name):
 
 def timed_rows(rows, steps):
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-    packs = [i for i, r in enumerate(rows) if family(r["Kernel_Name"]).startswith(("pack_kernel", "pack4_kernel"))]
+    packs = [i for i, r in enumerate(rows) if family(r["Kernel_Name"]).startswith(("pack_kernel", "pack2_kernel", "pack4_kernel"))]
     if len(packs) < steps:
         raise SystemExit(f"found {len(packs)} pack dispatches, need {steps}")
     return rows[packs[-steps]:]
@@ -217,7 +217,7 @@ def cmd_traffic(a):
 PEAK_TFLOPS, PEAK_GBS = 2500.0, 8000.0
 RIDGE = PEAK_TFLOPS * 1e12 / (PEAK_GBS * 1e9)
 # the segment's boundary conversions (fp32 NCHW <-> NC4HW4 fp16), which belong to no operator
-BOUNDARY = ("pack_kernel", "pack4_kernel", "unpack", "boundary_convert")
+BOUNDARY = ("pack_kernel", "pack2_kernel", "pack4_kernel", "unpack", "boundary_convert")
 
 
 def read_plan(path):
@@ -233,7 +233,7 @@ def marker_groups(rows, steps, n_ops, boundary=None):
     """Per timed step, the dispatch rows of each operator (cut at the markers); the boundary
     conversions of each step go to `boundary` (a list) if given."""
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
-    starts = [i for i, r in enumerate(rows) if family(r["Kernel_Name"]).startswith(("pack_kernel", "pack4_kernel"))]
+    starts = [i for i, r in enumerate(rows) if family(r["Kernel_Name"]).startswith(("pack_kernel", "pack2_kernel", "pack4_kernel"))]
     if len(starts) < steps:
         raise SystemExit(f"found {len(starts)} pack dispatches, need {steps}")
     out = []
