@@ -1577,7 +1577,8 @@ namespace vknn {
             // In-place concat / split (planViews); VKNN_HIP_VIEWS=0 keeps their copies (A/B).
             {
                 std::set<int> noWrite, noRead;
-                for (auto &kv: convPool) noWrite.insert(kv.first);
+                // a conv + pool kernel reads a dense input and writes the pool's output densely
+                for (auto &kv: convPool) noWrite.insert(kv.first), noWrite.insert(kv.second), noRead.insert(kv.first);
                 for (auto &kv: scaled) noRead.insert(kv.first);
                 for (int m: folded) noRead.insert(m), noWrite.insert(m);
                 for (auto &kv: gapConv) noWrite.insert(kv.second);
